@@ -1,0 +1,194 @@
+"""MoE-layer decode throughput on one MI355X.
+
+Workload: one Mixtral-shape MoE FFN layer — d_model 4096, 8 experts, top-2, expert FFN
+14336 SwiGLU, gate/up/down quantised to Q4_K (build-side quantiser) from N(0, 0.02^2)
+weights, f32 router N(0, 0.02^2), N(0, 1) activations — decoded at a batch of tokens.
+A step is one call of the layer (route -> dispatch -> gate/up -> down -> combine) on
+inputs already resident in HBM. Steps rotate over `--layers` distinct copies of the
+layer in HBM (different router weights, separate slab copies of the experts) so each
+step streams its experts from HBM rather than from the 256 MB MALL.
+
+Prints one JSON line with `roofline` (the gate/up kernel: algorithmic bytes per launch /
+its average duration from HIP events on its stream) and `cpu_baseline` (the oracle's
+restatement of the reference's packed CPU path, threaded over rows, on a bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+D, F, NE, K = 4096, 14336, 8, 2
+HBM_PEAK_GBS = 8000.0
+SEED = 0x6761_7275_6461_2000  # build-side seeds, "garuda" + tag
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_experts(threads):
+    import garuda_amd as G
+    from garuda_amd import moe as M
+    mats = {}
+    for p, (name, rows, cols) in enumerate((("gate", F, D), ("up", F, D), ("down", D, F))):
+        parts = []
+        for e in range(NE):
+            x = M.fill_gaussian(SEED + 16 * e + p, rows * cols, 0.0, 0.02, threads)
+            parts.append(M.quantize(G.Q4_K, x, threads))
+            del x
+        mats[name] = np.concatenate(parts)
+    return mats
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--batch", type=int, default=8, help="tokens per step for the headline value")
+    ap.add_argument("--sweep", default="1,2,4,8", help="other decode batch sizes to report")
+    ap.add_argument("--layers", type=int, default=8)
+    ap.add_argument("--math", choices=("packed", "f32"), default="packed")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=1.5, help="wall-clock budget of the CPU sample")
+    a = ap.parse_args()
+
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X only: this build has no multi-GPU path "
+              "(expert-parallel sharding is a design note in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import garuda_amd as G
+    from garuda_amd import moe as M
+
+    threads = len(os.sched_getaffinity(0))
+    t0 = time.time()
+    mats = make_experts(threads)
+    log(f"experts generated and quantised in {time.time() - t0:.1f}s ({sum(m.size for m in mats.values()) / 1e6:.0f} MB packed)")
+
+    math = G.MATH_PACKED if a.math == "packed" else G.MATH_F32
+    expert_bytes = 3 * M.byte_size(G.Q4_K, F * D)
+    slab = a.layers * NE * (expert_bytes + 3 * 4096) + (256 << 20)
+    dev = G.Device(0, slab_bytes=slab)
+    layers = []
+    t0 = time.time()
+    for l in range(a.layers):
+        router = M.fill_gaussian(SEED + 0x100 + l, NE * D, 0.0, 0.02, threads)
+        layers.append(G.MoeLayer(dev, D, F, NE, K, router, mats["gate"], mats["up"], mats["down"],
+                                 (G.Q4_K,) * 3, math=math))
+    log(f"{a.layers} layers staged into HBM in {time.time() - t0:.1f}s")
+
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+    results = {}
+    batches = sorted(set([a.batch] + [int(b) for b in a.sweep.split(",") if b]))
+    for n in batches:
+        hs = torch.from_numpy(M.fill_gaussian(SEED + 0x200 + n, n * D, 0.0, 1.0, threads).reshape(n, D)).cuda()
+        out = torch.empty((n, D), dtype=torch.float32, device="cuda")
+        ids = torch.empty((len(layers), n, K), dtype=torch.int32, device="cuda")
+        wts = torch.empty((len(layers), n, K), dtype=torch.float32, device="cuda")
+
+        def step(i):
+            l = i % len(layers)
+            layers[l].forward_async(hs.data_ptr(), n, out.data_ptr(), ids[l].data_ptr(), wts[l].data_ptr(),
+                                    0, sh)
+
+        for i in range(a.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        dev.kernel_time(0)  # drain
+        base = [dev.kernel_time(w) for w in range(3)]
+        dev.set_kernel_timing(True)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        for i in range(a.steps):
+            step(i)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        dev.set_kernel_timing(False)
+        ms = ev0.elapsed_time(ev1)
+        kt = [dev.kernel_time(w) for w in range(3)]
+        cnt = kt[0][1] - base[0][1]
+        gu_ms = (kt[0][0] - base[0][0]) / cnt
+        dn_ms = (kt[1][0] - base[1][0]) / cnt
+        ex_ms = (kt[2][0] - base[2][0]) / cnt
+        touched = [len(np.unique(ids[l].cpu().numpy())) for l in range(len(layers))]
+        # steps cycle through the layers evenly
+        e_avg = float(np.mean([touched[i % len(layers)] for i in range(a.steps)]))
+        gu_bytes = e_avg * 2 * M.byte_size(G.Q4_K, F * D) + n * D + n * K * F  # weights + int8 x in + int8 h out
+        dn_bytes = e_avg * M.byte_size(G.Q4_K, D * F) + n * K * F + n * K * D * 4
+        layer_bytes = e_avg * expert_bytes + NE * D * 4 + 2 * n * D * 4
+        results[n] = dict(
+            tokens_per_s=n * a.steps / (ms / 1e3), ms_per_step=ms / a.steps, experts_touched=e_avg,
+            gateup_us=gu_ms * 1e3, down_us=dn_ms * 1e3, experts_us=ex_ms * 1e3,
+            gateup_GBs=gu_bytes / (gu_ms / 1e3) / 1e9, down_GBs=dn_bytes / (dn_ms / 1e3) / 1e9,
+            layer_GBs=layer_bytes / (ms / a.steps / 1e3) / 1e9, gateup_bytes=gu_bytes)
+        log(f"n={n}: {results[n]['tokens_per_s']:.0f} tok/s, {ms / a.steps * 1e3:.1f} us/step, "
+            f"E={e_avg:.2f}, gate/up {gu_ms * 1e3:.1f} us ({results[n]['gateup_GBs']:.0f} GB/s), "
+            f"down {dn_ms * 1e3:.1f} us ({results[n]['down_GBs']:.0f} GB/s), layer {results[n]['layer_GBs']:.0f} GB/s")
+
+    cpu = None
+    if not a.no_cpu:
+        from oracle import oracle as O
+        n = a.batch
+        hs_np = M.fill_gaussian(SEED + 0x200 + n, n * D, 0.0, 1.0, threads).reshape(n, D)
+        L = dict(d=D, f=F, ne=NE, k=K, packed=1 if math == G.MATH_PACKED else 0,
+                 router=layers[0].router, qtypes=(G.Q4_K,) * 3, **mats)
+        reps, t0 = 0, time.time()
+        while True:
+            O.feed_forward_batch(L, hs_np, threads=threads)
+            reps += 1
+            if time.time() - t0 >= a.cpu_seconds:
+                break
+        wall = time.time() - t0
+        cpu = {"value": n * reps / wall, "unit": "tokens/s", "cores": threads, "kind": "port",
+               "sample": f"{reps} calls of the C2 layer at batch {n} (layer 0), oracle restatement of "
+                         f"quant::matmul's packed int8 path, rows split over {threads} threads, {wall:.1f}s wall"}
+        log(f"cpu baseline: {cpu['value']:.1f} tok/s on {threads} threads")
+
+    r = results[a.batch]
+    gu_s = r["gateup_us"] / 1e6
+    line = {
+        "metric": "MoE-layer tokens/s (Q4_K Mixtral-shape decode, 1 MI355X)",
+        "value": r["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": r["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8" if math == G.MATH_PACKED else "f32",
+        "data": "synthetic (N(0,0.02^2) weights quantised to Q4_K by this build; N(0,1) activations)",
+        "config": {"workload": f"C2 decode: Mixtral-shape MoE layer d4096 f14336 8 experts top-2 Q4_K, "
+                               f"batch {a.batch}, {a.layers} HBM copies rotated",
+                   "batch": a.batch, "d_model": D, "d_ff": F, "n_experts": NE, "top_k": K, "qtype": "Q4_K",
+                   "math": a.math},
+        "roofline": {"bound": "hbm", "kernel": "k_gateup_packed<Q4_K>" if math == G.MATH_PACKED else "k_gateup_f32<Q4_K>",
+                     "achieved": r["gateup_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": r["gateup_GBs"] / HBM_PEAK_GBS, "traffic": None,
+                     "bytes_per_launch": r["gateup_bytes"], "avg_launch_us": r["gateup_us"]},
+        "cpu_baseline": cpu,
+        "sweep": {str(n): {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res.items()}
+                  for n, res in results.items()},
+    }
+    print(json.dumps(line), flush=True)
+    for l in layers:
+        l.release()
+    dev.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,79 @@
+"""ctypes binding of include/garuda_moe.h (libgaruda_moe.so, built in-tree).
+
+Loading fails loudly: there is no fallback path. If the library is missing,
+build it with `python -m garuda_amd.build`.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libgaruda_moe.so"
+
+u32, u64, i32, f32p, u32p = C.c_uint32, C.c_uint64, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_uint32)
+vp = C.c_void_p
+
+
+class GmoeTensor(C.Structure):
+    _fields_ = [("qtype", u32), ("layout", u32), ("data", vp), ("experts", C.POINTER(vp))]
+
+
+class GmoeLayerDesc(C.Structure):
+    _fields_ = [
+        ("d_model", u32), ("d_ff", u32), ("n_experts", u32), ("top_k", u32),
+        ("gating", u32), ("combine", u32), ("math", u32),
+        ("router", f32p),
+        ("gate", GmoeTensor), ("up", GmoeTensor), ("down", GmoeTensor),
+    ]
+
+
+class GmoeSlabStats(C.Structure):
+    _fields_ = [("hits", u64), ("misses", u64), ("evictions", u64), ("entries", u64),
+                ("bytes", u64), ("capacity", u64), ("h2d_bytes", u64)]
+
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "gmoe_abi_version": (u32, []),
+    "gmoe_last_error": (C.c_char_p, []),
+    "gmoe_init": (i32, [i32, u64, C.POINTER(vp)]),
+    "gmoe_shutdown": (None, [vp]),
+    "gmoe_layer_register": (i32, [vp, C.POINTER(GmoeLayerDesc), u32p]),
+    "gmoe_layer_release": (i32, [vp, u32]),
+    "gmoe_ffn_forward": (i32, [vp, u32, f32p, u32, f32p, u32p, f32p]),
+    "gmoe_ffn_forward_logits": (i32, [vp, u32, f32p, f32p, u32, f32p, u32p, f32p]),
+    "gmoe_ffn_forward_async": (i32, [vp, u32, vp, vp, u32, vp, vp, vp, vp]),
+    "gmoe_expert_prefetch": (i32, [vp, u32, u32]),
+    "gmoe_expert_is_resident": (i32, [vp, u32, u32]),
+    "gmoe_expert_evict": (i32, [vp, u32, u32]),
+    "gmoe_slab_get_stats": (i32, [vp, C.POINTER(GmoeSlabStats)]),
+    "gmoe_dequant": (i32, [vp, u32, vp, u64, u64, f32p]),
+    "gmoe_matmul": (i32, [vp, u32, u32, vp, u64, u32, u32, f32p, u32, f32p]),
+    "gmoe_route": (i32, [vp, u32, f32p, f32p, u32, u32, u32, u32, u32p, f32p, f32p]),
+    "gmoe_dispatch": (i32, [vp, u32p, f32p, u32, u32, u32, u32p, u32p, f32p, u32p]),
+    "gmoe_expf": (i32, [vp, f32p, u64, f32p]),
+    "gmoe_quantize": (i32, [u32, f32p, u64, vp, i32]),
+    "gmoe_fill_gaussian": (i32, [u64, C.c_float, C.c_float, u64, f32p, i32]),
+    "gmoe_set_kernel_timing": (i32, [vp, i32]),
+    "gmoe_kernel_time": (i32, [vp, u32, C.POINTER(C.c_double), C.POINTER(u64)]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded library with typed entry points. Raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: the MI355X path has no fallback. "
+                "Build it with `python -m garuda_amd.build`."
+            )
+        h = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = h
+    return _lib

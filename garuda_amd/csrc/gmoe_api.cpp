@@ -1,0 +1,915 @@
+// gmoe_api.cpp — host runtime behind include/garuda_moe.h.
+//
+// Owns the device context, the HBM expert slab (the L1 tier: cache::ExpertCache's
+// byte-budgeted LRU, garuda/src/cache/mod.rs:18-137, holding still-packed experts),
+// the per-context scratch arena, and the launch sequence of one feed-forward call:
+//   route -> dispatch -> (activation quantiser) -> gate/up -> down -> combine.
+// Every entry validates before touching the device so a refused call changes nothing
+// (garuda/src/llama/mod.rs:1160-1172), and reports errors as status codes with a
+// thread-local message (never aborts; core/mod.rs:255-258).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <list>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/garuda_moe.h"
+#include "gmoe_internal.h"
+
+using namespace gmoe;
+
+namespace {
+
+thread_local std::string g_err;
+
+gmoe_status fail(gmoe_status s, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return s;
+}
+
+#define HIP_TRY(expr)                                                                    \
+  do {                                                                                   \
+    hipError_t e_ = (expr);                                                              \
+    if (e_ != hipSuccess)                                                                \
+      return fail(GMOE_ERR_DEVICE, "%s failed: %s", #expr, hipGetErrorString(e_));       \
+  } while (0)
+
+const char* type_name(uint32_t t) {
+  switch (t) {
+    case F32: return "F32";
+    case F16: return "F16";
+    case Q4_0: return "Q4_0";
+    case 3: return "Q4_1";
+    case 6: return "Q5_0";
+    case 7: return "Q5_1";
+    case Q8_0: return "Q8_0";
+    case Q2_K: return "Q2_K";
+    case Q3_K: return "Q3_K";
+    case Q4_K: return "Q4_K";
+    case Q5_K: return "Q5_K";
+    case Q6_K: return "Q6_K";
+  }
+  return "unknown";
+}
+
+// quant/mod.rs:89-98
+gmoe_status byte_size(uint32_t t, uint64_t n, uint64_t* out) {
+  uint32_t e, b;
+  if (!block_layout(t, &e, &b))
+    return fail(GMOE_ERR_MODEL, "tensor type %s (%u) is not supported", type_name(t), t);
+  if (n % e != 0)
+    return fail(GMOE_ERR_MODEL, "%s tensor has %llu elements, not a multiple of the block size %u",
+                type_name(t), (unsigned long long)n, e);
+  *out = n / e * b;
+  return GMOE_OK;
+}
+
+// Kernels walk F32/F16 rows 32 values at a time and the activation quantiser works per
+// 32, so every product's K must be a multiple of 32 (true of every k-quant row).
+bool k_ok(uint32_t t, uint32_t K) {
+  uint32_t e, b;
+  block_layout(t, &e, &b);
+  return K % 32 == 0 && K % e == 0;
+}
+
+struct Slab {
+  uint8_t* base = nullptr;
+  uint64_t cap = 0;
+  std::map<uint64_t, uint64_t> free_;  // offset -> size
+  uint64_t used = 0;
+
+  bool alloc(uint64_t size, uint64_t* off) {
+    size = (size + 255) & ~uint64_t(255);
+    for (auto it = free_.begin(); it != free_.end(); ++it) {
+      if (it->second >= size) {
+        *off = it->first;
+        uint64_t rest = it->second - size, noff = it->first + size;
+        free_.erase(it);
+        if (rest) free_[noff] = rest;
+        used += size;
+        return true;
+      }
+    }
+    return false;
+  }
+  void release(uint64_t off, uint64_t size) {
+    size = (size + 255) & ~uint64_t(255);
+    used -= size;
+    auto it = free_.emplace(off, size).first;
+    auto nx = std::next(it);
+    if (nx != free_.end() && it->first + it->second == nx->first) {
+      it->second += nx->second;
+      free_.erase(nx);
+    }
+    if (it != free_.begin()) {
+      auto pv = std::prev(it);
+      if (pv->first + pv->second == it->first) {
+        pv->second += it->second;
+        free_.erase(it);
+      }
+    }
+  }
+};
+
+struct Proj {
+  uint32_t qtype, rows, cols;
+  uint64_t row_bytes, pitch, bytes_dev;  // bytes_dev = rows*pitch + 256 pad
+  std::vector<const uint8_t*> host;      // per expert
+};
+
+struct Layer {
+  uint32_t d, f, ne, k, gating, combine, math;
+  Proj p[3];                      // gate, up, down
+  float* router = nullptr;        // device
+  const uint8_t** eptr = nullptr; // device [3][ne]
+  std::vector<const uint8_t*> eptr_host;
+  std::vector<int64_t> slot;      // per expert: slab offset or -1
+  uint64_t expert_bytes = 0;
+  bool alive = true;
+};
+
+struct Timing {
+  hipEvent_t a, b, c;
+};
+
+}  // namespace
+
+struct gmoe_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipStream_t copy_stream = nullptr;
+  std::mutex mu;
+  Slab slab;
+  std::vector<std::unique_ptr<Layer>> layers;
+  std::list<std::pair<uint32_t, uint32_t>> lru;  // (layer, expert), least recent first
+  gmoe_slab_stats stats{};
+  uint8_t* pinned = nullptr;
+  size_t pinned_bytes = 0;
+  hipEvent_t pin_ev[2]{};
+  // scratch arena
+  uint8_t* scratch = nullptr;
+  size_t scratch_bytes = 0;
+  // timing
+  bool timing = false;
+  std::vector<Timing> pending;
+  std::vector<Timing> pool;
+  double t_ms[3] = {0, 0, 0};
+  uint64_t t_cnt = 0;
+};
+
+namespace {
+
+// ---- staging: host packed rows -> slab at row pitch, through pinned memory ----
+gmoe_status stage_proj(gmoe_ctx* c, const Proj& P, const uint8_t* src, uint8_t* dst) {
+  const size_t chunk = c->pinned_bytes / 2;
+  size_t rows_per = std::max<size_t>(1, chunk / P.pitch);
+  int buf = 0;
+  for (uint32_t r0 = 0; r0 < P.rows; r0 += (uint32_t)rows_per, buf ^= 1) {
+    uint32_t nr = (uint32_t)std::min<size_t>(rows_per, P.rows - r0);
+    HIP_TRY(hipEventSynchronize(c->pin_ev[buf]));
+    uint8_t* pin = c->pinned + buf * chunk;
+    if (P.pitch == P.row_bytes) {
+      memcpy(pin, src + (size_t)r0 * P.row_bytes, (size_t)nr * P.row_bytes);
+    } else {
+      for (uint32_t r = 0; r < nr; r++) {
+        memcpy(pin + (size_t)r * P.pitch, src + (size_t)(r0 + r) * P.row_bytes, P.row_bytes);
+        memset(pin + (size_t)r * P.pitch + P.row_bytes, 0, P.pitch - P.row_bytes);
+      }
+    }
+    HIP_TRY(hipMemcpyAsync(dst + (size_t)r0 * P.pitch, pin, (size_t)nr * P.pitch,
+                           hipMemcpyHostToDevice, c->copy_stream));
+    HIP_TRY(hipEventRecord(c->pin_ev[buf], c->copy_stream));
+  }
+  c->stats.h2d_bytes += (uint64_t)P.rows * P.pitch;
+  return GMOE_OK;
+}
+
+void touch(gmoe_ctx* c, uint32_t l, uint32_t e) {
+  for (auto it = c->lru.begin(); it != c->lru.end(); ++it)
+    if (it->first == l && it->second == e) {
+      c->lru.erase(it);
+      break;
+    }
+  c->lru.emplace_back(l, e);
+}
+
+gmoe_status evict(gmoe_ctx* c, uint32_t l, uint32_t e) {
+  Layer& L = *c->layers[l];
+  if (L.slot[e] < 0) return GMOE_OK;
+  // the slab region may still be read by queued work
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  c->slab.release((uint64_t)L.slot[e], L.expert_bytes);
+  L.slot[e] = -1;
+  for (int p = 0; p < 3; p++) L.eptr_host[p * L.ne + e] = nullptr;
+  HIP_TRY(hipMemcpy(L.eptr, L.eptr_host.data(), L.eptr_host.size() * sizeof(void*), hipMemcpyHostToDevice));
+  for (auto it = c->lru.begin(); it != c->lru.end(); ++it)
+    if (it->first == l && it->second == e) {
+      c->lru.erase(it);
+      break;
+    }
+  c->stats.entries--;
+  c->stats.bytes -= L.expert_bytes;
+  return GMOE_OK;
+}
+
+// Make expert e of layer l resident. `pinned_set` marks experts of the current call that
+// must not be evicted to make room. evict_ok = false only fills free space.
+gmoe_status make_resident(gmoe_ctx* c, uint32_t l, uint32_t e, bool evict_ok,
+                          const std::vector<std::pair<uint32_t, uint32_t>>* keep) {
+  Layer& L = *c->layers[l];
+  if (L.slot[e] >= 0) {
+    touch(c, l, e);
+    return GMOE_OK;
+  }
+  uint64_t off;
+  while (!c->slab.alloc(L.expert_bytes, &off)) {
+    if (!evict_ok) return fail(GMOE_ERR_CACHE, "HBM slab is full");
+    auto victim = c->lru.end();
+    for (auto it = c->lru.begin(); it != c->lru.end(); ++it) {
+      bool kept = false;
+      if (keep)
+        for (auto& kp : *keep) kept |= (kp == *it);
+      if (!kept) {
+        victim = it;
+        break;
+      }
+    }
+    if (victim == c->lru.end())
+      return fail(GMOE_ERR_CACHE, "HBM slab of %llu bytes cannot hold the experts this call needs",
+                  (unsigned long long)c->slab.cap);
+    auto v = *victim;
+    gmoe_status s = evict(c, v.first, v.second);
+    if (s) return s;
+    c->stats.evictions++;
+  }
+  uint8_t* base = c->slab.base + off;
+  uint64_t o = 0;
+  for (int p = 0; p < 3; p++) {
+    gmoe_status s = stage_proj(c, L.p[p], L.p[p].host[e], base + o);
+    if (s) {
+      c->slab.release(off, L.expert_bytes);
+      return s;
+    }
+    L.eptr_host[p * L.ne + e] = base + o;
+    o += (L.p[p].bytes_dev + 255) & ~uint64_t(255);
+  }
+  HIP_TRY(hipStreamSynchronize(c->copy_stream));
+  HIP_TRY(hipMemcpy(L.eptr, L.eptr_host.data(), L.eptr_host.size() * sizeof(void*), hipMemcpyHostToDevice));
+  L.slot[e] = (int64_t)off;
+  c->lru.emplace_back(l, e);
+  c->stats.entries++;
+  c->stats.bytes += L.expert_bytes;
+  return GMOE_OK;
+}
+
+// ---- scratch arena ----
+struct ScratchPlan {
+  size_t total = 0;
+  size_t add(size_t bytes) {
+    size_t o = total;
+    total += (bytes + 255) & ~size_t(255);
+    return o;
+  }
+};
+
+struct Carved {
+  FwdBufs B;
+  float* d_hs;
+  float* d_out;
+  float* d_logits_in;
+};
+
+size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
+  ScratchPlan P;
+  uint64_t nk = (uint64_t)n * L.k;
+  size_t o_hs = P.add((size_t)n * L.d * 4), o_out = P.add((size_t)n * L.d * 4);
+  size_t o_lin = P.add((size_t)n * L.ne * 4);
+  size_t o_ids = P.add(nk * 4), o_w = P.add(nk * 4), o_lg = P.add((size_t)n * L.ne * 4);
+  size_t o_xq = P.add((size_t)n * L.d), o_xs = P.add((size_t)n * (L.d / 32) * 4);
+  size_t o_x16 = P.add((size_t)n * (L.d / 16) * 4);
+  size_t o_off = P.add((L.ne + 1) * 4), o_act = P.add((L.ne + 1) * 4);
+  size_t o_st = P.add(nk * 4), o_sw = P.add(nk * 4), o_sr = P.add(nk * 4), o_so = P.add(nk * 4);
+  size_t o_hq = P.add(nk * L.f), o_hsc = P.add(nk * (L.f / 32) * 4), o_h16 = P.add(nk * (L.f / 16) * 4);
+  size_t o_hf = P.add(nk * L.f * 4), o_y = P.add(nk * L.d * 4);
+  if (cv && base) {
+    FwdBufs& B = cv->B;
+    memset(&B, 0, sizeof B);
+    cv->d_hs = (float*)(base + o_hs);
+    cv->d_out = (float*)(base + o_out);
+    cv->d_logits_in = (float*)(base + o_lin);
+    B.ids = (uint32_t*)(base + o_ids);
+    B.w = (float*)(base + o_w);
+    B.logits = (float*)(base + o_lg);
+    B.xq = (int8_t*)(base + o_xq);
+    B.xs = (float*)(base + o_xs);
+    B.x16 = (int32_t*)(base + o_x16);
+    B.offsets = (uint32_t*)(base + o_off);
+    B.active = (uint32_t*)(base + o_act);
+    B.slot_tok = (uint32_t*)(base + o_st);
+    B.slot_w = (float*)(base + o_sw);
+    B.slot_rank = (uint32_t*)(base + o_sr);
+    B.slot_of = (uint32_t*)(base + o_so);
+    B.hq = (int8_t*)(base + o_hq);
+    B.hsc = (float*)(base + o_hsc);
+    B.h16 = (int32_t*)(base + o_h16);
+    B.hf = (float*)(base + o_hf);
+    B.y = (float*)(base + o_y);
+  }
+  return P.total;
+}
+
+gmoe_status ensure_scratch(gmoe_ctx* c, size_t bytes) {
+  if (bytes <= c->scratch_bytes) return GMOE_OK;
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  if (c->scratch) HIP_TRY(hipFree(c->scratch));
+  c->scratch = nullptr;
+  c->scratch_bytes = 0;
+  size_t want = std::max(bytes, (size_t)64 << 20);
+  HIP_TRY(hipMalloc(&c->scratch, want));
+  c->scratch_bytes = want;
+  return GMOE_OK;
+}
+
+LayerDev layer_dev(const Layer& L) {
+  LayerDev D;
+  D.d = L.d; D.f = L.f; D.ne = L.ne; D.k = L.k;
+  D.gating = L.gating; D.combine = L.combine; D.math = L.math;
+  D.qt_gate = L.p[0].qtype; D.qt_up = L.p[1].qtype; D.qt_down = L.p[2].qtype;
+  D.router = L.router;
+  D.eptr = L.eptr;
+  D.pitch_gate = (uint32_t)L.p[0].pitch;
+  D.pitch_up = (uint32_t)L.p[1].pitch;
+  D.pitch_down = (uint32_t)L.p[2].pitch;
+  return D;
+}
+
+bool uses_int8(uint32_t math, uint32_t qt) { return math == GMOE_MATH_PACKED && has_int8_kernel(qt); }
+
+Timing take_timing(gmoe_ctx* c) {
+  if (!c->pool.empty()) {
+    Timing t = c->pool.back();
+    c->pool.pop_back();
+    return t;
+  }
+  Timing t;
+  hipEventCreate(&t.a);
+  hipEventCreate(&t.b);
+  hipEventCreate(&t.c);
+  return t;
+}
+
+// The launch sequence of one call. B's activation/output pointers are set by the caller.
+gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStream_t st) {
+  LayerDev D = layer_dev(L);
+  // int8 h only when the down product reads it; f32 h otherwise
+  if (!uses_int8(L.math, L.p[2].qtype)) {
+    B.hq = nullptr;
+    B.hsc = nullptr;
+    B.h16 = nullptr;
+  } else {
+    B.hf = nullptr;
+  }
+  HIP_TRY(launch_route(D, B, n, st));
+  HIP_TRY(launch_dispatch(D, B, n, st));
+  if (uses_int8(L.math, L.p[0].qtype)) HIP_TRY(launch_quant_act(B.hs, n, L.d, B.xq, B.xs, B.x16, st));
+  Timing tm{};
+  if (c->timing) {
+    tm = take_timing(c);
+    HIP_TRY(hipEventRecord(tm.a, st));
+  }
+  HIP_TRY(launch_gateup(D, B, n, st));
+  if (c->timing) HIP_TRY(hipEventRecord(tm.b, st));
+  HIP_TRY(launch_down(D, B, n, st));
+  if (c->timing) {
+    HIP_TRY(hipEventRecord(tm.c, st));
+    c->pending.push_back(tm);
+  }
+  HIP_TRY(launch_combine(D, B, n, st));
+  return GMOE_OK;
+}
+
+gmoe_status check_ctx(gmoe_ctx* c) {
+  if (!c) return fail(GMOE_ERR_INFERENCE, "null context");
+  return GMOE_OK;
+}
+
+gmoe_status get_layer(gmoe_ctx* c, uint32_t id, Layer** out) {
+  if (id >= c->layers.size() || !c->layers[id] || !c->layers[id]->alive)
+    return fail(GMOE_ERR_INFERENCE, "unknown layer id %u", id);
+  *out = c->layers[id].get();
+  return GMOE_OK;
+}
+
+gmoe_status forward_host(gmoe_ctx* c, uint32_t lid, const float* hs, const float* logits, uint32_t n,
+                         float* out, uint32_t* ids, float* w) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (!hs || !out) return fail(GMOE_ERR_INFERENCE, "null activation pointer");
+  if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
+  std::lock_guard<std::mutex> g(c->mu);
+  Layer* L;
+  if (gmoe_status s = get_layer(c, lid, &L)) return s;
+  HIP_TRY(hipSetDevice(c->device));
+  Carved cv;
+  size_t need = plan_scratch(*L, n, nullptr, nullptr);
+  if (gmoe_status s = ensure_scratch(c, need)) return s;
+  plan_scratch(*L, n, &cv, c->scratch);
+  hipStream_t st = c->stream;
+  HIP_TRY(hipMemcpyAsync(cv.d_hs, hs, (size_t)n * L->d * 4, hipMemcpyHostToDevice, st));
+  FwdBufs B = cv.B;
+  B.hs = cv.d_hs;
+  B.out = cv.d_out;
+  B.logits_in = nullptr;
+  if (logits) {
+    HIP_TRY(hipMemcpyAsync(cv.d_logits_in, logits, (size_t)n * L->ne * 4, hipMemcpyHostToDevice, st));
+    B.logits_in = cv.d_logits_in;
+  }
+  // residency: route first if anything is missing, then stage exactly what is routed
+  bool all = true;
+  for (uint32_t e = 0; e < L->ne; e++) all &= L->slot[e] >= 0;
+  std::vector<uint32_t> hid((size_t)n * L->k);
+  if (!all) {
+    LayerDev D = layer_dev(*L);
+    HIP_TRY(launch_route(D, B, n, st));
+    HIP_TRY(hipMemcpyAsync(hid.data(), B.ids, hid.size() * 4, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    std::vector<std::pair<uint32_t, uint32_t>> keep;
+    for (uint32_t v : hid) {
+      auto kp = std::make_pair(lid, v);
+      if (std::find(keep.begin(), keep.end(), kp) == keep.end()) keep.push_back(kp);
+    }
+    for (auto& kp : keep) {
+      if (L->slot[kp.second] >= 0) c->stats.hits++;
+      else c->stats.misses++;
+      if (gmoe_status s = make_resident(c, lid, kp.second, true, &keep)) return s;
+    }
+  } else {
+    for (uint32_t e = 0; e < L->ne; e++) touch(c, lid, e);
+  }
+  if (gmoe_status s = run_layer(c, *L, B, n, st)) return s;
+  HIP_TRY(hipMemcpyAsync(out, B.out, (size_t)n * L->d * 4, hipMemcpyDeviceToHost, st));
+  if (ids) HIP_TRY(hipMemcpyAsync(ids, B.ids, (size_t)n * L->k * 4, hipMemcpyDeviceToHost, st));
+  if (w) HIP_TRY(hipMemcpyAsync(w, B.w, (size_t)n * L->k * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (all) {
+    // every routed expert was a hit
+    c->stats.hits += 0;
+  }
+  return GMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t gmoe_abi_version(void) { return GMOE_ABI_VERSION; }
+
+const char* gmoe_last_error(void) { return g_err.c_str(); }
+
+gmoe_status gmoe_init(int device, uint64_t slab_bytes, gmoe_ctx** out) {
+  if (!out) return fail(GMOE_ERR_INFERENCE, "null output pointer");
+  *out = nullptr;
+  int count = 0;
+  HIP_TRY(hipGetDeviceCount(&count));
+  if (device < 0 || device >= count) return fail(GMOE_ERR_DEVICE, "device %d not present (%d visible)", device, count);
+  HIP_TRY(hipSetDevice(device));
+  std::unique_ptr<gmoe_ctx> c(new gmoe_ctx);
+  c->device = device;
+  HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+  HIP_TRY(hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking));
+  if (slab_bytes) {
+    if (hipMalloc(&c->slab.base, slab_bytes) != hipSuccess)
+      return fail(GMOE_ERR_CACHE, "cannot reserve an HBM slab of %llu bytes", (unsigned long long)slab_bytes);
+    c->slab.cap = slab_bytes;
+    c->slab.free_[0] = slab_bytes;
+  }
+  c->stats.capacity = slab_bytes;
+  c->pinned_bytes = (size_t)64 << 20;
+  HIP_TRY(hipHostMalloc((void**)&c->pinned, c->pinned_bytes, hipHostMallocDefault));
+  HIP_TRY(hipEventCreateWithFlags(&c->pin_ev[0], hipEventDisableTiming));
+  HIP_TRY(hipEventCreateWithFlags(&c->pin_ev[1], hipEventDisableTiming));
+  HIP_TRY(hipEventRecord(c->pin_ev[0], c->copy_stream));
+  HIP_TRY(hipEventRecord(c->pin_ev[1], c->copy_stream));
+  *out = c.release();
+  return GMOE_OK;
+}
+
+void gmoe_shutdown(gmoe_ctx* c) {
+  if (!c) return;
+  hipSetDevice(c->device);
+  hipStreamSynchronize(c->stream);
+  hipStreamSynchronize(c->copy_stream);
+  for (auto& L : c->layers)
+    if (L) {
+      hipFree(L->router);
+      hipFree((void*)L->eptr);
+    }
+  for (auto& t : c->pending) c->pool.push_back(t);
+  for (auto& t : c->pool) {
+    hipEventDestroy(t.a);
+    hipEventDestroy(t.b);
+    hipEventDestroy(t.c);
+  }
+  if (c->slab.base) hipFree(c->slab.base);
+  if (c->scratch) hipFree(c->scratch);
+  if (c->pinned) hipHostFree(c->pinned);
+  hipEventDestroy(c->pin_ev[0]);
+  hipEventDestroy(c->pin_ev[1]);
+  hipStreamDestroy(c->stream);
+  hipStreamDestroy(c->copy_stream);
+  delete c;
+}
+
+gmoe_status gmoe_layer_register(gmoe_ctx* c, const gmoe_layer_desc* desc, uint32_t* layer_id) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (!desc || !layer_id) return fail(GMOE_ERR_INFERENCE, "null descriptor");
+  const gmoe_layer_desc& D = *desc;
+  if (D.d_model == 0 || D.d_ff == 0 || D.n_experts == 0)
+    return fail(GMOE_ERR_CONFIG, "d_model, d_ff and n_experts must be non-zero");
+  if (D.top_k == 0 || D.top_k > D.n_experts)
+    return fail(GMOE_ERR_CONFIG, "top_k (%u) must be in 1..=%u", D.top_k, D.n_experts);
+  if (D.top_k > 32) return fail(GMOE_ERR_CONFIG, "top_k above 32 is not supported");
+  if (D.gating > 3 || D.combine > 1 || D.math > 1) return fail(GMOE_ERR_CONFIG, "unknown gating/combine/math");
+  if (!D.router) return fail(GMOE_ERR_MODEL, "router weights missing");
+  const gmoe_tensor* T[3] = {&D.gate, &D.up, &D.down};
+  std::unique_ptr<Layer> L(new Layer);
+  L->d = D.d_model; L->f = D.d_ff; L->ne = D.n_experts; L->k = D.top_k;
+  L->gating = D.gating; L->combine = D.combine; L->math = D.math;
+  for (int p = 0; p < 3; p++) {
+    Proj& P = L->p[p];
+    P.qtype = T[p]->qtype;
+    P.rows = p < 2 ? D.d_ff : D.d_model;
+    P.cols = p < 2 ? D.d_model : D.d_ff;
+    uint64_t rb;
+    if (gmoe_status s = byte_size(P.qtype, P.cols, &rb)) return s;
+    if (!k_ok(P.qtype, P.cols))
+      return fail(GMOE_ERR_MODEL, "%s rows of %u values: width must be a multiple of 32", type_name(P.qtype), P.cols);
+    P.row_bytes = rb;
+    P.pitch = row_pitch(rb);
+    P.bytes_dev = (uint64_t)P.rows * P.pitch + 256;
+    P.host.resize(L->ne);
+    if (T[p]->layout == GMOE_LAYOUT_STACKED) {
+      if (!T[p]->data) return fail(GMOE_ERR_MODEL, "stacked tensor %d has no data", p);
+      for (uint32_t e = 0; e < L->ne; e++)
+        P.host[e] = (const uint8_t*)T[p]->data + (uint64_t)e * P.rows * rb;
+    } else if (T[p]->layout == GMOE_LAYOUT_SPLIT) {
+      if (!T[p]->experts) return fail(GMOE_ERR_MODEL, "split tensor %d has no expert list", p);
+      for (uint32_t e = 0; e < L->ne; e++) {
+        if (!T[p]->experts[e]) return fail(GMOE_ERR_MODEL, "expert %u of tensor %d is missing", e, p);
+        P.host[e] = (const uint8_t*)T[p]->experts[e];
+      }
+    } else {
+      return fail(GMOE_ERR_CONFIG, "unknown tensor layout %u", T[p]->layout);
+    }
+  }
+  if (L->p[0].qtype != L->p[1].qtype)
+    return fail(GMOE_ERR_MODEL, "gate (%s) and up (%s) must share a type", type_name(L->p[0].qtype),
+                type_name(L->p[1].qtype));
+  if (uses_int8(L->math, L->p[2].qtype) && L->f % 32)
+    return fail(GMOE_ERR_MODEL, "d_ff must be a multiple of 32");
+  for (int p = 0; p < 3; p++) L->expert_bytes += (L->p[p].bytes_dev + 255) & ~uint64_t(255);
+
+  std::lock_guard<std::mutex> g(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  HIP_TRY(hipMalloc(&L->router, (size_t)L->ne * L->d * 4));
+  HIP_TRY(hipMemcpy(L->router, D.router, (size_t)L->ne * L->d * 4, hipMemcpyHostToDevice));
+  L->eptr_host.assign(3 * L->ne, nullptr);
+  HIP_TRY(hipMalloc((void**)&L->eptr, 3 * L->ne * sizeof(void*)));
+  HIP_TRY(hipMemcpy(L->eptr, L->eptr_host.data(), 3 * L->ne * sizeof(void*), hipMemcpyHostToDevice));
+  L->slot.assign(L->ne, -1);
+  uint32_t id = (uint32_t)c->layers.size();
+  c->layers.push_back(std::move(L));
+  Layer& LL = *c->layers.back();
+  for (uint32_t e = 0; e < LL.ne; e++) {
+    gmoe_status s = make_resident(c, id, e, false, nullptr);
+    if (s == GMOE_ERR_CACHE) break;  // the rest stays on the host tier
+    if (s) return s;
+  }
+  *layer_id = id;
+  return GMOE_OK;
+}
+
+gmoe_status gmoe_layer_release(gmoe_ctx* c, uint32_t id) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  std::lock_guard<std::mutex> g(c->mu);
+  Layer* L;
+  if (gmoe_status s = get_layer(c, id, &L)) return s;
+  HIP_TRY(hipSetDevice(c->device));
+  for (uint32_t e = 0; e < L->ne; e++)
+    if (gmoe_status s = evict(c, id, e)) return s;
+  hipFree(L->router);
+  hipFree((void*)L->eptr);
+  L->router = nullptr;
+  L->eptr = nullptr;
+  L->alive = false;
+  return GMOE_OK;
+}
+
+gmoe_status gmoe_ffn_forward(gmoe_ctx* c, uint32_t layer, const float* hs, uint32_t n, float* out,
+                             uint32_t* ids, float* w) {
+  return forward_host(c, layer, hs, nullptr, n, out, ids, w);
+}
+
+gmoe_status gmoe_ffn_forward_logits(gmoe_ctx* c, uint32_t layer, const float* hs, const float* logits,
+                                    uint32_t n, float* out, uint32_t* ids, float* w) {
+  if (!logits) return fail(GMOE_ERR_INFERENCE, "null logits");
+  return forward_host(c, layer, hs, logits, n, out, ids, w);
+}
+
+gmoe_status gmoe_ffn_forward_async(gmoe_ctx* c, uint32_t lid, const float* d_hs, const float* d_logits,
+                                   uint32_t n, float* d_out, uint32_t* d_ids, float* d_w, void* stream) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (!d_hs || !d_out) return fail(GMOE_ERR_INFERENCE, "null activation pointer");
+  if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
+  std::lock_guard<std::mutex> g(c->mu);
+  Layer* L;
+  if (gmoe_status s = get_layer(c, lid, &L)) return s;
+  for (uint32_t e = 0; e < L->ne; e++)
+    if (L->slot[e] < 0) return fail(GMOE_ERR_CACHE, "expert %u of layer %u is not resident", e, lid);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+  size_t need = plan_scratch(*L, n, nullptr, nullptr);
+  if (need > c->scratch_bytes) {
+    // growing the arena frees the old one, which queued work on any stream may use
+    HIP_TRY(hipDeviceSynchronize());
+    if (gmoe_status s = ensure_scratch(c, need)) return s;
+  }
+  Carved cv;
+  plan_scratch(*L, n, &cv, c->scratch);
+  FwdBufs B = cv.B;
+  B.hs = d_hs;
+  B.logits_in = d_logits;
+  B.out = d_out;
+  if (d_ids) B.ids = d_ids;
+  if (d_w) B.w = d_w;
+  return run_layer(c, *L, B, n, st);
+}
+
+gmoe_status gmoe_expert_prefetch(gmoe_ctx* c, uint32_t lid, uint32_t e) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  std::lock_guard<std::mutex> g(c->mu);
+  Layer* L;
+  if (gmoe_status s = get_layer(c, lid, &L)) return s;
+  if (e >= L->ne) return fail(GMOE_ERR_INFERENCE, "expert %u out of range", e);
+  HIP_TRY(hipSetDevice(c->device));
+  std::vector<std::pair<uint32_t, uint32_t>> keep{{lid, e}};
+  return make_resident(c, lid, e, true, &keep);
+}
+
+int gmoe_expert_is_resident(gmoe_ctx* c, uint32_t lid, uint32_t e) {
+  if (!c) return 0;
+  std::lock_guard<std::mutex> g(c->mu);
+  if (lid >= c->layers.size() || !c->layers[lid] || !c->layers[lid]->alive) return 0;
+  Layer& L = *c->layers[lid];
+  return e < L.ne && L.slot[e] >= 0;
+}
+
+gmoe_status gmoe_expert_evict(gmoe_ctx* c, uint32_t lid, uint32_t e) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  std::lock_guard<std::mutex> g(c->mu);
+  Layer* L;
+  if (gmoe_status s = get_layer(c, lid, &L)) return s;
+  if (e >= L->ne) return fail(GMOE_ERR_INFERENCE, "expert %u out of range", e);
+  HIP_TRY(hipSetDevice(c->device));
+  return evict(c, lid, e);
+}
+
+gmoe_status gmoe_slab_get_stats(gmoe_ctx* c, gmoe_slab_stats* out) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (!out) return fail(GMOE_ERR_INFERENCE, "null output");
+  std::lock_guard<std::mutex> g(c->mu);
+  *out = c->stats;
+  return GMOE_OK;
+}
+
+// ---- single steps ----
+
+gmoe_status gmoe_dequant(gmoe_ctx* c, uint32_t qt, const void* blocks, uint64_t nbytes, uint64_t n,
+                         float* out) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  uint64_t want;
+  if (gmoe_status s = byte_size(qt, n, &want)) return s;
+  if (nbytes != want)
+    return fail(GMOE_ERR_MODEL, "%s tensor: expected %llu bytes for %llu elements, got %llu", type_name(qt),
+                (unsigned long long)want, (unsigned long long)n, (unsigned long long)nbytes);
+  if ((qt == F32 || qt == F16) && n % 32)
+    return fail(GMOE_ERR_MODEL, "%s dequant on the device takes multiples of 32 values", type_name(qt));
+  if (n == 0) return GMOE_OK;
+  std::lock_guard<std::mutex> g(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  uint8_t* db = nullptr;
+  float* dout = nullptr;
+  HIP_TRY(hipMalloc(&db, nbytes + 16));
+  hipError_t e1 = hipMalloc(&dout, n * 4);
+  if (e1 != hipSuccess) {
+    hipFree(db);
+    return fail(GMOE_ERR_DEVICE, "hipMalloc: %s", hipGetErrorString(e1));
+  }
+  uint32_t el, by;
+  block_layout(qt, &el, &by);
+  uint64_t nb = (qt == F32 || qt == F16) ? n / 32 : n / el;
+  hipError_t e = hipMemcpy(db, blocks, nbytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = launch_dequant(qt, db, nb, dout, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e == hipSuccess) e = hipMemcpy(out, dout, n * 4, hipMemcpyDeviceToHost);
+  hipFree(db);
+  hipFree(dout);
+  if (e != hipSuccess) return fail(GMOE_ERR_DEVICE, "dequant: %s", hipGetErrorString(e));
+  return GMOE_OK;
+}
+
+gmoe_status gmoe_expf(gmoe_ctx* c, const float* x, uint64_t n, float* y) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (n == 0) return GMOE_OK;
+  std::lock_guard<std::mutex> g(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  float *dx = nullptr, *dy = nullptr;
+  HIP_TRY(hipMalloc(&dx, n * 4));
+  hipError_t e = hipMalloc(&dy, n * 4);
+  if (e == hipSuccess) e = hipMemcpy(dx, x, n * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = launch_expf(dx, dy, n, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e == hipSuccess) e = hipMemcpy(y, dy, n * 4, hipMemcpyDeviceToHost);
+  hipFree(dx);
+  if (dy) hipFree(dy);
+  if (e != hipSuccess) return fail(GMOE_ERR_DEVICE, "expf: %s", hipGetErrorString(e));
+  return GMOE_OK;
+}
+
+// A one-off layer around a single matrix: expert 0's down projection, every vector
+// routed to it, so the split-K down kernel computes out[b*rows + r].
+gmoe_status gmoe_matmul(gmoe_ctx* c, uint32_t qt, uint32_t math, const void* w, uint64_t nbytes, uint32_t rows,
+                        uint32_t cols, const float* xs, uint32_t n, float* out) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (math > 1) return fail(GMOE_ERR_CONFIG, "unknown math");
+  uint64_t rb;
+  if (gmoe_status s = byte_size(qt, cols, &rb)) return s;
+  if (nbytes != rb * rows)
+    return fail(GMOE_ERR_MODEL, "%s matmul: weight is %llu bytes, expected %llu (%u rows x %llu)", type_name(qt),
+                (unsigned long long)nbytes, (unsigned long long)(rb * rows), rows, (unsigned long long)rb);
+  if (!k_ok(qt, cols)) return fail(GMOE_ERR_MODEL, "matmul width must be a multiple of 32");
+  if (n == 0 || rows == 0) return fail(GMOE_ERR_INFERENCE, "matmul dimension mismatch");
+  std::lock_guard<std::mutex> g(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  size_t pitch = row_pitch(rb);
+  size_t wbytes = (size_t)rows * pitch + 256;
+  size_t nb_x = (size_t)n * cols;
+  // device layout: [w][x f32][xq][xs][x16][y][offsets(2)][active(2)][eptr(3)]
+  ScratchPlan P;
+  size_t o_w = P.add(wbytes), o_x = P.add(nb_x * 4), o_q = P.add(nb_x), o_s = P.add(nb_x / 32 * 4),
+         o_16 = P.add(nb_x / 16 * 4), o_y = P.add((size_t)n * rows * 4), o_off = P.add(8), o_act = P.add(8),
+         o_ep = P.add(3 * sizeof(void*));
+  uint8_t* base = nullptr;
+  HIP_TRY(hipMalloc(&base, P.total));
+  std::vector<uint8_t> hw(wbytes, 0);
+  for (uint32_t r = 0; r < rows; r++) memcpy(hw.data() + (size_t)r * pitch, (const uint8_t*)w + (size_t)r * rb, rb);
+  uint32_t offs[2] = {0, n}, act[2] = {1, 0};
+  const uint8_t* ep[3] = {base + o_w, base + o_w, base + o_w};
+  hipError_t e = hipMemcpy(base + o_w, hw.data(), wbytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(base + o_x, xs, nb_x * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(base + o_off, offs, 8, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(base + o_act, act, 8, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(base + o_ep, ep, sizeof ep, hipMemcpyHostToDevice);
+  LayerDev D{};
+  D.d = rows; D.f = cols; D.ne = 1; D.k = 1; D.math = math;
+  D.qt_gate = D.qt_up = D.qt_down = qt;
+  D.eptr = (const uint8_t* const*)(base + o_ep);
+  D.pitch_down = (uint32_t)pitch;
+  FwdBufs B{};
+  B.offsets = (uint32_t*)(base + o_off);
+  B.active = (uint32_t*)(base + o_act);
+  B.y = (float*)(base + o_y);
+  if (uses_int8(math, qt)) {
+    B.hq = (int8_t*)(base + o_q);
+    B.hsc = (float*)(base + o_s);
+    B.h16 = (int32_t*)(base + o_16);
+    if (e == hipSuccess) e = launch_quant_act((const float*)(base + o_x), n, cols, B.hq, B.hsc, B.h16, c->stream);
+  } else {
+    B.hf = (float*)(base + o_x);
+  }
+  if (e == hipSuccess) e = launch_down(D, B, n, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e == hipSuccess) e = hipMemcpy(out, B.y, (size_t)n * rows * 4, hipMemcpyDeviceToHost);
+  hipFree(base);
+  if (e != hipSuccess) return fail(GMOE_ERR_DEVICE, "matmul: %s", hipGetErrorString(e));
+  return GMOE_OK;
+}
+
+gmoe_status gmoe_route(gmoe_ctx* c, uint32_t gating, const float* router, const float* x, uint32_t d, uint32_t ne,
+                       uint32_t k, uint32_t n, uint32_t* ids, float* w, float* logits_out) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (gating > 3) return fail(GMOE_ERR_CONFIG, "unknown gating");
+  if (k == 0 || k > ne || k > 32) return fail(GMOE_ERR_CONFIG, "top_k (%u) must be in 1..=%u", k, ne);
+  if (n == 0 || !x || !ids || !w) return fail(GMOE_ERR_INFERENCE, "bad route arguments");
+  if (router && d % 4) return fail(GMOE_ERR_INFERENCE, "router width must be a multiple of 4");
+  std::lock_guard<std::mutex> g(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  ScratchPlan P;
+  size_t xlen = router ? (size_t)n * d : (size_t)n * ne;
+  size_t o_r = P.add(router ? (size_t)ne * d * 4 : 4), o_x = P.add(xlen * 4), o_i = P.add((size_t)n * k * 4),
+         o_w = P.add((size_t)n * k * 4), o_l = P.add((size_t)n * ne * 4);
+  uint8_t* base = nullptr;
+  HIP_TRY(hipMalloc(&base, P.total));
+  hipError_t e = hipSuccess;
+  if (router) e = hipMemcpy(base + o_r, router, (size_t)ne * d * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(base + o_x, x, xlen * 4, hipMemcpyHostToDevice);
+  LayerDev D{};
+  D.d = d; D.ne = ne; D.k = k; D.gating = gating;
+  D.router = (const float*)(base + o_r);
+  FwdBufs B{};
+  if (router) B.hs = (const float*)(base + o_x);
+  else B.logits_in = (const float*)(base + o_x);
+  B.ids = (uint32_t*)(base + o_i);
+  B.w = (float*)(base + o_w);
+  B.logits = (float*)(base + o_l);
+  if (e == hipSuccess) e = launch_route(D, B, n, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e == hipSuccess) e = hipMemcpy(ids, B.ids, (size_t)n * k * 4, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(w, B.w, (size_t)n * k * 4, hipMemcpyDeviceToHost);
+  if (e == hipSuccess && logits_out) e = hipMemcpy(logits_out, B.logits, (size_t)n * ne * 4, hipMemcpyDeviceToHost);
+  hipFree(base);
+  if (e != hipSuccess) return fail(GMOE_ERR_DEVICE, "route: %s", hipGetErrorString(e));
+  return GMOE_OK;
+}
+
+gmoe_status gmoe_dispatch(gmoe_ctx* c, const uint32_t* ids, const float* w, uint32_t n, uint32_t k, uint32_t ne,
+                          uint32_t* offsets, uint32_t* slot_token, float* slot_weight, uint32_t* slot_rank) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (!ids || !w || !offsets || n == 0 || k == 0 || k > ne) return fail(GMOE_ERR_INFERENCE, "bad dispatch arguments");
+  for (uint64_t i = 0; i < (uint64_t)n * k; i++)
+    if (ids[i] >= ne) return fail(GMOE_ERR_INFERENCE, "expert id %u out of range", ids[i]);
+  std::lock_guard<std::mutex> g(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  size_t nk = (size_t)n * k;
+  ScratchPlan P;
+  size_t o_i = P.add(nk * 4), o_w = P.add(nk * 4), o_off = P.add((ne + 1) * 4), o_act = P.add((ne + 1) * 4),
+         o_st = P.add(nk * 4), o_sw = P.add(nk * 4), o_sr = P.add(nk * 4), o_so = P.add(nk * 4);
+  uint8_t* base = nullptr;
+  HIP_TRY(hipMalloc(&base, P.total));
+  hipError_t e = hipMemcpy(base + o_i, ids, nk * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(base + o_w, w, nk * 4, hipMemcpyHostToDevice);
+  LayerDev D{};
+  D.ne = ne; D.k = k;
+  FwdBufs B{};
+  B.ids = (uint32_t*)(base + o_i);
+  B.w = (float*)(base + o_w);
+  B.offsets = (uint32_t*)(base + o_off);
+  B.active = (uint32_t*)(base + o_act);
+  B.slot_tok = (uint32_t*)(base + o_st);
+  B.slot_w = (float*)(base + o_sw);
+  B.slot_rank = (uint32_t*)(base + o_sr);
+  B.slot_of = (uint32_t*)(base + o_so);
+  if (e == hipSuccess) e = launch_dispatch(D, B, n, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e == hipSuccess) e = hipMemcpy(offsets, B.offsets, (ne + 1) * 4, hipMemcpyDeviceToHost);
+  if (e == hipSuccess && slot_token) e = hipMemcpy(slot_token, B.slot_tok, nk * 4, hipMemcpyDeviceToHost);
+  if (e == hipSuccess && slot_weight) e = hipMemcpy(slot_weight, B.slot_w, nk * 4, hipMemcpyDeviceToHost);
+  if (e == hipSuccess && slot_rank) e = hipMemcpy(slot_rank, B.slot_rank, nk * 4, hipMemcpyDeviceToHost);
+  hipFree(base);
+  if (e != hipSuccess) return fail(GMOE_ERR_DEVICE, "dispatch: %s", hipGetErrorString(e));
+  return GMOE_OK;
+}
+
+gmoe_status gmoe_set_kernel_timing(gmoe_ctx* c, int on) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  std::lock_guard<std::mutex> g(c->mu);
+  c->timing = on != 0;
+  return GMOE_OK;
+}
+
+// which: 0 = gate/up kernel, 1 = down kernel, 2 = both (gate/up start to down end)
+gmoe_status gmoe_kernel_time(gmoe_ctx* c, uint32_t which, double* total_ms, uint64_t* count) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (which > 2 || !total_ms || !count) return fail(GMOE_ERR_INFERENCE, "bad kernel_time arguments");
+  std::lock_guard<std::mutex> g(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  for (auto& t : c->pending) {
+    HIP_TRY(hipEventSynchronize(t.c));
+    float a = 0, b = 0, ab = 0;
+    HIP_TRY(hipEventElapsedTime(&a, t.a, t.b));
+    HIP_TRY(hipEventElapsedTime(&b, t.b, t.c));
+    HIP_TRY(hipEventElapsedTime(&ab, t.a, t.c));
+    c->t_ms[0] += a;
+    c->t_ms[1] += b;
+    c->t_ms[2] += ab;
+    c->t_cnt++;
+    c->pool.push_back(t);
+  }
+  c->pending.clear();
+  *total_ms = c->t_ms[which];
+  *count = c->t_cnt;
+  return GMOE_OK;
+}
+
+}  // extern "C"

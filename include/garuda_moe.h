@@ -1,0 +1,188 @@
+/*
+ * garuda_moe.h — C-ABI of the MI355X mixture-of-experts feed-forward path.
+ *
+ * Drop-in boundary for Garuda's MoE FFN (hanumanit/garuda 0.31.0). The library
+ * replaces the body of `LlamaBackend::feed_forward_batch` for `Ffn::Moe`
+ * (garuda/src/llama/mod.rs:922-997): routing, token->expert dispatch, the
+ * SwiGLU expert products on still-packed GGUF blocks, and the gate-weighted
+ * combine. Everything else in `logits_batch` (llama/mod.rs:1134-1202) stays on
+ * the caller's side, so the plugin contract of `core::InferenceBackend`
+ * (garuda/src/core/mod.rs:232-348) is unchanged.
+ *
+ * Plain C types only. The caller owns every host pointer it passes; the library
+ * owns device memory (the HBM expert slab and per-context scratch). Every entry
+ * point validates its arguments before touching the device, returns a status and
+ * never aborts; a refused call changes nothing (llama/mod.rs:1160-1172).
+ * gmoe_last_error() returns the calling thread's message for the last failure.
+ */
+#ifndef GARUDA_MOE_H
+#define GARUDA_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GMOE_ABI_VERSION 1u
+
+/* Status codes. Mirrors the GarudaError variants the reference returns on this
+ * path (garuda/src/core/mod.rs:10-47). */
+typedef enum gmoe_status {
+  GMOE_OK = 0,
+  GMOE_ERR_MODEL = 1,     /* GarudaError::Model: unsupported ggml type, byte-length mismatch */
+  GMOE_ERR_INFERENCE = 2, /* GarudaError::Inference: n/d mismatch, unknown layer */
+  GMOE_ERR_CACHE = 3,     /* GarudaError::Cache: the HBM slab cannot hold what is asked */
+  GMOE_ERR_CONFIG = 4,    /* GarudaError::Config: top_k outside 1..=n_experts (core/mod.rs:103-108) */
+  GMOE_ERR_DEVICE = 5     /* HIP runtime failure; the context stays usable for teardown */
+} gmoe_status;
+
+/* ggml type ids (garuda/src/quant/mod.rs:22-30). */
+enum {
+  GMOE_F32 = 0, GMOE_F16 = 1, GMOE_Q4_0 = 2, GMOE_Q8_0 = 8, GMOE_Q2_K = 10,
+  GMOE_Q3_K = 11, GMOE_Q4_K = 12, GMOE_Q5_K = 13, GMOE_Q6_K = 14
+};
+
+/* Gating rule. LLAMA is feed_forward_batch's own (llama/mod.rs:938-949: softmax over
+ * all experts, stable sort, top-k, renormalise). The other three are
+ * router::RouterType (garuda/src/router/mod.rs:17-37, :58-118). */
+enum {
+  GMOE_GATING_LLAMA = 0, GMOE_GATING_MIXTRAL = 1, GMOE_GATING_DEEPSEEK = 2, GMOE_GATING_QWEN = 3
+};
+
+/* Order of the weighted sum over a token's experts: ascending expert id
+ * (llama/mod.rs:977-995) or routed rank (moe/mod.rs:104-109). */
+enum { GMOE_COMBINE_EXPERT_ORDER = 0, GMOE_COMBINE_RANK_ORDER = 1 };
+
+/* Arithmetic of the expert products. PACKED is Weight::Packed under `mmap = true`
+ * (llama/mod.rs:175-193 -> quant::matmul, quant/mod.rs:223-304): activations are
+ * quantised to int8 per 32 and dotted with the packed rows for Q8_0 and Q2_K..Q6_K;
+ * Q4_0/F16/F32 dequantise. F32 is Weight::Full under `mmap = false`
+ * (llama/mod.rs:376-381 -> simd::matmul): every weight is the exact dequantised f32. */
+enum { GMOE_MATH_PACKED = 0, GMOE_MATH_F32 = 1 };
+
+/* Expert tensor layout (llama/mod.rs:223-226): one stacked `..._exps` tensor with
+ * expert e at rows [e*rows, (e+1)*rows), or one tensor per expert. */
+enum { GMOE_LAYOUT_STACKED = 0, GMOE_LAYOUT_SPLIT = 1 };
+
+typedef struct gmoe_ctx gmoe_ctx;
+
+typedef struct gmoe_tensor {
+  uint32_t qtype;               /* ggml type id */
+  uint32_t layout;              /* GMOE_LAYOUT_* */
+  const void* data;             /* STACKED: n_experts*rows packed rows */
+  const void* const* experts;   /* SPLIT: n_experts pointers, each `rows` packed rows */
+} gmoe_tensor;
+
+/* One MoE FFN layer: the `Ffn::Moe` arm of llama/mod.rs:495-507. gate/up are
+ * [d_ff x d_model] per expert, down is [d_model x d_ff] (core/mod.rs:181-184). */
+typedef struct gmoe_layer_desc {
+  uint32_t d_model, d_ff, n_experts, top_k;
+  uint32_t gating, combine, math;
+  const float* router;          /* ffn_gate_inp, [n_experts x d_model] f32 row-major */
+  gmoe_tensor gate, up, down;
+} gmoe_layer_desc;
+
+typedef struct gmoe_slab_stats {
+  uint64_t hits, misses, evictions; /* as cache::CacheStats (cache/mod.rs:34-40) */
+  uint64_t entries, bytes, capacity;
+  uint64_t h2d_bytes;               /* bytes staged host->HBM since init */
+} gmoe_slab_stats;
+
+/* ---- context ---- */
+
+/* Open device `device` and reserve an HBM slab of `slab_bytes` for packed experts
+ * (the L1 tier; cache::ExpertCache's byte budget, cache/mod.rs:18-22). */
+gmoe_status gmoe_init(int device, uint64_t slab_bytes, gmoe_ctx** out);
+void gmoe_shutdown(gmoe_ctx* ctx);
+const char* gmoe_last_error(void);
+uint32_t gmoe_abi_version(void);
+
+/* Register a layer. Validates dims and byte lengths (quant::byte_size,
+ * quant/mod.rs:89-98), copies the router to HBM and stages as many experts into
+ * the slab as fit (least recently used first out). The host expert bytes are
+ * borrowed: they must stay valid until gmoe_layer_release, because an evicted
+ * expert is staged again from them. */
+gmoe_status gmoe_layer_register(gmoe_ctx* ctx, const gmoe_layer_desc* desc, uint32_t* layer_id);
+gmoe_status gmoe_layer_release(gmoe_ctx* ctx, uint32_t layer_id);
+
+/* ---- the hot path ---- */
+
+/* feed_forward_batch for n tokens: hs is [n x d_model] (vector-major), out the same.
+ * routed_ids/routed_w (may be NULL) receive each token's top_k experts in ranked
+ * order, the ids the advisory predictor consumes (llama/mod.rs:951-962).
+ * Synchronous; host pointers. */
+gmoe_status gmoe_ffn_forward(gmoe_ctx* ctx, uint32_t layer_id, const float* hs, uint32_t n,
+                             float* out, uint32_t* routed_ids, float* routed_w);
+
+/* As gmoe_ffn_forward, with precomputed router logits [n x n_experts] in place of
+ * the router matvec (llama/mod.rs:939). */
+gmoe_status gmoe_ffn_forward_logits(gmoe_ctx* ctx, uint32_t layer_id, const float* hs,
+                                    const float* logits, uint32_t n, float* out,
+                                    uint32_t* routed_ids, float* routed_w);
+
+/* Device-pointer form: every pointer is device memory, work is queued on `stream`
+ * (a hipStream_t; NULL = the context's own stream) and the call returns without
+ * waiting. Requires every expert of the layer to be resident (GMOE_ERR_CACHE
+ * otherwise). Calls on one context share its scratch, so they must be ordered on
+ * one stream. d_logits may be NULL. */
+gmoe_status gmoe_ffn_forward_async(gmoe_ctx* ctx, uint32_t layer_id, const float* d_hs,
+                                   const float* d_logits, uint32_t n, float* d_out,
+                                   uint32_t* d_routed_ids, float* d_routed_w, void* stream);
+
+/* ---- the L1 tier (core::ExpertLoader, core/mod.rs:215-223) ---- */
+gmoe_status gmoe_expert_prefetch(gmoe_ctx* ctx, uint32_t layer_id, uint32_t expert);
+int gmoe_expert_is_resident(gmoe_ctx* ctx, uint32_t layer_id, uint32_t expert);
+gmoe_status gmoe_expert_evict(gmoe_ctx* ctx, uint32_t layer_id, uint32_t expert);
+gmoe_status gmoe_slab_get_stats(gmoe_ctx* ctx, gmoe_slab_stats* out);
+
+/* ---- single steps of the path, for parity tests (host pointers, synchronous) ---- */
+
+/* quant::dequantize (quant/mod.rs:104-114) on the device: n_elems values of qtype. */
+gmoe_status gmoe_dequant(gmoe_ctx* ctx, uint32_t qtype, const void* blocks, uint64_t nbytes,
+                         uint64_t n_elems, float* out);
+
+/* quant::matmul (quant/mod.rs:223-304) for math = PACKED, simd::matmul over the
+ * dequantised rows for math = F32: out[b*rows + r] = dot(row r, xs[b]). */
+gmoe_status gmoe_matmul(gmoe_ctx* ctx, uint32_t qtype, uint32_t math, const void* w,
+                        uint64_t nbytes, uint32_t rows, uint32_t cols, const float* xs,
+                        uint32_t n, float* out);
+
+/* Router logits (when router != NULL; otherwise `x` already holds [n x ne] logits),
+ * then gating: ids/w are [n x top_k] in ranked order; logits_out (may be NULL)
+ * receives the [n x ne] logits. */
+gmoe_status gmoe_route(gmoe_ctx* ctx, uint32_t gating, const float* router, const float* x,
+                       uint32_t d, uint32_t ne, uint32_t top_k, uint32_t n, uint32_t* ids,
+                       float* w, float* logits_out);
+
+/* Routing inversion (llama/mod.rs:966-972) as a stable counting sort: offsets[ne+1],
+ * and for each slot in [0, n*k): its token, its routing weight and its rank. */
+gmoe_status gmoe_dispatch(gmoe_ctx* ctx, const uint32_t* ids, const float* w, uint32_t n,
+                          uint32_t top_k, uint32_t ne, uint32_t* offsets, uint32_t* slot_token,
+                          float* slot_weight, uint32_t* slot_rank);
+
+/* The device exp used by softmax and SiLU, applied elementwise. */
+gmoe_status gmoe_expf(gmoe_ctx* ctx, const float* x, uint64_t n, float* y);
+
+/* ---- build-side data preparation (host code; the reference has no quantiser) ---- */
+
+/* Quantise n f32 values (n a multiple of the block size) into `out`
+ * (byte_size(qtype, n) bytes). Round-to-nearest min/max quantisers; see DESIGN. */
+gmoe_status gmoe_quantize(uint32_t qtype, const float* x, uint64_t n, void* out, int threads);
+
+/* n values of N(mean, std^2) from a counter-based splitmix64 stream keyed by seed. */
+gmoe_status gmoe_fill_gaussian(uint64_t seed, float mean, float std, uint64_t n, float* out,
+                               int threads);
+
+/* ---- measurement ---- */
+
+/* When on, every forward records HIP events around the dominant expert kernels on
+ * the stream they run on; gmoe_kernel_time returns their accumulated milliseconds. */
+gmoe_status gmoe_set_kernel_timing(gmoe_ctx* ctx, int on);
+gmoe_status gmoe_kernel_time(gmoe_ctx* ctx, uint32_t which, double* total_ms, uint64_t* count);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
