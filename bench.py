@@ -88,7 +88,10 @@ def main():
                                  (G.Q4_K,) * 3, math=math))
     log(f"{a.layers} layers staged into HBM in {time.time() - t0:.1f}s")
 
-    stream = torch.cuda.current_stream()
+    # a stream of its own (default priority): torch's default stream is the null stream,
+    # which the library's non-blocking streams do not order against
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
     sh = stream.cuda_stream
     results = {}
     batches = sorted(set([a.batch] + [int(b) for b in a.sweep.split(",") if b]))

@@ -302,7 +302,7 @@ size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
   size_t o_off = P.add((L.ne + 1) * 4), o_act = P.add((L.ne + 1) * 4);
   size_t o_st = P.add(nk * 4), o_sw = P.add(nk * 4), o_sr = P.add(nk * 4), o_so = P.add(nk * 4);
   size_t o_hq = P.add(nk * L.f), o_hsc = P.add(nk * (L.f / 32) * 4), o_h16 = P.add(nk * (L.f / 16) * 4);
-  size_t o_hf = P.add(nk * L.f * 4), o_y = P.add(nk * L.d * 4);
+  size_t o_hf = P.add(nk * L.f * 4), o_y = P.add(kMaxKsg * nk * L.d * 4);
   if (cv && base) {
     FwdBufs& B = cv->B;
     memset(&B, 0, sizeof B);
@@ -381,9 +381,14 @@ gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStr
   } else {
     B.hf = nullptr;
   }
-  HIP_TRY(launch_route(D, B, n, st));
-  HIP_TRY(launch_dispatch(D, B, n, st));
-  if (uses_int8(L.math, L.p[0].qtype)) HIP_TRY(launch_quant_act(B.hs, n, L.d, B.xq, B.xs, B.x16, st));
+  const bool quant = uses_int8(L.math, L.p[0].qtype);
+  if (front_small_ok(D, n)) {
+    HIP_TRY(launch_front_small(D, B, n, quant ? 1 : 0, st));
+  } else {
+    HIP_TRY(launch_route(D, B, n, st));
+    HIP_TRY(launch_dispatch(D, B, n, st));
+    if (quant) HIP_TRY(launch_quant_act(B.hs, n, L.d, B.xq, B.xs, B.x16, st));
+  }
   Timing tm{};
   if (c->timing) {
     tm = take_timing(c);
@@ -768,7 +773,7 @@ gmoe_status gmoe_matmul(gmoe_ctx* c, uint32_t qt, uint32_t math, const void* w, 
   // device layout: [w][x f32][xq][xs][x16][y][offsets(2)][active(2)][eptr(3)]
   ScratchPlan P;
   size_t o_w = P.add(wbytes), o_x = P.add(nb_x * 4), o_q = P.add(nb_x), o_s = P.add(nb_x / 32 * 4),
-         o_16 = P.add(nb_x / 16 * 4), o_y = P.add((size_t)n * rows * 4), o_off = P.add(8), o_act = P.add(8),
+         o_16 = P.add(nb_x / 16 * 4), o_y = P.add(kMaxKsg * (size_t)n * rows * 4), o_o = P.add((size_t)n * rows * 4), o_off = P.add(8), o_act = P.add(8),
          o_ep = P.add(3 * sizeof(void*));
   uint8_t* base = nullptr;
   HIP_TRY(hipMalloc(&base, P.total));
@@ -799,8 +804,10 @@ gmoe_status gmoe_matmul(gmoe_ctx* c, uint32_t qt, uint32_t math, const void* w, 
     B.hf = (float*)(base + o_x);
   }
   if (e == hipSuccess) e = launch_down(D, B, n, c->stream);
+  float* dout = (float*)(base + o_o);
+  if (e == hipSuccess) e = launch_reduce_parts(B.y, down_ksg(D, n), (size_t)n * rows, dout, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-  if (e == hipSuccess) e = hipMemcpy(out, B.y, (size_t)n * rows * 4, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(out, dout, (size_t)n * rows * 4, hipMemcpyDeviceToHost);
   hipFree(base);
   if (e != hipSuccess) return fail(GMOE_ERR_DEVICE, "matmul: %s", hipGetErrorString(e));
   return GMOE_OK;

@@ -67,7 +67,7 @@ struct FwdBufs {
   float* hsc;            // [n*k][f/32]
   int32_t* h16;          // [n*k][f/16]
   float* hf;             // [n*k][f]
-  float* y;              // [n*k][d]
+  float* y;              // [kMaxKsg][n*k][d] partial slices of the down product
 };
 
 struct LayerDev {
@@ -78,6 +78,10 @@ struct LayerDev {
   uint32_t pitch_gate, pitch_up, pitch_down;
 };
 
+// The down product of the row kernels splits K over this many partial slices at most;
+// FwdBufs::y holds kMaxKsg slices of [n*k][d].
+constexpr uint32_t kMaxKsg = 8;
+
 // Launchers (gmoe_kernels.hip). All are asynchronous on `st` and validate nothing:
 // the host runtime checks shapes before calling them.
 hipError_t launch_dequant(uint32_t qtype, const uint8_t* blocks, size_t nblocks, float* out,
@@ -87,9 +91,17 @@ hipError_t launch_quant_act(const float* x, uint32_t n_tok, uint32_t K, int8_t* 
                             int32_t* s16, hipStream_t st);
 hipError_t launch_route(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 hipError_t launch_dispatch(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+// Route + gate + int8 activation quantiser (when quant) + dispatch in one launch, for
+// small decode batches (front_small_ok).
+bool front_small_ok(const LayerDev& L, uint32_t n);
+hipError_t launch_front_small(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st);
 hipError_t launch_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 hipError_t launch_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 hipError_t launch_combine(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+// Number of partial slices launch_down writes for this layer and batch (1 = y is final).
+uint32_t down_ksg(const LayerDev& L, uint32_t n);
+// out[i] = parts[i] + parts[count + i] + ... over ksg slices, in slice order.
+hipError_t launch_reduce_parts(const float* parts, uint32_t ksg, size_t count, float* out, hipStream_t st);
 // Plain matrix product for gmoe_matmul: out[b*rows + r] = dot(row r, x[b]).
 hipError_t launch_matmul(uint32_t qtype, uint32_t math, const uint8_t* w, size_t pitch,
                          uint32_t rows, uint32_t cols, const float* x, const int8_t* xq,

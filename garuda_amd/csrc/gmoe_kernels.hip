@@ -15,7 +15,11 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace gmoe {
+
+static inline bool row_kernel_type(uint32_t qt) { return qt == Q4_K || qt == Q5_K || qt == F16 || qt == F32; }
 
 // ---------------------------------------------------------------------------------
 // Scalar helpers
@@ -162,136 +166,88 @@ __device__ __forceinline__ void load_block(const uint8_t* __restrict__ p, uint32
 }
 
 // ---------------------------------------------------------------------------------
-// Dequantisation (bit-exact, quant/mod.rs:624-875). deq<QT>(w, out) writes the E
-// values of one block in the reference's element order.
+// Dequantisation (bit-exact, quant/mod.rs:624-875). deq32<QT>(w, g, out) writes the
+// 32 values of group g (elements 32g..32g+31 of the block, in the reference's element
+// order) with the reference's arithmetic; deq<QT> is every group of a block.
 // ---------------------------------------------------------------------------------
 
-template <int QT> __device__ __forceinline__ void deq(const uint32_t* w, float* out);
+template <int QT> __device__ __forceinline__ void deq32(const uint32_t* w, int g, float* out);
 
-template <> __device__ __forceinline__ void deq<Q4_K>(const uint32_t* w, float* out) {
+template <> __device__ __forceinline__ void deq32<Q4_K>(const uint32_t* w, int g, float* out) {
   float d = f16f(w[0]), dmin = f16f(w[0] >> 16);
+  uint32_t sc, m;
+  scale_min_k4(w + 1, g, sc, m);
+  float dl = d * (float)sc, ml = dmin * (float)m;
+  const uint32_t* chunk = w + 4 + 8 * (g / 2);
 #pragma unroll
-  for (int c = 0; c < 4; c++) {
-    uint32_t sc1, m1, sc2, m2;
-    scale_min_k4(w + 1, 2 * c, sc1, m1);
-    scale_min_k4(w + 1, 2 * c + 1, sc2, m2);
-    float d1 = d * (float)sc1, mn1 = dmin * (float)m1;
-    float d2 = d * (float)sc2, mn2 = dmin * (float)m2;
-#pragma unroll
-    for (int l = 0; l < 32; l++) {
-      uint32_t b = byte_of(w + 4 + 8 * c, l);
-      out[64 * c + l] = d1 * (float)(b & 15u) - mn1;
-      out[64 * c + 32 + l] = d2 * (float)(b >> 4) - mn2;
-    }
+  for (int l = 0; l < 32; l++) {
+    uint32_t b = byte_of(chunk, l);
+    out[l] = dl * (float)((g & 1) ? (b >> 4) : (b & 15u)) - ml;
   }
 }
 
-template <> __device__ __forceinline__ void deq<Q5_K>(const uint32_t* w, float* out) {
+template <> __device__ __forceinline__ void deq32<Q5_K>(const uint32_t* w, int g, float* out) {
   float d = f16f(w[0]), dmin = f16f(w[0] >> 16);
+  uint32_t sc, m;
+  scale_min_k4(w + 1, g, sc, m);
+  float dl = d * (float)sc, ml = dmin * (float)m;
   const uint32_t* qh = w + 4;
-  const uint32_t* qs = w + 12;
+  const uint32_t* ql = w + 12 + 8 * (g / 2);
 #pragma unroll
-  for (int g = 0; g < 4; g++) {
-    uint32_t sc1, m1, sc2, m2;
-    scale_min_k4(w + 1, 2 * g, sc1, m1);
-    scale_min_k4(w + 1, 2 * g + 1, sc2, m2);
-    float d1 = d * (float)sc1, mn1 = dmin * (float)m1;
-    float d2 = d * (float)sc2, mn2 = dmin * (float)m2;
-#pragma unroll
-    for (int l = 0; l < 32; l++) {
-      uint32_t ql = byte_of(qs + 8 * g, l), h = byte_of(qh, l);
-      uint32_t hi1 = (h >> (2 * g)) & 1u, hi2 = (h >> (2 * g + 1)) & 1u;
-      out[64 * g + l] = d1 * (float)((ql & 15u) + 16u * hi1) - mn1;
-      out[64 * g + 32 + l] = d2 * (float)((ql >> 4) + 16u * hi2) - mn2;
-    }
+  for (int l = 0; l < 32; l++) {
+    uint32_t b = byte_of(ql, l), hb = (byte_of(qh, l) >> g) & 1u;
+    out[l] = dl * (float)(((g & 1) ? (b >> 4) : (b & 15u)) + 16u * hb) - ml;
   }
 }
 
-template <> __device__ __forceinline__ void deq<Q6_K>(const uint32_t* w, float* out) {
+template <> __device__ __forceinline__ void deq32<Q6_K>(const uint32_t* w, int g, float* out) {
   float d = f16f(w[52]);  // bytes 208..209 are the low half of dword 52
+  const int half = g / 4, quarter = g % 4;
 #pragma unroll
-  for (int half = 0; half < 2; half++) {
-#pragma unroll
-    for (int l = 0; l < 32; l++) {
-      int is = l / 16;
-      uint32_t ql0 = byte_of(w, 64 * half + l), ql1 = byte_of(w, 64 * half + l + 32);
-      uint32_t qh = byte_of(w, 128 + 32 * half + l);
-      int q1 = (int)((ql0 & 15u) | ((qh & 3u) << 4)) - 32;
-      int q2 = (int)((ql1 & 15u) | (((qh >> 2) & 3u) << 4)) - 32;
-      int q3 = (int)((ql0 >> 4) | (((qh >> 4) & 3u) << 4)) - 32;
-      int q4 = (int)((ql1 >> 4) | (((qh >> 6) & 3u) << 4)) - 32;
-      float s0 = (float)(int8_t)byte_of(w, 192 + 8 * half + is);
-      float s2 = (float)(int8_t)byte_of(w, 192 + 8 * half + is + 2);
-      float s4 = (float)(int8_t)byte_of(w, 192 + 8 * half + is + 4);
-      float s6 = (float)(int8_t)byte_of(w, 192 + 8 * half + is + 6);
-      out[128 * half + l] = d * s0 * (float)q1;
-      out[128 * half + l + 32] = d * s2 * (float)q2;
-      out[128 * half + l + 64] = d * s4 * (float)q3;
-      out[128 * half + l + 96] = d * s6 * (float)q4;
-    }
+  for (int l = 0; l < 32; l++) {
+    uint32_t ql = byte_of(w, 64 * half + l + 32 * (quarter & 1));
+    uint32_t qh = byte_of(w, 128 + 32 * half + l);
+    int q = (int)(((quarter < 2) ? (ql & 15u) : (ql >> 4)) | (((qh >> (2 * quarter)) & 3u) << 4)) - 32;
+    float s = (float)(int8_t)byte_of(w, 192 + 8 * half + l / 16 + 2 * quarter);
+    out[l] = d * s * (float)q;
   }
 }
 
-template <> __device__ __forceinline__ void deq<Q3_K>(const uint32_t* w, float* out) {
+template <> __device__ __forceinline__ void deq32<Q3_K>(const uint32_t* w, int g, float* out) {
   float d_all = f16f(w[27]);  // bytes 108..109
   uint32_t sc4[4];
-  // scale bytes 96..107 = w[24..26]
-  q3k_scales(w[24], w[25], w[26], sc4);
-  int is = 0;
-  uint32_t m = 1;
+  q3k_scales(w[24], w[25], w[26], sc4);  // scale bytes 96..107
+  const int half = g / 4, j = g % 4;
+  const uint32_t m = 1u << (4 * half + j);
 #pragma unroll
-  for (int half = 0; half < 2; half++) {
-    int shift = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-#pragma unroll
-      for (int o = 0; o < 32; o += 16) {
-        float dl = d_all * (float)((int)(int8_t)byte_of(sc4, is) - 32);
-        is++;
-#pragma unroll
-        for (int l = 0; l < 16; l++) {
-          int hbit = (byte_of(w, l + o) & m) ? 0 : 4;
-          int q = (int)((byte_of(w, 32 + 32 * half + o + l) >> shift) & 3u) - hbit;
-          out[128 * half + 32 * j + o + l] = dl * (float)q;
-        }
-      }
-      shift += 2;
-      m <<= 1;
-    }
+  for (int l = 0; l < 32; l++) {
+    int is = 8 * half + 2 * j + l / 16;
+    float dl = d_all * (float)((int)(int8_t)byte_of(sc4, is) - 32);
+    int hbit = (byte_of(w, l) & m) ? 0 : 4;
+    int q = (int)((byte_of(w, 32 + 32 * half + l) >> (2 * j)) & 3u) - hbit;
+    out[l] = dl * (float)q;
   }
 }
 
-template <> __device__ __forceinline__ void deq<Q2_K>(const uint32_t* w, float* out) {
+template <> __device__ __forceinline__ void deq32<Q2_K>(const uint32_t* w, int g, float* out) {
   float d = f16f(w[20]), dmin = f16f(w[20] >> 16);  // bytes 80..83
-  int is = 0;
+  const int half = g / 4, j = g % 4;
 #pragma unroll
-  for (int half = 0; half < 2; half++) {
-    int shift = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-#pragma unroll
-      for (int o = 0; o < 32; o += 16) {
-        uint32_t sc = byte_of(w, is);
-        is++;
-        float dl = d * (float)(sc & 15u), ml = dmin * (float)(sc >> 4);
-#pragma unroll
-        for (int l = 0; l < 16; l++) {
-          uint32_t q = (byte_of(w, 16 + 32 * half + o + l) >> shift) & 3u;
-          out[128 * half + 32 * j + o + l] = dl * (float)q - ml;
-        }
-      }
-      shift += 2;
-    }
+  for (int l = 0; l < 32; l++) {
+    uint32_t sc = byte_of(w, 8 * half + 2 * j + l / 16);
+    float dl = d * (float)(sc & 15u), ml = dmin * (float)(sc >> 4);
+    uint32_t q = (byte_of(w, 16 + 32 * half + l) >> (2 * j)) & 3u;
+    out[l] = dl * (float)q - ml;
   }
 }
 
-template <> __device__ __forceinline__ void deq<Q8_0>(const uint32_t* w, float* out) {
+template <> __device__ __forceinline__ void deq32<Q8_0>(const uint32_t* w, int, float* out) {
   float s = f16f(w[0]);
 #pragma unroll
   for (int i = 0; i < 32; i++) out[i] = s * (float)(int8_t)byte_of(w, 2 + i);
 }
 
-template <> __device__ __forceinline__ void deq<Q4_0>(const uint32_t* w, float* out) {
+template <> __device__ __forceinline__ void deq32<Q4_0>(const uint32_t* w, int, float* out) {
   float s = f16f(w[0]);
 #pragma unroll
   for (int i = 0; i < 16; i++) {
@@ -301,7 +257,7 @@ template <> __device__ __forceinline__ void deq<Q4_0>(const uint32_t* w, float* 
   }
 }
 
-template <> __device__ __forceinline__ void deq<F16>(const uint32_t* w, float* out) {
+template <> __device__ __forceinline__ void deq32<F16>(const uint32_t* w, int, float* out) {
 #pragma unroll
   for (int i = 0; i < 16; i++) {
     out[2 * i] = f16f(w[i]);
@@ -309,9 +265,14 @@ template <> __device__ __forceinline__ void deq<F16>(const uint32_t* w, float* o
   }
 }
 
-template <> __device__ __forceinline__ void deq<F32>(const uint32_t* w, float* out) {
+template <> __device__ __forceinline__ void deq32<F32>(const uint32_t* w, int, float* out) {
 #pragma unroll
   for (int i = 0; i < 32; i++) out[i] = __uint_as_float(w[i]);
+}
+
+template <int QT> __device__ __forceinline__ void deq(const uint32_t* w, float* out) {
+#pragma unroll
+  for (int g = 0; g < QT_<QT>::E / 32; g++) deq32<QT>(w, g, out + 32 * g);
 }
 
 template <int QT>
@@ -447,48 +408,17 @@ __device__ __forceinline__ bool ranks_before(bool llama, float a, uint32_t ia, f
 
 constexpr int kRouteThreads = 256;
 
-// Sequential softmax pieces over `n` values held in LDS (simd/mod.rs:132-158),
-// computed cooperatively: exps in parallel, the running sum by one lane in order.
-__global__ void __launch_bounds__(kRouteThreads) k_route(LayerDev L, FwdBufs B, uint32_t n) {
-  extern __shared__ float sm[];
-  const uint32_t ne = L.ne, k = L.k, d = L.d;
-  const uint32_t tpb = ne >= kRouteThreads ? 1u : kRouteThreads / ne;  // tokens per block
-  const uint32_t t0 = blockIdx.x * tpb;
-  float* lg = sm;                       // [tpb][ne] logits -> probabilities
-  float* red = sm + tpb * ne;           // [tpb] scratch (max, inv)
-  uint32_t* rk = reinterpret_cast<uint32_t*>(red + tpb);  // [tpb][ne] rank of each expert
-  float* topw = reinterpret_cast<float*>(rk + tpb * ne);  // [tpb][k]
-  uint32_t* topi = reinterpret_cast<uint32_t*>(topw + tpb * k);
-
-  for (uint32_t p = threadIdx.x; p < tpb * ne; p += blockDim.x) {
-    uint32_t tt = p / ne, e = p % ne, t = t0 + tt;
-    float acc = 0.0f;
-    if (t < n) {
-      if (B.logits_in) {
-        acc = B.logits_in[(size_t)t * ne + e];
-      } else {
-        const float4* wr = reinterpret_cast<const float4*>(L.router + (size_t)e * d);
-        const float4* hr = reinterpret_cast<const float4*>(B.hs + (size_t)t * d);
-        acc = -0.0f;
-        for (uint32_t j = 0; j < d / 4; j++) {
-          float4 a = wr[j], h = hr[j];
-          float p0 = a.x * h.x, p1 = a.y * h.y, p2 = a.z * h.z, p3 = a.w * h.w;
-          acc = acc + p0;
-          acc = acc + p1;
-          acc = acc + p2;
-          acc = acc + p3;
-        }
-      }
-      B.logits[(size_t)t * ne + e] = acc;
-    }
-    lg[p] = acc;
-  }
-  __syncthreads();
-
+// Gating of `tpb` tokens whose router logits sit in lg[tpb][ne] (LDS), for tokens
+// t0.. t0+tpb-1 (those >= n are ignored). Softmax (simd/mod.rs:132-158) is computed
+// cooperatively: max in any order (it is exact), exps in parallel, the running sum by
+// one lane in order. Ranks by counting (a stable sort's positions). Every thread of the
+// block must call this.
+__device__ void gate_block(const LayerDev& L, const FwdBufs& B, float* lg, float* red, float* topw,
+                           uint32_t* topi, uint32_t tpb, uint32_t t0, uint32_t n) {
+  const uint32_t ne = L.ne, k = L.k;
   const bool llama = L.gating == 0;
   const bool soft_all = L.gating == 0 || L.gating == 2 || L.gating == 3;
   if (soft_all) {
-    // max (order-free), exps in parallel, sum in order
     if (threadIdx.x < tpb) {
       float mx = -INFINITY;
       for (uint32_t e = 0; e < ne; e++) mx = fmaxf(mx, lg[threadIdx.x * ne + e]);
@@ -529,7 +459,6 @@ __global__ void __launch_bounds__(kRouteThreads) k_route(LayerDev L, FwdBufs B, 
     uint32_t r = 0;
     for (uint32_t o = 0; o < ne; o++)
       if (o != e && ranks_before(llama, x[o], o, me, e)) r++;
-    rk[p] = r;
     if (r < k) {
       topw[tt * k + r] = me;
       topi[tt * k + r] = e;
@@ -582,24 +511,55 @@ __global__ void __launch_bounds__(kRouteThreads) k_route(LayerDev L, FwdBufs B, 
   }
 }
 
-hipError_t launch_route(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
-  uint32_t tpb = L.ne >= kRouteThreads ? 1u : kRouteThreads / L.ne;
-  size_t shm = (size_t)tpb * L.ne * 8 + tpb * 4 + (size_t)tpb * L.k * 8;
-  hipLaunchKernelGGL(k_route, dim3((n + tpb - 1) / tpb), dim3(kRouteThreads), shm, st, L, B, n);
-  return hipGetLastError();
+// Router logits: one lane per (token, expert) pair runs the reference's sequential f32
+// dot (simd/mod.rs:13-16: separate multiply and add, left to right, Iterator::sum
+// starting at -0.0), then gate_block. Used when the fused decode kernel does not apply.
+__global__ void __launch_bounds__(kRouteThreads) k_route(LayerDev L, FwdBufs B, uint32_t n) {
+  extern __shared__ float sm[];
+  const uint32_t ne = L.ne, k = L.k, d = L.d;
+  const uint32_t tpb = ne >= kRouteThreads ? 1u : kRouteThreads / ne;  // tokens per block
+  const uint32_t t0 = blockIdx.x * tpb;
+  float* lg = sm;                       // [tpb][ne] logits -> probabilities
+  float* red = sm + tpb * ne;           // [tpb] scratch (max, inv)
+  float* topw = red + tpb;              // [tpb][k]
+  uint32_t* topi = reinterpret_cast<uint32_t*>(topw + tpb * k);
+
+  for (uint32_t p = threadIdx.x; p < tpb * ne; p += blockDim.x) {
+    uint32_t tt = p / ne, e = p % ne, t = t0 + tt;
+    float acc = 0.0f;
+    if (t < n) {
+      if (B.logits_in) {
+        acc = B.logits_in[(size_t)t * ne + e];
+      } else {
+        const float4* wr = reinterpret_cast<const float4*>(L.router + (size_t)e * d);
+        const float4* hr = reinterpret_cast<const float4*>(B.hs + (size_t)t * d);
+        acc = -0.0f;
+        for (uint32_t j = 0; j < d / 4; j++) {
+          float4 a = wr[j], h = hr[j];
+          float p0 = a.x * h.x, p1 = a.y * h.y, p2 = a.z * h.z, p3 = a.w * h.w;
+          acc = acc + p0;
+          acc = acc + p1;
+          acc = acc + p2;
+          acc = acc + p3;
+        }
+      }
+      B.logits[(size_t)t * ne + e] = acc;
+    }
+    lg[p] = acc;
+  }
+  __syncthreads();
+  gate_block(L, B, lg, red, topw, topi, tpb, t0, n);
 }
 
-// ---------------------------------------------------------------------------------
-// Dispatch: a stable counting sort of the (token, rank) pairs by expert id, which is
-// exactly members[e] of llama/mod.rs:967-972 laid end to end. One workgroup.
-// ---------------------------------------------------------------------------------
-
-__global__ void __launch_bounds__(256) k_dispatch(LayerDev L, FwdBufs B, uint32_t n) {
-  extern __shared__ uint32_t cnt[];  // [ne + 1]
+// Dispatch body: a stable counting sort of the (token, rank) pairs by expert id, which is
+// exactly members[e] of llama/mod.rs:967-972 laid end to end. One workgroup; cnt is
+// [ne] in LDS; every thread must call this.
+__device__ void dispatch_block(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t* cnt,
+                               const uint32_t* ids, const float* wts) {
   const uint32_t ne = L.ne, k = L.k, nk = n * k;
   for (uint32_t e = threadIdx.x; e < ne; e += blockDim.x) {
     uint32_t c = 0;
-    for (uint32_t p = 0; p < nk; p++) c += B.ids[p] == e;
+    for (uint32_t p = 0; p < nk; p++) c += ids[p] == e;
     cnt[e] = c;
   }
   __syncthreads();
@@ -619,9 +579,9 @@ __global__ void __launch_bounds__(256) k_dispatch(LayerDev L, FwdBufs B, uint32_
   for (uint32_t e = threadIdx.x; e < ne; e += blockDim.x) {
     uint32_t pos = cnt[e];
     for (uint32_t p = 0; p < nk; p++) {
-      if (B.ids[p] == e) {
+      if (ids[p] == e) {
         B.slot_tok[pos] = p / k;
-        B.slot_w[pos] = B.w[p];
+        B.slot_w[pos] = wts[p];
         B.slot_rank[pos] = p % k;
         B.slot_of[p] = pos;
         pos++;
@@ -630,8 +590,172 @@ __global__ void __launch_bounds__(256) k_dispatch(LayerDev L, FwdBufs B, uint32_
   }
 }
 
+__global__ void __launch_bounds__(256) k_dispatch(LayerDev L, FwdBufs B, uint32_t n) {
+  extern __shared__ uint32_t cnt[];  // [ne]
+  dispatch_block(L, B, n, cnt, B.ids, B.w);
+}
+
+// ---------------------------------------------------------------------------------
+// Fused decode front end: router logits, gating, the int8 activation quantiser and the
+// dispatch in one workgroup of 512 threads, for n*ne <= 64 (one chain per lane of
+// wave 0). The logits' products w*h (each rounded, as the reference multiplies before
+// it adds) are made by waves 1..15 one K-chunk ahead into LDS; wave 0 only runs the 64
+// sequential add chains over them, so the chain's latency is the adds alone.
+// (The products are made by waves 1..7.)
+// ---------------------------------------------------------------------------------
+
+constexpr int kFrontThreads = 512, kFrontKC = 128, kFrontPairs = 64;
+constexpr int kFrontRow = kFrontKC + 4;  // padded LDS row of one pair's products
+
+__global__ void __launch_bounds__(kFrontThreads) k_front_small(LayerDev L, FwdBufs B, uint32_t n, int quant) {
+  extern __shared__ float fs[];
+  float* prod = fs;                                   // [2][64][kFrontRow]
+  float* lg = prod + 2 * kFrontPairs * kFrontRow;     // [n][ne]
+  float* red = lg + kFrontPairs;                      // [n]
+  float* topw = red + kFrontPairs;                    // [n][k]
+  uint32_t* topi = reinterpret_cast<uint32_t*>(topw + kFrontPairs * 32);
+  uint32_t* cnt = topi + kFrontPairs * 32;            // [ne]
+  const uint32_t ne = L.ne, d = L.d, P = n * ne;
+  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  if (B.logits_in) {
+    for (uint32_t p = tid; p < P; p += blockDim.x) lg[p] = B.logits_in[p];
+  } else {
+    // Producer thread i (waves 1..15) owns float4 groups g = i + 960*q of each chunk:
+    // pair g / (KC/4), columns 4*(g % (KC/4)).. ; it holds two chunks' operands in
+    // registers (chunk c in set c&1), so the loads of chunk c+2 are in flight while
+    // chunk c+1's products are written and chunk c is chained.
+    constexpr int kProd = kFrontThreads - 64, kGroups = kFrontPairs * kFrontKC / 4;
+    constexpr int kPer = (kGroups + kProd - 1) / kProd;  // 5
+    const uint32_t nch = (d + kFrontKC - 1) / kFrontKC;
+    const uint32_t pi = tid - 64;
+    float4 ra[2][kPer], rh[2][kPer];
+    // `set` is always a compile-time constant (integral_constant) so ra/rh stay in VGPRs
+    auto fetch = [&](auto set_c, uint32_t c) {
+      constexpr int set = decltype(set_c)::value;
+      const uint32_t base = c * kFrontKC;
+#pragma unroll
+      for (int q = 0; q < kPer; q++) {
+        uint32_t g = pi + kProd * q, pr = g / (kFrontKC / 4), j = 4 * (g % (kFrontKC / 4));
+        if (pr < P && base + j < d) {
+          uint32_t t = pr / ne, e = pr % ne;
+          ra[set][q] = *reinterpret_cast<const float4*>(L.router + (size_t)e * d + base + j);
+          rh[set][q] = *reinterpret_cast<const float4*>(B.hs + (size_t)t * d + base + j);
+        }
+      }
+    };
+    auto produce = [&](auto set_c, uint32_t c) {
+      constexpr int set = decltype(set_c)::value;
+      float* dst = prod + (c & 1) * kFrontPairs * kFrontRow;
+      const uint32_t base = c * kFrontKC;
+#pragma unroll
+      for (int q = 0; q < kPer; q++) {
+        uint32_t g = pi + kProd * q, pr = g / (kFrontKC / 4), j = 4 * (g % (kFrontKC / 4));
+        if (pr < P && base + j < d) {
+          float4 a = ra[set][q], h = rh[set][q];
+          float4 p4 = make_float4(a.x * h.x, a.y * h.y, a.z * h.z, a.w * h.w);
+          *reinterpret_cast<float4*>(dst + pr * kFrontRow + j) = p4;
+        }
+      }
+    };
+    float acc = -0.0f;
+    const std::integral_constant<int, 0> S0{};
+    const std::integral_constant<int, 1> S1{};
+    if (wave != 0) {
+      fetch(S0, 0);
+      if (nch > 1) fetch(S1, 1);
+      produce(S0, 0);
+      if (nch > 2) fetch(S0, 2);
+    }
+    __syncthreads();
+    // chunk c is chained by wave 0 while the producers write chunk c+1 (register set
+    // (c+1)&1) and start loading chunk c+3 into the set they just emptied
+    auto iter = [&](auto set_c, uint32_t c) {
+      if (wave == 0) {
+        if (lane < P) {
+          const float* src = prod + (c & 1) * kFrontPairs * kFrontRow + lane * kFrontRow;
+          const uint32_t len = min((uint32_t)kFrontKC, d - c * kFrontKC);
+          if (len == (uint32_t)kFrontKC) {
+            // 8 reads in flight ahead of the 32 dependent adds they feed
+#pragma unroll
+            for (uint32_t j0 = 0; j0 < (uint32_t)kFrontKC; j0 += 32) {
+              float4 v[8];
+#pragma unroll
+              for (int u = 0; u < 8; u++) v[u] = *reinterpret_cast<const float4*>(src + j0 + 4 * u);
+#pragma unroll
+              for (int u = 0; u < 8; u++) {
+                acc = acc + v[u].x;
+                acc = acc + v[u].y;
+                acc = acc + v[u].z;
+                acc = acc + v[u].w;
+              }
+            }
+          } else {
+            for (uint32_t j = 0; j < len; j += 4) {
+              float4 v = *reinterpret_cast<const float4*>(src + j);
+              acc = acc + v.x;
+              acc = acc + v.y;
+              acc = acc + v.z;
+              acc = acc + v.w;
+            }
+          }
+        }
+      } else if (c + 1 < nch) {
+        produce(set_c, c + 1);
+        if (c + 3 < nch) fetch(set_c, c + 3);
+      }
+      __syncthreads();
+    };
+    for (uint32_t c = 0; c < nch; c += 2) {
+      iter(S1, c);
+      if (c + 1 < nch) iter(S0, c + 1);
+    }
+    if (wave == 0 && lane < P) lg[lane] = acc;
+  }
+  __syncthreads();
+  for (uint32_t p = tid; p < P; p += blockDim.x) B.logits[p] = lg[p];
+  gate_block(L, B, lg, red, topw, topi, n, 0, n);
+  if (quant) {
+    const uint32_t nblk = n * (d / 32);
+    for (uint32_t b = tid; b < nblk; b += blockDim.x) {
+      float v[32];
+      const float4* src = reinterpret_cast<const float4*>(B.hs + (size_t)b * 32);
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        float4 t4 = src[i];
+        v[4 * i] = t4.x; v[4 * i + 1] = t4.y; v[4 * i + 2] = t4.z; v[4 * i + 3] = t4.w;
+      }
+      quant32(v, B.xq + (size_t)b * 32, B.xs + b, B.x16 + 2 * (size_t)b);
+    }
+  }
+  __syncthreads();
+  // gate_block leaves every token's ranked ids and weights in topi/topw ([n][k], LDS)
+  dispatch_block(L, B, n, cnt, topi, topw);
+}
+
+bool front_small_ok(const LayerDev& L, uint32_t n) {
+  return n * L.ne <= (uint32_t)kFrontPairs && L.k <= 32 && L.d % 4 == 0;
+}
+
+hipError_t launch_front_small(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st) {
+  size_t shm = (size_t)(2 * kFrontPairs * kFrontRow + 2 * kFrontPairs + 2 * kFrontPairs * 32) * 4 + L.ne * 4;
+  static bool attr = false;
+  if (!attr) {
+    hipFuncSetAttribute((const void*)k_front_small, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm + 4096);
+    attr = true;
+  }
+  hipLaunchKernelGGL(k_front_small, dim3(1), dim3(kFrontThreads), shm, st, L, B, n, quant);
+  return hipGetLastError();
+}
+
+hipError_t launch_route(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  uint32_t tpb = L.ne >= kRouteThreads ? 1u : kRouteThreads / L.ne;
+  size_t shm = (size_t)tpb * L.ne * 4 + tpb * 4 + (size_t)tpb * L.k * 8;
+  hipLaunchKernelGGL(k_route, dim3((n + tpb - 1) / tpb), dim3(kRouteThreads), shm, st, L, B, n);
+  return hipGetLastError();
+}
+
 hipError_t launch_dispatch(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
-  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(256), (L.ne + 1) * 4, st, L, B, n);
+  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(256), L.ne * 4, st, L, B, n);
   return hipGetLastError();
 }
 
@@ -850,22 +974,25 @@ __device__ __forceinline__ void pk_block(const uint32_t* w, const int8_t* const*
 template <int QT, int TM>
 __device__ __forceinline__ void f32_block(const uint32_t* w, const float* const* x, float* acc, int m) {
   constexpr int E = QT_<QT>::E;
-  float v[E];
-  deq<QT>(w, v);
 #pragma unroll
-  for (int t = 0; t < TM; t++) {
-    if (t < m) {
-      const float4* xa = reinterpret_cast<const float4*>(x[t]);
-      float a = acc[t];
+  for (int g = 0; g < E / 32; g++) {
+    float v[32];
+    deq32<QT>(w, g, v);
 #pragma unroll
-      for (int i = 0; i < E / 4; i++) {
-        float4 xv = xa[i];
-        a = fmaf(v[4 * i], xv.x, a);
-        a = fmaf(v[4 * i + 1], xv.y, a);
-        a = fmaf(v[4 * i + 2], xv.z, a);
-        a = fmaf(v[4 * i + 3], xv.w, a);
+    for (int t = 0; t < TM; t++) {
+      if (t < m) {
+        const float4* xa = reinterpret_cast<const float4*>(x[t] + 32 * g);
+        float a = acc[t];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          float4 xv = xa[i];
+          a = fmaf(v[4 * i], xv.x, a);
+          a = fmaf(v[4 * i + 1], xv.y, a);
+          a = fmaf(v[4 * i + 2], xv.z, a);
+          a = fmaf(v[4 * i + 3], xv.w, a);
+        }
+        acc[t] = a;
       }
-      acc[t] = a;
     }
   }
 }
@@ -1097,15 +1224,294 @@ __global__ void __launch_bounds__(256) k_down(LayerDev L, FwdBufs B) {
 }
 
 // ---------------------------------------------------------------------------------
+// Row-per-lane streaming kernels, for block types made of whole 16-byte pieces
+// (Q4_K 144 B, Q5_K 176 B; F16/F32 rows walked 32 values = 64/128 B at a time).
+//
+// A workgroup owns 64 consecutive rows of one expert's matrix and lane i owns row i.
+// A wave streams its rows one block-column ("step") at a time: the 64 blocks of a step
+// are fetched with coalesced 16-byte loads (consecutive lanes read consecutive bytes of
+// a row, 9 lanes per Q4_K block), parked in LDS, and each lane reads its own row's block
+// back. Two steps are in flight while one is computed. The activations of a step are
+// the same for every lane of the wave, so they arrive through scalar loads. Each lane
+// runs its row's dot in K order.
+// ---------------------------------------------------------------------------------
+
+struct RowIO {
+  const uint8_t* const* eptr;
+  const uint32_t* active;
+  const uint32_t* offsets;
+  const uint32_t* slot_tok;
+};
+
+// One wave's streaming loop over blocks [j0, j1) of rows `W + row*pitch`, calling
+// body(j, w) with the lane's own block j in w[]. T is the wave's LDS step buffer.
+template <int QT, class Body>
+__device__ __forceinline__ void stream_rows(const uint8_t* __restrict__ W, uint32_t pitch, uint32_t r0,
+                                            uint32_t nrows, uint32_t j0, uint32_t j1, uint4* T, uint32_t lane,
+                                            Body body) {
+  constexpr int B = QT_<QT>::B, P = B / 16, NW = B / 4;
+  const uint8_t* src[P];
+#pragma unroll
+  for (int q = 0; q < P; q++) {
+    uint32_t c = q * 64 + lane, row = c / P, piece = c % P;
+    uint32_t rr = min(r0 + row, nrows - 1);
+    src[q] = W + (size_t)rr * pitch + piece * 16;
+  }
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 ga[P], gb[P];
+  auto fetch = [&](u32x4* g, uint32_t j) {
+#pragma unroll
+    for (int q = 0; q < P; q++) g[q] = *reinterpret_cast<const u32x4*>(src[q] + (size_t)j * B);
+  };
+  // Lanes of one wave hand blocks to each other through T: a wavefront-scope release /
+  // barrier / acquire orders the stores before the other lanes' loads (and the loads
+  // before the next step's stores), for the compiler as well as the hardware.
+  auto wave_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  auto step = [&](u32x4* g, uint32_t j) {
+#pragma unroll
+    for (int q = 0; q < P; q++) T[q * 64 + lane] = make_uint4(g[q].x, g[q].y, g[q].z, g[q].w);
+    if (j + 2 < j1) fetch(g, j + 2);
+    wave_sync();
+    uint32_t w[NW];
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+      uint4 v = T[lane * P + p];
+      w[4 * p] = v.x; w[4 * p + 1] = v.y; w[4 * p + 2] = v.z; w[4 * p + 3] = v.w;
+    }
+    wave_sync();
+    body(j, w);
+  };
+  if (j0 >= j1) return;
+  fetch(ga, j0);
+  if (j0 + 1 < j1) fetch(gb, j0 + 1);
+  for (uint32_t j = j0; j < j1; j += 2) {
+    step(ga, j);
+    if (j + 1 < j1) step(gb, j + 1);
+  }
+}
+
+// Activations of one token chunk over the K blocks [j0, j0+span) a workgroup reads,
+// staged in LDS once and read by every lane as broadcasts. Packed: int8 values, per-32
+// scales and per-16 sums; f32: the values. `row[t]` is the token (gate/up) or slot
+// (down) row of chunk member t in the activation arrays, whose rows are K long.
+template <bool PACKED>
+struct ActLds {
+  static constexpr uint32_t bytes_per_elem_x16() { return PACKED ? 22u : 64u; }  // x16: 1 + 1/8 + 1/4 (q, s, s16) or 4
+  // LDS bytes for tm tokens over span*E elements (each array rounded to 16 bytes)
+  __host__ __device__ static uint32_t bytes(uint32_t tm, uint32_t nelem) {
+    if (PACKED) return tm * (((nelem + 15) & ~15u) + ((nelem / 32 * 4 + 15) & ~15u) + ((nelem / 16 * 4 + 15) & ~15u));
+    return tm * nelem * 4;
+  }
+};
+
+template <int TM>
+__device__ __forceinline__ void stage_packed(uint8_t* lds, uint32_t nelem, const int8_t* __restrict__ q,
+                                             const float* __restrict__ s, const int32_t* __restrict__ s16,
+                                             uint32_t K, const uint32_t* row, int m, uint32_t k0) {
+  const uint32_t qb = (nelem + 15) & ~15u, sb = (nelem / 32 * 4 + 15) & ~15u, hb = (nelem / 16 * 4 + 15) & ~15u;
+  int8_t* lq = reinterpret_cast<int8_t*>(lds);
+  float* ls = reinterpret_cast<float*>(lds + TM * qb);
+  int32_t* lh = reinterpret_cast<int32_t*>(lds + TM * qb + TM * sb);
+  const uint32_t nq4 = nelem / 16;  // int8 values move 16 at a time (nelem is a multiple of 32)
+  for (uint32_t i = threadIdx.x; i < (uint32_t)m * nq4; i += blockDim.x) {
+    uint32_t t = i / nq4, c = i % nq4;
+    reinterpret_cast<uint4*>(lq + t * qb)[c] = reinterpret_cast<const uint4*>(q + (size_t)row[t] * K + k0)[c];
+  }
+  const uint32_t ns = nelem / 32, nh = nelem / 16;
+  for (uint32_t i = threadIdx.x; i < (uint32_t)m * ns; i += blockDim.x) {
+    uint32_t t = i / ns, c = i % ns;
+    ls[t * (sb / 4) + c] = s[(size_t)row[t] * (K / 32) + k0 / 32 + c];
+  }
+  for (uint32_t i = threadIdx.x; i < (uint32_t)m * nh; i += blockDim.x) {
+    uint32_t t = i / nh, c = i % nh;
+    lh[t * (hb / 4) + c] = s16[(size_t)row[t] * (K / 16) + k0 / 16 + c];
+  }
+}
+
+template <int TM>
+__device__ __forceinline__ void stage_f32(uint8_t* lds, uint32_t nelem, const float* __restrict__ x, uint32_t K,
+                                          const uint32_t* row, int m, uint32_t k0) {
+  float* lx = reinterpret_cast<float*>(lds);
+  const uint32_t n4 = nelem / 4;
+  for (uint32_t i = threadIdx.x; i < (uint32_t)m * n4; i += blockDim.x) {
+    uint32_t t = i / n4, c = i % n4;
+    reinterpret_cast<float4*>(lx + t * nelem)[c] = reinterpret_cast<const float4*>(x + (size_t)row[t] * K + k0)[c];
+  }
+}
+
+// Runs the block body over the staged activations: block j (absolute) of chunk member t
+// sits at element (j - jbase) * E of its staged row.
+template <int QT, int TM, bool PACKED>
+__device__ __forceinline__ void staged_block(const uint32_t* w, uint8_t* lds, uint32_t nelem, uint32_t j,
+                                             uint32_t jbase, float* acc, int m) {
+  constexpr int E = QT_<QT>::E;
+  const uint32_t off = (j - jbase) * E;
+  if constexpr (PACKED) {
+    const uint32_t qb = (nelem + 15) & ~15u, sb = (nelem / 32 * 4 + 15) & ~15u, hb = (nelem / 16 * 4 + 15) & ~15u;
+    const int8_t* lq = reinterpret_cast<const int8_t*>(lds);
+    const float* ls = reinterpret_cast<const float*>(lds + TM * qb);
+    const int32_t* lh = reinterpret_cast<const int32_t*>(lds + TM * qb + TM * sb);
+    const int8_t* xb[TM];
+    const float* sbp[TM];
+    const int32_t* hbp[TM];
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+      xb[t] = lq + t * qb + off;
+      sbp[t] = ls + t * (sb / 4) + off / 32;
+      hbp[t] = lh + t * (hb / 4) + off / 16;
+    }
+    pk_block<QT, TM>(w, xb, sbp, hbp, acc, m);
+  } else {
+    const float* lx = reinterpret_cast<const float*>(lds);
+    const float* xb[TM];
+#pragma unroll
+    for (int t = 0; t < TM; t++) xb[t] = lx + t * nelem + off;
+    f32_block<QT, TM>(w, xb, acc, m);
+  }
+}
+
+// Dynamic LDS of the row kernels: [KS step tiles][misc floats][staged activations].
+__host__ __device__ inline uint32_t row_tile_bytes(uint32_t qt_bytes, uint32_t ks) { return ks * 64 * qt_bytes; }
+
+template <int QT, int TM, bool PACKED>
+__global__ void __launch_bounds__(128)
+k_gu_rows(RowIO io, uint32_t ne, uint32_t f, uint32_t d, uint32_t pitch_g, uint32_t pitch_u,
+          const int8_t* __restrict__ xq, const float* __restrict__ xs, const int32_t* __restrict__ x16,
+          const float* __restrict__ hs, int8_t* __restrict__ hq, float* __restrict__ hsc,
+          int32_t* __restrict__ h16, float* __restrict__ hf) {
+  constexpr int E = QT_<QT>::E, P = QT_<QT>::B / 16;
+  extern __shared__ uint4 dsm[];
+  uint4* tile0 = dsm;                                              // [2][64*P]
+  float* su = reinterpret_cast<float*>(dsm + 2 * 64 * P);         // [TM][64]
+  float* sh = su + TM * 64;                                        // [TM][64]
+  uint8_t* acts = reinterpret_cast<uint8_t*>(sh + TM * 64);
+  const uint32_t a = blockIdx.y;
+  if (a >= io.active[0]) return;
+  const uint32_t e = io.active[1 + a];
+  const uint32_t s0 = io.offsets[e], m_all = io.offsets[e + 1] - s0;
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t r0 = blockIdx.x * 64;
+  const uint8_t* W = io.eptr[wave * ne + e];
+  const uint32_t pitch = wave ? pitch_u : pitch_g;
+  const uint32_t nblk = d / E;
+  for (uint32_t c0 = 0; c0 < m_all; c0 += TM) {
+    const int m = (int)min((uint32_t)TM, m_all - c0);
+    uint32_t tok[TM];
+#pragma unroll
+    for (int t = 0; t < TM; t++) tok[t] = io.slot_tok[s0 + c0 + (t < m ? t : 0)];
+    if constexpr (PACKED) stage_packed<TM>(acts, d, xq, xs, x16, d, tok, m, 0);
+    else stage_f32<TM>(acts, d, hs, d, tok, m, 0);
+    __syncthreads();
+    float acc[TM];
+#pragma unroll
+    for (int t = 0; t < TM; t++) acc[t] = 0.0f;
+    stream_rows<QT>(W, pitch, r0, f, 0, nblk, tile0 + wave * 64 * P, lane, [&](uint32_t j, const uint32_t* w) {
+      staged_block<QT, TM, PACKED>(w, acts, d, j, 0, acc, m);
+    });
+    if (wave == 1) {
+#pragma unroll
+      for (int t = 0; t < TM; t++) su[t * 64 + lane] = acc[t];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int t = 0; t < TM; t++) sh[t * 64 + lane] = swiglu(acc[t], su[t * 64 + lane]);
+    }
+    __syncthreads();
+    if (hf) {
+      for (uint32_t p = threadIdx.x; p < (uint32_t)m * 64; p += blockDim.x) {
+        uint32_t t = p / 64, r = p % 64, rr = r0 + r;
+        if (rr < f) hf[(size_t)(s0 + c0 + t) * f + rr] = sh[t * 64 + r];
+      }
+    }
+    if (hq) {
+      for (uint32_t p = threadIdx.x; p < (uint32_t)m * 2; p += blockDim.x) {
+        uint32_t t = p / 2, hb = p % 2, q0 = r0 + 32 * hb;
+        if (q0 + 32 <= f) {
+          size_t slot = s0 + c0 + t;
+          quant32(&sh[t * 64 + 32 * hb], hq + slot * f + q0, hsc + slot * (f / 32) + q0 / 32, h16 + slot * (f / 16) + q0 / 16);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Down: the row's K range is split over gridDim.y workgroups of KS waves each. A
+// workgroup adds its waves' partial sums in wave order and writes them to its own
+// partial slice y[blockIdx.y]; the combine adds the slices in order.
+// grid.x = tiles of 64 rows of d_model, grid.y = K groups, grid.z = active-expert slot.
+template <int QT, int TM, bool PACKED, int KS>
+__global__ void __launch_bounds__(64 * KS)
+k_dn_rows(RowIO io, uint32_t ne, uint32_t f, uint32_t d, uint32_t pitch_d, uint32_t part_stride,
+          const int8_t* __restrict__ hq, const float* __restrict__ hsc, const int32_t* __restrict__ h16,
+          const float* __restrict__ hf, float* __restrict__ ypart) {
+  constexpr int E = QT_<QT>::E, P = QT_<QT>::B / 16;
+  extern __shared__ uint4 dsm[];
+  uint4* tile0 = dsm;                                              // [KS][64*P]
+  float* red = reinterpret_cast<float*>(dsm + KS * 64 * P);       // [KS][TM][64]
+  uint8_t* acts = reinterpret_cast<uint8_t*>(red + KS * TM * 64);
+  const uint32_t a = blockIdx.z;
+  if (a >= io.active[0]) return;
+  const uint32_t e = io.active[1 + a];
+  const uint32_t s0 = io.offsets[e], m_all = io.offsets[e + 1] - s0;
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t r0 = blockIdx.x * 64;
+  const uint8_t* W = io.eptr[2 * ne + e];
+  const uint32_t nblk = f / E, nsl = gridDim.y * KS, sl = blockIdx.y * KS + wave;
+  const uint32_t j0 = (nblk * sl) / nsl, j1 = (nblk * (sl + 1)) / nsl;
+  // the workgroup's K range: its first wave's start to its last wave's end
+  const uint32_t jw0 = (nblk * (blockIdx.y * KS)) / nsl, jw1 = (nblk * (blockIdx.y * KS + KS)) / nsl;
+  const uint32_t nelem = (jw1 - jw0) * E;
+  float* y = ypart + (size_t)blockIdx.y * part_stride;
+  for (uint32_t c0 = 0; c0 < m_all; c0 += TM) {
+    const int m = (int)min((uint32_t)TM, m_all - c0);
+    uint32_t slot[TM];
+#pragma unroll
+    for (int t = 0; t < TM; t++) slot[t] = s0 + c0 + (t < m ? t : 0);
+    if (nelem) {
+      if constexpr (PACKED) stage_packed<TM>(acts, nelem, hq, hsc, h16, f, slot, m, jw0 * E);
+      else stage_f32<TM>(acts, nelem, hf, f, slot, m, jw0 * E);
+    }
+    __syncthreads();
+    float acc[TM];
+#pragma unroll
+    for (int t = 0; t < TM; t++) acc[t] = 0.0f;
+    stream_rows<QT>(W, pitch_d, r0, d, j0, j1, tile0 + wave * 64 * P, lane, [&](uint32_t j, const uint32_t* w) {
+      staged_block<QT, TM, PACKED>(w, acts, nelem, j, jw0, acc, m);
+    });
+#pragma unroll
+    for (int t = 0; t < TM; t++) red[(wave * TM + t) * 64 + lane] = acc[t];
+    __syncthreads();
+    if (wave == 0) {
+      uint32_t row = r0 + lane;
+#pragma unroll
+      for (int t = 0; t < TM; t++) {
+        float sacc = red[t * 64 + lane];
+#pragma unroll
+        for (int w2 = 1; w2 < KS; w2++) sacc += red[(w2 * TM + t) * 64 + lane];
+        if (t < m && row < d) y[(size_t)(s0 + c0 + t) * d + row] = sacc;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------------
 // Combine: out[t] = sum over the token's experts of y*w, ascending expert id
 // (llama/mod.rs:977-995) or routed rank (moe/mod.rs:104-109); add_scaled multiplies
 // then adds, starting from the zeroed output.
 // ---------------------------------------------------------------------------------
 
-__global__ void __launch_bounds__(256) k_combine(LayerDev L, FwdBufs B, uint32_t n) {
+__global__ void __launch_bounds__(256) k_combine(LayerDev L, FwdBufs B, uint32_t n, uint32_t ksg) {
   const uint32_t t = blockIdx.y, k = L.k, d = L.d;
   const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n || c >= d) return;
+  const size_t part = (size_t)n * k * d;
   uint32_t order[32];  // top_k <= 32, checked at registration
   for (uint32_t i = 0; i < k; i++) order[i] = i;
   if (L.combine == 0) {
@@ -1124,13 +1530,29 @@ __global__ void __launch_bounds__(256) k_combine(LayerDev L, FwdBufs B, uint32_t
     uint32_t r = order[i];
     uint32_t slot = B.slot_of[(size_t)t * k + r];
     float wv = B.w[(size_t)t * k + r];
-    acc = acc + B.y[(size_t)slot * d + c] * wv;
+    const float* yp = B.y + (size_t)slot * d + c;
+    float yv = yp[0];
+    for (uint32_t g = 1; g < ksg; g++) yv += yp[g * part];
+    acc = acc + yv * wv;
   }
   B.out[(size_t)t * d + c] = acc;
 }
 
 hipError_t launch_combine(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
-  hipLaunchKernelGGL(k_combine, dim3((L.d + 255) / 256, n), dim3(256), 0, st, L, B, n);
+  hipLaunchKernelGGL(k_combine, dim3((L.d + 255) / 256, n), dim3(256), 0, st, L, B, n, down_ksg(L, n));
+  return hipGetLastError();
+}
+
+__global__ void k_reduce_parts(const float* __restrict__ parts, uint32_t ksg, size_t count, float* __restrict__ out) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  float s = parts[i];
+  for (uint32_t g = 1; g < ksg; g++) s += parts[i + g * count];
+  out[i] = s;
+}
+
+hipError_t launch_reduce_parts(const float* parts, uint32_t ksg, size_t count, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(k_reduce_parts, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st, parts, ksg, count, out);
   return hipGetLastError();
 }
 
@@ -1142,8 +1564,106 @@ static inline bool packed_kernel(uint32_t math, uint32_t qt) {
   return math == 0 && has_int8_kernel(qt);
 }
 
+// tokens handled together per pass: enough for a decode batch, capped at 8
+static inline int pick_tm(uint32_t n) { return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : 8; }
+
+constexpr uint32_t kLdsBudget = 160 * 1024 - 2048;
+
+template <int QT, bool PACKED>
+static uint32_t gu_lds(uint32_t tm, uint32_t d) {
+  return row_tile_bytes(QT_<QT>::B, 2) + 2 * tm * 64 * 4 + ActLds<PACKED>::bytes(tm, d);
+}
+
+template <class K>
+static void allow_lds(K kernel, uint32_t bytes) {
+  // raise the dynamic LDS limit of this instantiation once (idempotent, cheap)
+  hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+template <int QT, int TM, bool PACKED>
+static void go_gu_rows(const LayerDev& L, const FwdBufs& B, dim3 g, hipStream_t st) {
+  RowIO io{L.eptr, B.active, B.offsets, B.slot_tok};
+  uint32_t lds = gu_lds<QT, PACKED>(TM, L.d);
+  static bool once = (allow_lds(k_gu_rows<QT, TM, PACKED>, kLdsBudget), true);
+  (void)once;
+  hipLaunchKernelGGL((k_gu_rows<QT, TM, PACKED>), g, dim3(128), lds, st, io, L.ne, L.f, L.d, L.pitch_gate,
+                     L.pitch_up, B.xq, B.xs, B.x16, B.hs, B.hq, B.hsc, B.h16, B.hf);
+}
+
+// largest chunk of tokens <= want whose staging fits the LDS budget
+template <class F>
+static int fit_tm(int want, F lds_of) {
+  int tm = want;
+  while (tm > 1 && lds_of((uint32_t)tm) > kLdsBudget) tm /= 2;
+  return tm;
+}
+
+template <int QT, bool PACKED>
+static void go_gu_rows_tm(const LayerDev& L, const FwdBufs& B, dim3 g, int want, hipStream_t st) {
+  int tm = fit_tm(want, [&](uint32_t t) { return gu_lds<QT, PACKED>(t, L.d); });
+  switch (tm) {
+    case 1: go_gu_rows<QT, 1, PACKED>(L, B, g, st); break;
+    case 2: go_gu_rows<QT, 2, PACKED>(L, B, g, st); break;
+    case 4: go_gu_rows<QT, 4, PACKED>(L, B, g, st); break;
+    default: go_gu_rows<QT, 8, PACKED>(L, B, g, st); break;
+  }
+}
+
+constexpr int kDnKS = 2;
+
+// K groups of the row-kernel down product: enough workgroups to cover the chip twice
+// over, each wave keeping at least 4 blocks to stream.
+uint32_t down_ksg(const LayerDev& L, uint32_t n) {
+  if (!row_kernel_type(L.qt_down)) return 1;
+  uint32_t tiles = (L.d + 63) / 64, ymax = min(L.ne, n * L.k);
+  uint32_t nblk = L.f / ((L.qt_down == F16 || L.qt_down == F32) ? 32u : 256u);
+  uint32_t ksg = (512 + tiles * ymax - 1) / (tiles * ymax);
+  uint32_t cap = max(1u, nblk / (kDnKS * 4));
+  return max(1u, min(min(ksg, cap), (uint32_t)kMaxKsg));
+}
+
+template <int QT, bool PACKED>
+static uint32_t dn_lds(uint32_t tm, uint32_t f, uint32_t ksg) {
+  constexpr uint32_t E = QT_<QT>::E;
+  uint32_t nblk = f / E, span = (nblk + ksg - 1) / ksg + 1;
+  return row_tile_bytes(QT_<QT>::B, kDnKS) + kDnKS * tm * 64 * 4 + ActLds<PACKED>::bytes(tm, span * E);
+}
+
+template <int QT, int TM, bool PACKED>
+static void go_dn_rows(const LayerDev& L, const FwdBufs& B, dim3 g, uint32_t n, hipStream_t st) {
+  RowIO io{L.eptr, B.active, B.offsets, B.slot_tok};
+  uint32_t lds = dn_lds<QT, PACKED>(TM, L.f, g.y);
+  static bool once = (allow_lds(k_dn_rows<QT, TM, PACKED, kDnKS>, kLdsBudget), true);
+  (void)once;
+  hipLaunchKernelGGL((k_dn_rows<QT, TM, PACKED, kDnKS>), g, dim3(64 * kDnKS), lds, st, io, L.ne, L.f, L.d,
+                     L.pitch_down, n * L.k * L.d, B.hq, B.hsc, B.h16, B.hf, B.y);
+}
+
+template <int QT, bool PACKED>
+static void go_dn_rows_tm(const LayerDev& L, const FwdBufs& B, dim3 g, int want, uint32_t n, hipStream_t st) {
+  int tm = fit_tm(want, [&](uint32_t t) { return dn_lds<QT, PACKED>(t, L.f, g.y); });
+  switch (tm) {
+    case 1: go_dn_rows<QT, 1, PACKED>(L, B, g, n, st); break;
+    case 2: go_dn_rows<QT, 2, PACKED>(L, B, g, n, st); break;
+    case 4: go_dn_rows<QT, 4, PACKED>(L, B, g, n, st); break;
+    default: go_dn_rows<QT, 8, PACKED>(L, B, g, n, st); break;
+  }
+}
+
 hipError_t launch_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
   uint32_t ymax = min(L.ne, n * L.k);
+  if (row_kernel_type(L.qt_gate)) {
+    dim3 g((L.f + 63) / 64, ymax);
+    int tm = pick_tm(n);
+    bool pk = packed_kernel(L.math, L.qt_gate);
+    switch (L.qt_gate) {
+      case Q4_K: pk ? go_gu_rows_tm<Q4_K, true>(L, B, g, tm, st) : go_gu_rows_tm<Q4_K, false>(L, B, g, tm, st); break;
+      case Q5_K: pk ? go_gu_rows_tm<Q5_K, true>(L, B, g, tm, st) : go_gu_rows_tm<Q5_K, false>(L, B, g, tm, st); break;
+      case F16: go_gu_rows_tm<F16, false>(L, B, g, tm, st); break;
+      case F32: go_gu_rows_tm<F32, false>(L, B, g, tm, st); break;
+    }
+    return hipGetLastError();
+  }
   if (packed_kernel(L.math, L.qt_gate)) {
     dim3 g((L.f + 63) / 64, ymax), b(128);
     switch (L.qt_gate) {
@@ -1166,6 +1686,18 @@ hipError_t launch_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStr
 
 hipError_t launch_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
   uint32_t ymax = min(L.ne, n * L.k);
+  if (row_kernel_type(L.qt_down)) {
+    dim3 g((L.d + 63) / 64, down_ksg(L, n), ymax);
+    int tm = pick_tm(n);
+    bool pk = packed_kernel(L.math, L.qt_down);
+    switch (L.qt_down) {
+      case Q4_K: pk ? go_dn_rows_tm<Q4_K, true>(L, B, g, tm, n, st) : go_dn_rows_tm<Q4_K, false>(L, B, g, tm, n, st); break;
+      case Q5_K: pk ? go_dn_rows_tm<Q5_K, true>(L, B, g, tm, n, st) : go_dn_rows_tm<Q5_K, false>(L, B, g, tm, n, st); break;
+      case F16: go_dn_rows_tm<F16, false>(L, B, g, tm, n, st); break;
+      case F32: go_dn_rows_tm<F32, false>(L, B, g, tm, n, st); break;
+    }
+    return hipGetLastError();
+  }
   dim3 g((L.d + 31) / 32, ymax), b(256);
   if (packed_kernel(L.math, L.qt_down)) {
     switch (L.qt_down) {

@@ -195,7 +195,7 @@ def test_layer_every_type(dev, qts, math):
 
 @pytest.mark.parametrize("gating,combine", [(1, 1), (2, 1), (3, 1), (0, 1), (1, 0)])
 def test_layer_gating_variants(dev, gating, combine):
-    check_layer(dev, 128, 256, 8, 2, (G.Q4_K,) * 3, (1, 9), G.MATH_PACKED, gating, combine, seed=gating)
+    check_layer(dev, 256, 512, 8, 2, (G.Q4_K,) * 3, (1, 9), G.MATH_PACKED, gating, combine, seed=gating)
 
 
 def test_split_layout_matches_stacked(dev):
@@ -233,7 +233,8 @@ def test_small_slab_stages_experts_on_demand():
     rng = np.random.default_rng(12)
     router, mats = make_layer(rng, d, f, ne, G.Q4_K, G.Q4_K)
     per = sum(M.byte_size(G.Q4_K, f * d) for _ in range(3))
-    with G.Device(0, slab_bytes=3 * per + (1 << 16)) as small:
+    # room for 4 experts: the most one call of n=2, top-2 can route to
+    with G.Device(0, slab_bytes=4 * per + (1 << 16)) as small:
         layer = G.MoeLayer(small, d, f, ne, k, router, mats["gate"], mats["up"], mats["down"], (G.Q4_K,) * 3)
         resident = [layer.is_resident(e) for e in range(ne)]
         assert 0 < sum(resident) < ne
@@ -244,7 +245,7 @@ def test_small_slab_stages_experts_on_demand():
             wout, wids, _ = O.feed_forward_batch(L, hs)
             assert np.array_equal(ids, wids) and np.allclose(out, wout, rtol=RTOL, atol=ATOL)
         st = small.slab_stats()
-        assert st.misses > 0 and st.evictions > 0 and st.entries <= 3
+        assert st.misses > 0 and st.evictions > 0 and st.entries <= 4
         layer.evict(int(ids[0, 0]))
         assert not layer.is_resident(int(ids[0, 0]))
         layer.prefetch(int(ids[0, 0]))
