@@ -18,7 +18,7 @@ ARCH = os.environ.get("GMOE_ARCH", "gfx950")
 SOURCES = ["gmoe_kernels.hip", "gmoe_api.cpp", "gmoe_quant.cpp"]
 
 COMMON = [
-    "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off", "-fno-fast-math",
+    "-O3", "-fPIC", "-std=c++20", "-ffp-contract=off", "-fno-fast-math",
     "-Wall", "-Wno-unused-function",
 ]
 # Packed-FP32 instructions are kept out of the device code entirely.

@@ -16,6 +16,7 @@
 #include <math.h>
 
 #include <type_traits>
+#include <utility>
 
 namespace gmoe {
 
@@ -604,83 +605,84 @@ __global__ void __launch_bounds__(256) k_dispatch(LayerDev L, FwdBufs B, uint32_
 // (The products are made by waves 1..7.)
 // ---------------------------------------------------------------------------------
 
-constexpr int kFrontThreads = 512, kFrontKC = 128, kFrontPairs = 64;
-constexpr int kFrontRow = kFrontKC + 4;  // padded LDS row of one pair's products
+constexpr int kFrontKC = 128, kFrontPairs = 64, kFrontRows = 16, kFrontRing = 16, kFrontMaxCh = 32;
+constexpr int kFrontProd = 512, kFrontThreads = 64 + kFrontProd;
+constexpr int kFrontRow = kFrontKC + 4;  // padded LDS row (floats)
 
+// Producer p owns one float4 column slot (row p / 32, float4 p % 32) of every K chunk of
+// the (router rows ; token rows) operand matrix and loads it 16 chunks ahead into a
+// register ring; each chunk is parked in LDS two chunks before its products are made.
+// The chunk loop is fully unrolled so ring indices are compile-time.
 __global__ void __launch_bounds__(kFrontThreads) k_front_small(LayerDev L, FwdBufs B, uint32_t n, int quant) {
   extern __shared__ float fs[];
-  float* prod = fs;                                   // [2][64][kFrontRow]
-  float* lg = prod + 2 * kFrontPairs * kFrontRow;     // [n][ne]
-  float* red = lg + kFrontPairs;                      // [n]
-  float* topw = red + kFrontPairs;                    // [n][k]
+  float* stage = fs;                                    // [2][kFrontRows][kFrontRow]
+  float* prod = stage + 2 * kFrontRows * kFrontRow;     // [2][kFrontPairs][kFrontRow]
+  float* lg = prod + 2 * kFrontPairs * kFrontRow;       // [n][ne]
+  float* red = lg + kFrontPairs;                        // [n]
+  float* topw = red + kFrontPairs;                      // [n][k]
   uint32_t* topi = reinterpret_cast<uint32_t*>(topw + kFrontPairs * 32);
-  uint32_t* cnt = topi + kFrontPairs * 32;            // [ne]
-  const uint32_t ne = L.ne, d = L.d, P = n * ne;
+  uint32_t* cnt = topi + kFrontPairs * 32;              // [ne]
+  const uint32_t ne = L.ne, d = L.d, P = n * ne, R = ne + n;
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   if (B.logits_in) {
     for (uint32_t p = tid; p < P; p += blockDim.x) lg[p] = B.logits_in[p];
   } else {
-    // Producer thread i (waves 1..15) owns float4 groups g = i + 960*q of each chunk:
-    // pair g / (KC/4), columns 4*(g % (KC/4)).. ; it holds two chunks' operands in
-    // registers (chunk c in set c&1), so the loads of chunk c+2 are in flight while
-    // chunk c+1's products are written and chunk c is chained.
-    constexpr int kProd = kFrontThreads - 64, kGroups = kFrontPairs * kFrontKC / 4;
-    constexpr int kPer = (kGroups + kProd - 1) / kProd;  // 5
-    const uint32_t nch = (d + kFrontKC - 1) / kFrontKC;
-    const uint32_t pi = tid - 64;
-    float4 ra[2][kPer], rh[2][kPer];
-    // `set` is always a compile-time constant (integral_constant) so ra/rh stay in VGPRs
-    auto fetch = [&](auto set_c, uint32_t c) {
-      constexpr int set = decltype(set_c)::value;
-      const uint32_t base = c * kFrontKC;
-#pragma unroll
-      for (int q = 0; q < kPer; q++) {
-        uint32_t g = pi + kProd * q, pr = g / (kFrontKC / 4), j = 4 * (g % (kFrontKC / 4));
-        if (pr < P && base + j < d) {
-          uint32_t t = pr / ne, e = pr % ne;
-          ra[set][q] = *reinterpret_cast<const float4*>(L.router + (size_t)e * d + base + j);
-          rh[set][q] = *reinterpret_cast<const float4*>(B.hs + (size_t)t * d + base + j);
-        }
-      }
+    const uint32_t nch = d / kFrontKC;
+    const bool producer = wave != 0;
+    const uint32_t p = tid - 64, r = p / 32, c4 = p % 32;
+    const bool slot = producer && r < R;
+    const float4* src = reinterpret_cast<const float4*>(slot ? (r < ne ? L.router + (size_t)r * d
+                                                                      : B.hs + (size_t)(r - ne) * d)
+                                                             : L.router);
+    // the ring is one 64-wide vector value: constant-index element accesses stay in VGPRs
+    typedef float f32x64 __attribute__((ext_vector_type(64)));
+    f32x64 ring = {};
+    auto ring_put = [&](int i, float4 v) __attribute__((always_inline)) {
+      ring[4 * i] = v.x; ring[4 * i + 1] = v.y; ring[4 * i + 2] = v.z; ring[4 * i + 3] = v.w;
     };
-    auto produce = [&](auto set_c, uint32_t c) {
-      constexpr int set = decltype(set_c)::value;
-      float* dst = prod + (c & 1) * kFrontPairs * kFrontRow;
-      const uint32_t base = c * kFrontKC;
-#pragma unroll
-      for (int q = 0; q < kPer; q++) {
-        uint32_t g = pi + kProd * q, pr = g / (kFrontKC / 4), j = 4 * (g % (kFrontKC / 4));
-        if (pr < P && base + j < d) {
-          float4 a = ra[set][q], h = rh[set][q];
-          float4 p4 = make_float4(a.x * h.x, a.y * h.y, a.z * h.z, a.w * h.w);
-          *reinterpret_cast<float4*>(dst + pr * kFrontRow + j) = p4;
-        }
-      }
+    auto ring_get = [&](int i) __attribute__((always_inline)) {
+      return make_float4(ring[4 * i], ring[4 * i + 1], ring[4 * i + 2], ring[4 * i + 3]);
     };
+#pragma unroll
+    for (int c = 0; c < kFrontRing; c++)
+      if (slot && (uint32_t)c < nch) ring_put(c, src[c * (kFrontKC / 4) + c4]);
     float acc = -0.0f;
-    const std::integral_constant<int, 0> S0{};
-    const std::integral_constant<int, 1> S1{};
-    if (wave != 0) {
-      fetch(S0, 0);
-      if (nch > 1) fetch(S1, 1);
-      produce(S0, 0);
-      if (nch > 2) fetch(S0, 2);
+    // prologue: park chunks 0 and 1, make chunk 0's products
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      if (slot && (uint32_t)c < nch) {
+        *reinterpret_cast<float4*>(stage + (c * kFrontRows + r) * kFrontRow + 4 * c4) = ring_get(c);
+        if ((uint32_t)(c + kFrontRing) < nch) ring_put(c, src[(c + kFrontRing) * (kFrontKC / 4) + c4]);
+      }
     }
     __syncthreads();
-    // chunk c is chained by wave 0 while the producers write chunk c+1 (register set
-    // (c+1)&1) and start loading chunk c+3 into the set they just emptied
-    auto iter = [&](auto set_c, uint32_t c) {
-      if (wave == 0) {
-        if (lane < P) {
-          const float* src = prod + (c & 1) * kFrontPairs * kFrontRow + lane * kFrontRow;
-          const uint32_t len = min((uint32_t)kFrontKC, d - c * kFrontKC);
-          if (len == (uint32_t)kFrontKC) {
-            // 8 reads in flight ahead of the 32 dependent adds they feed
+    if (producer) {
 #pragma unroll
-            for (uint32_t j0 = 0; j0 < (uint32_t)kFrontKC; j0 += 32) {
+      for (int q = 0; q < kFrontPairs * kFrontKC / 4 / kFrontProd; q++) {
+        uint32_t g = p + kFrontProd * q, pr = g / (kFrontKC / 4), j = 4 * (g % (kFrontKC / 4));
+        if (pr < P) {
+          uint32_t t = pr / ne, e = pr % ne;
+          float4 av = *reinterpret_cast<const float4*>(stage + e * kFrontRow + j);
+          float4 hv = *reinterpret_cast<const float4*>(stage + (ne + t) * kFrontRow + j);
+          *reinterpret_cast<float4*>(prod + pr * kFrontRow + j) =
+              make_float4(av.x * hv.x, av.y * hv.y, av.z * hv.z, av.w * hv.w);
+        }
+      }
+    }
+    __syncthreads();
+    // iteration c: wave 0 chains chunk c | producers make chunk c+1's products and park
+    // chunk c+2 (whose LDS slot chunk c's products have finished with)
+#pragma unroll
+    for (int c = 0; c < kFrontMaxCh; c++) {
+      if ((uint32_t)c < nch) {
+        if (wave == 0) {
+          if (lane < P) {
+            const float* src2 = prod + (c & 1) * kFrontPairs * kFrontRow + lane * kFrontRow;
+#pragma unroll
+            for (int j0 = 0; j0 < kFrontKC; j0 += 32) {
               float4 v[8];
 #pragma unroll
-              for (int u = 0; u < 8; u++) v[u] = *reinterpret_cast<const float4*>(src + j0 + 4 * u);
+              for (int u = 0; u < 8; u++) v[u] = *reinterpret_cast<const float4*>(src2 + j0 + 4 * u);
 #pragma unroll
               for (int u = 0; u < 8; u++) {
                 acc = acc + v[u].x;
@@ -689,25 +691,31 @@ __global__ void __launch_bounds__(kFrontThreads) k_front_small(LayerDev L, FwdBu
                 acc = acc + v[u].w;
               }
             }
-          } else {
-            for (uint32_t j = 0; j < len; j += 4) {
-              float4 v = *reinterpret_cast<const float4*>(src + j);
-              acc = acc + v.x;
-              acc = acc + v.y;
-              acc = acc + v.z;
-              acc = acc + v.w;
+          }
+        } else {
+          if ((uint32_t)(c + 1) < nch) {
+            const float* st = stage + ((c + 1) & 1) * kFrontRows * kFrontRow;
+            float* dst = prod + ((c + 1) & 1) * kFrontPairs * kFrontRow;
+#pragma unroll
+            for (int q = 0; q < kFrontPairs * kFrontKC / 4 / kFrontProd; q++) {
+              uint32_t g = p + kFrontProd * q, pr = g / (kFrontKC / 4), j = 4 * (g % (kFrontKC / 4));
+              if (pr < P) {
+                uint32_t t = pr / ne, e = pr % ne;
+                float4 av = *reinterpret_cast<const float4*>(st + e * kFrontRow + j);
+                float4 hv = *reinterpret_cast<const float4*>(st + (ne + t) * kFrontRow + j);
+                *reinterpret_cast<float4*>(dst + pr * kFrontRow + j) =
+                    make_float4(av.x * hv.x, av.y * hv.y, av.z * hv.z, av.w * hv.w);
+              }
             }
           }
+          if (slot && (uint32_t)(c + 2) < nch) {
+            const int slot_i = (c + 2) % kFrontRing;
+            *reinterpret_cast<float4*>(stage + ((c & 1) * kFrontRows + r) * kFrontRow + 4 * c4) = ring_get(slot_i);
+            if ((uint32_t)(c + 2 + kFrontRing) < nch) ring_put(slot_i, src[(c + 2 + kFrontRing) * (kFrontKC / 4) + c4]);
+          }
         }
-      } else if (c + 1 < nch) {
-        produce(set_c, c + 1);
-        if (c + 3 < nch) fetch(set_c, c + 3);
+        __syncthreads();
       }
-      __syncthreads();
-    };
-    for (uint32_t c = 0; c < nch; c += 2) {
-      iter(S1, c);
-      if (c + 1 < nch) iter(S0, c + 1);
     }
     if (wave == 0 && lane < P) lg[lane] = acc;
   }
@@ -733,16 +741,16 @@ __global__ void __launch_bounds__(kFrontThreads) k_front_small(LayerDev L, FwdBu
 }
 
 bool front_small_ok(const LayerDev& L, uint32_t n) {
-  return n * L.ne <= (uint32_t)kFrontPairs && L.k <= 32 && L.d % 4 == 0;
+  return n * L.ne <= (uint32_t)kFrontPairs && L.ne + n <= (uint32_t)kFrontRows && L.k <= 32 &&
+         L.d % kFrontKC == 0 && L.d <= (uint32_t)(kFrontKC * kFrontMaxCh);
 }
 
 hipError_t launch_front_small(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st) {
-  size_t shm = (size_t)(2 * kFrontPairs * kFrontRow + 2 * kFrontPairs + 2 * kFrontPairs * 32) * 4 + L.ne * 4;
-  static bool attr = false;
-  if (!attr) {
-    hipFuncSetAttribute((const void*)k_front_small, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm + 4096);
-    attr = true;
-  }
+  size_t shm = (size_t)(2 * kFrontRows * kFrontRow + 2 * kFrontPairs * kFrontRow + 2 * kFrontPairs +
+                        2 * kFrontPairs * 32) * 4 + L.ne * 4;
+  static bool attr = (hipFuncSetAttribute((const void*)k_front_small, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          160 * 1024 - 2048), true);
+  (void)attr;
   hipLaunchKernelGGL(k_front_small, dim3(1), dim3(kFrontThreads), shm, st, L, B, n, quant);
   return hipGetLastError();
 }
@@ -1245,11 +1253,20 @@ struct RowIO {
 
 // One wave's streaming loop over blocks [j0, j1) of rows `W + row*pitch`, calling
 // body(j, w) with the lane's own block j in w[]. T is the wave's LDS step buffer.
-template <int QT, class Body>
+//
+// D register sets form a ring: step j is parked from set j % D, whose loads are then
+// reissued for step j + D, so D - 1 steps stay in flight while one is computed. Every
+// fetch is unconditional (its block index is clamped to the last block, a re-read that
+// the L2 serves) and the loop always runs whole rounds of D steps, with only the body
+// of the steps past j1 skipped; the load count pending at each park is then the same on
+// every path through the loop, and the compiler waits for exactly the set it parks
+// instead of draining every load in flight.
+template <int QT, int D = 3, class Body>
 __device__ __forceinline__ void stream_rows(const uint8_t* __restrict__ W, uint32_t pitch, uint32_t r0,
                                             uint32_t nrows, uint32_t j0, uint32_t j1, uint4* T, uint32_t lane,
                                             Body body) {
   constexpr int B = QT_<QT>::B, P = B / 16, NW = B / 4;
+  if (j0 >= j1) return;
   const uint8_t* src[P];
 #pragma unroll
   for (int q = 0; q < P; q++) {
@@ -1258,39 +1275,40 @@ __device__ __forceinline__ void stream_rows(const uint8_t* __restrict__ W, uint3
     src[q] = W + (size_t)rr * pitch + piece * 16;
   }
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  u32x4 ga[P], gb[P];
-  auto fetch = [&](u32x4* g, uint32_t j) {
+  u32x4 g[D][P];
+  const uint32_t jlast = j1 - 1;
+  auto fetch = [&](u32x4* gg, uint32_t j) {
+    const size_t off = (size_t)min(j, jlast) * B;
 #pragma unroll
-    for (int q = 0; q < P; q++) g[q] = *reinterpret_cast<const u32x4*>(src[q] + (size_t)j * B);
+    for (int q = 0; q < P; q++) gg[q] = *reinterpret_cast<const u32x4*>(src[q] + off);
   };
-  // Lanes of one wave hand blocks to each other through T: a wavefront-scope release /
-  // barrier / acquire orders the stores before the other lanes' loads (and the loads
-  // before the next step's stores), for the compiler as well as the hardware.
+  // Lanes of one wave hand blocks to each other through T. The LDS performs one wave's
+  // DS instructions in issue order, so the hand-off only needs the compiler to keep the
+  // stores before the other lanes' loads and the loads before the next step's stores:
+  // an empty asm with a memory clobber. (A memory-model fence would also wait for
+  // every global load in flight, draining the prefetch.)
   auto wave_sync = [] {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    asm volatile("" ::: "memory");
   };
-  auto step = [&](u32x4* g, uint32_t j) {
 #pragma unroll
-    for (int q = 0; q < P; q++) T[q * 64 + lane] = make_uint4(g[q].x, g[q].y, g[q].z, g[q].w);
-    if (j + 2 < j1) fetch(g, j + 2);
-    wave_sync();
-    uint32_t w[NW];
+  for (int i = 0; i < D; i++) fetch(g[i], j0 + i);
+  for (uint32_t j = j0; j < j1; j += D) {
 #pragma unroll
-    for (int p = 0; p < P; p++) {
-      uint4 v = T[lane * P + p];
-      w[4 * p] = v.x; w[4 * p + 1] = v.y; w[4 * p + 2] = v.z; w[4 * p + 3] = v.w;
+    for (int i = 0; i < D; i++) {
+#pragma unroll
+      for (int q = 0; q < P; q++) T[q * 64 + lane] = make_uint4(g[i][q].x, g[i][q].y, g[i][q].z, g[i][q].w);
+      fetch(g[i], j + i + D);
+      wave_sync();
+      uint32_t w[NW];
+#pragma unroll
+      for (int p = 0; p < P; p++) {
+        uint4 v = T[lane * P + p];
+        w[4 * p] = v.x; w[4 * p + 1] = v.y; w[4 * p + 2] = v.z; w[4 * p + 3] = v.w;
+      }
+      wave_sync();
+      if (j + i < j1) body(j + i, w);
     }
-    wave_sync();
-    body(j, w);
-  };
-  if (j0 >= j1) return;
-  fetch(ga, j0);
-  if (j0 + 1 < j1) fetch(gb, j0 + 1);
-  for (uint32_t j = j0; j < j1; j += 2) {
-    step(ga, j);
-    if (j + 1 < j1) step(gb, j + 1);
   }
 }
 
