@@ -8,6 +8,7 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -16,6 +17,9 @@ LIB = PKG / "libgaruda_moe.so"
 ARCH = os.environ.get("GMOE_ARCH", "gfx950")
 
 SOURCES = ["gmoe_kernels.hip", "gmoe_api.cpp", "gmoe_quant.cpp"]
+# gmoe_units.hip is built once per block type (ggml type ids), each object holding one
+# type's expert kernels.
+UNIT_TYPES = {"f32": 0, "f16": 1, "q4_0": 2, "q8_0": 8, "q2_k": 10, "q3_k": 11, "q4_k": 12, "q5_k": 13, "q6_k": 14}
 
 COMMON = [
     "-O3", "-fPIC", "-std=c++20", "-ffp-contract=off", "-fno-fast-math",
@@ -33,24 +37,31 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build step failed: {' '.join(cmd)}")
 
 
+def _jobs(hipcc: str, objdir: Path) -> list[tuple[list[str], Path]]:
+    jobs = []
+    for src in SOURCES:
+        obj = objdir / (src + ".o")
+        extra = DEVICE if src.endswith(".hip") else ["-D__HIP_PLATFORM_AMD__"]
+        jobs.append(([hipcc, *extra, *COMMON, "-c", str(CSRC / src), "-o", str(obj)], obj))
+    for name, qt in UNIT_TYPES.items():
+        obj = objdir / f"gmoe_units_{name}.o"
+        jobs.append(([hipcc, *DEVICE, *COMMON, f"-DGMOE_QT={qt}", "-c", str(CSRC / "gmoe_units.hip"), "-o", str(obj)], obj))
+    return jobs
+
+
 def build(verbose: bool = False) -> Path:
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
     objdir = PKG / "_build"
     objdir.mkdir(exist_ok=True)
-    objs = []
-    for src in SOURCES:
-        obj = objdir / (src + ".o")
-        cmd = [hipcc, *COMMON, "-c", str(CSRC / src), "-o", str(obj)]
-        if src.endswith(".hip"):
-            cmd[1:1] = DEVICE
-        else:
-            cmd[1:1] = ["-D__HIP_PLATFORM_AMD__"]
-        if verbose:
+    jobs = _jobs(hipcc, objdir)
+    if verbose:
+        for cmd, _ in jobs:
             print(" ".join(cmd))
-        _run(cmd)
-        objs.append(str(obj))
+    workers = max(1, min(len(jobs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        list(ex.map(lambda j: _run(j[0]), jobs))
     tmp = LIB.with_suffix(".so.tmp")
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *objs, "-lpthread"])
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *[str(o) for _, o in jobs], "-lpthread"])
     os.replace(tmp, LIB)
     return LIB
 

@@ -125,7 +125,7 @@ struct Slab {
 
 struct Proj {
   uint32_t qtype, rows, cols;
-  uint64_t row_bytes, pitch, bytes_dev;  // bytes_dev = rows*pitch + 256 pad
+  uint64_t row_bytes, bytes_dev;  // bytes_dev = size of the tiled matrix in the slab
   std::vector<const uint8_t*> host;      // per expert
 };
 
@@ -157,6 +157,7 @@ struct gmoe_ctx {
   gmoe_slab_stats stats{};
   uint8_t* pinned = nullptr;
   size_t pinned_bytes = 0;
+  uint8_t* bounce = nullptr;  // device landing area of the pinned halves (same size)
   hipEvent_t pin_ev[2]{};
   // scratch arena
   uint8_t* scratch = nullptr;
@@ -171,28 +172,28 @@ struct gmoe_ctx {
 
 namespace {
 
-// ---- staging: host packed rows -> slab at row pitch, through pinned memory ----
+// ---- staging: host packed rows -> pinned half -> device bounce half -> tiled slab ----
+// Whole 64-row tiles move per pass; the copy and the tiling kernel of a pass run on the
+// copy stream, and the half's event tells when both have finished with it.
 gmoe_status stage_proj(gmoe_ctx* c, const Proj& P, const uint8_t* src, uint8_t* dst) {
   const size_t chunk = c->pinned_bytes / 2;
-  size_t rows_per = std::max<size_t>(1, chunk / P.pitch);
+  const size_t tile_raw = (size_t)kTileRows * P.row_bytes;
+  if (tile_raw > chunk)
+    return fail(GMOE_ERR_CONFIG, "rows of %llu bytes exceed the staging buffer", (unsigned long long)P.row_bytes);
+  const uint32_t rows_per = (uint32_t)(chunk / tile_raw) * kTileRows;
   int buf = 0;
-  for (uint32_t r0 = 0; r0 < P.rows; r0 += (uint32_t)rows_per, buf ^= 1) {
-    uint32_t nr = (uint32_t)std::min<size_t>(rows_per, P.rows - r0);
+  for (uint32_t r0 = 0; r0 < P.rows; r0 += rows_per, buf ^= 1) {
+    const uint32_t nr = std::min(rows_per, P.rows - r0);
+    const size_t nbytes = (size_t)nr * P.row_bytes;
     HIP_TRY(hipEventSynchronize(c->pin_ev[buf]));
     uint8_t* pin = c->pinned + buf * chunk;
-    if (P.pitch == P.row_bytes) {
-      memcpy(pin, src + (size_t)r0 * P.row_bytes, (size_t)nr * P.row_bytes);
-    } else {
-      for (uint32_t r = 0; r < nr; r++) {
-        memcpy(pin + (size_t)r * P.pitch, src + (size_t)(r0 + r) * P.row_bytes, P.row_bytes);
-        memset(pin + (size_t)r * P.pitch + P.row_bytes, 0, P.pitch - P.row_bytes);
-      }
-    }
-    HIP_TRY(hipMemcpyAsync(dst + (size_t)r0 * P.pitch, pin, (size_t)nr * P.pitch,
-                           hipMemcpyHostToDevice, c->copy_stream));
+    uint8_t* land = c->bounce + buf * chunk;
+    memcpy(pin, src + (size_t)r0 * P.row_bytes, nbytes);
+    HIP_TRY(hipMemcpyAsync(land, pin, nbytes, hipMemcpyHostToDevice, c->copy_stream));
+    HIP_TRY(launch_tile_rows(P.qtype, land, r0, nr, P.rows, P.cols, dst, c->copy_stream));
     HIP_TRY(hipEventRecord(c->pin_ev[buf], c->copy_stream));
   }
-  c->stats.h2d_bytes += (uint64_t)P.rows * P.pitch;
+  c->stats.h2d_bytes += (uint64_t)P.rows * P.row_bytes;
   return GMOE_OK;
 }
 
@@ -349,9 +350,6 @@ LayerDev layer_dev(const Layer& L) {
   D.qt_gate = L.p[0].qtype; D.qt_up = L.p[1].qtype; D.qt_down = L.p[2].qtype;
   D.router = L.router;
   D.eptr = L.eptr;
-  D.pitch_gate = (uint32_t)L.p[0].pitch;
-  D.pitch_up = (uint32_t)L.p[1].pitch;
-  D.pitch_down = (uint32_t)L.p[2].pitch;
   return D;
 }
 
@@ -502,6 +500,7 @@ gmoe_status gmoe_init(int device, uint64_t slab_bytes, gmoe_ctx** out) {
   c->stats.capacity = slab_bytes;
   c->pinned_bytes = (size_t)64 << 20;
   HIP_TRY(hipHostMalloc((void**)&c->pinned, c->pinned_bytes, hipHostMallocDefault));
+  HIP_TRY(hipMalloc(&c->bounce, c->pinned_bytes));
   HIP_TRY(hipEventCreateWithFlags(&c->pin_ev[0], hipEventDisableTiming));
   HIP_TRY(hipEventCreateWithFlags(&c->pin_ev[1], hipEventDisableTiming));
   HIP_TRY(hipEventRecord(c->pin_ev[0], c->copy_stream));
@@ -529,6 +528,7 @@ void gmoe_shutdown(gmoe_ctx* c) {
   if (c->slab.base) hipFree(c->slab.base);
   if (c->scratch) hipFree(c->scratch);
   if (c->pinned) hipHostFree(c->pinned);
+  if (c->bounce) hipFree(c->bounce);
   hipEventDestroy(c->pin_ev[0]);
   hipEventDestroy(c->pin_ev[1]);
   hipStreamDestroy(c->stream);
@@ -561,8 +561,9 @@ gmoe_status gmoe_layer_register(gmoe_ctx* c, const gmoe_layer_desc* desc, uint32
     if (!k_ok(P.qtype, P.cols))
       return fail(GMOE_ERR_MODEL, "%s rows of %u values: width must be a multiple of 32", type_name(P.qtype), P.cols);
     P.row_bytes = rb;
-    P.pitch = row_pitch(rb);
-    P.bytes_dev = (uint64_t)P.rows * P.pitch + 256;
+    Unit un;
+    if (!unit_of(P.qtype, &un)) return fail(GMOE_ERR_MODEL, "unsupported tensor type %u", P.qtype);
+    P.bytes_dev = tiled_bytes(un, P.rows, P.cols);
     P.host.resize(L->ne);
     if (T[p]->layout == GMOE_LAYOUT_STACKED) {
       if (!T[p]->data) return fail(GMOE_ERR_MODEL, "stacked tensor %d has no data", p);
@@ -767,21 +768,21 @@ gmoe_status gmoe_matmul(gmoe_ctx* c, uint32_t qt, uint32_t math, const void* w, 
   if (n == 0 || rows == 0) return fail(GMOE_ERR_INFERENCE, "matmul dimension mismatch");
   std::lock_guard<std::mutex> g(c->mu);
   HIP_TRY(hipSetDevice(c->device));
-  size_t pitch = row_pitch(rb);
-  size_t wbytes = (size_t)rows * pitch + 256;
+  Unit un;
+  unit_of(qt, &un);
+  size_t wbytes = tiled_bytes(un, rows, cols);
   size_t nb_x = (size_t)n * cols;
-  // device layout: [w][x f32][xq][xs][x16][y][offsets(2)][active(2)][eptr(3)]
+  // device layout: [w tiled][w raw][x f32][xq][xs][x16][y][out][offsets(2)][active(2)][eptr(3)]
   ScratchPlan P;
-  size_t o_w = P.add(wbytes), o_x = P.add(nb_x * 4), o_q = P.add(nb_x), o_s = P.add(nb_x / 32 * 4),
+  size_t o_w = P.add(wbytes), o_raw = P.add(nbytes), o_x = P.add(nb_x * 4), o_q = P.add(nb_x), o_s = P.add(nb_x / 32 * 4),
          o_16 = P.add(nb_x / 16 * 4), o_y = P.add(kMaxKsg * (size_t)n * rows * 4), o_o = P.add((size_t)n * rows * 4), o_off = P.add(8), o_act = P.add(8),
          o_ep = P.add(3 * sizeof(void*));
   uint8_t* base = nullptr;
   HIP_TRY(hipMalloc(&base, P.total));
-  std::vector<uint8_t> hw(wbytes, 0);
-  for (uint32_t r = 0; r < rows; r++) memcpy(hw.data() + (size_t)r * pitch, (const uint8_t*)w + (size_t)r * rb, rb);
   uint32_t offs[2] = {0, n}, act[2] = {1, 0};
   const uint8_t* ep[3] = {base + o_w, base + o_w, base + o_w};
-  hipError_t e = hipMemcpy(base + o_w, hw.data(), wbytes, hipMemcpyHostToDevice);
+  hipError_t e = hipMemcpy(base + o_raw, w, nbytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = launch_tile_rows(qt, base + o_raw, 0, rows, rows, cols, base + o_w, c->stream);
   if (e == hipSuccess) e = hipMemcpy(base + o_x, xs, nb_x * 4, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(base + o_off, offs, 8, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(base + o_act, act, 8, hipMemcpyHostToDevice);
@@ -790,7 +791,6 @@ gmoe_status gmoe_matmul(gmoe_ctx* c, uint32_t qt, uint32_t math, const void* w, 
   D.d = rows; D.f = cols; D.ne = 1; D.k = 1; D.math = math;
   D.qt_gate = D.qt_up = D.qt_down = qt;
   D.eptr = (const uint8_t* const*)(base + o_ep);
-  D.pitch_down = (uint32_t)pitch;
   FwdBufs B{};
   B.offsets = (uint32_t*)(base + o_off);
   B.active = (uint32_t*)(base + o_act);

@@ -1,0 +1,517 @@
+// gmoe_device.h — device-side helpers shared by the gfx950 kernels: half decoding,
+// the bit-exact expf, block traits, the dequantisers, the activation quantiser and
+// the packed (int8-activation) block dots.
+#pragma once
+
+#include "gmoe_internal.h"
+
+#include <math.h>
+
+namespace gmoe {
+
+// ---------------------------------------------------------------------------------
+// Scalar helpers
+// ---------------------------------------------------------------------------------
+
+// quant/mod.rs:878-890. The hardware conversion is exact for every finite half and
+// for infinities; NaN is canonicalised the way the reference builds it (f32::NAN,
+// sign applied by negation).
+__device__ __forceinline__ float f16f(uint32_t h) {
+  h &= 0xffffu;
+  if ((h & 0x7c00u) == 0x7c00u && (h & 0x3ffu)) return __uint_as_float((h & 0x8000u) ? 0xffc00000u : 0x7fc00000u);
+  _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
+  return (float)v;
+}
+
+// expf, reproducing the host libm the reference links (glibc >= 2.28 on x86-64 with
+// FMA). Method: exp2f-table reduction of Szabolcs Nagy (ARM optimized-routines,
+// 2017): x*N/ln2 = k + r, 2^(k/N) from a 32-entry table, 2^(r/N) by a cubic, all in
+// double; the scaled product is fused into both of its uses as the FMA build does.
+// Checked bit-for-bit against the host expf over every float in the finite range.
+__constant__ uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+__device__ __forceinline__ float gm_expf(float x) {
+  const double kInvLn2N = 0x1.71547652b82fep+0 * 32;
+  const double kShift = 0x1.8p+52;
+  const double kC0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
+  const double kC1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
+  const double kC2 = 0x1.62e42ff0c52d6p-1 / 32;
+  uint32_t ux = __float_as_uint(x);
+  uint32_t abstop = (ux >> 20) & 0x7ffu;
+  if (abstop >= 0x42bu) {                    // |x| >= 88 or NaN
+    if (ux == 0xff800000u) return 0.0f;      // -inf
+    if (abstop >= 0x7f8u) return x + x;      // inf or NaN
+    if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);  // overflow
+    if (x < -0x1.9fe368p6f) return 0.0f;                         // underflow
+  }
+  double xd = (double)x;
+  double kd = fma(kInvLn2N, xd, kShift);
+  uint64_t ki = (uint64_t)__double_as_longlong(kd);
+  kd -= kShift;
+  double r = fma(kInvLn2N, xd, -kd);
+  uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+  double s = __longlong_as_double((long long)t);
+  double z = fma(kC0, r, kC1);
+  double r2 = r * r;
+  double y = fma(kC2, r, 1.0);
+  y = fma(z, r2, y);
+  y = y * s;
+  return (float)y;
+}
+
+__device__ __forceinline__ float fdiv(float a, float b) { return __fdiv_rn(a, b); }
+
+// simd::silu then simd::mul_assign (simd/mod.rs:161-163, :188-191).
+__device__ __forceinline__ float swiglu(float g, float u) {
+  float s = fdiv(g, 1.0f + gm_expf(-g));
+  return s * u;
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+__device__ __forceinline__ uint32_t byte_of(const uint32_t* w, int i) {
+  return (w[i >> 2] >> ((i & 3) * 8)) & 0xffu;
+}
+
+// quant/mod.rs:656-664, on the 12 scale bytes held in w[0..2] (little endian).
+__device__ __forceinline__ void scale_min_k4(const uint32_t* s3, int j, uint32_t& sc, uint32_t& m) {
+  if (j < 4) {
+    sc = byte_of(s3, j) & 63u;
+    m = byte_of(s3, j + 4) & 63u;
+  } else {
+    sc = (byte_of(s3, j + 4) & 0x0fu) | ((byte_of(s3, j - 4) >> 6) << 4);
+    m = (byte_of(s3, j + 4) >> 4) | ((byte_of(s3, j) >> 6) << 4);
+  }
+}
+
+// quant/mod.rs:812-833
+__device__ __forceinline__ void q3k_scales(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t out[4]) {
+  const uint32_t K1 = 0x03030303u, K2 = 0x0f0f0f0fu;
+  out[0] = (a0 & K2) | ((a2 & K1) << 4);
+  out[1] = (a1 & K2) | (((a2 >> 2) & K1) << 4);
+  out[2] = ((a0 >> 4) & K2) | (((a2 >> 4) & K1) << 4);
+  out[3] = ((a1 >> 4) & K2) | (((a2 >> 6) & K1) << 4);
+}
+
+// ---------------------------------------------------------------------------------
+// Block traits, and loads of raw packed blocks as the dequantiser entry receives them:
+// a block is 16-, 4- or 2-byte aligned depending on its size.
+// ---------------------------------------------------------------------------------
+
+template <int QT> struct QT_;
+template <> struct QT_<Q4_K> { static constexpr int E = 256, B = 144, A = 16; };
+template <> struct QT_<Q5_K> { static constexpr int E = 256, B = 176, A = 16; };
+template <> struct QT_<Q6_K> { static constexpr int E = 256, B = 210, A = 2; };
+template <> struct QT_<Q3_K> { static constexpr int E = 256, B = 110, A = 2; };
+template <> struct QT_<Q2_K> { static constexpr int E = 256, B = 84, A = 4; };
+template <> struct QT_<Q8_0> { static constexpr int E = 32, B = 34, A = 2; };
+template <> struct QT_<Q4_0> { static constexpr int E = 32, B = 18, A = 2; };
+// F32/F16 rows are handled 32 elements at a time.
+template <> struct QT_<F16> { static constexpr int E = 32, B = 64, A = 16; };
+template <> struct QT_<F32> { static constexpr int E = 32, B = 128, A = 16; };
+
+template <int QT> constexpr int ndw() { return (QT_<QT>::B + 3) / 4; }
+
+// Load block bytes p[0..B) into w[] (byte i of the block = byte i%4 of w[i/4]).
+// 2-byte aligned blocks read one dword past the block; the slab pads every matrix.
+template <int QT>
+__device__ __forceinline__ void load_block(const uint8_t* __restrict__ p, uint32_t* w) {
+  constexpr int B = QT_<QT>::B, A = QT_<QT>::A, N = ndw<QT>();
+  if constexpr (A == 16) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4* q = reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < B / 16; i++) {
+      u32x4 v = q[i];
+      w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+    }
+  } else if constexpr (A == 4) {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+    for (int i = 0; i < N; i++) w[i] = q[i];
+  } else {
+    uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+    uint32_t sh = (uint32_t)(a & 3);
+    uint32_t prev = q[0];
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+      uint32_t nxt = q[i + 1];
+      w[i] = __builtin_amdgcn_alignbyte(nxt, prev, sh);
+      prev = nxt;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Dequantisation (bit-exact, quant/mod.rs:624-875). deq32<QT>(w, g, out) writes the
+// 32 values of group g (elements 32g..32g+31 of the block, in the reference's element
+// order) with the reference's arithmetic; deq<QT> is every group of a block.
+// ---------------------------------------------------------------------------------
+
+template <int QT> __device__ __forceinline__ void deq32(const uint32_t* w, int g, float* out);
+
+template <> __device__ __forceinline__ void deq32<Q4_K>(const uint32_t* w, int g, float* out) {
+  float d = f16f(w[0]), dmin = f16f(w[0] >> 16);
+  uint32_t sc, m;
+  scale_min_k4(w + 1, g, sc, m);
+  float dl = d * (float)sc, ml = dmin * (float)m;
+  const uint32_t* chunk = w + 4 + 8 * (g / 2);
+#pragma unroll
+  for (int l = 0; l < 32; l++) {
+    uint32_t b = byte_of(chunk, l);
+    out[l] = dl * (float)((g & 1) ? (b >> 4) : (b & 15u)) - ml;
+  }
+}
+
+template <> __device__ __forceinline__ void deq32<Q5_K>(const uint32_t* w, int g, float* out) {
+  float d = f16f(w[0]), dmin = f16f(w[0] >> 16);
+  uint32_t sc, m;
+  scale_min_k4(w + 1, g, sc, m);
+  float dl = d * (float)sc, ml = dmin * (float)m;
+  const uint32_t* qh = w + 4;
+  const uint32_t* ql = w + 12 + 8 * (g / 2);
+#pragma unroll
+  for (int l = 0; l < 32; l++) {
+    uint32_t b = byte_of(ql, l), hb = (byte_of(qh, l) >> g) & 1u;
+    out[l] = dl * (float)(((g & 1) ? (b >> 4) : (b & 15u)) + 16u * hb) - ml;
+  }
+}
+
+template <> __device__ __forceinline__ void deq32<Q6_K>(const uint32_t* w, int g, float* out) {
+  float d = f16f(w[52]);  // bytes 208..209 are the low half of dword 52
+  const int half = g / 4, quarter = g % 4;
+#pragma unroll
+  for (int l = 0; l < 32; l++) {
+    uint32_t ql = byte_of(w, 64 * half + l + 32 * (quarter & 1));
+    uint32_t qh = byte_of(w, 128 + 32 * half + l);
+    int q = (int)(((quarter < 2) ? (ql & 15u) : (ql >> 4)) | (((qh >> (2 * quarter)) & 3u) << 4)) - 32;
+    float s = (float)(int8_t)byte_of(w, 192 + 8 * half + l / 16 + 2 * quarter);
+    out[l] = d * s * (float)q;
+  }
+}
+
+template <> __device__ __forceinline__ void deq32<Q3_K>(const uint32_t* w, int g, float* out) {
+  float d_all = f16f(w[27]);  // bytes 108..109
+  uint32_t sc4[4];
+  q3k_scales(w[24], w[25], w[26], sc4);  // scale bytes 96..107
+  const int half = g / 4, j = g % 4;
+  const uint32_t m = 1u << (4 * half + j);
+#pragma unroll
+  for (int l = 0; l < 32; l++) {
+    int is = 8 * half + 2 * j + l / 16;
+    float dl = d_all * (float)((int)(int8_t)byte_of(sc4, is) - 32);
+    int hbit = (byte_of(w, l) & m) ? 0 : 4;
+    int q = (int)((byte_of(w, 32 + 32 * half + l) >> (2 * j)) & 3u) - hbit;
+    out[l] = dl * (float)q;
+  }
+}
+
+template <> __device__ __forceinline__ void deq32<Q2_K>(const uint32_t* w, int g, float* out) {
+  float d = f16f(w[20]), dmin = f16f(w[20] >> 16);  // bytes 80..83
+  const int half = g / 4, j = g % 4;
+#pragma unroll
+  for (int l = 0; l < 32; l++) {
+    uint32_t sc = byte_of(w, 8 * half + 2 * j + l / 16);
+    float dl = d * (float)(sc & 15u), ml = dmin * (float)(sc >> 4);
+    uint32_t q = (byte_of(w, 16 + 32 * half + l) >> (2 * j)) & 3u;
+    out[l] = dl * (float)q - ml;
+  }
+}
+
+template <> __device__ __forceinline__ void deq32<Q8_0>(const uint32_t* w, int, float* out) {
+  float s = f16f(w[0]);
+#pragma unroll
+  for (int i = 0; i < 32; i++) out[i] = s * (float)(int8_t)byte_of(w, 2 + i);
+}
+
+template <> __device__ __forceinline__ void deq32<Q4_0>(const uint32_t* w, int, float* out) {
+  float s = f16f(w[0]);
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    uint32_t b = byte_of(w, 2 + i);
+    out[i] = s * (float)((int)(b & 15u) - 8);
+    out[i + 16] = s * (float)((int)(b >> 4) - 8);
+  }
+}
+
+template <> __device__ __forceinline__ void deq32<F16>(const uint32_t* w, int, float* out) {
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    out[2 * i] = f16f(w[i]);
+    out[2 * i + 1] = f16f(w[i] >> 16);
+  }
+}
+
+template <> __device__ __forceinline__ void deq32<F32>(const uint32_t* w, int, float* out) {
+#pragma unroll
+  for (int i = 0; i < 32; i++) out[i] = __uint_as_float(w[i]);
+}
+
+template <int QT> __device__ __forceinline__ void deq(const uint32_t* w, float* out) {
+#pragma unroll
+  for (int g = 0; g < QT_<QT>::E / 32; g++) deq32<QT>(w, g, out + 32 * g);
+}
+
+// ---------------------------------------------------------------------------------
+// Activation quantiser (quant/mod.rs:331-345, :322-326): one thread per 32-block.
+// ---------------------------------------------------------------------------------
+
+__device__ __forceinline__ void quant32(const float* v, int8_t* q, float* s, int32_t* s16) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
+  float scale = fdiv(amax, 127.0f);
+  *s = scale;
+  float inv = scale > 0.0f ? fdiv(1.0f, scale) : 0.0f;
+  int sum0 = 0, sum1 = 0;
+  uint32_t packed[8];
+#pragma unroll
+  for (int j = 0; j < 32; j++) {
+    float r = roundf(v[j] * inv);
+    int qi;
+    if (r != r) qi = 0;
+    else if (r < -127.0f) qi = -127;
+    else if (r > 127.0f) qi = 127;
+    else qi = (int)r;
+    if (j < 16) sum0 += qi; else sum1 += qi;
+    if ((j & 3) == 0) packed[j >> 2] = 0;
+    packed[j >> 2] |= ((uint32_t)qi & 0xffu) << (8 * (j & 3));
+  }
+  uint4* q4 = reinterpret_cast<uint4*>(q);
+  q4[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  q4[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+  s16[0] = sum0;
+  s16[1] = sum1;
+}
+
+// quant32 over a wave: lane l holds value l%32 of block l/32 (two consecutive 32-blocks
+// per wave). The block maximum and the sums of 16 are cross-lane reductions, which their
+// order does not change (the maximum starts from 0, so NaN never wins, as in the serial
+// fold); every lane then quantises its own value with quant32's arithmetic. Lanes
+// l%4 == 0 store four packed values, lanes 0/32 the scales, lanes 0/16/32/48 the sums.
+// `valid` (uniform over each 32-lane half) leaves blocks past the end of the row
+// unwritten; every lane of the wave must call this.
+__device__ __forceinline__ void quant_wave(float v, uint32_t lane, bool valid, int8_t* q, float* s, int32_t* s16) {
+  float a = fmaxf(0.0f, fabsf(v));
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+  const float scale = fdiv(a, 127.0f);
+  const float inv = scale > 0.0f ? fdiv(1.0f, scale) : 0.0f;
+  const float r = roundf(v * inv);
+  const int qi = (r != r) ? 0 : r < -127.0f ? -127 : r > 127.0f ? 127 : (int)r;
+  int sum = qi;
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  const uint32_t b = (uint32_t)qi & 0xffu;
+  const uint32_t word = b | (__shfl_down(b, 1, 64) << 8) | (__shfl_down(b, 2, 64) << 16) | (__shfl_down(b, 3, 64) << 24);
+  if (valid) {
+    if ((lane & 3) == 0) reinterpret_cast<uint32_t*>(q)[lane / 4] = word;
+    if ((lane & 31) == 0) s[lane / 32] = scale;
+    if ((lane & 15) == 0) s16[lane / 16] = sum;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Packed (int8-activation) block dots. Each adds its block's sub-block terms to `acc`
+// in the reference's order, each term evaluated exactly as the reference writes it.
+// x: the block's int8 activations; xs: its per-32 scales; sm: its activation sums in
+// the form the type's dot reads them (sum_kind below).
+// ---------------------------------------------------------------------------------
+
+// The activation sums a packed dot reads, one 32-bit word each: f32 sums of 32 values
+// (Q4_K, Q5_K: the reference converts the i32 sum, which is exact below 2^24), f32
+// sums of 16 (Q2_K), i32 sums of 16 (Q6_K, Q3_K fold them into the integer dot), or
+// none (Q8_0).
+enum SumKind { kSumNone = 0, kSumF32x32 = 1, kSumF32x16 = 2, kSumI32x16 = 3 };
+template <int QT>
+__host__ __device__ constexpr int sum_kind() {
+  return (QT == Q4_K || QT == Q5_K) ? kSumF32x32 : QT == Q2_K ? kSumF32x16 : (QT == Q6_K || QT == Q3_K) ? kSumI32x16 : kSumNone;
+}
+__host__ __device__ constexpr uint32_t sum_width(int kind) { return kind == kSumF32x32 ? 32u : kind ? 16u : 0u; }
+
+// quant/mod.rs:586-621
+template <int TM>
+__device__ __forceinline__ void pk_q4k(const uint32_t* w, const int8_t* const* x, const float* const* xs,
+                                       const uint32_t* const* sm, float* acc, int m) {
+  float d = f16f(w[0]), dmin = f16f(w[0] >> 16);
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    uint32_t sc1, m1, sc2, m2;
+    scale_min_k4(w + 1, 2 * c, sc1, m1);
+    scale_min_k4(w + 1, 2 * c + 1, sc2, m2);
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      uint32_t v = w[4 + 8 * c + i];
+      lo[i] = v & 0x0f0f0f0fu;
+      hi[i] = (v >> 4) & 0x0f0f0f0fu;
+    }
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+      if (t < m) {
+        const uint32_t* xa = reinterpret_cast<const uint32_t*>(x[t] + 64 * c);
+        int dl = 0, dh = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          dl = sdot4(lo[i], xa[i], dl);
+          dh = sdot4(hi[i], xa[8 + i], dh);
+        }
+        const float s1 = __uint_as_float(sm[t][2 * c]), s2 = __uint_as_float(sm[t][2 * c + 1]);
+        acc[t] += xs[t][2 * c] * (d * (float)sc1 * (float)dl - dmin * (float)m1 * s1);
+        acc[t] += xs[t][2 * c + 1] * (d * (float)sc2 * (float)dh - dmin * (float)m2 * s2);
+      }
+    }
+  }
+}
+
+// quant/mod.rs:454-495
+template <int TM>
+__device__ __forceinline__ void pk_q5k(const uint32_t* w, const int8_t* const* x, const float* const* xs,
+                                       const uint32_t* const* sm, float* acc, int m) {
+  float d = f16f(w[0]), dmin = f16f(w[0] >> 16);
+  const uint32_t* qh = w + 4;
+  const uint32_t* qs = w + 12;
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    uint32_t sc1, m1, sc2, m2;
+    scale_min_k4(w + 1, 2 * g, sc1, m1);
+    scale_min_k4(w + 1, 2 * g + 1, sc2, m2);
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      uint32_t v = qs[8 * g + i], h = qh[i];
+      lo[i] = (v & 0x0f0f0f0fu) | (((h >> (2 * g)) & 0x01010101u) << 4);
+      hi[i] = ((v >> 4) & 0x0f0f0f0fu) | (((h >> (2 * g + 1)) & 0x01010101u) << 4);
+    }
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+      if (t < m) {
+        const uint32_t* xa = reinterpret_cast<const uint32_t*>(x[t] + 64 * g);
+        int dl = 0, dh = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          dl = sdot4(lo[i], xa[i], dl);
+          dh = sdot4(hi[i], xa[8 + i], dh);
+        }
+        const float s1 = __uint_as_float(sm[t][2 * g]), s2 = __uint_as_float(sm[t][2 * g + 1]);
+        acc[t] += xs[t][2 * g] * (d * (float)sc1 * (float)dl - dmin * (float)m1 * s1);
+        acc[t] += xs[t][2 * g + 1] * (d * (float)sc2 * (float)dh - dmin * (float)m2 * s2);
+      }
+    }
+  }
+}
+
+// quant/mod.rs:417-445. Sub-block s (16 wide): q-32 is dotted as q then -32*sum.
+template <int TM>
+__device__ __forceinline__ void pk_q6k(const uint32_t* w, const int8_t* const* x, const float* const* xs,
+                                       const uint32_t* const* sm, float* acc, int m) {
+  float d = f16f(w[52]);
+#pragma unroll
+  for (int s = 0; s < 16; s++) {
+    const int half = s / 8, quarter = (s % 8) / 2, l0 = 16 * (s % 2);
+    uint32_t q[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      int l = l0 + 4 * i;
+      uint32_t ql = w[(64 * half + l + (quarter & 1) * 32) / 4];
+      uint32_t qh = w[(128 + 32 * half + l) / 4];
+      uint32_t lo4 = (quarter < 2) ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
+      uint32_t hi2 = ((qh >> (2 * quarter)) & 0x03030303u) << 4;
+      q[i] = lo4 | hi2;
+    }
+    float sc = (float)(int8_t)byte_of(w, 192 + s);
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+      if (t < m) {
+        const uint32_t* xa = reinterpret_cast<const uint32_t*>(x[t] + 16 * s);
+        int dt = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
+        dt -= 32 * (int)sm[t][s];
+        acc[t] += xs[t][s / 2] * d * sc * (float)dt;
+      }
+    }
+  }
+}
+
+// quant/mod.rs:503-540. q = ((qs >> shift) & 3) - (hmask bit ? 0 : 4), dotted as
+// (low2 | hbit << 2) then -4*sum.
+template <int TM>
+__device__ __forceinline__ void pk_q3k(const uint32_t* w, const int8_t* const* x, const float* const* xs,
+                                       const uint32_t* const* sm, float* acc, int m) {
+  float d_all = f16f(w[27]);
+  uint32_t sc4[4];
+  q3k_scales(w[24], w[25], w[26], sc4);
+#pragma unroll
+  for (int s = 0; s < 16; s++) {
+    const int half = s / 8, j = (s % 8) / 2, o = 16 * (s % 2);
+    uint32_t q[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      uint32_t qs = w[(32 + 32 * half + o) / 4 + i];
+      uint32_t hm = w[o / 4 + i];
+      q[i] = ((qs >> (2 * j)) & 0x03030303u) | (((hm >> (4 * half + j)) & 0x01010101u) << 2);
+    }
+    float dl = d_all * (float)((int)(int8_t)byte_of(sc4, s) - 32);
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+      if (t < m) {
+        const uint32_t* xa = reinterpret_cast<const uint32_t*>(x[t] + 16 * s);
+        int dt = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
+        dt -= 4 * (int)sm[t][s];
+        acc[t] += xs[t][s / 2] * dl * (float)dt;
+      }
+    }
+  }
+}
+
+// quant/mod.rs:548-581
+template <int TM>
+__device__ __forceinline__ void pk_q2k(const uint32_t* w, const int8_t* const* x, const float* const* xs,
+                                       const uint32_t* const* sm, float* acc, int m) {
+  float d = f16f(w[20]), dmin = f16f(w[20] >> 16);
+#pragma unroll
+  for (int s = 0; s < 16; s++) {
+    const int half = s / 8, j = (s % 8) / 2, o = 16 * (s % 2);
+    uint32_t q[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) q[i] = (w[(16 + 32 * half + o) / 4 + i] >> (2 * j)) & 0x03030303u;
+    uint32_t sc = byte_of(w, s);
+    float dl = d * (float)(sc & 15u), ml = dmin * (float)(sc >> 4);
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+      if (t < m) {
+        const uint32_t* xa = reinterpret_cast<const uint32_t*>(x[t] + 16 * s);
+        int dt = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
+        acc[t] += xs[t][s / 2] * (dl * (float)dt - ml * __uint_as_float(sm[t][s]));
+      }
+    }
+  }
+}
+
+template <int QT, int TM>
+__device__ __forceinline__ void pk_block(const uint32_t* w, const int8_t* const* x, const float* const* xs,
+                                         const uint32_t* const* sm, float* acc, int m) {
+  if constexpr (QT == Q4_K) pk_q4k<TM>(w, x, xs, sm, acc, m);
+  else if constexpr (QT == Q5_K) pk_q5k<TM>(w, x, xs, sm, acc, m);
+  else if constexpr (QT == Q6_K) pk_q6k<TM>(w, x, xs, sm, acc, m);
+  else if constexpr (QT == Q3_K) pk_q3k<TM>(w, x, xs, sm, acc, m);
+  else if constexpr (QT == Q2_K) pk_q2k<TM>(w, x, xs, sm, acc, m);
+}
+
+}  // namespace gmoe

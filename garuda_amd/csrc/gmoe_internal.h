@@ -29,22 +29,82 @@ inline bool block_layout(uint32_t t, uint32_t* elems, uint32_t* bytes) {
 }
 
 // quant/mod.rs:379-381: types whose packed rows are dotted against int8 activations.
-inline bool has_int8_kernel(uint32_t t) {
+__host__ __device__ constexpr bool has_int8_kernel(uint32_t t) {
   return t == Q8_0 || t == Q2_K || t == Q3_K || t == Q4_K || t == Q5_K || t == Q6_K;
 }
 
-// Rows of every packed matrix are stored in the slab at a pitch rounded up to 16 bytes,
-// so each row starts 16-byte aligned whatever the block size.
-inline size_t row_pitch(size_t row_bytes) { return (row_bytes + 15) & ~size_t(15); }
+// ---------------------------------------------------------------------------------
+// Tiled slab layout of an expert matrix (rows x cols, packed rows of blocks).
+//
+// A row is cut into units of G consecutive blocks (EU elements) stored as U bytes, U a
+// multiple of 16: one block padded with zeros (Q4_K, Q5_K, Q6_K, Q3_K, Q2_K, F32), two
+// F16 blocks of 32 values, or eight Q8_0/Q4_0 blocks repacked as their eight f16 scales
+// (16 bytes) followed by their quant bytes, so every block's quants stay dword
+// aligned. Rows are grouped in tiles of 64, and a tile stores its units one after
+// another; within a unit, 16-byte piece p of row i of the tile sits at p*1024 + i*16.
+// A wave that streams a tile therefore reads each unit as NP = U/16 fully coalesced
+// 1 KiB loads, and lane i receives its own row's unit in registers. Rows past the end
+// of the matrix and blocks past the end of a row are zero bytes.
+// ---------------------------------------------------------------------------------
+constexpr uint32_t kTileRows = 64;
 
-// Activations of one matrix product, in the format its kernel reads.
-// int8 form (quant/mod.rs:331-345, :322-326): per token K int8 values, K/32 scales,
-// K/16 sums of 16 (sums of 32 are the pairwise totals).
-struct ActQ {
-  const int8_t* q;     // [rows_of_tokens][K]
-  const float* s;      // [..][K/32]
-  const int32_t* s16;  // [..][K/16]
+struct Unit {
+  uint32_t G;   // blocks per unit
+  uint32_t EU;  // elements per unit
+  uint32_t U;   // bytes per unit in the slab
+  uint32_t B;   // bytes per block in the packed row
 };
+
+__host__ __device__ inline bool unit_of(uint32_t t, Unit* u) {
+  switch (t) {
+    case F32: *u = {1, 32, 128, 128}; return true;
+    case F16: *u = {2, 64, 128, 64}; return true;
+    case Q4_0: *u = {8, 256, 144, 18}; return true;
+    case Q8_0: *u = {8, 256, 272, 34}; return true;
+    case Q2_K: *u = {1, 256, 96, 84}; return true;
+    case Q3_K: *u = {1, 256, 112, 110}; return true;
+    case Q4_K: *u = {1, 256, 144, 144}; return true;
+    case Q5_K: *u = {1, 256, 176, 176}; return true;
+    case Q6_K: *u = {1, 256, 224, 210}; return true;
+  }
+  return false;
+}
+
+// Blocks in a row of `cols` elements (F32/F16 counted as blocks of 32 values).
+__host__ __device__ inline uint32_t row_blocks(const Unit& u, uint32_t cols) { return cols / (u.EU / u.G); }
+__host__ __device__ inline uint32_t row_units(const Unit& u, uint32_t cols) {
+  return (row_blocks(u, cols) + u.G - 1) / u.G;
+}
+// Bytes of one 64-row tile and of the whole tiled matrix.
+__host__ __device__ inline uint64_t tile_bytes(const Unit& u, uint32_t cols) {
+  return (uint64_t)row_units(u, cols) * kTileRows * u.U;
+}
+__host__ __device__ inline uint64_t tiled_bytes(const Unit& u, uint32_t rows, uint32_t cols) {
+  return (uint64_t)((rows + kTileRows - 1) / kTileRows) * tile_bytes(u, cols);
+}
+
+// Byte `b` of unit `un` of a row with `nblk` blocks: its offset in the packed row, or
+// -1 where the unit holds padding.
+__host__ __device__ inline int64_t unit_src_byte(uint32_t t, const Unit& u, uint32_t nblk, uint32_t un,
+                                                 uint32_t b) {
+  const uint64_t b0 = (uint64_t)un * u.G;  // first block of the unit
+  if (t == Q8_0 || t == Q4_0) {
+    uint32_t g, o;
+    if (b < 16) {
+      g = b / 2;
+      o = b % 2;
+    } else {
+      const uint32_t qb = u.B - 2;  // quant bytes per block
+      g = (b - 16) / qb;
+      o = 2 + (b - 16) % qb;
+    }
+    if (g >= u.G || b0 + g >= nblk) return -1;
+    return (int64_t)((b0 + g) * u.B + o);
+  }
+  const uint32_t g = b / u.B;
+  if (g >= u.G || b0 + g >= nblk) return -1;
+  return (int64_t)((b0 + g) * u.B + b % u.B);
+}
 
 // Per-call device buffers. Token-indexed arrays have n rows; slot-indexed ones n*k.
 struct FwdBufs {
@@ -74,13 +134,17 @@ struct LayerDev {
   uint32_t d, f, ne, k, gating, combine, math;
   uint32_t qt_gate, qt_up, qt_down;
   const float* router;          // device [ne][d]
-  const uint8_t* const* eptr;   // device [3][ne]: gate, up, down base of each expert (null = absent)
-  uint32_t pitch_gate, pitch_up, pitch_down;
+  const uint8_t* const* eptr;   // device [3][ne]: gate, up, down tiled matrix of each expert (null = absent)
 };
 
-// The down product of the row kernels splits K over this many partial slices at most;
-// FwdBufs::y holds kMaxKsg slices of [n*k][d].
+// The down product splits K over this many partial slices at most; FwdBufs::y holds
+// kMaxKsg slices of [n*k][d]. A down workgroup has kDnKS waves, each its own K range.
 constexpr uint32_t kMaxKsg = 8;
+constexpr int kDnKS = 2;
+
+// Expert products of one block type (gmoe_units.hip, built once per type).
+template <int QT> hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+template <int QT> hipError_t units_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
 
 // Launchers (gmoe_kernels.hip). All are asynchronous on `st` and validate nothing:
 // the host runtime checks shapes before calling them.
@@ -102,10 +166,9 @@ hipError_t launch_combine(const LayerDev& L, const FwdBufs& B, uint32_t n, hipSt
 uint32_t down_ksg(const LayerDev& L, uint32_t n);
 // out[i] = parts[i] + parts[count + i] + ... over ksg slices, in slice order.
 hipError_t launch_reduce_parts(const float* parts, uint32_t ksg, size_t count, float* out, hipStream_t st);
-// Plain matrix product for gmoe_matmul: out[b*rows + r] = dot(row r, x[b]).
-hipError_t launch_matmul(uint32_t qtype, uint32_t math, const uint8_t* w, size_t pitch,
-                         uint32_t rows, uint32_t cols, const float* x, const int8_t* xq,
-                         const float* xs, const int32_t* x16, uint32_t n, float* out,
-                         hipStream_t st);
+// Rows [r0, r0 + nrows) of a packed matrix (raw rows of row_bytes each, r0 a multiple of
+// 64) -> the tiles they make up in the tiled layout of the whole matrix at dst.
+hipError_t launch_tile_rows(uint32_t qtype, const uint8_t* raw, uint32_t r0, uint32_t nrows, uint32_t rows,
+                            uint32_t cols, uint8_t* dst, hipStream_t st);
 
 }  // namespace gmoe

@@ -198,6 +198,14 @@ def test_layer_gating_variants(dev, gating, combine):
     check_layer(dev, 256, 512, 8, 2, (G.Q4_K,) * 3, (1, 9), G.MATH_PACKED, gating, combine, seed=gating)
 
 
+@pytest.mark.parametrize("qts", [(G.Q4_K,) * 3, (G.Q6_K, G.Q6_K, G.Q8_0), (G.Q3_K, G.Q3_K, G.Q4_K), (G.Q8_0,) * 3])
+@pytest.mark.parametrize("math", [G.MATH_PACKED, G.MATH_F32])
+def test_wide_rows_split_over_waves(dev, qts, math):
+    # d_model 4096 gives 16 units a row: decode batches of 1-2 tokens split each
+    # gate/up row over 2-4 waves, larger ones keep one wave per row
+    check_layer(dev, 4096, 512, 8, 2, qts, (1, 2, 3, 8), math, seed=6)
+
+
 def test_split_layout_matches_stacked(dev):
     check_layer(dev, 256, 512, 8, 2, (G.Q4_K,) * 3, (3,), G.MATH_PACKED, seed=4, split=True)
 
