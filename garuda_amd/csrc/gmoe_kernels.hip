@@ -588,13 +588,13 @@ hipError_t launch_reduce_parts(const float* parts, uint32_t ksg, size_t count, f
 // Expert-product dispatch by block type (the kernels live in gmoe_units.hip)
 // ---------------------------------------------------------------------------------
 
-// K groups of the down product: enough workgroups to cover the chip twice over, each
-// wave keeping at least 4 units to stream.
+// K groups of the down product: enough workgroups for two waves per SIMD (1024
+// workgroups of kDnKS = 2 waves on 256 CUs), each wave keeping at least 4 units.
 uint32_t down_ksg(const LayerDev& L, uint32_t n) {
   Unit un;
   if (!unit_of(L.qt_down, &un)) return 1;
   const uint32_t tiles = (L.d + kTileRows - 1) / kTileRows, ymax = min(L.ne, n * L.k);
-  const uint32_t ksg = (512 + tiles * ymax - 1) / (tiles * ymax);
+  const uint32_t ksg = (1024 + tiles * ymax - 1) / (tiles * ymax);
   const uint32_t cap = max(1u, row_units(un, L.f) / (kDnKS * 4));
   return max(1u, min(min(ksg, cap), kMaxKsg));
 }

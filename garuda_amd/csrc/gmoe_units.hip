@@ -291,7 +291,7 @@ __host__ __device__ constexpr uint32_t unit_count(uint32_t cols) {
 // and u are quant::matmul's row dots term for term (quant/mod.rs:266-279).
 // grid.x = row tiles, grid.y = active-expert slot.
 template <int QT, int TM, bool PACKED, int KG>
-__global__ void __launch_bounds__(128 * KG)
+__global__ void __launch_bounds__(128 * KG, 2)
 k_gu_units(RowIO io, uint32_t ne, uint32_t f, uint32_t d, const int8_t* __restrict__ xq, const float* __restrict__ xs,
            const int32_t* __restrict__ x16, const float* __restrict__ hs, int8_t* __restrict__ hq,
            float* __restrict__ hsc, int32_t* __restrict__ h16, float* __restrict__ hf) {
@@ -352,7 +352,7 @@ k_gu_units(RowIO io, uint32_t ne, uint32_t f, uint32_t d, const int8_t* __restri
 // partial slice y[blockIdx.y]; the combine adds the slices in order.
 // grid.x = row tiles of d_model, grid.y = K groups, grid.z = active-expert slot.
 template <int QT, int TM, bool PACKED, int KS>
-__global__ void __launch_bounds__(64 * KS)
+__global__ void __launch_bounds__(64 * KS, 2)
 k_dn_units(RowIO io, uint32_t ne, uint32_t f, uint32_t d, uint32_t part_stride, const int8_t* __restrict__ hq,
            const float* __restrict__ hsc, const int32_t* __restrict__ h16, const float* __restrict__ hf,
            float* __restrict__ ypart) {
@@ -412,8 +412,6 @@ k_dn_units(RowIO io, uint32_t ne, uint32_t f, uint32_t d, uint32_t part_stride, 
 
 constexpr uint32_t kLdsBudget = 160 * 1024 - 2048;
 
-// tokens handled together per pass: enough for a decode batch, capped at 8
-static inline int pick_tm(uint32_t n) { return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : 8; }
 
 template <class K>
 static bool allow_lds(K kernel) {
@@ -462,9 +460,16 @@ static int pick_kg(const LayerDev& L, uint32_t n, int tm) {
   return kg;
 }
 
+// Tokens per pass: the decode batch, capped at 8 (packed) or 4 (f32 math, whose body
+// holds a dequantised group of 32 values besides the accumulators).
+template <bool PACKED>
+static inline int pick_tm(uint32_t n) {
+  return n <= 1 ? 1 : n <= 2 ? 2 : (n <= 4 || !PACKED) ? 4 : 8;
+}
+
 template <int QT, bool PACKED>
 static void go_gu_tm(const LayerDev& L, const FwdBufs& B, dim3 g, uint32_t n, hipStream_t st) {
-  const int tm = fit_tm(pick_tm(n), [&](uint32_t t) { return gu_lds<QT, PACKED>(t, 1, L.d); });
+  const int tm = fit_tm(pick_tm<PACKED>(n), [&](uint32_t t) { return gu_lds<QT, PACKED>(t, 1, L.d); });
   const int kg = pick_kg<QT, PACKED>(L, n, tm);
   if constexpr (!PACKED) {
     if (kg > 1) {
@@ -479,7 +484,9 @@ static void go_gu_tm(const LayerDev& L, const FwdBufs& B, dim3 g, uint32_t n, hi
     case 1: go_gu<QT, 1, PACKED, 1>(L, B, g, st); break;
     case 2: go_gu<QT, 2, PACKED, 1>(L, B, g, st); break;
     case 4: go_gu<QT, 4, PACKED, 1>(L, B, g, st); break;
-    default: go_gu<QT, 8, PACKED, 1>(L, B, g, st); break;
+    default:
+      if constexpr (PACKED) go_gu<QT, 8, PACKED, 1>(L, B, g, st);
+      break;
   }
 }
 
@@ -506,7 +513,9 @@ static void go_dn_tm(const LayerDev& L, const FwdBufs& B, dim3 g, int want, uint
     case 1: go_dn<QT, 1, PACKED>(L, B, g, n, st); break;
     case 2: go_dn<QT, 2, PACKED>(L, B, g, n, st); break;
     case 4: go_dn<QT, 4, PACKED>(L, B, g, n, st); break;
-    default: go_dn<QT, 8, PACKED>(L, B, g, n, st); break;
+    default:
+      if constexpr (PACKED) go_dn<QT, 8, PACKED>(L, B, g, n, st);
+      break;
   }
 }
 
@@ -525,12 +534,11 @@ hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStre
 template <int QT>
 hipError_t units_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st) {
   const dim3 g((L.d + kTileRows - 1) / kTileRows, ksg, min(L.ne, n * L.k));
-  const int tm = pick_tm(n);
   if constexpr (has_int8_kernel(QT)) {
-    if (L.math == 0) go_dn_tm<QT, true>(L, B, g, tm, n, st);
-    else go_dn_tm<QT, false>(L, B, g, tm, n, st);
+    if (L.math == 0) go_dn_tm<QT, true>(L, B, g, pick_tm<true>(n), n, st);
+    else go_dn_tm<QT, false>(L, B, g, pick_tm<false>(n), n, st);
   } else {
-    go_dn_tm<QT, false>(L, B, g, tm, n, st);
+    go_dn_tm<QT, false>(L, B, g, pick_tm<false>(n), n, st);
   }
   return hipGetLastError();
 }
