@@ -158,6 +158,7 @@ struct gmoe_ctx {
   uint8_t* pinned = nullptr;
   size_t pinned_bytes = 0;
   uint8_t* bounce = nullptr;  // device landing area of the pinned halves (same size)
+  uint32_t* done = nullptr;   // front-end completion counter (device, zero between calls)
   hipEvent_t pin_ev[2]{};
   // scratch arena
   uint8_t* scratch = nullptr;
@@ -371,6 +372,7 @@ Timing take_timing(gmoe_ctx* c) {
 // The launch sequence of one call. B's activation/output pointers are set by the caller.
 gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStream_t st) {
   LayerDev D = layer_dev(L);
+  B.done = c->done;
   // int8 h only when the down product reads it; f32 h otherwise
   if (!uses_int8(L.math, L.p[2].qtype)) {
     B.hq = nullptr;
@@ -501,6 +503,8 @@ gmoe_status gmoe_init(int device, uint64_t slab_bytes, gmoe_ctx** out) {
   c->pinned_bytes = (size_t)64 << 20;
   HIP_TRY(hipHostMalloc((void**)&c->pinned, c->pinned_bytes, hipHostMallocDefault));
   HIP_TRY(hipMalloc(&c->bounce, c->pinned_bytes));
+  HIP_TRY(hipMalloc(&c->done, 256));
+  HIP_TRY(hipMemset(c->done, 0, 256));
   HIP_TRY(hipEventCreateWithFlags(&c->pin_ev[0], hipEventDisableTiming));
   HIP_TRY(hipEventCreateWithFlags(&c->pin_ev[1], hipEventDisableTiming));
   HIP_TRY(hipEventRecord(c->pin_ev[0], c->copy_stream));
@@ -529,6 +533,7 @@ void gmoe_shutdown(gmoe_ctx* c) {
   if (c->scratch) hipFree(c->scratch);
   if (c->pinned) hipHostFree(c->pinned);
   if (c->bounce) hipFree(c->bounce);
+  if (c->done) hipFree(c->done);
   hipEventDestroy(c->pin_ev[0]);
   hipEventDestroy(c->pin_ev[1]);
   hipStreamDestroy(c->stream);

@@ -128,6 +128,7 @@ struct FwdBufs {
   int32_t* h16;          // [n*k][f/16]
   float* hf;             // [n*k][f]
   float* y;              // [kMaxKsg][n*k][d] partial slices of the down product
+  uint32_t* done;        // [1] workgroups of the front end that have finished; 0 between calls
 };
 
 struct LayerDev {

@@ -314,161 +314,291 @@ __global__ void __launch_bounds__(256) k_dispatch(LayerDev L, FwdBufs B, uint32_
 }
 
 // ---------------------------------------------------------------------------------
-// Fused decode front end: router logits, gating, the int8 activation quantiser and the
-// dispatch in one workgroup of 512 threads, for n*ne <= 64 (one chain per lane of
-// wave 0). The logits' products w*h (each rounded, as the reference multiplies before
-// it adds) are made by waves 1..15 one K-chunk ahead into LDS; wave 0 only runs the 64
-// sequential add chains over them, so the chain's latency is the adds alone.
-// (The products are made by waves 1..7.)
+// Gating and dispatch by one wave (ne <= 64: lane e holds expert e). They compute what
+// gate_block and dispatch_block do, with every ordered sum taken lane by lane in index
+// order through readlane, so the arithmetic is the same; maxima and counts, which no
+// order changes, are cross-lane reductions.
 // ---------------------------------------------------------------------------------
 
-constexpr int kFrontKC = 128, kFrontPairs = 64, kFrontRows = 16, kFrontRing = 16, kFrontMaxCh = 32;
-constexpr int kFrontProd = 512, kFrontThreads = 64 + kFrontProd;
-constexpr int kFrontRow = kFrontKC + 4;  // padded LDS row (floats)
+__device__ __forceinline__ float lane_f(float v, uint32_t l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)l));
+}
+__device__ __forceinline__ uint32_t lane_u(uint32_t v, uint32_t l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l);
+}
 
-// Producer p owns one float4 column slot (row p / 32, float4 p % 32) of every K chunk of
-// the (router rows ; token rows) operand matrix and loads it 16 chunks ahead into a
-// register ring; each chunk is parked in LDS two chunks before its products are made.
-// The chunk loop is fully unrolled so ring indices are compile-time.
-__global__ void __launch_bounds__(kFrontThreads) k_front_small(LayerDev L, FwdBufs B, uint32_t n, int quant) {
-  extern __shared__ float fs[];
-  float* stage = fs;                                    // [2][kFrontRows][kFrontRow]
-  float* prod = stage + 2 * kFrontRows * kFrontRow;     // [2][kFrontPairs][kFrontRow]
-  float* lg = prod + 2 * kFrontPairs * kFrontRow;       // [n][ne]
-  float* red = lg + kFrontPairs;                        // [n]
-  float* topw = red + kFrontPairs;                      // [n][k]
-  uint32_t* topi = reinterpret_cast<uint32_t*>(topw + kFrontPairs * 32);
-  uint32_t* cnt = topi + kFrontPairs * 32;              // [ne]
-  const uint32_t ne = L.ne, d = L.d, P = n * ne, R = ne + n;
-  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  if (B.logits_in) {
-    for (uint32_t p = tid; p < P; p += blockDim.x) lg[p] = B.logits_in[p];
-  } else {
-    const uint32_t nch = d / kFrontKC;
-    const bool producer = wave != 0;
-    const uint32_t p = tid - 64, r = p / 32, c4 = p % 32;
-    const bool slot = producer && r < R;
-    const float4* src = reinterpret_cast<const float4*>(slot ? (r < ne ? L.router + (size_t)r * d
-                                                                      : B.hs + (size_t)(r - ne) * d)
-                                                             : L.router);
-    // the ring is one 64-wide vector value: constant-index element accesses stay in VGPRs
-    typedef float f32x64 __attribute__((ext_vector_type(64)));
-    f32x64 ring = {};
-    auto ring_put = [&](int i, float4 v) __attribute__((always_inline)) {
-      ring[4 * i] = v.x; ring[4 * i + 1] = v.y; ring[4 * i + 2] = v.z; ring[4 * i + 3] = v.w;
-    };
-    auto ring_get = [&](int i) __attribute__((always_inline)) {
-      return make_float4(ring[4 * i], ring[4 * i + 1], ring[4 * i + 2], ring[4 * i + 3]);
-    };
-#pragma unroll
-    for (int c = 0; c < kFrontRing; c++)
-      if (slot && (uint32_t)c < nch) ring_put(c, src[c * (kFrontKC / 4) + c4]);
-    float acc = -0.0f;
-    // prologue: park chunks 0 and 1, make chunk 0's products
-#pragma unroll
-    for (int c = 0; c < 2; c++) {
-      if (slot && (uint32_t)c < nch) {
-        *reinterpret_cast<float4*>(stage + (c * kFrontRows + r) * kFrontRow + 4 * c4) = ring_get(c);
-        if ((uint32_t)(c + kFrontRing) < nch) ring_put(c, src[(c + kFrontRing) * (kFrontKC / 4) + c4]);
-      }
+// One token's routing from its logit x (lane e < ne). Lanes r < k receive the r-th
+// ranked expert and its weight. `scratch` holds 2*k words of LDS.
+__device__ void gate_wave(uint32_t gating, uint32_t ne, uint32_t k, float x, uint32_t lane, uint32_t* id_out,
+                          float* w_out, uint32_t* scratch) {
+  const bool llama = gating == 0;
+  float v = x;
+  if (gating == 0 || gating == 2 || gating == 3) {  // softmax over all experts (simd/mod.rs:132-158)
+    float mx = -INFINITY;
+    for (uint32_t e = 0; e < ne; e++) mx = fmaxf(mx, lane_f(x, e));
+    if (isfinite(mx)) v = gm_expf(x - mx);
+    float inv = -1.0f;  // uniform
+    if (isfinite(mx)) {
+      float sum = 0.0f;
+      for (uint32_t e = 0; e < ne; e++) sum += lane_f(v, e);
+      if (isfinite(sum) && sum > 0.0f) inv = fdiv(1.0f, sum);
     }
-    __syncthreads();
-    if (producer) {
-#pragma unroll
-      for (int q = 0; q < kFrontPairs * kFrontKC / 4 / kFrontProd; q++) {
-        uint32_t g = p + kFrontProd * q, pr = g / (kFrontKC / 4), j = 4 * (g % (kFrontKC / 4));
-        if (pr < P) {
-          uint32_t t = pr / ne, e = pr % ne;
-          float4 av = *reinterpret_cast<const float4*>(stage + e * kFrontRow + j);
-          float4 hv = *reinterpret_cast<const float4*>(stage + (ne + t) * kFrontRow + j);
-          *reinterpret_cast<float4*>(prod + pr * kFrontRow + j) =
-              make_float4(av.x * hv.x, av.y * hv.y, av.z * hv.z, av.w * hv.w);
-        }
-      }
-    }
-    __syncthreads();
-    // iteration c: wave 0 chains chunk c | producers make chunk c+1's products and park
-    // chunk c+2 (whose LDS slot chunk c's products have finished with)
-#pragma unroll
-    for (int c = 0; c < kFrontMaxCh; c++) {
-      if ((uint32_t)c < nch) {
-        if (wave == 0) {
-          if (lane < P) {
-            const float* src2 = prod + (c & 1) * kFrontPairs * kFrontRow + lane * kFrontRow;
-#pragma unroll
-            for (int j0 = 0; j0 < kFrontKC; j0 += 32) {
-              float4 v[8];
-#pragma unroll
-              for (int u = 0; u < 8; u++) v[u] = *reinterpret_cast<const float4*>(src2 + j0 + 4 * u);
-#pragma unroll
-              for (int u = 0; u < 8; u++) {
-                acc = acc + v[u].x;
-                acc = acc + v[u].y;
-                acc = acc + v[u].z;
-                acc = acc + v[u].w;
-              }
-            }
-          }
-        } else {
-          if ((uint32_t)(c + 1) < nch) {
-            const float* st = stage + ((c + 1) & 1) * kFrontRows * kFrontRow;
-            float* dst = prod + ((c + 1) & 1) * kFrontPairs * kFrontRow;
-#pragma unroll
-            for (int q = 0; q < kFrontPairs * kFrontKC / 4 / kFrontProd; q++) {
-              uint32_t g = p + kFrontProd * q, pr = g / (kFrontKC / 4), j = 4 * (g % (kFrontKC / 4));
-              if (pr < P) {
-                uint32_t t = pr / ne, e = pr % ne;
-                float4 av = *reinterpret_cast<const float4*>(st + e * kFrontRow + j);
-                float4 hv = *reinterpret_cast<const float4*>(st + (ne + t) * kFrontRow + j);
-                *reinterpret_cast<float4*>(dst + pr * kFrontRow + j) =
-                    make_float4(av.x * hv.x, av.y * hv.y, av.z * hv.z, av.w * hv.w);
-              }
-            }
-          }
-          if (slot && (uint32_t)(c + 2) < nch) {
-            const int slot_i = (c + 2) % kFrontRing;
-            *reinterpret_cast<float4*>(stage + ((c & 1) * kFrontRows + r) * kFrontRow + 4 * c4) = ring_get(slot_i);
-            if ((uint32_t)(c + 2 + kFrontRing) < nch) ring_put(slot_i, src[(c + 2 + kFrontRing) * (kFrontKC / 4) + c4]);
-          }
-        }
-        __syncthreads();
-      }
-    }
-    if (wave == 0 && lane < P) lg[lane] = acc;
+    v = inv < 0.0f ? fdiv(1.0f, (float)ne) : v * inv;
   }
-  __syncthreads();
-  for (uint32_t p = tid; p < P; p += blockDim.x) B.logits[p] = lg[p];
-  gate_block(L, B, lg, red, topw, topi, n, 0, n);
-  if (quant) {
-    const uint32_t nblk = n * (d / 32);
-    for (uint32_t b = tid; b < nblk; b += blockDim.x) {
+  // rank = how many experts come before this one
+  uint32_t r = 0;
+  for (uint32_t o = 0; o < ne; o++)
+    if (o != lane && ranks_before(llama, lane_f(v, o), o, v, lane)) r++;
+  float* tw = reinterpret_cast<float*>(scratch);
+  uint32_t* ti = scratch + k;
+  if (lane < ne && r < k) {
+    tw[r] = v;
+    ti[r] = lane;
+  }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");  // one wave: its DS writes land before these reads
+  float w = lane < k ? tw[lane] : 0.0f;
+  const uint32_t id = lane < k ? ti[lane] : 0u;
+  if (gating == 0) {  // llama/mod.rs:945-949
+    float sum = -0.0f;
+    for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
+    w *= sum > 0.0f ? fdiv(1.0f, sum) : fdiv(1.0f, (float)k);
+  } else if (gating == 1) {  // router/mod.rs:91-97: softmax over the k kept logits
+    float mx = -INFINITY;
+    for (uint32_t i = 0; i < k; i++) mx = fmaxf(mx, lane_f(w, i));
+    if (!isfinite(mx)) {
+      w = fdiv(1.0f, (float)k);
+    } else {
+      w = gm_expf(w - mx);
+      float sum = 0.0f;
+      for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
+      w = (isfinite(sum) && sum > 0.0f) ? w * fdiv(1.0f, sum) : fdiv(1.0f, (float)k);
+    }
+  } else if (gating == 3) {  // router/mod.rs:102-115
+    float sum = -0.0f;
+    for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
+    w = sum > 0.0f ? fdiv(w, sum) : fdiv(1.0f, (float)k);
+  }
+  *id_out = id;
+  *w_out = w;
+}
+
+// Stable counting sort of the nk (token, rank) pairs by expert: members[e] of
+// llama/mod.rs:967-972 laid end to end, as dispatch_block makes it. pair(p, &id, &w)
+// reads pair p. Pairs go 64 at a time; per expert a ballot finds its pairs in the chunk
+// and lane e keeps expert e's count, then its next free slot.
+template <class Pair>
+__device__ void dispatch_wave(const FwdBufs& B, uint32_t ne, uint32_t k, uint32_t nk, uint32_t lane, Pair pair) {
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint32_t cnt = 0;
+  for (uint32_t c0 = 0; c0 < nk; c0 += 64) {
+    uint32_t id = ~0u;
+    float w;
+    if (c0 + lane < nk) pair(c0 + lane, &id, &w);
+    for (uint32_t e = 0; e < ne; e++) {
+      const uint32_t c = (uint32_t)__popcll(__ballot(id == e));
+      if (lane == e) cnt += c;
+    }
+  }
+  uint32_t off = 0, run = 0;
+  for (uint32_t e = 0; e < ne; e++) {
+    if (lane == e) off = run;
+    run += lane_u(cnt, e);
+  }
+  const uint64_t act = __ballot(lane < ne && cnt > 0);
+  if (lane < ne) {
+    B.offsets[lane] = off;
+    if (cnt > 0) B.active[1 + __popcll(act & below)] = lane;
+  }
+  if (lane == 0) {
+    B.offsets[ne] = run;
+    B.active[0] = (uint32_t)__popcll(act);
+  }
+  for (uint32_t c0 = 0; c0 < nk; c0 += 64) {
+    uint32_t id = ~0u, pos = 0;
+    float w = 0.0f;
+    const uint32_t p = c0 + lane;
+    if (p < nk) pair(p, &id, &w);
+    for (uint32_t e = 0; e < ne; e++) {
+      const uint64_t m = __ballot(id == e);
+      if (id == e) pos = lane_u(off, e) + (uint32_t)__popcll(m & below);
+      if (lane == e) off += (uint32_t)__popcll(m);
+    }
+    if (p < nk) {
+      B.slot_tok[pos] = p / k;
+      B.slot_w[pos] = w;
+      B.slot_rank[pos] = p % k;
+      B.slot_of[p] = pos;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Fused front end: router logits, gating, the int8 activation quantiser and the
+// dispatch in one launch of one workgroup per token (ne <= 64 experts).
+//
+// A logit is the reference's sequential f32 dot (simd/mod.rs:13-16): products w*h, each
+// rounded, added left to right from -0.0. Its latency is its d dependent adds, so wave
+// 0 (lane e = expert e) does only those adds while eight producer waves make the
+// products into LDS ahead of it. K is cut into sections as long as two LDS halves of
+// [ne][section] allow (2432 values for 8 experts), and the two sides meet at a barrier
+// once per section: while wave 0 adds section s from one half, the producers fill the
+// other with section s+1 (and quantise the token's activations during the last one).
+// Wave 0 reads its products 32 at a time from two fixed register buffers, each batch
+// fetched one batch ahead by an unconditional load, so it waits only for the batch it
+// adds. Gating follows per token. The workgroup that finishes last (a device-wide
+// counter taken after a release fence) does the dispatch over every token's routing and
+// puts the counter back to zero.
+// ---------------------------------------------------------------------------------
+
+constexpr int kFrontExperts = 64, kFrontProdWaves = 8, kFrontThreads = 64 * (1 + kFrontProdWaves);
+constexpr uint32_t kFrontProdBytes = 156 * 1024;  // both LDS halves of products (the rest: < 1 KB)
+constexpr int kFrontItems = 12;                   // float4 products a producer lane has in flight
+
+// Section length for ne experts: the longest multiple of 128 whose two halves fit.
+static inline uint32_t front_section(uint32_t ne, uint32_t d) {
+  const uint32_t sec = (kFrontProdBytes / (8 * ne) - 4) & ~127u;
+  return sec < d ? sec : d;
+}
+
+__global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, uint32_t n, int quant, uint32_t sec) {
+  extern __shared__ float fs[];
+  const uint32_t ne = L.ne, d = L.d, k = L.k, t = blockIdx.x, row = sec + 4;  // padded row of one expert
+  float* prod = fs;                                                 // [2][ne][row]
+  uint32_t* scratch = reinterpret_cast<uint32_t*>(prod + 2 * ne * row);  // [2k] gating
+  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const uint32_t nsec = (d + sec - 1) / sec;
+  const float* hs = B.hs + (size_t)t * d;
+  // producer wave pw (1..8) makes the rows of experts pw-1, pw-1+8, ...; its items are
+  // (expert, float4 column) pairs, kFrontItems of them in flight per lane
+  auto produce = [&](uint32_t s) {
+    const uint32_t k0 = s * sec, len4 = min(sec, d - k0) / 4, e0 = wave - 1;
+    const uint32_t nexp = e0 < ne ? (ne - e0 + kFrontProdWaves - 1) / kFrontProdWaves : 0;
+    const uint32_t total = nexp * len4;
+    const float4* xr = reinterpret_cast<const float4*>(hs + k0);
+    float* half = prod + (s & 1) * ne * row;
+    for (uint32_t base = 0; base < total; base += 64 * kFrontItems) {
+      float4 wv[kFrontItems], xv[kFrontItems];
+      uint32_t off[kFrontItems];
+#pragma unroll
+      for (int i = 0; i < kFrontItems; i++) {
+        const uint32_t q = base + lane + 64 * i;
+        if (q < total) {
+          const uint32_t el = q / len4, j = q - el * len4, e = e0 + kFrontProdWaves * el;
+          wv[i] = reinterpret_cast<const float4*>(L.router + (size_t)e * d + k0)[j];
+          xv[i] = xr[j];
+          off[i] = e * row + 4 * j;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kFrontItems; i++) {
+        if (base + lane + 64 * i < total)
+          *reinterpret_cast<float4*>(half + off[i]) =
+              make_float4(wv[i].x * xv[i].x, wv[i].y * xv[i].y, wv[i].z * xv[i].z, wv[i].w * xv[i].w);
+      }
+    }
+  };
+  auto quantise = [&] {
+    const uint32_t nblk = d / 32;
+    for (uint32_t b = tid - 64; b < nblk; b += 64 * kFrontProdWaves) {
       float v[32];
-      const float4* src = reinterpret_cast<const float4*>(B.hs + (size_t)b * 32);
+      const float4* src = reinterpret_cast<const float4*>(hs + (size_t)b * 32);
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         float4 t4 = src[i];
         v[4 * i] = t4.x; v[4 * i + 1] = t4.y; v[4 * i + 2] = t4.z; v[4 * i + 3] = t4.w;
       }
-      quant32(v, B.xq + (size_t)b * 32, B.xs + b, B.x16 + 2 * (size_t)b);
+      const size_t gb = (size_t)t * nblk + b;
+      quant32(v, B.xq + gb * 32, B.xs + gb, B.x16 + 2 * gb);
     }
+  };
+  float x = 0.0f;  // wave 0, lane e < ne: the logit of expert e
+  if (B.logits_in) {
+    if (wave == 0 && lane < ne) x = B.logits_in[(size_t)t * ne + lane];
+    if (quant && wave != 0) quantise();
+  } else {
+    if (wave != 0) produce(0);
+    __syncthreads();
+    float acc = -0.0f;
+    for (uint32_t s = 0; s < nsec; s++) {
+      if (wave == 0) {
+        if (lane < ne) {
+          // nb batches of 8 float4; sections are multiples of 128 values, so nb is even
+          const uint32_t nb = min(sec, d - s * sec) / 32;
+          const float4* src = reinterpret_cast<const float4*>(prod + (s & 1) * ne * row + lane * row);
+          float4 ba[8], bb[8];
+          auto fetch = [&](float4* dst, uint32_t b) {
+#pragma unroll
+            for (int u = 0; u < 8; u++) dst[u] = src[8 * b + u];
+          };
+          auto add = [&](const float4* v) {
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+              acc = acc + v[u].x;
+              acc = acc + v[u].y;
+              acc = acc + v[u].z;
+              acc = acc + v[u].w;
+            }
+          };
+          fetch(ba, 0);
+          for (uint32_t b = 0; b < nb; b += 2) {
+            fetch(bb, b + 1);
+            add(ba);
+            fetch(ba, min(b + 2, nb - 1));  // the last round re-reads a batch it does not add
+            add(bb);
+          }
+        }
+      } else if (s + 1 < nsec) {
+        produce(s + 1);
+      } else if (quant) {
+        quantise();
+      }
+      __syncthreads();
+    }
+    if (wave == 0) x = acc;
   }
-  __syncthreads();
-  // gate_block leaves every token's ranked ids and weights in topi/topw ([n][k], LDS)
-  dispatch_block(L, B, n, cnt, topi, topw);
+  // the producer waves are done (their last stores were the quantised activations)
+  if (wave != 0) return;
+  if (lane < ne) B.logits[(size_t)t * ne + lane] = x;
+  uint32_t id;
+  float w;
+  gate_wave(L.gating, ne, k, x, lane, &id, &w, scratch);
+  if (lane < k) {
+    B.ids[(size_t)t * k + lane] = id;
+    B.w[(size_t)t * k + lane] = w;
+  }
+  if (n == 1) {  // the only workgroup: pair p (< k) is rank p, which lane p holds
+    dispatch_wave(B, ne, k, k, lane, [&](uint32_t, uint32_t* pid, float* pw) {
+      *pid = id;
+      *pw = w;
+    });
+    return;
+  }
+  // every workgroup's ids and weights are in memory before its count is taken
+  __threadfence();
+  uint32_t prev = 0;
+  if (lane == 0) prev = atomicAdd(B.done, 1u);
+  if (lane_u(prev, 0) == n - 1) {
+    __threadfence();
+    dispatch_wave(B, ne, k, n * k, lane, [&](uint32_t p, uint32_t* pid, float* pw) {
+      *pid = B.ids[p];
+      *pw = B.w[p];
+    });
+    if (lane == 0) *B.done = 0;
+  }
 }
 
 bool front_small_ok(const LayerDev& L, uint32_t n) {
-  return n * L.ne <= (uint32_t)kFrontPairs && L.ne + n <= (uint32_t)kFrontRows && L.k <= 32 &&
-         L.d % kFrontKC == 0 && L.d <= (uint32_t)(kFrontKC * kFrontMaxCh);
+  return n >= 1 && L.ne <= (uint32_t)kFrontExperts && L.k <= 32 && L.d % 128 == 0;
 }
 
 hipError_t launch_front_small(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st) {
-  size_t shm = (size_t)(2 * kFrontRows * kFrontRow + 2 * kFrontPairs * kFrontRow + 2 * kFrontPairs +
-                        2 * kFrontPairs * 32) * 4 + L.ne * 4;
-  static bool attr = (hipFuncSetAttribute((const void*)k_front_small, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                          160 * 1024 - 2048), true);
+  const uint32_t sec = front_section(L.ne, L.d);
+  const size_t shm = ((size_t)2 * L.ne * (sec + 4) + 2 * L.k) * 4;
+  static const bool attr =
+      hipFuncSetAttribute((const void*)k_front, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
   (void)attr;
-  hipLaunchKernelGGL(k_front_small, dim3(1), dim3(kFrontThreads), shm, st, L, B, n, quant);
+  hipLaunchKernelGGL(k_front, dim3(n), dim3(kFrontThreads), shm, st, L, B, n, quant, sec);
   return hipGetLastError();
 }
 

@@ -148,7 +148,8 @@ def oracle_layer(d, f, ne, k, router, mats, qts, math, gating=0, combine=0):
                 router=router, qtypes=qts, **mats)
 
 
-def check_layer(dev, d, f, ne, k, qts, ns, math, gating=0, combine=0, seed=0, logits_scale=None, split=False):
+def check_layer(dev, d, f, ne, k, qts, ns, math, gating=0, combine=0, seed=0, logits_scale=None, split=False,
+                tie_logits=False):
     rng = np.random.default_rng(seed)
     router, mats = make_layer(rng, d, f, ne, qts[0], qts[2])
     gpu_mats = dict(mats)
@@ -167,6 +168,8 @@ def check_layer(dev, d, f, ne, k, qts, ns, math, gating=0, combine=0, seed=0, lo
             logits = None
             if logits_scale is not None:
                 logits = (rng.random((n, ne), dtype=np.float32) * np.float32(logits_scale)).astype(np.float32)
+            if tie_logits:  # four distinct values: most tokens have ties inside and across the top k
+                logits = (rng.integers(0, 4, (n, ne)) * 0.5).astype(np.float32)
             out, ids, w = layer.feed_forward_batch(hs, logits)
             wout, wids, ww = O.feed_forward_batch(L, hs, logits, threads=8)
             assert np.array_equal(ids, wids), "routing differs"
@@ -204,6 +207,16 @@ def test_wide_rows_split_over_waves(dev, qts, math):
     # d_model 4096 gives 16 units a row: decode batches of 1-2 tokens split each
     # gate/up row over 2-4 waves, larger ones keep one wave per row
     check_layer(dev, 4096, 512, 8, 2, qts, (1, 2, 3, 8), math, seed=6)
+
+
+@pytest.mark.parametrize("gating", [G.GATING_LLAMA, G.GATING_MIXTRAL, G.GATING_DEEPSEEK, G.GATING_QWEN])
+def test_front_end_given_logits_with_ties(dev, gating):
+    # ties go to the lower expert id; one workgroup per token, the last one dispatching
+    check_layer(dev, 256, 512, 8, 2, (G.Q4_K,) * 3, (1, 3, 8, 40), G.MATH_PACKED, gating, seed=7, tie_logits=True)
+
+
+def test_front_end_64_experts(dev):
+    check_layer(dev, 256, 256, 64, 6, (G.Q4_K,) * 3, (1, 5, 12), G.MATH_PACKED, seed=8)
 
 
 def test_split_layout_matches_stacked(dev):
