@@ -11,6 +11,10 @@ step streams its experts from HBM rather than from the 256 MB MALL.
 Prints one JSON line with `roofline` (the gate/up kernel: algorithmic bytes per launch /
 its average duration from HIP events on its stream) and `cpu_baseline` (the oracle's
 restatement of the reference's packed CPU path, threaded over rows, on a bounded sample).
+`roofline.traffic` is the HBM bytes per gate/up launch that rocprofv3's FETCH_SIZE and
+WRITE_SIZE counters measured on this same workload, scaled by what they read for a copy of
+known size (`--calibrate-copy`), as recorded in profiles/ (TRAFFIC_FILE); it is null for
+any other configuration.
 """
 from __future__ import annotations
 
@@ -28,6 +32,7 @@ sys.path.insert(0, str(ROOT))
 
 D, F, NE, K = 4096, 14336, 8, 2
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "k_gu_units_q4k_c2_b8_traffic.md"
 SEED = 0x6761_7275_6461_2000  # build-side seeds, "garuda" + tag
 
 
@@ -49,6 +54,30 @@ def make_experts(threads):
     return mats
 
 
+def tm_of(n, packed):
+    """Tokens per pass of the expert kernels for a decode batch (the library's choice)."""
+    return 1 if n <= 1 else 2 if n <= 2 else 4 if (n <= 4 or not packed) else 8
+
+
+def measured_traffic(batch, math, layers):
+    """HBM bytes per gate/up launch from the committed counter summary, if it covers this run."""
+    try:
+        text = TRAFFIC_FILE.read_text()
+    except OSError:
+        return None
+    vals = {}
+    for line in text.splitlines():
+        if ":" in line and line.strip().startswith("- "):
+            key, _, v = line.strip()[2:].partition(":")
+            vals[key.strip()] = v.strip()
+    try:
+        if int(vals["batch"]) != batch or vals["math"] != math or int(vals["layers"]) != layers:
+            return None
+        return float(vals["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -60,6 +89,8 @@ def main():
     ap.add_argument("--math", choices=("packed", "f32"), default="packed")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=1.5, help="wall-clock budget of the CPU sample")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
+                    help="also run one device-to-device copy of MB MiB (the counter calibration of profiles/)")
     a = ap.parse_args()
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -141,6 +172,15 @@ def main():
             f"E={e_avg:.2f}, gate/up {gu_ms * 1e3:.1f} us ({results[n]['gateup_GBs']:.0f} GB/s), "
             f"down {dn_ms * 1e3:.1f} us ({results[n]['down_GBs']:.0f} GB/s), layer {results[n]['layer_GBs']:.0f} GB/s")
 
+    if a.calibrate_copy:
+        src = torch.empty(a.calibrate_copy << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {a.calibrate_copy} MiB read, {a.calibrate_copy} MiB written")
+        del src, dst
+
     cpu = None
     if not a.no_cpu:
         from oracle import oracle as O
@@ -179,9 +219,10 @@ def main():
                                f"batch {a.batch}, {a.layers} HBM copies rotated",
                    "batch": a.batch, "d_model": D, "d_ff": F, "n_experts": NE, "top_k": K, "qtype": "Q4_K",
                    "math": a.math},
-        "roofline": {"bound": "hbm", "kernel": "k_gateup_packed<Q4_K>" if math == G.MATH_PACKED else "k_gateup_f32<Q4_K>",
+        "roofline": {"bound": "hbm", "kernel": f"k_gu_units<Q4_K, TM={tm_of(a.batch, math == G.MATH_PACKED)}, {a.math}>",
                      "achieved": r["gateup_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": r["gateup_GBs"] / HBM_PEAK_GBS, "traffic": None,
+                     "frac": r["gateup_GBs"] / HBM_PEAK_GBS,
+                     "traffic": measured_traffic(a.batch, a.math, a.layers),
                      "bytes_per_launch": r["gateup_bytes"], "avg_launch_us": r["gateup_us"]},
         "cpu_baseline": cpu,
         "sweep": {str(n): {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res.items()}
