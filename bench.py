@@ -8,6 +8,10 @@ inputs already resident in HBM. Steps rotate over `--layers` distinct copies of 
 layer in HBM (different router weights, separate slab copies of the experts) so each
 step streams its experts from HBM rather than from the 256 MB MALL.
 
+Each batch is timed twice over the same steps: bare, for `value` and `ms_per_step`, and
+with HIP events recorded on the stream around every gate/up and down launch, for the
+kernel times (the events themselves add about 3 us per launch to a step).
+
 Prints one JSON line with `roofline` (the gate/up kernel: algorithmic bytes per launch /
 its average duration from HIP events on its stream) and `cpu_baseline` (the oracle's
 restatement of the reference's packed CPU path, threaded over rows, on a bounded sample).
@@ -89,6 +93,9 @@ def main():
     ap.add_argument("--math", choices=("packed", "f32"), default="packed")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=1.5, help="wall-clock budget of the CPU sample")
+    ap.add_argument("--kernel-events", choices=("on", "off"), default="on",
+                    help="also time the steps with HIP events around every gate/up and down launch "
+                         "(the roofline's kernel times); off skips that second pass")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="also run one device-to-device copy of MB MiB (the counter calibration of profiles/)")
     a = ap.parse_args()
@@ -140,23 +147,31 @@ def main():
         for i in range(a.warmup):
             step(i)
         torch.cuda.synchronize()
-        dev.kernel_time(0)  # drain
-        base = [dev.kernel_time(w) for w in range(3)]
-        dev.set_kernel_timing(True)
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        ev0.record(stream)
-        for i in range(a.steps):
-            step(i)
-        ev1.record(stream)
-        torch.cuda.synchronize()
-        dev.set_kernel_timing(False)
-        ms = ev0.elapsed_time(ev1)
-        kt = [dev.kernel_time(w) for w in range(3)]
-        cnt = kt[0][1] - base[0][1]
-        gu_ms = (kt[0][0] - base[0][0]) / cnt
-        dn_ms = (kt[1][0] - base[1][0]) / cnt
-        ex_ms = (kt[2][0] - base[2][0]) / cnt
+
+        def timed(events):
+            """K steps between two synchronisations; with events, also the gate/up and down
+            launch times (HIP events on the stream around each launch)."""
+            dev.kernel_time(0)  # drain
+            base = [dev.kernel_time(w) for w in range(3)]
+            dev.set_kernel_timing(events)
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            ev0.record(stream)
+            for i in range(a.steps):
+                step(i)
+            ev1.record(stream)
+            torch.cuda.synchronize()
+            dev.set_kernel_timing(False)
+            kt = [dev.kernel_time(w) for w in range(3)]
+            cnt = max(kt[0][1] - base[0][1], 1)
+            return ev0.elapsed_time(ev1), [(kt[w][0] - base[w][0]) / cnt for w in range(3)]
+
+        # the throughput is timed bare (the per-launch events cost ~3 us each); the kernel
+        # times come from a second pass over the same steps with events around each launch
+        ms, _ = timed(False)
+        ms_ev, kms = timed(a.kernel_events == "on")
+        nan = float("nan")
+        gu_ms, dn_ms, ex_ms = kms if a.kernel_events == "on" else (nan, nan, nan)
         touched = [len(np.unique(ids[l].cpu().numpy())) for l in range(len(layers))]
         # steps cycle through the layers evenly
         e_avg = float(np.mean([touched[i % len(layers)] for i in range(a.steps)]))

@@ -305,6 +305,7 @@ size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
   size_t o_st = P.add(nk * 4), o_sw = P.add(nk * 4), o_sr = P.add(nk * 4), o_so = P.add(nk * 4);
   size_t o_hq = P.add(nk * L.f), o_hsc = P.add(nk * (L.f / 32) * 4), o_h16 = P.add(nk * (L.f / 16) * 4);
   size_t o_hf = P.add(nk * L.f * 4), o_y = P.add(kMaxKsg * nk * L.d * 4);
+  size_t o_work = P.add((size_t)L.ne * sizeof(ExpertWork));
   if (cv && base) {
     FwdBufs& B = cv->B;
     memset(&B, 0, sizeof B);
@@ -328,6 +329,7 @@ size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
     B.h16 = (int32_t*)(base + o_h16);
     B.hf = (float*)(base + o_hf);
     B.y = (float*)(base + o_y);
+    B.work = (ExpertWork*)(base + o_work);
   }
   return P.total;
 }
@@ -777,11 +779,11 @@ gmoe_status gmoe_matmul(gmoe_ctx* c, uint32_t qt, uint32_t math, const void* w, 
   unit_of(qt, &un);
   size_t wbytes = tiled_bytes(un, rows, cols);
   size_t nb_x = (size_t)n * cols;
-  // device layout: [w tiled][w raw][x f32][xq][xs][x16][y][out][offsets(2)][active(2)][eptr(3)]
+  // device layout: [w tiled][w raw][x f32][xq][xs][x16][y][out][offsets(2)][active(2)][eptr(3)][work(1)]
   ScratchPlan P;
   size_t o_w = P.add(wbytes), o_raw = P.add(nbytes), o_x = P.add(nb_x * 4), o_q = P.add(nb_x), o_s = P.add(nb_x / 32 * 4),
          o_16 = P.add(nb_x / 16 * 4), o_y = P.add(kMaxKsg * (size_t)n * rows * 4), o_o = P.add((size_t)n * rows * 4), o_off = P.add(8), o_act = P.add(8),
-         o_ep = P.add(3 * sizeof(void*));
+         o_ep = P.add(3 * sizeof(void*)), o_wk = P.add(sizeof(ExpertWork));
   uint8_t* base = nullptr;
   HIP_TRY(hipMalloc(&base, P.total));
   uint32_t offs[2] = {0, n}, act[2] = {1, 0};
@@ -792,6 +794,8 @@ gmoe_status gmoe_matmul(gmoe_ctx* c, uint32_t qt, uint32_t math, const void* w, 
   if (e == hipSuccess) e = hipMemcpy(base + o_off, offs, 8, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(base + o_act, act, 8, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(base + o_ep, ep, sizeof ep, hipMemcpyHostToDevice);
+  ExpertWork wk{{base + o_w, base + o_w, base + o_w}, 0, 0, n, 0};
+  if (e == hipSuccess) e = hipMemcpy(base + o_wk, &wk, sizeof wk, hipMemcpyHostToDevice);
   LayerDev D{};
   D.d = rows; D.f = cols; D.ne = 1; D.k = 1; D.math = math;
   D.qt_gate = D.qt_up = D.qt_down = qt;
@@ -800,6 +804,7 @@ gmoe_status gmoe_matmul(gmoe_ctx* c, uint32_t qt, uint32_t math, const void* w, 
   B.offsets = (uint32_t*)(base + o_off);
   B.active = (uint32_t*)(base + o_act);
   B.y = (float*)(base + o_y);
+  B.work = (ExpertWork*)(base + o_wk);
   if (uses_int8(math, qt)) {
     B.hq = (int8_t*)(base + o_q);
     B.hsc = (float*)(base + o_s);

@@ -106,6 +106,17 @@ __host__ __device__ inline int64_t unit_src_byte(uint32_t t, const Unit& u, uint
   return (int64_t)((b0 + g) * u.B + b % u.B);
 }
 
+// One active expert of a call as the expert kernels read it, in a single load: the
+// dispatch writes entry a for the a-th active expert (ascending id) and m = 0 for the
+// entries after the last one.
+struct ExpertWork {
+  const uint8_t* w[3];  // tiled gate, up, down matrices
+  uint32_t e;           // expert id
+  uint32_t s0;          // first slot of its tokens
+  uint32_t m;           // number of its tokens
+  uint32_t pad;
+};
+
 // Per-call device buffers. Token-indexed arrays have n rows; slot-indexed ones n*k.
 struct FwdBufs {
   const float* hs;       // [n][d]
@@ -123,6 +134,7 @@ struct FwdBufs {
   float* slot_w;         // [n*k]
   uint32_t* slot_rank;   // [n*k]
   uint32_t* slot_of;     // [n*k]: (t, rank) -> slot
+  ExpertWork* work;      // [ne] active experts for the expert kernels (may be null outside a layer call)
   int8_t* hq;            // [n*k][f]
   float* hsc;            // [n*k][f/32]
   int32_t* h16;          // [n*k][f/16]

@@ -287,11 +287,22 @@ __device__ void dispatch_block(const LayerDev& L, const FwdBufs& B, uint32_t n, 
       uint32_t c = cnt[e];
       cnt[e] = off;
       B.offsets[e] = off;
-      if (c) B.active[1 + na++] = e;
+      if (c) {
+        if (B.work) {
+          ExpertWork& W = B.work[na];
+          for (int p = 0; p < 3; p++) W.w[p] = L.eptr[p * ne + e];
+          W.e = e;
+          W.s0 = off;
+          W.m = c;
+        }
+        B.active[1 + na++] = e;
+      }
       off += c;
     }
     B.offsets[ne] = off;
     B.active[0] = na;
+    if (B.work)
+      for (uint32_t a = na; a < ne; a++) B.work[a].m = 0;
   }
   __syncthreads();
   for (uint32_t e = threadIdx.x; e < ne; e += blockDim.x) {
@@ -388,7 +399,8 @@ __device__ void gate_wave(uint32_t gating, uint32_t ne, uint32_t k, float x, uin
 // reads pair p. Pairs go 64 at a time; per expert a ballot finds its pairs in the chunk
 // and lane e keeps expert e's count, then its next free slot.
 template <class Pair>
-__device__ void dispatch_wave(const FwdBufs& B, uint32_t ne, uint32_t k, uint32_t nk, uint32_t lane, Pair pair) {
+__device__ void dispatch_wave(const FwdBufs& B, const uint8_t* const* eptr, uint32_t ne, uint32_t k, uint32_t nk,
+                              uint32_t lane, Pair pair) {
   const uint64_t below = (1ull << lane) - 1ull;
   uint32_t cnt = 0;
   for (uint32_t c0 = 0; c0 < nk; c0 += 64) {
@@ -406,13 +418,25 @@ __device__ void dispatch_wave(const FwdBufs& B, uint32_t ne, uint32_t k, uint32_
     run += lane_u(cnt, e);
   }
   const uint64_t act = __ballot(lane < ne && cnt > 0);
+  const uint32_t na = (uint32_t)__popcll(act);
   if (lane < ne) {
     B.offsets[lane] = off;
-    if (cnt > 0) B.active[1 + __popcll(act & below)] = lane;
+    if (cnt > 0) {
+      const uint32_t a = (uint32_t)__popcll(act & below);
+      B.active[1 + a] = lane;
+      if (B.work) {
+        ExpertWork& W = B.work[a];
+        for (int p = 0; p < 3; p++) W.w[p] = eptr[p * ne + lane];
+        W.e = lane;
+        W.s0 = off;
+        W.m = cnt;
+      }
+    }
+    if (B.work && lane >= na) B.work[lane].m = 0;
   }
   if (lane == 0) {
     B.offsets[ne] = run;
-    B.active[0] = (uint32_t)__popcll(act);
+    B.active[0] = na;
   }
   for (uint32_t c0 = 0; c0 < nk; c0 += 64) {
     uint32_t id = ~0u, pos = 0;
@@ -568,7 +592,7 @@ __global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, 
     B.w[(size_t)t * k + lane] = w;
   }
   if (n == 1) {  // the only workgroup: pair p (< k) is rank p, which lane p holds
-    dispatch_wave(B, ne, k, k, lane, [&](uint32_t, uint32_t* pid, float* pw) {
+    dispatch_wave(B, L.eptr, ne, k, k, lane, [&](uint32_t, uint32_t* pid, float* pw) {
       *pid = id;
       *pw = w;
     });
@@ -580,7 +604,7 @@ __global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, 
   if (lane == 0) prev = atomicAdd(B.done, 1u);
   if (lane_u(prev, 0) == n - 1) {
     __threadfence();
-    dispatch_wave(B, ne, k, n * k, lane, [&](uint32_t p, uint32_t* pid, float* pw) {
+    dispatch_wave(B, L.eptr, ne, k, n * k, lane, [&](uint32_t p, uint32_t* pid, float* pw) {
       *pid = B.ids[p];
       *pw = B.w[p];
     });
