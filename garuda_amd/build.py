@@ -18,8 +18,9 @@ ARCH = os.environ.get("GMOE_ARCH", "gfx950")
 
 SOURCES = ["gmoe_kernels.hip", "gmoe_api.cpp", "gmoe_quant.cpp"]
 # gmoe_units.hip is built once per block type (ggml type ids), each object holding one
-# type's expert kernels.
+# type's expert kernels; gmoe_prefill.hip likewise for the types with MFMA prefill.
 UNIT_TYPES = {"f32": 0, "f16": 1, "q4_0": 2, "q8_0": 8, "q2_k": 10, "q3_k": 11, "q4_k": 12, "q5_k": 13, "q6_k": 14}
+PREFILL_TYPES = {k: v for k, v in UNIT_TYPES.items() if k != "f32"}
 
 COMMON = [
     "-O3", "-fPIC", "-std=c++20", "-ffp-contract=off", "-fno-fast-math",
@@ -46,6 +47,9 @@ def _jobs(hipcc: str, objdir: Path) -> list[tuple[list[str], Path]]:
     for name, qt in UNIT_TYPES.items():
         obj = objdir / f"gmoe_units_{name}.o"
         jobs.append(([hipcc, *DEVICE, *COMMON, f"-DGMOE_QT={qt}", "-c", str(CSRC / "gmoe_units.hip"), "-o", str(obj)], obj))
+    for name, qt in PREFILL_TYPES.items():
+        obj = objdir / f"gmoe_prefill_{name}.o"
+        jobs.append(([hipcc, *DEVICE, *COMMON, f"-DGMOE_QT={qt}", "-c", str(CSRC / "gmoe_prefill.hip"), "-o", str(obj)], obj))
     return jobs
 
 

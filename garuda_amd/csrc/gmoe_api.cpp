@@ -306,6 +306,9 @@ size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
   size_t o_hq = P.add(nk * L.f), o_hsc = P.add(nk * (L.f / 32) * 4), o_h16 = P.add(nk * (L.f / 16) * 4);
   size_t o_hf = P.add(nk * L.f * 4), o_y = P.add(kMaxKsg * nk * L.d * 4);
   size_t o_work = P.add((size_t)L.ne * sizeof(ExpertWork));
+  const uint32_t pcap = prefill_tiles_cap(n, L.k, L.ne);
+  size_t o_pt = P.add((size_t)pcap * 4), o_xh = P.add(2 * nk * L.d * 2), o_hh = P.add(2 * nk * L.f * 2);
+  size_t o_xsh = P.add(2 * nk * (L.d / 16) * 2), o_hsh = P.add(2 * nk * (L.f / 16) * 2);
   if (cv && base) {
     FwdBufs& B = cv->B;
     memset(&B, 0, sizeof B);
@@ -330,6 +333,12 @@ size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
     B.hf = (float*)(base + o_hf);
     B.y = (float*)(base + o_y);
     B.work = (ExpertWork*)(base + o_work);
+    B.ptile = (uint32_t*)(base + o_pt);
+    B.ptile_cap = pcap;
+    B.xh = (_Float16*)(base + o_xh);
+    B.hh = (_Float16*)(base + o_hh);
+    B.xsh = (_Float16*)(base + o_xsh);
+    B.hsh = (_Float16*)(base + o_hsh);
   }
   return P.total;
 }
@@ -384,6 +393,12 @@ gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStr
     B.hf = nullptr;
   }
   const bool quant = uses_int8(L.math, L.p[0].qtype);
+  // prefill-sized f32-math calls run the expert products on MFMA over token tiles
+  const bool pf = prefill_ok(D, n);
+  if (!pf) {
+    B.ptile = nullptr;
+    B.xh = B.xsh = B.hh = B.hsh = nullptr;
+  }
   if (front_small_ok(D, n)) {
     HIP_TRY(launch_front_small(D, B, n, quant ? 1 : 0, st));
   } else {
@@ -391,19 +406,20 @@ gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStr
     HIP_TRY(launch_dispatch(D, B, n, st));
     if (quant) HIP_TRY(launch_quant_act(B.hs, n, L.d, B.xq, B.xs, B.x16, st));
   }
+  if (pf) HIP_TRY(launch_gather_f16(D, B, n, st));
   Timing tm{};
   if (c->timing) {
     tm = take_timing(c);
     HIP_TRY(hipEventRecord(tm.a, st));
   }
-  HIP_TRY(launch_gateup(D, B, n, st));
+  HIP_TRY(pf ? launch_prefill_gateup(D, B, n, st) : launch_gateup(D, B, n, st));
   if (c->timing) HIP_TRY(hipEventRecord(tm.b, st));
-  HIP_TRY(launch_down(D, B, n, st));
+  HIP_TRY(pf ? launch_prefill_down(D, B, n, st) : launch_down(D, B, n, st));
   if (c->timing) {
     HIP_TRY(hipEventRecord(tm.c, st));
     c->pending.push_back(tm);
   }
-  HIP_TRY(launch_combine(D, B, n, st));
+  HIP_TRY(launch_combine(D, B, n, pf ? 1 : down_ksg(D, n), st));
   return GMOE_OK;
 }
 

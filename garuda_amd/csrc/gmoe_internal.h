@@ -135,6 +135,14 @@ struct FwdBufs {
   uint32_t* slot_rank;   // [n*k]
   uint32_t* slot_of;     // [n*k]: (t, rank) -> slot
   ExpertWork* work;      // [ne] active experts for the expert kernels (may be null outside a layer call)
+  // prefill (f32 math, MFMA): token tiles; activations and h in slot order as fp16
+  // pairs (v = hi + lo, hi plane then lo plane) and their sums over 16 or 32 values
+  uint32_t* ptile;       // [ptile_cap] (active slot << 16) | tile of kPfTok tokens; ~0u past the last tile
+  uint32_t ptile_cap;
+  _Float16* xh;          // [2][n*k][d]
+  _Float16* xsh;         // [2][n*k][d/16]
+  _Float16* hh;          // [2][n*k][f]
+  _Float16* hsh;         // [2][n*k][f/16]
   int8_t* hq;            // [n*k][f]
   float* hsc;            // [n*k][f/32]
   int32_t* h16;          // [n*k][f/16]
@@ -159,6 +167,20 @@ constexpr int kDnKS = 2;
 template <int QT> hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 template <int QT> hipError_t units_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
 
+// Prefill products (f32 math) on MFMA over token tiles of kPfTok (gmoe_prefill.hip,
+// built once per type; F32 weights are not supported). prefill_ok says when the path
+// applies. Sums of activations are kept per 32 values for Q4_K/Q5_K and per 16 for Q2_K
+// (the widths of their min terms), none otherwise.
+constexpr uint32_t kPfTok = 64;
+constexpr uint32_t kPfMinSlots = 64;
+__host__ __device__ constexpr uint32_t pf_sum_width(uint32_t qt) {
+  return (qt == Q4_K || qt == Q5_K) ? 32u : qt == Q2_K ? 16u : 0u;
+}
+template <int QT> hipError_t prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+template <int QT> hipError_t prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+// Token tiles a call of n tokens can need at most.
+inline uint32_t prefill_tiles_cap(uint32_t n, uint32_t k, uint32_t ne) { return (n * k) / kPfTok + ne + 1; }
+
 // Launchers (gmoe_kernels.hip). All are asynchronous on `st` and validate nothing:
 // the host runtime checks shapes before calling them.
 hipError_t launch_dequant(uint32_t qtype, const uint8_t* blocks, size_t nblocks, float* out,
@@ -174,7 +196,13 @@ bool front_small_ok(const LayerDev& L, uint32_t n);
 hipError_t launch_front_small(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st);
 hipError_t launch_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 hipError_t launch_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
-hipError_t launch_combine(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+hipError_t launch_combine(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
+// Prefill path: whether it applies (f32 math, at least kPfMinSlots slots, supported
+// types and shapes), the per-slot fp16 gather of the activations, and the products.
+bool prefill_ok(const LayerDev& L, uint32_t n);
+hipError_t launch_gather_f16(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+hipError_t launch_prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+hipError_t launch_prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 // Number of partial slices launch_down writes for this layer and batch (1 = y is final).
 uint32_t down_ksg(const LayerDev& L, uint32_t n);
 // out[i] = parts[i] + parts[count + i] + ... over ksg slices, in slice order.

@@ -303,6 +303,14 @@ __device__ void dispatch_block(const LayerDev& L, const FwdBufs& B, uint32_t n, 
     B.active[0] = na;
     if (B.work)
       for (uint32_t a = na; a < ne; a++) B.work[a].m = 0;
+    if (B.ptile) {  // token tiles of kPfTok per active expert, in slot order
+      uint32_t nt = 0;
+      for (uint32_t a = 0; a < na; a++) {
+        const uint32_t e = B.active[1 + a], m = B.offsets[e + 1] - B.offsets[e];
+        for (uint32_t t = 0; t * kPfTok < m; t++) B.ptile[nt++] = (a << 16) | t;
+      }
+      for (; nt < B.ptile_cap; nt++) B.ptile[nt] = ~0u;
+    }
   }
   __syncthreads();
   for (uint32_t e = threadIdx.x; e < ne; e += blockDim.x) {
@@ -437,6 +445,19 @@ __device__ void dispatch_wave(const FwdBufs& B, const uint8_t* const* eptr, uint
   if (lane == 0) {
     B.offsets[ne] = run;
     B.active[0] = na;
+  }
+  if (B.ptile) {  // token tiles of kPfTok per active expert, in slot order
+    const uint32_t nt = (cnt + kPfTok - 1) / kPfTok;
+    uint32_t t0 = 0, tr = 0;
+    for (uint32_t e = 0; e < ne; e++) {
+      if (lane == e) t0 = tr;
+      tr += lane_u(nt, e);
+    }
+    if (lane < ne && cnt > 0) {
+      const uint32_t a = (uint32_t)__popcll(act & below);
+      for (uint32_t t = 0; t < nt; t++) B.ptile[t0 + t] = (a << 16) | t;
+    }
+    for (uint32_t i = tr + lane; i < B.ptile_cap; i += 64) B.ptile[i] = ~0u;
   }
   for (uint32_t c0 = 0; c0 < nk; c0 += 64) {
     uint32_t id = ~0u, pos = 0;
@@ -720,8 +741,8 @@ __global__ void __launch_bounds__(256) k_combine(LayerDev L, FwdBufs B, uint32_t
   B.out[(size_t)t * d + c] = acc;
 }
 
-hipError_t launch_combine(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
-  hipLaunchKernelGGL(k_combine, dim3((L.d + 255) / 256, n), dim3(256), 0, st, L, B, n, down_ksg(L, n));
+hipError_t launch_combine(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st) {
+  hipLaunchKernelGGL(k_combine, dim3((L.d + 255) / 256, n), dim3(256), 0, st, L, B, n, ksg);
   return hipGetLastError();
 }
 
@@ -758,6 +779,85 @@ hipError_t launch_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStr
 #define GU(T) case T: return units_gateup<T>(L, B, n, st);
     GU(Q4_K) GU(Q5_K) GU(Q6_K) GU(Q3_K) GU(Q2_K) GU(Q8_0) GU(Q4_0) GU(F16) GU(F32)
 #undef GU
+  }
+  return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------------
+// Prefill (f32 math on MFMA, gmoe_prefill.hip)
+// ---------------------------------------------------------------------------------
+
+static bool prefill_type(uint32_t qt) {
+  return qt == Q4_K || qt == Q5_K || qt == Q6_K || qt == Q3_K || qt == Q2_K || qt == Q8_0 || qt == Q4_0 ||
+         qt == F16;
+}
+
+bool prefill_ok(const LayerDev& L, uint32_t n) {
+  const uint32_t nk = n * L.k;
+  return L.math == 1 && nk >= kPfMinSlots && nk >= 4 * L.ne && L.qt_gate == L.qt_up && prefill_type(L.qt_gate) &&
+         prefill_type(L.qt_down) && L.d % 256 == 0 && L.f % 256 == 0 && L.ne < 65536;
+}
+
+// The activations in slot order as fp16 pairs, x = hi + lo (hi = fp16(x), lo =
+// fp16(x - hi)), hi plane then lo plane, and with sw > 0 the sums of each sw values
+// (f32, left to right) as pairs the same way. One thread per 32 values.
+__global__ void __launch_bounds__(256) k_gather_f16(const float* __restrict__ hs, const uint32_t* __restrict__ slot_tok,
+                                                    uint32_t d, uint32_t nk, uint32_t sw, _Float16* __restrict__ xh,
+                                                    _Float16* __restrict__ xsh) {
+  typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+  const uint32_t s = blockIdx.y, c = 32 * (blockIdx.x * blockDim.x + threadIdx.x);
+  if (c >= d) return;
+  const float4* src = reinterpret_cast<const float4*>(hs + (size_t)slot_tok[s] * d + c);
+  const size_t o = (size_t)s * d + c, plane = (size_t)nk * d;
+  float sum[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float4 a = src[2 * i], b = src[2 * i + 1];
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    half8 hi, lo;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      hi[j] = (_Float16)v[j];
+      lo[j] = (_Float16)(v[j] - (float)hi[j]);
+      sum[i / 2] += v[j];
+    }
+    *reinterpret_cast<half8*>(xh + o + 8 * i) = hi;
+    *reinterpret_cast<half8*>(xh + plane + o + 8 * i) = lo;
+  }
+  if (sw) {
+    const uint32_t ns = d / sw, per = 32 / sw;
+    const size_t so = (size_t)s * ns + c / sw, splane = (size_t)nk * ns;
+    const float tot[2] = {sum[0] + sum[1], 0.0f};
+    for (uint32_t i = 0; i < per; i++) {
+      const float v = per == 1 ? tot[0] : sum[i];
+      const _Float16 hi = (_Float16)v;
+      xsh[so + i] = hi;
+      xsh[splane + so + i] = (_Float16)(v - (float)hi);
+    }
+  }
+}
+
+hipError_t launch_gather_f16(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  const uint32_t nk = n * L.k;
+  hipLaunchKernelGGL(k_gather_f16, dim3((L.d / 32 + 255) / 256, nk), dim3(256), 0, st, B.hs, B.slot_tok, L.d, nk,
+                     pf_sum_width(L.qt_gate), B.xh, B.xsh);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  switch (L.qt_gate) {
+#define GU(T) case T: return prefill_gateup<T>(L, B, n, st);
+    GU(Q4_K) GU(Q5_K) GU(Q6_K) GU(Q3_K) GU(Q2_K) GU(Q8_0) GU(Q4_0) GU(F16)
+#undef GU
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  switch (L.qt_down) {
+#define DN(T) case T: return prefill_down<T>(L, B, n, st);
+    DN(Q4_K) DN(Q5_K) DN(Q6_K) DN(Q3_K) DN(Q2_K) DN(Q8_0) DN(Q4_0) DN(F16)
+#undef DN
   }
   return hipErrorInvalidValue;
 }

@@ -1,0 +1,615 @@
+// gmoe_prefill.hip — prefill-sized expert products on MFMA, f32 math.
+//
+// Compiled once per block type, with -DGMOE_QT=<ggml type id>, like gmoe_units.hip.
+//
+// Reference semantics: llama/mod.rs:1002-1020 under Weight::Full (mmap = false): the
+// weights are the dequantised f32 values (quant/mod.rs:624-875) and every product is an
+// f32 dot (simd/mod.rs:96-129); layer outputs must stay within rtol 1e-3 / atol 1e-4 of
+// it. A single fp16 (or bf16) MFMA pass rounds both operands and misses that bar, so
+// the products are made exact instead:
+//
+//  * weights: a dequantised value is w = d * (sc * q) - dmin * m (K-quants) or d * q
+//    (Q8_0/Q4_0, Q6_K with d*sc as d), with q a small integer. The integer part (sc * q,
+//    or q) is exact in fp16 (|.| <= 1953 < 2048) and is the MFMA operand; the block
+//    scale d (f32) multiplies the block's partial sums afterwards.
+//  * activations: x = hi + lo, both fp16 (22 significant bits); two MFMAs per step.
+//  * mins (Q4_K/Q5_K/Q2_K): the sum over sub-blocks of (dmin * m) * S, S the
+//    sub-block's sum of x, is a GEMM of length K/32 (or K/16) run on MFMA with both
+//    operands split (three passes).
+//
+// Every product is then an exact fp16 x fp16 product accumulated in f32, and the layer
+// differs from the f32 reference by reordered f32 sums (~1e-6 relative).
+//
+// Work layout. The dispatch lists the call's token tiles (kPfTok = 64 tokens of one
+// expert, in slot order) in B.ptile; blockIdx.y is a token tile. Gate/up workgroups
+// take 128 rows of f (both matrices), down workgroups 256 rows of d. Each of the 4
+// waves owns two 32-row MFMA row tiles (gate and up of its 32 rows, or two 32-row
+// halves of its 64 down rows) and both 32-token tiles: 4 accumulators of 32x32, plus 4
+// of partial block sums. Per chunk of K (128 values, 64 for F16) the workgroup copies the
+// chunk's raw 16-byte pieces of its rows (the slab's tiled layout makes each piece of 64
+// rows one 1 KiB run) and the tokens' hi/lo activations into LDS; a lane then decodes
+// its row's 8 values of each 16-value K step straight into the MFMA B operand.
+//
+// v_mfma_f32_32x32x16_f16 (operand layout checked on the device): lane l supplies row
+// l%32 of A and column l%32 of B, each with k = 8*(l/32) .. +7, and holds D[i][l%32] for
+// i = 8*(r/4) + 4*(l/32) + r%4, r = 0..15. A is the tokens, B the weight rows, so a
+// lane's 16 results share one weight row and one block scale.
+#include <utility>
+
+#include "gmoe_unit.h"
+
+#ifndef GMOE_QT
+#error "gmoe_prefill.hip is compiled once per block type with -DGMOE_QT=<type id>"
+#endif
+
+namespace gmoe {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kPfWaves = 4, kPfThreads = 64 * kPfWaves;
+
+// f(integral_constant<int, I>) for I = 0 .. N-1, each call with I a constant.
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+  }(std::make_integer_sequence<int, N>{});
+}
+
+// ---------------------------------------------------------------------------------
+// Per-type shape: EU values per slab unit, KC values per LDS chunk, NPC 16-byte pieces
+// of a unit that chunk c needs (piece(c, i) is the i-th), SU16 K16 steps per scale
+// (0: the decoded values are the weights), SW the width of a min-term sub-block.
+// Unit byte layouts are those of the packed blocks (quant/mod.rs:624-875); Q8_0/Q4_0
+// units are eight blocks repacked as 8 f16 scales then the quants.
+// ---------------------------------------------------------------------------------
+template <int QT> struct PF;
+template <> struct PF<Q4_K> {  // d dmin | scales[12] | qs[128]: sub-blocks 4c..4c+3 in pieces 1+4c..
+  static constexpr int EU = 256, KC = 128, NPC = 5, SU16 = 16, SW = 32;
+  static constexpr int piece(int c, int i) { return i == 0 ? 0 : 4 * c + i; }
+};
+template <> struct PF<Q5_K> {  // d dmin scales | qh[32] | qs[128]
+  static constexpr int EU = 256, KC = 128, NPC = 7, SU16 = 16, SW = 32;
+  static constexpr int piece(int c, int i) { return i < 3 ? i : 4 * c + i; }
+};
+template <> struct PF<Q6_K> {  // ql[128] | qh[64] | scales[16] | d
+  static constexpr int EU = 256, KC = 128, NPC = 8, SU16 = 1, SW = 0;
+  static constexpr int piece(int c, int i) { return i < 4 ? 4 * c + i : i < 6 ? 8 + 2 * c + (i - 4) : 12 + (i - 6); }
+};
+template <> struct PF<Q3_K> {  // hmask[32] | qs[64] | scales[12] d
+  static constexpr int EU = 256, KC = 128, NPC = 5, SU16 = 16, SW = 0;
+  static constexpr int piece(int c, int i) { return i < 2 ? i : i < 4 ? 2 + 2 * c + (i - 2) : 6; }
+};
+template <> struct PF<Q2_K> {  // scales[16] | qs[64] | d dmin
+  static constexpr int EU = 256, KC = 128, NPC = 4, SU16 = 16, SW = 16;
+  static constexpr int piece(int c, int i) { return i == 0 ? 0 : i < 3 ? 1 + 2 * c + (i - 1) : 5; }
+};
+template <> struct PF<Q8_0> {  // 8 scales | 8 x 32 quants
+  static constexpr int EU = 256, KC = 128, NPC = 9, SU16 = 2, SW = 0;
+  static constexpr int piece(int c, int i) { return i == 0 ? 0 : 8 * c + i; }
+};
+template <> struct PF<Q4_0> {  // 8 scales | 8 x 16 quant bytes
+  static constexpr int EU = 256, KC = 128, NPC = 5, SU16 = 2, SW = 0;
+  static constexpr int piece(int c, int i) { return i == 0 ? 0 : 4 * c + i; }
+};
+template <> struct PF<F16> {  // 64 halves
+  static constexpr int EU = 64, KC = 64, NPC = 8, SU16 = 0, SW = 0;
+  static constexpr int piece(int, int i) { return i; }
+};
+
+template <int QT>
+constexpr int pf_slot(int c, int p) {
+  for (int i = 0; i < PF<QT>::NPC; i++)
+    if (PF<QT>::piece(c, i) == p) return i;
+  return -1;
+}
+
+// Byte OFF of the lane's unit, chunk C staged: row points at the row's piece in slot 0.
+template <int QT, int C, int OFF>
+__device__ __forceinline__ const uint8_t* pf_at(const uint8_t* row) {
+  constexpr int sl = pf_slot<QT>(C, OFF / 16);
+  static_assert(sl >= 0, "piece not staged for this chunk");
+  return row + sl * 1024 + OFF % 16;
+}
+__device__ __forceinline__ u32x2 ld8(const uint8_t* p) { return *reinterpret_cast<const u32x2*>(p); }
+__device__ __forceinline__ u32x4 ld16(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// 16 bytes at src -> LDS at dst + 16 * lane (dst the same for the whole wave).
+__device__ __forceinline__ void lds_load16(const void* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+}
+
+__device__ __forceinline__ half2_t h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
+__device__ __forceinline__ half2_t h2s(_Float16 v) { return half2_t{v, v}; }
+
+// Four bytes b0..b3 (each < 1024) as fp16 pairs (1024 + b0, 1024 + b1), (1024 + b2,
+// 1024 + b3): byte-permute each beside the exponent byte 0x64.
+__device__ __forceinline__ void magic4(uint32_t b, half2_t& p0, half2_t& p1) {
+  p0 = h2(__builtin_amdgcn_perm(b, 0x64646464u, 0x00050004u));
+  p1 = h2(__builtin_amdgcn_perm(b, 0x64646464u, 0x00070006u));
+}
+
+// 8 bytes (two dwords) -> 8 fp16 values f(1024 + byte) with f(t) = fma(t, mul, add);
+// exact when the result is an integer of magnitude <= 2048.
+__device__ __forceinline__ half8 bytes_fma(u32x2 b, half2_t mul, half2_t add) {
+  half8 o;
+#pragma unroll
+  for (int d = 0; d < 2; d++) {
+    half2_t p0, p1;
+    magic4(b[d], p0, p1);
+    p0 = __builtin_elementwise_fma(p0, mul, add);
+    p1 = __builtin_elementwise_fma(p1, mul, add);
+    o[4 * d] = p0.x; o[4 * d + 1] = p0.y; o[4 * d + 2] = p1.x; o[4 * d + 3] = p1.y;
+  }
+  return o;
+}
+
+__device__ __forceinline__ _Float16 fh(uint32_t v) { return (_Float16)(float)v; }
+// The low half of v as f32 (a scale or min; non-finite ones give non-finite outputs).
+__device__ __forceinline__ float f16v(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)v); }
+
+// ---------------------------------------------------------------------------------
+// Decoders: frag<C, S>(row, h) = the integer parts of values 16S + 8h .. +7 of the unit
+// (K16 step S, staged in chunk C), as exact fp16; scale<C, S>(row) = the f32 factor of
+// the scale group that step S closes; mins<C>(row, h, hi, lo) = -(dmin * m) of the
+// lane's 8 min-term sub-blocks as an fp16 pair.
+// ---------------------------------------------------------------------------------
+template <int QT> struct Dec;
+
+template <> struct Dec<Q4_K> {
+  static constexpr int QT = Q4_K;
+  template <int C, int S>
+  static __device__ __forceinline__ half8 frag(const uint8_t* row, uint32_t h) {
+    constexpr int sb = S / 2;
+    constexpr bool high = sb & 1;
+    const u32x4 hd = ld16(pf_at<QT, C, 0>(row));
+    const uint32_t s3[3] = {hd.y, hd.z, hd.w};
+    uint32_t sc, m;
+    scale_min_k4(s3, sb, sc, m);
+    u32x2 q = ld8(pf_at<QT, C, 16 + 32 * (sb / 2) + 16 * (S % 2)>(row) + 8 * h);
+    const uint32_t mask = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+    q.x &= mask;
+    q.y &= mask;
+    // high nibbles stay in place (16q): scale by sc/16
+    const _Float16 f = high ? fh(sc) * (_Float16)0.0625f : fh(sc);
+    return bytes_fma(q, h2s(f), h2s(f * (_Float16)-1024.0f));
+  }
+  template <int C, int S>
+  static __device__ __forceinline__ float scale(const uint8_t* row) {
+    return f16v(ld16(pf_at<QT, C, 0>(row)).x);
+  }
+  template <int C>
+  static __device__ __forceinline__ void mins(const uint8_t* row, uint32_t h, half8& hi, half8& lo) {
+    const u32x4 hd = ld16(pf_at<QT, C, 0>(row));
+    const uint32_t s3[3] = {hd.y, hd.z, hd.w};
+    const float dmin = f16v(hd.x >> 16);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      uint32_t sc, m;
+      scale_min_k4(s3, j, sc, m);
+      const float b = h ? 0.0f : -(dmin * (float)m);
+      hi[j] = (_Float16)b;
+      lo[j] = (_Float16)(b - (float)hi[j]);
+    }
+  }
+};
+
+template <> struct Dec<Q5_K> {
+  static constexpr int QT = Q5_K;
+  template <int C, int S>
+  static __device__ __forceinline__ half8 frag(const uint8_t* row, uint32_t h) {
+    constexpr int sb = S / 2;
+    const u32x4 hd = ld16(pf_at<QT, C, 0>(row));
+    const uint32_t s3[3] = {hd.y, hd.z, hd.w};
+    uint32_t sc, m;
+    scale_min_k4(s3, sb, sc, m);
+    const u32x2 qh = ld8(pf_at<QT, C, 16 + 16 * (S % 2)>(row) + 8 * h);
+    const u32x2 ql = ld8(pf_at<QT, C, 48 + 32 * (sb / 2) + 16 * (S % 2)>(row) + 8 * h);
+    u32x2 b;
+#pragma unroll
+    for (int d = 0; d < 2; d++)
+      b[d] = ((sb & 1 ? ql[d] >> 4 : ql[d]) & 0x0f0f0f0fu) | (((qh[d] >> sb) & 0x01010101u) << 4);
+    const _Float16 f = fh(sc);
+    return bytes_fma(b, h2s(f), h2s(f * (_Float16)-1024.0f));
+  }
+  template <int C, int S>
+  static __device__ __forceinline__ float scale(const uint8_t* row) {
+    return f16v(ld16(pf_at<QT, C, 0>(row)).x);
+  }
+  template <int C>
+  static __device__ __forceinline__ void mins(const uint8_t* row, uint32_t h, half8& hi, half8& lo) {
+    const u32x4 hd = ld16(pf_at<QT, C, 0>(row));  // same header layout as Q4_K
+    const uint32_t s3[3] = {hd.y, hd.z, hd.w};
+    const float dmin = f16v(hd.x >> 16);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      uint32_t sc, m;
+      scale_min_k4(s3, j, sc, m);
+      const float b = h ? 0.0f : -(dmin * (float)m);
+      hi[j] = (_Float16)b;
+      lo[j] = (_Float16)(b - (float)hi[j]);
+    }
+  }
+};
+
+template <> struct Dec<Q6_K> {
+  static constexpr int QT = Q6_K;
+  template <int C, int S>
+  static __device__ __forceinline__ half8 frag(const uint8_t* row, uint32_t h) {
+    constexpr int n = S / 8, j4 = (S % 8) / 2;
+    const u32x2 ql = ld8(pf_at<QT, C, 64 * n + 32 * (j4 % 2) + 16 * (S % 2)>(row) + 8 * h);
+    const u32x2 qh = ld8(pf_at<QT, C, 128 + 32 * n + 16 * (S % 2)>(row) + 8 * h);
+    u32x2 b;
+#pragma unroll
+    for (int d = 0; d < 2; d++)
+      b[d] = ((j4 >= 2 ? ql[d] >> 4 : ql[d]) & 0x0f0f0f0fu) | (((qh[d] >> (2 * j4)) & 0x03030303u) << 4);
+    return bytes_fma(b, h2s((_Float16)1.0f), h2s((_Float16)-1056.0f));  // q - 32
+  }
+  template <int C, int S>
+  static __device__ __forceinline__ float scale(const uint8_t* row) {
+    constexpr int n = S / 8, j4 = (S % 8) / 2, is = 8 * n + 2 * j4 + S % 2;
+    const u32x4 sc = ld16(pf_at<QT, C, 192>(row));
+    const float d = f16v(ld16(pf_at<QT, C, 208>(row)).x);
+    const float s = (float)(int8_t)((sc[is / 4] >> (8 * (is % 4))) & 0xffu);
+    return d * s;  // (d * sc) * q, as the reference orders it
+  }
+  template <int C>
+  static __device__ __forceinline__ void mins(const uint8_t*, uint32_t, half8&, half8&) {}
+};
+
+template <> struct Dec<Q3_K> {
+  static constexpr int QT = Q3_K;
+  template <int C, int S>
+  static __device__ __forceinline__ half8 frag(const uint8_t* row, uint32_t h) {
+    constexpr int n = S / 8, j4 = (S % 8) / 2, is = 8 * n + 2 * j4 + S % 2;
+    const u32x2 hm = ld8(pf_at<QT, C, 16 * (S % 2)>(row) + 8 * h);
+    const u32x2 qs = ld8(pf_at<QT, C, 32 + 32 * n + 16 * (S % 2)>(row) + 8 * h);
+    const u32x4 tl = ld16(pf_at<QT, C, 96>(row));  // scales[12] | d
+    uint32_t sc4[4];
+    q3k_scales(tl.x, tl.y, tl.z, sc4);
+    const int scs = (int)((sc4[is / 4] >> (8 * (is % 4))) & 0xffu) - 32;
+    u32x2 b;  // q2 + 4 * hbit in [0, 7]; the value is b - 4
+#pragma unroll
+    for (int d = 0; d < 2; d++)
+      b[d] = ((qs[d] >> (2 * j4)) & 0x03030303u) | (((hm[d] >> (4 * n + j4)) & 0x01010101u) << 2);
+    half8 o;
+    const half2_t s2 = h2s((_Float16)(float)scs);
+#pragma unroll
+    for (int d = 0; d < 2; d++) {
+      half2_t p0, p1;
+      magic4(b[d], p0, p1);
+      p0 = (p0 - h2s((_Float16)1028.0f)) * s2;  // (b - 4) * (sc - 32): |.| <= 128
+      p1 = (p1 - h2s((_Float16)1028.0f)) * s2;
+      o[4 * d] = p0.x; o[4 * d + 1] = p0.y; o[4 * d + 2] = p1.x; o[4 * d + 3] = p1.y;
+    }
+    return o;
+  }
+  template <int C, int S>
+  static __device__ __forceinline__ float scale(const uint8_t* row) {
+    return f16v(ld16(pf_at<QT, C, 96>(row)).w);
+  }
+  template <int C>
+  static __device__ __forceinline__ void mins(const uint8_t*, uint32_t, half8&, half8&) {}
+};
+
+template <> struct Dec<Q2_K> {
+  static constexpr int QT = Q2_K;
+  template <int C, int S>
+  static __device__ __forceinline__ half8 frag(const uint8_t* row, uint32_t h) {
+    constexpr int n = S / 8, j4 = (S % 8) / 2, is = 8 * n + 2 * j4 + S % 2;
+    const u32x2 qs = ld8(pf_at<QT, C, 16 + 32 * n + 16 * (S % 2)>(row) + 8 * h);
+    const u32x4 scb = ld16(pf_at<QT, C, 0>(row));
+    const uint32_t sc = (scb[is / 4] >> (8 * (is % 4))) & 15u;
+    u32x2 b;
+#pragma unroll
+    for (int d = 0; d < 2; d++) b[d] = (qs[d] >> (2 * j4)) & 0x03030303u;
+    const _Float16 f = fh(sc);
+    return bytes_fma(b, h2s(f), h2s(f * (_Float16)-1024.0f));
+  }
+  template <int C, int S>
+  static __device__ __forceinline__ float scale(const uint8_t* row) {
+    return f16v(ld16(pf_at<QT, C, 80>(row)).x);
+  }
+  template <int C>
+  static __device__ __forceinline__ void mins(const uint8_t* row, uint32_t h, half8& hi, half8& lo) {
+    const u32x4 scb = ld16(pf_at<QT, C, 0>(row));
+    const float dmin = f16v(ld16(pf_at<QT, C, 80>(row)).x >> 16);
+    const uint32_t w0 = h ? scb.z : scb.x, w1 = h ? scb.w : scb.y;  // sub-blocks 8h .. 8h+7
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const uint32_t m = (((j < 4 ? w0 : w1) >> (8 * (j % 4))) & 0xffu) >> 4;
+      const float b = -(dmin * (float)m);
+      hi[j] = (_Float16)b;
+      lo[j] = (_Float16)(b - (float)hi[j]);
+    }
+  }
+};
+
+template <> struct Dec<Q8_0> {
+  static constexpr int QT = Q8_0;
+  template <int C, int S>
+  static __device__ __forceinline__ half8 frag(const uint8_t* row, uint32_t h) {
+    u32x2 q = ld8(pf_at<QT, C, 16 + 32 * (S / 2) + 16 * (S % 2)>(row) + 8 * h);
+    q.x ^= 0x80808080u;  // q + 128 as unsigned bytes
+    q.y ^= 0x80808080u;
+    return bytes_fma(q, h2s((_Float16)1.0f), h2s((_Float16)-1152.0f));
+  }
+  template <int C, int S>
+  static __device__ __forceinline__ float scale(const uint8_t* row) {
+    constexpr int b = S / 2;
+    return f16v(ld16(pf_at<QT, C, 0>(row))[b / 2] >> (16 * (b % 2)));
+  }
+  template <int C>
+  static __device__ __forceinline__ void mins(const uint8_t*, uint32_t, half8&, half8&) {}
+};
+
+template <> struct Dec<Q4_0> {
+  static constexpr int QT = Q4_0;
+  template <int C, int S>
+  static __device__ __forceinline__ half8 frag(const uint8_t* row, uint32_t h) {
+    constexpr bool high = S & 1;  // values 16..31 of the block are the high nibbles
+    u32x2 q = ld8(pf_at<QT, C, 16 + 16 * (S / 2)>(row) + 8 * h);
+    const uint32_t mask = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+    q.x &= mask;
+    q.y &= mask;
+    // low: (1024 + q) - 1032; high: (1024 + 16q) / 16 - 72
+    return high ? bytes_fma(q, h2s((_Float16)0.0625f), h2s((_Float16)-72.0f))
+                : bytes_fma(q, h2s((_Float16)1.0f), h2s((_Float16)-1032.0f));
+  }
+  template <int C, int S>
+  static __device__ __forceinline__ float scale(const uint8_t* row) {
+    constexpr int b = S / 2;
+    return f16v(ld16(pf_at<QT, C, 0>(row))[b / 2] >> (16 * (b % 2)));
+  }
+  template <int C>
+  static __device__ __forceinline__ void mins(const uint8_t*, uint32_t, half8&, half8&) {}
+};
+
+template <> struct Dec<F16> {
+  template <int C, int S>
+  static __device__ __forceinline__ half8 frag(const uint8_t* row, uint32_t h) {
+    // values 16S + 8h .. are bytes 32S + 16h ..: piece (and slot) 2S + h
+    return __builtin_bit_cast(half8, ld16(row + (2 * S + h) * 1024));
+  }
+  template <int C, int S>
+  static __device__ __forceinline__ float scale(const uint8_t*) { return 1.0f; }
+  template <int C>
+  static __device__ __forceinline__ void mins(const uint8_t*, uint32_t, half8&, half8&) {}
+};
+
+// ---------------------------------------------------------------------------------
+// The kernel. GU: gate/up (rows of f, input x planes of width d, output h planes and,
+// when the down type has mins, h sums of width swo). !GU: down (rows of d, input h of
+// width f, output y slice 0).
+// ---------------------------------------------------------------------------------
+struct PfArgs {
+  const ExpertWork* work;
+  const uint32_t* ptile;
+  const _Float16* in;     // [2][nk][K] hi, lo planes
+  const _Float16* ins;    // [2][nk][K/SW] sums (types with mins)
+  uint32_t nk, K, rows;   // slots, input width, output rows (f or d)
+  _Float16* out;          // GU: [2][nk][rows] h planes
+  _Float16* outs;         // GU: [2][nk][rows/swo] h sums, or null
+  uint32_t swo;           // GU: width of the h sums (0: none)
+  float* y;               // down: [nk][rows]
+};
+
+template <int QT, bool GU>
+__global__ void __launch_bounds__(kPfThreads, 2) k_pf(PfArgs a) {
+  using T = PF<QT>;
+  using D = Dec<QT>;
+  constexpr int KC = T::KC, NCK = KC / 8, NPC = T::NPC, NCH = T::EU / KC, SPC = KC / 16;
+  constexpr int U = UT_<QT>::U, NP = U / 16;
+  constexpr uint32_t WROWS = GU ? 128 : 256;  // rows of a workgroup
+  __shared__ __attribute__((aligned(16))) uint8_t wl[4 * NPC * 1024];
+  __shared__ __attribute__((aligned(16))) uint8_t xl[2 * kPfTok * KC * 2];
+
+  const uint32_t pt = a.ptile[blockIdx.y];
+  if (pt == ~0u) return;
+  const ExpertWork* W = a.work + (pt >> 16);
+  const uint32_t t0 = (pt & 0xffffu) * kPfTok;
+  const uint32_t m = min(kPfTok, W->m - t0), s0 = W->s0 + t0;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t K = a.K, nunit = K / T::EU;
+  const size_t plane = (size_t)a.nk * K;
+
+  // slab tiles of the workgroup's 4 (matrix, tile) pairs: gate tiles 2x, 2x+1 then up
+  // tiles 2x, 2x+1 (GU), or down tiles 4x .. 4x+3
+  const size_t tile_bytes = (size_t)nunit * kTileRows * U;
+  const uint8_t* m_lo = GU ? W->w[0] + 2 * blockIdx.x * tile_bytes : W->w[2] + 4 * blockIdx.x * tile_bytes;
+  const uint8_t* m_hi = GU ? W->w[1] + 2 * blockIdx.x * tile_bytes : m_lo + 2 * tile_bytes;
+  // the lane's row in each of its two row tiles
+  const uint8_t* row[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; rt++) {
+    const uint32_t tm = GU ? 2 * rt + wave / 2 : wave, i = GU ? 32 * (wave % 2) + l32 : 32 * rt + l32;
+    row[rt] = wl + (tm * NPC * 64 + i) * 16;
+  }
+  // the lane's token row of each 32-token tile in xl, and its column swizzle (t % NCK,
+  // the same for both tiles), in bytes
+  const uint8_t* xrow = xl + l32 * NCK * 16;
+  uint32_t tsw = (l32 % NCK) * 16;
+
+  f32x16 acc[2][2], P[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = P[i][j][r] = 0.0f;
+  const f32x16 zero = acc[0][0];
+
+  for (uint32_t u = 0; u < nunit; u++) {
+    static_for<NCH>([&](auto cc) {
+      constexpr int C = decltype(cc)::value;
+      const uint32_t k0 = u * T::EU + C * KC;
+      __syncthreads();  // the previous chunk's readers are done
+      // stage straight into LDS (global_load_lds: lane i of a wave writes 16 bytes at the
+      // wave's base + 16 i); the wave's j-th batch is items 64 wq + lane, wq = 4 j + wave,
+      // at LDS byte 16 * item. Weight pieces: item (tm, pc, row i) ...
+#pragma unroll
+      for (int j = 0; j < NPC; j++) {
+        const uint32_t wq = 4 * j + wave, tm = wq / NPC, pc = wq % NPC;
+        const uint8_t* src = (tm < 2 ? m_lo : m_hi) + (tm % 2) * tile_bytes;
+        lds_load16(src + ((size_t)u * NP + (uint32_t)T::piece(C, (int)pc)) * 1024 + lane * 16, wl + 1024 * wq);
+      }
+      // ... and the tokens' hi/lo chunks: item (plane, token t, position), 16-byte column
+      // c of token t at position c ^ (t % NCK)
+      constexpr uint32_t RW = 64 / NCK;  // token rows per wave batch
+#pragma unroll
+      for (int j = 0; j < 2 * (int)kPfTok * NCK / kPfThreads; j++) {
+        const uint32_t wq = 4 * j + wave, pl = wq / NCK;
+        const uint32_t t = (RW * wq) % kPfTok + lane / NCK, c = (lane % NCK) ^ (t % NCK), tc = min(t, m - 1);
+        const _Float16* src = a.in + pl * plane;
+        lds_load16(src + ((s0 + tc) * K + k0 + 8 * c), xl + 1024 * wq);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      asm volatile("" : "+v"(tsw));  // per-step addresses are made here, not kept across chunks
+      static_for<SPC>([&](auto ss) {
+        constexpr int SL = decltype(ss)::value, S = C * SPC + SL;
+        half8 bw[2], ax[2][2];
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++) bw[rt] = D::template frag<C, S>(row[rt], h);
+        const uint32_t pos = ((2 * SL + h) * 16) ^ tsw;
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+          for (int pl = 0; pl < 2; pl++)
+            ax[tt][pl] = *reinterpret_cast<const half8*>(xrow + pos + (pl * kPfTok + 32 * tt) * NCK * 16);
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+          for (int tt = 0; tt < 2; tt++) {
+            if constexpr (T::SU16 == 0) {
+              acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[tt][0], bw[rt], acc[rt][tt], 0, 0, 0);
+              acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[tt][1], bw[rt], acc[rt][tt], 0, 0, 0);
+            } else {
+              const f32x16 c0 = (S % T::SU16 == 0) ? zero : P[rt][tt];
+              P[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[tt][0], bw[rt], c0, 0, 0, 0);
+              P[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[tt][1], bw[rt], P[rt][tt], 0, 0, 0);
+            }
+          }
+        if constexpr (T::SU16 != 0) {
+          if constexpr ((S + 1) % T::SU16 == 0) {
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++) {
+              const float sc = D::template scale<C, S>(row[rt]);
+#pragma unroll
+              for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[rt][tt][r] = __builtin_fmaf(sc, P[rt][tt][r], acc[rt][tt][r]);
+            }
+          }
+        }
+      });
+      if constexpr (T::SW != 0 && C == NCH - 1) {
+        // min term of unit u: -sum over its sub-blocks of (dmin*m) * S, three MFMA passes
+        constexpr int NS = T::EU / (T::SW ? T::SW : 1);  // sub-blocks per unit (8 or 16)
+        const uint32_t ns_row = K / T::SW;
+        half8 bh[2], bl[2];
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++) D::template mins<C>(row[rt], h, bh[rt], bl[rt]);
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+          const uint32_t t = min(32 * tt + l32, m - 1);
+          const uint32_t idx = u * NS + (NS == 16 ? 8 * h : 0);  // 8 sub-blocks: upper lanes carry zeros
+          const _Float16* sp = a.ins + (size_t)(s0 + t) * ns_row + idx;
+          const half8 sh = *reinterpret_cast<const half8*>(sp);
+          const half8 sl = *reinterpret_cast<const half8*>(sp + (size_t)a.nk * ns_row);
+#pragma unroll
+          for (int rt = 0; rt < 2; rt++) {
+            acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh, bh[rt], acc[rt][tt], 0, 0, 0);
+            acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sl, bh[rt], acc[rt][tt], 0, 0, 0);
+            acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh, bl[rt], acc[rt][tt], 0, 0, 0);
+          }
+        }
+      }
+    });
+  }
+
+  // epilogue
+#pragma unroll
+  for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const uint32_t t = 32 * tt + 8 * (r / 4) + 4 * h + (r % 4);
+      if constexpr (GU) {
+        const uint32_t fr = blockIdx.x * WROWS + 32 * wave + l32;
+        const float hv = swiglu(acc[0][tt][r], acc[1][tt][r]);
+        const _Float16 hi = (_Float16)hv, lo = (_Float16)(hv - (float)hi);
+        if (t < m) {
+          const size_t o = (size_t)(s0 + t) * a.rows + fr;
+          a.out[o] = hi;
+          a.out[o + (size_t)a.nk * a.rows] = lo;
+        }
+        if (a.swo) {  // sums of h over swo consecutive rows (lanes): the down min term's S
+          float s = hv;
+          for (uint32_t o = 1; o < a.swo; o <<= 1) s += __shfl_xor(s, (int)o, 64);
+          if (t < m && (l32 % a.swo) == 0) {
+            const uint32_t ns = a.rows / a.swo;
+            const size_t o = (size_t)(s0 + t) * ns + fr / a.swo;
+            const _Float16 shi = (_Float16)s;
+            a.outs[o] = shi;
+            a.outs[o + (size_t)a.nk * ns] = (_Float16)(s - (float)shi);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++) {
+          const uint32_t dr = blockIdx.x * WROWS + 64 * wave + 32 * rt + l32;
+          if (t < m) a.y[(size_t)(s0 + t) * a.rows + dr] = acc[rt][tt][r];
+        }
+      }
+    }
+}
+
+template <int QT>
+hipError_t prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  if constexpr (QT == F32) {
+    return hipErrorNotSupported;
+  } else {
+    PfArgs a{};
+    a.work = B.work;
+    a.ptile = B.ptile;
+    a.in = B.xh;
+    a.ins = B.xsh;
+    a.nk = n * L.k;
+    a.K = L.d;
+    a.rows = L.f;
+    a.out = B.hh;
+    a.swo = pf_sum_width(L.qt_down);
+    a.outs = a.swo ? B.hsh : nullptr;
+    hipLaunchKernelGGL((k_pf<QT, true>), dim3(L.f / 128, B.ptile_cap), dim3(kPfThreads), 0, st, a);
+    return hipGetLastError();
+  }
+}
+
+template <int QT>
+hipError_t prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  if constexpr (QT == F32) {
+    return hipErrorNotSupported;
+  } else {
+    PfArgs a{};
+    a.work = B.work;
+    a.ptile = B.ptile;
+    a.in = B.hh;
+    a.ins = B.hsh;
+    a.nk = n * L.k;
+    a.K = L.f;
+    a.rows = L.d;
+    a.y = B.y;
+    hipLaunchKernelGGL((k_pf<QT, false>), dim3(L.d / 256, B.ptile_cap), dim3(kPfThreads), 0, st, a);
+    return hipGetLastError();
+  }
+}
+
+template hipError_t prefill_gateup<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, hipStream_t);
+template hipError_t prefill_down<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, hipStream_t);
+
+}  // namespace gmoe

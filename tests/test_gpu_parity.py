@@ -13,7 +13,7 @@ import pytest
 import garuda_amd as G
 from garuda_amd import moe as M
 from oracle import oracle as O
-from tests.helpers import fast_random_blocks
+from tests.helpers import fast_random_blocks, skew_direction, skew_router, skew_tokens
 
 pytestmark = pytest.mark.gpu
 
@@ -138,7 +138,11 @@ def test_dispatch_is_a_stable_counting_sort(dev):
 def make_layer(rng, d, f, ne, qt_gu, qt_dn, wstd=0.02):
     mats = {}
     for name, rows, cols, qt in (("gate", f, d, qt_gu), ("up", f, d, qt_gu), ("down", d, f, qt_dn)):
-        mats[name] = M.quantize(qt, rng.normal(0, wstd, ne * rows * cols).astype(np.float32))
+        if ne * rows * cols > (1 << 26):  # full-size layers: the library's threaded generator
+            x = M.fill_gaussian(int(rng.integers(1 << 62)), ne * rows * cols, 0.0, wstd, 16)
+        else:
+            x = rng.normal(0, wstd, ne * rows * cols).astype(np.float32)
+        mats[name] = M.quantize(qt, x, 16)
     router = rng.normal(0, wstd, ne * d).astype(np.float32)
     return router, mats
 
@@ -149,9 +153,15 @@ def oracle_layer(d, f, ne, k, router, mats, qts, math, gating=0, combine=0):
 
 
 def check_layer(dev, d, f, ne, k, qts, ns, math, gating=0, combine=0, seed=0, logits_scale=None, split=False,
-                tie_logits=False):
+                tie_logits=False, zipf=False, sample=None):
+    """zipf: tokens and router biased along one shared direction so the expert load
+    follows Zipf(1.1); sample: compare only this many tokens (spread over the batch)
+    with the oracle, which then runs on those tokens alone."""
     rng = np.random.default_rng(seed)
     router, mats = make_layer(rng, d, f, ne, qts[0], qts[2])
+    if zipf:
+        u = skew_direction(seed + 1, d)
+        router = skew_router(router, ne, d, u)
     gpu_mats = dict(mats)
     if split:
         for name, rows, cols in (("gate", f, d), ("up", f, d), ("down", d, f)):
@@ -170,7 +180,15 @@ def check_layer(dev, d, f, ne, k, qts, ns, math, gating=0, combine=0, seed=0, lo
                 logits = (rng.random((n, ne), dtype=np.float32) * np.float32(logits_scale)).astype(np.float32)
             if tie_logits:  # four distinct values: most tokens have ties inside and across the top k
                 logits = (rng.integers(0, 4, (n, ne)) * 0.5).astype(np.float32)
+            if zipf:
+                hs = skew_tokens(hs, u)
             out, ids, w = layer.feed_forward_batch(hs, logits)
+            if zipf:
+                say(f"  expert loads: {np.bincount(ids.reshape(-1), minlength=ne).tolist()}")
+            if sample is not None and sample < n:
+                pick = np.linspace(0, n - 1, sample).astype(np.int64)
+                hs, out, ids, w = hs[pick], out[pick], ids[pick], w[pick]
+                logits = None if logits is None else logits[pick]
             wout, wids, ww = O.feed_forward_batch(L, hs, logits, threads=8)
             assert np.array_equal(ids, wids), "routing differs"
             assert np.array_equal(bits(w), bits(ww)), "routing weights differ"
@@ -217,6 +235,28 @@ def test_front_end_given_logits_with_ties(dev, gating):
 
 def test_front_end_64_experts(dev):
     check_layer(dev, 256, 256, 64, 6, (G.Q4_K,) * 3, (1, 5, 12), G.MATH_PACKED, seed=8)
+
+
+# f32 math from kPfMinSlots = 64 slots runs the expert products on MFMA (fp16 operands,
+# f32 sums) over token tiles of 128; Zipf-skewed loads give the busiest expert several
+# tiles, the last one partial.
+@pytest.mark.parametrize("qts", [(G.Q4_K,) * 3, (G.Q5_K,) * 3, (G.Q6_K,) * 3, (G.Q3_K, G.Q3_K, G.Q4_K),
+                                 (G.Q2_K,) * 3, (G.Q8_0,) * 3, (G.Q6_K, G.Q6_K, G.Q8_0), (G.Q4_0,) * 3,
+                                 (G.F16,) * 3])
+def test_prefill_every_type(dev, qts):
+    check_layer(dev, 256, 512, 8, 2, qts, (32, 300), G.MATH_F32, seed=20 + qts[0], zipf=True)
+
+
+@pytest.mark.parametrize("qts", [(G.Q4_K,) * 3, (G.Q6_K, G.Q6_K, G.Q8_0), (G.Q4_0,) * 3])
+def test_prefill_zipf_512_tokens(dev, qts):
+    # 1024 slots, ~400 on the busiest expert (4 tiles); K = 1024 (gate/up) and 2048 (down)
+    check_layer(dev, 1024, 2048, 8, 2, qts, (512,), G.MATH_F32, seed=30, zipf=True)
+
+
+def test_prefill_c3_shape_sampled(dev):
+    # d 4096, f 14336, 8 experts, top-2, Q4_K, 512 Zipf-skewed tokens;
+    # all 512 go through the GPU, 24 of them are checked against the oracle
+    check_layer(dev, 4096, 14336, 8, 2, (G.Q4_K,) * 3, (512,), G.MATH_F32, seed=31, zipf=True, sample=24)
 
 
 def test_split_layout_matches_stacked(dev):
