@@ -36,6 +36,7 @@ sys.path.insert(0, str(ROOT))
 
 D, F, NE, K = 4096, 14336, 8, 2
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
 TRAFFIC_FILE = ROOT / "profiles" / "k_gu_units_q4k_c2_b8_traffic.md"
 SEED = 0x6761_7275_6461_2000  # build-side seeds, "garuda" + tag
 
@@ -82,6 +83,61 @@ def measured_traffic(batch, math, layers):
         return None
 
 
+def prefill_leg(a, dev, mats, threads, stream, timed):
+    """the same Q4_K layer at a prefill of `a.prefill_tokens` tokens,
+    routing skewed to Zipf(1.1) expert loads through one shared activation direction, f32
+    math (the expert products on MFMA). Returns the JSON object of the leg."""
+    import torch
+    import garuda_amd as G
+    from garuda_amd import moe as M
+
+    n = a.prefill_tokens
+    u = M.skew_direction(SEED + 0x300, D)
+    layers = []
+    for l in range(a.prefill_layers):
+        router = M.skew_router(M.fill_gaussian(SEED + 0x100 + l, NE * D, 0.0, 0.02, threads), NE, D, u)
+        layers.append(G.MoeLayer(dev, D, F, NE, K, router, mats["gate"], mats["up"], mats["down"],
+                                 (G.Q4_K,) * 3, math=G.MATH_F32))
+    hs_np = M.skew_tokens(M.fill_gaussian(SEED + 0x400, n * D, 0.0, 1.0, threads).reshape(n, D), u)
+    hs = torch.from_numpy(hs_np).cuda()
+    out = torch.empty((n, D), dtype=torch.float32, device="cuda")
+    ids = torch.empty((len(layers), n, K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((len(layers), n, K), dtype=torch.float32, device="cuda")
+    sh = stream.cuda_stream
+
+    def step(i):
+        l = i % len(layers)
+        layers[l].forward_async(hs.data_ptr(), n, out.data_ptr(), ids[l].data_ptr(), wts[l].data_ptr(), 0, sh)
+
+    for i in range(max(3, a.warmup // 4)):
+        step(i)
+    torch.cuda.synchronize()
+    ms, _ = timed(step, a.prefill_steps, False)
+    _, (gu_ms, dn_ms, _) = timed(step, a.prefill_steps, True)
+    loads = [np.bincount(ids[l].cpu().numpy().reshape(-1), minlength=NE) for l in range(len(layers))]
+    flops = float(np.mean([ld.sum() for ld in loads])) * 6 * D * F  # 2 flops per MAC, 3 matrices
+    ex_s = (gu_ms + dn_ms) / 1e3
+    step_s = ms / a.prefill_steps / 1e3
+    tflops = flops / ex_s / 1e12
+    log(f"prefill n={n}: {n / step_s:.0f} tok/s, {step_s * 1e6:.0f} us/call, gate/up {gu_ms * 1e3:.0f} us, "
+        f"down {dn_ms * 1e3:.0f} us, {tflops:.0f} TFLOP/s algorithmic ({tflops / MFMA_PEAK_TFLOPS:.1%} of peak), "
+        f"loads {loads[0].tolist()}")
+    for l in layers:
+        l.release()
+    return {
+        "workload": f"C3 prefill: the C2 layer at {n} tokens, Zipf(1.1)-skewed routing, f32 math, "
+                    f"{len(layers)} HBM copies rotated",
+        "tokens_per_s": n / step_s, "ms_per_call": step_s * 1e3, "steps": a.prefill_steps,
+        "expert_loads": [int(x) for x in loads[0]],
+        "gateup_us": gu_ms * 1e3, "down_us": dn_ms * 1e3,
+        "roofline": {"bound": "mfma", "kernels": "k_pf<Q4_K, gate/up> + k_pf<Q4_K, down>",
+                     "achieved": tflops, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": tflops / MFMA_PEAK_TFLOPS,
+                     "flops_per_call": flops,
+                     "note": "algorithmic flops (sum of expert tokens x 6 d f) over the two MFMA launches' "
+                             "time; the exact-product scheme issues two fp16 MFMA passes per product"},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -98,6 +154,10 @@ def main():
                          "(the roofline's kernel times); off skips that second pass")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="also run one device-to-device copy of MB MiB (the counter calibration of profiles/)")
+    ap.add_argument("--prefill-tokens", type=int, default=512,
+                    help="tokens of the C3 prefill leg (Zipf-skewed routing, f32 math on MFMA); 0 skips it")
+    ap.add_argument("--prefill-steps", type=int, default=40)
+    ap.add_argument("--prefill-layers", type=int, default=2)
     a = ap.parse_args()
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -116,7 +176,8 @@ def main():
 
     math = G.MATH_PACKED if a.math == "packed" else G.MATH_F32
     expert_bytes = 3 * M.byte_size(G.Q4_K, F * D)
-    slab = a.layers * NE * (expert_bytes + 3 * 4096) + (256 << 20)
+    n_pf_layers = a.prefill_layers if a.prefill_tokens else 0
+    slab = (a.layers + n_pf_layers) * NE * (expert_bytes + 3 * 4096) + (256 << 20)
     dev = G.Device(0, slab_bytes=slab)
     layers = []
     t0 = time.time()
@@ -131,6 +192,25 @@ def main():
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     sh = stream.cuda_stream
+
+    def timed(step, steps, events):
+        """`steps` calls of step(i) between two synchronisations; with events, also the
+        gate/up and down launch times (HIP events on the stream around each launch)."""
+        dev.kernel_time(0)  # drain
+        base = [dev.kernel_time(w) for w in range(3)]
+        dev.set_kernel_timing(events)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        for i in range(steps):
+            step(i)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        dev.set_kernel_timing(False)
+        kt = [dev.kernel_time(w) for w in range(3)]
+        cnt = max(kt[0][1] - base[0][1], 1)
+        return ev0.elapsed_time(ev1), [(kt[w][0] - base[w][0]) / cnt for w in range(3)]
+
     results = {}
     batches = sorted(set([a.batch] + [int(b) for b in a.sweep.split(",") if b]))
     for n in batches:
@@ -147,29 +227,10 @@ def main():
         for i in range(a.warmup):
             step(i)
         torch.cuda.synchronize()
-
-        def timed(events):
-            """K steps between two synchronisations; with events, also the gate/up and down
-            launch times (HIP events on the stream around each launch)."""
-            dev.kernel_time(0)  # drain
-            base = [dev.kernel_time(w) for w in range(3)]
-            dev.set_kernel_timing(events)
-            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            ev0.record(stream)
-            for i in range(a.steps):
-                step(i)
-            ev1.record(stream)
-            torch.cuda.synchronize()
-            dev.set_kernel_timing(False)
-            kt = [dev.kernel_time(w) for w in range(3)]
-            cnt = max(kt[0][1] - base[0][1], 1)
-            return ev0.elapsed_time(ev1), [(kt[w][0] - base[w][0]) / cnt for w in range(3)]
-
         # the throughput is timed bare (the per-launch events cost ~3 us each); the kernel
         # times come from a second pass over the same steps with events around each launch
-        ms, _ = timed(False)
-        ms_ev, kms = timed(a.kernel_events == "on")
+        ms, _ = timed(step, a.steps, False)
+        ms_ev, kms = timed(step, a.steps, a.kernel_events == "on")
         nan = float("nan")
         gu_ms, dn_ms, ex_ms = kms if a.kernel_events == "on" else (nan, nan, nan)
         touched = [len(np.unique(ids[l].cpu().numpy())) for l in range(len(layers))]
@@ -186,6 +247,10 @@ def main():
         log(f"n={n}: {results[n]['tokens_per_s']:.0f} tok/s, {ms / a.steps * 1e3:.1f} us/step, "
             f"E={e_avg:.2f}, gate/up {gu_ms * 1e3:.1f} us ({results[n]['gateup_GBs']:.0f} GB/s), "
             f"down {dn_ms * 1e3:.1f} us ({results[n]['down_GBs']:.0f} GB/s), layer {results[n]['layer_GBs']:.0f} GB/s")
+
+    prefill = None
+    if a.prefill_tokens:
+        prefill = prefill_leg(a, dev, mats, threads, stream, timed)
 
     if a.calibrate_copy:
         src = torch.empty(a.calibrate_copy << 18, dtype=torch.float32, device="cuda")
@@ -240,6 +305,7 @@ def main():
                      "traffic": measured_traffic(a.batch, a.math, a.layers),
                      "bytes_per_launch": r["gateup_bytes"], "avg_launch_us": r["gateup_us"]},
         "cpu_baseline": cpu,
+        "prefill": prefill,
         "sweep": {str(n): {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res.items()}
                   for n, res in results.items()},
     }

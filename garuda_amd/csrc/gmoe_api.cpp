@@ -407,6 +407,7 @@ gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStr
     if (quant) HIP_TRY(launch_quant_act(B.hs, n, L.d, B.xq, B.xs, B.x16, st));
   }
   if (pf) HIP_TRY(launch_gather_f16(D, B, n, st));
+  const uint32_t ksg = pf ? prefill_ksg(D, B) : down_ksg(D, n);
   Timing tm{};
   if (c->timing) {
     tm = take_timing(c);
@@ -414,12 +415,12 @@ gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStr
   }
   HIP_TRY(pf ? launch_prefill_gateup(D, B, n, st) : launch_gateup(D, B, n, st));
   if (c->timing) HIP_TRY(hipEventRecord(tm.b, st));
-  HIP_TRY(pf ? launch_prefill_down(D, B, n, st) : launch_down(D, B, n, st));
+  HIP_TRY(pf ? launch_prefill_down(D, B, n, ksg, st) : launch_down(D, B, n, st));
   if (c->timing) {
     HIP_TRY(hipEventRecord(tm.c, st));
     c->pending.push_back(tm);
   }
-  HIP_TRY(launch_combine(D, B, n, pf ? 1 : down_ksg(D, n), st));
+  HIP_TRY(launch_combine(D, B, n, ksg, st));
   return GMOE_OK;
 }
 

@@ -177,7 +177,10 @@ __host__ __device__ constexpr uint32_t pf_sum_width(uint32_t qt) {
   return (qt == Q4_K || qt == Q5_K) ? 32u : qt == Q2_K ? 16u : 0u;
 }
 template <int QT> hipError_t prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
-template <int QT> hipError_t prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+template <int QT> hipError_t prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg,
+                                          hipStream_t st);
+// K slices of the prefill down product (partial slices of y, added by the combine).
+template <int QT> uint32_t prefill_down_slices(const LayerDev& L, const FwdBufs& B);
 // Token tiles a call of n tokens can need at most.
 inline uint32_t prefill_tiles_cap(uint32_t n, uint32_t k, uint32_t ne) { return (n * k) / kPfTok + ne + 1; }
 
@@ -202,7 +205,8 @@ hipError_t launch_combine(const LayerDev& L, const FwdBufs& B, uint32_t n, uint3
 bool prefill_ok(const LayerDev& L, uint32_t n);
 hipError_t launch_gather_f16(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 hipError_t launch_prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
-hipError_t launch_prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+hipError_t launch_prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
+uint32_t prefill_ksg(const LayerDev& L, const FwdBufs& B);
 // Number of partial slices launch_down writes for this layer and batch (1 = y is final).
 uint32_t down_ksg(const LayerDev& L, uint32_t n);
 // out[i] = parts[i] + parts[count + i] + ... over ksg slices, in slice order.

@@ -794,8 +794,9 @@ static bool prefill_type(uint32_t qt) {
 
 bool prefill_ok(const LayerDev& L, uint32_t n) {
   const uint32_t nk = n * L.k;
+  // rows: gate/up workgroups take up to 256 rows of f, down ones up to 512 of d
   return L.math == 1 && nk >= kPfMinSlots && nk >= 4 * L.ne && L.qt_gate == L.qt_up && prefill_type(L.qt_gate) &&
-         prefill_type(L.qt_down) && L.d % 256 == 0 && L.f % 256 == 0 && L.ne < 65536;
+         prefill_type(L.qt_down) && L.d % 512 == 0 && L.f % 256 == 0 && L.ne < 65536;
 }
 
 // The activations in slot order as fp16 pairs, x = hi + lo (hi = fp16(x), lo =
@@ -853,13 +854,22 @@ hipError_t launch_prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+hipError_t launch_prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st) {
   switch (L.qt_down) {
-#define DN(T) case T: return prefill_down<T>(L, B, n, st);
+#define DN(T) case T: return prefill_down<T>(L, B, n, ksg, st);
     DN(Q4_K) DN(Q5_K) DN(Q6_K) DN(Q3_K) DN(Q2_K) DN(Q8_0) DN(Q4_0) DN(F16)
 #undef DN
   }
   return hipErrorInvalidValue;
+}
+
+uint32_t prefill_ksg(const LayerDev& L, const FwdBufs& B) {
+  switch (L.qt_down) {
+#define DN(T) case T: return prefill_down_slices<T>(L, B);
+    DN(Q4_K) DN(Q5_K) DN(Q6_K) DN(Q3_K) DN(Q2_K) DN(Q8_0) DN(Q4_0) DN(F16)
+#undef DN
+  }
+  return 1;
 }
 
 hipError_t launch_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {

@@ -63,42 +63,44 @@ __device__ __forceinline__ void static_for(F&& f) {
 // ---------------------------------------------------------------------------------
 // Per-type shape: EU values per slab unit, KC values per LDS chunk, NPC 16-byte pieces
 // of a unit that chunk c needs (piece(c, i) is the i-th), SU16 K16 steps per scale
-// (0: the decoded values are the weights), SW the width of a min-term sub-block.
+// (0: the decoded values are the weights), SW the width of a min-term sub-block, NW
+// waves per workgroup. A workgroup double-buffers its chunks, 2 x (NW * NPC KiB of
+// weight pieces + 2 * kPfTok * KC * 2 bytes of activations), within the 160 KiB of LDS.
 // Unit byte layouts are those of the packed blocks (quant/mod.rs:624-875); Q8_0/Q4_0
 // units are eight blocks repacked as 8 f16 scales then the quants.
 // ---------------------------------------------------------------------------------
 template <int QT> struct PF;
 template <> struct PF<Q4_K> {  // d dmin | scales[12] | qs[128]: sub-blocks 4c..4c+3 in pieces 1+4c..
-  static constexpr int EU = 256, KC = 128, NPC = 5, SU16 = 16, SW = 32;
+  static constexpr int EU = 256, KC = 128, NPC = 5, SU16 = 16, SW = 32, NW = 8;
   static constexpr int piece(int c, int i) { return i == 0 ? 0 : 4 * c + i; }
 };
-template <> struct PF<Q5_K> {  // d dmin scales | qh[32] | qs[128]
-  static constexpr int EU = 256, KC = 128, NPC = 7, SU16 = 16, SW = 32;
-  static constexpr int piece(int c, int i) { return i < 3 ? i : 4 * c + i; }
+template <> struct PF<Q5_K> {  // d dmin scales | qh[32] | qs[128]: sub-blocks 2c, 2c+1 in pieces 3+2c..
+  static constexpr int EU = 256, KC = 64, NPC = 5, SU16 = 16, SW = 32, NW = 8;
+  static constexpr int piece(int c, int i) { return i < 3 ? i : 2 * c + i; }
 };
 template <> struct PF<Q6_K> {  // ql[128] | qh[64] | scales[16] | d
-  static constexpr int EU = 256, KC = 128, NPC = 8, SU16 = 1, SW = 0;
+  static constexpr int EU = 256, KC = 128, NPC = 8, SU16 = 1, SW = 0, NW = 4;
   static constexpr int piece(int c, int i) { return i < 4 ? 4 * c + i : i < 6 ? 8 + 2 * c + (i - 4) : 12 + (i - 6); }
 };
 template <> struct PF<Q3_K> {  // hmask[32] | qs[64] | scales[12] d
-  static constexpr int EU = 256, KC = 128, NPC = 5, SU16 = 16, SW = 0;
+  static constexpr int EU = 256, KC = 128, NPC = 5, SU16 = 16, SW = 0, NW = 8;
   static constexpr int piece(int c, int i) { return i < 2 ? i : i < 4 ? 2 + 2 * c + (i - 2) : 6; }
 };
 template <> struct PF<Q2_K> {  // scales[16] | qs[64] | d dmin
-  static constexpr int EU = 256, KC = 128, NPC = 4, SU16 = 16, SW = 16;
+  static constexpr int EU = 256, KC = 128, NPC = 4, SU16 = 16, SW = 16, NW = 8;
   static constexpr int piece(int c, int i) { return i == 0 ? 0 : i < 3 ? 1 + 2 * c + (i - 1) : 5; }
 };
-template <> struct PF<Q8_0> {  // 8 scales | 8 x 32 quants
-  static constexpr int EU = 256, KC = 128, NPC = 9, SU16 = 2, SW = 0;
-  static constexpr int piece(int c, int i) { return i == 0 ? 0 : 8 * c + i; }
-};
-template <> struct PF<Q4_0> {  // 8 scales | 8 x 16 quant bytes
-  static constexpr int EU = 256, KC = 128, NPC = 5, SU16 = 2, SW = 0;
+template <> struct PF<Q8_0> {  // 8 scales | 8 x 32 quants: blocks 2c, 2c+1 in pieces 1+4c..4+4c
+  static constexpr int EU = 256, KC = 64, NPC = 5, SU16 = 2, SW = 0, NW = 8;
   static constexpr int piece(int c, int i) { return i == 0 ? 0 : 4 * c + i; }
 };
-template <> struct PF<F16> {  // 64 halves
-  static constexpr int EU = 64, KC = 64, NPC = 8, SU16 = 0, SW = 0;
-  static constexpr int piece(int, int i) { return i; }
+template <> struct PF<Q4_0> {  // 8 scales | 8 x 16 quant bytes
+  static constexpr int EU = 256, KC = 128, NPC = 5, SU16 = 2, SW = 0, NW = 8;
+  static constexpr int piece(int c, int i) { return i == 0 ? 0 : 4 * c + i; }
+};
+template <> struct PF<F16> {  // 64 halves: values 32c.. in pieces 4c..4c+3
+  static constexpr int EU = 64, KC = 32, NPC = 4, SU16 = 0, SW = 0, NW = 8;
+  static constexpr int piece(int c, int i) { return 4 * c + i; }
 };
 
 template <int QT>
@@ -372,8 +374,8 @@ template <> struct Dec<Q4_0> {
 template <> struct Dec<F16> {
   template <int C, int S>
   static __device__ __forceinline__ half8 frag(const uint8_t* row, uint32_t h) {
-    // values 16S + 8h .. are bytes 32S + 16h ..: piece (and slot) 2S + h
-    return __builtin_bit_cast(half8, ld16(row + (2 * S + h) * 1024));
+    // values 16S + 8h .. are bytes 32S + 16h ..: piece 2S + h, slot 2S + h - 4C
+    return __builtin_bit_cast(half8, ld16(row + (2 * S - 4 * C + h) * 1024));
   }
   template <int C, int S>
   static __device__ __forceinline__ float scale(const uint8_t*) { return 1.0f; }
@@ -384,7 +386,7 @@ template <> struct Dec<F16> {
 // ---------------------------------------------------------------------------------
 // The kernel. GU: gate/up (rows of f, input x planes of width d, output h planes and,
 // when the down type has mins, h sums of width swo). !GU: down (rows of d, input h of
-// width f, output y slice 0).
+// width f, units [u0, u1) of K per blockIdx.z slice, output y slice blockIdx.z).
 // ---------------------------------------------------------------------------------
 struct PfArgs {
   const ExpertWork* work;
@@ -392,21 +394,25 @@ struct PfArgs {
   const _Float16* in;     // [2][nk][K] hi, lo planes
   const _Float16* ins;    // [2][nk][K/SW] sums (types with mins)
   uint32_t nk, K, rows;   // slots, input width, output rows (f or d)
+  uint32_t upk;           // down: units of K per slice
   _Float16* out;          // GU: [2][nk][rows] h planes
   _Float16* outs;         // GU: [2][nk][rows/swo] h sums, or null
   uint32_t swo;           // GU: width of the h sums (0: none)
-  float* y;               // down: [nk][rows]
+  float* y;               // down: [slices][nk][rows]
 };
 
 template <int QT, bool GU>
-__global__ void __launch_bounds__(kPfThreads, 2) k_pf(PfArgs a) {
+__global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
   using T = PF<QT>;
   using D = Dec<QT>;
+  constexpr int NW = T::NW, NT = 64 * NW;
   constexpr int KC = T::KC, NCK = KC / 8, NPC = T::NPC, NCH = T::EU / KC, SPC = KC / 16;
   constexpr int U = UT_<QT>::U, NP = U / 16;
-  constexpr uint32_t WROWS = GU ? 128 : 256;  // rows of a workgroup
-  __shared__ __attribute__((aligned(16))) uint8_t wl[4 * NPC * 1024];
-  __shared__ __attribute__((aligned(16))) uint8_t xl[2 * kPfTok * KC * 2];
+  constexpr uint32_t WROWS = 32 * NW * (GU ? 1 : 2);    // rows of a workgroup
+  constexpr uint32_t WBYTES = NW * NPC * 1024, XBYTES = 2 * kPfTok * KC * 2;
+  constexpr int NX = 2 * (int)kPfTok * NCK / NT;        // activation loads per thread per chunk
+  static_assert(2 * (WBYTES + XBYTES) <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * (WBYTES + XBYTES)];
 
   const uint32_t pt = a.ptile[blockIdx.y];
   if (pt == ~0u) return;
@@ -416,24 +422,51 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf(PfArgs a) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t K = a.K, nunit = K / T::EU;
+  const uint32_t u0 = GU ? 0 : blockIdx.z * a.upk, u1 = GU ? nunit : min(nunit, u0 + a.upk);
   const size_t plane = (size_t)a.nk * K;
 
-  // slab tiles of the workgroup's 4 (matrix, tile) pairs: gate tiles 2x, 2x+1 then up
-  // tiles 2x, 2x+1 (GU), or down tiles 4x .. 4x+3
+  // slab tiles of the workgroup's NW (matrix, tile) pairs: NW/2 gate tiles then NW/2 up
+  // tiles (GU), or NW down tiles
   const size_t tile_bytes = (size_t)nunit * kTileRows * U;
-  const uint8_t* m_lo = GU ? W->w[0] + 2 * blockIdx.x * tile_bytes : W->w[2] + 4 * blockIdx.x * tile_bytes;
-  const uint8_t* m_hi = GU ? W->w[1] + 2 * blockIdx.x * tile_bytes : m_lo + 2 * tile_bytes;
-  // the lane's row in each of its two row tiles
-  const uint8_t* row[2];
+  const uint8_t* m_lo = GU ? W->w[0] + (NW / 2) * blockIdx.x * tile_bytes : W->w[2] + NW * blockIdx.x * tile_bytes;
+  const uint8_t* m_hi = GU ? W->w[1] + (NW / 2) * blockIdx.x * tile_bytes : m_lo + (NW / 2) * tile_bytes;
+  // the lane's row in each of its two row tiles (offsets into a weight buffer)
+  uint32_t row[2];
 #pragma unroll
   for (int rt = 0; rt < 2; rt++) {
-    const uint32_t tm = GU ? 2 * rt + wave / 2 : wave, i = GU ? 32 * (wave % 2) + l32 : 32 * rt + l32;
-    row[rt] = wl + (tm * NPC * 64 + i) * 16;
+    const uint32_t tm = GU ? rt * (NW / 2) + wave / 2 : wave, i = GU ? 32 * (wave % 2) + l32 : 32 * rt + l32;
+    row[rt] = (tm * NPC * 64 + i) * 16;
   }
-  // the lane's token row of each 32-token tile in xl, and its column swizzle (t % NCK,
-  // the same for both tiles), in bytes
-  const uint8_t* xrow = xl + l32 * NCK * 16;
+  // the lane's token row of its first 32-token tile in an activation buffer, and its
+  // column swizzle (t % NCK, the same for both tiles), in bytes
+  const uint32_t xrow = l32 * NCK * 16;
   uint32_t tsw = (l32 % NCK) * 16;
+
+  // chunk (u, c) into buffer b: straight into LDS (global_load_lds: lane i of a wave
+  // writes 16 bytes at the wave's base + 16 i); the wave's j-th batch is items
+  // 64 wq + lane, wq = NW j + wave, at byte 16 * item of the buffer's part
+  auto stage = [&](uint32_t u, auto cc, uint32_t b) {
+    constexpr int C = decltype(cc)::value;
+    uint8_t* wb = lds + b * (WBYTES + XBYTES);
+    uint8_t* xb = wb + WBYTES;
+    // weight pieces: item (tm, pc, row i)
+#pragma unroll
+    for (int j = 0; j < NPC; j++) {
+      const uint32_t wq = NW * j + wave, tm = wq / NPC, pc = wq % NPC;
+      const uint8_t* src = (tm < NW / 2 ? m_lo : m_hi) + (tm % (NW / 2)) * tile_bytes;
+      lds_load16(src + ((size_t)u * NP + (uint32_t)T::piece(C, (int)pc)) * 1024 + lane * 16, wb + 1024 * wq);
+    }
+    // activations: item (plane, token t, position); 16-byte column c of token t at
+    // position c ^ (t % NCK)
+    constexpr uint32_t RW = 64 / NCK;  // token rows per wave batch
+    const uint32_t k0 = u * T::EU + C * KC;
+#pragma unroll
+    for (int j = 0; j < NX; j++) {
+      const uint32_t wq = NW * j + wave, pl = wq / NCK;
+      const uint32_t t = (RW * wq) % kPfTok + lane / NCK, c = (lane % NCK) ^ (t % NCK), tc = min(t, m - 1);
+      lds_load16(a.in + pl * plane + ((s0 + tc) * K + k0 + 8 * c), xb + 1024 * wq);
+    }
+  };
 
   f32x16 acc[2][2], P[2][2];
 #pragma unroll
@@ -444,44 +477,35 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf(PfArgs a) {
       for (int r = 0; r < 16; r++) acc[i][j][r] = P[i][j][r] = 0.0f;
   const f32x16 zero = acc[0][0];
 
-  for (uint32_t u = 0; u < nunit; u++) {
+  // one barrier per chunk: chunk k computes from buffer k % 2 while chunk k+1 loads into
+  // the other; the barrier after it says both that every wave is done reading buffer
+  // k % 2 and that every wave's loads of chunk k+1 have landed
+  if (u0 < u1) stage(u0, std::integral_constant<int, 0>{}, 0);  // a slice past the end writes zeros
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (uint32_t u = u0; u < u1; u++) {
     static_for<NCH>([&](auto cc) {
       constexpr int C = decltype(cc)::value;
-      const uint32_t k0 = u * T::EU + C * KC;
-      __syncthreads();  // the previous chunk's readers are done
-      // stage straight into LDS (global_load_lds: lane i of a wave writes 16 bytes at the
-      // wave's base + 16 i); the wave's j-th batch is items 64 wq + lane, wq = 4 j + wave,
-      // at LDS byte 16 * item. Weight pieces: item (tm, pc, row i) ...
-#pragma unroll
-      for (int j = 0; j < NPC; j++) {
-        const uint32_t wq = 4 * j + wave, tm = wq / NPC, pc = wq % NPC;
-        const uint8_t* src = (tm < 2 ? m_lo : m_hi) + (tm % 2) * tile_bytes;
-        lds_load16(src + ((size_t)u * NP + (uint32_t)T::piece(C, (int)pc)) * 1024 + lane * 16, wl + 1024 * wq);
+      const uint32_t b = (NCH % 2 == 0) ? (uint32_t)(C % 2) : ((u - u0) * NCH + C) % 2;
+      if constexpr (C + 1 < NCH) {
+        stage(u, std::integral_constant<int, C + 1>{}, b ^ 1);
+      } else {
+        if (u + 1 < u1) stage(u + 1, std::integral_constant<int, 0>{}, b ^ 1);
       }
-      // ... and the tokens' hi/lo chunks: item (plane, token t, position), 16-byte column
-      // c of token t at position c ^ (t % NCK)
-      constexpr uint32_t RW = 64 / NCK;  // token rows per wave batch
-#pragma unroll
-      for (int j = 0; j < 2 * (int)kPfTok * NCK / kPfThreads; j++) {
-        const uint32_t wq = 4 * j + wave, pl = wq / NCK;
-        const uint32_t t = (RW * wq) % kPfTok + lane / NCK, c = (lane % NCK) ^ (t % NCK), tc = min(t, m - 1);
-        const _Float16* src = a.in + pl * plane;
-        lds_load16(src + ((s0 + tc) * K + k0 + 8 * c), xl + 1024 * wq);
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
+      const uint8_t* wb = lds + b * (WBYTES + XBYTES);
+      const uint8_t* xb = wb + WBYTES;
       asm volatile("" : "+v"(tsw));  // per-step addresses are made here, not kept across chunks
       static_for<SPC>([&](auto ss) {
         constexpr int SL = decltype(ss)::value, S = C * SPC + SL;
         half8 bw[2], ax[2][2];
 #pragma unroll
-        for (int rt = 0; rt < 2; rt++) bw[rt] = D::template frag<C, S>(row[rt], h);
+        for (int rt = 0; rt < 2; rt++) bw[rt] = D::template frag<C, S>(wb + row[rt], h);
         const uint32_t pos = ((2 * SL + h) * 16) ^ tsw;
 #pragma unroll
         for (int tt = 0; tt < 2; tt++)
 #pragma unroll
           for (int pl = 0; pl < 2; pl++)
-            ax[tt][pl] = *reinterpret_cast<const half8*>(xrow + pos + (pl * kPfTok + 32 * tt) * NCK * 16);
+            ax[tt][pl] = *reinterpret_cast<const half8*>(xb + xrow + pos + (pl * kPfTok + 32 * tt) * NCK * 16);
 #pragma unroll
         for (int rt = 0; rt < 2; rt++)
 #pragma unroll
@@ -499,7 +523,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf(PfArgs a) {
           if constexpr ((S + 1) % T::SU16 == 0) {
 #pragma unroll
             for (int rt = 0; rt < 2; rt++) {
-              const float sc = D::template scale<C, S>(row[rt]);
+              const float sc = D::template scale<C, S>(wb + row[rt]);
 #pragma unroll
               for (int tt = 0; tt < 2; tt++)
 #pragma unroll
@@ -514,7 +538,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf(PfArgs a) {
         const uint32_t ns_row = K / T::SW;
         half8 bh[2], bl[2];
 #pragma unroll
-        for (int rt = 0; rt < 2; rt++) D::template mins<C>(row[rt], h, bh[rt], bl[rt]);
+        for (int rt = 0; rt < 2; rt++) D::template mins<C>(wb + row[rt], h, bh[rt], bl[rt]);
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
           const uint32_t t = min(32 * tt + l32, m - 1);
@@ -530,6 +554,8 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf(PfArgs a) {
           }
         }
       }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
     });
   }
 
@@ -549,24 +575,34 @@ __global__ void __launch_bounds__(kPfThreads, 2) k_pf(PfArgs a) {
           a.out[o + (size_t)a.nk * a.rows] = lo;
         }
         if (a.swo) {  // sums of h over swo consecutive rows (lanes): the down min term's S
-          float s = hv;
-          for (uint32_t o = 1; o < a.swo; o <<= 1) s += __shfl_xor(s, (int)o, 64);
+          float sm = hv;
+          for (uint32_t o = 1; o < a.swo; o <<= 1) sm += __shfl_xor(sm, (int)o, 64);
           if (t < m && (l32 % a.swo) == 0) {
             const uint32_t ns = a.rows / a.swo;
             const size_t o = (size_t)(s0 + t) * ns + fr / a.swo;
-            const _Float16 shi = (_Float16)s;
+            const _Float16 shi = (_Float16)sm;
             a.outs[o] = shi;
-            a.outs[o + (size_t)a.nk * ns] = (_Float16)(s - (float)shi);
+            a.outs[o + (size_t)a.nk * ns] = (_Float16)(sm - (float)shi);
           }
         }
       } else {
+        float* y = a.y + (size_t)blockIdx.z * a.nk * a.rows;
 #pragma unroll
         for (int rt = 0; rt < 2; rt++) {
           const uint32_t dr = blockIdx.x * WROWS + 64 * wave + 32 * rt + l32;
-          if (t < m) a.y[(size_t)(s0 + t) * a.rows + dr] = acc[rt][tt][r];
+          if (t < m) y[(size_t)(s0 + t) * a.rows + dr] = acc[rt][tt][r];
         }
       }
     }
+}
+
+template <int QT>
+uint32_t pf_rows(bool gu) {
+  if constexpr (QT == F32) {
+    return 0;
+  } else {
+    return 32u * PF<QT>::NW * (gu ? 1u : 2u);
+  }
 }
 
 template <int QT>
@@ -574,6 +610,7 @@ hipError_t prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipSt
   if constexpr (QT == F32) {
     return hipErrorNotSupported;
   } else {
+    if (L.f % pf_rows<QT>(true)) return hipErrorInvalidValue;
     PfArgs a{};
     a.work = B.work;
     a.ptile = B.ptile;
@@ -585,16 +622,32 @@ hipError_t prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipSt
     a.out = B.hh;
     a.swo = pf_sum_width(L.qt_down);
     a.outs = a.swo ? B.hsh : nullptr;
-    hipLaunchKernelGGL((k_pf<QT, true>), dim3(L.f / 128, B.ptile_cap), dim3(kPfThreads), 0, st, a);
+    hipLaunchKernelGGL((k_pf<QT, true>), dim3(L.f / pf_rows<QT>(true), B.ptile_cap), dim3(64 * PF<QT>::NW), 0, st,
+                       a);
     return hipGetLastError();
   }
 }
 
+// The down product's K slices: enough workgroups for about four rounds of one per CU
+// over the token tiles the call can have, each slice keeping at least 8 units.
 template <int QT>
-hipError_t prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+uint32_t prefill_down_slices(const LayerDev& L, const FwdBufs& B) {
+  if constexpr (QT == F32) {
+    return 1;
+  } else {
+    const uint32_t tiles = (L.d / pf_rows<QT>(false)) * B.ptile_cap, nunit = L.f / PF<QT>::EU;
+    uint32_t ks = (4 * 256 + tiles - 1) / tiles;
+    ks = min(ks, max(1u, nunit / 8));
+    return max(1u, min(ks, kMaxKsg));
+  }
+}
+
+template <int QT>
+hipError_t prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st) {
   if constexpr (QT == F32) {
     return hipErrorNotSupported;
   } else {
+    if (L.d % pf_rows<QT>(false) || ksg < 1 || ksg > kMaxKsg) return hipErrorInvalidValue;
     PfArgs a{};
     a.work = B.work;
     a.ptile = B.ptile;
@@ -603,13 +656,17 @@ hipError_t prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStre
     a.nk = n * L.k;
     a.K = L.f;
     a.rows = L.d;
+    const uint32_t nunit = L.f / PF<QT>::EU;
+    a.upk = (nunit + ksg - 1) / ksg;
     a.y = B.y;
-    hipLaunchKernelGGL((k_pf<QT, false>), dim3(L.d / 256, B.ptile_cap), dim3(kPfThreads), 0, st, a);
+    hipLaunchKernelGGL((k_pf<QT, false>), dim3(L.d / pf_rows<QT>(false), B.ptile_cap, ksg), dim3(64 * PF<QT>::NW),
+                       0, st, a);
     return hipGetLastError();
   }
 }
 
+template uint32_t prefill_down_slices<GMOE_QT>(const LayerDev&, const FwdBufs&);
 template hipError_t prefill_gateup<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, hipStream_t);
-template hipError_t prefill_down<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, hipStream_t);
+template hipError_t prefill_down<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, uint32_t, hipStream_t);
 
 }  // namespace gmoe

@@ -104,6 +104,37 @@ def fill_gaussian(seed: int, n: int, mean: float = 0.0, std: float = 1.0, thread
     return out
 
 
+# ---- synthetic prefill routing: Zipf-skewed expert loads ----
+
+# Logit offsets, in units of the per-token logit noise, under which top-2 of 8 experts
+# picks expert e with the shares of Zipf(s = 1.1): 0.398 0.186 0.119 0.087 0.068 0.055
+# 0.047 0.040 (fitted by simulating Gaussian logits; the realised counts of a run are
+# what tests and benchmarks report).
+ZIPF_MU = (2.134, 1.046, 0.696, 0.469, 0.310, 0.188, 0.084, 0.0)
+
+
+def skew_direction(seed: int, d: int) -> np.ndarray:
+    """A unit vector of R^d, deterministic in seed."""
+    u = np.random.default_rng(seed).normal(0.0, 1.0, d)
+    return u / np.linalg.norm(u)
+
+
+def skew_router(router, ne: int, d: int, u, alpha: float = 4.0, wstd: float = 0.02, mu=ZIPF_MU) -> np.ndarray:
+    """Router rows with their component along the unit vector u replaced by
+    mu[e] * sigma / alpha, sigma = wstd * sqrt(d) being the logit noise of N(0, 1)
+    tokens: tokens whose component along u is alpha (skew_tokens) then have logits
+    mu[e] * sigma plus noise, so the expert load follows mu. f32 out."""
+    R = np.asarray(router, np.float64).reshape(ne, d)
+    R = R - np.outer(R @ u, u) + np.outer(np.asarray(mu[:ne], np.float64) * wstd * np.sqrt(d) / alpha, u)
+    return R.astype(np.float32).reshape(-1)
+
+
+def skew_tokens(hs, u, alpha: float = 4.0) -> np.ndarray:
+    """N(0, 1) tokens with their component along u set to alpha (a shared mean direction)."""
+    H = np.asarray(hs, np.float64)
+    return (H + np.outer(alpha - H @ u, u)).astype(np.float32)
+
+
 @dataclass
 class SlabStats:
     hits: int

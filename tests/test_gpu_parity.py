@@ -13,7 +13,7 @@ import pytest
 import garuda_amd as G
 from garuda_amd import moe as M
 from oracle import oracle as O
-from tests.helpers import fast_random_blocks, skew_direction, skew_router, skew_tokens
+from tests.helpers import fast_random_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -160,8 +160,8 @@ def check_layer(dev, d, f, ne, k, qts, ns, math, gating=0, combine=0, seed=0, lo
     rng = np.random.default_rng(seed)
     router, mats = make_layer(rng, d, f, ne, qts[0], qts[2])
     if zipf:
-        u = skew_direction(seed + 1, d)
-        router = skew_router(router, ne, d, u)
+        u = M.skew_direction(seed + 1, d)
+        router = M.skew_router(router, ne, d, u)
     gpu_mats = dict(mats)
     if split:
         for name, rows, cols in (("gate", f, d), ("up", f, d), ("down", d, f)):
@@ -181,7 +181,7 @@ def check_layer(dev, d, f, ne, k, qts, ns, math, gating=0, combine=0, seed=0, lo
             if tie_logits:  # four distinct values: most tokens have ties inside and across the top k
                 logits = (rng.integers(0, 4, (n, ne)) * 0.5).astype(np.float32)
             if zipf:
-                hs = skew_tokens(hs, u)
+                hs = M.skew_tokens(hs, u)
             out, ids, w = layer.feed_forward_batch(hs, logits)
             if zipf:
                 say(f"  expert loads: {np.bincount(ids.reshape(-1), minlength=ne).tolist()}")
@@ -237,8 +237,8 @@ def test_front_end_64_experts(dev):
     check_layer(dev, 256, 256, 64, 6, (G.Q4_K,) * 3, (1, 5, 12), G.MATH_PACKED, seed=8)
 
 
-# f32 math from kPfMinSlots = 64 slots runs the expert products on MFMA (fp16 operands,
-# f32 sums) over token tiles of 128; Zipf-skewed loads give the busiest expert several
+# f32 math from kPfMinSlots = 64 slots runs the expert products on MFMA (exact fp16
+# products, f32 sums) over token tiles of 64; Zipf-skewed loads give the busiest expert several
 # tiles, the last one partial.
 @pytest.mark.parametrize("qts", [(G.Q4_K,) * 3, (G.Q5_K,) * 3, (G.Q6_K,) * 3, (G.Q3_K, G.Q3_K, G.Q4_K),
                                  (G.Q2_K,) * 3, (G.Q8_0,) * 3, (G.Q6_K, G.Q6_K, G.Q8_0), (G.Q4_0,) * 3,
