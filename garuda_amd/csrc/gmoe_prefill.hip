@@ -409,10 +409,13 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
   constexpr int KC = T::KC, NCK = KC / 8, NPC = T::NPC, NCH = T::EU / KC, SPC = KC / 16;
   constexpr int U = UT_<QT>::U, NP = U / 16;
   constexpr uint32_t WROWS = 32 * NW * (GU ? 1 : 2);    // rows of a workgroup
-  constexpr uint32_t WBYTES = NW * NPC * 1024, XBYTES = 2 * kPfTok * KC * 2;
+  // min-term sums of a unit: NS halves per token and plane, staged with its last chunk
+  constexpr int NS = T::SW ? T::EU / T::SW : 0;
+  constexpr uint32_t WBYTES = NW * NPC * 1024, XBYTES = 2 * kPfTok * KC * 2, SBYTES = 2 * kPfTok * NS * 2;
+  constexpr uint32_t BUF = WBYTES + XBYTES + SBYTES;
   constexpr int NX = 2 * (int)kPfTok * NCK / NT;        // activation loads per thread per chunk
-  static_assert(2 * (WBYTES + XBYTES) <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * (WBYTES + XBYTES)];
+  static_assert(2 * BUF <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * BUF];
 
   const uint32_t pt = a.ptile[blockIdx.y];
   if (pt == ~0u) return;
@@ -447,7 +450,7 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
   // 64 wq + lane, wq = NW j + wave, at byte 16 * item of the buffer's part
   auto stage = [&](uint32_t u, auto cc, uint32_t b) {
     constexpr int C = decltype(cc)::value;
-    uint8_t* wb = lds + b * (WBYTES + XBYTES);
+    uint8_t* wb = lds + b * BUF;
     uint8_t* xb = wb + WBYTES;
     // weight pieces: item (tm, pc, row i)
 #pragma unroll
@@ -465,6 +468,22 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
       const uint32_t wq = NW * j + wave, pl = wq / NCK;
       const uint32_t t = (RW * wq) % kPfTok + lane / NCK, c = (lane % NCK) ^ (t % NCK), tc = min(t, m - 1);
       lds_load16(a.in + pl * plane + ((s0 + tc) * K + k0 + 8 * c), xb + 1024 * wq);
+    }
+    if constexpr (NS != 0 && C == NCH - 1) {
+      // the unit's sub-block sums: item (plane, token t, piece e) = sums 8e .. 8e+7 of
+      // token t, at byte 16 * item of the sums part
+      constexpr uint32_t NE8 = NS / 8, ITEMS = 2 * kPfTok * NE8;
+      const uint32_t ns_row = K / T::SW;
+#pragma unroll
+      for (uint32_t j = 0; j < (ITEMS + NT - 1) / NT; j++) {
+        const uint32_t wq = NW * j + wave;
+        if (wq * 64 < ITEMS) {
+          const uint32_t q = 64 * wq + lane, e = q % NE8, t = (q / NE8) % kPfTok, pl = q / (NE8 * kPfTok);
+          const uint32_t tc = min(t, m - 1);
+          lds_load16(a.ins + (size_t)pl * a.nk * ns_row + (size_t)(s0 + tc) * ns_row + u * NS + 8 * e,
+                     xb + XBYTES + 1024 * wq);
+        }
+      }
     }
   };
 
@@ -492,7 +511,7 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
       } else {
         if (u + 1 < u1) stage(u + 1, std::integral_constant<int, 0>{}, b ^ 1);
       }
-      const uint8_t* wb = lds + b * (WBYTES + XBYTES);
+      const uint8_t* wb = lds + b * BUF;
       const uint8_t* xb = wb + WBYTES;
       asm volatile("" : "+v"(tsw));  // per-step addresses are made here, not kept across chunks
       static_for<SPC>([&](auto ss) {
@@ -530,22 +549,23 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
                 for (int r = 0; r < 16; r++) acc[rt][tt][r] = __builtin_fmaf(sc, P[rt][tt][r], acc[rt][tt][r]);
             }
           }
+          // short scale groups: keep the scheduler from overlapping the next group's
+          // partial sums with these (two live sets of P do not fit the registers)
+          if constexpr (T::SU16 <= 2) __builtin_amdgcn_sched_barrier(0);
         }
       });
       if constexpr (T::SW != 0 && C == NCH - 1) {
         // min term of unit u: -sum over its sub-blocks of (dmin*m) * S, three MFMA passes
-        constexpr int NS = T::EU / (T::SW ? T::SW : 1);  // sub-blocks per unit (8 or 16)
-        const uint32_t ns_row = K / T::SW;
         half8 bh[2], bl[2];
 #pragma unroll
         for (int rt = 0; rt < 2; rt++) D::template mins<C>(wb + row[rt], h, bh[rt], bl[rt]);
+        const uint8_t* sb = xb + XBYTES;
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
-          const uint32_t t = min(32 * tt + l32, m - 1);
-          const uint32_t idx = u * NS + (NS == 16 ? 8 * h : 0);  // 8 sub-blocks: upper lanes carry zeros
-          const _Float16* sp = a.ins + (size_t)(s0 + t) * ns_row + idx;
-          const half8 sh = *reinterpret_cast<const half8*>(sp);
-          const half8 sl = *reinterpret_cast<const half8*>(sp + (size_t)a.nk * ns_row);
+          // sums 8h'.. of token t (h' = h with 16 sub-blocks; with 8 the upper lanes' B is zero)
+          const uint32_t t = 32 * tt + l32, e = NS == 16 ? h : 0;
+          const half8 sh = *reinterpret_cast<const half8*>(sb + ((0 * kPfTok + t) * (NS / 8) + e) * 16);
+          const half8 sl = *reinterpret_cast<const half8*>(sb + ((1 * kPfTok + t) * (NS / 8) + e) * 16);
 #pragma unroll
           for (int rt = 0; rt < 2; rt++) {
             acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh, bh[rt], acc[rt][tt], 0, 0, 0);
