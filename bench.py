@@ -59,11 +59,6 @@ def make_experts(threads):
     return mats
 
 
-def tm_of(n, packed):
-    """Tokens per pass of the expert kernels for a decode batch (the library's choice)."""
-    return 1 if n <= 1 else 2 if n <= 2 else 4 if (n <= 4 or not packed) else 8
-
-
 def measured_traffic(batch, math, layers):
     """HBM bytes per gate/up launch from the committed counter summary, if it covers this run."""
     try:
@@ -299,7 +294,7 @@ def main():
                                f"batch {a.batch}, {a.layers} HBM copies rotated",
                    "batch": a.batch, "d_model": D, "d_ff": F, "n_experts": NE, "top_k": K, "qtype": "Q4_K",
                    "math": a.math},
-        "roofline": {"bound": "hbm", "kernel": f"k_gu_units<Q4_K, TM={tm_of(a.batch, math == G.MATH_PACKED)}, {a.math}>",
+        "roofline": {"bound": "hbm", "kernel": f"k_gu_units<Q4_K, {a.math} math>",
                      "achieved": r["gateup_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": r["gateup_GBs"] / HBM_PEAK_GBS,
                      "traffic": measured_traffic(a.batch, a.math, a.layers),
