@@ -293,18 +293,26 @@ struct Carved {
   float* d_logits_in;
 };
 
+// Slot rows a call of n tokens may need: n*k routed pairs, or n*ne when the speculative
+// front end may dispatch candidate pairs.
+uint32_t slot_capacity(const Layer& L, uint32_t n) {
+  const uint64_t spec = (uint64_t)n * L.ne;
+  return spec <= kSpecMaxSlots ? (uint32_t)std::max<uint64_t>(spec, (uint64_t)n * L.k) : n * L.k;
+}
+
 size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
   ScratchPlan P;
-  uint64_t nk = (uint64_t)n * L.k;
+  const uint64_t nk = (uint64_t)n * L.k, ns = slot_capacity(L, n);
   size_t o_hs = P.add((size_t)n * L.d * 4), o_out = P.add((size_t)n * L.d * 4);
   size_t o_lin = P.add((size_t)n * L.ne * 4);
   size_t o_ids = P.add(nk * 4), o_w = P.add(nk * 4), o_lg = P.add((size_t)n * L.ne * 4);
   size_t o_xq = P.add((size_t)n * L.d), o_xs = P.add((size_t)n * (L.d / 32) * 4);
   size_t o_x16 = P.add((size_t)n * (L.d / 16) * 4);
   size_t o_off = P.add((L.ne + 1) * 4), o_act = P.add((L.ne + 1) * 4);
-  size_t o_st = P.add(nk * 4), o_sw = P.add(nk * 4), o_sr = P.add(nk * 4), o_so = P.add(nk * 4);
-  size_t o_hq = P.add(nk * L.f), o_hsc = P.add(nk * (L.f / 32) * 4), o_h16 = P.add(nk * (L.f / 16) * 4);
-  size_t o_hf = P.add(nk * L.f * 4), o_y = P.add(kMaxKsg * nk * L.d * 4);
+  size_t o_st = P.add(ns * 4), o_sw = P.add(ns * 4), o_sr = P.add(ns * 4), o_so = P.add(nk * 4);
+  size_t o_hq = P.add(ns * L.f), o_hsc = P.add(ns * (L.f / 32) * 4), o_h16 = P.add(ns * (L.f / 16) * 4);
+  size_t o_hf = P.add(ns * L.f * 4), o_y = P.add(kMaxKsg * ns * L.d * 4);
+  size_t o_cand = P.add((size_t)n * L.ne * 4);
   size_t o_work = P.add((size_t)L.ne * sizeof(ExpertWork));
   const uint32_t pcap = prefill_tiles_cap(n, L.k, L.ne);
   size_t o_pt = P.add((size_t)pcap * 4), o_xh = P.add(2 * nk * L.d * 2), o_hh = P.add(2 * nk * L.f * 2);
@@ -333,6 +341,8 @@ size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
     B.hf = (float*)(base + o_hf);
     B.y = (float*)(base + o_y);
     B.work = (ExpertWork*)(base + o_work);
+    B.nslot = (uint32_t)ns;
+    B.cand = (uint32_t*)(base + o_cand);
     B.ptile = (uint32_t*)(base + o_pt);
     B.ptile_cap = pcap;
     B.xh = (_Float16*)(base + o_xh);
@@ -399,21 +409,41 @@ gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStr
     B.ptile = nullptr;
     B.xh = B.xsh = B.hh = B.hsh = nullptr;
   }
-  if (front_small_ok(D, n)) {
-    HIP_TRY(launch_front_small(D, B, n, quant ? 1 : 0, st));
+  // decode calls that compute their router logits: the expert products start on the
+  // candidate experts, and the exact routing rides along in the gate/up launch
+  const bool spec = !pf && !B.logits_in && spec_ok(D, n);
+  B.spec = spec ? 1u : 0u;
+  if (!spec) B.nslot = n * L.k;
+  RouteArgs ra{};
+  if (spec) {
+    ra.router = D.router;
+    ra.hs = B.hs;
+    ra.logits = B.logits;
+    ra.ids = B.ids;
+    ra.w = B.w;
+    ra.n = n;
+    ra.ne = D.ne;
+    ra.k = D.k;
+    ra.d = D.d;
+    ra.gating = D.gating;
+    ra.sec = std::min(D.d, kRouteSection);
+    ra.tok_done = c->done + 64;
+    HIP_TRY(launch_spec_front(D, B, n, quant ? 1 : 0, st));
+  } else if (front_small_ok(D, n)) {
+    HIP_TRY(launch_front_small(D, B, n, quant ? 1 : 0, true, st));
   } else {
     HIP_TRY(launch_route(D, B, n, st));
     HIP_TRY(launch_dispatch(D, B, n, st));
     if (quant) HIP_TRY(launch_quant_act(B.hs, n, L.d, B.xq, B.xs, B.x16, st));
   }
   if (pf) HIP_TRY(launch_gather_f16(D, B, n, st));
-  const uint32_t ksg = pf ? prefill_ksg(D, B) : down_ksg(D, n);
+  const uint32_t ksg = pf ? prefill_ksg(D, B) : down_ksg(D, n * L.k);
   Timing tm{};
   if (c->timing) {
     tm = take_timing(c);
     HIP_TRY(hipEventRecord(tm.a, st));
   }
-  HIP_TRY(pf ? launch_prefill_gateup(D, B, n, st) : launch_gateup(D, B, n, st));
+  HIP_TRY(pf ? launch_prefill_gateup(D, B, n, st) : launch_gateup(D, B, n, ra, st));
   if (c->timing) HIP_TRY(hipEventRecord(tm.b, st));
   HIP_TRY(pf ? launch_prefill_down(D, B, n, ksg, st) : launch_down(D, B, n, st));
   if (c->timing) {
@@ -522,8 +552,9 @@ gmoe_status gmoe_init(int device, uint64_t slab_bytes, gmoe_ctx** out) {
   c->pinned_bytes = (size_t)64 << 20;
   HIP_TRY(hipHostMalloc((void**)&c->pinned, c->pinned_bytes, hipHostMallocDefault));
   HIP_TRY(hipMalloc(&c->bounce, c->pinned_bytes));
-  HIP_TRY(hipMalloc(&c->done, 256));
-  HIP_TRY(hipMemset(c->done, 0, 256));
+  // [0]: front-end workgroups done; [64 .. 64 + kSpecMaxSlots): per-token routing counters
+  HIP_TRY(hipMalloc(&c->done, (64 + kSpecMaxSlots) * 4));
+  HIP_TRY(hipMemset(c->done, 0, (64 + kSpecMaxSlots) * 4));
   HIP_TRY(hipEventCreateWithFlags(&c->pin_ev[0], hipEventDisableTiming));
   HIP_TRY(hipEventCreateWithFlags(&c->pin_ev[1], hipEventDisableTiming));
   HIP_TRY(hipEventRecord(c->pin_ev[0], c->copy_stream));
@@ -821,6 +852,7 @@ gmoe_status gmoe_matmul(gmoe_ctx* c, uint32_t qt, uint32_t math, const void* w, 
   B.offsets = (uint32_t*)(base + o_off);
   B.active = (uint32_t*)(base + o_act);
   B.y = (float*)(base + o_y);
+  B.nslot = n;
   B.work = (ExpertWork*)(base + o_wk);
   if (uses_int8(math, qt)) {
     B.hq = (int8_t*)(base + o_q);

@@ -514,4 +514,175 @@ __device__ __forceinline__ void pk_block(const uint32_t* w, const int8_t* const*
   else if constexpr (QT == Q2_K) pk_q2k<TM>(w, x, xs, sm, acc, m);
 }
 
+// ---------------------------------------------------------------------------------
+// Ranking and gating
+// ---------------------------------------------------------------------------------
+
+// f32::total_cmp key
+__device__ __forceinline__ int total_key(float f) {
+  int i = __float_as_int(f);
+  return i ^ (int)(((uint32_t)(i >> 31)) >> 1);
+}
+
+// rank order: llama = total_cmp descending, stable (llama/mod.rs:943);
+// router = partial_cmp descending, unordered/equal -> lower id first (router/mod.rs:83-88).
+__device__ __forceinline__ bool ranks_before(bool llama, float a, uint32_t ia, float b, uint32_t ib) {
+  if (llama) {
+    int ka = total_key(a), kb = total_key(b);
+    return ka > kb || (ka == kb && ia < ib);
+  }
+  if (a > b) return true;
+  if (a < b) return false;
+  return ia < ib;
+}
+
+// ---------------------------------------------------------------------------------
+// Gating by one wave (ne <= 64: lane e holds expert e). It computes what gate_block does,
+// with every ordered sum taken lane by lane in index order through readlane, so the
+// arithmetic is the same; maxima, which no order changes, are cross-lane reductions.
+// ---------------------------------------------------------------------------------
+
+__device__ __forceinline__ float lane_f(float v, uint32_t l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)l));
+}
+__device__ __forceinline__ uint32_t lane_u(uint32_t v, uint32_t l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l);
+}
+
+// One token's routing from its logit x (lane e < ne). Lanes r < k receive the r-th
+// ranked expert and its weight. `scratch` holds 2*k words of LDS.
+__device__ void gate_wave(uint32_t gating, uint32_t ne, uint32_t k, float x, uint32_t lane, uint32_t* id_out,
+                          float* w_out, uint32_t* scratch) {
+  const bool llama = gating == 0;
+  float v = x;
+  if (gating == 0 || gating == 2 || gating == 3) {  // softmax over all experts (simd/mod.rs:132-158)
+    float mx = -INFINITY;
+    for (uint32_t e = 0; e < ne; e++) mx = fmaxf(mx, lane_f(x, e));
+    if (isfinite(mx)) v = gm_expf(x - mx);
+    float inv = -1.0f;  // uniform
+    if (isfinite(mx)) {
+      float sum = 0.0f;
+      for (uint32_t e = 0; e < ne; e++) sum += lane_f(v, e);
+      if (isfinite(sum) && sum > 0.0f) inv = fdiv(1.0f, sum);
+    }
+    v = inv < 0.0f ? fdiv(1.0f, (float)ne) : v * inv;
+  }
+  // rank = how many experts come before this one
+  uint32_t r = 0;
+  for (uint32_t o = 0; o < ne; o++)
+    if (o != lane && ranks_before(llama, lane_f(v, o), o, v, lane)) r++;
+  float* tw = reinterpret_cast<float*>(scratch);
+  uint32_t* ti = scratch + k;
+  if (lane < ne && r < k) {
+    tw[r] = v;
+    ti[r] = lane;
+  }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");  // one wave: its DS writes land before these reads
+  float w = lane < k ? tw[lane] : 0.0f;
+  const uint32_t id = lane < k ? ti[lane] : 0u;
+  if (gating == 0) {  // llama/mod.rs:945-949
+    float sum = -0.0f;
+    for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
+    w *= sum > 0.0f ? fdiv(1.0f, sum) : fdiv(1.0f, (float)k);
+  } else if (gating == 1) {  // router/mod.rs:91-97: softmax over the k kept logits
+    float mx = -INFINITY;
+    for (uint32_t i = 0; i < k; i++) mx = fmaxf(mx, lane_f(w, i));
+    if (!isfinite(mx)) {
+      w = fdiv(1.0f, (float)k);
+    } else {
+      w = gm_expf(w - mx);
+      float sum = 0.0f;
+      for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
+      w = (isfinite(sum) && sum > 0.0f) ? w * fdiv(1.0f, sum) : fdiv(1.0f, (float)k);
+    }
+  } else if (gating == 3) {  // router/mod.rs:102-115
+    float sum = -0.0f;
+    for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
+    w = sum > 0.0f ? fdiv(w, sum) : fdiv(1.0f, (float)k);
+  }
+  *id_out = id;
+  *w_out = w;
+}
+
+
+// ---------------------------------------------------------------------------------
+// Exact router logit of one (token, expert) pair by one workgroup of two or more waves,
+// then the token's gating by the last of its ne workgroups. Wave 1 puts the products w*h
+// of a section of d into LDS (two halves: the next section while wave 0 adds the
+// current one); lane 0 of wave 0 runs the chain, the reference's sequential f32 sum from
+// -0.0 (simd/mod.rs:13-16). The logit goes to memory; the workgroup that brings the
+// token's counter to ne (after a release fence) gates all ne logits (gate_wave) and puts
+// the counter back to zero. lds holds 2 * sec floats and 2k words. Every thread of the
+// workgroup must call this.
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ void route_logit(const RouteArgs& r, uint32_t x, float* lds) {
+  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const uint32_t ne = r.ne, d = r.d, sec = r.sec, nsec = (d + sec - 1) / sec;
+  const uint32_t t = x / ne, e = x % ne;
+  const float* hs = r.hs + (size_t)t * d;
+  const float* wr = r.router + (size_t)e * d;
+  uint32_t* scratch = reinterpret_cast<uint32_t*>(lds + 2 * sec);
+  constexpr int kItems = 16;
+  auto produce = [&](uint32_t s) {
+    const uint32_t k0 = s * sec, len4 = min(sec, d - k0) / 4;
+    float* half = lds + (s & 1) * sec;
+    for (uint32_t base = 0; base < len4; base += 64 * kItems) {
+      float4 wv[kItems], xv[kItems];
+#pragma unroll
+      for (int i = 0; i < kItems; i++) {
+        const uint32_t j = base + lane + 64 * i;
+        if (j < len4) {
+          wv[i] = reinterpret_cast<const float4*>(wr + k0)[j];
+          xv[i] = reinterpret_cast<const float4*>(hs + k0)[j];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kItems; i++) {
+        const uint32_t j = base + lane + 64 * i;
+        if (j < len4)
+          reinterpret_cast<float4*>(half)[j] =
+              make_float4(wv[i].x * xv[i].x, wv[i].y * xv[i].y, wv[i].z * xv[i].z, wv[i].w * xv[i].w);
+      }
+    }
+  };
+  if (wave == 1) produce(0);
+  __syncthreads();
+  float acc = -0.0f;
+  for (uint32_t s = 0; s < nsec; s++) {
+    if (wave == 0) {
+      if (lane == 0) {
+        const float4* src = reinterpret_cast<const float4*>(lds + (s & 1) * sec);
+        const uint32_t len4 = min(sec, d - s * sec) / 4;
+        for (uint32_t j = 0; j < len4; j++) {
+          const float4 v = src[j];
+          acc = acc + v.x;
+          acc = acc + v.y;
+          acc = acc + v.z;
+          acc = acc + v.w;
+        }
+      }
+    } else if (wave == 1 && s + 1 < nsec) {
+      produce(s + 1);
+    }
+    __syncthreads();
+  }
+  if (wave != 0) return;
+  if (lane == 0) r.logits[(size_t)t * ne + e] = acc;
+  __threadfence();
+  uint32_t prev = 0;
+  if (lane == 0) prev = atomicAdd(r.tok_done + t, 1u);
+  if (lane_u(prev, 0) != ne - 1) return;
+  __threadfence();
+  const float lg = lane < ne ? r.logits[(size_t)t * ne + lane] : 0.0f;
+  uint32_t id;
+  float w;
+  gate_wave(r.gating, ne, r.k, lg, lane, &id, &w, scratch);
+  if (lane < r.k) {
+    r.ids[(size_t)t * r.k + lane] = id;
+    r.w[(size_t)t * r.k + lane] = w;
+  }
+  if (lane == 0) r.tok_done[t] = 0;
+}
+
 }  // namespace gmoe

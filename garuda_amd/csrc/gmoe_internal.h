@@ -117,7 +117,8 @@ struct ExpertWork {
   uint32_t pad;
 };
 
-// Per-call device buffers. Token-indexed arrays have n rows; slot-indexed ones n*k.
+// Per-call device buffers. Token-indexed arrays have n rows; slot-indexed ones nslot
+// (n*k, or n*ne when the speculative front end may dispatch more than k experts a token).
 struct FwdBufs {
   const float* hs;       // [n][d]
   const float* logits_in;// [n][ne] or null
@@ -149,7 +150,24 @@ struct FwdBufs {
   float* hf;             // [n*k][f]
   float* y;              // [kMaxKsg][n*k][d] partial slices of the down product
   uint32_t* done;        // [1] workgroups of the front end that have finished; 0 between calls
+  uint32_t nslot;        // rows of the slot-indexed arrays; y slices are nslot*d apart
+  uint32_t* cand;        // [n][ne] speculative front end: each token's candidate experts, ~0u-padded
+  uint32_t spec;         // 1: slots hold candidate pairs; the combine finds (token, expert) by search
 };
+
+// Exact routing carried by the gate/up launch of a speculative decode call: one extra
+// workgroup per (token, expert) runs route_logit (gmoe_device.h). n = 0: none.
+struct RouteArgs {
+  const float* router;  // [ne][d]
+  const float* hs;      // [n][d]
+  float* logits;        // [n][ne]
+  uint32_t* ids;        // [n][k]
+  float* w;             // [n][k]
+  uint32_t* tok_done;   // [n] logits finished per token; 0 between calls
+  uint32_t n, ne, k, d, gating, sec;
+};
+constexpr uint32_t kRouteSection = 4096;  // values of d per LDS half in route_logit
+inline uint32_t route_logit_lds(uint32_t k, uint32_t sec) { return (2 * sec + 2 * k) * 4; }
 
 struct LayerDev {
   uint32_t d, f, ne, k, gating, combine, math;
@@ -164,7 +182,8 @@ constexpr uint32_t kMaxKsg = 8;
 constexpr int kDnKS = 2;
 
 // Expert products of one block type (gmoe_units.hip, built once per type).
-template <int QT> hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+template <int QT> hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra,
+                                          hipStream_t st);
 template <int QT> hipError_t units_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
 
 // Prefill products (f32 math) on MFMA over token tiles of kPfTok (gmoe_prefill.hip,
@@ -196,8 +215,16 @@ hipError_t launch_dispatch(const LayerDev& L, const FwdBufs& B, uint32_t n, hipS
 // Route + gate + int8 activation quantiser (when quant) + dispatch in one launch, for
 // small decode batches (front_small_ok).
 bool front_small_ok(const LayerDev& L, uint32_t n);
-hipError_t launch_front_small(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st);
-hipError_t launch_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+// dispatch = false: logits, ids and weights only (the exact half of the speculative front end)
+hipError_t launch_front_small(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, bool dispatch,
+                              hipStream_t st);
+// Speculative front end: router logits by a parallel dot with a rigorous bound on their
+// distance to the sequential dot, every expert that can be among a token's top k, the
+// int8 activation quantiser, and the dispatch of all (token, candidate) pairs.
+constexpr uint32_t kSpecMaxSlots = 512;
+bool spec_ok(const LayerDev& L, uint32_t n);
+hipError_t launch_spec_front(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st);
+hipError_t launch_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st);
 hipError_t launch_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 hipError_t launch_combine(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
 // Prefill path: whether it applies (f32 math, at least kPfMinSlots slots, supported
@@ -207,8 +234,9 @@ hipError_t launch_gather_f16(const LayerDev& L, const FwdBufs& B, uint32_t n, hi
 hipError_t launch_prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 hipError_t launch_prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
 uint32_t prefill_ksg(const LayerDev& L, const FwdBufs& B);
-// Number of partial slices launch_down writes for this layer and batch (1 = y is final).
-uint32_t down_ksg(const LayerDev& L, uint32_t n);
+// Number of partial slices launch_down writes for this layer and about `pairs` routed
+// (token, expert) pairs (1 = y is final).
+uint32_t down_ksg(const LayerDev& L, uint32_t pairs);
 // out[i] = parts[i] + parts[count + i] + ... over ksg slices, in slice order.
 hipError_t launch_reduce_parts(const float* parts, uint32_t ksg, size_t count, float* out, hipStream_t st);
 // Rows [r0, r0 + nrows) of a packed matrix (raw rows of row_bytes each, r0 a multiple of

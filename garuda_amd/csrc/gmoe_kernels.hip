@@ -106,24 +106,6 @@ hipError_t launch_quant_act(const float* x, uint32_t n_tok, uint32_t K, int8_t* 
 // multiply and add, left to right, Iterator::sum starting at -0.0).
 // ---------------------------------------------------------------------------------
 
-// f32::total_cmp key
-__device__ __forceinline__ int total_key(float f) {
-  int i = __float_as_int(f);
-  return i ^ (int)(((uint32_t)(i >> 31)) >> 1);
-}
-
-// rank order: llama = total_cmp descending, stable (llama/mod.rs:943);
-// router = partial_cmp descending, unordered/equal -> lower id first (router/mod.rs:83-88).
-__device__ __forceinline__ bool ranks_before(bool llama, float a, uint32_t ia, float b, uint32_t ib) {
-  if (llama) {
-    int ka = total_key(a), kb = total_key(b);
-    return ka > kb || (ka == kb && ia < ib);
-  }
-  if (a > b) return true;
-  if (a < b) return false;
-  return ia < ib;
-}
-
 constexpr int kRouteThreads = 256;
 
 // Gating of `tpb` tokens whose router logits sit in lg[tpb][ne] (LDS), for tokens
@@ -333,74 +315,9 @@ __global__ void __launch_bounds__(256) k_dispatch(LayerDev L, FwdBufs B, uint32_
 }
 
 // ---------------------------------------------------------------------------------
-// Gating and dispatch by one wave (ne <= 64: lane e holds expert e). They compute what
-// gate_block and dispatch_block do, with every ordered sum taken lane by lane in index
-// order through readlane, so the arithmetic is the same; maxima and counts, which no
-// order changes, are cross-lane reductions.
+// Dispatch by one wave (ne <= 64: lane e holds expert e); its counts are cross-lane
+// reductions, its positions running sums in index order.
 // ---------------------------------------------------------------------------------
-
-__device__ __forceinline__ float lane_f(float v, uint32_t l) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)l));
-}
-__device__ __forceinline__ uint32_t lane_u(uint32_t v, uint32_t l) {
-  return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l);
-}
-
-// One token's routing from its logit x (lane e < ne). Lanes r < k receive the r-th
-// ranked expert and its weight. `scratch` holds 2*k words of LDS.
-__device__ void gate_wave(uint32_t gating, uint32_t ne, uint32_t k, float x, uint32_t lane, uint32_t* id_out,
-                          float* w_out, uint32_t* scratch) {
-  const bool llama = gating == 0;
-  float v = x;
-  if (gating == 0 || gating == 2 || gating == 3) {  // softmax over all experts (simd/mod.rs:132-158)
-    float mx = -INFINITY;
-    for (uint32_t e = 0; e < ne; e++) mx = fmaxf(mx, lane_f(x, e));
-    if (isfinite(mx)) v = gm_expf(x - mx);
-    float inv = -1.0f;  // uniform
-    if (isfinite(mx)) {
-      float sum = 0.0f;
-      for (uint32_t e = 0; e < ne; e++) sum += lane_f(v, e);
-      if (isfinite(sum) && sum > 0.0f) inv = fdiv(1.0f, sum);
-    }
-    v = inv < 0.0f ? fdiv(1.0f, (float)ne) : v * inv;
-  }
-  // rank = how many experts come before this one
-  uint32_t r = 0;
-  for (uint32_t o = 0; o < ne; o++)
-    if (o != lane && ranks_before(llama, lane_f(v, o), o, v, lane)) r++;
-  float* tw = reinterpret_cast<float*>(scratch);
-  uint32_t* ti = scratch + k;
-  if (lane < ne && r < k) {
-    tw[r] = v;
-    ti[r] = lane;
-  }
-  __builtin_amdgcn_wave_barrier();
-  asm volatile("" ::: "memory");  // one wave: its DS writes land before these reads
-  float w = lane < k ? tw[lane] : 0.0f;
-  const uint32_t id = lane < k ? ti[lane] : 0u;
-  if (gating == 0) {  // llama/mod.rs:945-949
-    float sum = -0.0f;
-    for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
-    w *= sum > 0.0f ? fdiv(1.0f, sum) : fdiv(1.0f, (float)k);
-  } else if (gating == 1) {  // router/mod.rs:91-97: softmax over the k kept logits
-    float mx = -INFINITY;
-    for (uint32_t i = 0; i < k; i++) mx = fmaxf(mx, lane_f(w, i));
-    if (!isfinite(mx)) {
-      w = fdiv(1.0f, (float)k);
-    } else {
-      w = gm_expf(w - mx);
-      float sum = 0.0f;
-      for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
-      w = (isfinite(sum) && sum > 0.0f) ? w * fdiv(1.0f, sum) : fdiv(1.0f, (float)k);
-    }
-  } else if (gating == 3) {  // router/mod.rs:102-115
-    float sum = -0.0f;
-    for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
-    w = sum > 0.0f ? fdiv(w, sum) : fdiv(1.0f, (float)k);
-  }
-  *id_out = id;
-  *w_out = w;
-}
 
 // Stable counting sort of the nk (token, rank) pairs by expert: members[e] of
 // llama/mod.rs:967-972 laid end to end, as dispatch_block makes it. pair(p, &id, &w)
@@ -408,7 +325,7 @@ __device__ void gate_wave(uint32_t gating, uint32_t ne, uint32_t k, float x, uin
 // and lane e keeps expert e's count, then its next free slot.
 template <class Pair>
 __device__ void dispatch_wave(const FwdBufs& B, const uint8_t* const* eptr, uint32_t ne, uint32_t k, uint32_t nk,
-                              uint32_t lane, Pair pair) {
+                              uint32_t lane, Pair pair, bool meta = true) {
   const uint64_t below = (1ull << lane) - 1ull;
   uint32_t cnt = 0;
   for (uint32_t c0 = 0; c0 < nk; c0 += 64) {
@@ -469,11 +386,13 @@ __device__ void dispatch_wave(const FwdBufs& B, const uint8_t* const* eptr, uint
       if (id == e) pos = lane_u(off, e) + (uint32_t)__popcll(m & below);
       if (lane == e) off += (uint32_t)__popcll(m);
     }
-    if (p < nk) {
+    if (id < ne) {  // pairs with id ~0u (no expert) are skipped
       B.slot_tok[pos] = p / k;
-      B.slot_w[pos] = w;
-      B.slot_rank[pos] = p % k;
-      B.slot_of[p] = pos;
+      if (meta) {
+        B.slot_w[pos] = w;
+        B.slot_rank[pos] = p % k;
+        B.slot_of[p] = pos;
+      }
     }
   }
 }
@@ -506,7 +425,8 @@ static inline uint32_t front_section(uint32_t ne, uint32_t d) {
   return sec < d ? sec : d;
 }
 
-__global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, uint32_t n, int quant, uint32_t sec) {
+__global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, uint32_t n, int quant, int dispatch,
+                                                          uint32_t sec) {
   extern __shared__ float fs[];
   const uint32_t ne = L.ne, d = L.d, k = L.k, t = blockIdx.x, row = sec + 4;  // padded row of one expert
   float* prod = fs;                                                 // [2][ne][row]
@@ -612,6 +532,7 @@ __global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, 
     B.ids[(size_t)t * k + lane] = id;
     B.w[(size_t)t * k + lane] = w;
   }
+  if (!dispatch) return;
   if (n == 1) {  // the only workgroup: pair p (< k) is rank p, which lane p holds
     dispatch_wave(B, L.eptr, ne, k, k, lane, [&](uint32_t, uint32_t* pid, float* pw) {
       *pid = id;
@@ -637,13 +558,161 @@ bool front_small_ok(const LayerDev& L, uint32_t n) {
   return n >= 1 && L.ne <= (uint32_t)kFrontExperts && L.k <= 32 && L.d % 128 == 0;
 }
 
-hipError_t launch_front_small(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st) {
+hipError_t launch_front_small(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, bool dispatch,
+                              hipStream_t st) {
   const uint32_t sec = front_section(L.ne, L.d);
   const size_t shm = ((size_t)2 * L.ne * (sec + 4) + 2 * L.k) * 4;
   static const bool attr =
       hipFuncSetAttribute((const void*)k_front, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
   (void)attr;
-  hipLaunchKernelGGL(k_front, dim3(n), dim3(kFrontThreads), shm, st, L, B, n, quant, sec);
+  hipLaunchKernelGGL(k_front, dim3(n), dim3(kFrontThreads), shm, st, L, B, n, quant, dispatch ? 1 : 0, sec);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------
+// Speculative front end (decode). The exact router logits are d dependent adds per
+// (token, expert) (simd/mod.rs:13-16), a chain of ~10 us that the expert products need
+// only to know which experts to stream. So the decode call runs k_front without its
+// dispatch on a side stream, for the exact logits, ids and weights the combine uses, and
+// this kernel on the call's stream:
+//
+//  * logit L~_e: the same rounded products w*h summed as d/64-long lane sums and a
+//    64-lane tree. With S the exact sum of the rounded products and A = sum |products|,
+//    recursive summation gives |L_seq - S| <= g(d-1) A and the tree |L~ - S| <= g(d/64+6) A
+//    (g(m) = m u / (1 - m u), u = 2^-24), so |L~ - L_seq| <= delta_e.
+//  * candidates: expert e is left out only when at least k others certainly rank before
+//    it, L~_j - delta_j > L~_e + delta_e + eps_e; eps_e keeps their probabilities apart
+//    after expf and the normalisation, so the exact order puts them first whatever the
+//    tie rule. Non-finite logits, or fewer than k experts safely above expf's underflow,
+//    make every expert a candidate. The exact top k is therefore a subset.
+//  * the int8 quantiser of the token's activations (packed math), and the dispatch of the
+//    (token, candidate) pairs by the last workgroup, as k_front does for the routed ones.
+//
+// The expert products then run on the candidate pairs (almost always exactly the routed
+// ones), and the combine picks each routed (token, expert) pair's slot by search.
+// ---------------------------------------------------------------------------------
+
+constexpr int kSpecThreads = 512;
+
+__device__ __forceinline__ double sum_gamma(double m) {
+  const double u = 0x1p-24;
+  return m * u / (1.0 - m * u);
+}
+
+__global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs B, uint32_t n, int quant) {
+  __shared__ float lt[kFrontExperts], la[kFrontExperts];
+  __shared__ uint32_t cl[kFrontExperts];
+  const uint32_t ne = L.ne, d = L.d, k = L.k, t = blockIdx.x;
+  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const float* hs = B.hs + (size_t)t * d;
+  const float4* xr = reinterpret_cast<const float4*>(hs);
+  // wave w: experts w, w + 8, ...; lane j: float4 columns j, j + 64, ..., 16 loads in flight
+  constexpr int kB = 16;
+  const uint32_t n4 = d / 4;
+  for (uint32_t e = wave; e < ne; e += kSpecThreads / 64) {
+    const float4* wr = reinterpret_cast<const float4*>(L.router + (size_t)e * d);
+    float sm = 0.0f, ab = 0.0f;
+    for (uint32_t j0 = 0; j0 < n4; j0 += 64 * kB) {
+      float4 wv[kB], xv[kB];
+#pragma unroll
+      for (int i = 0; i < kB; i++) {
+        const uint32_t j = j0 + lane + 64 * i;
+        if (j < n4) {
+          wv[i] = wr[j];
+          xv[i] = xr[j];
+        } else {
+          wv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          xv[i] = wv[i];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kB; i++) {
+        const float p0 = wv[i].x * xv[i].x, p1 = wv[i].y * xv[i].y, p2 = wv[i].z * xv[i].z, p3 = wv[i].w * xv[i].w;
+        sm = sm + p0; sm = sm + p1; sm = sm + p2; sm = sm + p3;
+        ab = ab + fabsf(p0); ab = ab + fabsf(p1); ab = ab + fabsf(p2); ab = ab + fabsf(p3);
+      }
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+      sm += __shfl_xor(sm, o, 64);
+      ab += __shfl_xor(ab, o, 64);
+    }
+    if (lane == 0) {
+      lt[e] = sm;
+      la[e] = ab;
+    }
+  }
+  if (quant) {
+    const uint32_t nblk = d / 32;
+    for (uint32_t b = tid; b < nblk; b += kSpecThreads) {
+      float v[32];
+      const float4* src = reinterpret_cast<const float4*>(hs + (size_t)b * 32);
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        float4 t4 = src[i];
+        v[4 * i] = t4.x; v[4 * i + 1] = t4.y; v[4 * i + 2] = t4.z; v[4 * i + 3] = t4.w;
+      }
+      const size_t gb = (size_t)t * nblk + b;
+      quant32(v, B.xq + gb * 32, B.xs + gb, B.x16 + 2 * gb);
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // candidate test, lane e < ne, in double
+  // each product passes through at most d/64 + 4*kB lane additions (zero padding included)
+  // and 6 tree levels
+  const double m_tree = (double)(d / 64 + 4 * kB + 7), m_seq = (double)d;
+  const bool valid = lane < ne;
+  const double Lt = valid ? (double)lt[lane] : 0.0;
+  const double A = valid ? (double)la[lane] / (1.0 - sum_gamma(m_tree)) : 0.0;
+  const double delta = (sum_gamma(m_seq) + sum_gamma(m_tree)) * A * (1.0 + 0x1p-20);
+  const bool fin = !valid || (isfinite(Lt) && isfinite(delta));
+  const double lo = Lt - delta, hi = Lt + delta;
+  double maxhi = valid ? hi : -INFINITY;
+  for (int o = 32; o >= 1; o >>= 1) maxhi = fmax(maxhi, __shfl_xor(maxhi, o, 64));
+  const bool all_fin = __ballot(!fin) == 0ull;
+  // experts certainly clear of expf's underflow relative to the largest logit
+  const uint32_t safe = (uint32_t)__popcll(__ballot(valid && lo - maxhi > -80.0));
+  const bool all = !all_fin || (L.gating != 1 && safe < k);
+  const double eps = 4e-6 * (1.0 + fabs(Lt) + fabs(maxhi));
+  uint32_t above = 0;
+  for (uint32_t j = 0; j < ne; j++) {
+    const double loj = __shfl(lo, (int)j, 64);
+    if (j != lane && loj > hi + eps) above++;
+  }
+  const bool cand = valid && (all || above < k);
+  const uint64_t cm = __ballot(cand);
+  const uint32_t pos = (uint32_t)__popcll(cm & ((1ull << lane) - 1ull)), nc = (uint32_t)__popcll(cm);
+  if (cand) cl[pos] = lane;
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");  // one wave: its DS writes land before these reads
+  const uint32_t my = lane < nc ? cl[lane] : ~0u;
+  if (lane < ne) B.cand[(size_t)t * ne + lane] = my;
+  if (n == 1) {
+    dispatch_wave(B, L.eptr, ne, ne, ne, lane, [&](uint32_t, uint32_t* pid, float* pw) {
+      *pid = my;
+      *pw = 0.0f;
+    }, false);
+    return;
+  }
+  __threadfence();
+  uint32_t prev = 0;
+  if (lane == 0) prev = atomicAdd(B.done, 1u);
+  if (lane_u(prev, 0) == n - 1) {
+    __threadfence();
+    dispatch_wave(B, L.eptr, ne, ne, n * ne, lane, [&](uint32_t p, uint32_t* pid, float* pw) {
+      *pid = B.cand[p];
+      *pw = 0.0f;
+    }, false);
+    if (lane == 0) *B.done = 0;
+  }
+}
+
+bool spec_ok(const LayerDev& L, uint32_t n) {
+  return front_small_ok(L, n) && (uint64_t)n * L.ne <= kSpecMaxSlots && L.k <= L.ne;
+}
+
+hipError_t launch_spec_front(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st) {
+  hipLaunchKernelGGL(k_spec_front, dim3(n), dim3(kSpecThreads), 0, st, L, B, n, quant);
   return hipGetLastError();
 }
 
@@ -714,7 +783,7 @@ __global__ void __launch_bounds__(256) k_combine(LayerDev L, FwdBufs B, uint32_t
   const uint32_t t = blockIdx.y, k = L.k, d = L.d;
   const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n || c >= d) return;
-  const size_t part = (size_t)n * k * d;
+  const size_t part = (size_t)B.nslot * d;
   uint32_t order[32];  // top_k <= 32, checked at registration
   for (uint32_t i = 0; i < k; i++) order[i] = i;
   if (L.combine == 0) {
@@ -731,11 +800,32 @@ __global__ void __launch_bounds__(256) k_combine(LayerDev L, FwdBufs B, uint32_t
   float acc = 0.0f;
   for (uint32_t i = 0; i < k; i++) {
     uint32_t r = order[i];
-    uint32_t slot = B.slot_of[(size_t)t * k + r];
     float wv = B.w[(size_t)t * k + r];
-    const float* yp = B.y + (size_t)slot * d + c;
-    float yv = yp[0];
-    for (uint32_t g = 1; g < ksg; g++) yv += yp[g * part];
+    float yv;
+    if (B.spec) {
+      // the (token, expert) pair among the expert's candidate slots, which are in token
+      // order; a pair the candidates missed gives NaN (the candidate sets are supersets)
+      const uint32_t e = B.ids[(size_t)t * k + r];
+      uint32_t lo = B.offsets[e], hi = B.offsets[e + 1];
+      const uint32_t end = hi;
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi) / 2;
+        if (B.slot_tok[mid] < t) lo = mid + 1;
+        else hi = mid;
+      }
+      if (lo < end && B.slot_tok[lo] == t) {
+        const float* yp = B.y + (size_t)lo * d + c;
+        yv = yp[0];
+        for (uint32_t g = 1; g < ksg; g++) yv += yp[g * part];
+      } else {
+        yv = __int_as_float(0x7fc00000);
+      }
+    } else {
+      const uint32_t slot = B.slot_of[(size_t)t * k + r];
+      const float* yp = B.y + (size_t)slot * d + c;
+      yv = yp[0];
+      for (uint32_t g = 1; g < ksg; g++) yv += yp[g * part];
+    }
     acc = acc + yv * wv;
   }
   B.out[(size_t)t * d + c] = acc;
@@ -765,18 +855,18 @@ hipError_t launch_reduce_parts(const float* parts, uint32_t ksg, size_t count, f
 
 // K groups of the down product: enough workgroups for two waves per SIMD (1024
 // workgroups of kDnKS = 2 waves on 256 CUs), each wave keeping at least 4 units.
-uint32_t down_ksg(const LayerDev& L, uint32_t n) {
+uint32_t down_ksg(const LayerDev& L, uint32_t pairs) {
   Unit un;
   if (!unit_of(L.qt_down, &un)) return 1;
-  const uint32_t tiles = (L.d + kTileRows - 1) / kTileRows, ymax = min(L.ne, n * L.k);
+  const uint32_t tiles = (L.d + kTileRows - 1) / kTileRows, ymax = min(L.ne, pairs);
   const uint32_t ksg = (1024 + tiles * ymax - 1) / (tiles * ymax);
   const uint32_t cap = max(1u, row_units(un, L.f) / (kDnKS * 4));
   return max(1u, min(min(ksg, cap), kMaxKsg));
 }
 
-hipError_t launch_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+hipError_t launch_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
   switch (L.qt_gate) {
-#define GU(T) case T: return units_gateup<T>(L, B, n, st);
+#define GU(T) case T: return units_gateup<T>(L, B, n, ra, st);
     GU(Q4_K) GU(Q5_K) GU(Q6_K) GU(Q3_K) GU(Q2_K) GU(Q8_0) GU(Q4_0) GU(F16) GU(F32)
 #undef GU
   }
@@ -873,7 +963,7 @@ uint32_t prefill_ksg(const LayerDev& L, const FwdBufs& B) {
 }
 
 hipError_t launch_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
-  const uint32_t ksg = down_ksg(L, n);
+  const uint32_t ksg = down_ksg(L, n * L.k);
   switch (L.qt_down) {
 #define DN(T) case T: return units_down<T>(L, B, n, ksg, st);
     DN(Q4_K) DN(Q5_K) DN(Q6_K) DN(Q3_K) DN(Q2_K) DN(Q8_0) DN(Q4_0) DN(F16) DN(F32)

@@ -223,20 +223,36 @@ __device__ __forceinline__ void unit_tokens(const uint32_t* w, const uint8_t* ac
 // quant::matmul's row dots term for term (quant/mod.rs:266-279). h = silu(g)*u; under
 // packed math h is then quantised per 32 rows for the down product
 // (quant/mod.rs:331-345). grid.x = row tiles, grid.y = active-expert slot.
+//
+// With ra.n > 0 (speculative decode) row 0 of the grid is the exact routing instead:
+// workgroup x < n*ne runs route_logit for token x / ne, expert x % ne, and the experts
+// are rows 1...
 template <int QT, bool PACKED>
 __global__ void __launch_bounds__(128, 2)
-k_gu_units(const ExpertWork* __restrict__ work, const uint32_t* __restrict__ slot_tok, uint32_t f, uint32_t d,
-           uint32_t mt, const int8_t* __restrict__ xq,
+k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __restrict__ slot_tok, uint32_t f,
+           uint32_t d, uint32_t mt, const int8_t* __restrict__ xq,
            const float* __restrict__ xs, const int32_t* __restrict__ x16, const float* __restrict__ hs,
-           int8_t* __restrict__ hq, float* __restrict__ hsc, int32_t* __restrict__ h16, float* __restrict__ hf) {
+           int8_t* __restrict__ hq, float* __restrict__ hsc, int32_t* __restrict__ h16, float* __restrict__ hf,
+           RouteArgs ra) {
   constexpr int U = UT_<QT>::U;
   extern __shared__ uint4 dsm[];
+  if (ra.n) {
+    if (blockIdx.y == 0) {
+      if (blockIdx.x < ra.n * ra.ne) route_logit(ra, blockIdx.x, reinterpret_cast<float*>(dsm));
+      return;
+    }
+  }
   float* accs = reinterpret_cast<float*>(dsm);                 // [2][mt][64] running row sums
   uint32_t* rows = reinterpret_cast<uint32_t*>(accs + 2 * mt * 64);  // [mt] token of each chunk member
   uint8_t* acts = reinterpret_cast<uint8_t*>(rows + ((mt + 3) & ~3u));
-  const ExpertWork* W = work + blockIdx.y;  // field by field: scalar loads
+  if (blockIdx.x * kTileRows >= f) return;  // (the routing row may widen the grid)
+  // active experts y0, y0 + ny, ... (the grid is sized for the usual count; rare extra
+  // candidates are taken by the same workgroups)
+  const uint32_t y0 = blockIdx.y - (ra.n ? 1 : 0), ny = gridDim.y - (ra.n ? 1 : 0);
+  for (uint32_t a = y0; a < ne; a += ny) {
+  const ExpertWork* W = work + a;  // field by field: scalar loads
   const uint32_t m_all = W->m;
-  if (m_all == 0) return;
+  if (m_all == 0) break;
   const uint32_t s0 = W->s0;
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const uint32_t r0 = blockIdx.x * kTileRows;
@@ -266,6 +282,7 @@ k_gu_units(const ExpertWork* __restrict__ work, const uint32_t* __restrict__ slo
     }
     __syncthreads();  // the sums and the staged activations are reused by the next chunk
   }
+  }
 }
 
 // Down: the row's units are split over gridDim.y workgroups of KS waves each. A
@@ -274,7 +291,7 @@ k_gu_units(const ExpertWork* __restrict__ work, const uint32_t* __restrict__ slo
 // grid.x = row tiles of d_model, grid.y = K groups, grid.z = active-expert slot.
 template <int QT, bool PACKED, int KS>
 __global__ void __launch_bounds__(64 * KS, 2)
-k_dn_units(const ExpertWork* __restrict__ work, uint32_t f, uint32_t d, uint32_t mt, uint32_t part_stride,
+k_dn_units(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32_t d, uint32_t mt, uint32_t part_stride,
            const int8_t* __restrict__ hq, const float* __restrict__ hsc, const int32_t* __restrict__ h16,
            const float* __restrict__ hf, float* __restrict__ ypart) {
   constexpr int U = UT_<QT>::U, EU = UT_<QT>::EU;
@@ -282,9 +299,10 @@ k_dn_units(const ExpertWork* __restrict__ work, uint32_t f, uint32_t d, uint32_t
   float* accs = reinterpret_cast<float*>(dsm);  // [KS][mt][64]
   uint32_t* rows = reinterpret_cast<uint32_t*>(accs + KS * mt * 64);  // [mt] slot of each chunk member
   uint8_t* acts = reinterpret_cast<uint8_t*>(rows + ((mt + 3) & ~3u));
-  const ExpertWork* W = work + blockIdx.z;  // field by field: scalar loads
+  for (uint32_t a = blockIdx.z; a < ne; a += gridDim.z) {  // active experts, as in k_gu_units
+  const ExpertWork* W = work + a;  // field by field: scalar loads
   const uint32_t m_all = W->m;
-  if (m_all == 0) return;
+  if (m_all == 0) break;
   const uint32_t s0 = W->s0;
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const uint32_t r0 = blockIdx.x * kTileRows;
@@ -319,6 +337,7 @@ k_dn_units(const ExpertWork* __restrict__ work, uint32_t f, uint32_t d, uint32_t
     }
     __syncthreads();
   }
+  }
 }
 
 // ---------------------------------------------------------------------------------
@@ -341,15 +360,18 @@ static uint32_t chunk_tokens(uint32_t n, uint32_t per_token_bytes) {
 }
 
 template <int QT, bool PACKED>
-static hipError_t go_gu(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+static hipError_t go_gu(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
   const uint32_t per = 2 * 64 * 4 + ActLds<QT, PACKED>::per_token(L.d) + 4;
   const uint32_t mt = chunk_tokens(n, per + 16);
   if (mt == 0) return hipErrorInvalidValue;
   static const bool once = allow_lds(k_gu_units<QT, PACKED>);
   (void)once;
-  const dim3 g((L.f + kTileRows - 1) / kTileRows, min(L.ne, n * L.k));
-  hipLaunchKernelGGL((k_gu_units<QT, PACKED>), g, dim3(128), mt * per + 16, st, B.work, B.slot_tok, L.f, L.d, mt, B.xq,
-                     B.xs, B.x16, B.hs, B.hq, B.hsc, B.h16, B.hf);
+  const uint32_t tiles = (L.f + kTileRows - 1) / kTileRows;
+  uint32_t lds = mt * per + 16;
+  if (ra.n) lds = max(lds, route_logit_lds(ra.k, ra.sec));
+  const dim3 g(max(tiles, ra.n * ra.ne), min(L.ne, n * L.k) + (ra.n ? 1 : 0));
+  hipLaunchKernelGGL((k_gu_units<QT, PACKED>), g, dim3(128), lds, st, B.work, L.ne, B.slot_tok, L.f, L.d, mt, B.xq,
+                     B.xs, B.x16, B.hs, B.hq, B.hsc, B.h16, B.hf, ra);
   return hipGetLastError();
 }
 
@@ -363,17 +385,17 @@ static hipError_t go_dn(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_
   static const bool once = allow_lds(k_dn_units<QT, PACKED, kDnKS>);
   (void)once;
   const dim3 g((L.d + kTileRows - 1) / kTileRows, ksg, min(L.ne, n * L.k));
-  hipLaunchKernelGGL((k_dn_units<QT, PACKED, kDnKS>), g, dim3(64 * kDnKS), mt * per + 16, st, B.work, L.f, L.d, mt,
-                     n * L.k * L.d, B.hq, B.hsc, B.h16, B.hf, B.y);
+  hipLaunchKernelGGL((k_dn_units<QT, PACKED, kDnKS>), g, dim3(64 * kDnKS), mt * per + 16, st, B.work, L.ne, L.f, L.d, mt,
+                     B.nslot * L.d, B.hq, B.hsc, B.h16, B.hf, B.y);
   return hipGetLastError();
 }
 
 template <int QT>
-hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
   if constexpr (has_int8_kernel(QT)) {
-    if (L.math == 0) return go_gu<QT, true>(L, B, n, st);
+    if (L.math == 0) return go_gu<QT, true>(L, B, n, ra, st);
   }
-  return go_gu<QT, false>(L, B, n, st);
+  return go_gu<QT, false>(L, B, n, ra, st);
 }
 
 template <int QT>
@@ -384,7 +406,7 @@ hipError_t units_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t 
   return go_dn<QT, false>(L, B, n, ksg, st);
 }
 
-template hipError_t units_gateup<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, hipStream_t);
+template hipError_t units_gateup<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, const RouteArgs&, hipStream_t);
 template hipError_t units_down<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, uint32_t, hipStream_t);
 
 }  // namespace gmoe

@@ -153,7 +153,7 @@ def oracle_layer(d, f, ne, k, router, mats, qts, math, gating=0, combine=0):
 
 
 def check_layer(dev, d, f, ne, k, qts, ns, math, gating=0, combine=0, seed=0, logits_scale=None, split=False,
-                tie_logits=False, zipf=False, sample=None):
+                tie_logits=False, zipf=False, sample=None, router_fn=None):
     """zipf: tokens and router biased along one shared direction so the expert load
     follows Zipf(1.1); sample: compare only this many tokens (spread over the batch)
     with the oracle, which then runs on those tokens alone."""
@@ -162,6 +162,8 @@ def check_layer(dev, d, f, ne, k, qts, ns, math, gating=0, combine=0, seed=0, lo
     if zipf:
         u = M.skew_direction(seed + 1, d)
         router = M.skew_router(router, ne, d, u)
+    if router_fn is not None:
+        router = np.ascontiguousarray(router_fn(router.reshape(ne, d).copy()).astype(np.float32).reshape(-1))
     gpu_mats = dict(mats)
     if split:
         for name, rows, cols in (("gate", f, d), ("up", f, d), ("down", d, f)):
@@ -257,6 +259,27 @@ def test_prefill_c3_shape_sampled(dev):
     # d 4096, f 14336, 8 experts, top-2, Q4_K, 512 Zipf-skewed tokens;
     # all 512 go through the GPU, 24 of them are checked against the oracle
     check_layer(dev, 4096, 14336, 8, 2, (G.Q4_K,) * 3, (512,), G.MATH_F32, seed=31, zipf=True, sample=24)
+
+
+# Decode calls that compute their logits dispatch every expert that can be among a
+# token's top k under a rigorous bound on the parallel logit, while the exact routing runs
+# beside; the combine uses the exact ids and weights. Rows that tie exactly or within
+# rounding force extra candidates; a router scaled so that most probabilities underflow
+# makes every expert a candidate.
+@pytest.mark.parametrize("gating", [G.GATING_LLAMA, G.GATING_MIXTRAL])
+def test_speculative_candidates_cover_near_ties(dev, gating):
+    def near_ties(R):
+        R[2] = R[1]                                   # exact tie: lower id first
+        R[4] = R[3] * np.float32(1 + 2 ** -20)        # within the parallel sum's error
+        R[6] = R[5] + np.float32(1e-7)
+        return R
+    check_layer(dev, 4096, 512, 8, 2, (G.Q4_K,) * 3, (1, 2, 8, 33), G.MATH_PACKED, gating, seed=9,
+                router_fn=near_ties)
+
+
+def test_speculative_all_candidates_when_probabilities_underflow(dev):
+    check_layer(dev, 256, 512, 8, 2, (G.Q4_K,) * 3, (1, 5, 16), G.MATH_PACKED, seed=10,
+                router_fn=lambda R: R * np.float32(400.0))
 
 
 def test_split_layout_matches_stacked(dev):
