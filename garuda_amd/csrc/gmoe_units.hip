@@ -224,9 +224,9 @@ __device__ __forceinline__ void unit_tokens(const uint32_t* w, const uint8_t* ac
 // packed math h is then quantised per 32 rows for the down product
 // (quant/mod.rs:331-345). grid.x = row tiles, grid.y = active-expert slot.
 //
-// With ra.n > 0 (speculative decode) row 0 of the grid is the exact routing instead:
-// workgroup x < n*ne runs route_logit for token x / ne, expert x % ne, and the experts
-// are rows 1...
+// With ra.n > 0 (speculative decode) the last row of the grid is the exact routing
+// instead: workgroup x < n*ne runs route_logit for token x / ne, expert x % ne. The
+// dispatcher starts it with the last wave of expert workgroups, whose tail hides it.
 template <int QT, bool PACKED>
 __global__ void __launch_bounds__(128, 2)
 k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __restrict__ slot_tok, uint32_t f,
@@ -237,7 +237,7 @@ k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __r
   constexpr int U = UT_<QT>::U;
   extern __shared__ uint4 dsm[];
   if (ra.n) {
-    if (blockIdx.y == 0) {
+    if (blockIdx.y == gridDim.y - 1) {
       if (blockIdx.x < ra.n * ra.ne) route_logit(ra, blockIdx.x, reinterpret_cast<float*>(dsm));
       return;
     }
@@ -248,7 +248,7 @@ k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __r
   if (blockIdx.x * kTileRows >= f) return;  // (the routing row may widen the grid)
   // active experts y0, y0 + ny, ... (the grid is sized for the usual count; rare extra
   // candidates are taken by the same workgroups)
-  const uint32_t y0 = blockIdx.y - (ra.n ? 1 : 0), ny = gridDim.y - (ra.n ? 1 : 0);
+  const uint32_t y0 = blockIdx.y, ny = gridDim.y - (ra.n ? 1 : 0);
   for (uint32_t a = y0; a < ne; a += ny) {
   const ExpertWork* W = work + a;  // field by field: scalar loads
   const uint32_t m_all = W->m;
