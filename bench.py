@@ -78,6 +78,70 @@ def measured_traffic(batch, math, layers):
         return None
 
 
+# BASELINE configs 4 and 5 (the per-layer slice of C5): name -> shape, types, batch
+EXTRA_CONFIGS = {
+    "c4": dict(d=2048, f=768, ne=128, k=8, n=64, qts=("Q6_K", "Q6_K", "Q8_0"), logits_scale=4.0,
+               workload="C4 fine-grained MoE layer: d2048 f768 128 experts top-8, Q6_K gate/up, Q8_0 down, "
+                        "64 tokens, router logits uniform x4 given"),
+    "c5_layer": dict(d=4096, f=14336, ne=8, k=2, n=8, qts=("Q3_K", "Q3_K", "Q4_K"), logits_scale=None,
+                     workload="C5 per-layer slice: Mixtral-shape layer with Q3_K gate/up and Q4_K down "
+                              "(Q3_K_M-style mix), 8 concurrent decode tokens"),
+}
+
+
+def extra_leg(name, a, dev, threads, stream, timed):
+    """One decode leg of a further BASELINE configuration: tokens/s and the layer's HBM rate
+    (touched experts' packed bytes + router + activations per call over the call time)."""
+    import torch
+    import garuda_amd as G
+    from garuda_amd import moe as M
+
+    c = EXTRA_CONFIGS[name]
+    d, f, ne, k, n = c["d"], c["f"], c["ne"], c["k"], c["n"]
+    qts = tuple(getattr(G, q) for q in c["qts"])
+    seed = SEED + 0x1000 * (1 + list(EXTRA_CONFIGS).index(name))
+    mats = {}
+    for p, (nm, rows, cols) in enumerate((("gate", f, d), ("up", f, d), ("down", d, f))):
+        mats[nm] = M.quantize(qts[p], M.fill_gaussian(seed + p, ne * rows * cols, 0.0, 0.02, threads), threads)
+    expert_bytes = sum(M.byte_size(qts[p], rows * cols) for p, (rows, cols) in enumerate(((f, d), (f, d), (d, f))))
+    layers = []
+    for l in range(2):
+        router = M.fill_gaussian(seed + 0x10 + l, ne * d, 0.0, 0.02, threads)
+        layers.append(G.MoeLayer(dev, d, f, ne, k, router, mats["gate"], mats["up"], mats["down"], qts,
+                                 math=G.MATH_PACKED))
+    del mats
+    hs = torch.from_numpy(M.fill_gaussian(seed + 0x20, n * d, 0.0, 1.0, threads).reshape(n, d)).cuda()
+    lg = None
+    if c["logits_scale"] is not None:
+        rng = np.random.default_rng(seed & 0xffffffff)
+        lg = torch.from_numpy((rng.random((n, ne), dtype=np.float32) * np.float32(c["logits_scale"]))).cuda()
+    out = torch.empty((n, d), dtype=torch.float32, device="cuda")
+    ids = torch.empty((len(layers), n, k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((len(layers), n, k), dtype=torch.float32, device="cuda")
+    sh = stream.cuda_stream
+
+    def step(i):
+        l = i % len(layers)
+        layers[l].forward_async(hs.data_ptr(), n, out.data_ptr(), ids[l].data_ptr(), wts[l].data_ptr(),
+                                lg.data_ptr() if lg is not None else 0, sh)
+
+    steps = max(50, a.steps // 2)
+    for i in range(max(5, a.warmup // 2)):
+        step(i)
+    torch.cuda.synchronize()
+    ms, _ = timed(step, steps, False)
+    touched = float(np.mean([len(np.unique(ids[l].cpu().numpy())) for l in range(len(layers))]))
+    step_s = ms / steps / 1e3
+    nbytes = touched * expert_bytes + (0 if lg is not None else ne * d * 4) + 2 * n * d * 4
+    log(f"{name}: {n / step_s:.0f} tok/s, {step_s * 1e6:.1f} us/call, {touched:.1f} experts touched, "
+        f"{nbytes / step_s / 1e9:.0f} GB/s")
+    for l in layers:
+        l.release()
+    return {"workload": c["workload"], "tokens_per_s": n / step_s, "us_per_call": step_s * 1e6,
+            "experts_touched": touched, "layer_bytes": nbytes, "layer_GBs": nbytes / step_s / 1e9,
+            "hbm_frac": nbytes / step_s / 1e9 / HBM_PEAK_GBS, "math": "packed", "steps": steps}
+
+
 def prefill_leg(a, dev, mats, threads, stream, timed):
     """the same Q4_K layer at a prefill of `a.prefill_tokens` tokens,
     routing skewed to Zipf(1.1) expert loads through one shared activation direction, f32
@@ -153,6 +217,8 @@ def main():
                     help="tokens of the C3 prefill leg (Zipf-skewed routing, f32 math on MFMA); 0 skips it")
     ap.add_argument("--prefill-steps", type=int, default=40)
     ap.add_argument("--prefill-layers", type=int, default=2)
+    ap.add_argument("--extra", default="c4,c5_layer",
+                    help="further BASELINE configurations to time at decode (c4, c5_layer); empty skips")
     a = ap.parse_args()
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -172,7 +238,8 @@ def main():
     math = G.MATH_PACKED if a.math == "packed" else G.MATH_F32
     expert_bytes = 3 * M.byte_size(G.Q4_K, F * D)
     n_pf_layers = a.prefill_layers if a.prefill_tokens else 0
-    slab = (a.layers + n_pf_layers) * NE * (expert_bytes + 3 * 4096) + (256 << 20)
+    # + the further configurations' 2 copies each (C4 ~0.55 GB, C5 slice ~0.67 GB per copy)
+    slab = (a.layers + n_pf_layers) * NE * (expert_bytes + 3 * 4096) + (256 << 20) + (3 << 30)
     dev = G.Device(0, slab_bytes=slab)
     layers = []
     t0 = time.time()
@@ -246,6 +313,9 @@ def main():
     prefill = None
     if a.prefill_tokens:
         prefill = prefill_leg(a, dev, mats, threads, stream, timed)
+    extra = {}
+    for name in [x for x in a.extra.split(",") if x]:
+        extra[name] = extra_leg(name, a, dev, threads, stream, timed)
 
     if a.calibrate_copy:
         src = torch.empty(a.calibrate_copy << 18, dtype=torch.float32, device="cuda")
@@ -301,6 +371,7 @@ def main():
                      "bytes_per_launch": r["gateup_bytes"], "avg_launch_us": r["gateup_us"]},
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "configs": extra,
         "sweep": {str(n): {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res.items()}
                   for n, res in results.items()},
     }

@@ -252,66 +252,106 @@ __global__ void __launch_bounds__(kRouteThreads) k_route(LayerDev L, FwdBufs B, 
 }
 
 // Dispatch body: a stable counting sort of the (token, rank) pairs by expert id, which is
-// exactly members[e] of llama/mod.rs:967-972 laid end to end. One workgroup; cnt is
-// [ne] in LDS; every thread must call this.
-__device__ void dispatch_block(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t* cnt,
+// exactly members[e] of llama/mod.rs:967-972 laid end to end. One workgroup of 256
+// threads; sm holds nk + 3*ne + 2 words of LDS. Counts by LDS atomics, offsets and the
+// active list by one wave's running scans, then every pair's slot = its expert's offset +
+// the pairs of that expert before it (counted chunk by chunk against the LDS copy of the
+// ids, the counts of earlier chunks carried per expert). Every thread must call this.
+__device__ void dispatch_block(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t* sm,
                                const uint32_t* ids, const float* wts) {
-  const uint32_t ne = L.ne, k = L.k, nk = n * k;
-  for (uint32_t e = threadIdx.x; e < ne; e += blockDim.x) {
-    uint32_t c = 0;
-    for (uint32_t p = 0; p < nk; p++) c += ids[p] == e;
-    cnt[e] = c;
-  }
+  const uint32_t ne = L.ne, k = L.k, nk = n * k, tid = threadIdx.x, T = blockDim.x;
+  uint32_t* idl = sm;            // [nk] ids
+  uint32_t* cnt = sm + nk;       // [ne] counts, then the running count of earlier chunks
+  uint32_t* start = cnt + ne;    // [ne] offsets
+  uint32_t* aidx = start + ne;   // [ne] active index (~0u: inactive)
+  uint32_t* tot = aidx + ne;     // [2] active experts, token tiles
+  for (uint32_t p = tid; p < nk; p += T) idl[p] = ids[p];
+  for (uint32_t e = tid; e < ne; e += T) cnt[e] = 0;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t off = 0, na = 0;
-    for (uint32_t e = 0; e < ne; e++) {
-      uint32_t c = cnt[e];
-      cnt[e] = off;
-      B.offsets[e] = off;
-      if (c) {
-        if (B.work) {
-          ExpertWork& W = B.work[na];
-          for (int p = 0; p < 3; p++) W.w[p] = L.eptr[p * ne + e];
-          W.e = e;
-          W.s0 = off;
-          W.m = c;
+  for (uint32_t p = tid; p < nk; p += T) atomicAdd(&cnt[idl[p]], 1u);
+  __syncthreads();
+  if (tid < 64) {  // running scans over the experts, 64 at a time
+    const uint32_t lane = tid;
+    uint32_t off = 0, na = 0, nt = 0;
+    for (uint32_t e0 = 0; e0 < ne; e0 += 64) {
+      const uint32_t e = e0 + lane;
+      const uint32_t c = e < ne ? cnt[e] : 0u, act = c ? 1u : 0u;
+      const uint32_t tl = B.ptile ? (c + kPfTok - 1) / kPfTok : 0u;
+      uint32_t ic = c, ia = act, it = tl;  // inclusive scans
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t vc = __shfl_up(ic, o, 64), va = __shfl_up(ia, o, 64), vt = __shfl_up(it, o, 64);
+        if (lane >= (uint32_t)o) {
+          ic += vc;
+          ia += va;
+          it += vt;
         }
-        B.active[1 + na++] = e;
       }
-      off += c;
+      if (e < ne) {
+        start[e] = off + ic - c;
+        aidx[e] = act ? na + ia - 1 : ~0u;
+        if (act && B.ptile) {
+          const uint32_t a = na + ia - 1, t0 = nt + it - tl;
+          for (uint32_t t = 0; t < tl; t++) B.ptile[t0 + t] = (a << 16) | t;
+        }
+      }
+      off += __shfl(ic, 63, 64);
+      na += __shfl(ia, 63, 64);
+      nt += __shfl(it, 63, 64);
     }
-    B.offsets[ne] = off;
-    B.active[0] = na;
-    if (B.work)
-      for (uint32_t a = na; a < ne; a++) B.work[a].m = 0;
-    if (B.ptile) {  // token tiles of kPfTok per active expert, in slot order
-      uint32_t nt = 0;
-      for (uint32_t a = 0; a < na; a++) {
-        const uint32_t e = B.active[1 + a], m = B.offsets[e + 1] - B.offsets[e];
-        for (uint32_t t = 0; t * kPfTok < m; t++) B.ptile[nt++] = (a << 16) | t;
-      }
-      for (; nt < B.ptile_cap; nt++) B.ptile[nt] = ~0u;
+    if (lane == 0) {
+      tot[0] = na;
+      tot[1] = nt;
+      B.offsets[ne] = off;
+      B.active[0] = na;
     }
   }
   __syncthreads();
-  for (uint32_t e = threadIdx.x; e < ne; e += blockDim.x) {
-    uint32_t pos = cnt[e];
-    for (uint32_t p = 0; p < nk; p++) {
-      if (ids[p] == e) {
-        B.slot_tok[pos] = p / k;
-        B.slot_w[pos] = wts[p];
-        B.slot_rank[pos] = p % k;
-        B.slot_of[p] = pos;
-        pos++;
+  const uint32_t na = tot[0], nt = tot[1];
+  for (uint32_t e = tid; e < ne; e += T) {
+    B.offsets[e] = start[e];
+    const uint32_t a = aidx[e];
+    if (a != ~0u) {
+      B.active[1 + a] = e;
+      if (B.work) {
+        ExpertWork& W = B.work[a];
+        for (int q = 0; q < 3; q++) W.w[q] = L.eptr[q * ne + e];
+        W.e = e;
+        W.s0 = start[e];
+        W.m = cnt[e];
       }
     }
+  }
+  if (B.work)
+    for (uint32_t a = na + tid; a < ne; a += T) B.work[a].m = 0;
+  if (B.ptile)
+    for (uint32_t i = nt + tid; i < B.ptile_cap; i += T) B.ptile[i] = ~0u;
+  __syncthreads();
+  for (uint32_t e = tid; e < ne; e += T) cnt[e] = 0;  // now: pairs placed by earlier chunks
+  __syncthreads();
+  for (uint32_t c0 = 0; c0 < nk; c0 += T) {
+    const uint32_t p = c0 + tid;
+    uint32_t e = ~0u, pos = 0;
+    if (p < nk) {
+      e = idl[p];
+      uint32_t r = 0;
+      for (uint32_t q = c0; q < p; q++) r += idl[q] == e;
+      pos = start[e] + cnt[e] + r;
+    }
+    __syncthreads();  // every pair of the chunk has read the carried counts
+    if (p < nk) {
+      atomicAdd(&cnt[e], 1u);
+      B.slot_tok[pos] = p / k;
+      B.slot_w[pos] = wts[p];
+      B.slot_rank[pos] = p % k;
+      B.slot_of[p] = pos;
+    }
+    __syncthreads();
   }
 }
 
 __global__ void __launch_bounds__(256) k_dispatch(LayerDev L, FwdBufs B, uint32_t n) {
-  extern __shared__ uint32_t cnt[];  // [ne]
-  dispatch_block(L, B, n, cnt, B.ids, B.w);
+  extern __shared__ uint32_t dsm_u32[];  // [n*k + 3*ne + 2]
+  dispatch_block(L, B, n, dsm_u32, B.ids, B.w);
 }
 
 // ---------------------------------------------------------------------------------
@@ -724,7 +764,13 @@ hipError_t launch_route(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStre
 }
 
 hipError_t launch_dispatch(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
-  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(256), L.ne * 4, st, L, B, n);
+  const size_t shm = ((size_t)n * L.k + 3 * (size_t)L.ne + 2) * 4;
+  if (shm > 160 * 1024) return hipErrorInvalidValue;  // the host keeps calls below this
+  static const bool attr =
+      hipFuncSetAttribute((const void*)k_dispatch, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) ==
+      hipSuccess;
+  (void)attr;
+  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(256), shm, st, L, B, n);
   return hipGetLastError();
 }
 

@@ -353,16 +353,20 @@ static bool allow_lds(K kernel) {
          hipSuccess;
 }
 
-// Tokens per chunk: the batch, as far as their staged activations and running sums fit
-// the LDS budget (a larger batch re-streams the weights once per chunk).
-static uint32_t chunk_tokens(uint32_t n, uint32_t per_token_bytes) {
-  return min(n, kLdsBudget / per_token_bytes);
+// Tokens per chunk: enough for the tokens an expert usually gets (twice the mean n*k/ne,
+// at least 16), as far as their staged activations and running sums fit the LDS budget;
+// an expert with more tokens takes several chunks, re-streaming its weights once per
+// chunk. Sizing for the whole batch instead would give every workgroup the LDS of n
+// tokens and one workgroup per CU when experts are many and tokens per expert few.
+static uint32_t chunk_tokens(const LayerDev& L, uint32_t n, uint32_t per_token_bytes) {
+  const uint32_t usual = max(16u, 2 * ((n * L.k + L.ne - 1) / L.ne));
+  return min(min(n, usual), kLdsBudget / per_token_bytes);
 }
 
 template <int QT, bool PACKED>
 static hipError_t go_gu(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
   const uint32_t per = 2 * 64 * 4 + ActLds<QT, PACKED>::per_token(L.d) + 4;
-  const uint32_t mt = chunk_tokens(n, per + 16);
+  const uint32_t mt = chunk_tokens(L, n, per + 16);
   if (mt == 0) return hipErrorInvalidValue;
   static const bool once = allow_lds(k_gu_units<QT, PACKED>);
   (void)once;
@@ -380,7 +384,7 @@ static hipError_t go_dn(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_
   // a workgroup stages at most ceil(units / ksg) + 1 units
   const uint32_t span = min(((unit_count<QT>(L.f) + ksg - 1) / ksg + 1) * UT_<QT>::EU, L.f);
   const uint32_t per = kDnKS * 64 * 4 + ActLds<QT, PACKED>::per_token(span) + 4;
-  const uint32_t mt = chunk_tokens(n, per + 16);
+  const uint32_t mt = chunk_tokens(L, n, per + 16);
   if (mt == 0) return hipErrorInvalidValue;
   static const bool once = allow_lds(k_dn_units<QT, PACKED, kDnKS>);
   (void)once;
