@@ -354,12 +354,12 @@ static bool allow_lds(K kernel) {
 }
 
 // Tokens per chunk: enough for the tokens an expert usually gets (twice the mean n*k/ne,
-// at least 16), as far as their staged activations and running sums fit the LDS budget;
+// at least 8), as far as their staged activations and running sums fit the LDS budget;
 // an expert with more tokens takes several chunks, re-streaming its weights once per
 // chunk. Sizing for the whole batch instead would give every workgroup the LDS of n
 // tokens and one workgroup per CU when experts are many and tokens per expert few.
 static uint32_t chunk_tokens(const LayerDev& L, uint32_t n, uint32_t per_token_bytes) {
-  const uint32_t usual = max(16u, 2 * ((n * L.k + L.ne - 1) / L.ne));
+  const uint32_t usual = max(8u, 2 * ((n * L.k + L.ne - 1) / L.ne));
   return min(min(n, usual), kLdsBudget / per_token_bytes);
 }
 
