@@ -32,6 +32,21 @@ class GmoeSlabStats(C.Structure):
                 ("bytes", u64), ("capacity", u64), ("h2d_bytes", u64)]
 
 
+class GmoeGgufHeader(C.Structure):
+    _fields_ = [("version", u32), ("n_tensors", u64), ("n_keys", u64), ("data_offset", u64),
+                ("file_bytes", u64)]
+
+
+class GmoeGgufValue(C.Structure):
+    _fields_ = [("type", u32), ("elem_type", u32), ("u", u64), ("f", C.c_double),
+                ("str", C.POINTER(C.c_char)), ("len", u64), ("node", vp)]
+
+
+class GmoeGgufTensorInfo(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("n_dims", u32), ("qtype", u32), ("dims", u64 * 4),
+                ("offset", u64), ("n_elements", u64), ("nbytes", u64), ("data", vp)]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "gmoe_abi_version": (u32, []),
@@ -54,6 +69,17 @@ SIGNATURES = {
     "gmoe_expf": (i32, [vp, f32p, u64, f32p]),
     "gmoe_quantize": (i32, [u32, f32p, u64, vp, i32]),
     "gmoe_fill_gaussian": (i32, [u64, C.c_float, C.c_float, u64, f32p, i32]),
+    "gmoe_gguf_open": (i32, [C.c_char_p, C.POINTER(vp)]),
+    "gmoe_gguf_parse": (i32, [vp, u64, C.POINTER(vp)]),
+    "gmoe_gguf_close": (None, [vp]),
+    "gmoe_gguf_get_header": (i32, [vp, C.POINTER(GmoeGgufHeader)]),
+    "gmoe_gguf_key_at": (i32, [vp, u64, C.POINTER(C.c_char_p)]),
+    "gmoe_gguf_get_value": (i32, [vp, C.c_char_p, C.POINTER(GmoeGgufValue)]),
+    "gmoe_gguf_array_item": (i32, [vp, C.POINTER(GmoeGgufValue), u64, C.POINTER(GmoeGgufValue)]),
+    "gmoe_gguf_tensor_at": (i32, [vp, u64, C.POINTER(GmoeGgufTensorInfo)]),
+    "gmoe_gguf_find_tensor": (i32, [vp, C.c_char_p, C.POINTER(GmoeGgufTensorInfo)]),
+    "gmoe_gguf_layer_desc": (i32, [vp, u32, u32, u32, u32, C.POINTER(GmoeLayerDesc)]),
+    "gmoe_gguf_expert_ranges": (i32, [vp, u32, u32, C.POINTER(u64), C.POINTER(u64)]),
     "gmoe_set_kernel_timing": (i32, [vp, i32]),
     "gmoe_kernel_time": (i32, [vp, u32, C.POINTER(C.c_double), C.POINTER(u64)]),
 }

@@ -146,6 +146,10 @@ struct Timing {
 
 }  // namespace
 
+namespace gmoe {
+void set_last_error(const char* msg) { g_err = msg; }
+}  // namespace gmoe
+
 struct gmoe_ctx {
   int device = 0;
   hipStream_t stream = nullptr;

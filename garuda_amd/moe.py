@@ -56,7 +56,11 @@ class DeviceError(GarudaError):
     pass
 
 
-_STATUS = {1: ModelError, 2: InferenceError, 3: CacheError, 4: ConfigError, 5: DeviceError}
+class NotFoundError(GarudaError, KeyError):
+    """No such GGUF metadata key or tensor (where the reference returns `None`)."""
+
+
+_STATUS = {1: ModelError, 2: InferenceError, 3: CacheError, 4: ConfigError, 5: DeviceError, 6: NotFoundError}
 
 
 def _check(status: int) -> None:
@@ -271,6 +275,24 @@ class MoeLayer:
         lid = C.c_uint32()
         _check(lib().gmoe_layer_register(dev.handle, C.byref(desc), C.byref(lid)))
         self.id = lid.value
+
+    @classmethod
+    def from_gguf(cls, dev: Device, gguf, layer: int, gating: int = GATING_LLAMA,
+                  combine: int = COMBINE_EXPERT_ORDER, math: int = MATH_PACKED) -> "MoeLayer":
+        """Layer `layer` of a GGUF checkpoint (garuda_amd.gguf.Gguf), registered straight
+        from the file's bytes: the `Ffn::Moe` arm of LlamaBackend::from_gguf
+        (llama/mod.rs:569-607). The checkpoint stays open while this layer lives."""
+        desc = GmoeLayerDesc()
+        _check(lib().gmoe_gguf_layer_desc(gguf.handle, layer, gating, combine, math, C.byref(desc)))
+        self = cls.__new__(cls)
+        self.dev = dev
+        self.d, self.f, self.ne, self.k = desc.d_model, desc.d_ff, desc.n_experts, desc.top_k
+        self._keep = [gguf]
+        self.router = np.ctypeslib.as_array(desc.router, shape=(self.ne, self.d)).copy()
+        lid = C.c_uint32()
+        _check(lib().gmoe_layer_register(dev.handle, C.byref(desc), C.byref(lid)))
+        self.id = lid.value
+        return self
 
     def feed_forward_batch(self, hs: np.ndarray, logits: np.ndarray | None = None):
         """(out [n, d], routed ids [n, k], routed weights [n, k]) for n hidden states."""

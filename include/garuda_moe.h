@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GMOE_ABI_VERSION 1u
+#define GMOE_ABI_VERSION 2u
 
 /* Status codes. Mirrors the GarudaError variants the reference returns on this
  * path (garuda/src/core/mod.rs:10-47). */
@@ -35,7 +35,8 @@ typedef enum gmoe_status {
   GMOE_ERR_INFERENCE = 2, /* GarudaError::Inference: n/d mismatch, unknown layer */
   GMOE_ERR_CACHE = 3,     /* GarudaError::Cache: the HBM slab cannot hold what is asked */
   GMOE_ERR_CONFIG = 4,    /* GarudaError::Config: top_k outside 1..=n_experts (core/mod.rs:103-108) */
-  GMOE_ERR_DEVICE = 5     /* HIP runtime failure; the context stays usable for teardown */
+  GMOE_ERR_DEVICE = 5,    /* HIP runtime failure; the context stays usable for teardown */
+  GMOE_ERR_NOT_FOUND = 6  /* no such GGUF metadata key or tensor (the reference's `None`) */
 } gmoe_status;
 
 /* ggml type ids (garuda/src/quant/mod.rs:22-30). */
@@ -136,6 +137,86 @@ gmoe_status gmoe_expert_prefetch(gmoe_ctx* ctx, uint32_t layer_id, uint32_t expe
 int gmoe_expert_is_resident(gmoe_ctx* ctx, uint32_t layer_id, uint32_t expert);
 gmoe_status gmoe_expert_evict(gmoe_ctx* ctx, uint32_t layer_id, uint32_t expert);
 gmoe_status gmoe_slab_get_stats(gmoe_ctx* ctx, gmoe_slab_stats* out);
+
+/* ---- GGUF checkpoints: the slab's source (garuda/src/gguf/mod.rs; llama/mod.rs:551-637) ----
+ *
+ * A parsed GGUF file: header, metadata and tensor descriptors, with the reference's
+ * bounds rules (gguf/mod.rs:247-330): every length is checked against the bytes that
+ * remain, counts are bounded by what those bytes could describe, so a malformed file
+ * is an error (GMOE_ERR_MODEL, message prefixed "gguf: ") and never a crash or an
+ * outsized allocation. Pure host code: no device, no context. */
+typedef struct gmoe_gguf gmoe_gguf;
+
+/* Metadata value types, as the file stores them (gguf/mod.rs:181-221). */
+enum {
+  GMOE_GGUF_U8 = 0, GMOE_GGUF_I8 = 1, GMOE_GGUF_U16 = 2, GMOE_GGUF_I16 = 3, GMOE_GGUF_U32 = 4,
+  GMOE_GGUF_I32 = 5, GMOE_GGUF_F32 = 6, GMOE_GGUF_BOOL = 7, GMOE_GGUF_STRING = 8,
+  GMOE_GGUF_ARRAY = 9, GMOE_GGUF_U64 = 10, GMOE_GGUF_I64 = 11, GMOE_GGUF_F64 = 12
+};
+
+typedef struct gmoe_gguf_header {
+  uint32_t version;      /* 2 or 3 */
+  uint64_t n_tensors;    /* tensor descriptors, in file order */
+  uint64_t n_keys;       /* distinct metadata keys (a repeated key keeps its last value) */
+  uint64_t data_offset;  /* start of the tensor data: the descriptors' end rounded up to
+                            general.alignment (32 by default), Gguf::data_offset */
+  uint64_t file_bytes;
+} gmoe_gguf_header;
+
+typedef struct gmoe_gguf_value {
+  uint32_t type;         /* GMOE_GGUF_* */
+  uint32_t elem_type;    /* ARRAY: the element type */
+  uint64_t u;            /* integer types and BOOL: the value (signed ones sign-extended) */
+  double f;              /* F32, F64 */
+  const char* str;       /* STRING: the bytes, NUL-terminated, valid until gmoe_gguf_close */
+  uint64_t len;          /* STRING: byte length; ARRAY: element count */
+  const void* node;      /* the value inside the handle (for gmoe_gguf_array_item) */
+} gmoe_gguf_value;
+
+typedef struct gmoe_gguf_tensor_info {
+  const char* name;      /* valid until gmoe_gguf_close */
+  uint32_t n_dims;       /* 0..4 */
+  uint32_t qtype;        /* raw ggml type id */
+  uint64_t dims[4];      /* ggml order: dims[0] is the row length */
+  uint64_t offset;       /* from the start of the tensor data (TensorInfo::offset) */
+  uint64_t n_elements;
+  uint64_t nbytes;       /* quant::byte_size of the tensor; 0 for a type this library has no
+                            block layout for */
+  const void* data;      /* its bytes inside the file; NULL when they run past the end */
+} gmoe_gguf_tensor_info;
+
+/* Map `path` read-only and parse it (Gguf::parse over the mapping). */
+gmoe_status gmoe_gguf_open(const char* path, gmoe_gguf** out);
+/* Parse `len` bytes at `bytes`, borrowed until gmoe_gguf_close. */
+gmoe_status gmoe_gguf_parse(const void* bytes, uint64_t len, gmoe_gguf** out);
+void gmoe_gguf_close(gmoe_gguf* g);
+gmoe_status gmoe_gguf_get_header(const gmoe_gguf* g, gmoe_gguf_header* out);
+/* The i-th metadata key in byte order (the reference's BTreeMap order). */
+gmoe_status gmoe_gguf_key_at(const gmoe_gguf* g, uint64_t i, const char** key);
+/* A metadata value keyed exactly (Gguf::get); GMOE_ERR_NOT_FOUND if absent. */
+gmoe_status gmoe_gguf_get_value(const gmoe_gguf* g, const char* key, gmoe_gguf_value* out);
+/* Element i of an ARRAY value read from the same handle (nested arrays to any depth). */
+gmoe_status gmoe_gguf_array_item(const gmoe_gguf* g, const gmoe_gguf_value* array, uint64_t i,
+                                 gmoe_gguf_value* out);
+gmoe_status gmoe_gguf_tensor_at(const gmoe_gguf* g, uint64_t i, gmoe_gguf_tensor_info* out);
+/* The first tensor named `name` (Gguf::tensor); GMOE_ERR_NOT_FOUND if none. */
+gmoe_status gmoe_gguf_find_tensor(const gmoe_gguf* g, const char* name, gmoe_gguf_tensor_info* out);
+
+/* The MoE layer `layer` of the checkpoint as a layer descriptor, as
+ * LlamaBackend::from_gguf reads it (llama/mod.rs:569-607, load_weight :358-381,
+ * pinned_weight :320-350): dimensions from {arch}.embedding_length,
+ * .feed_forward_length, .expert_count, .expert_used_count and .block_count; the
+ * stacked blk.L.ffn_{gate,up,down}_exps tensors when present, else the split
+ * blk.L.ffn_{gate,up,down}.E tensors; router blk.L.ffn_gate_inp (F32, or F16 widened
+ * exactly). Element counts and byte ranges are checked. The descriptor's pointers
+ * point into the file (or into buffers the handle owns) and stay valid until
+ * gmoe_gguf_close, so a layer registered from it must be released first. */
+gmoe_status gmoe_gguf_layer_desc(gmoe_gguf* g, uint32_t layer, uint32_t gating, uint32_t combine,
+                                 uint32_t math, gmoe_layer_desc* out);
+/* File byte ranges of expert `expert`'s gate, up and down weights in layer `layer`
+ * (ExpertWeight::byte_range, llama/mod.rs:250-269; expert_page_ranges :664-682). */
+gmoe_status gmoe_gguf_expert_ranges(gmoe_gguf* g, uint32_t layer, uint32_t expert, uint64_t offset[3],
+                                    uint64_t length[3]);
 
 /* ---- single steps of the path, for parity tests (host pointers, synchronous) ---- */
 
