@@ -197,6 +197,66 @@ def prefill_leg(a, dev, mats, threads, stream, timed):
     }
 
 
+def gguf_leg(a, dev, mats, threads):
+    """The slab's source: the C2 layer written as a one-layer GGUF
+    checkpoint (stacked Q4_K experts, F32 router), then Gguf.open + MoeLayer.from_gguf timed
+    to the end of staging: the mapped file's expert bytes copied through the pinned double
+    buffer, over the host link, and tiled into the HBM slab. Beside it, the host link's own
+    rate for a pinned copy of one expert's bytes, with HIP events."""
+    import shutil
+    import tempfile
+
+    import torch
+    import garuda_amd as G
+    from garuda_amd import gguf as gg
+    from garuda_amd import moe as M
+
+    tmp = Path(tempfile.mkdtemp(prefix="gmoe_gguf_"))
+    try:
+        router = M.fill_gaussian(SEED + 0x500, NE * D, 0.0, 0.02, threads)
+        meta = [("general.architecture", gg.STRING, "llama"), ("llama.embedding_length", gg.U32, D),
+                ("llama.feed_forward_length", gg.U32, F), ("llama.block_count", gg.U32, 1),
+                ("llama.expert_count", gg.U32, NE), ("llama.expert_used_count", gg.U32, K)]
+        tensors = [("blk.0.ffn_gate_inp.weight", [D, NE], G.F32, router),
+                   ("blk.0.ffn_gate_exps.weight", [D, F, NE], G.Q4_K, mats["gate"]),
+                   ("blk.0.ffn_up_exps.weight", [D, F, NE], G.Q4_K, mats["up"]),
+                   ("blk.0.ffn_down_exps.weight", [F, D, NE], G.Q4_K, mats["down"])]
+        path = tmp / "c2_layer.gguf"
+        size = gg.write_gguf_file(path, meta, tensors)
+        staged = NE * 3 * M.byte_size(G.Q4_K, F * D)
+        times = []
+        for _ in range(a.gguf_reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            with G.Gguf.open(path) as g:
+                layer = G.MoeLayer.from_gguf(dev, g, 0)
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t0)
+                layer.release()
+        nb = staged // NE
+        host = torch.empty(nb, dtype=torch.uint8, pin_memory=True)
+        devb = torch.empty(nb, dtype=torch.uint8, device="cuda")
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        link = []
+        for _ in range(3):
+            ev0.record()
+            devb.copy_(host, non_blocking=True)
+            ev1.record()
+            torch.cuda.synchronize()
+            link.append(nb / (ev0.elapsed_time(ev1) / 1e3) / 1e9)
+        del host, devb
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    best = min(times)
+    gbs, link_gbs = staged / best / 1e9, max(link)
+    log(f"gguf: {size / 1e6:.0f} MB file, {staged / 1e6:.0f} MB of experts staged into HBM in "
+        f"{best * 1e3:.0f} ms ({gbs:.1f} GB/s; pinned host->device copy {link_gbs:.1f} GB/s)")
+    return {"workload": "C2 layer as a one-layer GGUF checkpoint (stacked Q4_K experts): open + register, "
+                        "mapped file -> pinned double buffer -> HBM slab, page-cache resident file",
+            "file_bytes": size, "staged_bytes": staged, "seconds": best, "reps": len(times),
+            "GB_s": gbs, "link_GB_s": link_gbs, "frac_of_link": gbs / link_gbs}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -217,6 +277,8 @@ def main():
                     help="tokens of the C3 prefill leg (Zipf-skewed routing, f32 math on MFMA); 0 skips it")
     ap.add_argument("--prefill-steps", type=int, default=40)
     ap.add_argument("--prefill-layers", type=int, default=2)
+    ap.add_argument("--gguf-reps", type=int, default=3,
+                    help="timed open+register passes of the GGUF staging leg (0: skip it)")
     ap.add_argument("--extra", default="c4,c5_layer",
                     help="further BASELINE configurations to time at decode (c4, c5_layer); empty skips")
     a = ap.parse_args()
@@ -317,6 +379,8 @@ def main():
     for name in [x for x in a.extra.split(",") if x]:
         extra[name] = extra_leg(name, a, dev, threads, stream, timed)
 
+    gguf = gguf_leg(a, dev, mats, threads) if a.gguf_reps > 0 else None
+
     if a.calibrate_copy:
         src = torch.empty(a.calibrate_copy << 18, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
@@ -372,6 +436,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill": prefill,
         "configs": extra,
+        "gguf_staging": gguf,
         "sweep": {str(n): {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res.items()}
                   for n, res in results.items()},
     }

@@ -274,11 +274,8 @@ def _put_value(out: bytearray, t: int, v) -> None:
         out += struct.pack(_PACK[t], int(v) if t == BOOL else v)
 
 
-def write_gguf(metadata, tensors, version: int = 3, alignment: int = 32) -> bytes:
-    """A GGUF file: `metadata` is [(key, type, value)], `tensors` is
-    [(name, dims, ggml_type, raw bytes)] with dims in ggml order (row length first).
-    Tensor data is laid out in order, each tensor at the next `alignment` boundary of
-    the data section, which starts at the next boundary after the descriptors."""
+def _layout(metadata, tensors, version: int, alignment: int):
+    """(header bytes up to the data section, tensor offsets, data section size)."""
     out = bytearray(b"GGUF")
     out += struct.pack("<IQQ", version, len(tensors), len(metadata))
     for key, t, v in metadata:
@@ -292,17 +289,42 @@ def write_gguf(metadata, tensors, version: int = 3, alignment: int = 32) -> byte
         n = 1
         for d in dims:
             n *= d
-        if len(raw) != byte_size(qt, n):
-            raise ValueError(f"tensor {name}: {len(raw)} bytes for {n} elements of type {qt}")
-        cur += len(raw)
+        nb = memoryview(raw).nbytes
+        if nb != byte_size(qt, n):
+            raise ValueError(f"tensor {name}: {nb} bytes for {n} elements of type {qt}")
+        cur += nb
     for (name, dims, qt, raw), off in zip(tensors, offs):
         _put_str(out, name)
         out += struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
         out += struct.pack("<IQ", qt, off)
-    base = (len(out) + alignment - 1) // alignment * alignment
-    out += bytes(base - len(out))
-    end = base + ((cur + alignment - 1) // alignment * alignment)
-    data = bytearray(end - base)
+    out += bytes(-len(out) % alignment)
+    return bytes(out), offs, (cur + alignment - 1) // alignment * alignment
+
+
+def write_gguf(metadata, tensors, version: int = 3, alignment: int = 32) -> bytes:
+    """A GGUF file: `metadata` is [(key, type, value)], `tensors` is
+    [(name, dims, ggml_type, raw bytes)] with dims in ggml order (row length first).
+    Tensor data is laid out in order, each tensor at the next `alignment` boundary of
+    the data section, which starts at the next boundary after the descriptors."""
+    head, offs, size = _layout(metadata, tensors, version, alignment)
+    data = bytearray(size)
     for (_, _, _, raw), off in zip(tensors, offs):
-        data[off:off + len(raw)] = bytes(raw)
-    return bytes(out + data)
+        b = memoryview(raw).cast("B")
+        data[off:off + b.nbytes] = b
+    return head + bytes(data)
+
+
+def write_gguf_file(path, metadata, tensors, version: int = 3, alignment: int = 32) -> int:
+    """write_gguf streamed to `path` tensor by tensor (raw may be any buffer, e.g. a numpy
+    array); returns the file size."""
+    head, offs, size = _layout(metadata, tensors, version, alignment)
+    with open(path, "wb") as fh:
+        fh.write(head)
+        at = 0
+        for (_, _, _, raw), off in zip(tensors, offs):
+            b = memoryview(raw).cast("B")
+            fh.write(bytes(off - at))
+            fh.write(b)
+            at = off + b.nbytes
+        fh.write(bytes(size - at))
+    return len(head) + size

@@ -453,3 +453,15 @@ def test_open_maps_a_file(tmp_path):
         assert t.bytes().tobytes() == data[g.data_offset + t.offset:g.data_offset + t.offset + t.nbytes]
     with pytest.raises(G.ModelError, match="cannot open"):
         G.Gguf.open(tmp_path / "missing.gguf")
+
+
+def test_streamed_writer_matches(tmp_path):
+    meta = [("general.architecture", gg.STRING, "x"), ("general.alignment", gg.U32, 64)]
+    tensors = [("a", [8], G.F32, np.arange(8, dtype=np.float32)), ("b", [32], G.Q8_0, np.zeros(34, np.uint8)),
+               ("c", [256], G.Q4_K, G.quantize(G.Q4_K, np.linspace(-1, 1, 256, dtype=np.float32)))]
+    n = gg.write_gguf_file(tmp_path / "w.gguf", meta, tensors, alignment=64)
+    data = (tmp_path / "w.gguf").read_bytes()
+    assert n == len(data) and data == gg.write_gguf(meta, tensors, alignment=64)
+    g = lib_parse(data)
+    assert g.data_offset % 64 == 0 and all(t.offset % 64 == 0 for t in g.tensors)
+    assert g.tensor("c").bytes().tobytes() == tensors[2][3].tobytes()
