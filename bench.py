@@ -197,6 +197,61 @@ def prefill_leg(a, dev, mats, threads, stream, timed):
     }
 
 
+def dense_leg(a, dev, threads, stream, timed):
+    """the dense projections through the same kernels, at C5's shapes
+    and a decode batch of 8 (packed math): one layer's attention projections q, k, v, o
+    (4096x4096, 1024x4096, 1024x4096, 4096x4096, Q4_K) and the output head (32000x4096,
+    Q6_K). Copies are rotated so each step's weights come from HBM, not the 256 MB MALL."""
+    import torch
+    import garuda_amd as G
+    from garuda_amd import moe as M
+
+    n = 8
+    shapes = {"q": (4096, 4096, G.Q4_K), "k": (1024, 4096, G.Q4_K), "v": (1024, 4096, G.Q4_K),
+              "o": (4096, 4096, G.Q4_K), "head": (32000, 4096, G.Q6_K)}
+    copies = {"attn": 16, "head": 4}
+    seed = SEED + 0x600
+    raws = {nm: M.quantize(qt, M.fill_gaussian(seed + i, r * c, 0.0, 0.02, threads), threads)
+            for i, (nm, (r, c, qt)) in enumerate(shapes.items())}
+    attn = [[G.DenseWeight(dev, shapes[nm][2], shapes[nm][0], shapes[nm][1], raws[nm]) for nm in "qkvo"]
+            for _ in range(copies["attn"])]
+    head = [G.DenseWeight(dev, G.Q6_K, 32000, 4096, raws["head"]) for _ in range(copies["head"])]
+    del raws
+    x = torch.from_numpy(M.fill_gaussian(seed + 0x10, n * 4096, 0.0, 1.0, threads).reshape(n, 4096)).cuda()
+    outs = {nm: torch.empty((n, shapes[nm][0]), dtype=torch.float32, device="cuda") for nm in shapes}
+    sh = stream.cuda_stream
+
+    def attn_step(i):
+        for W, nm in zip(attn[i % len(attn)], "qkvo"):
+            W.forward_async(x.data_ptr(), n, outs[nm].data_ptr(), sh)
+
+    def head_step(i):
+        head[i % len(head)].forward_async(x.data_ptr(), n, outs["head"].data_ptr(), sh)
+
+    res = {}
+    steps = max(64, a.steps // 4)
+    for name, step, nbytes in (
+            ("attention q,k,v,o", attn_step, sum(M.byte_size(qt, r * c) for nm, (r, c, qt) in shapes.items()
+                                                 if nm != "head")),
+            ("output head", head_step, M.byte_size(G.Q6_K, 32000 * 4096))):
+        for i in range(8):
+            step(i)
+        torch.cuda.synchronize()
+        ms, _ = timed(step, steps, False)
+        us = ms / steps * 1e3
+        gbs = (nbytes + n * 4096 * 4) / (us / 1e6) / 1e9
+        log(f"dense {name}: {us:.1f} us per call at batch {n}, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
+        res[name] = {"us_per_call": us, "weight_bytes": nbytes, "GB_s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS}
+    for ws in attn:
+        for W in ws:
+            W.release()
+    for W in head:
+        W.release()
+    return {"workload": "C5 dense projections at decode batch 8, packed math: one layer's q,k,v,o "
+                        "(Q4_K; 4096x4096, 1024x4096 x2, 4096x4096) and the 32000x4096 Q6_K output head; "
+                        f"{copies['attn']} and {copies['head']} copies rotated", "batch": n, "legs": res}
+
+
 def gguf_leg(a, dev, mats, threads):
     """The slab's source: the C2 layer written as a one-layer GGUF
     checkpoint (stacked Q4_K experts, F32 router), then Gguf.open + MoeLayer.from_gguf timed
@@ -277,6 +332,7 @@ def main():
                     help="tokens of the C3 prefill leg (Zipf-skewed routing, f32 math on MFMA); 0 skips it")
     ap.add_argument("--prefill-steps", type=int, default=40)
     ap.add_argument("--prefill-layers", type=int, default=2)
+    ap.add_argument("--dense", type=int, default=1, help="run the dense-projection leg (0: skip)")
     ap.add_argument("--gguf-reps", type=int, default=3,
                     help="timed open+register passes of the GGUF staging leg (0: skip it)")
     ap.add_argument("--extra", default="c4,c5_layer",
@@ -379,6 +435,7 @@ def main():
     for name in [x for x in a.extra.split(",") if x]:
         extra[name] = extra_leg(name, a, dev, threads, stream, timed)
 
+    dense = dense_leg(a, dev, threads, stream, timed) if a.dense else None
     gguf = gguf_leg(a, dev, mats, threads) if a.gguf_reps > 0 else None
 
     if a.calibrate_copy:
@@ -436,6 +493,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill": prefill,
         "configs": extra,
+        "dense_projections": dense,
         "gguf_staging": gguf,
         "sweep": {str(n): {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res.items()}
                   for n, res in results.items()},

@@ -32,6 +32,10 @@ class GmoeSlabStats(C.Structure):
                 ("bytes", u64), ("capacity", u64), ("h2d_bytes", u64)]
 
 
+class GmoeDenseDesc(C.Structure):
+    _fields_ = [("rows", u32), ("cols", u32), ("qtype", u32), ("math", u32), ("data", vp)]
+
+
 class GmoeGgufHeader(C.Structure):
     _fields_ = [("version", u32), ("n_tensors", u64), ("n_keys", u64), ("data_offset", u64),
                 ("file_bytes", u64)]
@@ -69,6 +73,10 @@ SIGNATURES = {
     "gmoe_expf": (i32, [vp, f32p, u64, f32p]),
     "gmoe_quantize": (i32, [u32, f32p, u64, vp, i32]),
     "gmoe_fill_gaussian": (i32, [u64, C.c_float, C.c_float, u64, f32p, i32]),
+    "gmoe_dense_register": (i32, [vp, C.POINTER(GmoeDenseDesc), u32p]),
+    "gmoe_dense_release": (i32, [vp, u32]),
+    "gmoe_dense_forward": (i32, [vp, u32, f32p, u32, f32p]),
+    "gmoe_dense_forward_async": (i32, [vp, u32, vp, u32, vp, vp]),
     "gmoe_gguf_open": (i32, [C.c_char_p, C.POINTER(vp)]),
     "gmoe_gguf_parse": (i32, [vp, u64, C.POINTER(vp)]),
     "gmoe_gguf_close": (None, [vp]),

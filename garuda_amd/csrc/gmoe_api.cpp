@@ -145,6 +145,16 @@ struct Timing {
   hipEvent_t a, b, c;
 };
 
+// A dense packed projection (Weight::Packed / Weight::Full, llama/mod.rs:43-85), tiled in
+// its own device allocation outside the expert slab's LRU: dense weights are read by every
+// token, so they stay resident.
+struct Dense {
+  uint32_t qtype, rows, cols, math;
+  uint8_t* tiled = nullptr;
+  uint64_t tiled_bytes = 0;
+  bool alive = true;
+};
+
 }  // namespace
 
 namespace gmoe {
@@ -158,6 +168,7 @@ struct gmoe_ctx {
   std::mutex mu;
   Slab slab;
   std::vector<std::unique_ptr<Layer>> layers;
+  std::vector<std::unique_ptr<Dense>> dense;
   std::list<std::pair<uint32_t, uint32_t>> lru;  // (layer, expert), least recent first
   gmoe_slab_stats stats{};
   uint8_t* pinned = nullptr;
@@ -486,6 +497,102 @@ gmoe_status check_ctx(gmoe_ctx* c) {
   return GMOE_OK;
 }
 
+// ---- dense projections: Weight::matmul_rows(0, xs, n, out) (llama/mod.rs:160-195) ----
+// The weight is the one "expert" of a down product: decode-sized calls quantise the
+// activations per 32 (packed math) or read them as f32 and run the K-split down kernel;
+// prefill-sized f32-math calls run it on MFMA over token tiles; the K slices are then
+// added in order into out [n][rows].
+LayerDev dense_dev(const Dense& W) {
+  LayerDev D{};
+  D.d = W.rows;
+  D.f = W.cols;
+  D.ne = 1;
+  D.k = 1;
+  D.math = W.math;
+  D.qt_gate = D.qt_up = D.qt_down = W.qtype;
+  return D;
+}
+
+struct DenseCarve {
+  FwdBufs B;
+  uint32_t ksg;
+  bool pf, int8;
+};
+
+// Scratch of one dense call: plan (base null) or carve.
+size_t plan_dense(const Dense& W, uint32_t n, uint8_t* base, DenseCarve* out) {
+  const LayerDev D = dense_dev(W);
+  const bool pf = prefill_dense_ok(D, n);
+  const bool int8 = !pf && uses_int8(W.math, W.qtype);
+  FwdBufs B{};
+  B.nslot = n;
+  B.ptile_cap = pf ? (n + kPfTok - 1) / kPfTok : 0;
+  const uint32_t ksg = pf ? 0u : down_ksg(D, n);  // prefill: from the carved buffers below
+  ScratchPlan P;
+  const size_t nx = (size_t)n * W.cols;
+  size_t o_work = P.add(sizeof(ExpertWork)), o_off = P.add(8), o_act = P.add(8), o_tok = P.add((size_t)n * 4),
+         o_pt = P.add((size_t)B.ptile_cap * 4 + 4);
+  size_t o_q = 0, o_s = 0, o_16 = 0, o_xh = 0, o_xsh = 0;
+  if (int8) {
+    o_q = P.add(nx);
+    o_s = P.add(nx / 32 * 4);
+    o_16 = P.add(nx / 16 * 4);
+  }
+  if (pf) {
+    o_xh = P.add(2 * nx * 2);
+    o_xsh = P.add(2 * (nx / 16) * 2);
+  }
+  const size_t o_y = P.add((size_t)kMaxKsg * n * W.rows * 4);
+  if (base && out) {
+    B.work = (ExpertWork*)(base + o_work);
+    B.offsets = (uint32_t*)(base + o_off);
+    B.active = (uint32_t*)(base + o_act);
+    B.slot_tok = (uint32_t*)(base + o_tok);
+    B.ptile = pf ? (uint32_t*)(base + o_pt) : nullptr;
+    if (int8) {
+      B.hq = (int8_t*)(base + o_q);
+      B.hsc = (float*)(base + o_s);
+      B.h16 = (int32_t*)(base + o_16);
+    }
+    if (pf) {
+      B.xh = B.hh = (_Float16*)(base + o_xh);
+      B.xsh = B.hsh = (_Float16*)(base + o_xsh);
+    }
+    B.y = (float*)(base + o_y);
+    out->B = B;
+    out->pf = pf;
+    out->int8 = int8;
+    out->ksg = pf ? prefill_ksg(D, B) : ksg;
+  }
+  return P.total;
+}
+
+gmoe_status run_dense(const Dense& W, const DenseCarve& cv, const float* x, uint32_t n, float* out, hipStream_t st) {
+  const LayerDev D = dense_dev(W);
+  FwdBufs B = cv.B;
+  HIP_TRY(launch_dense_setup(B.work, B.offsets, B.active, B.ptile, B.ptile_cap, B.slot_tok, W.tiled, n, st));
+  if (cv.pf) {
+    LayerDev Gd = D;  // the gather reads rows of the input's width
+    Gd.d = W.cols;
+    B.hs = x;
+    HIP_TRY(launch_gather_f16(Gd, B, n, st));
+    HIP_TRY(launch_prefill_down(D, B, n, cv.ksg, st));
+  } else {
+    if (cv.int8) HIP_TRY(launch_quant_act(x, n, W.cols, B.hq, B.hsc, B.h16, st));
+    else B.hf = const_cast<float*>(x);
+    HIP_TRY(launch_down(D, B, n, st));
+  }
+  HIP_TRY(launch_reduce_parts(B.y, cv.ksg, (size_t)n * W.rows, out, st));
+  return GMOE_OK;
+}
+
+gmoe_status get_dense(gmoe_ctx* c, uint32_t id, Dense** out) {
+  if (id >= c->dense.size() || !c->dense[id] || !c->dense[id]->alive)
+    return fail(GMOE_ERR_INFERENCE, "unknown dense weight id %u", id);
+  *out = c->dense[id].get();
+  return GMOE_OK;
+}
+
 gmoe_status get_layer(gmoe_ctx* c, uint32_t id, Layer** out) {
   if (id >= c->layers.size() || !c->layers[id] || !c->layers[id]->alive)
     return fail(GMOE_ERR_INFERENCE, "unknown layer id %u", id);
@@ -609,6 +716,8 @@ void gmoe_shutdown(gmoe_ctx* c) {
     hipEventDestroy(t.b);
     hipEventDestroy(t.c);
   }
+  for (auto& W : c->dense)
+    if (W && W->tiled) hipFree(W->tiled);
   if (c->slab.base) hipFree(c->slab.base);
   if (c->scratch) hipFree(c->scratch);
   if (c->pinned) hipHostFree(c->pinned);
@@ -785,6 +894,101 @@ gmoe_status gmoe_slab_get_stats(gmoe_ctx* c, gmoe_slab_stats* out) {
 }
 
 // ---- single steps ----
+
+gmoe_status gmoe_dense_register(gmoe_ctx* c, const gmoe_dense_desc* desc, uint32_t* id) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (!desc || !id || !desc->data) return fail(GMOE_ERR_INFERENCE, "null descriptor, data or id");
+  if (desc->math > 1) return fail(GMOE_ERR_CONFIG, "unknown math %u", desc->math);
+  if (desc->rows == 0 || desc->cols == 0) return fail(GMOE_ERR_MODEL, "empty dense weight");
+  uint64_t rb;
+  if (gmoe_status s = byte_size(desc->qtype, desc->cols, &rb)) return s;
+  if (!k_ok(desc->qtype, desc->cols)) return fail(GMOE_ERR_MODEL, "dense width %u is not a multiple of 32", desc->cols);
+  std::lock_guard<std::mutex> g(c->mu);
+  HIP_TRY(hipSetDevice(c->device));
+  auto W = std::make_unique<Dense>();
+  W->qtype = desc->qtype;
+  W->rows = desc->rows;
+  W->cols = desc->cols;
+  W->math = desc->math;
+  Unit un;
+  unit_of(W->qtype, &un);
+  W->tiled_bytes = tiled_bytes(un, W->rows, W->cols);
+  HIP_TRY(hipMalloc(&W->tiled, W->tiled_bytes));
+  Proj P;
+  P.qtype = W->qtype;
+  P.rows = W->rows;
+  P.cols = W->cols;
+  P.row_bytes = rb;
+  P.bytes_dev = W->tiled_bytes;
+  gmoe_status s = stage_proj(c, P, static_cast<const uint8_t*>(desc->data), W->tiled);
+  if (s == GMOE_OK && hipStreamSynchronize(c->copy_stream) != hipSuccess)
+    s = fail(GMOE_ERR_DEVICE, "staging the dense weight failed");
+  if (s != GMOE_OK) {
+    hipStreamSynchronize(c->copy_stream);
+    hipFree(W->tiled);
+    return s;
+  }
+  *id = (uint32_t)c->dense.size();
+  c->dense.push_back(std::move(W));
+  return GMOE_OK;
+}
+
+gmoe_status gmoe_dense_release(gmoe_ctx* c, uint32_t id) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  std::lock_guard<std::mutex> g(c->mu);
+  Dense* W;
+  if (gmoe_status s = get_dense(c, id, &W)) return s;
+  HIP_TRY(hipSetDevice(c->device));
+  HIP_TRY(hipDeviceSynchronize());  // queued work on any stream may still read it
+  hipFree(W->tiled);
+  W->tiled = nullptr;
+  W->alive = false;
+  return GMOE_OK;
+}
+
+gmoe_status gmoe_dense_forward(gmoe_ctx* c, uint32_t id, const float* xs, uint32_t n, float* out) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (!xs || !out) return fail(GMOE_ERR_INFERENCE, "null activation pointer");
+  if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
+  std::lock_guard<std::mutex> g(c->mu);
+  Dense* W;
+  if (gmoe_status s = get_dense(c, id, &W)) return s;
+  HIP_TRY(hipSetDevice(c->device));
+  ScratchPlan io;
+  const size_t o_x = io.add((size_t)n * W->cols * 4), o_o = io.add((size_t)n * W->rows * 4);
+  const size_t need = io.total + plan_dense(*W, n, nullptr, nullptr);
+  if (gmoe_status s = ensure_scratch(c, need)) return s;
+  DenseCarve cv;
+  plan_dense(*W, n, c->scratch + io.total, &cv);
+  hipStream_t st = c->stream;
+  float* dx = (float*)(c->scratch + o_x);
+  float* dout = (float*)(c->scratch + o_o);
+  HIP_TRY(hipMemcpyAsync(dx, xs, (size_t)n * W->cols * 4, hipMemcpyHostToDevice, st));
+  if (gmoe_status s = run_dense(*W, cv, dx, n, dout, st)) return s;
+  HIP_TRY(hipMemcpyAsync(out, dout, (size_t)n * W->rows * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return GMOE_OK;
+}
+
+gmoe_status gmoe_dense_forward_async(gmoe_ctx* c, uint32_t id, const float* d_xs, uint32_t n, float* d_out,
+                                     void* stream) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (!d_xs || !d_out) return fail(GMOE_ERR_INFERENCE, "null activation pointer");
+  if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
+  std::lock_guard<std::mutex> g(c->mu);
+  Dense* W;
+  if (gmoe_status s = get_dense(c, id, &W)) return s;
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+  const size_t need = plan_dense(*W, n, nullptr, nullptr);
+  if (need > c->scratch_bytes) {
+    HIP_TRY(hipDeviceSynchronize());  // growing the arena frees the old one
+    if (gmoe_status s = ensure_scratch(c, need)) return s;
+  }
+  DenseCarve cv;
+  plan_dense(*W, n, c->scratch, &cv);
+  return run_dense(*W, cv, d_xs, n, d_out, st);
+}
 
 gmoe_status gmoe_dequant(gmoe_ctx* c, uint32_t qt, const void* blocks, uint64_t nbytes, uint64_t n,
                          float* out) {

@@ -230,6 +230,9 @@ hipError_t launch_combine(const LayerDev& L, const FwdBufs& B, uint32_t n, uint3
 // Prefill path: whether it applies (f32 math, at least kPfMinSlots slots, supported
 // types and shapes), the per-slot fp16 gather of the activations, and the products.
 bool prefill_ok(const LayerDev& L, uint32_t n);
+bool prefill_dense_ok(const LayerDev& L, uint32_t n);
+hipError_t launch_dense_setup(ExpertWork* work, uint32_t* offsets, uint32_t* active, uint32_t* ptile,
+                              uint32_t ptile_cap, uint32_t* slot_tok, const uint8_t* w, uint32_t n, hipStream_t st);
 hipError_t launch_gather_f16(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 hipError_t launch_prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 hipError_t launch_prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);

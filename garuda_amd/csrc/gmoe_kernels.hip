@@ -935,6 +935,44 @@ bool prefill_ok(const LayerDev& L, uint32_t n) {
          prefill_type(L.qt_down) && L.d % 512 == 0 && L.f % 256 == 0 && L.ne < 65536;
 }
 
+// A dense projection run through the down-product path: rows = L.d, width = L.f.
+bool prefill_dense_ok(const LayerDev& L, uint32_t n) {
+  return L.math == 1 && n >= kPfMinSlots && prefill_type(L.qt_down) && L.d % 512 == 0 && L.f % 256 == 0;
+}
+
+// The work list of a dense projection: one "expert" (the weight, tiled) holding all n
+// tokens as slots 0..n-1, its token tiles, and the identity slot -> token map.
+__global__ void __launch_bounds__(256) k_dense_setup(ExpertWork* __restrict__ work, uint32_t* __restrict__ offsets,
+                                                     uint32_t* __restrict__ active, uint32_t* __restrict__ ptile,
+                                                     uint32_t ptile_cap, uint32_t* __restrict__ slot_tok,
+                                                     const uint8_t* w, uint32_t n) {
+  const uint32_t t = threadIdx.x;
+  if (t == 0) {
+    ExpertWork e;
+    e.w[0] = e.w[1] = e.w[2] = w;
+    e.e = 0;
+    e.s0 = 0;
+    e.m = n;
+    e.pad = 0;
+    work[0] = e;
+    offsets[0] = 0;
+    offsets[1] = n;
+    active[0] = 1;
+    active[1] = 0;
+  }
+  const uint32_t tiles = (n + kPfTok - 1) / kPfTok;
+  if (ptile)
+    for (uint32_t i = t; i < ptile_cap; i += blockDim.x) ptile[i] = i < tiles ? i : ~0u;
+  if (slot_tok)
+    for (uint32_t i = t; i < n; i += blockDim.x) slot_tok[i] = i;
+}
+
+hipError_t launch_dense_setup(ExpertWork* work, uint32_t* offsets, uint32_t* active, uint32_t* ptile,
+                              uint32_t ptile_cap, uint32_t* slot_tok, const uint8_t* w, uint32_t n, hipStream_t st) {
+  hipLaunchKernelGGL(k_dense_setup, dim3(1), dim3(256), 0, st, work, offsets, active, ptile, ptile_cap, slot_tok, w, n);
+  return hipGetLastError();
+}
+
 // The activations in slot order as fp16 pairs, x = hi + lo (hi = fp16(x), lo =
 // fp16(x - hi)), hi plane then lo plane, and with sw > 0 the sums of each sw values
 // (f32, left to right) as pairs the same way. One thread per 32 values.

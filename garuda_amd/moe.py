@@ -17,7 +17,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from ._lib import GmoeLayerDesc, GmoeSlabStats, GmoeTensor, lib
+from ._lib import GmoeDenseDesc, GmoeLayerDesc, GmoeSlabStats, GmoeTensor, lib
 
 # ggml type ids, quant/mod.rs:22-30
 F32, F16, Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 0, 1, 2, 8, 10, 11, 12, 13, 14
@@ -330,3 +330,48 @@ class MoeLayer:
 
     def release(self) -> None:
         _check(lib().gmoe_layer_release(self.dev.handle, self.id))
+
+
+class DenseWeight:
+    """A dense packed projection on a Device: `Weight::matmul_rows(0, xs, n, out)`
+    (llama/mod.rs:148-195) for the attention projections and the output head. `raw` is
+    `rows` packed rows of `cols` values of `qtype`; it is copied to the device."""
+
+    def __init__(self, dev: Device, qtype: int, rows: int, cols: int, raw, math: int = MATH_PACKED):
+        self.dev, self.qtype, self.rows, self.cols, self.math = dev, qtype, rows, cols, math
+        a = np.ascontiguousarray(raw, dtype=np.uint8) if not isinstance(raw, (bytes, bytearray, memoryview)) \
+            else np.frombuffer(raw, dtype=np.uint8)
+        if a.size != byte_size(qtype, rows * cols):
+            raise ModelError(f"dense weight: {a.size} bytes for {rows} x {cols} values of type {qtype}")
+        desc = GmoeDenseDesc(rows, cols, qtype, math, a.ctypes.data)
+        i = C.c_uint32()
+        _check(lib().gmoe_dense_register(dev.handle, C.byref(desc), C.byref(i)))
+        self.id = i.value
+
+    @classmethod
+    def from_gguf(cls, dev: Device, gguf, name: str, math: int = MATH_PACKED) -> "DenseWeight":
+        """The tensor `name` of a GGUF checkpoint (ggml dims [cols, rows])."""
+        t = gguf.tensor(name)
+        if t is None:
+            raise ModelError(f"gguf: tensor '{name}' not found")
+        cols = t.dims[0]
+        rows = t.n_elements() // max(cols, 1)
+        return cls(dev, t.ggml_type, rows, cols, t.bytes(), math)
+
+    def matmul_rows(self, xs: np.ndarray) -> np.ndarray:
+        """out [n, rows] for xs [n, cols]."""
+        xs = np.ascontiguousarray(xs, dtype=np.float32)
+        if xs.ndim == 1:
+            xs = xs.reshape(1, -1)
+        if xs.shape[1] != self.cols:
+            raise InferenceError(f"activations must be [n, {self.cols}], got {xs.shape}")
+        out = np.empty((xs.shape[0], self.rows), dtype=np.float32)
+        _check(lib().gmoe_dense_forward(self.dev.handle, self.id, _fp(xs), xs.shape[0], _fp(out)))
+        return out
+
+    def forward_async(self, d_xs: int, n: int, d_out: int, stream: int = 0) -> None:
+        _check(lib().gmoe_dense_forward_async(self.dev.handle, self.id, d_xs or None, n, d_out or None,
+                                              stream or None))
+
+    def release(self) -> None:
+        _check(lib().gmoe_dense_release(self.dev.handle, self.id))

@@ -138,6 +138,32 @@ int gmoe_expert_is_resident(gmoe_ctx* ctx, uint32_t layer_id, uint32_t expert);
 gmoe_status gmoe_expert_evict(gmoe_ctx* ctx, uint32_t layer_id, uint32_t expert);
 gmoe_status gmoe_slab_get_stats(gmoe_ctx* ctx, gmoe_slab_stats* out);
 
+/* ---- dense projections (Weight::matmul_rows, llama/mod.rs:148-195) ----
+ *
+ * The attention projections and the output head (llama/mod.rs:743-757, :880, :1198,
+ * :1240) through the expert kernels: a packed rows x cols matrix, tiled into device
+ * memory of its own (outside the expert slab, never evicted). PACKED math quantises the
+ * activations per 32 and dots them as quant::matmul does (quant/mod.rs:223-304); F32
+ * math uses the exact dequantised weights (simd::matmul), on MFMA for prefill-sized
+ * calls. A row's dot may be split over K and its slices added in order, so results
+ * match the reference within the layer tolerance rather than bit for bit. */
+typedef struct gmoe_dense_desc {
+  uint32_t rows, cols;          /* out_features x in_features */
+  uint32_t qtype, math;         /* ggml type id; GMOE_MATH_* */
+  const void* data;             /* rows packed rows, quant::byte_size(qtype, cols) bytes each;
+                                   copied during the call */
+} gmoe_dense_desc;
+
+gmoe_status gmoe_dense_register(gmoe_ctx* ctx, const gmoe_dense_desc* desc, uint32_t* dense_id);
+gmoe_status gmoe_dense_release(gmoe_ctx* ctx, uint32_t dense_id);
+/* Weight::matmul_rows(0, xs, n, out): xs [n x cols] -> out [n x rows], vector-major.
+ * Synchronous; host pointers. */
+gmoe_status gmoe_dense_forward(gmoe_ctx* ctx, uint32_t dense_id, const float* xs, uint32_t n, float* out);
+/* Device-pointer form on `stream` (NULL: the context's stream); returns without waiting.
+ * Shares the context's scratch with the layer calls: order them on one stream. */
+gmoe_status gmoe_dense_forward_async(gmoe_ctx* ctx, uint32_t dense_id, const float* d_xs, uint32_t n,
+                                     float* d_out, void* stream);
+
 /* ---- GGUF checkpoints: the slab's source (garuda/src/gguf/mod.rs; llama/mod.rs:551-637) ----
  *
  * A parsed GGUF file: header, metadata and tensor descriptors, with the reference's
