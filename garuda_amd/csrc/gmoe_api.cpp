@@ -152,8 +152,12 @@ struct Dense {
   uint32_t qtype, rows, cols, math;
   uint8_t* tiled = nullptr;
   uint64_t tiled_bytes = 0;
+  ExpertWork* work_tab = nullptr;  // [kDenseTab]: entry i is the call of i + 1 tokens
   bool alive = true;
 };
+// Calls of up to kDenseTab tokens read a precomputed work entry and the context's
+// identity table (slot -> token, and token tiles) instead of a setup launch.
+constexpr uint32_t kDenseTab = 2048;
 
 }  // namespace
 
@@ -169,6 +173,7 @@ struct gmoe_ctx {
   Slab slab;
   std::vector<std::unique_ptr<Layer>> layers;
   std::vector<std::unique_ptr<Dense>> dense;
+  uint32_t* ident = nullptr;  // [kDenseTab] = 0, 1, 2, ... (device)
   std::list<std::pair<uint32_t, uint32_t>> lru;  // (layer, expert), least recent first
   gmoe_slab_stats stats{};
   uint8_t* pinned = nullptr;
@@ -520,14 +525,14 @@ struct DenseCarve {
 };
 
 // Scratch of one dense call: plan (base null) or carve.
-size_t plan_dense(const Dense& W, uint32_t n, uint8_t* base, DenseCarve* out) {
+size_t plan_dense(const gmoe_ctx* c, const Dense& W, uint32_t n, uint8_t* base, DenseCarve* out) {
   const LayerDev D = dense_dev(W);
   const bool pf = prefill_dense_ok(D, n);
   const bool int8 = !pf && uses_int8(W.math, W.qtype);
   FwdBufs B{};
   B.nslot = n;
   B.ptile_cap = pf ? (n + kPfTok - 1) / kPfTok : 0;
-  const uint32_t ksg = pf ? 0u : down_ksg(D, n);  // prefill: from the carved buffers below
+  const uint32_t ksg = pf ? 0u : dense_ksg(D);  // prefill: from the carved buffers below
   ScratchPlan P;
   const size_t nx = (size_t)n * W.cols;
   size_t o_work = P.add(sizeof(ExpertWork)), o_off = P.add(8), o_act = P.add(8), o_tok = P.add((size_t)n * 4),
@@ -559,6 +564,11 @@ size_t plan_dense(const Dense& W, uint32_t n, uint8_t* base, DenseCarve* out) {
       B.xsh = B.hsh = (_Float16*)(base + o_xsh);
     }
     B.y = (float*)(base + o_y);
+    if (n <= kDenseTab) {  // the precomputed tables: no setup launch
+      B.work = W.work_tab + (n - 1);
+      B.slot_tok = c->ident;
+      if (pf) B.ptile = c->ident;
+    }
     out->B = B;
     out->pf = pf;
     out->int8 = int8;
@@ -570,7 +580,8 @@ size_t plan_dense(const Dense& W, uint32_t n, uint8_t* base, DenseCarve* out) {
 gmoe_status run_dense(const Dense& W, const DenseCarve& cv, const float* x, uint32_t n, float* out, hipStream_t st) {
   const LayerDev D = dense_dev(W);
   FwdBufs B = cv.B;
-  HIP_TRY(launch_dense_setup(B.work, B.offsets, B.active, B.ptile, B.ptile_cap, B.slot_tok, W.tiled, n, st));
+  if (n > kDenseTab)
+    HIP_TRY(launch_dense_setup(B.work, B.offsets, B.active, B.ptile, B.ptile_cap, B.slot_tok, W.tiled, n, st));
   if (cv.pf) {
     LayerDev Gd = D;  // the gather reads rows of the input's width
     Gd.d = W.cols;
@@ -580,7 +591,7 @@ gmoe_status run_dense(const Dense& W, const DenseCarve& cv, const float* x, uint
   } else {
     if (cv.int8) HIP_TRY(launch_quant_act(x, n, W.cols, B.hq, B.hsc, B.h16, st));
     else B.hf = const_cast<float*>(x);
-    HIP_TRY(launch_down(D, B, n, st));
+    HIP_TRY(launch_down(D, B, n, st, cv.ksg));
   }
   HIP_TRY(launch_reduce_parts(B.y, cv.ksg, (size_t)n * W.rows, out, st));
   return GMOE_OK;
@@ -717,7 +728,11 @@ void gmoe_shutdown(gmoe_ctx* c) {
     hipEventDestroy(t.c);
   }
   for (auto& W : c->dense)
-    if (W && W->tiled) hipFree(W->tiled);
+    if (W) {
+      if (W->tiled) hipFree(W->tiled);
+      if (W->work_tab) hipFree(W->work_tab);
+    }
+  if (c->ident) hipFree(c->ident);
   if (c->slab.base) hipFree(c->slab.base);
   if (c->scratch) hipFree(c->scratch);
   if (c->pinned) hipHostFree(c->pinned);
@@ -914,6 +929,27 @@ gmoe_status gmoe_dense_register(gmoe_ctx* c, const gmoe_dense_desc* desc, uint32
   unit_of(W->qtype, &un);
   W->tiled_bytes = tiled_bytes(un, W->rows, W->cols);
   HIP_TRY(hipMalloc(&W->tiled, W->tiled_bytes));
+  {
+    std::vector<ExpertWork> tab(kDenseTab);
+    for (uint32_t i = 0; i < kDenseTab; i++) tab[i] = ExpertWork{{W->tiled, W->tiled, W->tiled}, 0, 0, i + 1, 0};
+    hipError_t e = hipMalloc(&W->work_tab, tab.size() * sizeof(ExpertWork));
+    if (e == hipSuccess) e = hipMemcpy(W->work_tab, tab.data(), tab.size() * sizeof(ExpertWork), hipMemcpyHostToDevice);
+    if (e == hipSuccess && !c->ident) {
+      std::vector<uint32_t> id(kDenseTab);
+      for (uint32_t i = 0; i < kDenseTab; i++) id[i] = i;
+      e = hipMalloc(&c->ident, kDenseTab * 4);
+      if (e == hipSuccess) e = hipMemcpy(c->ident, id.data(), kDenseTab * 4, hipMemcpyHostToDevice);
+      if (e != hipSuccess && c->ident) {
+        hipFree(c->ident);
+        c->ident = nullptr;
+      }
+    }
+    if (e != hipSuccess) {
+      hipFree(W->tiled);
+      if (W->work_tab) hipFree(W->work_tab);
+      return fail(GMOE_ERR_DEVICE, "dense weight tables: %s", hipGetErrorString(e));
+    }
+  }
   Proj P;
   P.qtype = W->qtype;
   P.rows = W->rows;
@@ -926,6 +962,7 @@ gmoe_status gmoe_dense_register(gmoe_ctx* c, const gmoe_dense_desc* desc, uint32
   if (s != GMOE_OK) {
     hipStreamSynchronize(c->copy_stream);
     hipFree(W->tiled);
+    hipFree(W->work_tab);
     return s;
   }
   *id = (uint32_t)c->dense.size();
@@ -941,7 +978,9 @@ gmoe_status gmoe_dense_release(gmoe_ctx* c, uint32_t id) {
   HIP_TRY(hipSetDevice(c->device));
   HIP_TRY(hipDeviceSynchronize());  // queued work on any stream may still read it
   hipFree(W->tiled);
+  hipFree(W->work_tab);
   W->tiled = nullptr;
+  W->work_tab = nullptr;
   W->alive = false;
   return GMOE_OK;
 }
@@ -956,10 +995,10 @@ gmoe_status gmoe_dense_forward(gmoe_ctx* c, uint32_t id, const float* xs, uint32
   HIP_TRY(hipSetDevice(c->device));
   ScratchPlan io;
   const size_t o_x = io.add((size_t)n * W->cols * 4), o_o = io.add((size_t)n * W->rows * 4);
-  const size_t need = io.total + plan_dense(*W, n, nullptr, nullptr);
+  const size_t need = io.total + plan_dense(c, *W, n, nullptr, nullptr);
   if (gmoe_status s = ensure_scratch(c, need)) return s;
   DenseCarve cv;
-  plan_dense(*W, n, c->scratch + io.total, &cv);
+  plan_dense(c, *W, n, c->scratch + io.total, &cv);
   hipStream_t st = c->stream;
   float* dx = (float*)(c->scratch + o_x);
   float* dout = (float*)(c->scratch + o_o);
@@ -980,13 +1019,13 @@ gmoe_status gmoe_dense_forward_async(gmoe_ctx* c, uint32_t id, const float* d_xs
   if (gmoe_status s = get_dense(c, id, &W)) return s;
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t st = stream ? (hipStream_t)stream : c->stream;
-  const size_t need = plan_dense(*W, n, nullptr, nullptr);
+  const size_t need = plan_dense(c, *W, n, nullptr, nullptr);
   if (need > c->scratch_bytes) {
     HIP_TRY(hipDeviceSynchronize());  // growing the arena frees the old one
     if (gmoe_status s = ensure_scratch(c, need)) return s;
   }
   DenseCarve cv;
-  plan_dense(*W, n, c->scratch, &cv);
+  plan_dense(c, *W, n, c->scratch, &cv);
   return run_dense(*W, cv, d_xs, n, d_out, st);
 }
 

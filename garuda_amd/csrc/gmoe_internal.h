@@ -225,7 +225,9 @@ constexpr uint32_t kSpecMaxSlots = 512;
 bool spec_ok(const LayerDev& L, uint32_t n);
 hipError_t launch_spec_front(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st);
 hipError_t launch_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st);
-hipError_t launch_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+// ksg = 0: down_ksg(L, n * L.k)
+hipError_t launch_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st, uint32_t ksg = 0);
+uint32_t dense_ksg(const LayerDev& L);
 hipError_t launch_combine(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
 // Prefill path: whether it applies (f32 math, at least kPfMinSlots slots, supported
 // types and shapes), the per-slot fp16 gather of the activations, and the products.

@@ -1046,8 +1046,19 @@ uint32_t prefill_ksg(const LayerDev& L, const FwdBufs& B) {
   return 1;
 }
 
-hipError_t launch_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
-  const uint32_t ksg = down_ksg(L, n * L.k);
+// K groups of a dense projection's down kernel (one matrix, no experts): enough for
+// about 960 workgroups (near four per CU), each wave keeping at least one unit.
+uint32_t dense_ksg(const LayerDev& L) {
+  Unit un;
+  if (!unit_of(L.qt_down, &un)) return 1;
+  const uint32_t tiles = (L.d + kTileRows - 1) / kTileRows;
+  const uint32_t ksg = (960 + tiles - 1) / tiles;
+  const uint32_t cap = max(1u, row_units(un, L.f) / kDnKS);
+  return max(1u, min(min(ksg, cap), kMaxKsg));
+}
+
+hipError_t launch_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st, uint32_t ksg_in) {
+  const uint32_t ksg = ksg_in ? ksg_in : down_ksg(L, n * L.k);
   switch (L.qt_down) {
 #define DN(T) case T: return units_down<T>(L, B, n, ksg, st);
     DN(Q4_K) DN(Q5_K) DN(Q6_K) DN(Q3_K) DN(Q2_K) DN(Q8_0) DN(Q4_0) DN(F16) DN(F32)
