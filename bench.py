@@ -252,6 +252,55 @@ def dense_leg(a, dev, threads, stream, timed):
                         f"{copies['attn']} and {copies['head']} copies rotated", "batch": n, "legs": res}
 
 
+def prefetch_leg(a, mats, threads):
+    """predictor-driven prefetch into a slab that holds 6 of the C2
+    layer's 8 experts, over a decode stream whose tokens drift (h_t = 0.9 h_{t-1} + 0.45
+    noise, so consecutive steps route alike). The same steps run without and with the
+    PrefetchEngine (depth = top-k); each step is the synchronous forward (staging what it
+    misses) plus, with prefetch, observe_step staging the predicted experts."""
+    import garuda_amd as G
+    from garuda_amd import moe as M
+    from garuda_amd.predict import ExpertPredictor, PrefetchEngine
+
+    expert_bytes = 3 * M.byte_size(G.Q4_K, F * D)
+    router = M.fill_gaussian(SEED + 0x700, NE * D, 0.0, 0.02, threads)
+    steps = a.prefetch_steps
+    res = {}
+    for mode in ("off", "on"):
+        dev2 = G.Device(0, slab_bytes=6 * (expert_bytes + (1 << 20)))
+        layer = G.MoeLayer(dev2, D, F, NE, K, router, mats["gate"], mats["up"], mats["down"], (G.Q4_K,) * 3)
+        eng = PrefetchEngine(dev2, ExpertPredictor(NE), depth=K) if mode == "on" else None
+        rng = np.random.default_rng(SEED & 0xffff)
+        h = rng.normal(0, 1, D).astype(np.float32)
+        prev, last = [], []
+        s0 = dev2.slab_stats()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            h = (0.9 * h + 0.45 * rng.normal(0, 1, D)).astype(np.float32)
+            _, ids, _ = layer.feed_forward_batch(h.reshape(1, D))
+            if eng is not None:
+                used = [int(x) for x in ids.reshape(-1)]
+                last = eng.observe_step(layer, 0, prev, used, last)
+                prev = used
+        dt = time.perf_counter() - t0
+        s1 = dev2.slab_stats()
+        r = {"ms_per_step": dt / steps * 1e3, "forward_misses": s1.misses - s0.misses,
+             "staged_GB": (s1.h2d_bytes - s0.h2d_bytes) / 1e9}
+        if eng is not None:
+            st = eng.predictor_stats()
+            r.update(precision=st.precision(), recall=st.recall(), prefetched=eng.launched, already_resident=eng.skipped)
+        res[mode] = r
+        layer.release()
+        dev2.close()
+    on, off = res["on"], res["off"]
+    log(f"prefetch: {steps} steps, slab of 6/8 experts: without {off['ms_per_step']:.2f} ms/step, "
+        f"{off['forward_misses']} forward misses; with {on['ms_per_step']:.2f} ms/step, {on['forward_misses']} "
+        f"misses, {on['prefetched']} prefetched, precision {on['precision']:.2f} recall {on['recall']:.2f}")
+    return {"workload": "C2 layer, slab of 6 of 8 experts, batch-1 decode stream with drifting tokens; "
+                        "synchronous forward per step (+ observe_step with prefetch)",
+            "steps": steps, "without": off, "with": on}
+
+
 def gguf_leg(a, dev, mats, threads):
     """The slab's source: the C2 layer written as a one-layer GGUF
     checkpoint (stacked Q4_K experts, F32 router), then Gguf.open + MoeLayer.from_gguf timed
@@ -333,6 +382,8 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=40)
     ap.add_argument("--prefill-layers", type=int, default=2)
     ap.add_argument("--dense", type=int, default=1, help="run the dense-projection leg (0: skip)")
+    ap.add_argument("--prefetch-steps", type=int, default=200,
+                    help="decode steps of the prefetch leg, each way (0: skip it)")
     ap.add_argument("--gguf-reps", type=int, default=3,
                     help="timed open+register passes of the GGUF staging leg (0: skip it)")
     ap.add_argument("--extra", default="c4,c5_layer",
@@ -436,6 +487,7 @@ def main():
         extra[name] = extra_leg(name, a, dev, threads, stream, timed)
 
     dense = dense_leg(a, dev, threads, stream, timed) if a.dense else None
+    prefetch = prefetch_leg(a, mats, threads) if a.prefetch_steps > 0 else None
     gguf = gguf_leg(a, dev, mats, threads) if a.gguf_reps > 0 else None
 
     if a.calibrate_copy:
@@ -494,6 +546,7 @@ def main():
         "prefill": prefill,
         "configs": extra,
         "dense_projections": dense,
+        "prefetch": prefetch,
         "gguf_staging": gguf,
         "sweep": {str(n): {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res.items()}
                   for n, res in results.items()},

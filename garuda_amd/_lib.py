@@ -51,6 +51,10 @@ class GmoeGgufTensorInfo(C.Structure):
                 ("offset", u64), ("n_elements", u64), ("nbytes", u64), ("data", vp)]
 
 
+class GmoePredictStats(C.Structure):
+    _fields_ = [("correct", u64), ("wasted", u64), ("missed", u64)]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "gmoe_abi_version": (u32, []),
@@ -77,6 +81,15 @@ SIGNATURES = {
     "gmoe_dense_release": (i32, [vp, u32]),
     "gmoe_dense_forward": (i32, [vp, u32, f32p, u32, f32p]),
     "gmoe_dense_forward_async": (i32, [vp, u32, vp, u32, vp, vp]),
+    "gmoe_predictor_create": (i32, [u32, C.POINTER(vp)]),
+    "gmoe_predictor_destroy": (None, [vp]),
+    "gmoe_predictor_observe": (i32, [vp, u32p, u32, u32p, u32]),
+    "gmoe_predictor_predict": (i32, [vp, u32p, u32, u32, u32p, u32p]),
+    "gmoe_predictor_score": (i32, [vp, u32p, u32, u32p, u32]),
+    "gmoe_predictor_stats": (i32, [vp, C.POINTER(GmoePredictStats)]),
+    "gmoe_predictor_get_counts": (i32, [vp, u32p, u64]),
+    "gmoe_predictor_set_counts": (i32, [vp, u32p, u64]),
+    "gmoe_prefetch_step": (i32, [vp, vp, u32, u32, u32p, u32, u32p, u32, u32p, u32, u32, u32p, u32p, u32p, u32p]),
     "gmoe_gguf_open": (i32, [C.c_char_p, C.POINTER(vp)]),
     "gmoe_gguf_parse": (i32, [vp, u64, C.POINTER(vp)]),
     "gmoe_gguf_close": (None, [vp]),

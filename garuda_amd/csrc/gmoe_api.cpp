@@ -253,8 +253,9 @@ void touch(gmoe_ctx* c, uint32_t l, uint32_t e) {
 gmoe_status evict(gmoe_ctx* c, uint32_t l, uint32_t e) {
   Layer& L = *c->layers[l];
   if (L.slot[e] < 0) return GMOE_OK;
-  // the slab region may still be read by queued work
-  HIP_TRY(hipStreamSynchronize(c->stream));
+  // the slab region may still be read by queued work, on the context's stream or on a
+  // caller's (gmoe_ffn_forward_async)
+  HIP_TRY(hipDeviceSynchronize());
   c->slab.release((uint64_t)L.slot[e], L.expert_bytes);
   L.slot[e] = -1;
   for (int p = 0; p < 3; p++) L.eptr_host[p * L.ne + e] = nullptr;
@@ -453,8 +454,11 @@ gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStr
     B.xh = B.xsh = B.hh = B.hsh = nullptr;
   }
   // decode calls that compute their router logits: the expert products start on the
-  // candidate experts, and the exact routing rides along in the gate/up launch
-  const bool spec = !pf && !B.logits_in && spec_ok(D, n);
+  // candidate experts, and the exact routing rides along in the gate/up launch. Any
+  // expert may be a candidate, so every one must be resident.
+  bool resident = true;
+  for (uint32_t e = 0; e < L.ne; e++) resident &= L.slot[e] >= 0;
+  const bool spec = !pf && !B.logits_in && resident && spec_ok(D, n);
   B.spec = spec ? 1u : 0u;
   if (!spec) B.nslot = n * L.k;
   RouteArgs ra{};
@@ -652,6 +656,13 @@ gmoe_status forward_host(gmoe_ctx* c, uint32_t lid, const float* hs, const float
       if (L->slot[kp.second] >= 0) c->stats.hits++;
       else c->stats.misses++;
       if (gmoe_status s = make_resident(c, lid, kp.second, true, &keep)) return s;
+    }
+    // Only the routed experts are resident now: the layer runs from these exact logits.
+    // The speculative front end would also compute products for candidate experts near
+    // the top-k cut, which need not be resident.
+    if (!B.logits_in) {
+      HIP_TRY(hipMemcpyAsync(cv.d_logits_in, B.logits, (size_t)n * L->ne * 4, hipMemcpyDeviceToDevice, st));
+      B.logits_in = cv.d_logits_in;
     }
   } else {
     for (uint32_t e = 0; e < L->ne; e++) touch(c, lid, e);
@@ -1027,6 +1038,47 @@ gmoe_status gmoe_dense_forward_async(gmoe_ctx* c, uint32_t id, const float* d_xs
   DenseCarve cv;
   plan_dense(c, *W, n, c->scratch, &cv);
   return run_dense(*W, cv, d_xs, n, d_out, st);
+}
+
+gmoe_status gmoe_prefetch_step(gmoe_ctx* c, gmoe_predictor* p, uint32_t lid, uint32_t base, const uint32_t* prev,
+                               uint32_t nprev, const uint32_t* used, uint32_t nused, const uint32_t* pl,
+                               uint32_t npl, uint32_t depth, uint32_t* pred, uint32_t* npred, uint32_t* launched,
+                               uint32_t* skipped) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (!p || !npred || (depth && !pred) || (nprev && !prev) || (nused && !used) || (npl && !pl))
+    return fail(GMOE_ERR_INFERENCE, "null predictor, ids or output");
+  // prefetch/mod.rs:84-100: score last step's guess, learn the transition, predict
+  if (npl)
+    if (gmoe_status s = gmoe_predictor_score(p, pl, npl, used, nused)) return s;
+  if (nprev)
+    if (gmoe_status s = gmoe_predictor_observe(p, prev, nprev, used, nused)) return s;
+  if (gmoe_status s = gmoe_predictor_predict(p, used, nused, depth, pred, npred)) return s;
+  uint32_t nl = 0, ns = 0;
+  std::lock_guard<std::mutex> g(c->mu);
+  Layer* L;
+  if (gmoe_status s = get_layer(c, lid, &L)) return s;
+  HIP_TRY(hipSetDevice(c->device));
+  // the experts this step used and the ones predicted stay; others may be evicted
+  std::vector<std::pair<uint32_t, uint32_t>> keep;
+  for (uint32_t i = 0; i < nused; i++)
+    if (used[i] >= base && used[i] - base < L->ne) keep.emplace_back(lid, used[i] - base);
+  for (uint32_t i = 0; i < *npred; i++)
+    if (pred[i] >= base && pred[i] - base < L->ne) keep.emplace_back(lid, pred[i] - base);
+  for (uint32_t i = 0; i < *npred; i++) {
+    if (pred[i] < base || pred[i] - base >= L->ne) continue;  // another layer's expert
+    const uint32_t e = pred[i] - base;
+    if (L->slot[e] >= 0) {
+      ns++;
+      continue;
+    }
+    gmoe_status s = make_resident(c, lid, e, true, &keep);
+    if (s == GMOE_ERR_CACHE) break;  // a prefetch that does not fit is dropped; the forward loads what it needs
+    if (s) return s;
+    nl++;
+  }
+  if (launched) *launched = nl;
+  if (skipped) *skipped = ns;
+  return GMOE_OK;
 }
 
 gmoe_status gmoe_dequant(gmoe_ctx* c, uint32_t qt, const void* blocks, uint64_t nbytes, uint64_t n,

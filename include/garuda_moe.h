@@ -244,6 +244,50 @@ gmoe_status gmoe_gguf_layer_desc(gmoe_gguf* g, uint32_t layer, uint32_t gating, 
 gmoe_status gmoe_gguf_expert_ranges(gmoe_gguf* g, uint32_t layer, uint32_t expert, uint64_t offset[3],
                                     uint64_t length[3]);
 
+/* ---- expert prediction and prefetch into the slab (predictor/mod.rs, prefetch/mod.rs) ----
+ *
+ * The reference's ExpertPredictor (predictor/mod.rs:15-134): a first-order Markov model,
+ * transition counts C[prev][next] over global expert ids (layer * n_experts + expert),
+ * saturating at 2^32 - 1. predict(current, k) ranks every q by sum over p in current of
+ * C[p][q], keeps positive scores, orders them by score then id, and returns the first k;
+ * cold, it returns nothing. Host code; thread-safe (one writer or many readers). */
+typedef struct gmoe_predictor gmoe_predictor;
+typedef struct gmoe_predict_stats {
+  uint64_t correct, wasted, missed;  /* PredictStats (predictor/mod.rs:22-30) */
+} gmoe_predict_stats;
+
+gmoe_status gmoe_predictor_create(uint32_t n_experts, gmoe_predictor** out);  /* n_experts 0 acts as 1 */
+void gmoe_predictor_destroy(gmoe_predictor* p);
+/* ExpertPredictor::observe: every prev -> next pair counts once; ids >= n_experts are ignored. */
+gmoe_status gmoe_predictor_observe(gmoe_predictor* p, const uint32_t* prev, uint32_t n_prev, const uint32_t* next,
+                                   uint32_t n_next);
+/* ExpertPredictor::predict: up to k ids into out (capacity k); *n_out receives the count. */
+gmoe_status gmoe_predictor_predict(const gmoe_predictor* p, const uint32_t* current, uint32_t n_current,
+                                   uint32_t k, uint32_t* out, uint32_t* n_out);
+/* ExpertPredictor::score: each predicted id counts correct or wasted, each actual id
+ * not predicted counts missed. */
+gmoe_status gmoe_predictor_score(gmoe_predictor* p, const uint32_t* predicted, uint32_t n_predicted,
+                                 const uint32_t* actual, uint32_t n_actual);
+gmoe_status gmoe_predictor_stats(const gmoe_predictor* p, gmoe_predict_stats* out);
+/* The transition table, n_experts^2 counts row-major: read it out (to save a learned
+ * model) or load one back. */
+gmoe_status gmoe_predictor_get_counts(const gmoe_predictor* p, uint32_t* counts, uint64_t n);
+gmoe_status gmoe_predictor_set_counts(gmoe_predictor* p, const uint32_t* counts, uint64_t n);
+
+/* PrefetchEngine::observe_step (prefetch/mod.rs:77-106) for layer `layer_id` whose
+ * experts are ids [id_base, id_base + n_experts) of the predictor. It scores last step's
+ * prediction against `used`, learns previous -> used, predicts up to `depth` ids into
+ * `predicted` (*n_predicted receives the count) and stages the predicted experts of this
+ * layer that are not resident into the slab. *launched and *skipped (may be NULL) count
+ * the staged and the already-resident ones. Staging is host copy work: call this after
+ * queuing the step's gmoe_ffn_forward_async, and it overlaps that step's device work.
+ * Evicting an expert to make room waits for all queued device work first. */
+gmoe_status gmoe_prefetch_step(gmoe_ctx* ctx, gmoe_predictor* p, uint32_t layer_id, uint32_t id_base,
+                               const uint32_t* previous, uint32_t n_previous, const uint32_t* used,
+                               uint32_t n_used, const uint32_t* predicted_last, uint32_t n_predicted_last,
+                               uint32_t depth, uint32_t* predicted, uint32_t* n_predicted, uint32_t* launched,
+                               uint32_t* skipped);
+
 /* ---- single steps of the path, for parity tests (host pointers, synchronous) ---- */
 
 /* quant::dequantize (quant/mod.rs:104-114) on the device: n_elems values of qtype. */

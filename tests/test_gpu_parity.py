@@ -338,6 +338,34 @@ def test_small_slab_stages_experts_on_demand():
             layer.forward_async(1, 1, 1)  # not every expert resident: refused before any launch
 
 
+def test_small_slab_with_near_tie_candidates():
+    # d = 4096 makes the logits' error bound wide enough that a near-tie expert is a
+    # candidate of the speculative front end; with a slab of two experts it is not
+    # resident, so a call that stages experts must run from its exact routing only
+    d, f, ne, k = 4096, 512, 8, 2
+    rng = np.random.default_rng(21)
+    _, mats = make_layer(rng, d, f, ne, G.Q4_K, G.Q4_K)
+    u = rng.normal(0, 1, d).astype(np.float32)
+    u /= np.linalg.norm(u)
+    r = rng.normal(0, 0.02, (ne, d)).astype(np.float32)
+    r[0] = u                                                            # always first
+    r[1] = 0.5 * u
+    r[2] = r[1] + rng.normal(0, 1e-7, d).astype(np.float32)            # a near tie with expert 1
+    router = np.ascontiguousarray(r.reshape(-1))
+    per = sum(M.byte_size(G.Q4_K, f * d) for _ in range(3))
+    with G.Device(0, slab_bytes=2 * per + (1 << 16)) as small:
+        layer = G.MoeLayer(small, d, f, ne, k, router, mats["gate"], mats["up"], mats["down"], (G.Q4_K,) * 3)
+        L = oracle_layer(d, f, ne, k, router, mats, (G.Q4_K,) * 3, G.MATH_PACKED)
+        for step in range(6):
+            hs = (rng.normal(0, 1, (1, d)) + 8 * u).astype(np.float32)
+            say(f"near-tie small-slab step {step}")
+            out, ids, _ = layer.feed_forward_batch(hs)
+            wout, wids, _ = O.feed_forward_batch(L, hs)
+            assert ids[0, 0] == 0 and ids[0, 1] in (1, 2)
+            assert np.array_equal(ids, wids) and np.allclose(out, wout, rtol=RTOL, atol=ATOL)
+        layer.release()
+
+
 def test_bad_inputs_are_errors_not_crashes(dev):
     rng = np.random.default_rng(13)
     router, mats = make_layer(rng, 256, 512, 8, G.Q4_K, G.Q4_K)

@@ -1,0 +1,72 @@
+"""Predictor-driven prefetch into a slab too small for the layer (gmoe_prefetch_step):
+predicted experts become resident, and outputs are bit-identical to the same decode
+without prefetch (prefetch/mod.rs:1-10: a guess can never change the answer;
+prefetch_engine_warms_experts_without_changing_logits, llama/mod.rs:2116-2165)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import garuda_amd as G
+from garuda_amd.predict import ExpertPredictor, PrefetchEngine
+from tests.test_gpu_parity import bits, make_layer, say
+
+pytestmark = pytest.mark.gpu
+
+D, F, NE, K = 256, 512, 8, 2
+
+
+def decode(prefetch: bool, steps: int = 60):
+    rng = np.random.default_rng(0)
+    router, mats = make_layer(rng, D, F, NE, G.Q4_K, G.Q4_K)
+    expert_bytes = 3 * G.byte_size(G.Q4_K, D * F)
+    dev = G.Device(0, slab_bytes=4 * (expert_bytes + 4096))  # four of the eight experts
+    layer = G.MoeLayer(dev, D, F, NE, K, router, mats["gate"], mats["up"], mats["down"], (G.Q4_K,) * 3)
+    eng = PrefetchEngine(dev, ExpertPredictor(NE), depth=K) if prefetch else None
+    walk = np.random.default_rng(1)
+    h = walk.normal(0, 1, D).astype(np.float32)
+    outs, prev, last = [], [], []
+    try:
+        for step in range(steps):
+            h = (0.9 * h + 0.45 * walk.normal(0, 1, D)).astype(np.float32)  # correlated steps
+            out, ids, _ = layer.feed_forward_batch(h.reshape(1, D))
+            outs.append((out.copy(), ids.copy()))
+            if eng is not None:
+                used = [int(x) for x in ids.reshape(-1)]
+                last = eng.observe_step(layer, 0, prev, used, last)
+                for e in last:
+                    assert layer.is_resident(e), f"step {step}: predicted expert {e} not staged"
+                prev = used
+        stats = eng.predictor_stats() if eng else None
+        return outs, stats, (eng.launched, eng.skipped) if eng else None, dev.slab_stats()
+    finally:
+        layer.release()
+        dev.close()
+
+
+def test_prefetch_never_changes_outputs():
+    base, _, _, s0 = decode(False)
+    got, stats, (launched, skipped), s1 = decode(True)
+    for i, ((o0, i0), (o1, i1)) in enumerate(zip(base, got)):
+        assert np.array_equal(i0, i1) and np.array_equal(bits(o0), bits(o1)), f"step {i}"
+    say(f"predictor precision {stats.precision():.2f} recall {stats.recall():.2f}, launched {launched}, "
+        f"skipped {skipped}; forward misses {s0.misses} without, {s1.misses} with prefetch")
+    # the predictor learns (llama/mod.rs:2158-2163: it must predict something) and every
+    # in-layer prediction was either staged or already resident; whether prefetching
+    # saves forward misses depends on the slab's size and the guesses' precision
+    # (the last step's prediction is never scored)
+    assert stats.correct > 0 and 0 < stats.correct + stats.wasted <= launched + skipped
+
+
+def test_prefetch_step_refusals():
+    dev = G.Device(0, slab_bytes=64 << 20)
+    try:
+        eng = PrefetchEngine(dev, ExpertPredictor(NE), depth=K)
+
+        class Fake:
+            id = 123
+        with pytest.raises(G.InferenceError):
+            eng.observe_step(Fake(), 0, [0], [1], [])
+        assert PrefetchEngine(dev, ExpertPredictor(NE), enabled=False).observe_step(Fake(), 0, [0], [1], []) == []
+    finally:
+        dev.close()
