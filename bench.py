@@ -301,6 +301,53 @@ def prefetch_leg(a, mats, threads):
             "steps": steps, "without": off, "with": on}
 
 
+def attention_leg(a, dev, threads, stream, timed):
+    """decode attention over the paged KV cache at C5's shape (32 query
+    heads on 8 kv heads of 128, pages of 16 positions, 8 concurrent sequences), one layer:
+    the sequences' prompts are prefilled to a context, then batch-8 decode steps (one
+    token per sequence) are timed. Bytes per step: every sequence's keys and values over
+    its context, the kernel's HBM floor."""
+    import torch
+    import garuda_amd as G
+    from garuda_amd.attention import KvCache
+
+    nh, nkv, hd, nseq = 32, 8, 128, 8
+    res = {}
+    for ctx_len in (128, 2048):
+        steps = 64
+        kv = KvCache(dev, 1, nh, nkv, hd, block_size=16, max_positions=ctx_len + steps + 8, max_seqs=nseq)
+        seqs = [kv.open_seq() for _ in range(nseq)]
+        g = torch.Generator(device="cpu").manual_seed(SEED & 0xffff)
+        chunk = 256
+        for p0 in range(0, ctx_len, chunk):  # prefill every sequence to ctx_len
+            m = min(chunk, ctx_len - p0)
+            ids = [s for s in seqs for _ in range(m)]
+            q = torch.randn(len(ids), nh * hd, generator=g).cuda()
+            k = torch.randn(len(ids), nkv * hd, generator=g).cuda()
+            v = torch.randn(len(ids), nkv * hd, generator=g).cuda()
+            o = torch.empty(len(ids), nh * hd, device="cuda")
+            kv.attention_async(0, ids, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), stream.cuda_stream)
+        torch.cuda.synchronize()
+        q = torch.randn(nseq, nh * hd, generator=g).cuda()
+        k = torch.randn(nseq, nkv * hd, generator=g).cuda()
+        v = torch.randn(nseq, nkv * hd, generator=g).cuda()
+        o = torch.empty(nseq, nh * hd, device="cuda")
+
+        def step(i):
+            kv.attention_async(0, seqs, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), stream.cuda_stream)
+
+        ms, _ = timed(step, steps, False)
+        us = ms / steps * 1e3
+        nbytes = nseq * nkv * hd * 4 * 2 * (ctx_len + steps // 2)
+        gbs = nbytes / (us / 1e6) / 1e9
+        log(f"attention ctx {ctx_len}: {us:.1f} us per batch-{nseq} decode step of one layer, {gbs:.0f} GB/s "
+            f"of K/V ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
+        res[str(ctx_len)] = {"us_per_step": us, "kv_bytes_per_step": nbytes, "GB_s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS}
+        kv.close()
+    return {"workload": "C5 attention, one layer: 8 sequences decoding (one token each) over a paged KV cache, "
+                        "32 query / 8 kv heads of 128, pages of 16, f32 K/V", "contexts": res}
+
+
 def gguf_leg(a, dev, mats, threads):
     """The slab's source: the C2 layer written as a one-layer GGUF
     checkpoint (stacked Q4_K experts, F32 router), then Gguf.open + MoeLayer.from_gguf timed
@@ -382,6 +429,7 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=40)
     ap.add_argument("--prefill-layers", type=int, default=2)
     ap.add_argument("--dense", type=int, default=1, help="run the dense-projection leg (0: skip)")
+    ap.add_argument("--attention", type=int, default=1, help="run the paged-attention leg (0: skip)")
     ap.add_argument("--prefetch-steps", type=int, default=200,
                     help="decode steps of the prefetch leg, each way (0: skip it)")
     ap.add_argument("--gguf-reps", type=int, default=3,
@@ -488,6 +536,7 @@ def main():
 
     dense = dense_leg(a, dev, threads, stream, timed) if a.dense else None
     prefetch = prefetch_leg(a, mats, threads) if a.prefetch_steps > 0 else None
+    attention = attention_leg(a, dev, threads, stream, timed) if a.attention else None
     gguf = gguf_leg(a, dev, mats, threads) if a.gguf_reps > 0 else None
 
     if a.calibrate_copy:
@@ -547,6 +596,7 @@ def main():
         "configs": extra,
         "dense_projections": dense,
         "prefetch": prefetch,
+        "attention": attention,
         "gguf_staging": gguf,
         "sweep": {str(n): {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res.items()}
                   for n, res in results.items()},

@@ -90,6 +90,13 @@ SIGNATURES = {
     "gmoe_predictor_get_counts": (i32, [vp, u32p, u64]),
     "gmoe_predictor_set_counts": (i32, [vp, u32p, u64]),
     "gmoe_prefetch_step": (i32, [vp, vp, u32, u32, u32p, u32, u32p, u32, u32p, u32, u32, u32p, u32p, u32p, u32p]),
+    "gmoe_kv_create": (i32, [vp, vp, C.POINTER(vp)]),
+    "gmoe_kv_destroy": (None, [vp]),
+    "gmoe_kv_seq_open": (i32, [vp, u32p]),
+    "gmoe_kv_seq_close": (i32, [vp, u32]),
+    "gmoe_kv_seq_len": (i32, [vp, u32, u32, u32p]),
+    "gmoe_attention": (i32, [vp, u32, u32p, u32, f32p, f32p, f32p, f32p]),
+    "gmoe_attention_async": (i32, [vp, u32, u32p, u32, vp, vp, vp, vp, vp]),
     "gmoe_gguf_open": (i32, [C.c_char_p, C.POINTER(vp)]),
     "gmoe_gguf_parse": (i32, [vp, u64, C.POINTER(vp)]),
     "gmoe_gguf_close": (None, [vp]),

@@ -192,6 +192,12 @@ struct gmoe_ctx {
   uint64_t t_cnt = 0;
 };
 
+namespace gmoe {
+// for the other host modules (gmoe_kv.cpp)
+int ctx_device(gmoe_ctx* c) { return c->device; }
+hipStream_t ctx_stream(gmoe_ctx* c) { return c->stream; }
+}  // namespace gmoe
+
 namespace {
 
 // memcpy by up to kCopyThreads threads in 64 KiB-aligned slices: one thread reading a

@@ -1,0 +1,200 @@
+// gmoe_attn.hip — grouped-query decode attention over a paged KV cache.
+//
+// Reference: LlamaBackend::attend_one (garuda/src/llama/mod.rs:766-821) and
+// KVCacheState (cache/mod.rs:143-600). Per token: rotate q (every query head) and k
+// (every kv head) by the token's position (simd::rope, simd/mod.rs:196-206), append k
+// and v to the sequence's cache, and for each query head h attend over positions
+// [start, pos] of kv head h / group: scores = q·k * (1/sqrt(hd)), softmax (simd.rs
+// :132-158), context = sum of p_j * v_j. f32 throughout; the reductions run in
+// parallel, so results match the reference within the layer tolerance.
+//
+// Device layout. Pages of `bs` positions: keys [n_kv][bs][hd] then values in the same
+// layout, f32, so one kv head's rows of a page are contiguous. Each (sequence, layer) has
+// a page table of `ppseq` page ids. A call's entries
+// are tokens, each with its sequence's page table, its position and the position
+// attention starts at; entries of one sequence come in position order, so the append
+// kernel writes every entry's k and v before any attends (causal within the call).
+#include "gmoe_device.h"
+
+namespace gmoe {
+
+
+// simd::rope for pair i of a head at position pos: the frequency theta^(-2i/hd) and
+// the angle in f32 as the reference forms them.
+__device__ __forceinline__ void rope_pair(float& a, float& b, uint32_t i, uint32_t hd, uint32_t pos, float theta) {
+  const float freq = 1.0f / powf(theta, (2.0f * (float)i) / (float)hd);
+  const float ang = (float)pos * freq;
+  float s, c;
+  sincosf(ang, &s, &c);
+  const float x = a, y = b;
+  a = x * c - y * s;
+  b = x * s + y * c;
+}
+
+__device__ __forceinline__ AttnEntry entry(const AttnArgs& a, uint32_t i) { return a.ent ? a.ent[i] : a.inl[i]; }
+
+// Key row of position p, kv head h (the value row is bs * kv_dim floats further on).
+__device__ __forceinline__ const float* key_row(const AttnArgs& a, const AttnEntry& e, uint32_t p, uint32_t h) {
+  return a.pool + (size_t)e.pages[p / a.bs] * a.page_floats + ((size_t)h * a.bs + p % a.bs) * a.hd;
+}
+
+// grid (n, ceil(pairs / 256)), pairs = (n_heads + n_kv) * hd / 2
+__global__ void __launch_bounds__(256) k_rope_append(AttnArgs a) {
+  const uint32_t i = blockIdx.x, half = a.hd / 2, kvd = a.n_kv * a.hd;
+  const uint32_t pr = blockIdx.y * 256 + threadIdx.x, qpairs = a.n_heads * half;
+  const AttnEntry e = entry(a, i);
+  const uint32_t page = e.page, slot = e.pos % a.bs;
+  if (e.fresh && pr == 0) e.pages[e.pos / a.bs] = page;  // read by the attention kernel after this one
+  float* kp = a.pool + (size_t)page * a.page_floats + (size_t)slot * a.hd;  // head h at + h * bs * hd
+  float* vp = kp + (size_t)a.bs * kvd;
+  if (pr < qpairs) {
+    const uint32_t h = pr / half, j = pr % half;
+    const float* src = a.q + (size_t)i * a.n_heads * a.hd + h * a.hd;
+    float x = src[2 * j], y = src[2 * j + 1];
+    rope_pair(x, y, j, a.hd, e.pos, a.theta);
+    float* dst = a.qr + (size_t)i * a.n_heads * a.hd + h * a.hd;
+    dst[2 * j] = x;
+    dst[2 * j + 1] = y;
+  } else if (pr < qpairs + a.n_kv * half) {
+    const uint32_t p2 = pr - qpairs, h = p2 / half, j = p2 % half;
+    const float* src = a.k + (size_t)i * kvd + h * a.hd;
+    float x = src[2 * j], y = src[2 * j + 1];
+    rope_pair(x, y, j, a.hd, e.pos, a.theta);
+    const size_t hoff = (size_t)h * a.bs * a.hd;
+    kp[hoff + 2 * j] = x;
+    kp[hoff + 2 * j + 1] = y;
+    const float* vs = a.v + (size_t)i * kvd + h * a.hd;
+    vp[hoff + 2 * j] = vs[2 * j];
+    vp[hoff + 2 * j + 1] = vs[2 * j + 1];
+  }
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// grid (n, n_kv, nchunk), 256 threads: one chunk of kAttnChunk positions for the
+// `group` query heads of one kv head. The chunk's keys, then its values, are staged in
+// LDS (rows padded by one float, so a column read is conflict-free); thread (g, j) scores
+// position j for head g; per head the chunk's max m, the sum l of exp(s - m) and
+// o = sum of exp(s - m) * v go to part.
+// Dynamic LDS: tile [kAttnChunk][hd + 1], q [G][hd], p [G][kAttnChunk], (m, l) [G][2].
+inline uint32_t attn_lds_bytes(uint32_t G, uint32_t hd) {
+  return (kAttnChunk * (hd + 1) + G * hd + G * kAttnChunk + 2 * G) * 4;
+}
+
+__global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
+  extern __shared__ float lds_f[];
+  const uint32_t i = blockIdx.x, h = blockIdx.y, c = blockIdx.z, t = threadIdx.x;
+  const uint32_t G = a.n_heads / a.n_kv, hd = a.hd, kvd = a.n_kv * hd, kRowPad = hd + 1;
+  float* tile = lds_f;
+  float* qs = tile + kAttnChunk * kRowPad;
+  float* psb = qs + G * hd;  // [G][kAttnChunk]
+  float* mlb = psb + G * kAttnChunk;  // [G][2]
+  auto ps = [&](uint32_t g, uint32_t j) -> float& { return psb[g * kAttnChunk + j]; };
+  auto ml = [&](uint32_t g, uint32_t k) -> float& { return mlb[2 * g + k]; };
+  const AttnEntry e = entry(a, i);
+  const uint32_t end = e.pos + 1, p0 = e.start + c * kAttnChunk;
+  float* out = a.part + (((size_t)i * a.n_heads + h * G) * a.nchunk + c) * (hd + 2);
+  const size_t gstride = (size_t)a.nchunk * (hd + 2);
+  if (p0 >= end) {  // past the entry's span: an empty chunk
+    if (t < G) {
+      out[t * gstride + hd] = -INFINITY;
+      out[t * gstride + hd + 1] = 0.0f;
+    }
+    return;
+  }
+  const uint32_t cnt = min(kAttnChunk, end - p0);
+  for (uint32_t x = t; x < G * hd; x += 256) qs[x] = a.qr[(size_t)i * a.n_heads * hd + (h * G) * hd + x];
+  // keys: row j of the chunk, 4 floats a thread per step, rows contiguous within a page
+  const uint32_t q4 = hd / 4;
+  for (uint32_t x = t; x < cnt * q4; x += 256) {
+    const uint32_t j = x / q4, d4 = x % q4;
+    const float4 v4 = *reinterpret_cast<const float4*>(key_row(a, e, p0 + j, h) + 4 * d4);
+    float* dst = tile + j * kRowPad + 4 * d4;
+    dst[0] = v4.x; dst[1] = v4.y; dst[2] = v4.z; dst[3] = v4.w;
+  }
+  __syncthreads();
+  // scores: thread (g, j) for g < G, j < kAttnChunk
+  for (uint32_t x = t; x < G * kAttnChunk; x += 256) {
+    const uint32_t g = x / kAttnChunk, j = x % kAttnChunk;
+    float s = -INFINITY;
+    if (j < cnt) {
+      const float* kr = tile + j * kRowPad;
+      const float* qg = qs + g * hd;
+      float acc = 0.0f;
+      for (uint32_t d = 0; d < hd; d++) acc = fmaf(qg[d], kr[d], acc);
+      s = acc * a.scale;
+    }
+    ps(g, j) = s;
+  }
+  __syncthreads();
+  // per head: max and sum over the chunk, one wave per head in turn
+  const uint32_t lane = t & 63, w = t >> 6;
+  for (uint32_t g = w; g < G; g += 4) {
+    const float s = ps(g, lane);  // kAttnChunk == 64: one position a lane
+    const float m = wave_max(s);
+    const float pv = lane < cnt ? gm_expf(s - m) : 0.0f;
+    ps(g, lane) = pv;
+    const float l = wave_sum(pv);
+    if (lane == 0) {
+      ml(g, 0) = m;
+      ml(g, 1) = l;
+    }
+  }
+  __syncthreads();
+  // values into the same tile
+  for (uint32_t x = t; x < cnt * q4; x += 256) {
+    const uint32_t j = x / q4, d4 = x % q4;
+    const float4 v4 = *reinterpret_cast<const float4*>(key_row(a, e, p0 + j, h) + (size_t)a.bs * kvd + 4 * d4);
+    float* dst = tile + j * kRowPad + 4 * d4;
+    dst[0] = v4.x; dst[1] = v4.y; dst[2] = v4.z; dst[3] = v4.w;
+  }
+  __syncthreads();
+  for (uint32_t x = t; x < G * hd; x += 256) {
+    const uint32_t g = x / hd, d = x % hd;
+    float acc = 0.0f;
+    for (uint32_t j = 0; j < cnt; j++) acc = fmaf(ps(g, j), tile[j * kRowPad + d], acc);
+    out[g * gstride + d] = acc;
+  }
+  if (t < G) {
+    out[t * gstride + hd] = ml(t, 0);
+    out[t * gstride + hd + 1] = ml(t, 1);
+  }
+}
+
+// grid (n, n_heads), hd threads: the chunks merged, context = o / l.
+__global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
+  const uint32_t i = blockIdx.x, hh = blockIdx.y, d = threadIdx.x, hd = a.hd;
+  const float* base = a.part + ((size_t)i * a.n_heads + hh) * a.nchunk * (hd + 2);
+  float M = -INFINITY;
+  for (uint32_t c = 0; c < a.nchunk; c++) M = fmaxf(M, base[(size_t)c * (hd + 2) + hd]);
+  float L = 0.0f, O = 0.0f;
+  for (uint32_t c = 0; c < a.nchunk; c++) {
+    const float m = base[(size_t)c * (hd + 2) + hd];
+    if (m == -INFINITY) continue;
+    const float f = gm_expf(m - M);
+    L = fmaf(base[(size_t)c * (hd + 2) + hd + 1], f, L);
+    if (d < hd) O = fmaf(base[(size_t)c * (hd + 2) + d], f, O);
+  }
+  if (d < hd) a.ctx[(size_t)i * a.n_heads * hd + hh * hd + d] = O / L;
+}
+
+hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
+  const uint32_t pairs = (a.n_heads + a.n_kv) * a.hd / 2;
+  hipLaunchKernelGGL(k_rope_append, dim3(a.n, (pairs + 255) / 256), dim3(256), 0, st, a);
+  static const bool once = hipFuncSetAttribute((const void*)k_attn_partial, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)attn_lds_bytes(kAttnMaxGroup, kAttnMaxHd)) == hipSuccess;
+  (void)once;
+  hipLaunchKernelGGL(k_attn_partial, dim3(a.n, a.n_kv, a.nchunk), dim3(256), attn_lds_bytes(a.n_heads / a.n_kv, a.hd),
+                     st, a);
+  hipLaunchKernelGGL(k_attn_combine, dim3(a.n, a.n_heads), dim3(a.hd), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace gmoe

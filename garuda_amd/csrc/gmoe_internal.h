@@ -246,6 +246,35 @@ uint32_t down_ksg(const LayerDev& L, uint32_t pairs);
 hipError_t launch_reduce_parts(const float* parts, uint32_t ksg, size_t count, float* out, hipStream_t st);
 // Rows [r0, r0 + nrows) of a packed matrix (raw rows of row_bytes each, r0 a multiple of
 // 64) -> the tiles they make up in the tiled layout of the whole matrix at dst.
+// ---- decode attention over a paged KV cache (gmoe_attn.hip) ----
+struct AttnEntry {
+  uint32_t* pages;  // the sequence's page table for this layer
+  uint32_t pos;     // this token's position
+  uint32_t start;   // first position it attends to (sliding window)
+  uint32_t page;    // the page holding pos
+  uint32_t fresh;   // 1: pos opens that page; the append records it in the table
+};
+
+constexpr uint32_t kAttnInline = 16;  // entries carried in the kernel arguments
+struct AttnArgs {
+  const AttnEntry* ent;  // [n] in device memory, or null: n <= kAttnInline entries in `inl`
+  AttnEntry inl[kAttnInline];
+  uint32_t n, n_heads, n_kv, hd, bs;
+  float theta, scale;
+  float* pool;           // page pool
+  uint64_t page_floats;  // 2 * bs * kv_dim
+  const float* q;        // [n][n_heads * hd]
+  const float* k;        // [n][kv_dim]
+  const float* v;        // [n][kv_dim]
+  float* qr;             // [n][n_heads * hd] rotated q
+  float* part;           // [n][n_heads][nchunk][hd + 2]: chunk partials (o, m, l)
+  uint32_t nchunk;       // chunks of kAttnChunk positions per entry
+  float* ctx;            // [n][n_heads * hd]
+};
+
+constexpr uint32_t kAttnChunk = 64, kAttnMaxGroup = 16, kAttnMaxHd = 256;
+hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
+
 hipError_t launch_tile_rows(uint32_t qtype, const uint8_t* raw, uint32_t r0, uint32_t nrows, uint32_t rows,
                             uint32_t cols, uint8_t* dst, hipStream_t st);
 

@@ -244,6 +244,46 @@ gmoe_status gmoe_gguf_layer_desc(gmoe_gguf* g, uint32_t layer, uint32_t gating, 
 gmoe_status gmoe_gguf_expert_ranges(gmoe_gguf* g, uint32_t layer, uint32_t expert, uint64_t offset[3],
                                     uint64_t length[3]);
 
+/* ---- decode attention over a paged KV cache (llama/mod.rs:766-821, cache/mod.rs:143-600) ----
+ *
+ * A pool of device pages, each `block_size` positions of keys then values (f32, kv_dim =
+ * n_kv_heads * head_dim wide), shared by every sequence and layer; each (sequence,
+ * layer) has its own length and page table, as KVCacheState does per layer. An
+ * attention call takes one token per entry (several entries of one sequence are its
+ * consecutive positions, in order), rotates q and k by the token's position (simd::rope),
+ * appends k and v, and attends over [start, position]: start is 0, or position + 1 -
+ * sliding_window when a window is set (KVCacheState::attention_start). The context
+ * window is max_positions; a call that would exceed it, or find no free page, is
+ * refused before any device work (GarudaError::Cache). Spill to storage is not done: the
+ * pool lives in HBM. */
+typedef struct gmoe_kv gmoe_kv;
+typedef struct gmoe_kv_desc {
+  uint32_t n_layers, n_heads, n_kv_heads, head_dim;  /* head_dim even, <= 256; n_heads a multiple
+                                                        of n_kv_heads, at most 16 per kv head */
+  uint32_t block_size;      /* positions per page */
+  uint32_t max_positions;   /* context window of a sequence */
+  uint32_t sliding_window;  /* 0: attend to every earlier position */
+  uint32_t max_seqs;        /* sequences open at once */
+  uint64_t max_pages;       /* pages in the pool, over all sequences and layers */
+  float rope_theta;
+} gmoe_kv_desc;
+
+gmoe_status gmoe_kv_create(gmoe_ctx* ctx, const gmoe_kv_desc* desc, gmoe_kv** out);
+void gmoe_kv_destroy(gmoe_kv* kv);
+gmoe_status gmoe_kv_seq_open(gmoe_kv* kv, uint32_t* seq);
+/* Frees the sequence's pages (after queued device work has finished). */
+gmoe_status gmoe_kv_seq_close(gmoe_kv* kv, uint32_t seq);
+gmoe_status gmoe_kv_seq_len(const gmoe_kv* kv, uint32_t seq, uint32_t layer, uint32_t* len);
+/* Attention for n tokens in layer `layer`: q [n x n_heads*head_dim], k and v
+ * [n x kv_dim] (projected, not yet rotated), context [n x n_heads*head_dim] out.
+ * Synchronous; host pointers. */
+gmoe_status gmoe_attention(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, const float* q,
+                           const float* k, const float* v, float* context);
+/* Device-pointer form on `stream` (NULL: the context's stream). Calls on one KV cache
+ * must be ordered on one stream. */
+gmoe_status gmoe_attention_async(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, const float* d_q,
+                                 const float* d_k, const float* d_v, float* d_context, void* stream);
+
 /* ---- expert prediction and prefetch into the slab (predictor/mod.rs, prefetch/mod.rs) ----
  *
  * The reference's ExpertPredictor (predictor/mod.rs:15-134): a first-order Markov model,
