@@ -481,6 +481,11 @@ gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStr
     ra.gating = D.gating;
     ra.sec = std::min(D.d, kRouteSection);
     ra.tok_done = c->done + 64;
+    ra.offsets = B.offsets;
+    ra.slot_tok = B.slot_tok;
+    ra.comb_slot = B.slot_of;  // unused by the speculative dispatch: the combine's slots
+    ra.comb_w = B.slot_w;      // (n*k <= the n*ne candidate slots)
+    ra.combine = D.combine;
     HIP_TRY(launch_spec_front(D, B, n, quant ? 1 : 0, st));
   } else if (front_small_ok(D, n)) {
     HIP_TRY(launch_front_small(D, B, n, quant ? 1 : 0, true, st));

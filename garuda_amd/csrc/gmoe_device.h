@@ -682,6 +682,24 @@ __device__ __forceinline__ void route_logit(const RouteArgs& r, uint32_t x, floa
     r.ids[(size_t)t * r.k + lane] = id;
     r.w[(size_t)t * r.k + lane] = w;
   }
+  // the combine's order and slots: the pair's place among the token's k ids (experts are
+  // distinct), and its slot by search among the expert's candidate slots
+  uint32_t pos = lane;
+  if (r.combine == 0) {
+    pos = 0;
+    for (uint32_t j = 0; j < r.k; j++) pos += lane_u(id, j) < id ? 1u : 0u;
+  }
+  if (lane < r.k) {
+    uint32_t lo = r.offsets[id], hi = r.offsets[id + 1];
+    const uint32_t end = hi;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) / 2;
+      if (r.slot_tok[mid] < t) lo = mid + 1;
+      else hi = mid;
+    }
+    r.comb_slot[(size_t)t * r.k + pos] = lo < end && r.slot_tok[lo] == t ? lo : ~0u;
+    r.comb_w[(size_t)t * r.k + pos] = w;
+  }
   if (lane == 0) r.tok_done[t] = 0;
 }
 

@@ -152,7 +152,9 @@ struct FwdBufs {
   uint32_t* done;        // [1] workgroups of the front end that have finished; 0 between calls
   uint32_t nslot;        // rows of the slot-indexed arrays; y slices are nslot*d apart
   uint32_t* cand;        // [n][ne] speculative front end: each token's candidate experts, ~0u-padded
-  uint32_t spec;         // 1: slots hold candidate pairs; the combine finds (token, expert) by search
+  uint32_t spec;         // 1: slots hold candidate pairs; slot_of / slot_w hold the combine's
+                         // (slot, weight) per (token, position in combine order), written by
+                         // the exact routing (RouteArgs::comb_slot, comb_w)
 };
 
 // Exact routing carried by the gate/up launch of a speculative decode call: one extra
@@ -164,7 +166,14 @@ struct RouteArgs {
   uint32_t* ids;        // [n][k]
   float* w;             // [n][k]
   uint32_t* tok_done;   // [n] logits finished per token; 0 between calls
-  uint32_t n, ne, k, d, gating, sec;
+  // The combine's inputs, in its order (ascending expert id, or rank with combine = 1):
+  // each routed pair's slot among the candidate slots (offsets / slot_tok of the
+  // speculative dispatch, ~0u if the candidates missed it) and its weight.
+  const uint32_t* offsets;  // [ne+1]
+  const uint32_t* slot_tok; // candidate slots' tokens, in token order per expert
+  uint32_t* comb_slot;      // [n][k]
+  float* comb_w;            // [n][k]
+  uint32_t n, ne, k, d, gating, sec, combine;
 };
 constexpr uint32_t kRouteSection = 4096;  // values of d per LDS half in route_logit
 inline uint32_t route_logit_lds(uint32_t k, uint32_t sec) { return (2 * sec + 2 * k) * 4; }

@@ -830,6 +830,24 @@ __global__ void __launch_bounds__(256) k_combine(LayerDev L, FwdBufs B, uint32_t
   const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n || c >= d) return;
   const size_t part = (size_t)B.nslot * d;
+  float acc = 0.0f;
+  if (B.spec) {
+    // the exact routing left (slot, weight) in combine order; slot ~0u: a pair the
+    // candidates missed, which gives NaN (the candidate sets are supersets)
+    for (uint32_t i = 0; i < k; i++) {
+      const uint32_t slot = B.slot_of[(size_t)t * k + i];
+      const float wv = B.slot_w[(size_t)t * k + i];
+      float yv = __int_as_float(0x7fc00000);
+      if (slot != ~0u) {
+        const float* yp = B.y + (size_t)slot * d + c;
+        yv = yp[0];
+        for (uint32_t g = 1; g < ksg; g++) yv += yp[g * part];
+      }
+      acc = acc + yv * wv;
+    }
+    B.out[(size_t)t * d + c] = acc;
+    return;
+  }
   uint32_t order[32];  // top_k <= 32, checked at registration
   for (uint32_t i = 0; i < k; i++) order[i] = i;
   if (L.combine == 0) {
@@ -843,35 +861,13 @@ __global__ void __launch_bounds__(256) k_combine(LayerDev L, FwdBufs B, uint32_t
       order[j + 1] = v;
     }
   }
-  float acc = 0.0f;
   for (uint32_t i = 0; i < k; i++) {
-    uint32_t r = order[i];
-    float wv = B.w[(size_t)t * k + r];
-    float yv;
-    if (B.spec) {
-      // the (token, expert) pair among the expert's candidate slots, which are in token
-      // order; a pair the candidates missed gives NaN (the candidate sets are supersets)
-      const uint32_t e = B.ids[(size_t)t * k + r];
-      uint32_t lo = B.offsets[e], hi = B.offsets[e + 1];
-      const uint32_t end = hi;
-      while (lo < hi) {
-        const uint32_t mid = (lo + hi) / 2;
-        if (B.slot_tok[mid] < t) lo = mid + 1;
-        else hi = mid;
-      }
-      if (lo < end && B.slot_tok[lo] == t) {
-        const float* yp = B.y + (size_t)lo * d + c;
-        yv = yp[0];
-        for (uint32_t g = 1; g < ksg; g++) yv += yp[g * part];
-      } else {
-        yv = __int_as_float(0x7fc00000);
-      }
-    } else {
-      const uint32_t slot = B.slot_of[(size_t)t * k + r];
-      const float* yp = B.y + (size_t)slot * d + c;
-      yv = yp[0];
-      for (uint32_t g = 1; g < ksg; g++) yv += yp[g * part];
-    }
+    const uint32_t r = order[i];
+    const float wv = B.w[(size_t)t * k + r];
+    const uint32_t slot = B.slot_of[(size_t)t * k + r];
+    const float* yp = B.y + (size_t)slot * d + c;
+    float yv = yp[0];
+    for (uint32_t g = 1; g < ksg; g++) yv += yp[g * part];
     acc = acc + yv * wv;
   }
   B.out[(size_t)t * d + c] = acc;

@@ -55,15 +55,15 @@ __host__ __device__ constexpr uint32_t unit_count(uint32_t cols) {
 // One wave's stream over units [u0, u1) of the tile at `tile`: prime() issues the first
 // loads, run(body) calls body(u, w) with the lane's row unit u in w[] for every unit in
 // order. Set s of the ring holds units u0+s, u0+s+D, ...; a set is reloaded right after
-// its body, so D-1 = 1 unit is in flight during body(u) (a third set measured no faster
-// and cost the body its registers). Every
+// its body, so D-1 units are in flight during body(u). D = 2 by default (a third set
+// measured no faster and cost the body its registers); single-token gate/up uses 4. Every
 // load is unconditional (the unit index is clamped to the last unit, a re-read the L2
 // serves) and the loop always runs whole rounds of D, only the bodies past u1 being
 // skipped: the loads pending at each use are then the same on every path and the
 // compiler waits for exactly the set it uses.
-template <int QT>
+template <int QT, int D = 2>
 struct UnitStream {
-  static constexpr int NP = UT_<QT>::U / 16, NW = UT_<QT>::U / 4, D = 2;
+  static constexpr int NP = UT_<QT>::U / 16, NW = UT_<QT>::U / 4;
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   const uint8_t* src;
   uint32_t u0, u1, ulast;

@@ -227,8 +227,8 @@ __device__ __forceinline__ void unit_tokens(const uint32_t* w, const uint8_t* ac
 // With ra.n > 0 (speculative decode) the last row of the grid is the exact routing
 // instead: workgroup x < n*ne runs route_logit for token x / ne, expert x % ne. The
 // dispatcher starts it with the last wave of expert workgroups, whose tail hides it.
-template <int QT, bool PACKED>
-__global__ void __launch_bounds__(128, 2)
+template <int QT, bool PACKED, int D>
+__global__ void __launch_bounds__(128, D > 2 ? 1 : 2)
 k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __restrict__ slot_tok, uint32_t f,
            uint32_t d, uint32_t mt, const int8_t* __restrict__ xq,
            const float* __restrict__ xs, const int32_t* __restrict__ x16, const float* __restrict__ hs,
@@ -260,7 +260,7 @@ k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __r
   const uint32_t per = ActLds<QT, PACKED>::per_token(d);
   float* my = accs + wave * mt * 64 + lane;  // token t's sum of this lane's row: my[t * 64]
   const uint8_t* mat = wave == 0 ? W->w[0] : W->w[1];
-  UnitStream<QT> st(mat + (size_t)blockIdx.x * nunit * kTileRows * U, 0, nunit, lane);
+  UnitStream<QT, D> st(mat + (size_t)blockIdx.x * nunit * kTileRows * U, 0, nunit, lane);
   for (uint32_t c0 = 0; c0 < m_all; c0 += mt) {
     const uint32_t m = min(mt, m_all - c0);
     st.prime();  // the weights' first loads overlap the staging of the activations
@@ -345,6 +345,10 @@ k_dn_units(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32_
 // ---------------------------------------------------------------------------------
 
 constexpr uint32_t kLdsBudget = 160 * 1024 - 2048;
+// Single-token calls stream gate/up with a ring of 4 unit sets: at one token the grid
+// has fewer waves than SIMDs, so the registers cost no occupancy, and on the C2 layer the
+// launch took 33.7 us instead of 35.4. At 2 or 4 tokens the deeper ring was slower.
+constexpr uint32_t kDeepRingTokens = 1;
 
 template <class K>
 static bool allow_lds(K kernel) {
@@ -363,18 +367,18 @@ static uint32_t chunk_tokens(const LayerDev& L, uint32_t n, uint32_t per_token_b
   return min(min(n, usual), kLdsBudget / per_token_bytes);
 }
 
-template <int QT, bool PACKED>
+template <int QT, bool PACKED, int D>
 static hipError_t go_gu(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
   const uint32_t per = 2 * 64 * 4 + ActLds<QT, PACKED>::per_token(L.d) + 4;
   const uint32_t mt = chunk_tokens(L, n, per + 16);
   if (mt == 0) return hipErrorInvalidValue;
-  static const bool once = allow_lds(k_gu_units<QT, PACKED>);
+  static const bool once = allow_lds(k_gu_units<QT, PACKED, D>);
   (void)once;
   const uint32_t tiles = (L.f + kTileRows - 1) / kTileRows;
   uint32_t lds = mt * per + 16;
   if (ra.n) lds = max(lds, route_logit_lds(ra.k, ra.sec));
   const dim3 g(max(tiles, ra.n * ra.ne), min(L.ne, n * L.k) + (ra.n ? 1 : 0));
-  hipLaunchKernelGGL((k_gu_units<QT, PACKED>), g, dim3(128), lds, st, B.work, L.ne, B.slot_tok, L.f, L.d, mt, B.xq,
+  hipLaunchKernelGGL((k_gu_units<QT, PACKED, D>), g, dim3(128), lds, st, B.work, L.ne, B.slot_tok, L.f, L.d, mt, B.xq,
                      B.xs, B.x16, B.hs, B.hq, B.hsc, B.h16, B.hf, ra);
   return hipGetLastError();
 }
@@ -397,9 +401,9 @@ static hipError_t go_dn(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_
 template <int QT>
 hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
   if constexpr (has_int8_kernel(QT)) {
-    if (L.math == 0) return go_gu<QT, true>(L, B, n, ra, st);
+    if (L.math == 0) return n <= kDeepRingTokens ? go_gu<QT, true, 4>(L, B, n, ra, st) : go_gu<QT, true, 2>(L, B, n, ra, st);
   }
-  return go_gu<QT, false>(L, B, n, ra, st);
+  return go_gu<QT, false, 2>(L, B, n, ra, st);
 }
 
 template <int QT>
