@@ -384,10 +384,18 @@ __device__ void dispatch_wave(const FwdBufs& B, const uint8_t* const* eptr, uint
   }
   const uint64_t act = __ballot(lane < ne && cnt > 0);
   const uint32_t na = (uint32_t)__popcll(act);
+  // active slot: experts by descending pair count, then ascending id. The expert kernels'
+  // grids run the active slots in this order, so the experts with the most tokens (the
+  // longest workgroups) start first and the short ones fill in behind them.
+  uint32_t arank = 0;
+  for (uint32_t e = 0; e < ne; e++) {
+    const uint32_t ce = lane_u(cnt, e);
+    arank += (ce > cnt || (ce == cnt && e < lane)) ? 1u : 0u;
+  }
   if (lane < ne) {
     B.offsets[lane] = off;
     if (cnt > 0) {
-      const uint32_t a = (uint32_t)__popcll(act & below);
+      const uint32_t a = arank;
       B.active[1 + a] = lane;
       if (B.work) {
         ExpertWork& W = B.work[a];
@@ -411,7 +419,7 @@ __device__ void dispatch_wave(const FwdBufs& B, const uint8_t* const* eptr, uint
       tr += lane_u(nt, e);
     }
     if (lane < ne && cnt > 0) {
-      const uint32_t a = (uint32_t)__popcll(act & below);
+      const uint32_t a = arank;
       for (uint32_t t = 0; t < nt; t++) B.ptile[t0 + t] = (a << 16) | t;
     }
     for (uint32_t i = tr + lane; i < B.ptile_cap; i += 64) B.ptile[i] = ~0u;
