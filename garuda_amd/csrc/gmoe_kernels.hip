@@ -253,8 +253,8 @@ __global__ void __launch_bounds__(kRouteThreads) k_route(LayerDev L, FwdBufs B, 
 
 // Dispatch body: a stable counting sort of the (token, rank) pairs by expert id, which is
 // exactly members[e] of llama/mod.rs:967-972 laid end to end. One workgroup of 256
-// threads; sm holds nk + 3*ne + 2 words of LDS. Counts by LDS atomics, offsets and the
-// active list by one wave's running scans, then every pair's slot = its expert's offset +
+// threads; sm holds nk + 3*ne + 2 words of LDS. Counts by LDS atomics, the active slots
+// by rank of count, offsets by one wave's running scans, then every pair's slot = its expert's offset +
 // the pairs of that expert before it (counted chunk by chunk against the LDS copy of the
 // ids, the counts of earlier chunks carried per expert). Every thread must call this.
 __device__ void dispatch_block(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t* sm,
@@ -263,12 +263,25 @@ __device__ void dispatch_block(const LayerDev& L, const FwdBufs& B, uint32_t n, 
   uint32_t* idl = sm;            // [nk] ids
   uint32_t* cnt = sm + nk;       // [ne] counts, then the running count of earlier chunks
   uint32_t* start = cnt + ne;    // [ne] offsets
-  uint32_t* aidx = start + ne;   // [ne] active index (~0u: inactive)
+  uint32_t* aidx = start + ne;   // [ne] active slot (~0u: inactive)
   uint32_t* tot = aidx + ne;     // [2] active experts, token tiles
   for (uint32_t p = tid; p < nk; p += T) idl[p] = ids[p];
   for (uint32_t e = tid; e < ne; e += T) cnt[e] = 0;
   __syncthreads();
   for (uint32_t p = tid; p < nk; p += T) atomicAdd(&cnt[idl[p]], 1u);
+  __syncthreads();
+  // active slot: experts by descending pair count, then ascending id, so that the expert
+  // kernels' grids start the experts with the most tokens first
+  for (uint32_t e = tid; e < ne; e += T) {
+    const uint32_t c = cnt[e];
+    uint32_t r = 0;
+    if (c)
+      for (uint32_t j = 0; j < ne; j++) {
+        const uint32_t cj = cnt[j];
+        r += (cj > c || (cj == c && j < e)) ? 1u : 0u;
+      }
+    aidx[e] = c ? r : ~0u;
+  }
   __syncthreads();
   if (tid < 64) {  // running scans over the experts, 64 at a time
     const uint32_t lane = tid;
@@ -288,9 +301,8 @@ __device__ void dispatch_block(const LayerDev& L, const FwdBufs& B, uint32_t n, 
       }
       if (e < ne) {
         start[e] = off + ic - c;
-        aidx[e] = act ? na + ia - 1 : ~0u;
         if (act && B.ptile) {
-          const uint32_t a = na + ia - 1, t0 = nt + it - tl;
+          const uint32_t a = aidx[e], t0 = nt + it - tl;
           for (uint32_t t = 0; t < tl; t++) B.ptile[t0 + t] = (a << 16) | t;
         }
       }
