@@ -79,16 +79,24 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // grid (n, n_kv, nchunk), 256 threads: one chunk of kAttnChunk positions for the
-// `group` query heads of one kv head. The chunk's keys, then its values, are staged in
-// LDS (rows padded by one float, so a column read is conflict-free); thread (g, j) scores
-// position j for head g; per head the chunk's max m, the sum l of exp(s - m) and
-// o = sum of exp(s - m) * v go to part.
+// `group` query heads of one kv head. Every thread loads its share of the chunk's keys
+// and values from the pages at once, so the value loads' latency is hidden behind the
+// scores and the softmax; the keys, then the values, are staged in one LDS tile (rows
+// padded by one float, so a column read is conflict-free). Thread (g, j) scores position
+// j for head g; per head the chunk's max m, the sum l of exp(s - m) and o = sum of
+// exp(s - m) * v go to part.
 // Dynamic LDS: tile [kAttnChunk][hd + 1], q [G][hd], p [G][kAttnChunk], (m, l) [G][2].
 inline uint32_t attn_lds_bytes(uint32_t G, uint32_t hd) {
   return (kAttnChunk * (hd + 1) + G * hd + G * kAttnChunk + 2 * G) * 4;
 }
 
+// float4 items of a chunk's keys (or values) per thread for heads of up to MAXHD
+template <int MAXHD>
+constexpr int attn_items() { return kAttnChunk * (MAXHD / 4) / 256; }
+
+template <int MAXHD>
 __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
+  constexpr int kAttnItems = attn_items<MAXHD>();
   extern __shared__ float lds_f[];
   const uint32_t i = blockIdx.x, h = blockIdx.y, c = blockIdx.z, t = threadIdx.x;
   const uint32_t G = a.n_heads / a.n_kv, hd = a.hd, kvd = a.n_kv * hd, kRowPad = hd + 1;
@@ -110,14 +118,26 @@ __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
     return;
   }
   const uint32_t cnt = min(kAttnChunk, end - p0);
+  // keys and values: item x = row x / q4, float4 column x % q4; rows contiguous in a page
+  const uint32_t q4 = hd / 4, items = cnt * q4;
+  float4 kreg[kAttnItems], vreg[kAttnItems];
+#pragma unroll
+  for (int r = 0; r < kAttnItems; r++) {
+    const uint32_t x = t + 256 * r;
+    if (x < items) {
+      const float* kr = key_row(a, e, p0 + x / q4, h) + 4 * (x % q4);
+      kreg[r] = *reinterpret_cast<const float4*>(kr);
+      vreg[r] = *reinterpret_cast<const float4*>(kr + (size_t)a.bs * kvd);
+    }
+  }
   for (uint32_t x = t; x < G * hd; x += 256) qs[x] = a.qr[(size_t)i * a.n_heads * hd + (h * G) * hd + x];
-  // keys: row j of the chunk, 4 floats a thread per step, rows contiguous within a page
-  const uint32_t q4 = hd / 4;
-  for (uint32_t x = t; x < cnt * q4; x += 256) {
-    const uint32_t j = x / q4, d4 = x % q4;
-    const float4 v4 = *reinterpret_cast<const float4*>(key_row(a, e, p0 + j, h) + 4 * d4);
-    float* dst = tile + j * kRowPad + 4 * d4;
-    dst[0] = v4.x; dst[1] = v4.y; dst[2] = v4.z; dst[3] = v4.w;
+#pragma unroll
+  for (int r = 0; r < kAttnItems; r++) {
+    const uint32_t x = t + 256 * r;
+    if (x < items) {
+      float* dst = tile + (x / q4) * kRowPad + 4 * (x % q4);
+      dst[0] = kreg[r].x; dst[1] = kreg[r].y; dst[2] = kreg[r].z; dst[3] = kreg[r].w;
+    }
   }
   __syncthreads();
   // scores: thread (g, j) for g < G, j < kAttnChunk
@@ -134,8 +154,17 @@ __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
     ps(g, j) = s;
   }
   __syncthreads();
-  // per head: max and sum over the chunk, one wave per head in turn
+  // per head: max and sum over the chunk, one wave per head in turn; the values go into
+  // the tile meanwhile (the scores no longer read it)
   const uint32_t lane = t & 63, w = t >> 6;
+#pragma unroll
+  for (int r = 0; r < kAttnItems; r++) {
+    const uint32_t x = t + 256 * r;
+    if (x < items) {
+      float* dst = tile + (x / q4) * kRowPad + 4 * (x % q4);
+      dst[0] = vreg[r].x; dst[1] = vreg[r].y; dst[2] = vreg[r].z; dst[3] = vreg[r].w;
+    }
+  }
   for (uint32_t g = w; g < G; g += 4) {
     const float s = ps(g, lane);  // kAttnChunk == 64: one position a lane
     const float m = wave_max(s);
@@ -146,14 +175,6 @@ __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
       ml(g, 0) = m;
       ml(g, 1) = l;
     }
-  }
-  __syncthreads();
-  // values into the same tile
-  for (uint32_t x = t; x < cnt * q4; x += 256) {
-    const uint32_t j = x / q4, d4 = x % q4;
-    const float4 v4 = *reinterpret_cast<const float4*>(key_row(a, e, p0 + j, h) + (size_t)a.bs * kvd + 4 * d4);
-    float* dst = tile + j * kRowPad + 4 * d4;
-    dst[0] = v4.x; dst[1] = v4.y; dst[2] = v4.z; dst[3] = v4.w;
   }
   __syncthreads();
   for (uint32_t x = t; x < G * hd; x += 256) {
@@ -168,32 +189,78 @@ __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
   }
 }
 
-// grid (n, n_heads), hd threads: the chunks merged, context = o / l.
+// grid (n, n_heads), 256 threads: the chunks merged, context = o / l. The chunks' maxima
+// and sums are reduced over all threads; for o, thread (g, d) with g < 256 / hd adds the
+// chunks c = g, g + 256 / hd, ... of column d, 8 loads in flight, and the groups are then
+// added in group order.
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
+  v = is_max ? wave_max(v) : wave_sum(v);
+  const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();  // red is free (an earlier reduction's reads are done)
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+  for (uint32_t k = 1; k < blockDim.x / 64; k++) r = is_max ? fmaxf(r, red[k]) : r + red[k];
+  return r;
+}
+
 __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
-  const uint32_t i = blockIdx.x, hh = blockIdx.y, d = threadIdx.x, hd = a.hd;
-  const float* base = a.part + ((size_t)i * a.n_heads + hh) * a.nchunk * (hd + 2);
-  float M = -INFINITY;
-  for (uint32_t c = 0; c < a.nchunk; c++) M = fmaxf(M, base[(size_t)c * (hd + 2) + hd]);
-  float L = 0.0f, O = 0.0f;
-  for (uint32_t c = 0; c < a.nchunk; c++) {
-    const float m = base[(size_t)c * (hd + 2) + hd];
-    if (m == -INFINITY) continue;
-    const float f = gm_expf(m - M);
-    L = fmaf(base[(size_t)c * (hd + 2) + hd + 1], f, L);
-    if (d < hd) O = fmaf(base[(size_t)c * (hd + 2) + d], f, O);
+  __shared__ float red[4];
+  __shared__ float og[256];
+  const uint32_t i = blockIdx.x, hh = blockIdx.y, t = threadIdx.x, hd = a.hd, row = hd + 2, nc = a.nchunk;
+  const float* base = a.part + ((size_t)i * a.n_heads + hh) * nc * row;
+  float m = -INFINITY;
+  for (uint32_t c = t; c < nc; c += 256) m = fmaxf(m, base[(size_t)c * row + hd]);
+  const float M = block_reduce(m, true, red);
+  float l = 0.0f;
+  for (uint32_t c = t; c < nc; c += 256) {
+    const float mc = base[(size_t)c * row + hd];
+    if (mc != -INFINITY) l += base[(size_t)c * row + hd + 1] * gm_expf(mc - M);
   }
-  if (d < hd) a.ctx[(size_t)i * a.n_heads * hd + hh * hd + d] = O / L;
+  const float L = block_reduce(l, false, red);
+  const uint32_t ng = 256 / hd, g = t / hd, d = t % hd;
+  float o = 0.0f;
+  if (g < ng) {
+    constexpr int kIn = 8;
+    for (uint32_t c0 = g; c0 < nc; c0 += kIn * ng) {
+      float mv[kIn], pv[kIn];
+#pragma unroll
+      for (int r = 0; r < kIn; r++) {
+        const uint32_t c = c0 + r * ng;
+        mv[r] = -INFINITY;
+        if (c < nc) {
+          mv[r] = base[(size_t)c * row + hd];
+          pv[r] = base[(size_t)c * row + d];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < kIn; r++)
+        if (mv[r] != -INFINITY) o = fmaf(pv[r], gm_expf(mv[r] - M), o);
+    }
+  }
+  og[t] = o;
+  __syncthreads();
+  if (t < hd) {
+    float sum = og[t];
+    for (uint32_t k = 1; k < ng; k++) sum += og[k * hd + t];
+    a.ctx[(size_t)i * a.n_heads * hd + hh * hd + t] = sum / L;
+  }
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
   const uint32_t pairs = (a.n_heads + a.n_kv) * a.hd / 2;
   hipLaunchKernelGGL(k_rope_append, dim3(a.n, (pairs + 255) / 256), dim3(256), 0, st, a);
-  static const bool once = hipFuncSetAttribute((const void*)k_attn_partial, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               (int)attn_lds_bytes(kAttnMaxGroup, kAttnMaxHd)) == hipSuccess;
+  static const bool once =
+      hipFuncSetAttribute((const void*)k_attn_partial<128>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)attn_lds_bytes(kAttnMaxGroup, 128)) == hipSuccess &&
+      hipFuncSetAttribute((const void*)k_attn_partial<kAttnMaxHd>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)attn_lds_bytes(kAttnMaxGroup, kAttnMaxHd)) == hipSuccess;
   (void)once;
-  hipLaunchKernelGGL(k_attn_partial, dim3(a.n, a.n_kv, a.nchunk), dim3(256), attn_lds_bytes(a.n_heads / a.n_kv, a.hd),
-                     st, a);
-  hipLaunchKernelGGL(k_attn_combine, dim3(a.n, a.n_heads), dim3(a.hd), 0, st, a);
+  const dim3 grid(a.n, a.n_kv, a.nchunk);
+  const uint32_t lds = attn_lds_bytes(a.n_heads / a.n_kv, a.hd);
+  if (a.hd <= 128) hipLaunchKernelGGL(k_attn_partial<128>, grid, dim3(256), lds, st, a);
+  else hipLaunchKernelGGL(k_attn_partial<kAttnMaxHd>, grid, dim3(256), lds, st, a);
+  hipLaunchKernelGGL(k_attn_combine, dim3(a.n, a.n_heads), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
