@@ -79,31 +79,32 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // grid (n, n_kv, nchunk), 256 threads: one chunk of kAttnChunk positions for the
-// `group` query heads of one kv head. Every thread loads its share of the chunk's keys
-// and values from the pages at once, so the value loads' latency is hidden behind the
-// scores and the softmax; the keys, then the values, are staged in one LDS tile (rows
-// padded by one float, so a column read is conflict-free). Thread (g, j) scores position
-// j for head g; per head the chunk's max m, the sum l of exp(s - m) and o = sum of
-// exp(s - m) * v go to part.
-// Dynamic LDS: tile [kAttnChunk][hd + 1], q [G][hd], p [G][kAttnChunk], (m, l) [G][2].
+// `group` query heads of one kv head. Thread t takes position j = t / 4 of the chunk and
+// every fourth float4 column of its key and value rows from column t % 4 on, loaded from
+// the page at once (the value loads' latency hides behind the scores). Scores: the
+// thread's columns dotted with each head's q (in LDS), the four partial dots added by
+// lane shuffles. The values go to an LDS tile [kAttnChunk][hd]; per head the chunk's max
+// m, the sum l of exp(s - m) and o = sum of exp(s - m) * v go to part, o by float4
+// columns with the positions split over the spare threads (parts added in order).
+// Dynamic LDS: tile, q [G][hd], p [G][kAttnChunk], (m, l) [kAttnMaxGroup][2], o parts [256] float4.
 inline uint32_t attn_lds_bytes(uint32_t G, uint32_t hd) {
-  return (kAttnChunk * (hd + 1) + G * hd + G * kAttnChunk + 2 * G) * 4;
+  return (kAttnChunk * hd + G * hd + G * kAttnChunk + 2 * kAttnMaxGroup) * 4 + 256 * 16;
 }
 
-// float4 items of a chunk's keys (or values) per thread for heads of up to MAXHD
-template <int MAXHD>
-constexpr int attn_items() { return kAttnChunk * (MAXHD / 4) / 256; }
+static_assert(kAttnChunk * 4 == 256, "four threads per position of a chunk");
 
 template <int MAXHD>
 __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
-  constexpr int kAttnItems = attn_items<MAXHD>();
-  extern __shared__ float lds_f[];
+  constexpr int NR = MAXHD / 16;  // float4 columns of a row per thread
+  extern __shared__ float4 lds_v4[];
+  float* lds_f = reinterpret_cast<float*>(lds_v4);
   const uint32_t i = blockIdx.x, h = blockIdx.y, c = blockIdx.z, t = threadIdx.x;
-  const uint32_t G = a.n_heads / a.n_kv, hd = a.hd, kvd = a.n_kv * hd, kRowPad = hd + 1;
-  float* tile = lds_f;
-  float* qs = tile + kAttnChunk * kRowPad;
-  float* psb = qs + G * hd;  // [G][kAttnChunk]
-  float* mlb = psb + G * kAttnChunk;  // [G][2]
+  const uint32_t G = a.n_heads / a.n_kv, hd = a.hd, kvd = a.n_kv * hd, q4 = hd / 4;
+  float* tile = lds_f;                  // [kAttnChunk][hd] values
+  float* qs = tile + kAttnChunk * hd;   // [G][hd]
+  float* psb = qs + G * hd;             // [G][kAttnChunk]
+  float* mlb = psb + G * kAttnChunk;    // [kAttnMaxGroup][2]
+  float4* og = reinterpret_cast<float4*>(mlb + 2 * kAttnMaxGroup);  // [256]
   auto ps = [&](uint32_t g, uint32_t j) -> float& { return psb[g * kAttnChunk + j]; };
   auto ml = [&](uint32_t g, uint32_t k) -> float& { return mlb[2 * g + k]; };
   const AttnEntry e = entry(a, i);
@@ -118,57 +119,71 @@ __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
     return;
   }
   const uint32_t cnt = min(kAttnChunk, end - p0);
-  // keys and values: item x = row x / q4, float4 column x % q4; rows contiguous in a page
-  const uint32_t q4 = hd / 4, items = cnt * q4;
-  float4 kreg[kAttnItems], vreg[kAttnItems];
+  const uint32_t j = t >> 2, qq = t & 3;
+  const bool rowok = j < cnt;
+  float4 kreg[NR], vreg[NR];
+  {
+    const float* kr = key_row(a, e, p0 + (rowok ? j : 0u), h);
 #pragma unroll
-  for (int r = 0; r < kAttnItems; r++) {
-    const uint32_t x = t + 256 * r;
-    if (x < items) {
-      const float* kr = key_row(a, e, p0 + x / q4, h) + 4 * (x % q4);
-      kreg[r] = *reinterpret_cast<const float4*>(kr);
-      vreg[r] = *reinterpret_cast<const float4*>(kr + (size_t)a.bs * kvd);
+    for (int r = 0; r < NR; r++) {
+      const uint32_t col = qq + 4 * r;
+      kreg[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      vreg[r] = kreg[r];
+      if (rowok && col < q4) {
+        kreg[r] = *reinterpret_cast<const float4*>(kr + 4 * col);
+        vreg[r] = *reinterpret_cast<const float4*>(kr + (size_t)a.bs * kvd + 4 * col);
+      }
     }
   }
-  for (uint32_t x = t; x < G * hd; x += 256) qs[x] = a.qr[(size_t)i * a.n_heads * hd + (h * G) * hd + x];
-#pragma unroll
-  for (int r = 0; r < kAttnItems; r++) {
-    const uint32_t x = t + 256 * r;
-    if (x < items) {
-      float* dst = tile + (x / q4) * kRowPad + 4 * (x % q4);
-      dst[0] = kreg[r].x; dst[1] = kreg[r].y; dst[2] = kreg[r].z; dst[3] = kreg[r].w;
-    }
+  {
+    const float4* qsrc = reinterpret_cast<const float4*>(a.qr + (size_t)i * a.n_heads * hd + (size_t)h * G * hd);
+    for (uint32_t x = t; x < G * q4; x += 256) reinterpret_cast<float4*>(qs)[x] = qsrc[x];
   }
   __syncthreads();
-  // scores: thread (g, j) for g < G, j < kAttnChunk
-  for (uint32_t x = t; x < G * kAttnChunk; x += 256) {
-    const uint32_t g = x / kAttnChunk, j = x % kAttnChunk;
-    float s = -INFINITY;
-    if (j < cnt) {
-      const float* kr = tile + j * kRowPad;
-      const float* qg = qs + g * hd;
-      float acc = 0.0f;
-      for (uint32_t d = 0; d < hd; d++) acc = fmaf(qg[d], kr[d], acc);
-      s = acc * a.scale;
+  // scores of position j, every head of the group
+  float acc[kAttnMaxGroup];
+#pragma unroll
+  for (int g = 0; g < kAttnMaxGroup; g++) acc[g] = 0.0f;
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    const uint32_t col = qq + 4 * r;
+    if (col < q4) {
+      const float4 kv = kreg[r];
+#pragma unroll
+      for (int g = 0; g < kAttnMaxGroup; g++) {
+        if ((uint32_t)g < G) {
+          const float4 qv = reinterpret_cast<const float4*>(qs + g * hd)[col];
+          float v = acc[g];
+          v = fmaf(qv.x, kv.x, v);
+          v = fmaf(qv.y, kv.y, v);
+          v = fmaf(qv.z, kv.z, v);
+          v = fmaf(qv.w, kv.w, v);
+          acc[g] = v;
+        }
+      }
     }
-    ps(g, j) = s;
+  }
+#pragma unroll
+  for (int g = 0; g < kAttnMaxGroup; g++) {
+    if ((uint32_t)g < G) {
+      float v = acc[g];
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      if (qq == 0) ps(g, j) = rowok ? v * a.scale : -INFINITY;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    const uint32_t col = qq + 4 * r;
+    if (rowok && col < q4) reinterpret_cast<float4*>(tile + j * hd)[col] = vreg[r];
   }
   __syncthreads();
-  // per head: max and sum over the chunk, one wave per head in turn; the values go into
-  // the tile meanwhile (the scores no longer read it)
+  // per head: max and sum over the chunk, one wave per head in turn
   const uint32_t lane = t & 63, w = t >> 6;
-#pragma unroll
-  for (int r = 0; r < kAttnItems; r++) {
-    const uint32_t x = t + 256 * r;
-    if (x < items) {
-      float* dst = tile + (x / q4) * kRowPad + 4 * (x % q4);
-      dst[0] = vreg[r].x; dst[1] = vreg[r].y; dst[2] = vreg[r].z; dst[3] = vreg[r].w;
-    }
-  }
   for (uint32_t g = w; g < G; g += 4) {
-    const float s = ps(g, lane);  // kAttnChunk == 64: one position a lane
-    const float m = wave_max(s);
-    const float pv = lane < cnt ? gm_expf(s - m) : 0.0f;
+    const float sc = ps(g, lane);  // kAttnChunk == 64: one position a lane
+    const float m = wave_max(sc);
+    const float pv = lane < cnt ? gm_expf(sc - m) : 0.0f;
     ps(g, lane) = pv;
     const float l = wave_sum(pv);
     if (lane == 0) {
@@ -177,11 +192,43 @@ __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
     }
   }
   __syncthreads();
-  for (uint32_t x = t; x < G * hd; x += 256) {
-    const uint32_t g = x / hd, d = x % hd;
-    float acc = 0.0f;
-    for (uint32_t j = 0; j < cnt; j++) acc = fmaf(ps(g, j), tile[j * kRowPad + d], acc);
-    out[g * gstride + d] = acc;
+  // o: item = (head, float4 column); with few items the positions split into parts
+  const uint32_t items = G * q4;
+  const float4* tile4 = reinterpret_cast<const float4*>(tile);
+  auto pv_sum = [&](uint32_t item, uint32_t j0, uint32_t j1) {
+    const uint32_t g = item / q4, d4 = item % q4;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t jj = j0; jj < j1; jj++) {
+      const float p = ps(g, jj);
+      const float4 v = tile4[jj * q4 + d4];
+      o.x = fmaf(p, v.x, o.x);
+      o.y = fmaf(p, v.y, o.y);
+      o.z = fmaf(p, v.z, o.z);
+      o.w = fmaf(p, v.w, o.w);
+    }
+    return o;
+  };
+  auto put = [&](uint32_t item, float4 o) {
+    float* dst = out + (item / q4) * gstride + 4 * (item % q4);
+    dst[0] = o.x; dst[1] = o.y; dst[2] = o.z; dst[3] = o.w;
+  };
+  if (items <= 128) {
+    const uint32_t parts = items <= 64 ? 4u : 2u, span = kAttnChunk / parts;
+    if (t < items * parts) {
+      const uint32_t part = t / items, j0 = part * span;
+      og[t] = pv_sum(t % items, min(j0, cnt), min(j0 + span, cnt));
+    }
+    __syncthreads();
+    if (t < items) {
+      float4 o = og[t];
+      for (uint32_t part = 1; part < parts; part++) {
+        const float4 v = og[part * items + t];
+        o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
+      }
+      put(t, o);
+    }
+  } else {
+    for (uint32_t x = t; x < items; x += 256) put(x, pv_sum(x, 0, cnt));
   }
   if (t < G) {
     out[t * gstride + hd] = ml(t, 0);

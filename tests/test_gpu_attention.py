@@ -66,6 +66,23 @@ def test_continuous_batch_prefill_and_window(dev):
             assert kv.seq_len(s) == o.seq_len(s)
 
 
+@pytest.mark.parametrize("nh,nkv,hd", [(32, 2, 256), (16, 2, 96), (8, 1, 128)])
+def test_wide_heads_and_groups(dev, nh, nkv, hd):
+    # heads wider than 128 (the wide-head kernel), widths not a multiple of 16, and
+    # groups whose (head, column) items exceed one pass of the workgroup
+    rng = np.random.default_rng(hd)
+    with KvCache(dev, 1, nh, nkv, hd, block_size=16, max_positions=300, max_seqs=2) as kv:
+        o = KvOracle(1, nh, nkv, hd, max_positions=300)
+        seqs = [kv.open_seq() for _ in range(2)]
+        ids = [seqs[0]] * 150 + [seqs[1]] * 70  # prompts across chunks, one call
+        q, k, v = (rng.normal(size=(len(ids), w)) for w in (nh * hd, nkv * hd, nkv * hd))
+        say(f"wide heads nh={nh} nkv={nkv} hd={hd}: prefill")
+        check(kv.attention(0, ids, q, k, v), o.attention(0, ids, q, k, v), "prefill")
+        for step in range(3):
+            q, k, v = (rng.normal(size=(2, w)) for w in (nh * hd, nkv * hd, nkv * hd))
+            check(kv.attention(0, seqs, q, k, v), o.attention(0, seqs, q, k, v), f"decode {step}")
+
+
 def test_c5_head_shape(dev):
     # 32 query heads on 8 kv heads of 128, eight sequences
     nh, nkv, hd = 32, 8, 128
