@@ -198,7 +198,7 @@ def prefill_leg(a, dev, mats, threads, stream, timed):
 
 
 def dense_leg(a, dev, threads, stream, timed):
-    """the dense projections through the same kernels, at C5's shapes
+    """Dense projections (Weight::matmul_rows) through the same kernels, at C5's shapes
     and a decode batch of 8 (packed math): one layer's attention projections q, k, v, o
     (4096x4096, 1024x4096, 1024x4096, 4096x4096, Q4_K) and the output head (32000x4096,
     Q6_K). Copies are rotated so each step's weights come from HBM, not the 256 MB MALL."""
@@ -253,7 +253,7 @@ def dense_leg(a, dev, threads, stream, timed):
 
 
 def prefetch_leg(a, mats, threads):
-    """predictor-driven prefetch into a slab that holds 6 of the C2
+    """Predictor-driven prefetch into a slab that holds 6 of the C2
     layer's 8 experts, over a decode stream whose tokens drift (h_t = 0.9 h_{t-1} + 0.45
     noise, so consecutive steps route alike). The same steps run without and with the
     PrefetchEngine (depth = top-k); each step is the synchronous forward (staging what it
@@ -302,7 +302,7 @@ def prefetch_leg(a, mats, threads):
 
 
 def attention_leg(a, dev, threads, stream, timed):
-    """decode attention over the paged KV cache at C5's shape (32 query
+    """Decode attention over the paged KV cache at C5's shape (32 query
     heads on 8 kv heads of 128, pages of 16 positions, 8 concurrent sequences), one layer:
     the sequences' prompts are prefilled to a context, then batch-8 decode steps (one
     token per sequence) are timed. Bytes per step: every sequence's keys and values over
@@ -349,7 +349,7 @@ def attention_leg(a, dev, threads, stream, timed):
 
 
 def gguf_leg(a, dev, mats, threads):
-    """The slab's source: the C2 layer written as a one-layer GGUF
+    """The slab's source, a GGUF checkpoint: the C2 layer written as a one-layer GGUF
     checkpoint (stacked Q4_K experts, F32 router), then Gguf.open + MoeLayer.from_gguf timed
     to the end of staging: the mapped file's expert bytes copied through the pinned double
     buffer, over the host link, and tiled into the HBM slab. Beside it, the host link's own
@@ -440,7 +440,7 @@ def main():
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
-              "(expert-parallel sharding is a design note in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(the path would shard by expert, one exchange each way). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
