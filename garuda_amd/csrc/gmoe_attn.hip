@@ -236,61 +236,68 @@ __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
   }
 }
 
-// grid (n, n_heads), 256 threads: the chunks merged, context = o / l. The chunks' maxima
-// and sums are reduced over all threads; for o, thread (g, d) with g < 256 / hd adds the
-// chunks c = g, g + 256 / hd, ... of column d, 8 loads in flight, and the groups are then
-// added in group order.
-__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
-  v = is_max ? wave_max(v) : wave_sum(v);
-  const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  __syncthreads();  // red is free (an earlier reduction's reads are done)
-  if (lane == 0) red[w] = v;
-  __syncthreads();
-  float r = red[0];
-  for (uint32_t k = 1; k < blockDim.x / 64; k++) r = is_max ? fmaxf(r, red[k]) : r + red[k];
-  return r;
-}
-
+// grid (n, n_heads), 256 threads: the chunks merged, context = o / l, in one pass.
+// Thread (g, d) with g < 256 / hd runs over the chunks c = g, g + 256 / hd, ... of column
+// d (16 chunks in flight) with a running max: (M, L, O) is rescaled when a chunk's max
+// exceeds M. The groups are then merged in group order.
 __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
-  __shared__ float red[4];
-  __shared__ float og[256];
+  __shared__ float gm[256], gl[256], go[256];
   const uint32_t i = blockIdx.x, hh = blockIdx.y, t = threadIdx.x, hd = a.hd, row = hd + 2, nc = a.nchunk;
   const float* base = a.part + ((size_t)i * a.n_heads + hh) * nc * row;
-  float m = -INFINITY;
-  for (uint32_t c = t; c < nc; c += 256) m = fmaxf(m, base[(size_t)c * row + hd]);
-  const float M = block_reduce(m, true, red);
-  float l = 0.0f;
-  for (uint32_t c = t; c < nc; c += 256) {
-    const float mc = base[(size_t)c * row + hd];
-    if (mc != -INFINITY) l += base[(size_t)c * row + hd + 1] * gm_expf(mc - M);
-  }
-  const float L = block_reduce(l, false, red);
   const uint32_t ng = 256 / hd, g = t / hd, d = t % hd;
-  float o = 0.0f;
+  float M = -INFINITY, L = 0.0f, O = 0.0f;
   if (g < ng) {
-    constexpr int kIn = 8;
+    constexpr int kIn = 16;
     for (uint32_t c0 = g; c0 < nc; c0 += kIn * ng) {
-      float mv[kIn], pv[kIn];
+      float mv[kIn], lv[kIn], pv[kIn];
 #pragma unroll
       for (int r = 0; r < kIn; r++) {
         const uint32_t c = c0 + r * ng;
         mv[r] = -INFINITY;
         if (c < nc) {
-          mv[r] = base[(size_t)c * row + hd];
-          pv[r] = base[(size_t)c * row + d];
+          const float* rc = base + (size_t)c * row;
+          mv[r] = rc[hd];
+          lv[r] = rc[hd + 1];
+          pv[r] = rc[d];
         }
       }
 #pragma unroll
-      for (int r = 0; r < kIn; r++)
-        if (mv[r] != -INFINITY) o = fmaf(pv[r], gm_expf(mv[r] - M), o);
+      for (int r = 0; r < kIn; r++) {
+        if (mv[r] == -INFINITY) continue;  // an empty chunk
+        if (mv[r] > M) {
+          const float f = gm_expf(M - mv[r]);  // 0 while M is -inf
+          L = fmaf(L, f, lv[r]);
+          O = fmaf(O, f, pv[r]);
+          M = mv[r];
+        } else {
+          const float f = gm_expf(mv[r] - M);
+          L = fmaf(lv[r], f, L);
+          O = fmaf(pv[r], f, O);
+        }
+      }
     }
   }
-  og[t] = o;
+  gm[t] = M;
+  gl[t] = L;
+  go[t] = O;
   __syncthreads();
   if (t < hd) {
-    float sum = og[t];
-    for (uint32_t k = 1; k < ng; k++) sum += og[k * hd + t];
-    a.ctx[(size_t)i * a.n_heads * hd + hh * hd + t] = sum / L;
+    float Mt = gm[t], Lt = gl[t], Ot = go[t];
+    for (uint32_t k = 1; k < ng; k++) {
+      const float m2 = gm[k * hd + t];
+      if (m2 == -INFINITY) continue;
+      if (m2 > Mt) {
+        const float f = gm_expf(Mt - m2);
+        Lt = fmaf(Lt, f, gl[k * hd + t]);
+        Ot = fmaf(Ot, f, go[k * hd + t]);
+        Mt = m2;
+      } else {
+        const float f = gm_expf(m2 - Mt);
+        Lt = fmaf(gl[k * hd + t], f, Lt);
+        Ot = fmaf(go[k * hd + t], f, Ot);
+      }
+    }
+    a.ctx[(size_t)i * a.n_heads * hd + hh * hd + t] = Ot / Lt;
   }
 }
 

@@ -375,8 +375,8 @@ __global__ void __launch_bounds__(256) k_dispatch(LayerDev L, FwdBufs B, uint32_
 // llama/mod.rs:967-972 laid end to end, as dispatch_block makes it. pair(p, &id, &w)
 // reads pair p. Pairs go 64 at a time; per expert a ballot finds its pairs in the chunk
 // and lane e keeps expert e's count, then its next free slot.
-template <class Pair>
-__device__ void dispatch_wave(const FwdBufs& B, const uint8_t* const* eptr, uint32_t ne, uint32_t k, uint32_t nk,
+template <class Ptr, class Pair>
+__device__ void dispatch_wave(const FwdBufs& B, Ptr eptr, uint32_t ne, uint32_t k, uint32_t nk,
                               uint32_t lane, Pair pair, bool meta = true) {
   const uint64_t below = (1ull << lane) - 1ull;
   uint32_t cnt = 0;
@@ -411,7 +411,7 @@ __device__ void dispatch_wave(const FwdBufs& B, const uint8_t* const* eptr, uint
       B.active[1 + a] = lane;
       if (B.work) {
         ExpertWork& W = B.work[a];
-        for (int p = 0; p < 3; p++) W.w[p] = eptr[p * ne + lane];
+        for (int p = 0; p < 3; p++) W.w[p] = eptr(p);
         W.e = lane;
         W.s0 = off;
         W.m = cnt;
@@ -594,7 +594,7 @@ __global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, 
   }
   if (!dispatch) return;
   if (n == 1) {  // the only workgroup: pair p (< k) is rank p, which lane p holds
-    dispatch_wave(B, L.eptr, ne, k, k, lane, [&](uint32_t, uint32_t* pid, float* pw) {
+    dispatch_wave(B, [&](int p) { return L.eptr[p * ne + lane]; }, ne, k, k, lane, [&](uint32_t, uint32_t* pid, float* pw) {
       *pid = id;
       *pw = w;
     });
@@ -606,7 +606,7 @@ __global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, 
   if (lane == 0) prev = atomicAdd(B.done, 1u);
   if (lane_u(prev, 0) == n - 1) {
     __threadfence();
-    dispatch_wave(B, L.eptr, ne, k, n * k, lane, [&](uint32_t p, uint32_t* pid, float* pw) {
+    dispatch_wave(B, [&](int p) { return L.eptr[p * ne + lane]; }, ne, k, n * k, lane, [&](uint32_t p, uint32_t* pid, float* pw) {
       *pid = B.ids[p];
       *pw = B.w[p];
     });
@@ -666,6 +666,23 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const float* hs = B.hs + (size_t)t * d;
   const float4* xr = reinterpret_cast<const float4*>(hs);
+  // loads whose use comes late, issued first: wave 0's slab pointers for the dispatch
+  // (lane e: expert e's gate, up, down) and the activations of this thread's 32-value
+  // block for the int8 quantiser
+  const uint8_t* ep[3] = {nullptr, nullptr, nullptr};
+  if (wave == 0 && lane < ne)
+    for (int p = 0; p < 3; p++) ep[p] = L.eptr[p * ne + lane];
+  const uint32_t nblk = d / 32;
+  float qv[32];
+  const bool qown = quant && tid < nblk && nblk <= kSpecThreads;
+  if (qown) {
+    const float4* src = reinterpret_cast<const float4*>(hs + (size_t)tid * 32);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float4 t4 = src[i];
+      qv[4 * i] = t4.x; qv[4 * i + 1] = t4.y; qv[4 * i + 2] = t4.z; qv[4 * i + 3] = t4.w;
+    }
+  }
   // wave w: experts w, w + 8, ...; lane j: float4 columns j, j + 64, ..., 16 loads in flight
   constexpr int kB = 16;
   const uint32_t n4 = d / 4;
@@ -701,8 +718,10 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
       la[e] = ab;
     }
   }
-  if (quant) {
-    const uint32_t nblk = d / 32;
+  if (qown) {
+    const size_t gb = (size_t)t * nblk + tid;
+    quant32(qv, B.xq + gb * 32, B.xs + gb, B.x16 + 2 * gb);
+  } else if (quant && nblk > kSpecThreads) {
     for (uint32_t b = tid; b < nblk; b += kSpecThreads) {
       float v[32];
       const float4* src = reinterpret_cast<const float4*>(hs + (size_t)b * 32);
@@ -748,7 +767,7 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
   const uint32_t my = lane < nc ? cl[lane] : ~0u;
   if (lane < ne) B.cand[(size_t)t * ne + lane] = my;
   if (n == 1) {
-    dispatch_wave(B, L.eptr, ne, ne, ne, lane, [&](uint32_t, uint32_t* pid, float* pw) {
+    dispatch_wave(B, [&](int p) { return ep[p]; }, ne, ne, ne, lane, [&](uint32_t, uint32_t* pid, float* pw) {
       *pid = my;
       *pw = 0.0f;
     }, false);
@@ -759,7 +778,7 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
   if (lane == 0) prev = atomicAdd(B.done, 1u);
   if (lane_u(prev, 0) == n - 1) {
     __threadfence();
-    dispatch_wave(B, L.eptr, ne, ne, n * ne, lane, [&](uint32_t p, uint32_t* pid, float* pw) {
+    dispatch_wave(B, [&](int p) { return ep[p]; }, ne, ne, n * ne, lane, [&](uint32_t p, uint32_t* pid, float* pw) {
       *pid = B.cand[p];
       *pw = 0.0f;
     }, false);
