@@ -539,6 +539,8 @@ struct DenseCarve {
   bool pf, int8;
 };
 
+constexpr uint32_t kDenseFuseKsg = 4;
+
 // Scratch of one dense call: plan (base null) or carve.
 size_t plan_dense(const gmoe_ctx* c, const Dense& W, uint32_t n, uint8_t* base, DenseCarve* out) {
   const LayerDev D = dense_dev(W);
@@ -552,8 +554,12 @@ size_t plan_dense(const gmoe_ctx* c, const Dense& W, uint32_t n, uint8_t* base, 
   const size_t nx = (size_t)n * W.cols;
   size_t o_work = P.add(sizeof(ExpertWork)), o_off = P.add(8), o_act = P.add(8), o_tok = P.add((size_t)n * 4),
          o_pt = P.add((size_t)B.ptile_cap * 4 + 4);
+  // packed math: with at least kDenseFuseKsg K slices each down workgroup stages a short
+  // K range, and quantises its activations itself; with fewer, a quantiser launch first
+  // (staging the f32 rows cost the 32000-row output head 2.3 us, saved q/k/v/o 11 us)
+  const bool fuse = int8 && ksg >= kDenseFuseKsg;
   size_t o_q = 0, o_s = 0, o_16 = 0, o_xh = 0, o_xsh = 0;
-  if (int8) {
+  if (int8 && !fuse) {
     o_q = P.add(nx);
     o_s = P.add(nx / 32 * 4);
     o_16 = P.add(nx / 16 * 4);
@@ -569,7 +575,7 @@ size_t plan_dense(const gmoe_ctx* c, const Dense& W, uint32_t n, uint8_t* base, 
     B.active = (uint32_t*)(base + o_act);
     B.slot_tok = (uint32_t*)(base + o_tok);
     B.ptile = pf ? (uint32_t*)(base + o_pt) : nullptr;
-    if (int8) {
+    if (int8 && !fuse) {
       B.hq = (int8_t*)(base + o_q);
       B.hsc = (float*)(base + o_s);
       B.h16 = (int32_t*)(base + o_16);
@@ -604,8 +610,14 @@ gmoe_status run_dense(const Dense& W, const DenseCarve& cv, const float* x, uint
     HIP_TRY(launch_gather_f16(Gd, B, n, st));
     HIP_TRY(launch_prefill_down(D, B, n, cv.ksg, st));
   } else {
-    if (cv.int8) HIP_TRY(launch_quant_act(x, n, W.cols, B.hq, B.hsc, B.h16, st));
-    else B.hf = const_cast<float*>(x);
+    if (cv.int8 && B.hq) {
+      HIP_TRY(launch_quant_act(x, n, W.cols, B.hq, B.hsc, B.h16, st));
+    } else {  // f32 math, or packed math quantised in the down kernel's staging (hq null)
+      B.hq = nullptr;
+      B.hsc = nullptr;
+      B.h16 = nullptr;
+      B.hf = const_cast<float*>(x);
+    }
     HIP_TRY(launch_down(D, B, n, st, cv.ksg));
   }
   HIP_TRY(launch_reduce_parts(B.y, cv.ksg, (size_t)n * W.rows, out, st));

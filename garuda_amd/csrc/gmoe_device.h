@@ -267,15 +267,15 @@ template <int QT> __device__ __forceinline__ void deq(const uint32_t* w, float* 
 // Activation quantiser (quant/mod.rs:331-345, :322-326): one thread per 32-block.
 // ---------------------------------------------------------------------------------
 
-__device__ __forceinline__ void quant32(const float* v, int8_t* q, float* s, int32_t* s16) {
+// The block's values packed four to a word, its scale, and the sums of its halves.
+__device__ __forceinline__ void quant32_regs(const float* v, uint32_t* packed, float* scale_out, int* sum0_out,
+                                             int* sum1_out) {
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
   float scale = fdiv(amax, 127.0f);
-  *s = scale;
   float inv = scale > 0.0f ? fdiv(1.0f, scale) : 0.0f;
   int sum0 = 0, sum1 = 0;
-  uint32_t packed[8];
 #pragma unroll
   for (int j = 0; j < 32; j++) {
     float r = roundf(v[j] * inv);
@@ -288,6 +288,17 @@ __device__ __forceinline__ void quant32(const float* v, int8_t* q, float* s, int
     if ((j & 3) == 0) packed[j >> 2] = 0;
     packed[j >> 2] |= ((uint32_t)qi & 0xffu) << (8 * (j & 3));
   }
+  *scale_out = scale;
+  *sum0_out = sum0;
+  *sum1_out = sum1;
+}
+
+__device__ __forceinline__ void quant32(const float* v, int8_t* q, float* s, int32_t* s16) {
+  uint32_t packed[8];
+  float scale;
+  int sum0, sum1;
+  quant32_regs(v, packed, &scale, &sum0, &sum1);
+  *s = scale;
   uint4* q4 = reinterpret_cast<uint4*>(q);
   q4[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
   q4[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);

@@ -102,7 +102,7 @@ struct ActLds {
 };
 
 // Stages tokens 0..m-1 of a chunk. rows[t] (LDS) is token t's row in the activation
-// arrays, whose rows are K long. Every thread issues up to four loads before it stores,
+// arrays, whose rows are K long. Packed with q null: quantised here from the f32 rows x. Every thread issues up to four loads before it stores,
 // over the chunk's tokens flattened, so the chunk costs about one memory round trip.
 template <int QT, bool PACKED>
 __device__ __forceinline__ void stage_acts(uint8_t* lds, uint32_t nelem, uint32_t m, const uint32_t* rows, uint32_t K,
@@ -134,6 +134,40 @@ __device__ __forceinline__ void stage_acts(uint8_t* lds, uint32_t nelem, uint32_
   };
   if constexpr (PACKED) {
     constexpr int KIND = sum_kind<QT>();
+    if (!q) {
+      // f32 activations (a dense call): each thread quantises 32-blocks into the token's
+      // LDS region with quant32's arithmetic, so the values match k_quant_act's bit for bit
+      const uint32_t nb = nelem / 32, total = m * nb;
+      for (uint32_t i = threadIdx.x; i < total; i += bd) {
+        const uint32_t t = i / nb, b = i - t * nb;
+        const float4* src = reinterpret_cast<const float4*>(x + (size_t)rows[t] * K + k0 + 32 * b);
+        float v[32];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const float4 f = src[j];
+          v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+        }
+        uint32_t pk[8];
+        float sc;
+        int s0, s1;
+        quant32_regs(v, pk, &sc, &s0, &s1);
+        uint8_t* tok = lds + t * per;
+        uint4* qd = reinterpret_cast<uint4*>(tok + 32 * b);
+        qd[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        qd[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+        reinterpret_cast<float*>(tok + A::qb(nelem))[b] = sc;
+        uint32_t* hs = reinterpret_cast<uint32_t*>(tok + A::qb(nelem) + A::sb(nelem));
+        if constexpr (KIND == kSumF32x32) hs[b] = __float_as_uint((float)(s0 + s1));
+        else if constexpr (KIND == kSumF32x16) {
+          hs[2 * b] = __float_as_uint((float)s0);
+          hs[2 * b + 1] = __float_as_uint((float)s1);
+        } else if constexpr (KIND == kSumI32x16) {
+          hs[2 * b] = (uint32_t)s0;
+          hs[2 * b + 1] = (uint32_t)s1;
+        }
+      }
+      return;
+    }
     copy(nelem / 16, 0u, [&](uint32_t r, uint32_t c) {
       return reinterpret_cast<const uint4*>(q + (size_t)r * K + k0)[c];
     });

@@ -55,6 +55,32 @@ def test_dense_every_type(dev, qtype, math):
     check(dev, qtype, 67, 1024 if e == 256 else 256, (1, 3, 8, 70), math)
 
 
+@pytest.mark.parametrize("qtype", [G.Q4_K, G.Q5_K, G.Q6_K, G.Q3_K, G.Q2_K, G.Q8_0, G.Q4_0])
+def test_dense_quantised_in_staging(dev, qtype):
+    # 4096 columns: the call splits K into 8 slices, so under packed math each down
+    # workgroup quantises its own activations (the 67-row shapes above take the
+    # separate quantiser); zero blocks and partly zero blocks included
+    rows, cols = 256, 4096
+    e, _ = O.block_layout(qtype)
+    raw = fast_random_blocks(qtype, rows * cols // e, 5 + qtype)
+    W = G.DenseWeight(dev, qtype, rows, cols, raw, G.MATH_PACKED)
+    try:
+        deq = O.dequantize(qtype, raw, rows * cols, checked=False).reshape(rows, cols)
+        for n in (1, 8, 70):
+            say(f"dense {qtype} {rows}x{cols} quantised in staging, n={n}")
+            xs = np.random.default_rng(n).normal(0, 1, (n, cols)).astype(np.float32)
+            xs[0, :7] = 0.0
+            if n > 1:
+                xs[1, 32:64] = 0.0
+            got = W.matmul_rows(xs)
+            want = O.matmul(qtype, raw, rows, cols, xs, n, threads=8).reshape(n, rows)
+            scale = np.abs(xs) @ np.abs(deq).T
+            bad = ~(np.abs(got - want) <= 1e-5 * scale + 1e-6)
+            assert not bad.any(), f"n={n}: {bad.sum()} values off, worst {np.abs(got - want).max()}"
+    finally:
+        W.release()
+
+
 @pytest.mark.parametrize("qtype", [G.Q4_K, G.Q6_K, G.Q8_0, G.Q2_K])
 def test_dense_prefill_on_mfma(dev, qtype):
     # rows a multiple of 512 and f32 math: the MFMA path, with a ragged last token tile
