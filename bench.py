@@ -348,6 +348,98 @@ def attention_leg(a, dev, threads, stream, timed):
                         "32 query / 8 kv heads of 128, pages of 16, f32 K/V", "contexts": res}
 
 
+def e2e_leg(a, threads, cpu):
+    """C5 end to end: a 32-layer Mixtral-shape model (Q3_K gate/up, Q4_K down, Q4_K
+    attention projections, Q6_K output head, f32 token table; GQA 32/8 of 128, paged KV
+    cache, rope theta 1e6) decoding 8 sequences at once through gmoe_model_decode: each
+    sequence is fed a 128-token prompt one token per step, then decodes greedily while
+    the steps are timed (each step returns its tokens to the host). The layers cycle over
+    8 HBM copies of one synthetic layer, so every layer's weights come from HBM, not the
+    MALL. With `cpu`, one batch-8 step of the same model at context 1 runs through the
+    oracle's restatement on the host threads."""
+    import garuda_amd as G
+    from garuda_amd import moe as M
+    from garuda_amd.attention import KvCache
+
+    d, f, ne, k, nh, nkv, hd, vocab, nseq = 4096, 14336, 8, 2, 32, 8, 128, 32000, 8
+    nl, copies, prompt, steps = a.e2e_layers, min(8, a.e2e_layers), a.e2e_prompt, a.e2e_steps
+    seed = SEED + 0x5000
+    t0 = time.time()
+
+    def q(qt, rows, cols, sd, std=0.02):
+        return M.quantize(qt, M.fill_gaussian(sd, rows * cols, 0.0, std, threads), threads)
+
+    ex = {nm: q(qt, ne * rows, cols, seed + i) for i, (nm, qt, rows, cols) in
+          enumerate((("gate", G.Q3_K, f, d), ("up", G.Q3_K, f, d), ("down", G.Q4_K, d, f)))}
+    att = {nm: q(G.Q4_K, rows, cols, seed + 8 + i) for i, (nm, rows, cols) in
+           enumerate((("wq", nh * hd, d), ("wk", nkv * hd, d), ("wv", nkv * hd, d), ("wo", d, nh * hd)))}
+    head_raw = q(G.Q6_K, vocab, d, seed + 16)
+    table = M.fill_gaussian(seed + 17, vocab * d, 0.0, 1.0, threads).reshape(vocab, d)
+    norms = [M.fill_gaussian(seed + 32 + i, d, 1.0, 0.05, threads) for i in range(2 * copies + 1)]
+    routers = [M.fill_gaussian(seed + 64 + c, ne * d, 0.0, 0.02, threads) for c in range(copies)]
+    gen_s = time.time() - t0
+    expert_bytes = sum(M.byte_size(qt, r * c) for qt, r, c in ((G.Q3_K, f, d), (G.Q3_K, f, d), (G.Q4_K, d, f)))
+    dev = G.Device(0, slab_bytes=copies * ne * (expert_bytes + 4096) + (64 << 20))
+    moe = [G.MoeLayer(dev, d, f, ne, k, routers[c], ex["gate"], ex["up"], ex["down"], (G.Q3_K, G.Q3_K, G.Q4_K))
+           for c in range(copies)]
+    dense = {nm: [G.DenseWeight(dev, G.Q4_K, r, cc, att[nm]) for _ in range(copies)]
+             for nm, r, cc in (("wq", nh * hd, d), ("wk", nkv * hd, d), ("wv", nkv * hd, d), ("wo", d, nh * hd))}
+    head = G.DenseWeight(dev, G.Q6_K, vocab, d, head_raw)
+    kv = KvCache(dev, nl, nh, nkv, hd, block_size=16, max_positions=prompt + steps + 8, max_seqs=nseq,
+                 rope_theta=1e6)
+    pick = [l % copies for l in range(nl)]
+    model = G.DecodeModel(dev, kv, [moe[c] for c in pick], *[[dense[nm][c] for c in pick] for nm in ("wq", "wk", "wv", "wo")],
+                          head, np.stack([norms[2 * c] for c in pick]), np.stack([norms[2 * c + 1] for c in pick]),
+                          norms[-1], table)
+    seqs = [kv.open_seq() for _ in range(nseq)]
+    toks = np.random.default_rng(seed & 0xffffffff).integers(0, vocab, (nseq, prompt)).astype(np.uint32)
+    t0 = time.time()
+    for p in range(prompt):
+        nxt = model.decode_step(seqs, toks[:, p])
+    prompt_s = time.time() - t0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        nxt = model.decode_step(seqs, nxt)
+    dt = time.perf_counter() - t0
+    tps = nseq * steps / dt
+    log(f"c5 end to end: {tps:.0f} tok/s ({dt / steps * 1e3:.2f} ms per batch-{nseq} step of {nl} layers, "
+        f"contexts {prompt + 1}-{prompt + steps}); prompts fed in {prompt_s:.1f}s, weights made in {gen_s:.1f}s")
+    res = {"workload": f"C5 end to end: {nl} Mixtral-shape layers (Q3_K gate/up, Q4_K down and attention "
+                       f"projections, Q6_K head, f32 token table, GQA 32/8 of 128, paged KV cache) cycling over "
+                       f"{copies} HBM copies of one synthetic layer; {nseq} sequences, {prompt}-token prompts fed "
+                       f"one token per step, then {steps} timed greedy decode steps",
+           "tokens_per_s": tps, "ms_per_step": dt / steps * 1e3, "layers": nl, "sequences": nseq,
+           "prompt": prompt, "steps": steps, "cpu": None}
+    model.close()
+    kv.close()
+    for ws in dense.values():
+        for w in ws:
+            w.release()
+    head.release()
+    for m in moe:
+        m.release()
+    dev.close()
+    if cpu:
+        from oracle import oracle as O  # the checker's restatement, timed as the CPU path
+        from oracle.model import ModelOracle
+        layers = [dict(attn_norm=norms[2 * c], ffn_norm=norms[2 * c + 1],
+                       wq=(O.Q4_K, att["wq"], nh * hd, d), wk=(O.Q4_K, att["wk"], nkv * hd, d),
+                       wv=(O.Q4_K, att["wv"], nkv * hd, d), wo=(O.Q4_K, att["wo"], d, nh * hd),
+                       moe=dict(d=d, f=f, ne=ne, k=k, router=routers[c], qtypes=(O.Q3_K, O.Q3_K, O.Q4_K), packed=1,
+                                gate=ex["gate"], up=ex["up"], down=ex["down"]))
+                  for c in pick]
+        orc = ModelOracle(layers, (O.Q6_K, head_raw, vocab, d), norms[-1], table, nh, nkv, hd,
+                          max_positions=8, rope_theta=1e6, threads=threads)
+        t0 = time.time()
+        orc.decode_step(list(range(nseq)), toks[:, 0])
+        wall = time.time() - t0
+        res["cpu"] = {"value": nseq / wall, "unit": "tokens/s", "cores": threads, "kind": "port",
+                      "sample": f"one batch-{nseq} decode step of the {nl}-layer model at context 1, oracle "
+                                f"restatement of logits_batch (packed int8 products), {threads} threads, {wall:.1f}s"}
+        log(f"c5 end to end on the CPU: {nseq / wall:.2f} tok/s on {threads} threads")
+    return res
+
+
 def gguf_leg(a, dev, mats, threads):
     """The slab's source, a GGUF checkpoint: the C2 layer written as a one-layer GGUF
     checkpoint (stacked Q4_K experts, F32 router), then Gguf.open + MoeLayer.from_gguf timed
@@ -434,6 +526,10 @@ def main():
                     help="decode steps of the prefetch leg, each way (0: skip it)")
     ap.add_argument("--gguf-reps", type=int, default=3,
                     help="timed open+register passes of the GGUF staging leg (0: skip it)")
+    ap.add_argument("--e2e-layers", type=int, default=32,
+                    help="layers of the C5 end-to-end decode leg (0: skip it)")
+    ap.add_argument("--e2e-prompt", type=int, default=128, help="prompt tokens per sequence of the end-to-end leg")
+    ap.add_argument("--e2e-steps", type=int, default=32, help="timed decode steps of the end-to-end leg")
     ap.add_argument("--extra", default="c4,c5_layer",
                     help="further BASELINE configurations to time at decode (c4, c5_layer); empty skips")
     a = ap.parse_args()
@@ -538,6 +634,7 @@ def main():
     prefetch = prefetch_leg(a, mats, threads) if a.prefetch_steps > 0 else None
     attention = attention_leg(a, dev, threads, stream, timed) if a.attention else None
     gguf = gguf_leg(a, dev, mats, threads) if a.gguf_reps > 0 else None
+    e2e = e2e_leg(a, threads, not a.no_cpu) if a.e2e_layers > 0 else None
 
     if a.calibrate_copy:
         src = torch.empty(a.calibrate_copy << 18, dtype=torch.float32, device="cuda")
@@ -598,6 +695,7 @@ def main():
         "prefetch": prefetch,
         "attention": attention,
         "gguf_staging": gguf,
+        "c5_end_to_end": e2e,
         "sweep": {str(n): {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res.items()}
                   for n, res in results.items()},
     }

@@ -8,6 +8,7 @@ from .moe import (  # noqa: F401
     COMBINE_EXPERT_ORDER, COMBINE_RANK_ORDER, F16, F32, GATING_DEEPSEEK, GATING_LLAMA,
     GATING_MIXTRAL, GATING_QWEN, MATH_F32, MATH_PACKED, Q2_K, Q3_K, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0,
     CacheError, ConfigError, Device, DeviceError, GarudaError, InferenceError, ModelError,
-    DenseWeight, MoeLayer, NotFoundError, block_layout, byte_size, fill_gaussian, quantize,
+    DenseWeight, InvalidTokenError, MoeLayer, NotFoundError, block_layout, byte_size, fill_gaussian, quantize,
 )
+from .model import DecodeModel  # noqa: F401
 from .gguf import Gguf, TensorInfo, Value, write_gguf  # noqa: F401

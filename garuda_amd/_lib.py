@@ -108,6 +108,9 @@ SIGNATURES = {
     "gmoe_gguf_find_tensor": (i32, [vp, C.c_char_p, C.POINTER(GmoeGgufTensorInfo)]),
     "gmoe_gguf_layer_desc": (i32, [vp, u32, u32, u32, u32, C.POINTER(GmoeLayerDesc)]),
     "gmoe_gguf_expert_ranges": (i32, [vp, u32, u32, C.POINTER(u64), C.POINTER(u64)]),
+    "gmoe_model_create": (i32, [vp, vp, C.POINTER(vp)]),
+    "gmoe_model_destroy": (None, [vp]),
+    "gmoe_model_decode": (i32, [vp, u32, u32p, u32p, u32p, f32p]),
     "gmoe_set_kernel_timing": (i32, [vp, i32]),
     "gmoe_kernel_time": (i32, [vp, u32, C.POINTER(C.c_double), C.POINTER(u64)]),
 }

@@ -704,6 +704,29 @@ gmoe_status forward_host(gmoe_ctx* c, uint32_t lid, const float* hs, const float
 
 }  // namespace
 
+namespace gmoe {
+
+// Shapes of registered weights, for the decode-step driver (gmoe_model.cpp).
+bool dense_shape(gmoe_ctx* c, uint32_t id, uint32_t* rows, uint32_t* cols) {
+  std::lock_guard<std::mutex> g(c->mu);
+  Dense* W;
+  if (get_dense(c, id, &W) != GMOE_OK) return false;
+  *rows = W->rows;
+  *cols = W->cols;
+  return true;
+}
+
+bool layer_width(gmoe_ctx* c, uint32_t id, uint32_t* d, uint32_t* ne) {
+  std::lock_guard<std::mutex> g(c->mu);
+  Layer* L;
+  if (get_layer(c, id, &L) != GMOE_OK) return false;
+  *d = L->d;
+  *ne = L->ne;
+  return true;
+}
+
+}  // namespace gmoe
+
 extern "C" {
 
 uint32_t gmoe_abi_version(void) { return GMOE_ABI_VERSION; }

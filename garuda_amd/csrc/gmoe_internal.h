@@ -284,6 +284,17 @@ struct AttnArgs {
 constexpr uint32_t kAttnChunk = 64, kAttnMaxGroup = 16, kAttnMaxHd = 256;
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 
+// Decode-step glue (gmoe_glue.hip): embedding rows, residual add + RMSNorm * weight,
+// greedy token. A decode step carries its tokens in the kernel arguments.
+constexpr uint32_t kModelMaxBatch = 64;
+struct GlueTokens {
+  uint32_t tok[kModelMaxBatch];
+};
+hipError_t launch_embed(const GlueTokens& tk, uint32_t n, const float* table, uint32_t d, float* x, hipStream_t st);
+hipError_t launch_add_norm(float* x, const float* y, const float* w, uint32_t n, uint32_t d, float eps, float* h,
+                           hipStream_t st);
+hipError_t launch_argmax(const float* logits, uint32_t n, uint32_t vocab, uint32_t* next, hipStream_t st);
+
 hipError_t launch_tile_rows(uint32_t qtype, const uint8_t* raw, uint32_t r0, uint32_t nrows, uint32_t rows,
                             uint32_t cols, uint8_t* dst, hipStream_t st);
 

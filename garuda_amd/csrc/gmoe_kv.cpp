@@ -194,6 +194,41 @@ gmoe_status attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n
 
 }  // namespace
 
+namespace gmoe {
+
+// For the decode-step driver (gmoe_model.cpp): the cache's widths, and whether each of
+// the (distinct) sequences can take one more position in every layer, refused before
+// any layer has run (as logits_batch refuses, llama/mod.rs:1163-1176).
+void kv_dims(gmoe_kv* kv, uint32_t* n_layers, uint32_t* q_dim, uint32_t* kv_dim) {
+  *n_layers = kv->d.n_layers;
+  *q_dim = kv->d.n_heads * kv->d.head_dim;
+  *kv_dim = kv->kvd;
+}
+
+gmoe_status kv_check_step(gmoe_kv* kv, const uint32_t* seqs, uint32_t n) {
+  std::lock_guard<std::mutex> g(kv->mu);
+  const gmoe_kv_desc& D = kv->d;
+  uint64_t pages = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    const uint32_t s = seqs[i];
+    if (s >= kv->seqs.size() || !kv->seqs[s].open) return kfail(GMOE_ERR_INFERENCE, "sequence %u is not open", s);
+    for (uint32_t j = 0; j < i; j++)
+      if (seqs[j] == s) return kfail(GMOE_ERR_INFERENCE, "sequence %u appears twice in one decode step", s);
+    for (uint32_t l = 0; l < D.n_layers; l++) {
+      const uint32_t pos = kv->seqs[s].len[l];
+      if (pos + 1 > D.max_positions)
+        return kfail(GMOE_ERR_CACHE, "context window of %u positions is exhausted", D.max_positions);
+      if (pos % D.block_size == 0) pages++;
+    }
+  }
+  if (pages > kv->free_pages.size())
+    return kfail(GMOE_ERR_CACHE, "the KV pool has %zu free pages, the step needs %llu", kv->free_pages.size(),
+                 (unsigned long long)pages);
+  return GMOE_OK;
+}
+
+}  // namespace gmoe
+
 extern "C" {
 
 gmoe_status gmoe_kv_create(gmoe_ctx* ctx, const gmoe_kv_desc* desc, gmoe_kv** out) {

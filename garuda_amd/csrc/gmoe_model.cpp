@@ -1,0 +1,221 @@
+// gmoe_model.cpp — one decode step of a Llama-family MoE model on the device.
+//
+// LlamaBackend::logits_batch (garuda/src/llama/mod.rs:1134-1206) for its decode case:
+// every sequence takes one new token. The step embeds the tokens, runs each layer as
+// layer_batch_over does (:851-893) — h = norm(x, attn_norm); q, k, v projections;
+// attend_one per token; x += wo(context); h = norm(x, ffn_norm); x += the MoE layer — then
+// norm(x, output_norm), the output head, and greedy sampling (runtime/mod.rs:98-105).
+// Everything is queued on the context's stream with no host synchronisation until the
+// chosen tokens come back; the pieces are the library's own entry points (dense
+// projections, paged attention, the MoE layer) and the glue kernels of gmoe_glue.hip.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "../../include/garuda_moe.h"
+#include "gmoe_internal.h"
+
+namespace gmoe {
+void set_last_error(const char* msg);
+int ctx_device(gmoe_ctx* c);
+hipStream_t ctx_stream(gmoe_ctx* c);
+bool dense_shape(gmoe_ctx* c, uint32_t id, uint32_t* rows, uint32_t* cols);
+bool layer_width(gmoe_ctx* c, uint32_t id, uint32_t* d, uint32_t* ne);
+void kv_dims(gmoe_kv* kv, uint32_t* n_layers, uint32_t* q_dim, uint32_t* kv_dim);
+gmoe_status kv_check_step(gmoe_kv* kv, const uint32_t* seqs, uint32_t n);
+}  // namespace gmoe
+
+using namespace gmoe;
+
+struct gmoe_model {
+  gmoe_ctx* ctx = nullptr;
+  gmoe_kv* kv = nullptr;
+  uint32_t n_layers = 0, d = 0, vocab = 0, qd = 0, kvd = 0;
+  float eps = 0.0f;
+  std::vector<uint32_t> moe, wq, wk, wv, wo;
+  uint32_t out_id = 0;
+  float* table = nullptr;  // [vocab][d] token embeddings
+  float* norms = nullptr;  // [2 n_layers + 1][d]: attn_norm, ffn_norm per layer, then output_norm
+  // per-step activations for up to kModelMaxBatch tokens
+  float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *cx = nullptr, *ao = nullptr,
+        *y = nullptr, *logits = nullptr;
+  uint32_t* next = nullptr;
+  uint32_t* pin_next = nullptr;
+  std::mutex mu;
+
+  ~gmoe_model() {
+    for (void* p : {(void*)table, (void*)norms, (void*)x, (void*)h, (void*)q, (void*)k, (void*)v, (void*)cx,
+                    (void*)ao, (void*)y, (void*)logits, (void*)next})
+      if (p) hipFree(p);
+    if (pin_next) hipHostFree(pin_next);
+  }
+};
+
+namespace {
+
+gmoe_status mfail(gmoe_status s, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  set_last_error(buf);
+  return s;
+}
+
+#define M_TRY(expr)                                                                              \
+  do {                                                                                           \
+    hipError_t e_ = (expr);                                                                      \
+    if (e_ != hipSuccess) return mfail(GMOE_ERR_DEVICE, "%s: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+#define S_TRY(expr)                 \
+  do {                              \
+    gmoe_status s_ = (expr);        \
+    if (s_ != GMOE_OK) return s_;   \
+  } while (0)
+
+gmoe_status check_dense(gmoe_ctx* c, uint32_t id, uint32_t rows, uint32_t cols, const char* what, uint32_t l) {
+  uint32_t r, k;
+  if (!dense_shape(c, id, &r, &k)) return mfail(GMOE_ERR_INFERENCE, "%s of layer %u: unknown dense weight %u", what, l, id);
+  if (r != rows || k != cols)
+    return mfail(GMOE_ERR_MODEL, "%s of layer %u is %u x %u, the model needs %u x %u", what, l, r, k, rows, cols);
+  return GMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+gmoe_status gmoe_model_create(gmoe_ctx* ctx, const gmoe_model_desc* desc, gmoe_model** out) {
+  if (!ctx || !desc || !out) return mfail(GMOE_ERR_INFERENCE, "null context, descriptor or output");
+  *out = nullptr;
+  const gmoe_model_desc& D = *desc;
+  if (!D.kv || !D.moe_layers || !D.wq || !D.wk || !D.wv || !D.wo || !D.attn_norm || !D.ffn_norm ||
+      !D.output_norm || !D.token_embd)
+    return mfail(GMOE_ERR_INFERENCE, "null weight array in the model descriptor");
+  if (D.n_layers == 0 || D.d_model == 0 || D.vocab == 0 || D.d_model % 4)
+    return mfail(GMOE_ERR_CONFIG, "model dimensions must be positive, d_model a multiple of 4");
+  if (D.token_embd_qtype != GMOE_F32) return mfail(GMOE_ERR_MODEL, "token embeddings must be F32 rows");
+  uint32_t kl, qd, kvd;
+  kv_dims(D.kv, &kl, &qd, &kvd);
+  if (kl != D.n_layers) return mfail(GMOE_ERR_INFERENCE, "the KV cache has %u layers, the model %u", kl, D.n_layers);
+  for (uint32_t l = 0; l < D.n_layers; l++) {
+    uint32_t w, ne;
+    if (!layer_width(ctx, D.moe_layers[l], &w, &ne))
+      return mfail(GMOE_ERR_INFERENCE, "layer %u: unknown MoE layer %u", l, D.moe_layers[l]);
+    if (w != D.d_model) return mfail(GMOE_ERR_MODEL, "MoE layer of layer %u has d_model %u, not %u", l, w, D.d_model);
+    S_TRY(check_dense(ctx, D.wq[l], qd, D.d_model, "wq", l));
+    S_TRY(check_dense(ctx, D.wk[l], kvd, D.d_model, "wk", l));
+    S_TRY(check_dense(ctx, D.wv[l], kvd, D.d_model, "wv", l));
+    S_TRY(check_dense(ctx, D.wo[l], D.d_model, qd, "wo", l));
+  }
+  S_TRY(check_dense(ctx, D.output, D.vocab, D.d_model, "output", D.n_layers));
+  auto* m = new (std::nothrow) gmoe_model;
+  if (!m) return mfail(GMOE_ERR_CONFIG, "out of host memory");
+  m->ctx = ctx;
+  m->kv = D.kv;
+  m->n_layers = D.n_layers;
+  m->d = D.d_model;
+  m->vocab = D.vocab;
+  m->qd = qd;
+  m->kvd = kvd;
+  m->eps = D.rms_eps;
+  m->moe.assign(D.moe_layers, D.moe_layers + D.n_layers);
+  m->wq.assign(D.wq, D.wq + D.n_layers);
+  m->wk.assign(D.wk, D.wk + D.n_layers);
+  m->wv.assign(D.wv, D.wv + D.n_layers);
+  m->wo.assign(D.wo, D.wo + D.n_layers);
+  m->out_id = D.output;
+  auto fail = [&](gmoe_status s) {
+    delete m;
+    return s;
+  };
+  const hipError_t se = hipSetDevice(ctx_device(ctx));
+  if (se != hipSuccess) return fail(mfail(GMOE_ERR_DEVICE, "hipSetDevice: %s", hipGetErrorString(se)));
+  const size_t B = kModelMaxBatch, d = D.d_model;
+  const size_t table_bytes = (size_t)D.vocab * d * 4, norm_bytes = (2 * (size_t)D.n_layers + 1) * d * 4;
+  struct Alloc {
+    void** p;
+    size_t bytes;
+  } allocs[] = {{(void**)&m->table, table_bytes},     {(void**)&m->norms, norm_bytes},
+                {(void**)&m->x, B * d * 4},           {(void**)&m->h, B * d * 4},
+                {(void**)&m->q, B * qd * 4},          {(void**)&m->k, B * kvd * 4},
+                {(void**)&m->v, B * kvd * 4},         {(void**)&m->cx, B * qd * 4},
+                {(void**)&m->ao, B * d * 4},          {(void**)&m->y, B * d * 4},
+                {(void**)&m->logits, B * D.vocab * 4}, {(void**)&m->next, B * 4}};
+  for (auto& a : allocs) {
+    const hipError_t e = hipMalloc(a.p, a.bytes);
+    if (e != hipSuccess) return fail(mfail(GMOE_ERR_CACHE, "device memory for the model: %s", hipGetErrorString(e)));
+  }
+  hipError_t e = hipHostMalloc((void**)&m->pin_next, B * 4, hipHostMallocDefault);
+  if (e == hipSuccess) e = hipMemcpy(m->table, D.token_embd, table_bytes, hipMemcpyHostToDevice);
+  for (uint32_t l = 0; l < D.n_layers && e == hipSuccess; l++) {
+    e = hipMemcpy(m->norms + (2 * (size_t)l) * d, D.attn_norm + (size_t)l * d, d * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+      e = hipMemcpy(m->norms + (2 * (size_t)l + 1) * d, D.ffn_norm + (size_t)l * d, d * 4, hipMemcpyHostToDevice);
+  }
+  if (e == hipSuccess)
+    e = hipMemcpy(m->norms + 2 * (size_t)D.n_layers * d, D.output_norm, d * 4, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return fail(mfail(GMOE_ERR_DEVICE, "model upload: %s", hipGetErrorString(e)));
+  *out = m;
+  return GMOE_OK;
+}
+
+void gmoe_model_destroy(gmoe_model* m) {
+  if (!m) return;
+  hipSetDevice(ctx_device(m->ctx));
+  hipStreamSynchronize(ctx_stream(m->ctx));
+  delete m;
+}
+
+gmoe_status gmoe_model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs, const uint32_t* tokens, uint32_t* next,
+                              float* logits) {
+  if (!m || !seqs || !tokens || !next) return mfail(GMOE_ERR_INFERENCE, "null model, sequences, tokens or output");
+  if (n == 0 || n > kModelMaxBatch)
+    return mfail(GMOE_ERR_INFERENCE, "a decode step takes 1 to %u sequences, not %u", kModelMaxBatch, n);
+  std::lock_guard<std::mutex> g(m->mu);
+  // refuse before any device work, so a step cannot leave a sequence half-advanced
+  GlueTokens tk{};
+  for (uint32_t i = 0; i < n; i++) {
+    if (tokens[i] >= m->vocab) return mfail(GMOE_ERR_INVALID_TOKEN, "token %u is outside the %u-entry vocabulary", tokens[i], m->vocab);
+    tk.tok[i] = tokens[i];
+  }
+  S_TRY(kv_check_step(m->kv, seqs, n));
+  for (uint32_t l = 0; l < m->n_layers; l++) {  // the MoE layers run from the slab: all resident
+    uint32_t w, ne;
+    if (!layer_width(m->ctx, m->moe[l], &w, &ne)) return mfail(GMOE_ERR_INFERENCE, "MoE layer %u was released", m->moe[l]);
+    for (uint32_t e = 0; e < ne; e++)
+      if (gmoe_expert_is_resident(m->ctx, m->moe[l], e) != 1)
+        return mfail(GMOE_ERR_CACHE, "expert %u of layer %u is not resident", e, l);
+  }
+  M_TRY(hipSetDevice(ctx_device(m->ctx)));
+  hipStream_t st = ctx_stream(m->ctx);
+  const uint32_t d = m->d;
+  M_TRY(launch_embed(tk, n, m->table, d, m->x, st));
+  for (uint32_t l = 0; l < m->n_layers; l++) {
+    // h = norm(x + previous layer's MoE output, attn_norm)
+    M_TRY(launch_add_norm(m->x, l ? m->y : nullptr, m->norms + (2 * (size_t)l) * d, n, d, m->eps, m->h, st));
+    S_TRY(gmoe_dense_forward_async(m->ctx, m->wq[l], m->h, n, m->q, st));
+    S_TRY(gmoe_dense_forward_async(m->ctx, m->wk[l], m->h, n, m->k, st));
+    S_TRY(gmoe_dense_forward_async(m->ctx, m->wv[l], m->h, n, m->v, st));
+    S_TRY(gmoe_attention_async(m->kv, l, seqs, n, m->q, m->k, m->v, m->cx, st));
+    S_TRY(gmoe_dense_forward_async(m->ctx, m->wo[l], m->cx, n, m->ao, st));
+    M_TRY(launch_add_norm(m->x, m->ao, m->norms + (2 * (size_t)l + 1) * d, n, d, m->eps, m->h, st));
+    S_TRY(gmoe_ffn_forward_async(m->ctx, m->moe[l], m->h, nullptr, n, m->y, nullptr, nullptr, st));
+  }
+  M_TRY(launch_add_norm(m->x, m->y, m->norms + 2 * (size_t)m->n_layers * d, n, d, m->eps, m->h, st));
+  S_TRY(gmoe_dense_forward_async(m->ctx, m->out_id, m->h, n, m->logits, st));
+  M_TRY(launch_argmax(m->logits, n, m->vocab, m->next, st));
+  M_TRY(hipMemcpyAsync(m->pin_next, m->next, n * 4, hipMemcpyDeviceToHost, st));
+  if (logits) M_TRY(hipMemcpyAsync(logits, m->logits, (size_t)n * m->vocab * 4, hipMemcpyDeviceToHost, st));
+  M_TRY(hipStreamSynchronize(st));
+  std::memcpy(next, m->pin_next, n * 4);
+  return GMOE_OK;
+}
+
+}  // extern "C"

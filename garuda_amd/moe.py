@@ -60,7 +60,12 @@ class NotFoundError(GarudaError, KeyError):
     """No such GGUF metadata key or tensor (where the reference returns `None`)."""
 
 
-_STATUS = {1: ModelError, 2: InferenceError, 3: CacheError, 4: ConfigError, 5: DeviceError, 6: NotFoundError}
+class InvalidTokenError(GarudaError):
+    """A token outside the vocabulary (GarudaError::InvalidToken)."""
+
+
+_STATUS = {1: ModelError, 2: InferenceError, 3: CacheError, 4: ConfigError, 5: DeviceError, 6: NotFoundError,
+           7: InvalidTokenError}
 
 
 def _check(status: int) -> None:

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GMOE_ABI_VERSION 2u
+#define GMOE_ABI_VERSION 3u
 
 /* Status codes. Mirrors the GarudaError variants the reference returns on this
  * path (garuda/src/core/mod.rs:10-47). */
@@ -36,7 +36,8 @@ typedef enum gmoe_status {
   GMOE_ERR_CACHE = 3,     /* GarudaError::Cache: the HBM slab cannot hold what is asked */
   GMOE_ERR_CONFIG = 4,    /* GarudaError::Config: top_k outside 1..=n_experts (core/mod.rs:103-108) */
   GMOE_ERR_DEVICE = 5,    /* HIP runtime failure; the context stays usable for teardown */
-  GMOE_ERR_NOT_FOUND = 6  /* no such GGUF metadata key or tensor (the reference's `None`) */
+  GMOE_ERR_NOT_FOUND = 6, /* no such GGUF metadata key or tensor (the reference's `None`) */
+  GMOE_ERR_INVALID_TOKEN = 7 /* GarudaError::InvalidToken: a token outside the vocabulary */
 } gmoe_status;
 
 /* ggml type ids (garuda/src/quant/mod.rs:22-30). */
@@ -327,6 +328,44 @@ gmoe_status gmoe_prefetch_step(gmoe_ctx* ctx, gmoe_predictor* p, uint32_t layer_
                                uint32_t n_used, const uint32_t* predicted_last, uint32_t n_predicted_last,
                                uint32_t depth, uint32_t* predicted, uint32_t* n_predicted, uint32_t* launched,
                                uint32_t* skipped);
+
+/* ---- one decode step of a whole model (LlamaBackend::logits_batch, llama/mod.rs:1134-1206) ----
+ *
+ * The caller around the MoE layer: every sequence takes one new token. The step embeds
+ * the tokens, runs each layer as layer_batch_over does (llama/mod.rs:851-893) — h =
+ * rmsnorm(x) * attn_norm; q, k, v = the dense projections; attention over the paged KV
+ * cache; x += wo(context); h = rmsnorm(x) * ffn_norm; x += the MoE layer — then
+ * rmsnorm(x) * output_norm, the output head, and greedy sampling (runtime/mod.rs:98-105:
+ * the first index of the largest logit). The weights are the library's own registered
+ * objects; the model keeps their ids (release them after the model). The token table
+ * and the norm weights are copied into device memory. */
+typedef struct gmoe_model gmoe_model;
+typedef struct gmoe_model_desc {
+  uint32_t n_layers, d_model, vocab;
+  float rms_eps;
+  gmoe_kv* kv;                  /* n_layers layers; its heads set the q and kv widths */
+  const uint32_t* moe_layers;   /* [n_layers] gmoe_layer_register ids (d_model wide) */
+  const uint32_t* wq;           /* [n_layers] dense ids: q_dim x d_model */
+  const uint32_t* wk;           /* [n_layers] kv_dim x d_model */
+  const uint32_t* wv;           /* [n_layers] kv_dim x d_model */
+  const uint32_t* wo;           /* [n_layers] d_model x q_dim */
+  uint32_t output;              /* dense id: vocab x d_model */
+  const float* attn_norm;       /* [n_layers][d_model] */
+  const float* ffn_norm;        /* [n_layers][d_model] */
+  const float* output_norm;     /* [d_model] */
+  uint32_t token_embd_qtype;    /* GMOE_F32 (rows of the table as f32) */
+  const float* token_embd;      /* [vocab][d_model] */
+} gmoe_model_desc;
+
+gmoe_status gmoe_model_create(gmoe_ctx* ctx, const gmoe_model_desc* desc, gmoe_model** out);
+void gmoe_model_destroy(gmoe_model* model);
+/* Sequences seqs[i] (open in the model's KV cache, distinct) take tokens[i]; next[i] is
+ * the greedy next token; logits ([n x vocab], host) may be NULL. 1 <= n <= 64. Refused
+ * before any device work when a token is outside the vocabulary (GMOE_ERR_INVALID_TOKEN),
+ * a sequence's window is exhausted or the pool lacks pages (GMOE_ERR_CACHE), or an
+ * expert is not resident. Synchronous: returns when next (and logits) are written. */
+gmoe_status gmoe_model_decode(gmoe_model* model, uint32_t n, const uint32_t* seqs, const uint32_t* tokens,
+                              uint32_t* next, float* logits);
 
 /* ---- single steps of the path, for parity tests (host pointers, synchronous) ---- */
 

@@ -1,0 +1,93 @@
+"""CPU restatement of one decode step of the whole model — TEST INFRASTRUCTURE ONLY
+(imported by tests/ as the checker; the product never loads it).
+
+LlamaBackend::logits_batch for its decode case (garuda/src/llama/mod.rs:1134-1206):
+every sequence takes one new token.
+
+    x = token_embd.row(token)                                       (:1179-1185)
+    per layer (layer_batch_over, :851-893):
+        h = norm(x, attn_norm); q, k, v = wq h, wk h, wv h          (:743-757)
+        context = attend_one(q, k, v) per token                     (:766-821)
+        x += wo context; h = norm(x, ffn_norm); x += ffn(h)
+    x = norm(x, output_norm); logits = output x                     (:1191-1199)
+    next = the first index of the largest logit                     (runtime/mod.rs:98-105)
+
+norm(x, w) is simd::rmsnorm (simd/mod.rs:166-173: the f32 mean of the squares summed
+left to right, scale = 1 / sqrt(mean + eps), x *= scale) then x *= w elementwise
+(`mul_assign`). The projections are quant::matmul under packed math (oracle.matmul),
+the attention KvOracle (oracle/attention.py), the MoE layer oracle.feed_forward_batch.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import oracle as O
+from .attention import KvOracle
+
+
+def rmsnorm(x: np.ndarray, eps: float) -> np.ndarray:
+    """simd::rmsnorm of one row: the squares rounded to f32 and summed in order."""
+    x = np.asarray(x, dtype=np.float32)
+    if x.size == 0:
+        return x.copy()
+    sq = (x * x).astype(np.float32)
+    mean_sq = np.float32(np.cumsum(sq, dtype=np.float32)[-1] / np.float32(x.size))
+    scale = np.float32(np.float32(1.0) / np.sqrt(np.float32(mean_sq + np.float32(eps))))
+    return (x * scale).astype(np.float32)
+
+
+def norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    return (rmsnorm(x, eps) * np.asarray(w, dtype=np.float32)).astype(np.float32)
+
+
+def greedy(logits: np.ndarray) -> int:
+    """runtime::sample at temperature 0: fold from (0, -inf), keeping strict improvements."""
+    bi, bv = 0, np.float32(-np.inf)
+    for i, v in enumerate(np.asarray(logits, dtype=np.float32)):
+        if v > bv:
+            bi, bv = i, v
+    return bi
+
+
+class ModelOracle:
+    """layers: per layer a dict with attn_norm, ffn_norm, wq/wk/wv/wo as (qtype, raw,
+    rows, cols) and moe (an oracle.feed_forward_batch layer dict); output: (qtype, raw,
+    vocab, d); output_norm [d]; token_embd [vocab, d] f32."""
+
+    def __init__(self, layers, output, output_norm, token_embd, n_heads, n_kv_heads, head_dim, rms_eps=1e-5,
+                 max_positions=2048, rope_theta=10000.0, threads=8):
+        self.layers, self.output, self.output_norm = layers, output, np.asarray(output_norm, dtype=np.float32)
+        self.table = np.asarray(token_embd, dtype=np.float32)
+        self.eps, self.threads = rms_eps, threads
+        self.kv = KvOracle(len(layers), n_heads, n_kv_heads, head_dim, max_positions=max_positions,
+                           rope_theta=rope_theta)
+
+    def _matmul(self, w, xs):
+        qt, raw, rows, cols = w
+        return O.matmul(qt, raw, rows, cols, xs, xs.shape[0], threads=self.threads).reshape(xs.shape[0], rows)
+
+    def decode_step(self, seqs, tokens):
+        """(next tokens, logits [n, vocab]) of one step; seqs distinct."""
+        n = len(seqs)
+        if len(set(seqs)) != n:
+            raise ValueError("a sequence appears twice in one decode step")
+        vocab = self.table.shape[0]
+        for t in tokens:
+            if t >= vocab:
+                raise ValueError(f"token {t} outside the vocabulary")
+        xs = [self.table[t].copy() for t in tokens]
+        for l, L in enumerate(self.layers):
+            hs = np.stack([norm(x, L["attn_norm"], self.eps) for x in xs])
+            q, k, v = self._matmul(L["wq"], hs), self._matmul(L["wk"], hs), self._matmul(L["wv"], hs)
+            ctx = np.stack([self.kv.attend_one(l, s, q[i], k[i], v[i]) for i, s in enumerate(seqs)])
+            ao = self._matmul(L["wo"], ctx.astype(np.float32))
+            hf = []
+            for i in range(n):
+                xs[i] = (xs[i] + ao[i]).astype(np.float32)
+                hf.append(norm(xs[i], L["ffn_norm"], self.eps))
+            ffn, _, _ = O.feed_forward_batch(L["moe"], np.stack(hf), threads=self.threads)
+            for i in range(n):
+                xs[i] = (xs[i] + ffn[i]).astype(np.float32)
+        hidden = np.stack([norm(x, self.output_norm, self.eps) for x in xs])
+        logits = self._matmul(self.output, hidden)
+        return np.array([greedy(r) for r in logits], dtype=np.uint32), logits
