@@ -692,12 +692,13 @@ gmoe_status forward_host(gmoe_ctx* c, uint32_t lid, const float* hs, const float
   }
   if (gmoe_status s = run_layer(c, *L, B, n, st)) return s;
   HIP_TRY(hipMemcpyAsync(out, B.out, (size_t)n * L->d * 4, hipMemcpyDeviceToHost, st));
+  if (all) HIP_TRY(hipMemcpyAsync(hid.data(), B.ids, hid.size() * 4, hipMemcpyDeviceToHost, st));
   if (ids) HIP_TRY(hipMemcpyAsync(ids, B.ids, (size_t)n * L->k * 4, hipMemcpyDeviceToHost, st));
   if (w) HIP_TRY(hipMemcpyAsync(w, B.w, (size_t)n * L->k * 4, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
-  if (all) {
-    // every routed expert was a hit
-    c->stats.hits += 0;
+  if (all) {  // every routed expert was resident: one hit per distinct expert, as above
+    std::sort(hid.begin(), hid.end());
+    c->stats.hits += (uint64_t)(std::unique(hid.begin(), hid.end()) - hid.begin());
   }
   return GMOE_OK;
 }

@@ -312,6 +312,22 @@ def test_reference_fixture_layer(dev):
 
 # ---------------- the L1 tier and error handling ----------------
 
+def test_resident_layer_counts_a_hit_per_routed_expert():
+    # ExpertCache::get on a resident expert is a hit (cache/mod.rs:18-137): one per
+    # distinct expert a call routes to
+    d, f, ne, k = 256, 512, 8, 2
+    rng = np.random.default_rng(21)
+    router, mats = make_layer(rng, d, f, ne, G.Q4_K, G.Q4_K)
+    with G.Device(0, slab_bytes=64 << 20) as dev:
+        layer = G.MoeLayer(dev, d, f, ne, k, router, mats["gate"], mats["up"], mats["down"], (G.Q4_K,) * 3)
+        assert all(layer.is_resident(e) for e in range(ne))
+        before = dev.slab_stats()
+        _, ids, _ = layer.feed_forward_batch(rng.normal(0, 1, (3, d)).astype(np.float32))
+        after = dev.slab_stats()
+        assert after.hits - before.hits == len(np.unique(ids)) and after.misses == before.misses
+        layer.release()
+
+
 def test_small_slab_stages_experts_on_demand():
     d, f, ne, k = 256, 512, 8, 2
     rng = np.random.default_rng(12)
