@@ -703,9 +703,76 @@ gmoe_status forward_host(gmoe_ctx* c, uint32_t lid, const float* hs, const float
   return GMOE_OK;
 }
 
+// The work records of every token count up to kDenseTab (and the context's identity
+// table) for W->tiled; frees W->tiled on failure.
+gmoe_status dense_tables(gmoe_ctx* c, Dense* W) {
+  std::vector<ExpertWork> tab(kDenseTab);
+  for (uint32_t i = 0; i < kDenseTab; i++) tab[i] = ExpertWork{{W->tiled, W->tiled, W->tiled}, 0, 0, i + 1, 0};
+  hipError_t e = hipMalloc(&W->work_tab, tab.size() * sizeof(ExpertWork));
+  if (e == hipSuccess) e = hipMemcpy(W->work_tab, tab.data(), tab.size() * sizeof(ExpertWork), hipMemcpyHostToDevice);
+  if (e == hipSuccess && !c->ident) {
+    std::vector<uint32_t> id(kDenseTab);
+    for (uint32_t i = 0; i < kDenseTab; i++) id[i] = i;
+    e = hipMalloc(&c->ident, kDenseTab * 4);
+    if (e == hipSuccess) e = hipMemcpy(c->ident, id.data(), kDenseTab * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess && c->ident) {
+      hipFree(c->ident);
+      c->ident = nullptr;
+    }
+  }
+  if (e != hipSuccess) {
+    hipFree(W->tiled);
+    W->tiled = nullptr;
+    if (W->work_tab) hipFree(W->work_tab);
+    W->work_tab = nullptr;
+    return fail(GMOE_ERR_DEVICE, "dense weight tables: %s", hipGetErrorString(e));
+  }
+  return GMOE_OK;
+}
+
 }  // namespace
 
 namespace gmoe {
+
+// One dense weight made of registered ones laid end to end: its rows are theirs in order
+// (out = [W0 x; W1 x; ...]). They share type, width and math, and every one but the last
+// has a whole number of 64-row tiles, so the tiled bytes simply follow one another.
+gmoe_status dense_stack(gmoe_ctx* c, const uint32_t* ids, uint32_t count, uint32_t* out) {
+  std::lock_guard<std::mutex> g(c->mu);
+  if (count == 0) return fail(GMOE_ERR_INFERENCE, "nothing to stack");
+  std::vector<Dense*> parts(count);
+  for (uint32_t i = 0; i < count; i++)
+    if (gmoe_status s = get_dense(c, ids[i], &parts[i])) return s;
+  auto W = std::make_unique<Dense>();
+  W->qtype = parts[0]->qtype;
+  W->cols = parts[0]->cols;
+  W->math = parts[0]->math;
+  for (uint32_t i = 0; i < count; i++) {
+    const Dense& P = *parts[i];
+    if (P.qtype != W->qtype || P.cols != W->cols || P.math != W->math)
+      return fail(GMOE_ERR_MODEL, "stacked weights differ in type, width or math");
+    if (i + 1 < count && P.rows % kTileRows)
+      return fail(GMOE_ERR_MODEL, "a stacked weight's rows (%u) are not whole tiles of %u", P.rows, kTileRows);
+    W->rows += P.rows;
+    W->tiled_bytes += P.tiled_bytes;
+  }
+  HIP_TRY(hipSetDevice(c->device));
+  HIP_TRY(hipMalloc(&W->tiled, W->tiled_bytes));
+  hipError_t e = hipSuccess;
+  uint64_t off = 0;
+  for (uint32_t i = 0; i < count && e == hipSuccess; i++) {
+    e = hipMemcpy(W->tiled + off, parts[i]->tiled, parts[i]->tiled_bytes, hipMemcpyDeviceToDevice);
+    off += parts[i]->tiled_bytes;
+  }
+  if (e != hipSuccess) {
+    hipFree(W->tiled);
+    return fail(GMOE_ERR_DEVICE, "stacking dense weights: %s", hipGetErrorString(e));
+  }
+  if (gmoe_status s = dense_tables(c, W.get())) return s;
+  *out = (uint32_t)c->dense.size();
+  c->dense.push_back(std::move(W));
+  return GMOE_OK;
+}
 
 // Shapes of registered weights, for the decode-step driver (gmoe_model.cpp).
 bool dense_shape(gmoe_ctx* c, uint32_t id, uint32_t* rows, uint32_t* cols) {
@@ -987,27 +1054,7 @@ gmoe_status gmoe_dense_register(gmoe_ctx* c, const gmoe_dense_desc* desc, uint32
   unit_of(W->qtype, &un);
   W->tiled_bytes = tiled_bytes(un, W->rows, W->cols);
   HIP_TRY(hipMalloc(&W->tiled, W->tiled_bytes));
-  {
-    std::vector<ExpertWork> tab(kDenseTab);
-    for (uint32_t i = 0; i < kDenseTab; i++) tab[i] = ExpertWork{{W->tiled, W->tiled, W->tiled}, 0, 0, i + 1, 0};
-    hipError_t e = hipMalloc(&W->work_tab, tab.size() * sizeof(ExpertWork));
-    if (e == hipSuccess) e = hipMemcpy(W->work_tab, tab.data(), tab.size() * sizeof(ExpertWork), hipMemcpyHostToDevice);
-    if (e == hipSuccess && !c->ident) {
-      std::vector<uint32_t> id(kDenseTab);
-      for (uint32_t i = 0; i < kDenseTab; i++) id[i] = i;
-      e = hipMalloc(&c->ident, kDenseTab * 4);
-      if (e == hipSuccess) e = hipMemcpy(c->ident, id.data(), kDenseTab * 4, hipMemcpyHostToDevice);
-      if (e != hipSuccess && c->ident) {
-        hipFree(c->ident);
-        c->ident = nullptr;
-      }
-    }
-    if (e != hipSuccess) {
-      hipFree(W->tiled);
-      if (W->work_tab) hipFree(W->work_tab);
-      return fail(GMOE_ERR_DEVICE, "dense weight tables: %s", hipGetErrorString(e));
-    }
-  }
+  if (gmoe_status s = dense_tables(c, W.get())) return s;
   Proj P;
   P.qtype = W->qtype;
   P.rows = W->rows;

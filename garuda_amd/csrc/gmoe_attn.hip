@@ -49,7 +49,7 @@ __global__ void __launch_bounds__(256) k_rope_append(AttnArgs a) {
   float* vp = kp + (size_t)a.bs * kvd;
   if (pr < qpairs) {
     const uint32_t h = pr / half, j = pr % half;
-    const float* src = a.q + (size_t)i * a.n_heads * a.hd + h * a.hd;
+    const float* src = a.q + (size_t)i * a.q_stride + h * a.hd;
     float x = src[2 * j], y = src[2 * j + 1];
     rope_pair(x, y, j, a.hd, e.pos, a.theta);
     float* dst = a.qr + (size_t)i * a.n_heads * a.hd + h * a.hd;
@@ -57,13 +57,13 @@ __global__ void __launch_bounds__(256) k_rope_append(AttnArgs a) {
     dst[2 * j + 1] = y;
   } else if (pr < qpairs + a.n_kv * half) {
     const uint32_t p2 = pr - qpairs, h = p2 / half, j = p2 % half;
-    const float* src = a.k + (size_t)i * kvd + h * a.hd;
+    const float* src = a.k + (size_t)i * a.kv_stride + h * a.hd;
     float x = src[2 * j], y = src[2 * j + 1];
     rope_pair(x, y, j, a.hd, e.pos, a.theta);
     const size_t hoff = (size_t)h * a.bs * a.hd;
     kp[hoff + 2 * j] = x;
     kp[hoff + 2 * j + 1] = y;
-    const float* vs = a.v + (size_t)i * kvd + h * a.hd;
+    const float* vs = a.v + (size_t)i * a.kv_stride + h * a.hd;
     vp[hoff + 2 * j] = vs[2 * j];
     vp[hoff + 2 * j + 1] = vs[2 * j + 1];
   }

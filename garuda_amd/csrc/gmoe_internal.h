@@ -279,6 +279,7 @@ struct AttnArgs {
   float* part;           // [n][n_heads][nchunk][hd + 2]: chunk partials (o, m, l)
   uint32_t nchunk;       // chunks of kAttnChunk positions per entry
   float* ctx;            // [n][n_heads * hd]
+  uint32_t q_stride, kv_stride;  // floats between consecutive rows of q, and of k and v
 };
 
 constexpr uint32_t kAttnChunk = 64, kAttnMaxGroup = 16, kAttnMaxHd = 256;

@@ -111,7 +111,7 @@ gmoe_status grow_pinned(gmoe_kv* kv, uint32_t n) {
 // Plans the call's entries (positions, windows, pages) and commits them: lengths advance
 // and pages are taken only when the whole call fits. Then queues the three launches.
 gmoe_status attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, const float* q, const float* k,
-                   const float* v, float* out, hipStream_t st) {
+                   const float* v, float* out, hipStream_t st, uint32_t q_stride = 0, uint32_t kv_stride = 0) {
   const gmoe_kv_desc& D = kv->d;
   if (layer >= D.n_layers) return kfail(GMOE_ERR_INFERENCE, "layer %u of %u", layer, D.n_layers);
   if (n == 0 || !seqs) return kfail(GMOE_ERR_INFERENCE, "empty attention call");
@@ -188,6 +188,8 @@ gmoe_status attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n
   a.part = reinterpret_cast<float*>(kv->scratch + o_part);
   a.nchunk = nchunk;
   a.ctx = out;
+  a.q_stride = q_stride ? q_stride : D.n_heads * D.head_dim;
+  a.kv_stride = kv_stride ? kv_stride : kv->kvd;
   KV_TRY(launch_attention(a, st));
   return GMOE_OK;
 }
@@ -203,6 +205,15 @@ void kv_dims(gmoe_kv* kv, uint32_t* n_layers, uint32_t* q_dim, uint32_t* kv_dim)
   *n_layers = kv->d.n_layers;
   *q_dim = kv->d.n_heads * kv->d.head_dim;
   *kv_dim = kv->kvd;
+}
+
+// Attention over rows of q, k and v that sit q_stride and kv_stride floats apart (the
+// model step's stacked q|k|v projection), queued on st.
+gmoe_status kv_attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, const float* q, const float* k,
+                      const float* v, uint32_t q_stride, uint32_t kv_stride, float* out, hipStream_t st) {
+  std::lock_guard<std::mutex> g(kv->mu);
+  KV_TRY(hipSetDevice(ctx_device(kv->ctx)));
+  return attend(kv, layer, seqs, n, q, k, v, out, st, q_stride, kv_stride);
 }
 
 gmoe_status kv_check_step(gmoe_kv* kv, const uint32_t* seqs, uint32_t n) {

@@ -27,6 +27,9 @@ bool dense_shape(gmoe_ctx* c, uint32_t id, uint32_t* rows, uint32_t* cols);
 bool layer_width(gmoe_ctx* c, uint32_t id, uint32_t* d, uint32_t* ne);
 void kv_dims(gmoe_kv* kv, uint32_t* n_layers, uint32_t* q_dim, uint32_t* kv_dim);
 gmoe_status kv_check_step(gmoe_kv* kv, const uint32_t* seqs, uint32_t n);
+gmoe_status kv_attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, const float* q, const float* k,
+                      const float* v, uint32_t q_stride, uint32_t kv_stride, float* out, hipStream_t st);
+gmoe_status dense_stack(gmoe_ctx* c, const uint32_t* ids, uint32_t count, uint32_t* out);
 }  // namespace gmoe
 
 using namespace gmoe;
@@ -37,7 +40,12 @@ struct gmoe_model {
   uint32_t n_layers = 0, d = 0, vocab = 0, qd = 0, kvd = 0;
   float eps = 0.0f;
   std::vector<uint32_t> moe, wq, wk, wv, wo;
+  // per layer, wq, wk and wv stacked into one weight of q_dim + 2 kv_dim rows (owned),
+  // when their rows are whole 64-row tiles and they share type and math: one product
+  // launch for the three, its output rows q | k | v
+  std::vector<uint32_t> wqkv;
   uint32_t out_id = 0;
+  float* qkv = nullptr;
   float* table = nullptr;  // [vocab][d] token embeddings
   float* norms = nullptr;  // [2 n_layers + 1][d]: attn_norm, ffn_norm per layer, then output_norm
   // per-step activations for up to kModelMaxBatch tokens
@@ -48,8 +56,9 @@ struct gmoe_model {
   std::mutex mu;
 
   ~gmoe_model() {
+    for (uint32_t id : wqkv) gmoe_dense_release(ctx, id);
     for (void* p : {(void*)table, (void*)norms, (void*)x, (void*)h, (void*)q, (void*)k, (void*)v, (void*)cx,
-                    (void*)ao, (void*)y, (void*)logits, (void*)next})
+                    (void*)ao, (void*)y, (void*)logits, (void*)next, (void*)qkv})
       if (p) hipFree(p);
     if (pin_next) hipHostFree(pin_next);
   }
@@ -147,7 +156,8 @@ gmoe_status gmoe_model_create(gmoe_ctx* ctx, const gmoe_model_desc* desc, gmoe_m
                 {(void**)&m->q, B * qd * 4},          {(void**)&m->k, B * kvd * 4},
                 {(void**)&m->v, B * kvd * 4},         {(void**)&m->cx, B * qd * 4},
                 {(void**)&m->ao, B * d * 4},          {(void**)&m->y, B * d * 4},
-                {(void**)&m->logits, B * D.vocab * 4}, {(void**)&m->next, B * 4}};
+                {(void**)&m->logits, B * D.vocab * 4}, {(void**)&m->next, B * 4},
+                {(void**)&m->qkv, B * (qd + 2 * (size_t)kvd) * 4}};
   for (auto& a : allocs) {
     const hipError_t e = hipMalloc(a.p, a.bytes);
     if (e != hipSuccess) return fail(mfail(GMOE_ERR_CACHE, "device memory for the model: %s", hipGetErrorString(e)));
@@ -162,6 +172,18 @@ gmoe_status gmoe_model_create(gmoe_ctx* ctx, const gmoe_model_desc* desc, gmoe_m
   if (e == hipSuccess)
     e = hipMemcpy(m->norms + 2 * (size_t)D.n_layers * d, D.output_norm, d * 4, hipMemcpyHostToDevice);
   if (e != hipSuccess) return fail(mfail(GMOE_ERR_DEVICE, "model upload: %s", hipGetErrorString(e)));
+  if (qd % kTileRows == 0 && kvd % kTileRows == 0) {
+    for (uint32_t l = 0; l < D.n_layers; l++) {
+      const uint32_t parts[3] = {D.wq[l], D.wk[l], D.wv[l]};
+      uint32_t id;
+      if (dense_stack(ctx, parts, 3, &id) != GMOE_OK) break;  // (types differ: separate projections)
+      m->wqkv.push_back(id);
+    }
+    if (m->wqkv.size() != D.n_layers) {
+      for (uint32_t id : m->wqkv) gmoe_dense_release(ctx, id);
+      m->wqkv.clear();
+    }
+  }
   *out = m;
   return GMOE_OK;
 }
@@ -200,10 +222,16 @@ gmoe_status gmoe_model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs, c
   for (uint32_t l = 0; l < m->n_layers; l++) {
     // h = norm(x + previous layer's MoE output, attn_norm)
     M_TRY(launch_add_norm(m->x, l ? m->y : nullptr, m->norms + (2 * (size_t)l) * d, n, d, m->eps, m->h, st));
-    S_TRY(gmoe_dense_forward_async(m->ctx, m->wq[l], m->h, n, m->q, st));
-    S_TRY(gmoe_dense_forward_async(m->ctx, m->wk[l], m->h, n, m->k, st));
-    S_TRY(gmoe_dense_forward_async(m->ctx, m->wv[l], m->h, n, m->v, st));
-    S_TRY(gmoe_attention_async(m->kv, l, seqs, n, m->q, m->k, m->v, m->cx, st));
+    if (!m->wqkv.empty()) {
+      const uint32_t row = m->qd + 2 * m->kvd;
+      S_TRY(gmoe_dense_forward_async(m->ctx, m->wqkv[l], m->h, n, m->qkv, st));
+      S_TRY(kv_attend(m->kv, l, seqs, n, m->qkv, m->qkv + m->qd, m->qkv + m->qd + m->kvd, row, row, m->cx, st));
+    } else {
+      S_TRY(gmoe_dense_forward_async(m->ctx, m->wq[l], m->h, n, m->q, st));
+      S_TRY(gmoe_dense_forward_async(m->ctx, m->wk[l], m->h, n, m->k, st));
+      S_TRY(gmoe_dense_forward_async(m->ctx, m->wv[l], m->h, n, m->v, st));
+      S_TRY(gmoe_attention_async(m->kv, l, seqs, n, m->q, m->k, m->v, m->cx, st));
+    }
     S_TRY(gmoe_dense_forward_async(m->ctx, m->wo[l], m->cx, n, m->ao, st));
     M_TRY(launch_add_norm(m->x, m->ao, m->norms + (2 * (size_t)l + 1) * d, n, d, m->eps, m->h, st));
     S_TRY(gmoe_ffn_forward_async(m->ctx, m->moe[l], m->h, nullptr, n, m->y, nullptr, nullptr, st));

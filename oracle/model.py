@@ -14,8 +14,9 @@ every sequence takes one new token.
 
 norm(x, w) is simd::rmsnorm (simd/mod.rs:166-173: the f32 mean of the squares summed
 left to right, scale = 1 / sqrt(mean + eps), x *= scale) then x *= w elementwise
-(`mul_assign`). The projections are quant::matmul under packed math (oracle.matmul),
-the attention KvOracle (oracle/attention.py), the MoE layer oracle.feed_forward_batch.
+(`mul_assign`). The projections are quant::matmul under packed math (oracle.matmul) or
+simd::matmul over the dequantised weights under f32 math, the attention KvOracle
+(oracle/attention.py), the MoE layer oracle.feed_forward_batch in the same math.
 """
 from __future__ import annotations
 
@@ -55,16 +56,31 @@ class ModelOracle:
     vocab, d); output_norm [d]; token_embd [vocab, d] f32."""
 
     def __init__(self, layers, output, output_norm, token_embd, n_heads, n_kv_heads, head_dim, rms_eps=1e-5,
-                 max_positions=2048, rope_theta=10000.0, threads=8):
+                 max_positions=2048, rope_theta=10000.0, threads=8, packed=True):
+        # packed: Weight::Packed (quant::matmul, int8 activations); else Weight::Full
+        # (simd::matmul over the dequantised weights), for the projections and the experts
+        self.packed, self._deq = packed, {}
+        if not packed:
+            layers = [dict(L, moe=dict(L["moe"], packed=0)) for L in layers]
         self.layers, self.output, self.output_norm = layers, output, np.asarray(output_norm, dtype=np.float32)
         self.table = np.asarray(token_embd, dtype=np.float32)
         self.eps, self.threads = rms_eps, threads
         self.kv = KvOracle(len(layers), n_heads, n_kv_heads, head_dim, max_positions=max_positions,
                            rope_theta=rope_theta)
+        # per token of the last step, the smallest gap over the layers between the k-th and
+        # (k+1)-th largest router logit (in float64): where it is tiny, any reordering of
+        # the sums upstream may pick the other expert
+        self.last_margins = None
 
     def _matmul(self, w, xs):
         qt, raw, rows, cols = w
-        return O.matmul(qt, raw, rows, cols, xs, xs.shape[0], threads=self.threads).reshape(xs.shape[0], rows)
+        n = xs.shape[0]
+        if self.packed:
+            return O.matmul(qt, raw, rows, cols, xs, n, threads=self.threads).reshape(n, rows)
+        key = id(raw)
+        if key not in self._deq:
+            self._deq[key] = (raw, O.dequantize(qt, raw, rows * cols, checked=False).reshape(rows, cols))
+        return O.simd_matmul(self._deq[key][1], rows, cols, xs, n, threads=self.threads).reshape(n, rows)
 
     def decode_step(self, seqs, tokens):
         """(next tokens, logits [n, vocab]) of one step; seqs distinct."""
@@ -76,6 +92,7 @@ class ModelOracle:
             if t >= vocab:
                 raise ValueError(f"token {t} outside the vocabulary")
         xs = [self.table[t].copy() for t in tokens]
+        margins = np.full(n, np.inf)
         for l, L in enumerate(self.layers):
             hs = np.stack([norm(x, L["attn_norm"], self.eps) for x in xs])
             q, k, v = self._matmul(L["wq"], hs), self._matmul(L["wk"], hs), self._matmul(L["wv"], hs)
@@ -85,9 +102,15 @@ class ModelOracle:
             for i in range(n):
                 xs[i] = (xs[i] + ao[i]).astype(np.float32)
                 hf.append(norm(xs[i], L["ffn_norm"], self.eps))
-            ffn, _, _ = O.feed_forward_batch(L["moe"], np.stack(hf), threads=self.threads)
+            mo = L["moe"]
+            if mo["k"] < mo["ne"]:
+                lg = np.stack(hf).astype(np.float64) @ np.asarray(mo["router"], dtype=np.float64).reshape(mo["ne"], -1).T
+                srt = np.sort(lg, axis=1)
+                margins = np.minimum(margins, srt[:, -mo["k"]] - srt[:, -mo["k"] - 1])
+            ffn, _, _ = O.feed_forward_batch(mo, np.stack(hf), threads=self.threads)
             for i in range(n):
                 xs[i] = (xs[i] + ffn[i]).astype(np.float32)
+        self.last_margins = margins
         hidden = np.stack([norm(x, self.output_norm, self.eps) for x in xs])
         logits = self._matmul(self.output, hidden)
         return np.array([greedy(r) for r in logits], dtype=np.uint32), logits
