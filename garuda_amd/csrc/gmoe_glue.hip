@@ -35,47 +35,88 @@ __global__ void __launch_bounds__(256) k_embed(GlueTokens tk, const float* __res
 }
 
 // grid n, 256 threads: with y, x[i] += y[i] first (written back); then
-// h[i] = (x[i] * scale) * w with scale = 1 / sqrt(mean(x[i]^2) + eps).
+// h[i] = (x[i] * scale) * w with scale = 1 / sqrt(mean(x[i]^2) + eps). A thread holds its
+// kNormVec float4 of the row (d <= 4 * 256 * kNormVec, checked by the model) in
+// registers, every load issued before any use.
 __global__ void __launch_bounds__(256) k_add_norm(float* __restrict__ x, const float* __restrict__ y,
                                                   const float* __restrict__ w, uint32_t d, float eps,
                                                   float* __restrict__ h) {
   __shared__ float part[4];
-  const uint32_t i = blockIdx.x, t = threadIdx.x;
-  float* xr = x + (size_t)i * d;
-  const float* yr = y ? y + (size_t)i * d : nullptr;
-  float sq = 0.0f;
-  for (uint32_t c = t; c < d; c += 256) {
-    float v = xr[c];
-    if (yr) {
-      v = v + yr[c];
-      xr[c] = v;
+  const uint32_t i = blockIdx.x, t = threadIdx.x, nv = d / 4;
+  float4* xr = reinterpret_cast<float4*>(x + (size_t)i * d);
+  const float4* yr = y ? reinterpret_cast<const float4*>(y + (size_t)i * d) : nullptr;
+  const float4* wr = reinterpret_cast<const float4*>(w);
+  float4* hr = reinterpret_cast<float4*>(h + (size_t)i * d);
+  float4 xv[kNormVec], yv[kNormVec];
+#pragma unroll
+  for (int r = 0; r < kNormVec; r++) {
+    const uint32_t c = t + 256 * r;
+    if (c < nv) xv[r] = xr[c];
+  }
+  if (yr) {
+#pragma unroll
+    for (int r = 0; r < kNormVec; r++) {
+      const uint32_t c = t + 256 * r;
+      if (c < nv) yv[r] = yr[c];
     }
-    sq = sq + v * v;
+#pragma unroll
+    for (int r = 0; r < kNormVec; r++) {
+      const uint32_t c = t + 256 * r;
+      if (c < nv) {
+        xv[r] = make_float4(xv[r].x + yv[r].x, xv[r].y + yv[r].y, xv[r].z + yv[r].z, xv[r].w + yv[r].w);
+        xr[c] = xv[r];
+      }
+    }
+  }
+  float sq = 0.0f;
+#pragma unroll
+  for (int r = 0; r < kNormVec; r++) {
+    const uint32_t c = t + 256 * r;
+    if (c < nv) {
+      sq = sq + xv[r].x * xv[r].x;
+      sq = sq + xv[r].y * xv[r].y;
+      sq = sq + xv[r].z * xv[r].z;
+      sq = sq + xv[r].w * xv[r].w;
+    }
   }
   sq = glue_wave_sum(sq);
   if ((t & 63) == 0) part[t >> 6] = sq;
   __syncthreads();
   const float mean = (part[0] + part[1] + part[2] + part[3]) / (float)d;
   const float scale = fdiv(1.0f, __fsqrt_rn(mean + eps));
-  float* hr = h + (size_t)i * d;
-  for (uint32_t c = t; c < d; c += 256) hr[c] = (xr[c] * scale) * w[c];
+#pragma unroll
+  for (int r = 0; r < kNormVec; r++) {
+    const uint32_t c = t + 256 * r;
+    if (c < nv) {
+      const float4 v = xv[r], g = wr[c];
+      hr[c] = make_float4((v.x * scale) * g.x, (v.y * scale) * g.y, (v.z * scale) * g.z, (v.w * scale) * g.w);
+    }
+  }
 }
 
 // grid n, 256 threads: next[i] = the first index of row i's largest value
 __global__ void __launch_bounds__(256) k_argmax(const float* __restrict__ logits, uint32_t vocab,
                                                 uint32_t* __restrict__ next) {
+  constexpr int U = 8;  // loads in flight per thread
   __shared__ float bvs[4];
   __shared__ uint32_t bis[4];
   const uint32_t i = blockIdx.x, t = threadIdx.x;
   const float* row = logits + (size_t)i * vocab;
   float bv = -INFINITY;
   uint32_t bi = ~0u;
-  for (uint32_t c = t; c < vocab; c += 256) {  // ascending: keeps the thread's first maximum
-    const float v = row[c];
-    if (v > bv) {
-      bv = v;
-      bi = c;
+  for (uint32_t c0 = t; c0 < vocab; c0 += 256 * U) {  // ascending: keeps the thread's first maximum
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const uint32_t c = c0 + 256 * u;
+      v[u] = c < vocab ? row[c] : -INFINITY;
     }
+#pragma unroll
+    for (int u = 0; u < U; u++)
+      if (v[u] > bv) {
+        bv = v[u];
+        bi = c0 + 256 * u;
+      }
   }
   // larger value first, then the lower index (an index of ~0u found nothing)
   for (int o = 32; o >= 1; o >>= 1) {

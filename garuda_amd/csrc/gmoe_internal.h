@@ -288,6 +288,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 // Decode-step glue (gmoe_glue.hip): embedding rows, residual add + RMSNorm * weight,
 // greedy token. A decode step carries its tokens in the kernel arguments.
 constexpr uint32_t kModelMaxBatch = 64;
+constexpr int kNormVec = 8;  // float4 of a row per thread in k_add_norm: d_model <= 8192
 struct GlueTokens {
   uint32_t tok[kModelMaxBatch];
 };

@@ -109,6 +109,8 @@ gmoe_status gmoe_model_create(gmoe_ctx* ctx, const gmoe_model_desc* desc, gmoe_m
     return mfail(GMOE_ERR_INFERENCE, "null weight array in the model descriptor");
   if (D.n_layers == 0 || D.d_model == 0 || D.vocab == 0 || D.d_model % 4)
     return mfail(GMOE_ERR_CONFIG, "model dimensions must be positive, d_model a multiple of 4");
+  if (D.d_model > 4u * 256u * kNormVec)
+    return mfail(GMOE_ERR_CONFIG, "d_model %u is above the %u a norm workgroup holds", D.d_model, 4u * 256u * kNormVec);
   if (D.token_embd_qtype != GMOE_F32) return mfail(GMOE_ERR_MODEL, "token embeddings must be F32 rows");
   uint32_t kl, qd, kvd;
   kv_dims(D.kv, &kl, &qd, &kvd);

@@ -341,7 +341,7 @@ gmoe_status gmoe_prefetch_step(gmoe_ctx* ctx, gmoe_predictor* p, uint32_t layer_
  * and the norm weights are copied into device memory. */
 typedef struct gmoe_model gmoe_model;
 typedef struct gmoe_model_desc {
-  uint32_t n_layers, d_model, vocab;
+  uint32_t n_layers, d_model, vocab;  /* d_model a multiple of 4, at most 8192 */
   float rms_eps;
   gmoe_kv* kv;                  /* n_layers layers; its heads set the q and kv widths */
   const uint32_t* moe_layers;   /* [n_layers] gmoe_layer_register ids (d_model wide) */

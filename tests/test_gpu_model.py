@@ -152,5 +152,11 @@ def test_refusals_leave_the_sequences_unchanged(dev, weights):
         moe[1].prefetch(0)
         model.decode_step([c], [1])
         assert kv.seq_len(c, NL - 1) == 1
+        # a model wider than a norm workgroup holds (8192) is refused at create
+        wide = 8196
+        with pytest.raises(G.ConfigError):
+            G.DecodeModel(dev, kv, moe, *[parts[3][n] for n in ("wq", "wk", "wv", "wo")], parts[4],
+                          np.ones((NL, wide), np.float32), np.ones((NL, wide), np.float32), np.ones(wide, np.float32),
+                          np.zeros((VOCAB, wide), np.float32))
     finally:
         release(*parts)
