@@ -342,13 +342,16 @@ __device__ __forceinline__ void quant_wave(float v, uint32_t lane, bool valid, i
 
 // The activation sums a packed dot reads, one 32-bit word each: f32 sums of 32 values
 // (Q4_K, Q5_K: the reference converts the i32 sum, which is exact below 2^24), f32
-// sums of 16 (Q2_K), i32 sums of 16 (Q6_K, Q3_K fold them into the integer dot), or
-// none (Q8_0).
+// sums of 16 (Q2_K), i32 sums of 16 times the type's offset (Q6_K -32, Q3_K -4: the
+// dot's integer chain starts from it, so it adds the -32 or -4 times the sum that the
+// reference subtracts; integer sums are exact in any order), or none (Q8_0).
 enum SumKind { kSumNone = 0, kSumF32x32 = 1, kSumF32x16 = 2, kSumI32x16 = 3 };
 template <int QT>
 __host__ __device__ constexpr int sum_kind() {
   return (QT == Q4_K || QT == Q5_K) ? kSumF32x32 : QT == Q2_K ? kSumF32x16 : (QT == Q6_K || QT == Q3_K) ? kSumI32x16 : kSumNone;
 }
+template <int QT>
+__host__ __device__ constexpr int32_t sum_offset() { return QT == Q6_K ? -32 : QT == Q3_K ? -4 : 1; }
 __host__ __device__ constexpr uint32_t sum_width(int kind) { return kind == kSumF32x32 ? 32u : kind ? 16u : 0u; }
 
 // quant/mod.rs:586-621
@@ -446,10 +449,9 @@ __device__ __forceinline__ void pk_q6k(const uint32_t* w, const int8_t* const* x
     for (int t = 0; t < TM; t++) {
       if (t < m) {
         const uint32_t* xa = reinterpret_cast<const uint32_t*>(x[t] + 16 * s);
-        int dt = 0;
+        int dt = (int)sm[t][s];  // -32 * the sub-block's sum
 #pragma unroll
         for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
-        dt -= 32 * (int)sm[t][s];
         acc[t] += xs[t][s / 2] * d * sc * (float)dt;
       }
     }
@@ -479,10 +481,9 @@ __device__ __forceinline__ void pk_q3k(const uint32_t* w, const int8_t* const* x
     for (int t = 0; t < TM; t++) {
       if (t < m) {
         const uint32_t* xa = reinterpret_cast<const uint32_t*>(x[t] + 16 * s);
-        int dt = 0;
+        int dt = (int)sm[t][s];  // -4 * the sub-block's sum
 #pragma unroll
         for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
-        dt -= 4 * (int)sm[t][s];
         acc[t] += xs[t][s / 2] * dl * (float)dt;
       }
     }

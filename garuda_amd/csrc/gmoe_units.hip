@@ -162,8 +162,8 @@ __device__ __forceinline__ void stage_acts(uint8_t* lds, uint32_t nelem, uint32_
           hs[2 * b] = __float_as_uint((float)s0);
           hs[2 * b + 1] = __float_as_uint((float)s1);
         } else if constexpr (KIND == kSumI32x16) {
-          hs[2 * b] = (uint32_t)s0;
-          hs[2 * b + 1] = (uint32_t)s1;
+          hs[2 * b] = (uint32_t)(sum_offset<QT>() * s0);
+          hs[2 * b + 1] = (uint32_t)(sum_offset<QT>() * s1);
         }
       }
       return;
@@ -177,7 +177,7 @@ __device__ __forceinline__ void stage_acts(uint8_t* lds, uint32_t nelem, uint32_
         const int32_t* src = s16 + (size_t)r * (K / 16) + k0 / 16;
         if constexpr (KIND == kSumF32x32) return __float_as_uint((float)(src[2 * c] + src[2 * c + 1]));
         else if constexpr (KIND == kSumF32x16) return __float_as_uint((float)src[c]);
-        else return (uint32_t)src[c];
+        else return (uint32_t)(sum_offset<QT>() * src[c]);
       });
     }
   } else {
