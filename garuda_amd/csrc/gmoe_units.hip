@@ -20,7 +20,8 @@ namespace gmoe {
 // A workgroup owns one 64-row tile of an expert matrix and lane i owns row i of it. A
 // wave streams the tile's units in K order: unit u arrives as NP coalesced 1 KiB loads
 // that leave row i's U bytes in lane i's registers, with no exchange between lanes.
-// Three register sets form a ring, so two units stay in flight while one is computed.
+// Register sets form a ring (two; four for single-token gate/up), so the next units'
+// loads are in flight while one is computed.
 // The activations of the chunk of tokens being served sit in LDS (staged once per
 // chunk) and are read as broadcasts.
 // ---------------------------------------------------------------------------------
