@@ -667,16 +667,18 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
   const float* hs = B.hs + (size_t)t * d;
   const float4* xr = reinterpret_cast<const float4*>(hs);
   // loads whose use comes late, issued first: wave 0's slab pointers for the dispatch
-  // (lane e: expert e's gate, up, down) and the activations of this thread's 32-value
-  // block for the int8 quantiser
+  // (lane e: expert e's gate, up, down) and, for the threads of waves 1 on, the
+  // activations of their 32-value block for the int8 quantiser. Only the expert kernels
+  // read the quantised activations, so those waves quantise after the barrier while
+  // wave 0 runs the candidate test and the dispatch.
   const uint8_t* ep[3] = {nullptr, nullptr, nullptr};
   if (wave == 0 && lane < ne)
     for (int p = 0; p < 3; p++) ep[p] = L.eptr[p * ne + lane];
-  const uint32_t nblk = d / 32;
+  const uint32_t nblk = d / 32, qb = tid - 64;  // block of thread tid >= 64
   float qv[32];
-  const bool qown = quant && tid < nblk && nblk <= kSpecThreads;
+  const bool qown = quant && tid >= 64 && qb < nblk && nblk <= kSpecThreads - 64;
   if (qown) {
-    const float4* src = reinterpret_cast<const float4*>(hs + (size_t)tid * 32);
+    const float4* src = reinterpret_cast<const float4*>(hs + (size_t)qb * 32);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const float4 t4 = src[i];
@@ -718,10 +720,7 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
       la[e] = ab;
     }
   }
-  if (qown) {
-    const size_t gb = (size_t)t * nblk + tid;
-    quant32(qv, B.xq + gb * 32, B.xs + gb, B.x16 + 2 * gb);
-  } else if (quant && nblk > kSpecThreads) {
+  if (quant && nblk > kSpecThreads - 64) {  // (wide rows: every thread, before the barrier)
     for (uint32_t b = tid; b < nblk; b += kSpecThreads) {
       float v[32];
       const float4* src = reinterpret_cast<const float4*>(hs + (size_t)b * 32);
@@ -735,7 +734,13 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
     }
   }
   __syncthreads();
-  if (wave != 0) return;
+  if (wave != 0) {
+    if (qown) {
+      const size_t gb = (size_t)t * nblk + qb;
+      quant32(qv, B.xq + gb * 32, B.xs + gb, B.x16 + 2 * gb);
+    }
+    return;
+  }
   // candidate test, lane e < ne, in double
   // each product passes through at most d/64 + 4*kB lane additions (zero padding included)
   // and 6 tree levels
