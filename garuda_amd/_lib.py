@@ -59,6 +59,7 @@ class GmoePredictStats(C.Structure):
 SIGNATURES = {
     "gmoe_abi_version": (u32, []),
     "gmoe_last_error": (C.c_char_p, []),
+    "gmoe_last_invalid_token": (u32, []),
     "gmoe_init": (i32, [i32, u64, C.POINTER(vp)]),
     "gmoe_shutdown": (None, [vp]),
     "gmoe_layer_register": (i32, [vp, C.POINTER(GmoeLayerDesc), u32p]),

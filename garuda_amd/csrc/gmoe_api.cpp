@@ -29,6 +29,7 @@ using namespace gmoe;
 namespace {
 
 thread_local std::string g_err;
+thread_local uint32_t g_bad_token = UINT32_MAX;  // the token of the last GMOE_ERR_INVALID_TOKEN
 
 gmoe_status fail(gmoe_status s, const char* fmt, ...) {
   char buf[512];
@@ -130,6 +131,8 @@ struct Proj {
   std::vector<const uint8_t*> host;      // per expert
 };
 
+using LruList = std::list<std::pair<uint32_t, uint32_t>>;  // (layer, expert), least recent first
+
 struct Layer {
   uint32_t d, f, ne, k, gating, combine, math;
   Proj p[3];                      // gate, up, down
@@ -137,7 +140,11 @@ struct Layer {
   const uint8_t** eptr = nullptr; // device [3][ne]
   std::vector<const uint8_t*> eptr_host;
   std::vector<int64_t> slot;      // per expert: slab offset or -1
+  std::vector<LruList::iterator> lru_pos;  // per resident expert: its place in the LRU
   uint64_t expert_bytes = 0;
+  // recorded on the call's stream after every forward of the layer: an evicted expert's
+  // region is free once the layer's last queued call has finished
+  hipEvent_t last_use = nullptr;
   bool alive = true;
 };
 
@@ -158,11 +165,14 @@ struct Dense {
 // Calls of up to kDenseTab tokens read a precomputed work entry and the context's
 // identity table (slot -> token, and token tiles) instead of a setup launch.
 constexpr uint32_t kDenseTab = 2048;
+// Experts a layer may have: the dispatch keeps three words per expert in LDS.
+constexpr uint32_t kMaxExperts = 4096;
 
 }  // namespace
 
 namespace gmoe {
 void set_last_error(const char* msg) { g_err = msg; }
+void set_invalid_token(uint32_t token) { g_bad_token = token; }
 }  // namespace gmoe
 
 struct gmoe_ctx {
@@ -174,16 +184,18 @@ struct gmoe_ctx {
   std::vector<std::unique_ptr<Layer>> layers;
   std::vector<std::unique_ptr<Dense>> dense;
   uint32_t* ident = nullptr;  // [kDenseTab] = 0, 1, 2, ... (device)
-  std::list<std::pair<uint32_t, uint32_t>> lru;  // (layer, expert), least recent first
+  LruList lru;
   gmoe_slab_stats stats{};
   uint8_t* pinned = nullptr;
   size_t pinned_bytes = 0;
   uint8_t* bounce = nullptr;  // device landing area of the pinned halves (same size)
   uint32_t* done = nullptr;   // front-end completion counter (device, zero between calls)
   hipEvent_t pin_ev[2]{};
-  // scratch arena
+  // scratch arena; scratch_ev is recorded after every call that uses it (calls on one
+  // context are ordered on one stream), so growing the arena waits for that call only
   uint8_t* scratch = nullptr;
   size_t scratch_bytes = 0;
+  hipEvent_t scratch_ev = nullptr;
   // timing
   bool timing = false;
   std::vector<Timing> pending;
@@ -247,30 +259,24 @@ gmoe_status stage_proj(gmoe_ctx* c, const Proj& P, const uint8_t* src, uint8_t* 
   return GMOE_OK;
 }
 
+// Mark resident expert e of layer l most recently used (ExpertCache::get, cache/mod.rs:70-84).
 void touch(gmoe_ctx* c, uint32_t l, uint32_t e) {
-  for (auto it = c->lru.begin(); it != c->lru.end(); ++it)
-    if (it->first == l && it->second == e) {
-      c->lru.erase(it);
-      break;
-    }
-  c->lru.emplace_back(l, e);
+  Layer& L = *c->layers[l];
+  if (L.slot[e] < 0) return;
+  c->lru.splice(c->lru.end(), c->lru, L.lru_pos[e]);
 }
 
 gmoe_status evict(gmoe_ctx* c, uint32_t l, uint32_t e) {
   Layer& L = *c->layers[l];
   if (L.slot[e] < 0) return GMOE_OK;
-  // the slab region may still be read by queued work, on the context's stream or on a
-  // caller's (gmoe_ffn_forward_async)
-  HIP_TRY(hipDeviceSynchronize());
+  // the slab region may still be read by the layer's queued calls, on the context's stream
+  // or on a caller's (gmoe_ffn_forward_async): wait for the last one
+  HIP_TRY(hipEventSynchronize(L.last_use));
   c->slab.release((uint64_t)L.slot[e], L.expert_bytes);
   L.slot[e] = -1;
   for (int p = 0; p < 3; p++) L.eptr_host[p * L.ne + e] = nullptr;
   HIP_TRY(hipMemcpy(L.eptr, L.eptr_host.data(), L.eptr_host.size() * sizeof(void*), hipMemcpyHostToDevice));
-  for (auto it = c->lru.begin(); it != c->lru.end(); ++it)
-    if (it->first == l && it->second == e) {
-      c->lru.erase(it);
-      break;
-    }
+  c->lru.erase(L.lru_pos[e]);
   c->stats.entries--;
   c->stats.bytes -= L.expert_bytes;
   return GMOE_OK;
@@ -320,7 +326,7 @@ gmoe_status make_resident(gmoe_ctx* c, uint32_t l, uint32_t e, bool evict_ok,
   HIP_TRY(hipStreamSynchronize(c->copy_stream));
   HIP_TRY(hipMemcpy(L.eptr, L.eptr_host.data(), L.eptr_host.size() * sizeof(void*), hipMemcpyHostToDevice));
   L.slot[e] = (int64_t)off;
-  c->lru.emplace_back(l, e);
+  L.lru_pos[e] = c->lru.emplace(c->lru.end(), l, e);
   c->stats.entries++;
   c->stats.bytes += L.expert_bytes;
   return GMOE_OK;
@@ -405,7 +411,7 @@ size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
 
 gmoe_status ensure_scratch(gmoe_ctx* c, size_t bytes) {
   if (bytes <= c->scratch_bytes) return GMOE_OK;
-  HIP_TRY(hipStreamSynchronize(c->stream));
+  HIP_TRY(hipEventSynchronize(c->scratch_ev));  // the last call that used the old arena
   if (c->scratch) HIP_TRY(hipFree(c->scratch));
   c->scratch = nullptr;
   c->scratch_bytes = 0;
@@ -509,8 +515,15 @@ gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStr
     c->pending.push_back(tm);
   }
   HIP_TRY(launch_combine(D, B, n, ksg, st));
+  HIP_TRY(hipEventRecord(L.last_use, st));
+  HIP_TRY(hipEventRecord(c->scratch_ev, st));
   return GMOE_OK;
 }
+
+// Tokens per layer launch sequence: the kernels index (token, expert) pairs in a grid
+// dimension of at most 65535, so a longer batch runs as consecutive sequences. Each
+// token's output depends on its own row only, so the split changes no result's meaning.
+uint32_t call_tokens(const Layer& L) { return std::min<uint32_t>(4096u, 65535u / L.k); }
 
 gmoe_status check_ctx(gmoe_ctx* c) {
   if (!c) return fail(GMOE_ERR_INFERENCE, "null context");
@@ -624,6 +637,11 @@ gmoe_status run_dense(const Dense& W, const DenseCarve& cv, const float* x, uint
   return GMOE_OK;
 }
 
+gmoe_status mark_scratch(gmoe_ctx* c, hipStream_t st) {
+  HIP_TRY(hipEventRecord(c->scratch_ev, st));
+  return GMOE_OK;
+}
+
 gmoe_status get_dense(gmoe_ctx* c, uint32_t id, Dense** out) {
   if (id >= c->dense.size() || !c->dense[id] || !c->dense[id]->alive)
     return fail(GMOE_ERR_INFERENCE, "unknown dense weight id %u", id);
@@ -638,15 +656,9 @@ gmoe_status get_layer(gmoe_ctx* c, uint32_t id, Layer** out) {
   return GMOE_OK;
 }
 
-gmoe_status forward_host(gmoe_ctx* c, uint32_t lid, const float* hs, const float* logits, uint32_t n,
-                         float* out, uint32_t* ids, float* w) {
-  if (gmoe_status s = check_ctx(c)) return s;
-  if (!hs || !out) return fail(GMOE_ERR_INFERENCE, "null activation pointer");
-  if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
-  std::lock_guard<std::mutex> g(c->mu);
-  Layer* L;
-  if (gmoe_status s = get_layer(c, lid, &L)) return s;
-  HIP_TRY(hipSetDevice(c->device));
+// One launch sequence of at most call_tokens(L) tokens, host pointers (the lock is held).
+gmoe_status forward_chunk(gmoe_ctx* c, uint32_t lid, Layer* L, const float* hs, const float* logits, uint32_t n,
+                          float* out, uint32_t* ids, float* w) {
   Carved cv;
   size_t need = plan_scratch(*L, n, nullptr, nullptr);
   if (gmoe_status s = ensure_scratch(c, need)) return s;
@@ -687,8 +699,6 @@ gmoe_status forward_host(gmoe_ctx* c, uint32_t lid, const float* hs, const float
       HIP_TRY(hipMemcpyAsync(cv.d_logits_in, B.logits, (size_t)n * L->ne * 4, hipMemcpyDeviceToDevice, st));
       B.logits_in = cv.d_logits_in;
     }
-  } else {
-    for (uint32_t e = 0; e < L->ne; e++) touch(c, lid, e);
   }
   if (gmoe_status s = run_layer(c, *L, B, n, st)) return s;
   HIP_TRY(hipMemcpyAsync(out, B.out, (size_t)n * L->d * 4, hipMemcpyDeviceToHost, st));
@@ -697,8 +707,33 @@ gmoe_status forward_host(gmoe_ctx* c, uint32_t lid, const float* hs, const float
   if (w) HIP_TRY(hipMemcpyAsync(w, B.w, (size_t)n * L->k * 4, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
   if (all) {  // every routed expert was resident: one hit per distinct expert, as above
-    std::sort(hid.begin(), hid.end());
-    c->stats.hits += (uint64_t)(std::unique(hid.begin(), hid.end()) - hid.begin());
+    std::vector<uint32_t> u(hid);
+    std::sort(u.begin(), u.end());
+    c->stats.hits += (uint64_t)(std::unique(u.begin(), u.end()) - u.begin());
+  }
+  // the LRU sees each routed expert as fetched in token order, then rank order, as the
+  // engine's loader fetches them (moe/mod.rs:98-112 -> ExpertCache::get); experts that
+  // were not routed keep their place
+  for (uint32_t e : hid) touch(c, lid, e);
+  return GMOE_OK;
+}
+
+gmoe_status forward_host(gmoe_ctx* c, uint32_t lid, const float* hs, const float* logits, uint32_t n,
+                         float* out, uint32_t* ids, float* w) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (!hs || !out) return fail(GMOE_ERR_INFERENCE, "null activation pointer");
+  if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
+  std::lock_guard<std::mutex> g(c->mu);
+  Layer* L;
+  if (gmoe_status s = get_layer(c, lid, &L)) return s;
+  HIP_TRY(hipSetDevice(c->device));
+  const uint32_t per = call_tokens(*L);
+  for (uint32_t t0 = 0; t0 < n; t0 += per) {
+    const uint32_t m = std::min(per, n - t0);
+    const size_t k = L->k;
+    if (gmoe_status s = forward_chunk(c, lid, L, hs + (size_t)t0 * L->d, logits ? logits + (size_t)t0 * L->ne : nullptr,
+                                      m, out + (size_t)t0 * L->d, ids ? ids + t0 * k : nullptr, w ? w + t0 * k : nullptr))
+      return s;
   }
   return GMOE_OK;
 }
@@ -801,6 +836,8 @@ uint32_t gmoe_abi_version(void) { return GMOE_ABI_VERSION; }
 
 const char* gmoe_last_error(void) { return g_err.c_str(); }
 
+uint32_t gmoe_last_invalid_token(void) { return g_bad_token; }
+
 gmoe_status gmoe_init(int device, uint64_t slab_bytes, gmoe_ctx** out) {
   if (!out) return fail(GMOE_ERR_INFERENCE, "null output pointer");
   *out = nullptr;
@@ -828,6 +865,8 @@ gmoe_status gmoe_init(int device, uint64_t slab_bytes, gmoe_ctx** out) {
   // [0]: front-end workgroups done; [64 .. 64 + kSpecMaxSlots): per-token routing counters
   HIP_TRY(hipMalloc(&c->done, (64 + kSpecMaxSlots) * 4));
   HIP_TRY(hipMemset(c->done, 0, (64 + kSpecMaxSlots) * 4));
+  HIP_TRY(hipEventCreateWithFlags(&c->scratch_ev, hipEventDisableTiming));
+  HIP_TRY(hipEventRecord(c->scratch_ev, c->stream));
   HIP_TRY(hipEventCreateWithFlags(&c->pin_ev[0], hipEventDisableTiming));
   HIP_TRY(hipEventCreateWithFlags(&c->pin_ev[1], hipEventDisableTiming));
   HIP_TRY(hipEventRecord(c->pin_ev[0], c->copy_stream));
@@ -845,6 +884,7 @@ void gmoe_shutdown(gmoe_ctx* c) {
     if (L) {
       hipFree(L->router);
       hipFree((void*)L->eptr);
+      if (L->last_use) hipEventDestroy(L->last_use);
     }
   for (auto& t : c->pending) c->pool.push_back(t);
   for (auto& t : c->pool) {
@@ -865,6 +905,7 @@ void gmoe_shutdown(gmoe_ctx* c) {
   if (c->done) hipFree(c->done);
   hipEventDestroy(c->pin_ev[0]);
   hipEventDestroy(c->pin_ev[1]);
+  if (c->scratch_ev) hipEventDestroy(c->scratch_ev);
   hipStreamDestroy(c->stream);
   hipStreamDestroy(c->copy_stream);
   delete c;
@@ -879,6 +920,8 @@ gmoe_status gmoe_layer_register(gmoe_ctx* c, const gmoe_layer_desc* desc, uint32
   if (D.top_k == 0 || D.top_k > D.n_experts)
     return fail(GMOE_ERR_CONFIG, "top_k (%u) must be in 1..=%u", D.top_k, D.n_experts);
   if (D.top_k > 32) return fail(GMOE_ERR_CONFIG, "top_k above 32 is not supported");
+  if (D.n_experts > kMaxExperts)
+    return fail(GMOE_ERR_CONFIG, "n_experts (%u) above %u is not supported", D.n_experts, kMaxExperts);
   if (D.gating > 3 || D.combine > 1 || D.math > 1) return fail(GMOE_ERR_CONFIG, "unknown gating/combine/math");
   if (!D.router) return fail(GMOE_ERR_MODEL, "router weights missing");
   const gmoe_tensor* T[3] = {&D.gate, &D.up, &D.down};
@@ -928,6 +971,9 @@ gmoe_status gmoe_layer_register(gmoe_ctx* c, const gmoe_layer_desc* desc, uint32
   HIP_TRY(hipMalloc((void**)&L->eptr, 3 * L->ne * sizeof(void*)));
   HIP_TRY(hipMemcpy(L->eptr, L->eptr_host.data(), 3 * L->ne * sizeof(void*), hipMemcpyHostToDevice));
   L->slot.assign(L->ne, -1);
+  L->lru_pos.resize(L->ne);
+  HIP_TRY(hipEventCreateWithFlags(&L->last_use, hipEventDisableTiming));
+  HIP_TRY(hipEventRecord(L->last_use, c->stream));
   uint32_t id = (uint32_t)c->layers.size();
   c->layers.push_back(std::move(L));
   Layer& LL = *c->layers.back();
@@ -979,21 +1025,21 @@ gmoe_status gmoe_ffn_forward_async(gmoe_ctx* c, uint32_t lid, const float* d_hs,
     if (L->slot[e] < 0) return fail(GMOE_ERR_CACHE, "expert %u of layer %u is not resident", e, lid);
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t st = stream ? (hipStream_t)stream : c->stream;
-  size_t need = plan_scratch(*L, n, nullptr, nullptr);
-  if (need > c->scratch_bytes) {
-    // growing the arena frees the old one, which queued work on any stream may use
-    HIP_TRY(hipDeviceSynchronize());
-    if (gmoe_status s = ensure_scratch(c, need)) return s;
+  const uint32_t per = call_tokens(*L);
+  if (gmoe_status s = ensure_scratch(c, plan_scratch(*L, std::min(n, per), nullptr, nullptr))) return s;
+  for (uint32_t t0 = 0; t0 < n; t0 += per) {
+    const uint32_t m = std::min(per, n - t0);
+    Carved cv;
+    plan_scratch(*L, m, &cv, c->scratch);
+    FwdBufs B = cv.B;
+    B.hs = d_hs + (size_t)t0 * L->d;
+    B.logits_in = d_logits ? d_logits + (size_t)t0 * L->ne : nullptr;
+    B.out = d_out + (size_t)t0 * L->d;
+    if (d_ids) B.ids = d_ids + (size_t)t0 * L->k;
+    if (d_w) B.w = d_w + (size_t)t0 * L->k;
+    if (gmoe_status s = run_layer(c, *L, B, m, st)) return s;
   }
-  Carved cv;
-  plan_scratch(*L, n, &cv, c->scratch);
-  FwdBufs B = cv.B;
-  B.hs = d_hs;
-  B.logits_in = d_logits;
-  B.out = d_out;
-  if (d_ids) B.ids = d_ids;
-  if (d_w) B.w = d_w;
-  return run_layer(c, *L, B, n, st);
+  return GMOE_OK;
 }
 
 gmoe_status gmoe_expert_prefetch(gmoe_ctx* c, uint32_t lid, uint32_t e) {
@@ -1109,6 +1155,7 @@ gmoe_status gmoe_dense_forward(gmoe_ctx* c, uint32_t id, const float* xs, uint32
   float* dout = (float*)(c->scratch + o_o);
   HIP_TRY(hipMemcpyAsync(dx, xs, (size_t)n * W->cols * 4, hipMemcpyHostToDevice, st));
   if (gmoe_status s = run_dense(*W, cv, dx, n, dout, st)) return s;
+  if (gmoe_status s = mark_scratch(c, st)) return s;
   HIP_TRY(hipMemcpyAsync(out, dout, (size_t)n * W->rows * 4, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
   return GMOE_OK;
@@ -1124,14 +1171,11 @@ gmoe_status gmoe_dense_forward_async(gmoe_ctx* c, uint32_t id, const float* d_xs
   if (gmoe_status s = get_dense(c, id, &W)) return s;
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t st = stream ? (hipStream_t)stream : c->stream;
-  const size_t need = plan_dense(c, *W, n, nullptr, nullptr);
-  if (need > c->scratch_bytes) {
-    HIP_TRY(hipDeviceSynchronize());  // growing the arena frees the old one
-    if (gmoe_status s = ensure_scratch(c, need)) return s;
-  }
+  if (gmoe_status s = ensure_scratch(c, plan_dense(c, *W, n, nullptr, nullptr))) return s;
   DenseCarve cv;
   plan_dense(c, *W, n, c->scratch, &cv);
-  return run_dense(*W, cv, d_xs, n, d_out, st);
+  if (gmoe_status s = run_dense(*W, cv, d_xs, n, d_out, st)) return s;
+  return mark_scratch(c, st);
 }
 
 gmoe_status gmoe_prefetch_step(gmoe_ctx* c, gmoe_predictor* p, uint32_t lid, uint32_t base, const uint32_t* prev,
@@ -1332,6 +1376,7 @@ gmoe_status gmoe_dispatch(gmoe_ctx* c, const uint32_t* ids, const float* w, uint
                           uint32_t* offsets, uint32_t* slot_token, float* slot_weight, uint32_t* slot_rank) {
   if (gmoe_status s = check_ctx(c)) return s;
   if (!ids || !w || !offsets || n == 0 || k == 0 || k > ne) return fail(GMOE_ERR_INFERENCE, "bad dispatch arguments");
+  if (ne > kMaxExperts) return fail(GMOE_ERR_CONFIG, "n_experts (%u) above %u is not supported", ne, kMaxExperts);
   for (uint64_t i = 0; i < (uint64_t)n * k; i++)
     if (ids[i] >= ne) return fail(GMOE_ERR_INFERENCE, "expert id %u out of range", ids[i]);
   std::lock_guard<std::mutex> g(c->mu);

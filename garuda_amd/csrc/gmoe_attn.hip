@@ -178,16 +178,19 @@ __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
     if (rowok && col < q4) reinterpret_cast<float4*>(tile + j * hd)[col] = vreg[r];
   }
   __syncthreads();
-  // per head: max and sum over the chunk, one wave per head in turn
+  // per head: max and sum over the chunk, one wave per head in turn. A NaN or +inf score
+  // makes the reference's softmax uniform over the whole span (simd/mod.rs:132-158): the
+  // chunk's max is then NaN, which the combine reads as that mark.
   const uint32_t lane = t & 63, w = t >> 6;
   for (uint32_t g = w; g < G; g += 4) {
     const float sc = ps(g, lane);  // kAttnChunk == 64: one position a lane
+    const bool bad = __ballot(lane < cnt && (sc != sc || sc == INFINITY)) != 0ull;
     const float m = wave_max(sc);
-    const float pv = lane < cnt ? gm_expf(sc - m) : 0.0f;
+    const float pv = lane < cnt && !bad ? gm_expf(sc - m) : 0.0f;
     ps(g, lane) = pv;
     const float l = wave_sum(pv);
     if (lane == 0) {
-      ml(g, 0) = m;
+      ml(g, 0) = bad ? __int_as_float(0x7fc00000) : m;
       ml(g, 1) = l;
     }
   }
@@ -236,16 +239,32 @@ __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
   }
 }
 
+// The reference's softmax falls back to uniform weights when a score is NaN or +inf, or
+// every score is -inf (simd/mod.rs:132-158); the context is then the values' plain mean,
+// summed as add_scaled does (out += v * (1 / len), positions in order). Column d of
+// query head hh; runs only on that rare input.
+__device__ float attn_uniform(const AttnArgs& a, uint32_t i, uint32_t hh, uint32_t d) {
+  const AttnEntry e = entry(a, i);
+  const uint32_t kh = hh / (a.n_heads / a.n_kv), len = e.pos + 1 - e.start;
+  const float u = fdiv(1.0f, (float)len);
+  const size_t voff = (size_t)a.bs * a.n_kv * a.hd;
+  float acc = 0.0f;
+  for (uint32_t p = e.start; p <= e.pos; p++) acc = acc + key_row(a, e, p, kh)[voff + d] * u;
+  return acc;
+}
+
 // grid (n, n_heads), 256 threads: the chunks merged, context = o / l, in one pass.
 // Thread (g, d) with g < 256 / hd runs over the chunks c = g, g + 256 / hd, ... of column
 // d (16 chunks in flight) with a running max: (M, L, O) is rescaled when a chunk's max
-// exceeds M. The groups are then merged in group order.
+// exceeds M. The groups are then merged in group order. A chunk marked NaN (a NaN or
+// +inf score), or no finite score at all, gives the uniform weights of attn_uniform.
 __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
   __shared__ float gm[256], gl[256], go[256];
   const uint32_t i = blockIdx.x, hh = blockIdx.y, t = threadIdx.x, hd = a.hd, row = hd + 2, nc = a.nchunk;
   const float* base = a.part + ((size_t)i * a.n_heads + hh) * nc * row;
   const uint32_t ng = 256 / hd, g = t / hd, d = t % hd;
   float M = -INFINITY, L = 0.0f, O = 0.0f;
+  bool bad = false;
   if (g < ng) {
     constexpr int kIn = 16;
     for (uint32_t c0 = g; c0 < nc; c0 += kIn * ng) {
@@ -263,6 +282,10 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
       }
 #pragma unroll
       for (int r = 0; r < kIn; r++) {
+        if (mv[r] != mv[r]) {  // a NaN or +inf score in that chunk
+          bad = true;
+          continue;
+        }
         if (mv[r] == -INFINITY) continue;  // an empty chunk
         if (mv[r] > M) {
           const float f = gm_expf(M - mv[r]);  // 0 while M is -inf
@@ -277,14 +300,20 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
       }
     }
   }
-  gm[t] = M;
+  gm[t] = bad ? __int_as_float(0x7fc00000) : M;
   gl[t] = L;
   go[t] = O;
   __syncthreads();
   if (t < hd) {
     float Mt = gm[t], Lt = gl[t], Ot = go[t];
+    bool bad_t = Mt != Mt;
+    if (bad_t) Mt = -INFINITY;
     for (uint32_t k = 1; k < ng; k++) {
       const float m2 = gm[k * hd + t];
+      if (m2 != m2) {
+        bad_t = true;
+        continue;
+      }
       if (m2 == -INFINITY) continue;
       if (m2 > Mt) {
         const float f = gm_expf(Mt - m2);
@@ -297,7 +326,8 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a) {
         Ot = fmaf(go[k * hd + t], f, Ot);
       }
     }
-    a.ctx[(size_t)i * a.n_heads * hd + hh * hd + t] = Ot / Lt;
+    a.ctx[(size_t)i * a.n_heads * hd + hh * hd + t] =
+        bad_t || Mt == -INFINITY ? attn_uniform(a, i, hh, t) : Ot / Lt;
   }
 }
 

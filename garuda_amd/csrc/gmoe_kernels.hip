@@ -252,23 +252,23 @@ __global__ void __launch_bounds__(kRouteThreads) k_route(LayerDev L, FwdBufs B, 
 }
 
 // Dispatch body: a stable counting sort of the (token, rank) pairs by expert id, which is
-// exactly members[e] of llama/mod.rs:967-972 laid end to end. One workgroup of 256
-// threads; sm holds nk + 3*ne + 2 words of LDS. Counts by LDS atomics, the active slots
-// by rank of count, offsets by one wave's running scans, then every pair's slot = its expert's offset +
-// the pairs of that expert before it (counted chunk by chunk against the LDS copy of the
-// ids, the counts of earlier chunks carried per expert). Every thread must call this.
+// exactly members[e] of llama/mod.rs:967-972 laid end to end. One workgroup of T
+// threads; sm holds T + 3*ne + 2 words of LDS, whatever the number of pairs. Counts by
+// LDS atomics, the active slots by rank of count, offsets by one wave's running scans,
+// then every pair's slot = its expert's offset + the pairs of that expert before it
+// (counted chunk of T pairs by chunk against an LDS copy of the chunk's ids, the counts
+// of earlier chunks carried per expert). Every thread must call this.
 __device__ void dispatch_block(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t* sm,
                                const uint32_t* ids, const float* wts) {
   const uint32_t ne = L.ne, k = L.k, nk = n * k, tid = threadIdx.x, T = blockDim.x;
-  uint32_t* idl = sm;            // [nk] ids
-  uint32_t* cnt = sm + nk;       // [ne] counts, then the running count of earlier chunks
+  uint32_t* idl = sm;            // [T] ids of the chunk being placed
+  uint32_t* cnt = sm + T;        // [ne] counts, then the running count of earlier chunks
   uint32_t* start = cnt + ne;    // [ne] offsets
   uint32_t* aidx = start + ne;   // [ne] active slot (~0u: inactive)
   uint32_t* tot = aidx + ne;     // [2] active experts, token tiles
-  for (uint32_t p = tid; p < nk; p += T) idl[p] = ids[p];
   for (uint32_t e = tid; e < ne; e += T) cnt[e] = 0;
   __syncthreads();
-  for (uint32_t p = tid; p < nk; p += T) atomicAdd(&cnt[idl[p]], 1u);
+  for (uint32_t p = tid; p < nk; p += T) atomicAdd(&cnt[ids[p]], 1u);
   __syncthreads();
   // active slot: experts by descending pair count, then ascending id, so that the expert
   // kernels' grids start the experts with the most tokens first
@@ -342,14 +342,16 @@ __device__ void dispatch_block(const LayerDev& L, const FwdBufs& B, uint32_t n, 
   __syncthreads();
   for (uint32_t c0 = 0; c0 < nk; c0 += T) {
     const uint32_t p = c0 + tid;
+    if (p < nk) idl[tid] = ids[p];
+    __syncthreads();
     uint32_t e = ~0u, pos = 0;
     if (p < nk) {
-      e = idl[p];
+      e = idl[tid];
       uint32_t r = 0;
-      for (uint32_t q = c0; q < p; q++) r += idl[q] == e;
+      for (uint32_t q = 0; q < tid; q++) r += idl[q] == e;
       pos = start[e] + cnt[e] + r;
     }
-    __syncthreads();  // every pair of the chunk has read the carried counts
+    __syncthreads();  // every pair of the chunk has read the carried counts and the chunk's ids
     if (p < nk) {
       atomicAdd(&cnt[e], 1u);
       B.slot_tok[pos] = p / k;
@@ -361,8 +363,10 @@ __device__ void dispatch_block(const LayerDev& L, const FwdBufs& B, uint32_t n, 
   }
 }
 
-__global__ void __launch_bounds__(256) k_dispatch(LayerDev L, FwdBufs B, uint32_t n) {
-  extern __shared__ uint32_t dsm_u32[];  // [n*k + 3*ne + 2]
+constexpr uint32_t kDispatchThreads = 256;
+
+__global__ void __launch_bounds__(kDispatchThreads) k_dispatch(LayerDev L, FwdBufs B, uint32_t n) {
+  extern __shared__ uint32_t dsm_u32[];  // [kDispatchThreads + 3*ne + 2]
   dispatch_block(L, B, n, dsm_u32, B.ids, B.w);
 }
 
@@ -808,13 +812,13 @@ hipError_t launch_route(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStre
 }
 
 hipError_t launch_dispatch(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
-  const size_t shm = ((size_t)n * L.k + 3 * (size_t)L.ne + 2) * 4;
-  if (shm > 160 * 1024) return hipErrorInvalidValue;  // the host keeps calls below this
+  const size_t shm = (kDispatchThreads + 3 * (size_t)L.ne + 2) * 4;
+  if (shm > 160 * 1024) return hipErrorInvalidValue;  // registration bounds ne far below this
   static const bool attr =
       hipFuncSetAttribute((const void*)k_dispatch, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) ==
       hipSuccess;
   (void)attr;
-  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(256), shm, st, L, B, n);
+  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(kDispatchThreads), shm, st, L, B, n);
   return hipGetLastError();
 }
 

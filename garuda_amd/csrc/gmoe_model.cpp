@@ -21,6 +21,7 @@
 
 namespace gmoe {
 void set_last_error(const char* msg);
+void set_invalid_token(uint32_t token);
 int ctx_device(gmoe_ctx* c);
 hipStream_t ctx_stream(gmoe_ctx* c);
 bool dense_shape(gmoe_ctx* c, uint32_t id, uint32_t* rows, uint32_t* cols);
@@ -206,6 +207,7 @@ gmoe_status gmoe_model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs, c
   // refuse before any device work, so a step cannot leave a sequence half-advanced
   GlueTokens tk{};
   for (uint32_t i = 0; i < n; i++) {
+    if (tokens[i] >= m->vocab) set_invalid_token(tokens[i]);
     if (tokens[i] >= m->vocab) return mfail(GMOE_ERR_INVALID_TOKEN, "token %u is outside the %u-entry vocabulary", tokens[i], m->vocab);
     tk.tok[i] = tokens[i];
   }

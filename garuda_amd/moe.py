@@ -61,7 +61,9 @@ class NotFoundError(GarudaError, KeyError):
 
 
 class InvalidTokenError(GarudaError):
-    """A token outside the vocabulary (GarudaError::InvalidToken)."""
+    """A token outside the vocabulary (GarudaError::InvalidToken); `token` is its id."""
+
+    token: int = -1
 
 
 _STATUS = {1: ModelError, 2: InferenceError, 3: CacheError, 4: ConfigError, 5: DeviceError, 6: NotFoundError,
@@ -71,7 +73,10 @@ _STATUS = {1: ModelError, 2: InferenceError, 3: CacheError, 4: ConfigError, 5: D
 def _check(status: int) -> None:
     if status != 0:
         msg = lib().gmoe_last_error().decode(errors="replace")
-        raise _STATUS.get(status, GarudaError)(msg)
+        err = _STATUS.get(status, GarudaError)(msg)
+        if status == 7:
+            err.token = int(lib().gmoe_last_invalid_token())
+        raise err
 
 
 def block_layout(qtype: int):

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GMOE_ABI_VERSION 3u
+#define GMOE_ABI_VERSION 4u
 
 /* Status codes. Mirrors the GarudaError variants the reference returns on this
  * path (garuda/src/core/mod.rs:10-47). */
@@ -99,6 +99,9 @@ typedef struct gmoe_slab_stats {
 gmoe_status gmoe_init(int device, uint64_t slab_bytes, gmoe_ctx** out);
 void gmoe_shutdown(gmoe_ctx* ctx);
 const char* gmoe_last_error(void);
+/* The token id of the calling thread's last GMOE_ERR_INVALID_TOKEN, the Token that
+ * GarudaError::InvalidToken carries (garuda/src/core/mod.rs:33-34); UINT32_MAX if none. */
+uint32_t gmoe_last_invalid_token(void);
 uint32_t gmoe_abi_version(void);
 
 /* Register a layer. Validates dims and byte lengths (quant::byte_size,

@@ -8,7 +8,8 @@ Follows LlamaBackend::attend_one (garuda/src/llama/mod.rs:766-821): rope q (ever
 head) and k (every kv head) at pos = the cache's length (simd::rope, simd/mod.rs:196-206,
 in f32 as the reference forms freq and angle), append, then per query head h with kv
 head h / group: scores over [attention_start, pos] = dot(q_h, k_j) * (1/sqrt(hd)),
-softmax, context = sum_j p_j v_j. KVCacheState (cache/mod.rs:221-600): per-layer
+softmax (uniform weights when a score is NaN or +inf, or none is finite, as simd::softmax
+falls back), context = sum_j p_j v_j. KVCacheState (cache/mod.rs:221-600): per-layer
 lengths, the context-window cap (:348-362) and attention_start with a sliding window
 (:333-338). The dot products, softmax and weighted sum are evaluated in float64 here
 (the reference's f32 sums are within the layer tolerance of them).
@@ -65,13 +66,22 @@ class KvOracle:
         V.append(np.asarray(v, dtype=np.float32).copy())
         start = max(0, pos + 1 - self.win) if self.win else 0
         Ks, Vs = np.array(K[start:], dtype=np.float64), np.array(V[start:], dtype=np.float64)
-        scale = 1.0 / np.sqrt(np.float32(hd))
+        Ks32 = np.array(K[start:], dtype=np.float32)
+        scale = np.float32(1.0) / np.sqrt(np.float32(hd))
         out = np.empty(self.nh * hd, dtype=np.float64)
         for h in range(self.nh):
             kh = h // group
-            s = Ks[:, kh * hd:(kh + 1) * hd] @ q[h * hd:(h + 1) * hd].astype(np.float64) * scale
-            p = np.exp(s - s.max())
-            p /= p.sum()
+            with np.errstate(invalid="ignore", over="ignore"):
+                s = Ks[:, kh * hd:(kh + 1) * hd] @ q[h * hd:(h + 1) * hd].astype(np.float64) * scale
+                # the reference's scores are f32 (simd::dot * scale): whether one is NaN or
+                # +inf, or none is above -inf, is read from an f32 evaluation
+                s32 = (Ks32[:, kh * hd:(kh + 1) * hd] @ q[h * hd:(h + 1) * hd]) * np.float32(scale)
+            if np.isnan(s32).any() or np.isposinf(s32).any() or np.isneginf(s32).all():
+                # simd/mod.rs:132-158: a NaN or +inf score, or nothing finite, gives uniform weights
+                p = np.full(s.size, 1.0 / s.size)
+            else:
+                p = np.exp(s - s.max())
+                p /= p.sum()
             out[h * hd:(h + 1) * hd] = p @ Vs[:, kh * hd:(kh + 1) * hd]
         return out
 

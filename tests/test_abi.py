@@ -26,7 +26,8 @@ def test_library_loads_and_exports_every_declared_symbol():
     for s in syms:
         assert hasattr(lib, s), s
     assert set(syms) == set(_lib.SIGNATURES), "ctypes table and header disagree"
-    assert lib.gmoe_abi_version() == 3
+    assert lib.gmoe_abi_version() == 4
+    assert lib.gmoe_last_invalid_token() == 0xFFFFFFFF  # none yet on this thread
 
 
 @pytest.mark.parametrize("qtype", [M.Q4_K, M.Q5_K, M.Q6_K, M.Q3_K, M.Q2_K, M.Q8_0, M.Q4_0, M.F16, M.F32])

@@ -79,3 +79,49 @@ def test_context_window_is_enforced():
         o.attend_one(0, 0, np.ones(4), np.ones(4), np.ones(4))
     with pytest.raises(ValueError):
         o.attend_one(0, 0, np.ones(4), np.ones(4), np.ones(4))
+
+
+def nan_inf_case(bad):
+    """Inputs whose scores hit the reference softmax's fallback: with bad = "nan" the key at
+    position 2 of kv head 0 carries a NaN (every later score of that head is NaN); with
+    bad = "inf" the key at position 0 is (1e30, 0, 0, 0) and the query at position 1 is
+    rotated back onto it, so its f32 score 1e60 / 2 overflows to +inf. Heads of 4 values
+    (2 query heads, 1 kv head) or 8 (4 query heads, 2 kv heads). Returns the steps as
+    (q, k, v) triples."""
+    rng = np.random.default_rng(3)
+    steps = []
+    if bad == "nan":
+        nh, nkv, hd = 4, 2, 8
+        for pos in range(6):
+            q, k, v = rng.normal(size=nh * hd), rng.normal(size=nkv * hd), rng.normal(size=nkv * hd)
+            if pos == 2:
+                k[0] = np.nan
+            steps.append((q, k, v))
+        return (nh, nkv, hd), steps
+    nh, nkv, hd = 2, 1, 4
+    k0 = np.array([1e30, 0, 0, 0])
+    q1 = np.array([np.cos(-1.0) * 1e30, np.sin(-1.0) * 1e30, 0, 0])  # rope at position 1 turns it by +1 rad
+    steps.append((rng.normal(size=nh * hd), k0, rng.normal(size=nkv * hd)))
+    steps.append((np.concatenate([q1, q1]), rng.normal(size=nkv * hd), rng.normal(size=nkv * hd)))
+    return (nh, nkv, hd), steps
+
+
+def test_a_nan_or_infinite_score_gives_uniform_weights():
+    """simd::softmax (simd/mod.rs:132-158): a NaN score poisons the sum and +inf makes the
+    maximum non-finite; both fall back to uniform weights, so the context is the mean of
+    the span's values. Only the kv head whose key carries the bad value is affected."""
+    for bad in ("nan", "inf"):
+        (nh, nkv, hd), steps = nan_inf_case(bad)
+        o = OA.KvOracle(1, nh, nkv, hd)
+        vals = []
+        for pos, (q, k, v) in enumerate(steps):
+            vals.append(v.astype(np.float32))
+            out = o.attend_one(0, 0, q, k, v)
+            if (bad == "nan" and pos >= 2) or (bad == "inf" and pos == 1):
+                mean0 = np.mean([x[:hd] for x in vals], axis=0)
+                for h in range(nh // nkv):  # the query heads of kv head 0
+                    assert np.allclose(out[h * hd:(h + 1) * hd], mean0, atol=1e-6), (bad, pos, h)
+                assert np.isfinite(out).all()
+        if bad == "inf":  # without the fallback position 0 would take all the weight
+            assert not np.allclose(out[:hd], vals[0][:hd], atol=1e-3)
+

@@ -148,3 +148,19 @@ def test_async_matches_sync(dev):
             hip.hipStreamDestroy(st)
             for b in bufs:
                 hip.hipFree(b)
+
+
+@pytest.mark.parametrize("bad", ["nan", "inf"])
+def test_nan_or_infinite_score_gives_uniform_weights(dev, bad):
+    # simd::softmax falls back to uniform weights on a NaN or +inf score (simd/mod.rs:132-158)
+    from tests.test_attention_oracle import nan_inf_case
+    (nh, nkv, hd), steps = nan_inf_case(bad)
+    with KvCache(dev, 1, nh, nkv, hd, block_size=4, max_positions=64, max_seqs=1) as kv:
+        o = KvOracle(1, nh, nkv, hd, max_positions=64)
+        s = kv.open_seq()
+        for pos, (q, k, v) in enumerate(steps):
+            say(f"{bad} score, position {pos}")
+            got = kv.attention(0, [s], q[None], k[None], v[None])
+            want = o.attention(0, [s], q[None], k[None], v[None])
+            assert np.isfinite(got).all()
+            check(got, want, f"{bad} position {pos}")

@@ -130,8 +130,9 @@ def test_refusals_leave_the_sequences_unchanged(dev, weights):
     try:
         a, b = kv.open_seq(), kv.open_seq()
         model.decode_step([a, b], [1, 2])
-        with pytest.raises(G.InvalidTokenError):
+        with pytest.raises(G.InvalidTokenError) as bad:
             model.decode_step([a, b], [1, VOCAB])
+        assert bad.value.token == VOCAB  # the Token GarudaError::InvalidToken carries
         with pytest.raises(G.InferenceError):
             model.decode_step([a, a], [1, 2])
         with pytest.raises(G.InferenceError):

@@ -5,6 +5,7 @@ weights and exp bit-exact; layer outputs within rtol 1e-3 / atol 1e-4 in fp32 of
 reference path with the same arithmetic (PACKED <-> Weight::Packed / mmap = true,
 F32 <-> Weight::Full / mmap = false).
 """
+import os
 import sys
 
 import numpy as np
@@ -191,7 +192,7 @@ def check_layer(dev, d, f, ne, k, qts, ns, math, gating=0, combine=0, seed=0, lo
                 pick = np.linspace(0, n - 1, sample).astype(np.int64)
                 hs, out, ids, w = hs[pick], out[pick], ids[pick], w[pick]
                 logits = None if logits is None else logits[pick]
-            wout, wids, ww = O.feed_forward_batch(L, hs, logits, threads=8)
+            wout, wids, ww = O.feed_forward_batch(L, hs, logits, threads=min(16, len(os.sched_getaffinity(0))))
             assert np.array_equal(ids, wids), "routing differs"
             assert np.array_equal(bits(w), bits(ww)), "routing weights differ"
             err = np.abs(out - wout)

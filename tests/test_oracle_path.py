@@ -137,6 +137,64 @@ def test_router_mixtral_tie_breaks_on_lower_id():
     assert ids.tolist() == [1, 2] and np.allclose(w, [0.5, 0.5])
 
 
+def softmax64(v):
+    v = np.asarray(v, np.float64)
+    e = np.exp(v - v.max())
+    return e / e.sum()
+
+
+def test_deepseek_weights_are_the_full_softmax_without_renormalisation():
+    """router/mod.rs:74-76, :99-101: DeepSeek softmaxes over every expert, keeps the top
+    k by probability (partial_cmp descending, ties to the lower id, :83-88) and leaves
+    the kept probabilities as they are. Pinned three ways: each weight is the full
+    softmax's entry bit for bit, within float32 rounding of a float64 softmax, and the
+    weights fall short of 1 by the probability left out."""
+    rng = np.random.default_rng(17)
+    for trial in range(400):
+        ne = int(rng.choice([4, 8, 16, 64, 128]))
+        k = int(rng.integers(1, min(ne, 8) + 1))
+        v = rng.normal(0, 1.5, ne).astype(np.float32)
+        if trial % 4 == 0:
+            v[rng.integers(0, ne, ne // 3)] = v[1]  # exact ties go to the lower id
+        ids, w = O.gate(2, v, k)
+        p = O.softmax(v)
+        order = sorted(range(ne), key=lambda i: (-float(p[i]), i))
+        assert ids.tolist() == order[:k]
+        assert np.array_equal(w.view(np.uint32), p[ids].view(np.uint32))
+        p64 = softmax64(v)[ids]
+        assert (np.abs(w.astype(np.float64) - p64) <= 1e-7 + 1e-6 * p64).all()
+        left = float(np.sort(p)[::-1][k]) if k < ne else 0.0
+        s = float(np.float32(sum(np.float32(x) for x in w)))
+        if left > 1e-6:
+            assert s <= 1.0 - left / 2, (trial, s, left)
+        else:
+            assert s <= 1.0 + 1e-6
+
+
+def test_deepseek_closed_form_and_qwen_is_its_renormalisation():
+    """Logits (2, 1, 0, -1), k = 2: the weights are e^2/Z and e^1/Z with Z = e^2 + e + 1 +
+    1/e (0.6439, 0.2369); QwenMoe keeps the same experts and divides by their sum
+    (router/mod.rs:102-115)."""
+    v = np.array([2.0, 1.0, 0.0, -1.0], np.float32)
+    ids, w = O.gate(2, v, 2)
+    z = np.exp(2.0) + np.exp(1.0) + 1.0 + np.exp(-1.0)
+    assert ids.tolist() == [0, 1]
+    assert np.allclose(w, [np.exp(2.0) / z, np.exp(1.0) / z], rtol=1e-6, atol=0)
+    assert 0.88 < float(w.sum()) < 0.881
+    rng = np.random.default_rng(23)
+    for _ in range(200):
+        ne = int(rng.choice([8, 16, 128]))
+        k = int(rng.integers(1, min(ne, 8) + 1))
+        v = rng.normal(0, 2, ne).astype(np.float32)
+        ids_d, w_d = O.gate(2, v, k)
+        ids_q, w_q = O.gate(3, v, k)
+        assert (ids_d == ids_q).all()
+        s = np.float32(-0.0)
+        for x in w_d:
+            s = np.float32(s + x)
+        assert np.array_equal(w_q.view(np.uint32), (w_d / s).astype(np.float32).view(np.uint32))
+
+
 # ---- the feed-forward layer on the reference's in-memory MoE fixture ----
 
 def gen(seed, n):
