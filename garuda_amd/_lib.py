@@ -67,6 +67,7 @@ SIGNATURES = {
     "gmoe_ffn_forward": (i32, [vp, u32, f32p, u32, f32p, u32p, f32p]),
     "gmoe_ffn_forward_logits": (i32, [vp, u32, f32p, f32p, u32, f32p, u32p, f32p]),
     "gmoe_ffn_forward_async": (i32, [vp, u32, vp, vp, u32, vp, vp, vp, vp]),
+    "gmoe_ffn_forward_noalloc": (i32, [vp, u32, vp, vp, u32, vp, vp, vp, vp]),
     "gmoe_expert_prefetch": (i32, [vp, u32, u32]),
     "gmoe_expert_is_resident": (i32, [vp, u32, u32]),
     "gmoe_expert_evict": (i32, [vp, u32, u32]),

@@ -196,6 +196,9 @@ struct gmoe_ctx {
   uint8_t* scratch = nullptr;
   size_t scratch_bytes = 0;
   hipEvent_t scratch_ev = nullptr;
+  // the device address of the allocation-free forward's static scratch (gmoe_noalloc.hip),
+  // shared by every context on this device
+  uint8_t* noalloc = nullptr;
   // timing
   bool timing = false;
   std::vector<Timing> pending;
@@ -356,9 +359,17 @@ uint32_t slot_capacity(const Layer& L, uint32_t n) {
   return spec <= kSpecMaxSlots ? (uint32_t)std::max<uint64_t>(spec, (uint64_t)n * L.k) : n * L.k;
 }
 
+LayerDev layer_dev(const Layer& L);
+bool uses_int8(uint32_t math, uint32_t qt);
+
+// The scratch of one launch sequence of n tokens: plan (base null) or carve. Buffers a
+// call of this size does not use take no room: h is int8 (packed math into an int8
+// down product) or f32, and only MFMA-prefill calls have token tiles and fp16 planes.
 size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
   ScratchPlan P;
   const uint64_t nk = (uint64_t)n * L.k, ns = slot_capacity(L, n);
+  const bool h8 = uses_int8(L.math, L.p[2].qtype), pf = prefill_ok(layer_dev(L), n);
+  const uint64_t nk_pf = pf ? nk : 0, ns8 = h8 ? ns : 0, ns32 = h8 ? 0 : ns;
   size_t o_hs = P.add((size_t)n * L.d * 4), o_out = P.add((size_t)n * L.d * 4);
   size_t o_lin = P.add((size_t)n * L.ne * 4);
   size_t o_ids = P.add(nk * 4), o_w = P.add(nk * 4), o_lg = P.add((size_t)n * L.ne * 4);
@@ -366,13 +377,13 @@ size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
   size_t o_x16 = P.add((size_t)n * (L.d / 16) * 4);
   size_t o_off = P.add((L.ne + 1) * 4), o_act = P.add((L.ne + 1) * 4);
   size_t o_st = P.add(ns * 4), o_sw = P.add(ns * 4), o_sr = P.add(ns * 4), o_so = P.add(nk * 4);
-  size_t o_hq = P.add(ns * L.f), o_hsc = P.add(ns * (L.f / 32) * 4), o_h16 = P.add(ns * (L.f / 16) * 4);
-  size_t o_hf = P.add(ns * L.f * 4), o_y = P.add(kMaxKsg * ns * L.d * 4);
+  size_t o_hq = P.add(ns8 * L.f), o_hsc = P.add(ns8 * (L.f / 32) * 4), o_h16 = P.add(ns8 * (L.f / 16) * 4);
+  size_t o_hf = P.add(ns32 * L.f * 4), o_y = P.add(kMaxKsg * ns * L.d * 4);
   size_t o_cand = P.add((size_t)n * L.ne * 4);
   size_t o_work = P.add((size_t)L.ne * sizeof(ExpertWork));
-  const uint32_t pcap = prefill_tiles_cap(n, L.k, L.ne);
-  size_t o_pt = P.add((size_t)pcap * 4), o_xh = P.add(2 * nk * L.d * 2), o_hh = P.add(2 * nk * L.f * 2);
-  size_t o_xsh = P.add(2 * nk * (L.d / 16) * 2), o_hsh = P.add(2 * nk * (L.f / 16) * 2);
+  const uint32_t pcap = pf ? prefill_tiles_cap(n, L.k, L.ne) : 0;
+  size_t o_pt = P.add((size_t)pcap * 4), o_xh = P.add(2 * nk_pf * L.d * 2), o_hh = P.add(2 * nk_pf * L.f * 2);
+  size_t o_xsh = P.add(2 * nk_pf * (L.d / 16) * 2), o_hsh = P.add(2 * nk_pf * (L.f / 16) * 2);
   if (cv && base) {
     FwdBufs& B = cv->B;
     memset(&B, 0, sizeof B);
@@ -447,7 +458,8 @@ Timing take_timing(gmoe_ctx* c) {
 }
 
 // The launch sequence of one call. B's activation/output pointers are set by the caller.
-gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStream_t st) {
+// timed = false never records kernel-timing events (creating one may allocate).
+gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStream_t st, bool timed = true) {
   LayerDev D = layer_dev(L);
   B.done = c->done;
   // int8 h only when the down product reads it; f32 h otherwise
@@ -503,14 +515,15 @@ gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStr
   if (pf) HIP_TRY(launch_gather_f16(D, B, n, st));
   const uint32_t ksg = pf ? prefill_ksg(D, B) : down_ksg(D, n * L.k);
   Timing tm{};
-  if (c->timing) {
+  timed = timed && c->timing;
+  if (timed) {
     tm = take_timing(c);
     HIP_TRY(hipEventRecord(tm.a, st));
   }
   HIP_TRY(pf ? launch_prefill_gateup(D, B, n, st) : launch_gateup(D, B, n, ra, st));
-  if (c->timing) HIP_TRY(hipEventRecord(tm.b, st));
+  if (timed) HIP_TRY(hipEventRecord(tm.b, st));
   HIP_TRY(pf ? launch_prefill_down(D, B, n, ksg, st) : launch_down(D, B, n, st));
-  if (c->timing) {
+  if (timed) {
     HIP_TRY(hipEventRecord(tm.c, st));
     c->pending.push_back(tm);
   }
@@ -524,6 +537,16 @@ gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStr
 // dimension of at most 65535, so a longer batch runs as consecutive sequences. Each
 // token's output depends on its own row only, so the split changes no result's meaning.
 uint32_t call_tokens(const Layer& L) { return std::min<uint32_t>(4096u, 65535u / L.k); }
+
+// The most scratch any launch sequence of an n-token call needs: the sequences are
+// call_tokens long but the last, and the need is not monotonic in the length (the
+// speculative front end's candidate slots stop at kSpecMaxSlots; MFMA prefill adds planes).
+size_t call_scratch(const Layer& L, uint32_t n) {
+  const uint32_t per = call_tokens(L), last = n % per;
+  size_t need = plan_scratch(L, std::min(n, per), nullptr, nullptr);
+  if (n > per && last) need = std::max(need, plan_scratch(L, last, nullptr, nullptr));
+  return need;
+}
 
 gmoe_status check_ctx(gmoe_ctx* c) {
   if (!c) return fail(GMOE_ERR_INFERENCE, "null context");
@@ -847,6 +870,14 @@ gmoe_status gmoe_init(int device, uint64_t slab_bytes, gmoe_ctx** out) {
   HIP_TRY(hipSetDevice(device));
   std::unique_ptr<gmoe_ctx> c(new gmoe_ctx);
   c->device = device;
+  {
+    void* p = nullptr;
+    const hipError_t e = noalloc_scratch(device, &p);
+    if (e != hipSuccess)
+      return fail(GMOE_ERR_DEVICE, "looking up the allocation-free scratch on device %d: %s", device,
+                  hipGetErrorString(e));
+    c->noalloc = static_cast<uint8_t*>(p);
+  }
   HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
   HIP_TRY(hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking));
   if (slab_bytes) {
@@ -1026,7 +1057,7 @@ gmoe_status gmoe_ffn_forward_async(gmoe_ctx* c, uint32_t lid, const float* d_hs,
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t st = stream ? (hipStream_t)stream : c->stream;
   const uint32_t per = call_tokens(*L);
-  if (gmoe_status s = ensure_scratch(c, plan_scratch(*L, std::min(n, per), nullptr, nullptr))) return s;
+  if (gmoe_status s = ensure_scratch(c, call_scratch(*L, n))) return s;
   for (uint32_t t0 = 0; t0 < n; t0 += per) {
     const uint32_t m = std::min(per, n - t0);
     Carved cv;
@@ -1038,6 +1069,41 @@ gmoe_status gmoe_ffn_forward_async(gmoe_ctx* c, uint32_t lid, const float* d_hs,
     if (d_ids) B.ids = d_ids + (size_t)t0 * L->k;
     if (d_w) B.w = d_w + (size_t)t0 * L->k;
     if (gmoe_status s = run_layer(c, *L, B, m, st)) return s;
+  }
+  return GMOE_OK;
+}
+
+gmoe_status gmoe_ffn_forward_noalloc(gmoe_ctx* c, uint32_t lid, const float* d_hs, const float* d_logits,
+                                     uint32_t n, float* d_out, uint32_t* d_ids, float* d_w, void* stream) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (!d_hs || !d_out) return fail(GMOE_ERR_INFERENCE, "null activation pointer");
+  if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
+  std::lock_guard<std::mutex> g(c->mu);
+  Layer* L;
+  if (gmoe_status s = get_layer(c, lid, &L)) return s;
+  for (uint32_t e = 0; e < L->ne; e++)
+    if (L->slot[e] < 0) return fail(GMOE_ERR_CACHE, "expert %u of layer %u is not resident", e, lid);
+  if (!c->noalloc) return fail(GMOE_ERR_DEVICE, "the allocation-free scratch is not set up on device %d", c->device);
+  const size_t need = call_scratch(*L, n);
+  if (need > kNoAllocScratchBytes)
+    return fail(GMOE_ERR_INFERENCE,
+                "a call of %u tokens on this layer needs %zu bytes of scratch; the allocation-free forward has %zu "
+                "(use gmoe_ffn_forward_async)",
+                n, need, kNoAllocScratchBytes);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+  const uint32_t per = call_tokens(*L);
+  for (uint32_t t0 = 0; t0 < n; t0 += per) {
+    const uint32_t m = std::min(per, n - t0);
+    Carved cv;
+    plan_scratch(*L, m, &cv, c->noalloc);
+    FwdBufs B = cv.B;
+    B.hs = d_hs + (size_t)t0 * L->d;
+    B.logits_in = d_logits ? d_logits + (size_t)t0 * L->ne : nullptr;
+    B.out = d_out + (size_t)t0 * L->d;
+    if (d_ids) B.ids = d_ids + (size_t)t0 * L->k;
+    if (d_w) B.w = d_w + (size_t)t0 * L->k;
+    if (gmoe_status s = run_layer(c, *L, B, m, st, false)) return s;
   }
   return GMOE_OK;
 }

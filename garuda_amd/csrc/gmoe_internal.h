@@ -185,6 +185,12 @@ struct LayerDev {
   const uint8_t* const* eptr;   // device [3][ne]: gate, up, down tiled matrix of each expert (null = absent)
 };
 
+// Scratch of the allocation-free forward: a static device array of this many bytes per
+// GPU (gmoe_noalloc.hip); a call whose launch sequence needs more is refused.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+// Its address on `device` (the current device), looked up once per device.
+hipError_t noalloc_scratch(int device, void** out);
+
 // The down product splits K over this many partial slices at most; FwdBufs::y holds
 // kMaxKsg slices of [n*k][d]. A down workgroup has kDnKS waves, each its own K range.
 constexpr uint32_t kMaxKsg = 8;

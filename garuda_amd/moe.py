@@ -329,6 +329,13 @@ class MoeLayer:
         _check(lib().gmoe_ffn_forward_async(self.dev.handle, self.id, d_hs or None, d_logits or None, n,
                                             d_out or None, d_ids or None, d_w or None, stream or None))
 
+    def forward_noalloc(self, d_hs: int, n: int, d_out: int, d_ids: int = 0, d_w: int = 0,
+                        d_logits: int = 0, stream: int = 0) -> None:
+        """gmoe_ffn_forward_noalloc: as forward_async, with the library's static device
+        scratch instead of its arena (no allocation during the call)."""
+        _check(lib().gmoe_ffn_forward_noalloc(self.dev.handle, self.id, d_hs or None, d_logits or None, n,
+                                              d_out or None, d_ids or None, d_w or None, stream or None))
+
     def prefetch(self, e: int) -> None:
         _check(lib().gmoe_expert_prefetch(self.dev.handle, self.id, e))
 

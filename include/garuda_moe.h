@@ -136,6 +136,21 @@ gmoe_status gmoe_ffn_forward_async(gmoe_ctx* ctx, uint32_t layer_id, const float
                                    const float* d_logits, uint32_t n, float* d_out,
                                    uint32_t* d_routed_ids, float* d_routed_w, void* stream);
 
+/* gmoe_ffn_forward_async without any allocation. It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory during a call (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Its
+ * scratch is a static device array of 64 MiB per GPU, set up when the library's first
+ * context on that GPU opens and held until the process ends; no call allocates or frees.
+ * A call whose scratch would exceed it is refused with GMOE_ERR_INFERENCE before any
+ * device work (a Mixtral-shape layer, d 4096 / f 14336 / 8 experts, fits every batch of
+ * up to 53 tokens; the 128-expert C4 layer fits 64). Every call on one GPU, from every
+ * context, shares that array and leaves its contents behind: calls that overlap on one
+ * GPU race, so order them on one stream. Same arguments and results as
+ * gmoe_ffn_forward_async. */
+gmoe_status gmoe_ffn_forward_noalloc(gmoe_ctx* ctx, uint32_t layer_id, const float* d_hs,
+                                     const float* d_logits, uint32_t n, float* d_out,
+                                     uint32_t* d_routed_ids, float* d_routed_w, void* stream);
+
 /* ---- the L1 tier (core::ExpertLoader, core/mod.rs:215-223) ---- */
 gmoe_status gmoe_expert_prefetch(gmoe_ctx* ctx, uint32_t layer_id, uint32_t expert);
 int gmoe_expert_is_resident(gmoe_ctx* ctx, uint32_t layer_id, uint32_t expert);
