@@ -142,9 +142,10 @@ struct Layer {
   std::vector<int64_t> slot;      // per expert: slab offset or -1
   std::vector<LruList::iterator> lru_pos;  // per resident expert: its place in the LRU
   uint64_t expert_bytes = 0;
-  // recorded on the call's stream after every forward of the layer: an evicted expert's
-  // region is free once the layer's last queued call has finished
-  hipEvent_t last_use = nullptr;
+  // the stream of the layer's last queued call (null: none): an evicted expert's region is
+  // free once that stream has drained. An event recorded per call would say exactly when,
+  // but each record puts a marker on the GPU timeline (about 4 us a call).
+  hipStream_t last_stream = nullptr;
   bool alive = true;
 };
 
@@ -191,11 +192,11 @@ struct gmoe_ctx {
   uint8_t* bounce = nullptr;  // device landing area of the pinned halves (same size)
   uint32_t* done = nullptr;   // front-end completion counter (device, zero between calls)
   hipEvent_t pin_ev[2]{};
-  // scratch arena; scratch_ev is recorded after every call that uses it (calls on one
-  // context are ordered on one stream), so growing the arena waits for that call only
+  // scratch arena (calls on one context are ordered on one stream, so growing it waits for
+  // the stream of the last call that used it)
   uint8_t* scratch = nullptr;
   size_t scratch_bytes = 0;
-  hipEvent_t scratch_ev = nullptr;
+  hipStream_t scratch_stream = nullptr;  // the stream of the last call that used the arena
   // the device address of the allocation-free forward's static scratch (gmoe_noalloc.hip),
   // shared by every context on this device
   uint8_t* noalloc = nullptr;
@@ -269,12 +270,21 @@ void touch(gmoe_ctx* c, uint32_t l, uint32_t e) {
   c->lru.splice(c->lru.end(), c->lru, L.lru_pos[e]);
 }
 
+// Wait until queued work on `st` has finished: the context's own streams directly; a
+// caller's stream (which the caller may have destroyed since) through the whole device.
+gmoe_status drain(gmoe_ctx* c, hipStream_t st) {
+  if (!st) return GMOE_OK;
+  if (st == c->stream || st == c->copy_stream) HIP_TRY(hipStreamSynchronize(st));
+  else HIP_TRY(hipDeviceSynchronize());
+  return GMOE_OK;
+}
+
 gmoe_status evict(gmoe_ctx* c, uint32_t l, uint32_t e) {
   Layer& L = *c->layers[l];
   if (L.slot[e] < 0) return GMOE_OK;
-  // the slab region may still be read by the layer's queued calls, on the context's stream
-  // or on a caller's (gmoe_ffn_forward_async): wait for the last one
-  HIP_TRY(hipEventSynchronize(L.last_use));
+  // the slab region may still be read by the layer's queued calls
+  if (gmoe_status s = drain(c, L.last_stream)) return s;
+  L.last_stream = nullptr;
   c->slab.release((uint64_t)L.slot[e], L.expert_bytes);
   L.slot[e] = -1;
   for (int p = 0; p < 3; p++) L.eptr_host[p * L.ne + e] = nullptr;
@@ -374,7 +384,7 @@ size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
   size_t o_lin = P.add((size_t)n * L.ne * 4);
   size_t o_ids = P.add(nk * 4), o_w = P.add(nk * 4), o_lg = P.add((size_t)n * L.ne * 4);
   size_t o_xq = P.add((size_t)n * L.d), o_xs = P.add((size_t)n * (L.d / 32) * 4);
-  size_t o_x16 = P.add((size_t)n * (L.d / 16) * 4);
+  size_t o_x16 = P.add((size_t)n * (L.d / 16) * 4);  // sums: at most one word per 16 values
   size_t o_off = P.add((L.ne + 1) * 4), o_act = P.add((L.ne + 1) * 4);
   size_t o_st = P.add(ns * 4), o_sw = P.add(ns * 4), o_sr = P.add(ns * 4), o_so = P.add(nk * 4);
   size_t o_hq = P.add(ns8 * L.f), o_hsc = P.add(ns8 * (L.f / 32) * 4), o_h16 = P.add(ns8 * (L.f / 16) * 4);
@@ -395,7 +405,7 @@ size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
     B.logits = (float*)(base + o_lg);
     B.xq = (int8_t*)(base + o_xq);
     B.xs = (float*)(base + o_xs);
-    B.x16 = (int32_t*)(base + o_x16);
+    B.xsum = (uint32_t*)(base + o_x16);
     B.offsets = (uint32_t*)(base + o_off);
     B.active = (uint32_t*)(base + o_act);
     B.slot_tok = (uint32_t*)(base + o_st);
@@ -404,7 +414,7 @@ size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
     B.slot_of = (uint32_t*)(base + o_so);
     B.hq = (int8_t*)(base + o_hq);
     B.hsc = (float*)(base + o_hsc);
-    B.h16 = (int32_t*)(base + o_h16);
+    B.hsum = (uint32_t*)(base + o_h16);
     B.hf = (float*)(base + o_hf);
     B.y = (float*)(base + o_y);
     B.work = (ExpertWork*)(base + o_work);
@@ -422,7 +432,8 @@ size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
 
 gmoe_status ensure_scratch(gmoe_ctx* c, size_t bytes) {
   if (bytes <= c->scratch_bytes) return GMOE_OK;
-  HIP_TRY(hipEventSynchronize(c->scratch_ev));  // the last call that used the old arena
+  if (gmoe_status s = drain(c, c->scratch_stream)) return s;  // the last call that used the old arena
+  c->scratch_stream = nullptr;
   if (c->scratch) HIP_TRY(hipFree(c->scratch));
   c->scratch = nullptr;
   c->scratch_bytes = 0;
@@ -459,14 +470,14 @@ Timing take_timing(gmoe_ctx* c) {
 
 // The launch sequence of one call. B's activation/output pointers are set by the caller.
 // timed = false never records kernel-timing events (creating one may allocate).
-gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStream_t st, bool timed = true) {
+gmoe_status run_layer(gmoe_ctx* c, Layer& L, FwdBufs B, uint32_t n, hipStream_t st, bool timed = true) {
   LayerDev D = layer_dev(L);
   B.done = c->done;
   // int8 h only when the down product reads it; f32 h otherwise
   if (!uses_int8(L.math, L.p[2].qtype)) {
     B.hq = nullptr;
     B.hsc = nullptr;
-    B.h16 = nullptr;
+    B.hsum = nullptr;
   } else {
     B.hf = nullptr;
   }
@@ -510,7 +521,7 @@ gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStr
   } else {
     HIP_TRY(launch_route(D, B, n, st));
     HIP_TRY(launch_dispatch(D, B, n, st));
-    if (quant) HIP_TRY(launch_quant_act(B.hs, n, L.d, B.xq, B.xs, B.x16, st));
+    if (quant) HIP_TRY(launch_quant_act(B.hs, n, L.d, B.xq, B.xs, B.xsum, L.p[0].qtype, st));
   }
   if (pf) HIP_TRY(launch_gather_f16(D, B, n, st));
   const uint32_t ksg = pf ? prefill_ksg(D, B) : down_ksg(D, n * L.k);
@@ -528,8 +539,7 @@ gmoe_status run_layer(gmoe_ctx* c, const Layer& L, FwdBufs B, uint32_t n, hipStr
     c->pending.push_back(tm);
   }
   HIP_TRY(launch_combine(D, B, n, ksg, st));
-  HIP_TRY(hipEventRecord(L.last_use, st));
-  HIP_TRY(hipEventRecord(c->scratch_ev, st));
+  L.last_stream = st;
   return GMOE_OK;
 }
 
@@ -614,7 +624,7 @@ size_t plan_dense(const gmoe_ctx* c, const Dense& W, uint32_t n, uint8_t* base, 
     if (int8 && !fuse) {
       B.hq = (int8_t*)(base + o_q);
       B.hsc = (float*)(base + o_s);
-      B.h16 = (int32_t*)(base + o_16);
+      B.hsum = (uint32_t*)(base + o_16);
     }
     if (pf) {
       B.xh = B.hh = (_Float16*)(base + o_xh);
@@ -647,11 +657,11 @@ gmoe_status run_dense(const Dense& W, const DenseCarve& cv, const float* x, uint
     HIP_TRY(launch_prefill_down(D, B, n, cv.ksg, st));
   } else {
     if (cv.int8 && B.hq) {
-      HIP_TRY(launch_quant_act(x, n, W.cols, B.hq, B.hsc, B.h16, st));
+      HIP_TRY(launch_quant_act(x, n, W.cols, B.hq, B.hsc, B.hsum, W.qtype, st));
     } else {  // f32 math, or packed math quantised in the down kernel's staging (hq null)
       B.hq = nullptr;
       B.hsc = nullptr;
-      B.h16 = nullptr;
+      B.hsum = nullptr;
       B.hf = const_cast<float*>(x);
     }
     HIP_TRY(launch_down(D, B, n, st, cv.ksg));
@@ -661,7 +671,7 @@ gmoe_status run_dense(const Dense& W, const DenseCarve& cv, const float* x, uint
 }
 
 gmoe_status mark_scratch(gmoe_ctx* c, hipStream_t st) {
-  HIP_TRY(hipEventRecord(c->scratch_ev, st));
+  c->scratch_stream = st;
   return GMOE_OK;
 }
 
@@ -724,6 +734,7 @@ gmoe_status forward_chunk(gmoe_ctx* c, uint32_t lid, Layer* L, const float* hs, 
     }
   }
   if (gmoe_status s = run_layer(c, *L, B, n, st)) return s;
+  c->scratch_stream = st;
   HIP_TRY(hipMemcpyAsync(out, B.out, (size_t)n * L->d * 4, hipMemcpyDeviceToHost, st));
   if (all) HIP_TRY(hipMemcpyAsync(hid.data(), B.ids, hid.size() * 4, hipMemcpyDeviceToHost, st));
   if (ids) HIP_TRY(hipMemcpyAsync(ids, B.ids, (size_t)n * L->k * 4, hipMemcpyDeviceToHost, st));
@@ -896,8 +907,6 @@ gmoe_status gmoe_init(int device, uint64_t slab_bytes, gmoe_ctx** out) {
   // [0]: front-end workgroups done; [64 .. 64 + kSpecMaxSlots): per-token routing counters
   HIP_TRY(hipMalloc(&c->done, (64 + kSpecMaxSlots) * 4));
   HIP_TRY(hipMemset(c->done, 0, (64 + kSpecMaxSlots) * 4));
-  HIP_TRY(hipEventCreateWithFlags(&c->scratch_ev, hipEventDisableTiming));
-  HIP_TRY(hipEventRecord(c->scratch_ev, c->stream));
   HIP_TRY(hipEventCreateWithFlags(&c->pin_ev[0], hipEventDisableTiming));
   HIP_TRY(hipEventCreateWithFlags(&c->pin_ev[1], hipEventDisableTiming));
   HIP_TRY(hipEventRecord(c->pin_ev[0], c->copy_stream));
@@ -915,7 +924,6 @@ void gmoe_shutdown(gmoe_ctx* c) {
     if (L) {
       hipFree(L->router);
       hipFree((void*)L->eptr);
-      if (L->last_use) hipEventDestroy(L->last_use);
     }
   for (auto& t : c->pending) c->pool.push_back(t);
   for (auto& t : c->pool) {
@@ -936,7 +944,6 @@ void gmoe_shutdown(gmoe_ctx* c) {
   if (c->done) hipFree(c->done);
   hipEventDestroy(c->pin_ev[0]);
   hipEventDestroy(c->pin_ev[1]);
-  if (c->scratch_ev) hipEventDestroy(c->scratch_ev);
   hipStreamDestroy(c->stream);
   hipStreamDestroy(c->copy_stream);
   delete c;
@@ -1003,8 +1010,6 @@ gmoe_status gmoe_layer_register(gmoe_ctx* c, const gmoe_layer_desc* desc, uint32
   HIP_TRY(hipMemcpy(L->eptr, L->eptr_host.data(), 3 * L->ne * sizeof(void*), hipMemcpyHostToDevice));
   L->slot.assign(L->ne, -1);
   L->lru_pos.resize(L->ne);
-  HIP_TRY(hipEventCreateWithFlags(&L->last_use, hipEventDisableTiming));
-  HIP_TRY(hipEventRecord(L->last_use, c->stream));
   uint32_t id = (uint32_t)c->layers.size();
   c->layers.push_back(std::move(L));
   Layer& LL = *c->layers.back();
@@ -1069,6 +1074,7 @@ gmoe_status gmoe_ffn_forward_async(gmoe_ctx* c, uint32_t lid, const float* d_hs,
     if (d_ids) B.ids = d_ids + (size_t)t0 * L->k;
     if (d_w) B.w = d_w + (size_t)t0 * L->k;
     if (gmoe_status s = run_layer(c, *L, B, m, st)) return s;
+    c->scratch_stream = st;
   }
   return GMOE_OK;
 }
@@ -1356,7 +1362,7 @@ gmoe_status gmoe_matmul(gmoe_ctx* c, uint32_t qt, uint32_t math, const void* w, 
   unit_of(qt, &un);
   size_t wbytes = tiled_bytes(un, rows, cols);
   size_t nb_x = (size_t)n * cols;
-  // device layout: [w tiled][w raw][x f32][xq][xs][x16][y][out][offsets(2)][active(2)][eptr(3)][work(1)]
+  // device layout: [w tiled][w raw][x f32][xq][xs][x sums][y][out][offsets(2)][active(2)][eptr(3)][work(1)]
   ScratchPlan P;
   size_t o_w = P.add(wbytes), o_raw = P.add(nbytes), o_x = P.add(nb_x * 4), o_q = P.add(nb_x), o_s = P.add(nb_x / 32 * 4),
          o_16 = P.add(nb_x / 16 * 4), o_y = P.add(kMaxKsg * (size_t)n * rows * 4), o_o = P.add((size_t)n * rows * 4), o_off = P.add(8), o_act = P.add(8),
@@ -1386,8 +1392,8 @@ gmoe_status gmoe_matmul(gmoe_ctx* c, uint32_t qt, uint32_t math, const void* w, 
   if (uses_int8(math, qt)) {
     B.hq = (int8_t*)(base + o_q);
     B.hsc = (float*)(base + o_s);
-    B.h16 = (int32_t*)(base + o_16);
-    if (e == hipSuccess) e = launch_quant_act((const float*)(base + o_x), n, cols, B.hq, B.hsc, B.h16, c->stream);
+    B.hsum = (uint32_t*)(base + o_16);
+    if (e == hipSuccess) e = launch_quant_act((const float*)(base + o_x), n, cols, B.hq, B.hsc, B.hsum, qt, c->stream);
   } else {
     B.hf = (float*)(base + o_x);
   }

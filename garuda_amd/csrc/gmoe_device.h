@@ -293,7 +293,10 @@ __device__ __forceinline__ void quant32_regs(const float* v, uint32_t* packed, f
   *sum1_out = sum1;
 }
 
-__device__ __forceinline__ void quant32(const float* v, int8_t* q, float* s, int32_t* s16) {
+// Block gb of an activation array (q and s point at the block's values and scale): its
+// sums go to words of `sums` in the form `kind` / `off` (sum_kind_of, sum_offset_of).
+__device__ __forceinline__ void quant32(const float* v, int8_t* q, float* s, uint32_t* sums, size_t gb, int kind,
+                                        int32_t off) {
   uint32_t packed[8];
   float scale;
   int sum0, sum1;
@@ -302,18 +305,28 @@ __device__ __forceinline__ void quant32(const float* v, int8_t* q, float* s, int
   uint4* q4 = reinterpret_cast<uint4*>(q);
   q4[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
   q4[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
-  s16[0] = sum0;
-  s16[1] = sum1;
+  if (kind == kSumF32x32) {
+    sums[gb] = __float_as_uint((float)(sum0 + sum1));
+  } else if (kind == kSumF32x16) {
+    sums[2 * gb] = __float_as_uint((float)sum0);
+    sums[2 * gb + 1] = __float_as_uint((float)sum1);
+  } else if (kind == kSumI32x16) {
+    sums[2 * gb] = (uint32_t)(off * sum0);
+    sums[2 * gb + 1] = (uint32_t)(off * sum1);
+  }
 }
 
 // quant32 over a wave: lane l holds value l%32 of block l/32 (two consecutive 32-blocks
 // per wave). The block maximum and the sums of 16 are cross-lane reductions, which their
 // order does not change (the maximum starts from 0, so NaN never wins, as in the serial
 // fold); every lane then quantises its own value with quant32's arithmetic. Lanes
-// l%4 == 0 store four packed values, lanes 0/32 the scales, lanes 0/16/32/48 the sums.
-// `valid` (uniform over each 32-lane half) leaves blocks past the end of the row
-// unwritten; every lane of the wave must call this.
-__device__ __forceinline__ void quant_wave(float v, uint32_t lane, bool valid, int8_t* q, float* s, int32_t* s16) {
+// l%4 == 0 store four packed values, lanes 0/32 the scales, lanes 0/32 (sums of 32) or
+// 0/16/32/48 (sums of 16) the sums, in the form kind / off, at their words of the row
+// `sums` of which the wave holds values r0 .. r0 + 63. `valid` (uniform over each 32-lane
+// half) leaves blocks past the end of the row unwritten; every lane of the wave must call
+// this.
+__device__ __forceinline__ void quant_wave(float v, uint32_t lane, bool valid, int8_t* q, float* s, uint32_t* sums,
+                                           uint32_t r0, int kind, int32_t off) {
   float a = fmaxf(0.0f, fabsf(v));
 #pragma unroll
   for (int o = 16; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
@@ -324,40 +337,47 @@ __device__ __forceinline__ void quant_wave(float v, uint32_t lane, bool valid, i
   int sum = qi;
 #pragma unroll
   for (int o = 8; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  const int sum32 = sum + __shfl_xor(sum, 16, 64);
   const uint32_t b = (uint32_t)qi & 0xffu;
   const uint32_t word = b | (__shfl_down(b, 1, 64) << 8) | (__shfl_down(b, 2, 64) << 16) | (__shfl_down(b, 3, 64) << 24);
   if (valid) {
     if ((lane & 3) == 0) reinterpret_cast<uint32_t*>(q)[lane / 4] = word;
     if ((lane & 31) == 0) s[lane / 32] = scale;
-    if ((lane & 15) == 0) s16[lane / 16] = sum;
+    if (kind == kSumF32x32) {
+      if ((lane & 31) == 0) sums[(r0 + lane) / 32] = __float_as_uint((float)sum32);
+    } else if (kind != kSumNone && (lane & 15) == 0) {
+      sums[(r0 + lane) / 16] = kind == kSumF32x16 ? __float_as_uint((float)sum) : (uint32_t)(off * sum);
+    }
   }
 }
 
 // ---------------------------------------------------------------------------------
-// Packed (int8-activation) block dots. Each adds its block's sub-block terms to `acc`
-// in the reference's order, each term evaluated exactly as the reference writes it.
-// x: the block's int8 activations; xs: its per-32 scales; sm: its activation sums in
-// the form the type's dot reads them (sum_kind below).
+// Packed (int8-activation) block dots. Each adds its block's sub-block terms to the
+// running row sums of m tokens, in the reference's order, each term evaluated exactly as
+// the reference writes it. tok(t) gives token t's view of the block (PkTok): x its int8
+// activations, xs its per-32 scales, sm its activation sums in the form the type's dot
+// reads them (sum_kind_of), acc its running sum. A sub-block group's quants are unpacked
+// once, then every token takes that group's terms before the next group's are unpacked:
+// only one group's unpacked quants are live, and each token still adds its terms in K
+// order.
 // ---------------------------------------------------------------------------------
 
-// The activation sums a packed dot reads, one 32-bit word each: f32 sums of 32 values
-// (Q4_K, Q5_K: the reference converts the i32 sum, which is exact below 2^24), f32
-// sums of 16 (Q2_K), i32 sums of 16 times the type's offset (Q6_K -32, Q3_K -4: the
-// dot's integer chain starts from it, so it adds the -32 or -4 times the sum that the
-// reference subtracts; integer sums are exact in any order), or none (Q8_0).
-enum SumKind { kSumNone = 0, kSumF32x32 = 1, kSumF32x16 = 2, kSumI32x16 = 3 };
+struct PkTok {
+  const int8_t* x;
+  const float* xs;
+  const uint32_t* sm;
+  float* acc;
+};
+
+// The activation sums a packed dot reads: sum_kind_of / sum_offset_of (gmoe_internal.h).
 template <int QT>
-__host__ __device__ constexpr int sum_kind() {
-  return (QT == Q4_K || QT == Q5_K) ? kSumF32x32 : QT == Q2_K ? kSumF32x16 : (QT == Q6_K || QT == Q3_K) ? kSumI32x16 : kSumNone;
-}
+__host__ __device__ constexpr int sum_kind() { return sum_kind_of(QT); }
 template <int QT>
-__host__ __device__ constexpr int32_t sum_offset() { return QT == Q6_K ? -32 : QT == Q3_K ? -4 : 1; }
-__host__ __device__ constexpr uint32_t sum_width(int kind) { return kind == kSumF32x32 ? 32u : kind ? 16u : 0u; }
+__host__ __device__ constexpr int32_t sum_offset() { return sum_offset_of(QT); }
 
 // quant/mod.rs:586-621
-template <int TM>
-__device__ __forceinline__ void pk_q4k(const uint32_t* w, const int8_t* const* x, const float* const* xs,
-                                       const uint32_t* const* sm, float* acc, int m) {
+template <class Tok>
+__device__ __forceinline__ void pk_q4k(const uint32_t* w, uint32_t m, Tok tok) {
   float d = f16f(w[0]), dmin = f16f(w[0] >> 16);
 #pragma unroll
   for (int c = 0; c < 4; c++) {
@@ -371,28 +391,27 @@ __device__ __forceinline__ void pk_q4k(const uint32_t* w, const int8_t* const* x
       lo[i] = v & 0x0f0f0f0fu;
       hi[i] = (v >> 4) & 0x0f0f0f0fu;
     }
+    for (uint32_t t = 0; t < m; t++) {
+      const PkTok a = tok(t);
+      const uint32_t* xa = reinterpret_cast<const uint32_t*>(a.x + 64 * c);
+      int dl = 0, dh = 0;
 #pragma unroll
-    for (int t = 0; t < TM; t++) {
-      if (t < m) {
-        const uint32_t* xa = reinterpret_cast<const uint32_t*>(x[t] + 64 * c);
-        int dl = 0, dh = 0;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          dl = sdot4(lo[i], xa[i], dl);
-          dh = sdot4(hi[i], xa[8 + i], dh);
-        }
-        const float s1 = __uint_as_float(sm[t][2 * c]), s2 = __uint_as_float(sm[t][2 * c + 1]);
-        acc[t] += xs[t][2 * c] * (d * (float)sc1 * (float)dl - dmin * (float)m1 * s1);
-        acc[t] += xs[t][2 * c + 1] * (d * (float)sc2 * (float)dh - dmin * (float)m2 * s2);
+      for (int i = 0; i < 8; i++) {
+        dl = sdot4(lo[i], xa[i], dl);
+        dh = sdot4(hi[i], xa[8 + i], dh);
       }
+      const float s1 = __uint_as_float(a.sm[2 * c]), s2 = __uint_as_float(a.sm[2 * c + 1]);
+      float acc = *a.acc;
+      acc += a.xs[2 * c] * (d * (float)sc1 * (float)dl - dmin * (float)m1 * s1);
+      acc += a.xs[2 * c + 1] * (d * (float)sc2 * (float)dh - dmin * (float)m2 * s2);
+      *a.acc = acc;
     }
   }
 }
 
 // quant/mod.rs:454-495
-template <int TM>
-__device__ __forceinline__ void pk_q5k(const uint32_t* w, const int8_t* const* x, const float* const* xs,
-                                       const uint32_t* const* sm, float* acc, int m) {
+template <class Tok>
+__device__ __forceinline__ void pk_q5k(const uint32_t* w, uint32_t m, Tok tok) {
   float d = f16f(w[0]), dmin = f16f(w[0] >> 16);
   const uint32_t* qh = w + 4;
   const uint32_t* qs = w + 12;
@@ -408,28 +427,27 @@ __device__ __forceinline__ void pk_q5k(const uint32_t* w, const int8_t* const* x
       lo[i] = (v & 0x0f0f0f0fu) | (((h >> (2 * g)) & 0x01010101u) << 4);
       hi[i] = ((v >> 4) & 0x0f0f0f0fu) | (((h >> (2 * g + 1)) & 0x01010101u) << 4);
     }
+    for (uint32_t t = 0; t < m; t++) {
+      const PkTok a = tok(t);
+      const uint32_t* xa = reinterpret_cast<const uint32_t*>(a.x + 64 * g);
+      int dl = 0, dh = 0;
 #pragma unroll
-    for (int t = 0; t < TM; t++) {
-      if (t < m) {
-        const uint32_t* xa = reinterpret_cast<const uint32_t*>(x[t] + 64 * g);
-        int dl = 0, dh = 0;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          dl = sdot4(lo[i], xa[i], dl);
-          dh = sdot4(hi[i], xa[8 + i], dh);
-        }
-        const float s1 = __uint_as_float(sm[t][2 * g]), s2 = __uint_as_float(sm[t][2 * g + 1]);
-        acc[t] += xs[t][2 * g] * (d * (float)sc1 * (float)dl - dmin * (float)m1 * s1);
-        acc[t] += xs[t][2 * g + 1] * (d * (float)sc2 * (float)dh - dmin * (float)m2 * s2);
+      for (int i = 0; i < 8; i++) {
+        dl = sdot4(lo[i], xa[i], dl);
+        dh = sdot4(hi[i], xa[8 + i], dh);
       }
+      const float s1 = __uint_as_float(a.sm[2 * g]), s2 = __uint_as_float(a.sm[2 * g + 1]);
+      float acc = *a.acc;
+      acc += a.xs[2 * g] * (d * (float)sc1 * (float)dl - dmin * (float)m1 * s1);
+      acc += a.xs[2 * g + 1] * (d * (float)sc2 * (float)dh - dmin * (float)m2 * s2);
+      *a.acc = acc;
     }
   }
 }
 
 // quant/mod.rs:417-445. Sub-block s (16 wide): q-32 is dotted as q then -32*sum.
-template <int TM>
-__device__ __forceinline__ void pk_q6k(const uint32_t* w, const int8_t* const* x, const float* const* xs,
-                                       const uint32_t* const* sm, float* acc, int m) {
+template <class Tok>
+__device__ __forceinline__ void pk_q6k(const uint32_t* w, uint32_t m, Tok tok) {
   float d = f16f(w[52]);
 #pragma unroll
   for (int s = 0; s < 16; s++) {
@@ -445,24 +463,21 @@ __device__ __forceinline__ void pk_q6k(const uint32_t* w, const int8_t* const* x
       q[i] = lo4 | hi2;
     }
     float sc = (float)(int8_t)byte_of(w, 192 + s);
+    for (uint32_t t = 0; t < m; t++) {
+      const PkTok a = tok(t);
+      const uint32_t* xa = reinterpret_cast<const uint32_t*>(a.x + 16 * s);
+      int dt = (int)a.sm[s];  // -32 * the sub-block's sum
 #pragma unroll
-    for (int t = 0; t < TM; t++) {
-      if (t < m) {
-        const uint32_t* xa = reinterpret_cast<const uint32_t*>(x[t] + 16 * s);
-        int dt = (int)sm[t][s];  // -32 * the sub-block's sum
-#pragma unroll
-        for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
-        acc[t] += xs[t][s / 2] * d * sc * (float)dt;
-      }
+      for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
+      *a.acc += a.xs[s / 2] * d * sc * (float)dt;
     }
   }
 }
 
 // quant/mod.rs:503-540. q = ((qs >> shift) & 3) - (hmask bit ? 0 : 4), dotted as
 // (low2 | hbit << 2) then -4*sum.
-template <int TM>
-__device__ __forceinline__ void pk_q3k(const uint32_t* w, const int8_t* const* x, const float* const* xs,
-                                       const uint32_t* const* sm, float* acc, int m) {
+template <class Tok>
+__device__ __forceinline__ void pk_q3k(const uint32_t* w, uint32_t m, Tok tok) {
   float d_all = f16f(w[27]);
   uint32_t sc4[4];
   q3k_scales(w[24], w[25], w[26], sc4);
@@ -477,23 +492,20 @@ __device__ __forceinline__ void pk_q3k(const uint32_t* w, const int8_t* const* x
       q[i] = ((qs >> (2 * j)) & 0x03030303u) | (((hm >> (4 * half + j)) & 0x01010101u) << 2);
     }
     float dl = d_all * (float)((int)(int8_t)byte_of(sc4, s) - 32);
+    for (uint32_t t = 0; t < m; t++) {
+      const PkTok a = tok(t);
+      const uint32_t* xa = reinterpret_cast<const uint32_t*>(a.x + 16 * s);
+      int dt = (int)a.sm[s];  // -4 * the sub-block's sum
 #pragma unroll
-    for (int t = 0; t < TM; t++) {
-      if (t < m) {
-        const uint32_t* xa = reinterpret_cast<const uint32_t*>(x[t] + 16 * s);
-        int dt = (int)sm[t][s];  // -4 * the sub-block's sum
-#pragma unroll
-        for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
-        acc[t] += xs[t][s / 2] * dl * (float)dt;
-      }
+      for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
+      *a.acc += a.xs[s / 2] * dl * (float)dt;
     }
   }
 }
 
 // quant/mod.rs:548-581
-template <int TM>
-__device__ __forceinline__ void pk_q2k(const uint32_t* w, const int8_t* const* x, const float* const* xs,
-                                       const uint32_t* const* sm, float* acc, int m) {
+template <class Tok>
+__device__ __forceinline__ void pk_q2k(const uint32_t* w, uint32_t m, Tok tok) {
   float d = f16f(w[20]), dmin = f16f(w[20] >> 16);
 #pragma unroll
   for (int s = 0; s < 16; s++) {
@@ -503,27 +515,49 @@ __device__ __forceinline__ void pk_q2k(const uint32_t* w, const int8_t* const* x
     for (int i = 0; i < 4; i++) q[i] = (w[(16 + 32 * half + o) / 4 + i] >> (2 * j)) & 0x03030303u;
     uint32_t sc = byte_of(w, s);
     float dl = d * (float)(sc & 15u), ml = dmin * (float)(sc >> 4);
+    for (uint32_t t = 0; t < m; t++) {
+      const PkTok a = tok(t);
+      const uint32_t* xa = reinterpret_cast<const uint32_t*>(a.x + 16 * s);
+      int dt = 0;
 #pragma unroll
-    for (int t = 0; t < TM; t++) {
-      if (t < m) {
-        const uint32_t* xa = reinterpret_cast<const uint32_t*>(x[t] + 16 * s);
+      for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
+      *a.acc += a.xs[s / 2] * (dl * (float)dt - ml * __uint_as_float(a.sm[s]));
+    }
+  }
+}
+
+// quant/mod.rs:398-407 over a repacked Q8_0 unit of the slab (eight blocks: their f16
+// scales in dwords 0..3, then their quants): block g adds ws*xs*dot. nvalid = blocks of
+// the unit inside the row.
+template <class Tok>
+__device__ __forceinline__ void pk_q80_unit(const uint32_t* w, uint32_t nvalid, uint32_t m, Tok tok) {
+#pragma unroll
+  for (int g = 0; g < 8; g++) {
+    if ((uint32_t)g < nvalid) {
+      const float ws = f16f(w[g / 2] >> (16 * (g % 2)));
+      const uint32_t* q = w + 4 + 8 * g;
+      for (uint32_t t = 0; t < m; t++) {
+        const PkTok a = tok(t);
+        const uint32_t* xa = reinterpret_cast<const uint32_t*>(a.x + 32 * g);
         int dt = 0;
 #pragma unroll
-        for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
-        acc[t] += xs[t][s / 2] * (dl * (float)dt - ml * __uint_as_float(sm[t][s]));
+        for (int i = 0; i < 8; i++) dt = sdot4(q[i], xa[i], dt);
+        *a.acc += ws * a.xs[g] * (float)dt;
       }
     }
   }
 }
 
-template <int QT, int TM>
-__device__ __forceinline__ void pk_block(const uint32_t* w, const int8_t* const* x, const float* const* xs,
-                                         const uint32_t* const* sm, float* acc, int m) {
-  if constexpr (QT == Q4_K) pk_q4k<TM>(w, x, xs, sm, acc, m);
-  else if constexpr (QT == Q5_K) pk_q5k<TM>(w, x, xs, sm, acc, m);
-  else if constexpr (QT == Q6_K) pk_q6k<TM>(w, x, xs, sm, acc, m);
-  else if constexpr (QT == Q3_K) pk_q3k<TM>(w, x, xs, sm, acc, m);
-  else if constexpr (QT == Q2_K) pk_q2k<TM>(w, x, xs, sm, acc, m);
+// One slab unit of a packed type against m tokens (nvalid: blocks of the unit inside the
+// row, for the eight-block Q8_0 units).
+template <int QT, class Tok>
+__device__ __forceinline__ void pk_unit(const uint32_t* w, uint32_t nvalid, uint32_t m, Tok tok) {
+  if constexpr (QT == Q4_K) pk_q4k(w, m, tok);
+  else if constexpr (QT == Q5_K) pk_q5k(w, m, tok);
+  else if constexpr (QT == Q6_K) pk_q6k(w, m, tok);
+  else if constexpr (QT == Q3_K) pk_q3k(w, m, tok);
+  else if constexpr (QT == Q2_K) pk_q2k(w, m, tok);
+  else if constexpr (QT == Q8_0) pk_q80_unit(w, nvalid, m, tok);
 }
 
 // ---------------------------------------------------------------------------------
@@ -635,7 +669,7 @@ __device__ __forceinline__ void route_logit(const RouteArgs& r, uint32_t x, floa
   const float* hs = r.hs + (size_t)t * d;
   const float* wr = r.router + (size_t)e * d;
   uint32_t* scratch = reinterpret_cast<uint32_t*>(lds + 2 * sec);
-  constexpr int kItems = 16;
+  constexpr int kItems = 4;  // a 1024-value section is one pass of 64 lanes; few registers, as the launch sizes them for the expert workgroups
   auto produce = [&](uint32_t s) {
     const uint32_t k0 = s * sec, len4 = min(sec, d - k0) / 4;
     float* half = lds + (s & 1) * sec;

@@ -33,6 +33,20 @@ __host__ __device__ constexpr bool has_int8_kernel(uint32_t t) {
   return t == Q8_0 || t == Q2_K || t == Q3_K || t == Q4_K || t == Q5_K || t == Q6_K;
 }
 
+// The activation sums a packed dot of type qt reads, one 32-bit word each: f32 sums of 32
+// values (Q4_K, Q5_K: the reference converts the i32 sum, which is exact below 2^24), f32
+// sums of 16 (Q2_K), i32 sums of 16 times the type's offset (Q6_K -32, Q3_K -4: the dot's
+// integer chain starts from it, so it adds the -32 or -4 times the sum that the reference
+// subtracts; integer sums are exact in any order), or none (Q8_0). The activation
+// quantisers write them in the form of the type that reads them, so that staging them is
+// a copy; a row of K values has K / sum_width words.
+enum SumKind { kSumNone = 0, kSumF32x32 = 1, kSumF32x16 = 2, kSumI32x16 = 3 };
+__host__ __device__ constexpr int sum_kind_of(uint32_t qt) {
+  return (qt == Q4_K || qt == Q5_K) ? kSumF32x32 : qt == Q2_K ? kSumF32x16 : (qt == Q6_K || qt == Q3_K) ? kSumI32x16 : kSumNone;
+}
+__host__ __device__ constexpr int32_t sum_offset_of(uint32_t qt) { return qt == Q6_K ? -32 : qt == Q3_K ? -4 : 1; }
+__host__ __device__ constexpr uint32_t sum_width(int kind) { return kind == kSumF32x32 ? 32u : kind ? 16u : 0u; }
+
 // ---------------------------------------------------------------------------------
 // Tiled slab layout of an expert matrix (rows x cols, packed rows of blocks).
 //
@@ -128,7 +142,7 @@ struct FwdBufs {
   float* logits;         // [n][ne]
   int8_t* xq;            // [n][d]
   float* xs;             // [n][d/32]
-  int32_t* x16;          // [n][d/16]
+  uint32_t* xsum;        // [n][d/sum_width]: sums in the gate/up type's form (sum_kind_of)
   uint32_t* offsets;     // [ne+1]
   uint32_t* active;      // [1 + ne]: count, then active expert ids ascending
   uint32_t* slot_tok;    // [n*k]
@@ -146,7 +160,7 @@ struct FwdBufs {
   _Float16* hsh;         // [2][n*k][f/16]
   int8_t* hq;            // [n*k][f]
   float* hsc;            // [n*k][f/32]
-  int32_t* h16;          // [n*k][f/16]
+  uint32_t* hsum;        // [n*k][f/sum_width]: sums in the down type's form
   float* hf;             // [n*k][f]
   float* y;              // [kMaxKsg][n*k][d] partial slices of the down product
   uint32_t* done;        // [1] workgroups of the front end that have finished; 0 between calls
@@ -175,7 +189,9 @@ struct RouteArgs {
   float* comb_w;            // [n][k]
   uint32_t n, ne, k, d, gating, sec, combine;
 };
-constexpr uint32_t kRouteSection = 4096;  // values of d per LDS half in route_logit
+// Values of d per LDS half in route_logit. It shares its launch's LDS size with the expert
+// workgroups, so it is kept small (8 KB in all).
+constexpr uint32_t kRouteSection = 1024;
 inline uint32_t route_logit_lds(uint32_t k, uint32_t sec) { return (2 * sec + 2 * k) * 4; }
 
 struct LayerDev {
@@ -223,8 +239,9 @@ inline uint32_t prefill_tiles_cap(uint32_t n, uint32_t k, uint32_t ne) { return 
 hipError_t launch_dequant(uint32_t qtype, const uint8_t* blocks, size_t nblocks, float* out,
                           hipStream_t st);
 hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t st);
+// sums in the form the packed dot of type `reader` reads (sum_kind_of)
 hipError_t launch_quant_act(const float* x, uint32_t n_tok, uint32_t K, int8_t* q, float* s,
-                            int32_t* s16, hipStream_t st);
+                            uint32_t* sums, uint32_t reader, hipStream_t st);
 hipError_t launch_route(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 hipError_t launch_dispatch(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 // Route + gate + int8 activation quantiser (when quant) + dispatch in one launch, for

@@ -80,7 +80,7 @@ hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t st) {
 
 __global__ void __launch_bounds__(256) k_quant_act(const float* __restrict__ x, uint32_t nblk,
                                                    int8_t* __restrict__ q, float* __restrict__ s,
-                                                   int32_t* __restrict__ s16) {
+                                                   uint32_t* __restrict__ sums, int kind, int32_t off) {
   uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= nblk) return;
   float v[32];
@@ -90,13 +90,14 @@ __global__ void __launch_bounds__(256) k_quant_act(const float* __restrict__ x, 
     float4 t = p[i];
     v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
   }
-  quant32(v, q + (size_t)b * 32, s + b, s16 + 2 * (size_t)b);
+  quant32(v, q + (size_t)b * 32, s + b, sums, b, kind, off);
 }
 
 hipError_t launch_quant_act(const float* x, uint32_t n_tok, uint32_t K, int8_t* q, float* s,
-                            int32_t* s16, hipStream_t st) {
+                            uint32_t* sums, uint32_t reader, hipStream_t st) {
   uint32_t nblk = n_tok * (K / 32);
-  hipLaunchKernelGGL(k_quant_act, dim3((nblk + 255) / 256), dim3(256), 0, st, x, nblk, q, s, s16);
+  hipLaunchKernelGGL(k_quant_act, dim3((nblk + 255) / 256), dim3(256), 0, st, x, nblk, q, s, sums,
+                     sum_kind_of(reader), sum_offset_of(reader));
   return hipGetLastError();
 }
 
@@ -538,7 +539,7 @@ __global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, 
         v[4 * i] = t4.x; v[4 * i + 1] = t4.y; v[4 * i + 2] = t4.z; v[4 * i + 3] = t4.w;
       }
       const size_t gb = (size_t)t * nblk + b;
-      quant32(v, B.xq + gb * 32, B.xs + gb, B.x16 + 2 * gb);
+      quant32(v, B.xq + gb * 32, B.xs + gb, B.xsum, gb, sum_kind_of(L.qt_gate), sum_offset_of(L.qt_gate));
     }
   };
   float x = 0.0f;  // wave 0, lane e < ne: the logit of expert e
@@ -734,14 +735,14 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
         v[4 * i] = t4.x; v[4 * i + 1] = t4.y; v[4 * i + 2] = t4.z; v[4 * i + 3] = t4.w;
       }
       const size_t gb = (size_t)t * nblk + b;
-      quant32(v, B.xq + gb * 32, B.xs + gb, B.x16 + 2 * gb);
+      quant32(v, B.xq + gb * 32, B.xs + gb, B.xsum, gb, sum_kind_of(L.qt_gate), sum_offset_of(L.qt_gate));
     }
   }
   __syncthreads();
   if (wave != 0) {
     if (qown) {
       const size_t gb = (size_t)t * nblk + qb;
-      quant32(qv, B.xq + gb * 32, B.xs + gb, B.x16 + 2 * gb);
+      quant32(qv, B.xq + gb * 32, B.xs + gb, B.xsum, gb, sum_kind_of(L.qt_gate), sum_offset_of(L.qt_gate));
     }
     return;
   }

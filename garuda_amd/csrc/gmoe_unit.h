@@ -85,9 +85,14 @@ struct UnitStream {
   }
 
   template <class Body>
-  __device__ __forceinline__ void run(Body body) {
+  __device__ __forceinline__ void run(Body body) { run_range(u0, u1, body); }
+
+  // The units [a, b) of the stream, a - u0 a multiple of D, the ring carried on from the
+  // previous range (its loads of the range's first units are in flight).
+  template <class Body>
+  __device__ __forceinline__ void run_range(uint32_t a, uint32_t b, Body body) {
     if (u0 >= u1) return;
-    for (uint32_t u = u0; u < u1; u += D) {
+    for (uint32_t u = a; u < b; u += D) {
 #pragma unroll
       for (int s = 0; s < D; s++) {
         if (u + s < u1) {

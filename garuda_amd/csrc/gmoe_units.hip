@@ -26,38 +26,6 @@ namespace gmoe {
 // chunk) and are read as broadcasts.
 // ---------------------------------------------------------------------------------
 
-// quant/mod.rs:398-407 over a repacked Q8_0 unit: block g adds ws*xs*dot.
-template <int TM>
-__device__ __forceinline__ void pk_q80_unit(const uint32_t* w, uint32_t nvalid, const int8_t* const* x,
-                                            const float* const* xs, float* acc, int m) {
-#pragma unroll
-  for (int g = 0; g < 8; g++) {
-    if ((uint32_t)g < nvalid) {
-      const float ws = f16f(w[g / 2] >> (16 * (g % 2)));
-      const uint32_t* q = w + 4 + 8 * g;
-#pragma unroll
-      for (int t = 0; t < TM; t++) {
-        if (t < m) {
-          const uint32_t* xa = reinterpret_cast<const uint32_t*>(x[t] + 32 * g);
-          int dt = 0;
-#pragma unroll
-          for (int i = 0; i < 8; i++) dt = sdot4(q[i], xa[i], dt);
-          acc[t] += ws * xs[t][g] * (float)dt;
-        }
-      }
-    }
-  }
-}
-
-// One unit's contribution to each chunk member's row dot. x/xs/sm (packed) or x (f32)
-// point at the unit's first element; nvalid = blocks of the unit inside the row.
-template <int QT, int TM>
-__device__ __forceinline__ void unit_packed(const uint32_t* w, uint32_t nvalid, const int8_t* const* x,
-                                            const float* const* xs, const uint32_t* const* sm, float* acc, int m) {
-  if constexpr (QT == Q8_0) pk_q80_unit<TM>(w, nvalid, x, xs, acc, m);
-  else pk_block<QT, TM>(w, x, xs, sm, acc, m);
-}
-
 template <int QT, int TM>
 __device__ __forceinline__ void unit_f32(const uint32_t* w, uint32_t nvalid, const float* const* x, float* acc, int m) {
   constexpr int NG = UT_<QT>::EU / 32, GPB = QT_<QT>::E / 32;  // groups per unit / per block
@@ -103,12 +71,14 @@ struct ActLds {
 };
 
 // Stages tokens 0..m-1 of a chunk. rows[t] (LDS) is token t's row in the activation
-// arrays, whose rows are K long. Packed with q null: quantised here from the f32 rows x. Every thread issues up to four loads before it stores,
-// over the chunk's tokens flattened, so the chunk costs about one memory round trip.
+// arrays, whose rows are K long; the sums are already in the type's form (the quantisers
+// write them so). Packed with q null: quantised here from the f32 rows x. Every thread
+// issues up to four loads before it stores, over the chunk's tokens flattened, so the
+// chunk costs about one memory round trip.
 template <int QT, bool PACKED>
 __device__ __forceinline__ void stage_acts(uint8_t* lds, uint32_t nelem, uint32_t m, const uint32_t* rows, uint32_t K,
                                            uint32_t k0, const int8_t* __restrict__ q, const float* __restrict__ s,
-                                           const int32_t* __restrict__ s16, const float* __restrict__ x) {
+                                           const uint32_t* __restrict__ sums, const float* __restrict__ x) {
   using A = ActLds<QT, PACKED>;
   const uint32_t per = A::per_token(nelem), bd = blockDim.x;
   // copies n items of `width` elements of type T per token: item c of token t comes from
@@ -174,12 +144,8 @@ __device__ __forceinline__ void stage_acts(uint8_t* lds, uint32_t nelem, uint32_
     });
     copy(nelem / 32, A::qb(nelem), [&](uint32_t r, uint32_t c) { return s[(size_t)r * (K / 32) + k0 / 32 + c]; });
     if constexpr (KIND != kSumNone) {
-      copy(nelem / A::SW, A::qb(nelem) + A::sb(nelem), [&](uint32_t r, uint32_t c) {
-        const int32_t* src = s16 + (size_t)r * (K / 16) + k0 / 16;
-        if constexpr (KIND == kSumF32x32) return __float_as_uint((float)(src[2 * c] + src[2 * c + 1]));
-        else if constexpr (KIND == kSumF32x16) return __float_as_uint((float)src[c]);
-        else return (uint32_t)(sum_offset<QT>() * src[c]);
-      });
+      copy(nelem / A::SW, A::qb(nelem) + A::sb(nelem),
+           [&](uint32_t r, uint32_t c) { return sums[(size_t)r * (K / A::SW) + k0 / A::SW + c]; });
     }
   } else {
     copy(nelem / 4, 0u, [&](uint32_t r, uint32_t c) {
@@ -188,40 +154,28 @@ __device__ __forceinline__ void stage_acts(uint8_t* lds, uint32_t nelem, uint32_
   }
 }
 
-// One token's share of unit u: acc += the unit's terms against the token's staged
-// activations `tok` (whose first element is unit ubase's).
-template <int QT, bool PACKED>
-__device__ __forceinline__ void token_unit(const uint32_t* w, const uint8_t* tok, uint32_t nelem, uint32_t u,
-                                           uint32_t ubase, uint32_t nblk, float& acc) {
-  constexpr int EU = UT_<QT>::EU, G = UT_<QT>::G;
-  using A = ActLds<QT, PACKED>;
-  const uint32_t off = (u - ubase) * EU;
-  const uint32_t nvalid = G == 1 ? 1u : min((uint32_t)G, nblk - u * G);
-  float a[1] = {acc};
-  if constexpr (PACKED) {
-    const int8_t* xb[1] = {reinterpret_cast<const int8_t*>(tok) + off};
-    const float* sbp[1] = {reinterpret_cast<const float*>(tok + A::qb(nelem)) + off / 32};
-    const uint32_t* hbp[1] = {reinterpret_cast<const uint32_t*>(tok + A::qb(nelem) + A::sb(nelem)) +
-                              (A::SW ? off / A::SW : 0)};
-    unit_packed<QT, 1>(w, nvalid, xb, sbp, hbp, a, 1);
-  } else {
-    const float* xb[1] = {reinterpret_cast<const float*>(tok) + off};
-    unit_f32<QT, 1>(w, nvalid, xb, a, 1);
-  }
-  acc = a[0];
-}
-
 // Unit u's share of every token of the chunk (`my[t * 64]` holds token t's running row
-// sum). Packed: the token loop runs over whole units (the unit's decoded quants and
-// scales stay in registers across it). f32: the dequantised values of one 32-value
+// sum; token t's staged activations start at acts + t * per, whose first element is unit
+// ubase's). Packed: the token loop runs over whole units, the row sum in a register
+// across each (the unit's decoded quants and scales stay in registers across the loop;
+// running the sub-block groups outermost instead, the sums read and written in LDS per
+// group, measured slower: C4 225 -> 305 us). f32: the dequantised values of one 32-value
 // group at a time, each group applied to every token, in group order.
 template <int QT, bool PACKED>
 __device__ __forceinline__ void unit_tokens(const uint32_t* w, const uint8_t* acts, uint32_t per, uint32_t nelem,
                                             uint32_t u, uint32_t ubase, uint32_t nblk, float* my, uint32_t m) {
   if constexpr (PACKED) {
+    using A = ActLds<QT, true>;
+    constexpr int EU = UT_<QT>::EU, G = UT_<QT>::G;
+    const uint32_t off = (u - ubase) * EU;
+    const uint32_t nvalid = G == 1 ? 1u : min((uint32_t)G, nblk - u * G);
+    const uint32_t o_s = A::qb(nelem) + off / 8, o_h = A::qb(nelem) + A::sb(nelem) + (A::SW ? off / A::SW * 4 : 0u);
     for (uint32_t t = 0; t < m; t++) {
+      const uint8_t* tok = acts + t * per;
       float acc = my[t * 64];
-      token_unit<QT, true>(w, acts + t * per, nelem, u, ubase, nblk, acc);
+      const PkTok a{reinterpret_cast<const int8_t*>(tok) + off, reinterpret_cast<const float*>(tok + o_s),
+                    reinterpret_cast<const uint32_t*>(tok + o_h), &acc};
+      pk_unit<QT>(w, nvalid, 1u, [&](uint32_t) { return a; });
       my[t * 64] = acc;
     }
   } else {
@@ -266,9 +220,9 @@ template <int QT, bool PACKED, int D>
 __global__ void __launch_bounds__(128, D > 2 ? 1 : 2)
 k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __restrict__ slot_tok, uint32_t f,
            uint32_t d, uint32_t mt, const int8_t* __restrict__ xq,
-           const float* __restrict__ xs, const int32_t* __restrict__ x16, const float* __restrict__ hs,
-           int8_t* __restrict__ hq, float* __restrict__ hsc, int32_t* __restrict__ h16, float* __restrict__ hf,
-           RouteArgs ra) {
+           const float* __restrict__ xs, const uint32_t* __restrict__ xsum, const float* __restrict__ hs,
+           int8_t* __restrict__ hq, float* __restrict__ hsc, uint32_t* __restrict__ hsum, float* __restrict__ hf,
+           int hkind, int32_t hoff, RouteArgs ra) {
   constexpr int U = UT_<QT>::U;
   extern __shared__ uint4 dsm[];
   if (ra.n) {
@@ -302,7 +256,7 @@ k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __r
     for (uint32_t t = threadIdx.x; t < m; t += blockDim.x) rows[t] = slot_tok[s0 + c0 + t];
     for (uint32_t t = 0; t < m; t++) my[t * 64] = 0.0f;
     __syncthreads();
-    stage_acts<QT, PACKED>(acts, d, m, rows, d, 0, xq, xs, x16, hs);
+    stage_acts<QT, PACKED>(acts, d, m, rows, d, 0, xq, xs, xsum, hs);
     __syncthreads();
     st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED>(w, acts, per, d, u, 0, nblk, my, m); });
     __syncthreads();
@@ -312,7 +266,9 @@ k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __r
         const float h = swiglu(accs[t * 64 + lane], accs[(mt + t) * 64 + lane]);
         const size_t slot = s0 + c0 + t;
         if (hf && r0 + lane < f) hf[slot * f + r0 + lane] = h;
-        if (hq) quant_wave(h, lane, valid, hq + slot * f + r0, hsc + slot * (f / 32) + r0 / 32, h16 + slot * (f / 16) + r0 / 16);
+        if (hq)
+          quant_wave(h, lane, valid, hq + slot * f + r0, hsc + slot * (f / 32) + r0 / 32,
+                     hkind ? hsum + slot * (f / sum_width(hkind)) : nullptr, r0, hkind, hoff);
       }
     }
     __syncthreads();  // the sums and the staged activations are reused by the next chunk
@@ -327,7 +283,7 @@ k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __r
 template <int QT, bool PACKED, int KS>
 __global__ void __launch_bounds__(64 * KS, 2)
 k_dn_units(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32_t d, uint32_t mt, uint32_t part_stride,
-           const int8_t* __restrict__ hq, const float* __restrict__ hsc, const int32_t* __restrict__ h16,
+           const int8_t* __restrict__ hq, const float* __restrict__ hsc, const uint32_t* __restrict__ hsum,
            const float* __restrict__ hf, float* __restrict__ ypart) {
   constexpr int U = UT_<QT>::U, EU = UT_<QT>::EU;
   extern __shared__ uint4 dsm[];
@@ -357,7 +313,7 @@ k_dn_units(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32_
     for (uint32_t t = threadIdx.x; t < m; t += blockDim.x) rows[t] = s0 + c0 + t;
     for (uint32_t t = 0; t < m; t++) my[t * 64] = 0.0f;
     __syncthreads();
-    if (nelem) stage_acts<QT, PACKED>(acts, nelem, m, rows, f, uw0 * EU, hq, hsc, h16, hf);
+    if (nelem) stage_acts<QT, PACKED>(acts, nelem, m, rows, f, uw0 * EU, hq, hsc, hsum, hf);
     __syncthreads();
     st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED>(w, acts, per, nelem, u, uw0, nblk, my, m); });
     __syncthreads();
@@ -393,13 +349,18 @@ static bool allow_lds(K kernel) {
 }
 
 // Tokens per chunk: enough for the tokens an expert usually gets (twice the mean n*k/ne,
-// at least 8), as far as their staged activations and running sums fit the LDS budget;
-// an expert with more tokens takes several chunks, re-streaming its weights once per
-// chunk. Sizing for the whole batch instead would give every workgroup the LDS of n
-// tokens and one workgroup per CU when experts are many and tokens per expert few.
+// at least 8), as far as their staged activations and running sums fit kChunkLds; an
+// expert with more tokens takes several chunks, re-streaming its weights once per chunk.
+// kChunkLds leaves four workgroups per CU, the most the expert kernels' registers (about
+// 180-240 VGPRs: two waves per SIMD) allow anyway: on the C2 layer at batch 8, 8 tokens
+// of 5.6 KB held the gate/up kernel to three (118 us), 7 tokens let it run four (112 us).
+// Sizing for the whole batch instead would give every workgroup the LDS of n tokens and
+// one workgroup per CU when experts are many and tokens per expert few.
+constexpr uint32_t kChunkLds = 40 * 1024 - 64;
 static uint32_t chunk_tokens(const LayerDev& L, uint32_t n, uint32_t per_token_bytes) {
   const uint32_t usual = max(8u, 2 * ((n * L.k + L.ne - 1) / L.ne));
-  return min(min(n, usual), kLdsBudget / per_token_bytes);
+  const uint32_t fit = kChunkLds / per_token_bytes;  // 0 when one token needs more (then one, if it fits at all)
+  return min(min(n, usual), fit ? fit : kLdsBudget / per_token_bytes);
 }
 
 template <int QT, bool PACKED, int D>
@@ -414,7 +375,7 @@ static hipError_t go_gu(const LayerDev& L, const FwdBufs& B, uint32_t n, const R
   if (ra.n) lds = max(lds, route_logit_lds(ra.k, ra.sec));
   const dim3 g(max(tiles, ra.n * ra.ne), min(L.ne, n * L.k) + (ra.n ? 1 : 0));
   hipLaunchKernelGGL((k_gu_units<QT, PACKED, D>), g, dim3(128), lds, st, B.work, L.ne, B.slot_tok, L.f, L.d, mt, B.xq,
-                     B.xs, B.x16, B.hs, B.hq, B.hsc, B.h16, B.hf, ra);
+                     B.xs, B.xsum, B.hs, B.hq, B.hsc, B.hsum, B.hf, sum_kind_of(L.qt_down), sum_offset_of(L.qt_down), ra);
   return hipGetLastError();
 }
 
@@ -429,7 +390,7 @@ static hipError_t go_dn(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_
   (void)once;
   const dim3 g((L.d + kTileRows - 1) / kTileRows, ksg, min(L.ne, n * L.k));
   hipLaunchKernelGGL((k_dn_units<QT, PACKED, kDnKS>), g, dim3(64 * kDnKS), mt * per + 16, st, B.work, L.ne, L.f, L.d, mt,
-                     B.nslot * L.d, B.hq, B.hsc, B.h16, B.hf, B.y);
+                     B.nslot * L.d, B.hq, B.hsc, B.hsum, B.hf, B.y);
   return hipGetLastError();
 }
 
