@@ -440,6 +440,63 @@ def e2e_leg(a, threads, cpu):
     return res
 
 
+def c1_leg(a, dev, threads, cpu):
+    """garuda's synthetic engine (MoeEngine) generalised to 4 layers,
+    d 256, 8 query / 2 kv heads of 32, 8 experts top-2 of 512, vocab 512, its f32 weights from
+    the engine's seeded generator and its experts through the L2 tier (synthesised into a
+    temporary directory, then staged into the slab). Batch-1 greedy decode of 64 tokens
+    after a 16-token prompt fed one token per step, on the GPU and, as the CPU figure, in
+    the oracle's restatement (configuration 1 is not runnable on the reference itself: its
+    engine is one MHA block)."""
+    import tempfile
+
+    from garuda_amd.synthetic import SyntheticEngine
+
+    dims = dict(n_layers=4, d_model=256, n_heads=8, n_kv_heads=2, head_dim=32, d_ff=512, n_experts=8, top_k=2,
+                vocab=512)
+    prompt = np.random.default_rng(SEED & 0xFFFFFFFF).integers(0, dims["vocab"], 16)
+    n_new = a.c1_tokens
+
+    def run(step, open_seq):
+        seq = open_seq()
+        t0 = time.perf_counter()
+        for t in prompt:
+            nxt = step(seq, int(t))
+        t1 = time.perf_counter()
+        toks = []
+        for _ in range(n_new):
+            toks.append(int(nxt))
+            nxt = step(seq, int(nxt))
+        return toks, t1 - t0, time.perf_counter() - t1
+
+    with tempfile.TemporaryDirectory() as td, SyntheticEngine(dev, td, max_positions=256, **dims) as eng:
+        gstep = lambda seq, t: eng.step([seq], [t])[0]
+        run(gstep, eng.open_seq)  # warm-up pass (its own sequence)
+        gtoks, gp, gd = run(gstep, eng.open_seq)
+    out = {"workload": "C1 synthetic engine restated: 4 layers d256 GQA 8/2 hd32, 8 experts top-2 of 512, "
+                       "vocab 512, f32 seeded weights, experts through the L2 tier; batch-1 greedy decode",
+           "prompt_tokens": len(prompt), "decode_tokens": n_new,
+           "prompt_tokens_per_s": len(prompt) / gp, "decode_tokens_per_s": n_new / gd,
+           "ms_per_decode_step": gd / n_new * 1e3}
+    log(f"c1: {out['decode_tokens_per_s']:.0f} decode tok/s ({out['ms_per_decode_step']:.3f} ms a step), "
+        f"prompt {out['prompt_tokens_per_s']:.0f} tok/s")
+    if cpu:
+        from oracle.model import synthetic_engine
+        orc = synthetic_engine(dims["n_layers"], dims["d_model"], dims["n_heads"], dims["n_kv_heads"],
+                               dims["head_dim"], dims["d_ff"], dims["n_experts"], dims["top_k"], dims["vocab"],
+                               max_positions=256, threads=threads)
+        cseq = iter(range(1 << 30))
+        ctoks, cp, cd = run(lambda seq, t: orc.decode_step([seq], [t])[0][0], lambda: next(cseq))
+        same = sum(1 for x, y in zip(gtoks, ctoks) if x == y)
+        out["cpu_restatement"] = {"value": n_new / cd, "unit": "tokens/s", "cores": threads, "kind": "port",
+                                  "sample": f"the same {len(prompt)}-token prompt and {n_new} greedy tokens through "
+                                            f"the oracle's restatement (oracle.model.synthetic_engine), "
+                                            f"{cd:.2f}s for the decode tokens"}
+        out["greedy_tokens_equal"] = f"{same}/{n_new}"
+        log(f"c1 cpu restatement: {n_new / cd:.1f} tok/s; greedy tokens equal {same}/{n_new}")
+    return out
+
+
 def gguf_leg(a, dev, mats, threads):
     """The slab's source, a GGUF checkpoint: the C2 layer written as a one-layer GGUF
     checkpoint (stacked Q4_K experts, F32 router), then Gguf.open + MoeLayer.from_gguf timed
@@ -530,6 +587,8 @@ def main():
                     help="layers of the C5 end-to-end decode leg (0: skip it)")
     ap.add_argument("--e2e-prompt", type=int, default=128, help="prompt tokens per sequence of the end-to-end leg")
     ap.add_argument("--e2e-steps", type=int, default=32, help="timed decode steps of the end-to-end leg")
+    ap.add_argument("--c1-tokens", type=int, default=64,
+                    help="greedy decode tokens of the C1 synthetic-engine leg after its 16-token prompt (0: skip)")
     ap.add_argument("--extra", default="c4,c5_layer",
                     help="further BASELINE configurations to time at decode (c4, c5_layer); empty skips")
     a = ap.parse_args()
@@ -635,6 +694,7 @@ def main():
     attention = attention_leg(a, dev, threads, stream, timed) if a.attention else None
     gguf = gguf_leg(a, dev, mats, threads) if a.gguf_reps > 0 else None
     e2e = e2e_leg(a, threads, not a.no_cpu) if a.e2e_layers > 0 else None
+    c1 = c1_leg(a, dev, threads, not a.no_cpu) if a.c1_tokens > 0 else None
 
     if a.calibrate_copy:
         src = torch.empty(a.calibrate_copy << 18, dtype=torch.float32, device="cuda")
@@ -696,6 +756,7 @@ def main():
         "attention": attention,
         "gguf_staging": gguf,
         "c5_end_to_end": e2e,
+        "c1_synthetic_engine": c1,
         "sweep": {str(n): {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res.items()}
                   for n, res in results.items()},
     }

@@ -51,6 +51,10 @@ class GmoeGgufTensorInfo(C.Structure):
                 ("offset", u64), ("n_elements", u64), ("nbytes", u64), ("data", vp)]
 
 
+class GmoeL2Counts(C.Structure):
+    _fields_ = [("l2", u64), ("synthesised", u64), ("written", u64)]
+
+
 class GmoePredictStats(C.Structure):
     _fields_ = [("correct", u64), ("wasted", u64), ("missed", u64)]
 
@@ -79,6 +83,11 @@ SIGNATURES = {
     "gmoe_expf": (i32, [vp, f32p, u64, f32p]),
     "gmoe_quantize": (i32, [u32, f32p, u64, vp, i32]),
     "gmoe_fill_gaussian": (i32, [u64, C.c_float, C.c_float, u64, f32p, i32]),
+    "gmoe_fill_seeded": (i32, [u64, u64, C.c_float, f32p]),
+    "gmoe_l2_open": (i32, [C.c_char_p, u32, u32, u32, u32, C.POINTER(vp)]),
+    "gmoe_l2_close": (None, [vp]),
+    "gmoe_l2_get_counts": (i32, [vp, C.POINTER(GmoeL2Counts)]),
+    "gmoe_l2_layer_desc": (i32, [vp, f32p, u32, u32, u32, C.POINTER(GmoeLayerDesc)]),
     "gmoe_dense_register": (i32, [vp, C.POINTER(GmoeDenseDesc), u32p]),
     "gmoe_dense_release": (i32, [vp, u32]),
     "gmoe_dense_forward": (i32, [vp, u32, f32p, u32, f32p]),

@@ -17,7 +17,7 @@ LIB = PKG / "libgaruda_moe.so"
 ARCH = os.environ.get("GMOE_ARCH", "gfx950")
 
 SOURCES = ["gmoe_kernels.hip", "gmoe_api.cpp", "gmoe_quant.cpp", "gmoe_gguf.cpp", "gmoe_predict.cpp", "gmoe_kv.cpp",
-           "gmoe_attn.hip", "gmoe_glue.hip", "gmoe_model.cpp", "gmoe_noalloc.hip"]
+           "gmoe_attn.hip", "gmoe_glue.hip", "gmoe_model.cpp", "gmoe_noalloc.hip", "gmoe_l2.cpp"]
 # gmoe_units.hip is built once per block type (ggml type ids), each object holding one
 # type's expert kernels; gmoe_prefill.hip likewise for the types with MFMA prefill.
 UNIT_TYPES = {"f32": 0, "f16": 1, "q4_0": 2, "q8_0": 8, "q2_k": 10, "q3_k": 11, "q4_k": 12, "q5_k": 13, "q6_k": 14}

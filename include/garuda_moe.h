@@ -263,6 +263,41 @@ gmoe_status gmoe_gguf_layer_desc(gmoe_gguf* g, uint32_t layer, uint32_t gating, 
 gmoe_status gmoe_gguf_expert_ranges(gmoe_gguf* g, uint32_t layer, uint32_t expert, uint64_t offset[3],
                                     uint64_t length[3]);
 
+/* ---- the synthetic engine's expert tiers (memory/mod.rs:114-184, weights/mod.rs:17-164) ----
+ *
+ * garuda's MoeEngine (moe/mod.rs:67-112) pulls each routed expert through MemoryManager:
+ * the L1 cache, else `expert_{id}.bin` in the L2 directory, else a deterministic synthesis
+ * written back to L2. Here the HBM slab is L1 and a gmoe_l2 handle is the L2 side. Each
+ * file is read as weights::expert_from_bytes reads it: little-endian f32, gate [f x d],
+ * up [f x d], down [d x f], exactly 3*f*d*4 bytes, every value finite (GMOE_ERR_MODEL with
+ * the reference's message otherwise). An expert with no file is synthesised as
+ * weights::synthesize_expert does and written to the directory (a failed write is not an
+ * error). Host code; the files stay mapped while the handle lives. */
+typedef struct gmoe_l2 gmoe_l2;
+typedef struct gmoe_l2_counts {
+  uint64_t l2;           /* experts read from their file (TierCounts::l2) */
+  uint64_t synthesised;  /* experts synthesised (TierCounts::synthesised) */
+  uint64_t written;      /* synthesised experts materialised into the directory */
+} gmoe_l2_counts;
+
+/* weights::seeded (weights/mod.rs:26-35): n values uniform in [-bound, bound] from the
+ * splitmix64 stream of `seed`; the engine's shared weights use it with bound(fan_in) =
+ * 1 / sqrt(fan_in) (:38-40) and the seeds of :43-51. */
+gmoe_status gmoe_fill_seeded(uint64_t seed, uint64_t n, float bound, float* out);
+/* Experts id_base .. id_base + n_experts - 1 of the directory `dir` (expert e of the layer
+ * is file expert_{id_base + e}.bin). */
+gmoe_status gmoe_l2_open(const char* dir, uint32_t d_model, uint32_t d_ff, uint32_t n_experts, uint32_t id_base,
+                         gmoe_l2** out);
+void gmoe_l2_close(gmoe_l2* l2);
+gmoe_status gmoe_l2_get_counts(const gmoe_l2* l2, gmoe_l2_counts* out);
+/* The tier's experts as a layer descriptor: split F32 tensors pointing into the handle
+ * (valid until gmoe_l2_close, so a layer registered from it is released first), the
+ * given router [n_experts x d_model], top_k, gating (the engine's Router types: MIXTRAL,
+ * DEEPSEEK, QWEN) and combine order (the engine's is RANK_ORDER, moe/mod.rs:104-109),
+ * math F32 (simd::matvec, moe/mod.rs:82-90). */
+gmoe_status gmoe_l2_layer_desc(const gmoe_l2* l2, const float* router, uint32_t top_k, uint32_t gating,
+                               uint32_t combine, gmoe_layer_desc* out);
+
 /* ---- decode attention over a paged KV cache (llama/mod.rs:766-821, cache/mod.rs:143-600) ----
  *
  * A pool of device pages, each `block_size` positions of keys then values (f32, kv_dim =

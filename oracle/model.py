@@ -114,3 +114,43 @@ class ModelOracle:
         hidden = np.stack([norm(x, self.output_norm, self.eps) for x in xs])
         logits = self._matmul(self.output, hidden)
         return np.array([greedy(r) for r in logits], dtype=np.uint32), logits
+
+
+# ---- garuda's synthetic engine (MoeEngine, moe/mod.rs:67-187) as a ModelOracle ----
+
+SEED_EMBED, SEED_WQ, SEED_WK, SEED_WV, SEED_WO, SEED_ROUTER = (0x6761_7275_6461_0000 + i for i in range(1, 7))
+
+
+def engine_layer_seed(seed: int, layer: int) -> int:
+    """Layer l's seed for a tensor of the (one-block) reference engine: seed XOR (l << 32)."""
+    return seed ^ (layer << 32)
+
+
+def engine_experts(d, f, ids):
+    """Stacked F32 gate, up, down of the synthesised experts `ids` (weights/mod.rs:98-109)."""
+    g, u, dn = zip(*(O.synthesize_expert(i, d, f) for i in ids))
+    as_u8 = lambda parts: np.concatenate(parts).astype("<f4").view(np.uint8)
+    return as_u8(g), as_u8(u), as_u8(dn)
+
+
+def synthetic_engine(n_layers, d, nh, nkv, hd, f, ne, k, vocab, max_positions=2048, threads=8):
+    """MoeEngine generalised to n_layers grouped-query layers, from the oracle's own
+    generators: ModelWeights::synthesize's seeded tensors (weights/mod.rs:70-87; layer l's
+    seeds XOR (l << 32)), layer l's experts l*ne .. (l+1)*ne - 1, unit norm weights
+    (simd::rmsnorm carries none), the Mixtral router with rank-order combine
+    (moe/mod.rs:98-109), f32 products, and the head tied to the embedding."""
+    b, kvd = O.lib().or_bound(d), nkv * hd
+    emb = O.seeded(SEED_EMBED, vocab * d, b).reshape(vocab, d)
+    f32 = lambda a, rows, cols: (O.F32, np.ascontiguousarray(a, np.float32).view(np.uint8), rows, cols)
+    layers = []
+    for l in range(n_layers):
+        gate, up, down = engine_experts(d, f, range(l * ne, (l + 1) * ne))
+        moe = dict(d=d, f=f, ne=ne, k=k, gating=1, combine=1, packed=0, qtypes=(O.F32,) * 3,
+                   router=O.seeded(engine_layer_seed(SEED_ROUTER, l), ne * d, b), gate=gate, up=up, down=down)
+        layers.append(dict(attn_norm=np.ones(d, np.float32), ffn_norm=np.ones(d, np.float32),
+                           wq=f32(O.seeded(engine_layer_seed(SEED_WQ, l), d * d, b), d, d),
+                           wk=f32(O.seeded(engine_layer_seed(SEED_WK, l), kvd * d, b), kvd, d),
+                           wv=f32(O.seeded(engine_layer_seed(SEED_WV, l), kvd * d, b), kvd, d),
+                           wo=f32(O.seeded(engine_layer_seed(SEED_WO, l), d * d, b), d, d), moe=moe))
+    return ModelOracle(layers, f32(emb, vocab, d), np.ones(d, np.float32), emb, nh, nkv, hd, packed=False,
+                       max_positions=max_positions, threads=threads)

@@ -1,0 +1,88 @@
+"""The synthetic engine's L2 expert tier in the library (gmoe_l2_*, gmoe_fill_seeded; host
+code, no GPU): files read as weights::expert_from_bytes reads them, missing experts
+synthesised as weights::synthesize_expert does and written back (memory/mod.rs:138-145).
+The synthesis is pinned by the reference's own fixture files models/l2_cache/expert_{0,3,6,7}.bin
+(their SHA-256, tests/golden/l2_cache_experts.json), and every expert by the oracle's
+restatement."""
+import ctypes as C
+import hashlib
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import garuda_amd as G
+from garuda_amd import _lib
+from garuda_amd.tiers import ExpertTier, bound, engine_weights, fill_seeded
+from oracle import oracle as O
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+D, F, NE = 128, 256, 8  # ModelDims::default (core/mod.rs:68-82)
+
+
+def test_fill_seeded_is_the_reference_stream():
+    for seed, n, fan in ((0x6761_7275_6461_0006, 1024, 128), (7, 1000, 256), (0, 3, 1)):
+        a = fill_seeded(seed, n, bound(fan))
+        b = O.seeded(seed, n, O.lib().or_bound(fan))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    w = engine_weights(D, NE, 260)
+    assert w["embedding"].shape == (260, D) and np.abs(w["router"]).max() <= bound(D)
+
+
+def test_missing_experts_are_synthesised_and_written_as_the_reference_fixtures(tmp_path):
+    with ExpertTier(tmp_path, D, F, NE) as tier:
+        c = tier.counts()
+        assert (c.l2, c.synthesised, c.written) == (0, NE, NE)
+    fx = json.loads((GOLDEN / "l2_cache_experts.json").read_text())
+    for e in range(NE):
+        raw = (tmp_path / f"expert_{e}.bin").read_bytes()
+        g, u, d = O.synthesize_expert(e)
+        assert raw == np.concatenate([g, u, d]).astype("<f4").tobytes()
+        if str(e) in fx:  # the reference's own models/l2_cache files
+            assert hashlib.sha256(raw).hexdigest() == fx[str(e)]["sha256"]
+    # a second open reads every expert from its file
+    with ExpertTier(tmp_path, D, F, NE) as tier:
+        c = tier.counts()
+        assert (c.l2, c.synthesised) == (NE, 0)
+
+
+def test_layer_descriptor_points_at_each_experts_gate_up_down(tmp_path):
+    rng = np.random.default_rng(0)
+    e3 = rng.normal(0, 0.1, 3 * F * D).astype("<f4")
+    (tmp_path / "expert_3.bin").write_bytes(e3.tobytes())  # a file that is not the synthesis
+    router = fill_seeded(0x6761_7275_6461_0006, NE * D, bound(D))
+    with ExpertTier(tmp_path, D, F, NE) as tier:
+        assert (tier.counts().l2, tier.counts().synthesised) == (1, NE - 1)
+        desc = _lib.GmoeLayerDesc()
+        assert _lib.lib().gmoe_l2_layer_desc(tier.handle, router.ctypes.data_as(C.POINTER(C.c_float)), 2,
+                                             G.GATING_MIXTRAL, G.COMBINE_RANK_ORDER, C.byref(desc)) == 0
+        assert (desc.d_model, desc.d_ff, desc.n_experts, desc.top_k) == (D, F, NE, 2)
+        assert desc.math == G.MATH_F32 and desc.combine == G.COMBINE_RANK_ORDER
+        for p, (name, n) in enumerate((("gate", F * D), ("up", F * D), ("down", D * F))):
+            t = getattr(desc, name)
+            assert t.qtype == G.F32 and t.layout == 1
+            for e in (0, 3, 7):
+                got = np.ctypeslib.as_array(C.cast(t.experts[e], C.POINTER(C.c_float)), shape=(n,))
+                want = e3.reshape(3, -1)[p] if e == 3 else O.synthesize_expert(e)[p]
+                assert np.array_equal(got.view(np.uint32), np.asarray(want, np.float32).view(np.uint32))
+
+
+def test_id_base_names_the_files_of_a_later_layer(tmp_path):
+    with ExpertTier(tmp_path, D, F, NE, id_base=NE) as tier:
+        assert tier.counts().synthesised == NE
+    assert sorted(p.name for p in tmp_path.iterdir()) == sorted(f"expert_{i}.bin" for i in range(NE, 2 * NE))
+    g, _, _ = O.synthesize_expert(NE + 5)
+    raw = np.frombuffer((tmp_path / f"expert_{NE + 5}.bin").read_bytes(), "<f4")
+    assert np.array_equal(raw[:F * D].view(np.uint32), g.view(np.uint32))
+
+
+def test_bad_files_are_model_errors(tmp_path):
+    (tmp_path / "expert_2.bin").write_bytes(b"\0" * 100)
+    with pytest.raises(G.ModelError, match=r"expert 2: expected 393216 bytes for dims 128x256, found 100"):
+        ExpertTier(tmp_path, D, F, NE)
+    bad = np.zeros(3 * F * D, "<f4")
+    bad[1234] = np.nan
+    (tmp_path / "expert_2.bin").write_bytes(bad.tobytes())
+    with pytest.raises(G.ModelError, match=r"expert 2: non-finite weight at index 1234"):
+        ExpertTier(tmp_path, D, F, NE)

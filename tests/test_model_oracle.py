@@ -123,3 +123,18 @@ def test_refusals(weights):
         m.decode_step([0, 0], [1, 2])
     with pytest.raises(ValueError):
         m.decode_step([0], [embd.shape[0]])
+
+
+def test_engine_oracle_seeds_are_the_references():
+    """The synthetic-engine oracle's layer 0 is ModelWeights::synthesize's (weights/mod.rs:
+    43-87): the per-tensor seeds, bound(d) = 1/sqrt(d), and the experts whose synthesis the
+    reference's models/l2_cache files pin."""
+    from oracle import model as OM
+    orc = OM.synthetic_engine(1, 128, 4, 4, 32, 256, 8, 2, 260)
+    b = O.lib().or_bound(128)
+    L = orc.layers[0]
+    assert np.array_equal(L["wq"][1].view(np.float32), O.seeded(0x6761_7275_6461_0002, 128 * 128, b))
+    assert np.array_equal(L["moe"]["router"], O.seeded(0x6761_7275_6461_0006, 8 * 128, b))
+    assert np.array_equal(orc.table.reshape(-1), O.seeded(0x6761_7275_6461_0001, 260 * 128, b))
+    g3 = L["moe"]["gate"].view(np.float32).reshape(8, -1)[3]
+    assert np.array_equal(g3, O.synthesize_expert(3)[0])
