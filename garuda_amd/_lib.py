@@ -73,6 +73,9 @@ SIGNATURES = {
     "gmoe_ffn_forward_async": (i32, [vp, u32, vp, vp, u32, vp, vp, vp, vp]),
     "gmoe_ffn_forward_noalloc": (i32, [vp, u32, vp, vp, u32, vp, vp, vp, vp]),
     "gmoe_expert_prefetch": (i32, [vp, u32, u32]),
+    "gmoe_expert_state": (i32, [vp, u32, u32]),
+    "gmoe_prefetch_hold": (i32, [vp, i32]),
+    "gmoe_prefetch_wait": (i32, [vp]),
     "gmoe_expert_is_resident": (i32, [vp, u32, u32]),
     "gmoe_expert_evict": (i32, [vp, u32, u32]),
     "gmoe_slab_get_stats": (i32, [vp, C.POINTER(GmoeSlabStats)]),

@@ -10,7 +10,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <condition_variable>
 #include <cstdarg>
+#include <deque>
 #include <cstdio>
 #include <cstring>
 #include <list>
@@ -132,6 +134,11 @@ struct Proj {
 };
 
 using LruList = std::list<std::pair<uint32_t, uint32_t>>;  // (layer, expert), least recent first
+using Keep = std::vector<std::pair<uint32_t, uint32_t>>;      // (layer, expert) pairs not to evict
+
+// An expert's place on the staging thread's way (Layer::pending); GMOE_EXPERT_* says the
+// same to callers.
+enum : uint8_t { kAbsent = 0, kQueued = 1, kStaging = 2 };
 
 struct Layer {
   uint32_t d, f, ne, k, gating, combine, math;
@@ -141,6 +148,7 @@ struct Layer {
   std::vector<const uint8_t*> eptr_host;
   std::vector<int64_t> slot;      // per expert: slab offset or -1
   std::vector<LruList::iterator> lru_pos;  // per resident expert: its place in the LRU
+  std::vector<uint8_t> pending;   // per expert: kAbsent, or queued / staging by the staging thread
   uint64_t expert_bytes = 0;
   // the stream of the layer's last queued call (null: none): an evicted expert's region is
   // free once that stream has drained. An event recorded per call would say exactly when,
@@ -180,7 +188,20 @@ struct gmoe_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   hipStream_t copy_stream = nullptr;
-  std::mutex mu;
+  // Locks, taken in this order: mu serialises the entry points (an entry holds it from
+  // start to end); slab_mu guards the slab, the LRU, the layers' residency and pending
+  // states, the staging queue and the statistics; stage_mu guards the pinned halves and
+  // the copy stream. Background staging (prefetch/mod.rs:102-127): gmoe_prefetch_step
+  // queues predicted experts and `stager` stages them, taking slab_mu to reserve a region
+  // and to publish the staged expert and stage_mu for the copy, never mu; an entry that
+  // waits for it waits on cv, releasing slab_mu but keeping mu.
+  std::mutex mu, slab_mu, stage_mu;
+  std::thread stager;
+  std::condition_variable cv;  // with slab_mu: queue, hold, stop and the pending states
+  std::deque<std::pair<uint32_t, uint32_t>> queue;
+  Keep prefetch_keep;          // the last prefetch step's used and predicted experts
+  bool stop = false, hold = false;
+  uint32_t staging = 0;        // experts the thread is staging now
   Slab slab;
   std::vector<std::unique_ptr<Layer>> layers;
   std::vector<std::unique_ptr<Dense>> dense;
@@ -206,6 +227,13 @@ struct gmoe_ctx {
   std::vector<Timing> pool;
   double t_ms[3] = {0, 0, 0};
   uint64_t t_cnt = 0;
+};
+
+// An entry point's hold on a context: mu for the call, slab_mu (releasable by a wait).
+struct CtxLock {
+  std::lock_guard<std::mutex> call;
+  std::unique_lock<std::mutex> slab;
+  explicit CtxLock(gmoe_ctx* c) : call(c->mu), slab(c->slab_mu) {}
 };
 
 namespace gmoe {
@@ -259,7 +287,20 @@ gmoe_status stage_proj(gmoe_ctx* c, const Proj& P, const uint8_t* src, uint8_t* 
     HIP_TRY(launch_tile_rows(P.qtype, land, r0, nr, P.rows, P.cols, dst, c->copy_stream));
     HIP_TRY(hipEventRecord(c->pin_ev[buf], c->copy_stream));
   }
-  c->stats.h2d_bytes += (uint64_t)P.rows * P.row_bytes;
+  return GMOE_OK;
+}
+
+// Stage expert e's three matrices into the slab region at `off` and wait for the copies.
+// Runs under stage_mu; reads only what registration fixed.
+gmoe_status stage_expert(gmoe_ctx* c, const Layer& L, uint32_t e, uint64_t off, uint8_t* ptrs[3]) {
+  uint8_t* base = c->slab.base + off;
+  uint64_t o = 0;
+  for (int p = 0; p < 3; p++) {
+    if (gmoe_status s = stage_proj(c, L.p[p], L.p[p].host[e], base + o)) return s;
+    ptrs[p] = base + o;
+    o += (L.p[p].bytes_dev + 255) & ~uint64_t(255);
+  }
+  HIP_TRY(hipStreamSynchronize(c->copy_stream));
   return GMOE_OK;
 }
 
@@ -295,17 +336,11 @@ gmoe_status evict(gmoe_ctx* c, uint32_t l, uint32_t e) {
   return GMOE_OK;
 }
 
-// Make expert e of layer l resident. `pinned_set` marks experts of the current call that
-// must not be evicted to make room. evict_ok = false only fills free space.
-gmoe_status make_resident(gmoe_ctx* c, uint32_t l, uint32_t e, bool evict_ok,
-                          const std::vector<std::pair<uint32_t, uint32_t>>* keep) {
+// A slab region for one expert of layer l, evicting the least recently used experts not in
+// `keep` (evict_ok false: free space only). The caller holds slab_mu.
+gmoe_status reserve(gmoe_ctx* c, uint32_t l, bool evict_ok, const Keep* keep, uint64_t* off) {
   Layer& L = *c->layers[l];
-  if (L.slot[e] >= 0) {
-    touch(c, l, e);
-    return GMOE_OK;
-  }
-  uint64_t off;
-  while (!c->slab.alloc(L.expert_bytes, &off)) {
+  while (!c->slab.alloc(L.expert_bytes, off)) {
     if (!evict_ok) return fail(GMOE_ERR_CACHE, "HBM slab is full");
     auto victim = c->lru.end();
     for (auto it = c->lru.begin(); it != c->lru.end(); ++it) {
@@ -321,28 +356,90 @@ gmoe_status make_resident(gmoe_ctx* c, uint32_t l, uint32_t e, bool evict_ok,
       return fail(GMOE_ERR_CACHE, "HBM slab of %llu bytes cannot hold the experts this call needs",
                   (unsigned long long)c->slab.cap);
     auto v = *victim;
-    gmoe_status s = evict(c, v.first, v.second);
-    if (s) return s;
+    if (gmoe_status s = evict(c, v.first, v.second)) return s;
     c->stats.evictions++;
   }
-  uint8_t* base = c->slab.base + off;
-  uint64_t o = 0;
-  for (int p = 0; p < 3; p++) {
-    gmoe_status s = stage_proj(c, L.p[p], L.p[p].host[e], base + o);
-    if (s) {
-      c->slab.release(off, L.expert_bytes);
-      return s;
-    }
-    L.eptr_host[p * L.ne + e] = base + o;
-    o += (L.p[p].bytes_dev + 255) & ~uint64_t(255);
-  }
-  HIP_TRY(hipStreamSynchronize(c->copy_stream));
+  return GMOE_OK;
+}
+
+// Publish expert e, staged at `off`, as resident (most recently used). The caller holds slab_mu.
+gmoe_status publish(gmoe_ctx* c, uint32_t l, uint32_t e, uint64_t off, uint8_t* const ptrs[3]) {
+  Layer& L = *c->layers[l];
+  for (int p = 0; p < 3; p++) L.eptr_host[p * L.ne + e] = ptrs[p];
   HIP_TRY(hipMemcpy(L.eptr, L.eptr_host.data(), L.eptr_host.size() * sizeof(void*), hipMemcpyHostToDevice));
   L.slot[e] = (int64_t)off;
   L.lru_pos[e] = c->lru.emplace(c->lru.end(), l, e);
   c->stats.entries++;
   c->stats.bytes += L.expert_bytes;
+  for (int p = 0; p < 3; p++) c->stats.h2d_bytes += (uint64_t)L.p[p].rows * L.p[p].row_bytes;
   return GMOE_OK;
+}
+
+// Make expert e of layer l resident, with slab_mu held through `lk`. `keep` marks experts of the
+// current call that must not be evicted to make room; evict_ok = false only fills free
+// space. An expert the staging thread has queued is taken off its queue and staged here;
+// one it is staging now is waited for (the wait releases slab_mu).
+gmoe_status make_resident(gmoe_ctx* c, std::unique_lock<std::mutex>& lk, uint32_t l, uint32_t e, bool evict_ok,
+                          const Keep* keep) {
+  Layer& L = *c->layers[l];
+  c->cv.wait(lk, [&] { return L.pending[e] != kStaging; });
+  if (L.slot[e] >= 0) {
+    touch(c, l, e);
+    return GMOE_OK;
+  }
+  if (L.pending[e] == kQueued) {
+    c->queue.erase(std::remove(c->queue.begin(), c->queue.end(), std::make_pair(l, e)), c->queue.end());
+    L.pending[e] = kAbsent;
+    c->cv.notify_all();
+  }
+  uint64_t off;
+  if (gmoe_status s = reserve(c, l, evict_ok, keep, &off)) return s;
+  uint8_t* ptrs[3];
+  gmoe_status s;
+  {
+    std::lock_guard<std::mutex> sg(c->stage_mu);
+    s = stage_expert(c, L, e, off, ptrs);
+  }
+  if (s) {
+    c->slab.release(off, L.expert_bytes);
+    return s;
+  }
+  return publish(c, l, e, off, ptrs);
+}
+
+// The staging thread: stages queued experts one after another, unless held or stopped.
+void stager_main(gmoe_ctx* c) {
+  hipSetDevice(c->device);
+  std::unique_lock<std::mutex> lk(c->slab_mu);
+  for (;;) {
+    c->cv.wait(lk, [&] { return c->stop || (!c->hold && !c->queue.empty()); });
+    if (c->stop) break;
+    const auto [l, e] = c->queue.front();
+    c->queue.pop_front();
+    Layer& L = *c->layers[l];
+    if (!L.alive || L.slot[e] >= 0 || L.pending[e] != kQueued) continue;
+    uint64_t off;
+    if (reserve(c, l, true, &c->prefetch_keep, &off) != GMOE_OK) {  // no room: dropped, as a failed warm is
+      L.pending[e] = kAbsent;
+      c->cv.notify_all();
+      continue;
+    }
+    L.pending[e] = kStaging;
+    c->staging++;
+    lk.unlock();
+    uint8_t* ptrs[3];
+    gmoe_status s;
+    {
+      std::lock_guard<std::mutex> sg(c->stage_mu);
+      s = stage_expert(c, L, e, off, ptrs);
+    }
+    lk.lock();
+    if (s == GMOE_OK) s = publish(c, l, e, off, ptrs);
+    if (s != GMOE_OK) c->slab.release(off, L.expert_bytes);  // the forward stages it itself when routed
+    L.pending[e] = kAbsent;
+    c->staging--;
+    c->cv.notify_all();
+  }
 }
 
 // ---- scratch arena ----
@@ -689,9 +786,10 @@ gmoe_status get_layer(gmoe_ctx* c, uint32_t id, Layer** out) {
   return GMOE_OK;
 }
 
-// One launch sequence of at most call_tokens(L) tokens, host pointers (the lock is held).
-gmoe_status forward_chunk(gmoe_ctx* c, uint32_t lid, Layer* L, const float* hs, const float* logits, uint32_t n,
-                          float* out, uint32_t* ids, float* w) {
+// One launch sequence of at most call_tokens(L) tokens, host pointers (the context held
+// through `lk`, its slab lock).
+gmoe_status forward_chunk(gmoe_ctx* c, std::unique_lock<std::mutex>& lk, uint32_t lid, Layer* L, const float* hs,
+                          const float* logits, uint32_t n, float* out, uint32_t* ids, float* w) {
   Carved cv;
   size_t need = plan_scratch(*L, n, nullptr, nullptr);
   if (gmoe_status s = ensure_scratch(c, need)) return s;
@@ -720,10 +818,17 @@ gmoe_status forward_chunk(gmoe_ctx* c, uint32_t lid, Layer* L, const float* hs, 
       auto kp = std::make_pair(lid, v);
       if (std::find(keep.begin(), keep.end(), kp) == keep.end()) keep.push_back(kp);
     }
+    // first wait for any of them the staging thread is copying now, then make them all
+    // resident without releasing the lock, so that none is evicted before the launch
+    c->cv.wait(lk, [&] {
+      for (auto& kp : keep)
+        if (L->pending[kp.second] == kStaging) return false;
+      return true;
+    });
     for (auto& kp : keep) {
       if (L->slot[kp.second] >= 0) c->stats.hits++;
       else c->stats.misses++;
-      if (gmoe_status s = make_resident(c, lid, kp.second, true, &keep)) return s;
+      if (gmoe_status s = make_resident(c, lk, lid, kp.second, true, &keep)) return s;
     }
     // Only the routed experts are resident now: the layer runs from these exact logits.
     // The speculative front end would also compute products for candidate experts near
@@ -757,7 +862,7 @@ gmoe_status forward_host(gmoe_ctx* c, uint32_t lid, const float* hs, const float
   if (gmoe_status s = check_ctx(c)) return s;
   if (!hs || !out) return fail(GMOE_ERR_INFERENCE, "null activation pointer");
   if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   Layer* L;
   if (gmoe_status s = get_layer(c, lid, &L)) return s;
   HIP_TRY(hipSetDevice(c->device));
@@ -765,7 +870,8 @@ gmoe_status forward_host(gmoe_ctx* c, uint32_t lid, const float* hs, const float
   for (uint32_t t0 = 0; t0 < n; t0 += per) {
     const uint32_t m = std::min(per, n - t0);
     const size_t k = L->k;
-    if (gmoe_status s = forward_chunk(c, lid, L, hs + (size_t)t0 * L->d, logits ? logits + (size_t)t0 * L->ne : nullptr,
+    if (gmoe_status s = forward_chunk(c, g.slab, lid, L, hs + (size_t)t0 * L->d,
+                                      logits ? logits + (size_t)t0 * L->ne : nullptr,
                                       m, out + (size_t)t0 * L->d, ids ? ids + t0 * k : nullptr, w ? w + t0 * k : nullptr))
       return s;
   }
@@ -807,7 +913,7 @@ namespace gmoe {
 // (out = [W0 x; W1 x; ...]). They share type, width and math, and every one but the last
 // has a whole number of 64-row tiles, so the tiled bytes simply follow one another.
 gmoe_status dense_stack(gmoe_ctx* c, const uint32_t* ids, uint32_t count, uint32_t* out) {
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   if (count == 0) return fail(GMOE_ERR_INFERENCE, "nothing to stack");
   std::vector<Dense*> parts(count);
   for (uint32_t i = 0; i < count; i++)
@@ -845,7 +951,7 @@ gmoe_status dense_stack(gmoe_ctx* c, const uint32_t* ids, uint32_t count, uint32
 
 // Shapes of registered weights, for the decode-step driver (gmoe_model.cpp).
 bool dense_shape(gmoe_ctx* c, uint32_t id, uint32_t* rows, uint32_t* cols) {
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   Dense* W;
   if (get_dense(c, id, &W) != GMOE_OK) return false;
   *rows = W->rows;
@@ -854,7 +960,7 @@ bool dense_shape(gmoe_ctx* c, uint32_t id, uint32_t* rows, uint32_t* cols) {
 }
 
 bool layer_width(gmoe_ctx* c, uint32_t id, uint32_t* d, uint32_t* ne) {
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   Layer* L;
   if (get_layer(c, id, &L) != GMOE_OK) return false;
   *d = L->d;
@@ -911,12 +1017,20 @@ gmoe_status gmoe_init(int device, uint64_t slab_bytes, gmoe_ctx** out) {
   HIP_TRY(hipEventCreateWithFlags(&c->pin_ev[1], hipEventDisableTiming));
   HIP_TRY(hipEventRecord(c->pin_ev[0], c->copy_stream));
   HIP_TRY(hipEventRecord(c->pin_ev[1], c->copy_stream));
+  gmoe_ctx* raw = c.get();
+  c->stager = std::thread([raw] { stager_main(raw); });
   *out = c.release();
   return GMOE_OK;
 }
 
 void gmoe_shutdown(gmoe_ctx* c) {
   if (!c) return;
+  {  // the staging thread finishes the expert it is copying and stops
+    std::lock_guard<std::mutex> lk(c->slab_mu);
+    c->stop = true;
+  }
+  c->cv.notify_all();
+  if (c->stager.joinable()) c->stager.join();
   hipSetDevice(c->device);
   hipStreamSynchronize(c->stream);
   hipStreamSynchronize(c->copy_stream);
@@ -1001,7 +1115,7 @@ gmoe_status gmoe_layer_register(gmoe_ctx* c, const gmoe_layer_desc* desc, uint32
     return fail(GMOE_ERR_MODEL, "d_ff must be a multiple of 32");
   for (int p = 0; p < 3; p++) L->expert_bytes += (L->p[p].bytes_dev + 255) & ~uint64_t(255);
 
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   HIP_TRY(hipSetDevice(c->device));
   HIP_TRY(hipMalloc(&L->router, (size_t)L->ne * L->d * 4));
   HIP_TRY(hipMemcpy(L->router, D.router, (size_t)L->ne * L->d * 4, hipMemcpyHostToDevice));
@@ -1010,11 +1124,12 @@ gmoe_status gmoe_layer_register(gmoe_ctx* c, const gmoe_layer_desc* desc, uint32
   HIP_TRY(hipMemcpy(L->eptr, L->eptr_host.data(), 3 * L->ne * sizeof(void*), hipMemcpyHostToDevice));
   L->slot.assign(L->ne, -1);
   L->lru_pos.resize(L->ne);
+  L->pending.assign(L->ne, kAbsent);
   uint32_t id = (uint32_t)c->layers.size();
   c->layers.push_back(std::move(L));
   Layer& LL = *c->layers.back();
   for (uint32_t e = 0; e < LL.ne; e++) {
-    gmoe_status s = make_resident(c, id, e, false, nullptr);
+    gmoe_status s = make_resident(c, g.slab, id, e, false, nullptr);
     if (s == GMOE_ERR_CACHE) break;  // the rest stays on the host tier
     if (s) return s;
   }
@@ -1024,10 +1139,20 @@ gmoe_status gmoe_layer_register(gmoe_ctx* c, const gmoe_layer_desc* desc, uint32
 
 gmoe_status gmoe_layer_release(gmoe_ctx* c, uint32_t id) {
   if (gmoe_status s = check_ctx(c)) return s;
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   Layer* L;
   if (gmoe_status s = get_layer(c, id, &L)) return s;
   HIP_TRY(hipSetDevice(c->device));
+  // its queued experts leave the staging queue; the one being staged is waited for
+  c->queue.erase(std::remove_if(c->queue.begin(), c->queue.end(), [&](const auto& q) { return q.first == id; }),
+                 c->queue.end());
+  for (uint32_t e = 0; e < L->ne; e++)
+    if (L->pending[e] == kQueued) L->pending[e] = kAbsent;
+  c->cv.wait(g.slab, [&] {
+    for (uint32_t e = 0; e < L->ne; e++)
+      if (L->pending[e] == kStaging) return false;
+    return true;
+  });
   for (uint32_t e = 0; e < L->ne; e++)
     if (gmoe_status s = evict(c, id, e)) return s;
   hipFree(L->router);
@@ -1054,7 +1179,7 @@ gmoe_status gmoe_ffn_forward_async(gmoe_ctx* c, uint32_t lid, const float* d_hs,
   if (gmoe_status s = check_ctx(c)) return s;
   if (!d_hs || !d_out) return fail(GMOE_ERR_INFERENCE, "null activation pointer");
   if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   Layer* L;
   if (gmoe_status s = get_layer(c, lid, &L)) return s;
   for (uint32_t e = 0; e < L->ne; e++)
@@ -1084,7 +1209,7 @@ gmoe_status gmoe_ffn_forward_noalloc(gmoe_ctx* c, uint32_t lid, const float* d_h
   if (gmoe_status s = check_ctx(c)) return s;
   if (!d_hs || !d_out) return fail(GMOE_ERR_INFERENCE, "null activation pointer");
   if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   Layer* L;
   if (gmoe_status s = get_layer(c, lid, &L)) return s;
   for (uint32_t e = 0; e < L->ne; e++)
@@ -1116,18 +1241,18 @@ gmoe_status gmoe_ffn_forward_noalloc(gmoe_ctx* c, uint32_t lid, const float* d_h
 
 gmoe_status gmoe_expert_prefetch(gmoe_ctx* c, uint32_t lid, uint32_t e) {
   if (gmoe_status s = check_ctx(c)) return s;
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   Layer* L;
   if (gmoe_status s = get_layer(c, lid, &L)) return s;
   if (e >= L->ne) return fail(GMOE_ERR_INFERENCE, "expert %u out of range", e);
   HIP_TRY(hipSetDevice(c->device));
   std::vector<std::pair<uint32_t, uint32_t>> keep{{lid, e}};
-  return make_resident(c, lid, e, true, &keep);
+  return make_resident(c, g.slab, lid, e, true, &keep);
 }
 
 int gmoe_expert_is_resident(gmoe_ctx* c, uint32_t lid, uint32_t e) {
   if (!c) return 0;
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   if (lid >= c->layers.size() || !c->layers[lid] || !c->layers[lid]->alive) return 0;
   Layer& L = *c->layers[lid];
   return e < L.ne && L.slot[e] >= 0;
@@ -1135,18 +1260,49 @@ int gmoe_expert_is_resident(gmoe_ctx* c, uint32_t lid, uint32_t e) {
 
 gmoe_status gmoe_expert_evict(gmoe_ctx* c, uint32_t lid, uint32_t e) {
   if (gmoe_status s = check_ctx(c)) return s;
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   Layer* L;
   if (gmoe_status s = get_layer(c, lid, &L)) return s;
   if (e >= L->ne) return fail(GMOE_ERR_INFERENCE, "expert %u out of range", e);
   HIP_TRY(hipSetDevice(c->device));
+  c->cv.wait(g.slab, [&] { return L->pending[e] != kStaging; });
+  if (L->pending[e] == kQueued) {
+    c->queue.erase(std::remove(c->queue.begin(), c->queue.end(), std::make_pair(lid, e)), c->queue.end());
+    L->pending[e] = kAbsent;
+  }
   return evict(c, lid, e);
+}
+
+int gmoe_expert_state(gmoe_ctx* c, uint32_t lid, uint32_t e) {
+  if (!c) return GMOE_EXPERT_ABSENT;
+  CtxLock g(c);
+  if (lid >= c->layers.size() || !c->layers[lid] || !c->layers[lid]->alive) return GMOE_EXPERT_ABSENT;
+  Layer& L = *c->layers[lid];
+  if (e >= L.ne) return GMOE_EXPERT_ABSENT;
+  if (L.slot[e] >= 0) return GMOE_EXPERT_RESIDENT;
+  return L.pending[e] == kQueued ? GMOE_EXPERT_QUEUED : L.pending[e] == kStaging ? GMOE_EXPERT_STAGING
+                                                                                    : GMOE_EXPERT_ABSENT;
+}
+
+gmoe_status gmoe_prefetch_hold(gmoe_ctx* c, int hold) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  CtxLock g(c);
+  c->hold = hold != 0;
+  c->cv.notify_all();
+  return GMOE_OK;
+}
+
+gmoe_status gmoe_prefetch_wait(gmoe_ctx* c) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  CtxLock g(c);
+  c->cv.wait(g.slab, [&] { return c->staging == 0 && (c->hold || c->queue.empty()); });
+  return GMOE_OK;
 }
 
 gmoe_status gmoe_slab_get_stats(gmoe_ctx* c, gmoe_slab_stats* out) {
   if (gmoe_status s = check_ctx(c)) return s;
   if (!out) return fail(GMOE_ERR_INFERENCE, "null output");
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   *out = c->stats;
   return GMOE_OK;
 }
@@ -1161,7 +1317,7 @@ gmoe_status gmoe_dense_register(gmoe_ctx* c, const gmoe_dense_desc* desc, uint32
   uint64_t rb;
   if (gmoe_status s = byte_size(desc->qtype, desc->cols, &rb)) return s;
   if (!k_ok(desc->qtype, desc->cols)) return fail(GMOE_ERR_MODEL, "dense width %u is not a multiple of 32", desc->cols);
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   HIP_TRY(hipSetDevice(c->device));
   auto W = std::make_unique<Dense>();
   W->qtype = desc->qtype;
@@ -1179,9 +1335,13 @@ gmoe_status gmoe_dense_register(gmoe_ctx* c, const gmoe_dense_desc* desc, uint32
   P.cols = W->cols;
   P.row_bytes = rb;
   P.bytes_dev = W->tiled_bytes;
-  gmoe_status s = stage_proj(c, P, static_cast<const uint8_t*>(desc->data), W->tiled);
-  if (s == GMOE_OK && hipStreamSynchronize(c->copy_stream) != hipSuccess)
-    s = fail(GMOE_ERR_DEVICE, "staging the dense weight failed");
+  gmoe_status s;
+  {
+    std::lock_guard<std::mutex> sg(c->stage_mu);  // the pinned halves and the copy stream
+    s = stage_proj(c, P, static_cast<const uint8_t*>(desc->data), W->tiled);
+    if (s == GMOE_OK && hipStreamSynchronize(c->copy_stream) != hipSuccess)
+      s = fail(GMOE_ERR_DEVICE, "staging the dense weight failed");
+  }
   if (s != GMOE_OK) {
     hipStreamSynchronize(c->copy_stream);
     hipFree(W->tiled);
@@ -1195,7 +1355,7 @@ gmoe_status gmoe_dense_register(gmoe_ctx* c, const gmoe_dense_desc* desc, uint32
 
 gmoe_status gmoe_dense_release(gmoe_ctx* c, uint32_t id) {
   if (gmoe_status s = check_ctx(c)) return s;
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   Dense* W;
   if (gmoe_status s = get_dense(c, id, &W)) return s;
   HIP_TRY(hipSetDevice(c->device));
@@ -1212,7 +1372,7 @@ gmoe_status gmoe_dense_forward(gmoe_ctx* c, uint32_t id, const float* xs, uint32
   if (gmoe_status s = check_ctx(c)) return s;
   if (!xs || !out) return fail(GMOE_ERR_INFERENCE, "null activation pointer");
   if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   Dense* W;
   if (gmoe_status s = get_dense(c, id, &W)) return s;
   HIP_TRY(hipSetDevice(c->device));
@@ -1238,7 +1398,7 @@ gmoe_status gmoe_dense_forward_async(gmoe_ctx* c, uint32_t id, const float* d_xs
   if (gmoe_status s = check_ctx(c)) return s;
   if (!d_xs || !d_out) return fail(GMOE_ERR_INFERENCE, "null activation pointer");
   if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   Dense* W;
   if (gmoe_status s = get_dense(c, id, &W)) return s;
   HIP_TRY(hipSetDevice(c->device));
@@ -1264,28 +1424,31 @@ gmoe_status gmoe_prefetch_step(gmoe_ctx* c, gmoe_predictor* p, uint32_t lid, uin
     if (gmoe_status s = gmoe_predictor_observe(p, prev, nprev, used, nused)) return s;
   if (gmoe_status s = gmoe_predictor_predict(p, used, nused, depth, pred, npred)) return s;
   uint32_t nl = 0, ns = 0;
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   Layer* L;
   if (gmoe_status s = get_layer(c, lid, &L)) return s;
   HIP_TRY(hipSetDevice(c->device));
   // the experts this step used and the ones predicted stay; others may be evicted
-  std::vector<std::pair<uint32_t, uint32_t>> keep;
+  Keep keep;
   for (uint32_t i = 0; i < nused; i++)
     if (used[i] >= base && used[i] - base < L->ne) keep.emplace_back(lid, used[i] - base);
   for (uint32_t i = 0; i < *npred; i++)
     if (pred[i] >= base && pred[i] - base < L->ne) keep.emplace_back(lid, pred[i] - base);
+  c->prefetch_keep = keep;
+  // PrefetchEngine::warm: an expert already resident, queued or being staged is skipped;
+  // the others are queued for the staging thread, and the call returns at once
   for (uint32_t i = 0; i < *npred; i++) {
     if (pred[i] < base || pred[i] - base >= L->ne) continue;  // another layer's expert
     const uint32_t e = pred[i] - base;
-    if (L->slot[e] >= 0) {
+    if (L->slot[e] >= 0 || L->pending[e] != kAbsent) {
       ns++;
       continue;
     }
-    gmoe_status s = make_resident(c, lid, e, true, &keep);
-    if (s == GMOE_ERR_CACHE) break;  // a prefetch that does not fit is dropped; the forward loads what it needs
-    if (s) return s;
+    L->pending[e] = kQueued;
+    c->queue.emplace_back(lid, e);
     nl++;
   }
+  if (nl) c->cv.notify_all();
   if (launched) *launched = nl;
   if (skipped) *skipped = ns;
   return GMOE_OK;
@@ -1302,7 +1465,7 @@ gmoe_status gmoe_dequant(gmoe_ctx* c, uint32_t qt, const void* blocks, uint64_t 
   if ((qt == F32 || qt == F16) && n % 32)
     return fail(GMOE_ERR_MODEL, "%s dequant on the device takes multiples of 32 values", type_name(qt));
   if (n == 0) return GMOE_OK;
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   HIP_TRY(hipSetDevice(c->device));
   uint8_t* db = nullptr;
   float* dout = nullptr;
@@ -1328,7 +1491,7 @@ gmoe_status gmoe_dequant(gmoe_ctx* c, uint32_t qt, const void* blocks, uint64_t 
 gmoe_status gmoe_expf(gmoe_ctx* c, const float* x, uint64_t n, float* y) {
   if (gmoe_status s = check_ctx(c)) return s;
   if (n == 0) return GMOE_OK;
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   HIP_TRY(hipSetDevice(c->device));
   float *dx = nullptr, *dy = nullptr;
   HIP_TRY(hipMalloc(&dx, n * 4));
@@ -1356,7 +1519,7 @@ gmoe_status gmoe_matmul(gmoe_ctx* c, uint32_t qt, uint32_t math, const void* w, 
                 (unsigned long long)nbytes, (unsigned long long)(rb * rows), rows, (unsigned long long)rb);
   if (!k_ok(qt, cols)) return fail(GMOE_ERR_MODEL, "matmul width must be a multiple of 32");
   if (n == 0 || rows == 0) return fail(GMOE_ERR_INFERENCE, "matmul dimension mismatch");
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   HIP_TRY(hipSetDevice(c->device));
   Unit un;
   unit_of(qt, &un);
@@ -1414,7 +1577,7 @@ gmoe_status gmoe_route(gmoe_ctx* c, uint32_t gating, const float* router, const 
   if (k == 0 || k > ne || k > 32) return fail(GMOE_ERR_CONFIG, "top_k (%u) must be in 1..=%u", k, ne);
   if (n == 0 || !x || !ids || !w) return fail(GMOE_ERR_INFERENCE, "bad route arguments");
   if (router && d % 4) return fail(GMOE_ERR_INFERENCE, "router width must be a multiple of 4");
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   HIP_TRY(hipSetDevice(c->device));
   ScratchPlan P;
   size_t xlen = router ? (size_t)n * d : (size_t)n * ne;
@@ -1451,7 +1614,7 @@ gmoe_status gmoe_dispatch(gmoe_ctx* c, const uint32_t* ids, const float* w, uint
   if (ne > kMaxExperts) return fail(GMOE_ERR_CONFIG, "n_experts (%u) above %u is not supported", ne, kMaxExperts);
   for (uint64_t i = 0; i < (uint64_t)n * k; i++)
     if (ids[i] >= ne) return fail(GMOE_ERR_INFERENCE, "expert id %u out of range", ids[i]);
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   HIP_TRY(hipSetDevice(c->device));
   size_t nk = (size_t)n * k;
   ScratchPlan P;
@@ -1485,7 +1648,7 @@ gmoe_status gmoe_dispatch(gmoe_ctx* c, const uint32_t* ids, const float* w, uint
 
 gmoe_status gmoe_set_kernel_timing(gmoe_ctx* c, int on) {
   if (gmoe_status s = check_ctx(c)) return s;
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   c->timing = on != 0;
   return GMOE_OK;
 }
@@ -1494,7 +1657,7 @@ gmoe_status gmoe_set_kernel_timing(gmoe_ctx* c, int on) {
 gmoe_status gmoe_kernel_time(gmoe_ctx* c, uint32_t which, double* total_ms, uint64_t* count) {
   if (gmoe_status s = check_ctx(c)) return s;
   if (which > 2 || !total_ms || !count) return fail(GMOE_ERR_INFERENCE, "bad kernel_time arguments");
-  std::lock_guard<std::mutex> g(c->mu);
+  CtxLock g(c);
   HIP_TRY(hipSetDevice(c->device));
   for (auto& t : c->pending) {
     HIP_TRY(hipEventSynchronize(t.c));

@@ -30,6 +30,7 @@ GATING_LLAMA, GATING_MIXTRAL, GATING_DEEPSEEK, GATING_QWEN = 0, 1, 2, 3
 COMBINE_EXPERT_ORDER, COMBINE_RANK_ORDER = 0, 1
 MATH_PACKED, MATH_F32 = 0, 1
 LAYOUT_STACKED, LAYOUT_SPLIT = 0, 1
+EXPERT_ABSENT, EXPERT_QUEUED, EXPERT_STAGING, EXPERT_RESIDENT = 0, 1, 2, 3
 
 
 class GarudaError(Exception):
@@ -237,6 +238,14 @@ class Device:
         _check(lib().gmoe_slab_get_stats(self._h, C.byref(s)))
         return SlabStats(s.hits, s.misses, s.evictions, s.entries, s.bytes, s.capacity, s.h2d_bytes)
 
+    def prefetch_hold(self, hold: bool) -> None:
+        """gmoe_prefetch_hold: the staging thread starts nothing new while held."""
+        _check(lib().gmoe_prefetch_hold(self._h, 1 if hold else 0))
+
+    def prefetch_wait(self) -> None:
+        """gmoe_prefetch_wait: until the staging thread is idle."""
+        _check(lib().gmoe_prefetch_wait(self._h))
+
     def set_kernel_timing(self, on: bool) -> None:
         _check(lib().gmoe_set_kernel_timing(self._h, 1 if on else 0))
 
@@ -341,6 +350,10 @@ class MoeLayer:
 
     def is_resident(self, e: int) -> bool:
         return bool(lib().gmoe_expert_is_resident(self.dev.handle, self.id, e))
+
+    def state(self, e: int) -> int:
+        """gmoe_expert_state: EXPERT_ABSENT, EXPERT_QUEUED, EXPERT_STAGING or EXPERT_RESIDENT."""
+        return int(lib().gmoe_expert_state(self.dev.handle, self.id, e))
 
     def evict(self, e: int) -> None:
         _check(lib().gmoe_expert_evict(self.dev.handle, self.id, e))

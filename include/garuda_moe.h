@@ -152,10 +152,27 @@ gmoe_status gmoe_ffn_forward_noalloc(gmoe_ctx* ctx, uint32_t layer_id, const flo
                                      uint32_t* d_routed_ids, float* d_routed_w, void* stream);
 
 /* ---- the L1 tier (core::ExpertLoader, core/mod.rs:215-223) ---- */
+/* ExpertLoader::prefetch: stage the expert now (returns when it is resident). */
 gmoe_status gmoe_expert_prefetch(gmoe_ctx* ctx, uint32_t layer_id, uint32_t expert);
 int gmoe_expert_is_resident(gmoe_ctx* ctx, uint32_t layer_id, uint32_t expert);
+/* ExpertLoader::unload: an expert queued for staging leaves the queue; one being staged
+ * is waited for, then evicted. */
 gmoe_status gmoe_expert_evict(gmoe_ctx* ctx, uint32_t layer_id, uint32_t expert);
 gmoe_status gmoe_slab_get_stats(gmoe_ctx* ctx, gmoe_slab_stats* out);
+
+/* Where an expert is on its way into the slab: gmoe_prefetch_step queues experts for the
+ * context's staging thread, which stages them one at a time (PrefetchEngine::warm's
+ * in-flight set and pool, prefetch/mod.rs:102-127). A forward that routes to a queued
+ * expert takes it off the queue and stages it itself; one that routes to an expert being
+ * staged waits for it. */
+enum { GMOE_EXPERT_ABSENT = 0, GMOE_EXPERT_QUEUED = 1, GMOE_EXPERT_STAGING = 2, GMOE_EXPERT_RESIDENT = 3 };
+int gmoe_expert_state(gmoe_ctx* ctx, uint32_t layer_id, uint32_t expert);
+/* hold != 0: the staging thread starts no new expert (the one it is copying finishes);
+ * queued experts stay queued until hold is lifted or a forward takes them. */
+gmoe_status gmoe_prefetch_hold(gmoe_ctx* ctx, int hold);
+/* Returns once the staging thread is idle: nothing being staged and, unless held, nothing
+ * queued. */
+gmoe_status gmoe_prefetch_wait(gmoe_ctx* ctx);
 
 /* ---- dense projections (Weight::matmul_rows, llama/mod.rs:148-195) ----
  *
@@ -372,10 +389,12 @@ gmoe_status gmoe_predictor_set_counts(gmoe_predictor* p, const uint32_t* counts,
  * experts are ids [id_base, id_base + n_experts) of the predictor. It scores last step's
  * prediction against `used`, learns previous -> used, predicts up to `depth` ids into
  * `predicted` (*n_predicted receives the count) and stages the predicted experts of this
- * layer that are not resident into the slab. *launched and *skipped (may be NULL) count
- * the staged and the already-resident ones. Staging is host copy work: call this after
- * queuing the step's gmoe_ffn_forward_async, and it overlaps that step's device work.
- * Evicting an expert to make room waits for all queued device work first. */
+ * layer that are neither resident nor already on their way into the slab for the
+ * context's staging thread, and returns without waiting for them (gmoe_expert_state,
+ * gmoe_prefetch_wait). *launched and *skipped (may be NULL) count the queued and the
+ * skipped ones. The staging thread makes room by evicting least recently used experts
+ * other than this step's used and predicted ones, after the evicted layer's last queued
+ * call has finished. */
 gmoe_status gmoe_prefetch_step(gmoe_ctx* ctx, gmoe_predictor* p, uint32_t layer_id, uint32_t id_base,
                                const uint32_t* previous, uint32_t n_previous, const uint32_t* used,
                                uint32_t n_used, const uint32_t* predicted_last, uint32_t n_predicted_last,
