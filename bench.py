@@ -45,6 +45,35 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def cpu_median(fn, calls=10, budget_s=20.0):
+    """fn() once as a warm-up (not counted), then at least `calls` timed calls, or as many as
+    fit `budget_s` but at least three; returns (median seconds, calls timed)."""
+    import statistics
+    fn()
+    ts, t_end = [], time.time() + budget_s
+    while len(ts) < calls and (len(ts) < 3 or time.time() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), len(ts)
+
+
+def cpu_record(value, unit, threads, sample):
+    return {"value": value, "unit": unit, "cores": threads, "cpu": cpu_model(), "kind": "port", "sample": sample}
+
+
 def make_experts(threads):
     import garuda_amd as G
     from garuda_amd import moe as M
@@ -89,7 +118,7 @@ EXTRA_CONFIGS = {
 }
 
 
-def extra_leg(name, a, dev, threads, stream, timed):
+def extra_leg(name, a, dev, threads, stream, timed, cpu):
     """One decode leg of a further BASELINE configuration: tokens/s and the layer's HBM rate
     (touched experts' packed bytes + router + activations per call over the call time)."""
     import torch
@@ -109,7 +138,7 @@ def extra_leg(name, a, dev, threads, stream, timed):
         router = M.fill_gaussian(seed + 0x10 + l, ne * d, 0.0, 0.02, threads)
         layers.append(G.MoeLayer(dev, d, f, ne, k, router, mats["gate"], mats["up"], mats["down"], qts,
                                  math=G.MATH_PACKED))
-    del mats
+    keep = mats if cpu else {}
     hs = torch.from_numpy(M.fill_gaussian(seed + 0x20, n * d, 0.0, 1.0, threads).reshape(n, d)).cuda()
     lg = None
     if c["logits_scale"] is not None:
@@ -135,14 +164,25 @@ def extra_leg(name, a, dev, threads, stream, timed):
     nbytes = touched * expert_bytes + (0 if lg is not None else ne * d * 4) + 2 * n * d * 4
     log(f"{name}: {n / step_s:.0f} tok/s, {step_s * 1e6:.1f} us/call, {touched:.1f} experts touched, "
         f"{nbytes / step_s / 1e9:.0f} GB/s")
+    res = {"workload": c["workload"], "tokens_per_s": n / step_s, "us_per_call": step_s * 1e6,
+           "experts_touched": touched, "layer_bytes": nbytes, "layer_GBs": nbytes / step_s / 1e9,
+           "hbm_frac": nbytes / step_s / 1e9 / HBM_PEAK_GBS, "math": "packed", "steps": steps, "cpu_baseline": None}
+    if cpu:
+        from oracle import oracle as O  # the checker's restatement, timed as the CPU path
+        L = dict(d=d, f=f, ne=ne, k=k, packed=1, router=layers[0].router, qtypes=qts, **keep)
+        hs_np = hs.cpu().numpy()
+        lg_np = lg.cpu().numpy() if lg is not None else None
+        med, calls = cpu_median(lambda: O.feed_forward_batch(L, hs_np, lg_np, threads=threads))
+        res["cpu_baseline"] = cpu_record(n / med, "tokens/s", threads,
+                                         f"median of {calls} calls (one warm-up call before) of this layer at batch "
+                                         f"{n}, oracle restatement of the packed int8 path, {threads} threads")
+        log(f"{name} cpu: {n / med:.1f} tok/s")
     for l in layers:
         l.release()
-    return {"workload": c["workload"], "tokens_per_s": n / step_s, "us_per_call": step_s * 1e6,
-            "experts_touched": touched, "layer_bytes": nbytes, "layer_GBs": nbytes / step_s / 1e9,
-            "hbm_frac": nbytes / step_s / 1e9 / HBM_PEAK_GBS, "math": "packed", "steps": steps}
+    return res
 
 
-def prefill_leg(a, dev, mats, threads, stream, timed):
+def prefill_leg(a, dev, mats, threads, stream, timed, cpu):
     """the same Q4_K layer at a prefill of `a.prefill_tokens` tokens,
     routing skewed to Zipf(1.1) expert loads through one shared activation direction, f32
     math (the expert products on MFMA). Returns the JSON object of the leg."""
@@ -181,9 +221,27 @@ def prefill_leg(a, dev, mats, threads, stream, timed):
     log(f"prefill n={n}: {n / step_s:.0f} tok/s, {step_s * 1e6:.0f} us/call, gate/up {gu_ms * 1e3:.0f} us, "
         f"down {dn_ms * 1e3:.0f} us, {tflops:.0f} TFLOP/s algorithmic ({tflops / MFMA_PEAK_TFLOPS:.1%} of peak), "
         f"loads {loads[0].tolist()}")
+    cpu_rec = None
+    if cpu:
+        # Weight::Full (llama/mod.rs:170-173): the experts expanded to f32 once, as the
+        # reference does at load, then simd::matmul over a sample of the same tokens
+        from oracle import oracle as O  # the checker's restatement, timed as the CPU path
+        sample = max(1, a.prefill_cpu_tokens)
+        pick = np.linspace(0, n - 1, sample).astype(np.int64)
+        full = {f"{nm}_f32": O.dequantize(G.Q4_K, mats[nm], mats[nm].size // 144 * 256, checked=False)
+                for nm in ("gate", "up", "down")}
+        L = dict(d=D, f=F, ne=NE, k=K, packed=0, router=layers[0].router, qtypes=(G.Q4_K,) * 3, **mats, **full)
+        med, calls = cpu_median(lambda: O.feed_forward_batch(L, hs_np[pick], threads=threads), calls=5)
+        del full, L
+        cpu_rec = cpu_record(sample / med, "tokens/s", threads,
+                             f"median of {calls} calls (one warm-up call before) on {sample} of the {n} skewed "
+                             f"tokens, oracle restatement of the f32 Weight::Full path (simd::matmul over the "
+                             f"dequantised experts), {threads} threads")
+        log(f"prefill cpu (f32 Full path): {sample / med:.1f} tok/s")
     for l in layers:
         l.release()
     return {
+        "cpu_baseline": cpu_rec,
         "workload": f"C3 prefill: the C2 layer at {n} tokens, Zipf(1.1)-skewed routing, f32 math, "
                     f"{len(layers)} HBM copies rotated",
         "tokens_per_s": n / step_s, "ms_per_call": step_s * 1e3, "steps": a.prefill_steps,
@@ -355,8 +413,9 @@ def e2e_leg(a, threads, cpu):
     sequence is fed a 128-token prompt one token per step, then decodes greedily while
     the steps are timed (each step returns its tokens to the host). The layers cycle over
     8 HBM copies of one synthetic layer, so every layer's weights come from HBM, not the
-    MALL. With `cpu`, one batch-8 step of the same model at context 1 runs through the
-    oracle's restatement on the host threads."""
+    MALL. With `cpu`, one batch-8 step of the same model at the middle of the GPU's timed
+    contexts (each cache filled with random keys and values to that length) runs through
+    the oracle's restatement on the host threads."""
     import garuda_amd as G
     from garuda_amd import moe as M
     from garuda_amd.attention import KvCache
@@ -428,14 +487,24 @@ def e2e_leg(a, threads, cpu):
                        moe=dict(d=d, f=f, ne=ne, k=k, router=routers[c], qtypes=(O.Q3_K, O.Q3_K, O.Q4_K), packed=1,
                                 gate=ex["gate"], up=ex["up"], down=ex["down"]))
                   for c in pick]
+        ctx = prompt + steps // 2  # the middle of the GPU's timed steps
         orc = ModelOracle(layers, (O.Q6_K, head_raw, vocab, d), norms[-1], table, nh, nkv, hd,
-                          max_positions=8, rope_theta=1e6, threads=threads)
+                          max_positions=ctx + 2, rope_theta=1e6, threads=threads)
+        # every sequence's cache holds ctx positions (random keys and values: only the
+        # step's cost is measured), so the step attends over as many as the GPU's do
+        kr = np.random.default_rng(SEED & 0xFFFF)
+        for sq in range(nseq):
+            for l in range(nl):
+                K_, V_ = orc.kv._kv(sq, l)
+                K_.extend(kr.normal(0, 1, (ctx, nkv * hd)).astype(np.float32))
+                V_.extend(kr.normal(0, 1, (ctx, nkv * hd)).astype(np.float32))
         t0 = time.time()
         orc.decode_step(list(range(nseq)), toks[:, 0])
         wall = time.time() - t0
-        res["cpu"] = {"value": nseq / wall, "unit": "tokens/s", "cores": threads, "kind": "port",
-                      "sample": f"one batch-{nseq} decode step of the {nl}-layer model at context 1, oracle "
-                                f"restatement of logits_batch (packed int8 products), {threads} threads, {wall:.1f}s"}
+        res["cpu"] = cpu_record(nseq / wall, "tokens/s", threads,
+                                f"one batch-{nseq} decode step of the {nl}-layer model at context {ctx + 1} (the "
+                                f"middle of the GPU's timed steps), oracle restatement of logits_batch (packed int8 "
+                                f"products), {threads} threads, {wall:.1f}s")
         log(f"c5 end to end on the CPU: {nseq / wall:.2f} tok/s on {threads} threads")
     return res
 
@@ -567,7 +636,7 @@ def main():
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--math", choices=("packed", "f32"), default="packed")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=1.5, help="wall-clock budget of the CPU sample")
+    ap.add_argument("--cpu-calls", type=int, default=10, help="timed calls of the CPU baseline (median)")
     ap.add_argument("--kernel-events", choices=("on", "off"), default="on",
                     help="also time the steps with HIP events around every gate/up and down launch "
                          "(the roofline's kernel times); off skips that second pass")
@@ -576,6 +645,8 @@ def main():
     ap.add_argument("--prefill-tokens", type=int, default=512,
                     help="tokens of the C3 prefill leg (Zipf-skewed routing, f32 math on MFMA); 0 skips it")
     ap.add_argument("--prefill-steps", type=int, default=40)
+    ap.add_argument("--prefill-cpu-tokens", type=int, default=32,
+                    help="tokens of the C3 CPU sample (the f32 path runs about 30 ms a token on 16 threads)")
     ap.add_argument("--prefill-layers", type=int, default=2)
     ap.add_argument("--dense", type=int, default=1, help="run the dense-projection leg (0: skip)")
     ap.add_argument("--attention", type=int, default=1, help="run the paged-attention leg (0: skip)")
@@ -684,10 +755,10 @@ def main():
 
     prefill = None
     if a.prefill_tokens:
-        prefill = prefill_leg(a, dev, mats, threads, stream, timed)
+        prefill = prefill_leg(a, dev, mats, threads, stream, timed, not a.no_cpu)
     extra = {}
     for name in [x for x in a.extra.split(",") if x]:
-        extra[name] = extra_leg(name, a, dev, threads, stream, timed)
+        extra[name] = extra_leg(name, a, dev, threads, stream, timed, not a.no_cpu)
 
     dense = dense_leg(a, dev, threads, stream, timed) if a.dense else None
     prefetch = prefetch_leg(a, mats, threads) if a.prefetch_steps > 0 else None
@@ -712,16 +783,11 @@ def main():
         hs_np = M.fill_gaussian(SEED + 0x200 + n, n * D, 0.0, 1.0, threads).reshape(n, D)
         L = dict(d=D, f=F, ne=NE, k=K, packed=1 if math == G.MATH_PACKED else 0,
                  router=layers[0].router, qtypes=(G.Q4_K,) * 3, **mats)
-        reps, t0 = 0, time.time()
-        while True:
-            O.feed_forward_batch(L, hs_np, threads=threads)
-            reps += 1
-            if time.time() - t0 >= a.cpu_seconds:
-                break
-        wall = time.time() - t0
-        cpu = {"value": n * reps / wall, "unit": "tokens/s", "cores": threads, "kind": "port",
-               "sample": f"{reps} calls of the C2 layer at batch {n} (layer 0), oracle restatement of "
-                         f"quant::matmul's packed int8 path, rows split over {threads} threads, {wall:.1f}s wall"}
+        med, calls = cpu_median(lambda: O.feed_forward_batch(L, hs_np, threads=threads), calls=a.cpu_calls)
+        cpu = cpu_record(n / med, "tokens/s", threads,
+                         f"median of {calls} calls (one warm-up call before) of the C2 layer at batch {n} "
+                         f"(layer 0), oracle restatement of quant::matmul's packed int8 path, rows split over "
+                         f"{threads} threads")
         log(f"cpu baseline: {cpu['value']:.1f} tok/s on {threads} threads")
 
     r = results[a.batch]
