@@ -182,21 +182,24 @@ def extra_leg(name, a, dev, threads, stream, timed, cpu):
     return res
 
 
-def prefill_leg(a, dev, mats, threads, stream, timed, cpu):
+def prefill_leg(a, dev, mats, threads, stream, timed, cpu, packed=False):
     """the same Q4_K layer at a prefill of `a.prefill_tokens` tokens,
-    routing skewed to Zipf(1.1) expert loads through one shared activation direction, f32
-    math (the expert products on MFMA). Returns the JSON object of the leg."""
+    routing skewed to Zipf(1.1) expert loads through one shared activation direction.
+    f32 math (Weight::Full) runs k_pf, packed math (Weight::Packed, mmap = true) k_pq;
+    both on MFMA. Returns the JSON object of the leg."""
     import torch
     import garuda_amd as G
     from garuda_amd import moe as M
 
+    math = G.MATH_PACKED if packed else G.MATH_F32
+    mname = "packed" if packed else "f32"
     n = a.prefill_tokens
     u = M.skew_direction(SEED + 0x300, D)
     layers = []
     for l in range(a.prefill_layers):
         router = M.skew_router(M.fill_gaussian(SEED + 0x100 + l, NE * D, 0.0, 0.02, threads), NE, D, u)
         layers.append(G.MoeLayer(dev, D, F, NE, K, router, mats["gate"], mats["up"], mats["down"],
-                                 (G.Q4_K,) * 3, math=G.MATH_F32))
+                                 (G.Q4_K,) * 3, math=math))
     hs_np = M.skew_tokens(M.fill_gaussian(SEED + 0x400, n * D, 0.0, 1.0, threads).reshape(n, D), u)
     hs = torch.from_numpy(hs_np).cuda()
     out = torch.empty((n, D), dtype=torch.float32, device="cuda")
@@ -218,11 +221,22 @@ def prefill_leg(a, dev, mats, threads, stream, timed, cpu):
     ex_s = (gu_ms + dn_ms) / 1e3
     step_s = ms / a.prefill_steps / 1e3
     tflops = flops / ex_s / 1e12
-    log(f"prefill n={n}: {n / step_s:.0f} tok/s, {step_s * 1e6:.0f} us/call, gate/up {gu_ms * 1e3:.0f} us, "
+    log(f"prefill ({mname}) n={n}: {n / step_s:.0f} tok/s, {step_s * 1e6:.0f} us/call, gate/up {gu_ms * 1e3:.0f} us, "
         f"down {dn_ms * 1e3:.0f} us, {tflops:.0f} TFLOP/s algorithmic ({tflops / MFMA_PEAK_TFLOPS:.1%} of peak), "
         f"loads {loads[0].tolist()}")
     cpu_rec = None
-    if cpu:
+    if cpu and packed:
+        # Weight::Packed: quant::matmul's int8 path over a sample of the same tokens
+        from oracle import oracle as O  # the checker's restatement, timed as the CPU path
+        sample = max(1, a.prefill_cpu_tokens)
+        pick = np.linspace(0, n - 1, sample).astype(np.int64)
+        L = dict(d=D, f=F, ne=NE, k=K, packed=1, router=layers[0].router, qtypes=(G.Q4_K,) * 3, **mats)
+        med, calls = cpu_median(lambda: O.feed_forward_batch(L, hs_np[pick], threads=threads), calls=5)
+        cpu_rec = cpu_record(sample / med, "tokens/s", threads,
+                             f"median of {calls} calls (one warm-up call before) on {sample} of the {n} skewed "
+                             f"tokens, oracle restatement of quant::matmul's packed int8 path, {threads} threads")
+        log(f"prefill cpu (packed path): {sample / med:.1f} tok/s")
+    elif cpu:
         # Weight::Full (llama/mod.rs:170-173): the experts expanded to f32 once, as the
         # reference does at load, then simd::matmul over a sample of the same tokens
         from oracle import oracle as O  # the checker's restatement, timed as the CPU path
@@ -240,18 +254,22 @@ def prefill_leg(a, dev, mats, threads, stream, timed, cpu):
         log(f"prefill cpu (f32 Full path): {sample / med:.1f} tok/s")
     for l in layers:
         l.release()
+    kname = "k_pq" if packed else "k_pf"
+    note = ("algorithmic flops (sum of expert tokens x 6 d f) over the two MFMA launches' time; the reference's "
+            "packed arithmetic adds one float term per 32-value sub-block per (row, token), five VALU operations "
+            "evaluated in K order, which bound the kernel" if packed else
+            "algorithmic flops (sum of expert tokens x 6 d f) over the two MFMA launches' "
+            "time; the exact-product scheme issues two fp16 MFMA passes per product")
     return {
         "cpu_baseline": cpu_rec,
-        "workload": f"C3 prefill: the C2 layer at {n} tokens, Zipf(1.1)-skewed routing, f32 math, "
+        "workload": f"C3 prefill: the C2 layer at {n} tokens, Zipf(1.1)-skewed routing, {mname} math, "
                     f"{len(layers)} HBM copies rotated",
         "tokens_per_s": n / step_s, "ms_per_call": step_s * 1e3, "steps": a.prefill_steps,
         "expert_loads": [int(x) for x in loads[0]],
         "gateup_us": gu_ms * 1e3, "down_us": dn_ms * 1e3,
-        "roofline": {"bound": "mfma", "kernels": "k_pf<Q4_K, gate/up> + k_pf<Q4_K, down>",
+        "roofline": {"bound": "mfma", "kernels": f"{kname}<Q4_K, gate/up> + {kname}<Q4_K, down>",
                      "achieved": tflops, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": tflops / MFMA_PEAK_TFLOPS,
-                     "flops_per_call": flops,
-                     "note": "algorithmic flops (sum of expert tokens x 6 d f) over the two MFMA launches' "
-                             "time; the exact-product scheme issues two fp16 MFMA passes per product"},
+                     "flops_per_call": flops, "note": note},
     }
 
 
@@ -643,7 +661,7 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="also run one device-to-device copy of MB MiB (the counter calibration of profiles/)")
     ap.add_argument("--prefill-tokens", type=int, default=512,
-                    help="tokens of the C3 prefill leg (Zipf-skewed routing, f32 math on MFMA); 0 skips it")
+                    help="tokens of the C3 prefill legs (Zipf-skewed routing, f32 and packed math on MFMA); 0 skips them")
     ap.add_argument("--prefill-steps", type=int, default=40)
     ap.add_argument("--prefill-cpu-tokens", type=int, default=32,
                     help="tokens of the C3 CPU sample (the f32 path runs about 30 ms a token on 16 threads)")
@@ -753,9 +771,10 @@ def main():
             f"E={e_avg:.2f}, gate/up {gu_ms * 1e3:.1f} us ({results[n]['gateup_GBs']:.0f} GB/s), "
             f"down {dn_ms * 1e3:.1f} us ({results[n]['down_GBs']:.0f} GB/s), layer {results[n]['layer_GBs']:.0f} GB/s")
 
-    prefill = None
+    prefill = prefill_packed = None
     if a.prefill_tokens:
         prefill = prefill_leg(a, dev, mats, threads, stream, timed, not a.no_cpu)
+        prefill_packed = prefill_leg(a, dev, mats, threads, stream, timed, not a.no_cpu, packed=True)
     extra = {}
     for name in [x for x in a.extra.split(",") if x]:
         extra[name] = extra_leg(name, a, dev, threads, stream, timed, not a.no_cpu)
@@ -816,6 +835,7 @@ def main():
                      "bytes_per_launch": r["gateup_bytes"], "avg_launch_us": r["gateup_us"]},
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "prefill_packed": prefill_packed,
         "configs": extra,
         "dense_projections": dense,
         "prefetch": prefetch,

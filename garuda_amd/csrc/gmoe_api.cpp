@@ -475,8 +475,12 @@ bool uses_int8(uint32_t math, uint32_t qt);
 size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
   ScratchPlan P;
   const uint64_t nk = (uint64_t)n * L.k, ns = slot_capacity(L, n);
-  const bool h8 = uses_int8(L.math, L.p[2].qtype), pf = prefill_ok(layer_dev(L), n);
-  const uint64_t nk_pf = pf ? nk : 0, ns8 = h8 ? ns : 0, ns32 = h8 ? 0 : ns;
+  const LayerDev D = layer_dev(L);
+  const bool h8 = uses_int8(L.math, L.p[2].qtype), pf = prefill_ok(D, n), pq = !pf && prefill_packed_ok(D, n);
+  // f32 prefill: hi and lo planes; packed prefill: one plane of codes and the transposed
+  // per-token scales and sums (nkp slots a row)
+  const uint64_t nk_pf = pf ? 2 * nk : pq ? nk : 0, ns8 = h8 ? ns : 0, ns32 = h8 ? 0 : ns;
+  const uint64_t nkp = pq ? nk + 64 : 0;
   size_t o_hs = P.add((size_t)n * L.d * 4), o_out = P.add((size_t)n * L.d * 4);
   size_t o_lin = P.add((size_t)n * L.ne * 4);
   size_t o_ids = P.add(nk * 4), o_w = P.add(nk * 4), o_lg = P.add((size_t)n * L.ne * 4);
@@ -488,9 +492,12 @@ size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
   size_t o_hf = P.add(ns32 * L.f * 4), o_y = P.add(kMaxKsg * ns * L.d * 4);
   size_t o_cand = P.add((size_t)n * L.ne * 4);
   size_t o_work = P.add((size_t)L.ne * sizeof(ExpertWork));
-  const uint32_t pcap = pf ? prefill_tiles_cap(n, L.k, L.ne) : 0;
-  size_t o_pt = P.add((size_t)pcap * 4), o_xh = P.add(2 * nk_pf * L.d * 2), o_hh = P.add(2 * nk_pf * L.f * 2);
-  size_t o_xsh = P.add(2 * nk_pf * (L.d / 16) * 2), o_hsh = P.add(2 * nk_pf * (L.f / 16) * 2);
+  const uint32_t pcap = (pf || pq) ? prefill_tiles_cap(n, L.k, L.ne) : 0;
+  size_t o_pt = P.add((size_t)pcap * 4), o_xh = P.add(nk_pf * L.d * 2), o_hh = P.add(nk_pf * L.f * 2);
+  const uint64_t nk_sh = pf ? 2 * nk : 0;
+  size_t o_xsh = P.add(nk_sh * (L.d / 16) * 2), o_hsh = P.add(nk_sh * (L.f / 16) * 2);
+  size_t o_qxs = P.add(nkp * (L.d / 32) * 4), o_qxm = P.add(nkp * (L.d / 16) * 4);
+  size_t o_qhs = P.add(nkp * (L.f / 32) * 4), o_qhm = P.add(nkp * (L.f / 16) * 4);
   if (cv && base) {
     FwdBufs& B = cv->B;
     memset(&B, 0, sizeof B);
@@ -523,6 +530,11 @@ size_t plan_scratch(const Layer& L, uint32_t n, Carved* cv, uint8_t* base) {
     B.hh = (_Float16*)(base + o_hh);
     B.xsh = (_Float16*)(base + o_xsh);
     B.hsh = (_Float16*)(base + o_hsh);
+    B.qxs = (float*)(base + o_qxs);
+    B.qxsum = (float*)(base + o_qxm);
+    B.qhs = (float*)(base + o_qhs);
+    B.qhsum = (float*)(base + o_qhm);
+    B.nkp = (uint32_t)nkp;
   }
   return P.total;
 }
@@ -579,18 +591,20 @@ gmoe_status run_layer(gmoe_ctx* c, Layer& L, FwdBufs B, uint32_t n, hipStream_t 
     B.hf = nullptr;
   }
   const bool quant = uses_int8(L.math, L.p[0].qtype);
-  // prefill-sized f32-math calls run the expert products on MFMA over token tiles
-  const bool pf = prefill_ok(D, n);
-  if (!pf) {
+  // prefill-sized calls run the expert products on MFMA over token tiles: f32 math
+  // (k_pf) or packed math (k_pq)
+  const bool pf = prefill_ok(D, n), pq = !pf && prefill_packed_ok(D, n);
+  if (!pf && !pq) {
     B.ptile = nullptr;
     B.xh = B.xsh = B.hh = B.hsh = nullptr;
   }
+  if (!pq) B.qxs = B.qxsum = B.qhs = B.qhsum = nullptr;
   // decode calls that compute their router logits: the expert products start on the
   // candidate experts, and the exact routing rides along in the gate/up launch. Any
   // expert may be a candidate, so every one must be resident.
   bool resident = true;
   for (uint32_t e = 0; e < L.ne; e++) resident &= L.slot[e] >= 0;
-  const bool spec = !pf && !B.logits_in && resident && spec_ok(D, n);
+  const bool spec = !pf && !pq && !B.logits_in && resident && spec_ok(D, n);
   B.spec = spec ? 1u : 0u;
   if (!spec) B.nslot = n * L.k;
   RouteArgs ra{};
@@ -621,16 +635,17 @@ gmoe_status run_layer(gmoe_ctx* c, Layer& L, FwdBufs B, uint32_t n, hipStream_t 
     if (quant) HIP_TRY(launch_quant_act(B.hs, n, L.d, B.xq, B.xs, B.xsum, L.p[0].qtype, st));
   }
   if (pf) HIP_TRY(launch_gather_f16(D, B, n, st));
-  const uint32_t ksg = pf ? prefill_ksg(D, B) : down_ksg(D, n * L.k);
+  if (pq) HIP_TRY(launch_gather_codes(D, B, n, st));
+  const uint32_t ksg = pf ? prefill_ksg(D, B) : pq ? pq_ksg(D, B) : down_ksg(D, n * L.k);
   Timing tm{};
   timed = timed && c->timing;
   if (timed) {
     tm = take_timing(c);
     HIP_TRY(hipEventRecord(tm.a, st));
   }
-  HIP_TRY(pf ? launch_prefill_gateup(D, B, n, st) : launch_gateup(D, B, n, ra, st));
+  HIP_TRY(pf ? launch_prefill_gateup(D, B, n, st) : pq ? launch_pq_gateup(D, B, n, st) : launch_gateup(D, B, n, ra, st));
   if (timed) HIP_TRY(hipEventRecord(tm.b, st));
-  HIP_TRY(pf ? launch_prefill_down(D, B, n, ksg, st) : launch_down(D, B, n, st));
+  HIP_TRY(pf ? launch_prefill_down(D, B, n, ksg, st) : pq ? launch_pq_down(D, B, n, ksg, st) : launch_down(D, B, n, st));
   if (timed) {
     HIP_TRY(hipEventRecord(tm.c, st));
     c->pending.push_back(tm);

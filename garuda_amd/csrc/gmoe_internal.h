@@ -158,6 +158,13 @@ struct FwdBufs {
   _Float16* xsh;         // [2][n*k][d/16]
   _Float16* hh;          // [2][n*k][f]
   _Float16* hsh;         // [2][n*k][f/16]
+  // packed-math prefill (k_pq): the codes in slot order as fp16 in xh / hh (one plane),
+  // per-token scales and sums transposed to [K/32][nkp] and [K/sum width][nkp]
+  float* qxs;
+  float* qxsum;
+  float* qhs;
+  float* qhsum;
+  uint32_t nkp;          // >= n*k + 64
   int8_t* hq;            // [n*k][f]
   float* hsc;            // [n*k][f/32]
   uint32_t* hsum;        // [n*k][f/sum_width]: sums in the down type's form
@@ -226,6 +233,14 @@ constexpr uint32_t kPfMinSlots = 64;
 __host__ __device__ constexpr uint32_t pf_sum_width(uint32_t qt) {
   return (qt == Q4_K || qt == Q5_K) ? 32u : qt == Q2_K ? 16u : 0u;
 }
+// Packed-math prefill on MFMA (gmoe_prefill.hip): the int8 types only. Activation sums
+// are kept per 32 values (Q4_K, Q5_K) or 16 (Q2_K); the others need none (Q6_K's and
+// Q3_K's MFMA operand carries the quant offset, Q8_0 has no min term).
+__host__ __device__ constexpr uint32_t pq_sum_width(uint32_t qt) {
+  return (qt == Q4_K || qt == Q5_K) ? 32u : qt == Q2_K ? 16u : 0u;
+}
+template <int QT> hipError_t pq_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+template <int QT> hipError_t pq_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
 template <int QT> hipError_t prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 template <int QT> hipError_t prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg,
                                           hipStream_t st);
@@ -264,6 +279,13 @@ hipError_t launch_combine(const LayerDev& L, const FwdBufs& B, uint32_t n, uint3
 // Prefill path: whether it applies (f32 math, at least kPfMinSlots slots, supported
 // types and shapes), the per-slot fp16 gather of the activations, and the products.
 bool prefill_ok(const LayerDev& L, uint32_t n);
+// Packed-math calls with enough tokens per expert run the products on MFMA (k_pq): the
+// activation codes gathered in slot order, then gate/up and down.
+bool prefill_packed_ok(const LayerDev& L, uint32_t n);
+hipError_t launch_gather_codes(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+hipError_t launch_pq_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+hipError_t launch_pq_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
+uint32_t pq_ksg(const LayerDev& L, const FwdBufs& B);
 bool prefill_dense_ok(const LayerDev& L, uint32_t n);
 hipError_t launch_dense_setup(ExpertWork* work, uint32_t* offsets, uint32_t* active, uint32_t* ptile,
                               uint32_t ptile_cap, uint32_t* slot_tok, const uint8_t* w, uint32_t n, hipStream_t st);

@@ -1068,6 +1068,87 @@ hipError_t launch_gather_f16(const LayerDev& L, const FwdBufs& B, uint32_t n, hi
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------
+// Packed-math prefill (k_pq, gmoe_prefill.hip)
+// ---------------------------------------------------------------------------------
+
+static bool pq_type_rt(uint32_t qt) {
+  return qt == Q4_K || qt == Q5_K || qt == Q6_K || qt == Q3_K || qt == Q2_K || qt == Q8_0;
+}
+
+// Tokens per expert from which the MFMA products beat the per-row decode kernels
+// (whose cost grows with every token an expert gets, while a token tile's is fixed).
+constexpr uint32_t kPqMinPerExpert = 16;
+
+bool prefill_packed_ok(const LayerDev& L, uint32_t n) {
+  const uint32_t nk = n * L.k;
+  return L.math == 0 && nk >= kPfMinSlots && nk >= kPqMinPerExpert * L.ne && L.qt_gate == L.qt_up &&
+         pq_type_rt(L.qt_gate) && pq_type_rt(L.qt_down) && L.d % 512 == 0 && L.f % 256 == 0 && L.ne < 65536;
+}
+
+// The int8 activation codes in slot order as fp16, their per-32 scales and their sums
+// (the gate type's width) transposed to [K/w][nkp]. Threads: 64 slots x 4 blocks of 32.
+__global__ void __launch_bounds__(256) k_gather_codes(const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                                      const uint32_t* __restrict__ xsum,
+                                                      const uint32_t* __restrict__ slot_tok, uint32_t d, uint32_t nk,
+                                                      uint32_t nkp, uint32_t sw, _Float16* __restrict__ xh,
+                                                      float* __restrict__ qxs, float* __restrict__ qxsum) {
+  typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+  const uint32_t s = blockIdx.x * 64 + (threadIdx.x & 63), b = blockIdx.y * 4 + (threadIdx.x >> 6), nb = d / 32;
+  if (s >= nk || b >= nb) return;
+  const uint32_t t = slot_tok[s];
+  const uint4* src = reinterpret_cast<const uint4*>(xq + (size_t)t * d + 32 * b);
+  const uint4 q[2] = {src[0], src[1]};
+  half8* dst = reinterpret_cast<half8*>(xh + (size_t)s * d + 32 * b);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint4 v = q[i / 2];
+    const uint32_t w0 = (i % 2) ? v.z : v.x, w1 = (i % 2) ? v.w : v.y;
+    half8 o;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      o[j] = (_Float16)(float)(int8_t)(w0 >> (8 * j));
+      o[4 + j] = (_Float16)(float)(int8_t)(w1 >> (8 * j));
+    }
+    dst[i] = o;
+  }
+  qxs[(size_t)b * nkp + s] = xs[(size_t)t * nb + b];
+  if (sw == 32) {
+    qxsum[(size_t)b * nkp + s] = __uint_as_float(xsum[(size_t)t * nb + b]);
+  } else if (sw == 16) {
+    qxsum[(size_t)(2 * b) * nkp + s] = __uint_as_float(xsum[(size_t)t * 2 * nb + 2 * b]);
+    qxsum[(size_t)(2 * b + 1) * nkp + s] = __uint_as_float(xsum[(size_t)t * 2 * nb + 2 * b + 1]);
+  }
+}
+
+hipError_t launch_gather_codes(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  const uint32_t nk = n * L.k;
+  hipLaunchKernelGGL(k_gather_codes, dim3((nk + 63) / 64, (L.d / 32 + 3) / 4), dim3(256), 0, st, B.xq, B.xs, B.xsum,
+                     B.slot_tok, L.d, nk, B.nkp, pq_sum_width(L.qt_gate), B.xh, B.qxs, B.qxsum);
+  return hipGetLastError();
+}
+
+hipError_t launch_pq_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  switch (L.qt_gate) {
+#define GU(T) case T: return pq_gateup<T>(L, B, n, st);
+    GU(Q4_K) GU(Q5_K) GU(Q6_K) GU(Q3_K) GU(Q2_K) GU(Q8_0)
+#undef GU
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_pq_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st) {
+  switch (L.qt_down) {
+#define DN(T) case T: return pq_down<T>(L, B, n, ksg, st);
+    DN(Q4_K) DN(Q5_K) DN(Q6_K) DN(Q3_K) DN(Q2_K) DN(Q8_0)
+#undef DN
+  }
+  return hipErrorInvalidValue;
+}
+
+// k_pq's down workgroups cover the same rows as k_pf's, so the slices are sized alike.
+uint32_t pq_ksg(const LayerDev& L, const FwdBufs& B) { return prefill_ksg(L, B); }
+
 hipError_t launch_prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
   switch (L.qt_gate) {
 #define GU(T) case T: return prefill_gateup<T>(L, B, n, st);

@@ -616,12 +616,436 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------------
+// Packed math on MFMA: quant::matmul's int8 path (quant/mod.rs:223-304, the q*_dot
+// kernels :398-621) for prefill-sized calls, the arithmetic of Weight::Packed under
+// mmap = true.
+//
+// The reference splits every row dot into sub-blocks (32 values for Q4_K/Q5_K/Q8_0, 16
+// for Q6_K/Q3_K/Q2_K), takes each sub-block's integer dot of the raw quants with the
+// int8 activations, and adds one float term per sub-block to the row sum, in K order:
+//   Q4_K, Q5_K, Q2_K:  acc += xs * ((d*sc) * dot - (dmin*m) * sum)
+//   Q6_K:              acc += ((xs * d) * sc) * dot      (dot over q - 32)
+//   Q3_K:              acc += (xs * (d*(sc-32))) * dot   (dot over q - 4*(1-hbit))
+//   Q8_0:              acc += (ws * xs) * dot
+// Here the integer dots come from fp16 MFMAs: the raw quants and the int8 activation
+// codes are exact fp16 values and every partial sum is an integer below 2^24, so the
+// f32 result of a sub-block's MFMA (one K16 step for 16-wide sub-blocks, two for
+// 32-wide) is the reference's dot exactly. The float term is then evaluated per (row,
+// token) exactly as the reference writes it and added in K order. With the whole K
+// range in one workgroup (gate/up) the row sums are the reference's bit for bit, so h
+// and its int8 requantisation are too; the down product splits K into slices that the
+// combine adds in order (outputs then within rtol 1e-3 / atol 1e-4).
+//
+// Inputs: the activation codes in slot order as fp16 ([nk][K]), and the per-token
+// factors transposed, [K/32][nkp] scales and [K/SW][nkp] sums (nkp >= nk + 64 so a
+// token tile's 64 slots are always in bounds). Gate/up writes h's codes, scales and
+// sums the same way for the down product.
+// ---------------------------------------------------------------------------------
+template <int QT> struct PQ;
+
+// (d*sc, dmin*m) of sub-block SB from a Q4_K/Q5_K header (d, dmin, scales[12]).
+template <int SB>
+__device__ __forceinline__ void kq_rowf(u32x4 hd, float* rf) {
+  const uint32_t s3[3] = {hd.y, hd.z, hd.w};
+  uint32_t sc, m;
+  scale_min_k4(s3, SB, sc, m);
+  rf[0] = f16v(hd.x) * (float)sc;
+  rf[1] = f16v(hd.x >> 16) * (float)m;
+}
+
+// Sub-block width SBW, activation-sum width SWS (0: the dot's operand carries the
+// offset, or the type has no min term), and the per-row factors of sub-block SB of the
+// unit staged in chunk C: rf[0], rf[1] as the term below reads them.
+template <> struct PQ<Q4_K> {
+  static constexpr int QT = Q4_K, SBW = 32, SWS = 32;
+  template <int C, int S>
+  static __device__ __forceinline__ half8 qfrag(const uint8_t* row, uint32_t h) {
+    constexpr int sb = S / 2;
+    constexpr bool high = sb & 1;
+    u32x2 q = ld8(pf_at<QT, C, 16 + 32 * (sb / 2) + 16 * (S % 2)>(row) + 8 * h);
+    const uint32_t mask = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+    q.x &= mask;
+    q.y &= mask;
+    // low nibble: (1024 + q) - 1024; high nibble in place (16q): (1024 + 16q) / 16 - 64
+    return high ? bytes_fma(q, h2s((_Float16)0.0625f), h2s((_Float16)-64.0f))
+                : bytes_fma(q, h2s((_Float16)1.0f), h2s((_Float16)-1024.0f));
+  }
+  template <int C, int SB>
+  static __device__ __forceinline__ void rowf(const uint8_t* row, float* rf) {
+    kq_rowf<SB>(ld16(pf_at<QT, C, 0>(row)), rf);
+  }
+  static __device__ __forceinline__ float term(float dot, const float* rf, float xs, float s) {
+    return xs * (rf[0] * dot - rf[1] * s);
+  }
+};
+
+template <> struct PQ<Q5_K> {
+  static constexpr int QT = Q5_K, SBW = 32, SWS = 32;
+  template <int C, int S>
+  static __device__ __forceinline__ half8 qfrag(const uint8_t* row, uint32_t h) {
+    constexpr int sb = S / 2;
+    const u32x2 qh = ld8(pf_at<QT, C, 16 + 16 * (S % 2)>(row) + 8 * h);
+    const u32x2 ql = ld8(pf_at<QT, C, 48 + 32 * (sb / 2) + 16 * (S % 2)>(row) + 8 * h);
+    u32x2 b;
+#pragma unroll
+    for (int d = 0; d < 2; d++)
+      b[d] = ((sb & 1 ? ql[d] >> 4 : ql[d]) & 0x0f0f0f0fu) | (((qh[d] >> sb) & 0x01010101u) << 4);
+    return bytes_fma(b, h2s((_Float16)1.0f), h2s((_Float16)-1024.0f));
+  }
+  template <int C, int SB>
+  static __device__ __forceinline__ void rowf(const uint8_t* row, float* rf) {
+    kq_rowf<SB>(ld16(pf_at<QT, C, 0>(row)), rf);
+  }
+  static __device__ __forceinline__ float term(float dot, const float* rf, float xs, float s) {
+    return xs * (rf[0] * dot - rf[1] * s);
+  }
+};
+
+template <> struct PQ<Q6_K> {
+  static constexpr int QT = Q6_K, SBW = 16, SWS = 0;
+  template <int C, int S>
+  static __device__ __forceinline__ half8 qfrag(const uint8_t* row, uint32_t h) {
+    return Dec<Q6_K>::frag<C, S>(row, h);  // q - 32
+  }
+  template <int C, int SB>
+  static __device__ __forceinline__ void rowf(const uint8_t* row, float* rf) {
+    const u32x4 sc = ld16(pf_at<QT, C, 192>(row));
+    rf[0] = f16v(ld16(pf_at<QT, C, 208>(row)).x);
+    rf[1] = (float)(int8_t)((sc[SB / 4] >> (8 * (SB % 4))) & 0xffu);
+  }
+  static __device__ __forceinline__ float term(float dot, const float* rf, float xs, float) {
+    return xs * rf[0] * rf[1] * dot;
+  }
+};
+
+template <> struct PQ<Q3_K> {
+  static constexpr int QT = Q3_K, SBW = 16, SWS = 0;
+  template <int C, int S>
+  static __device__ __forceinline__ half8 qfrag(const uint8_t* row, uint32_t h) {
+    constexpr int n = S / 8, j4 = (S % 8) / 2;
+    const u32x2 hm = ld8(pf_at<QT, C, 16 * (S % 2)>(row) + 8 * h);
+    const u32x2 qs = ld8(pf_at<QT, C, 32 + 32 * n + 16 * (S % 2)>(row) + 8 * h);
+    u32x2 b;  // q2 + 4 * hbit in [0, 7]; the quant is b - 4
+#pragma unroll
+    for (int d = 0; d < 2; d++)
+      b[d] = ((qs[d] >> (2 * j4)) & 0x03030303u) | (((hm[d] >> (4 * n + j4)) & 0x01010101u) << 2);
+    return bytes_fma(b, h2s((_Float16)1.0f), h2s((_Float16)-1028.0f));
+  }
+  template <int C, int SB>
+  static __device__ __forceinline__ void rowf(const uint8_t* row, float* rf) {
+    const u32x4 tl = ld16(pf_at<QT, C, 96>(row));  // scales[12] | d
+    uint32_t sc4[4];
+    q3k_scales(tl.x, tl.y, tl.z, sc4);
+    const int scs = (int)(int8_t)((sc4[SB / 4] >> (8 * (SB % 4))) & 0xffu) - 32;
+    rf[0] = f16v(tl.w) * (float)scs;
+  }
+  static __device__ __forceinline__ float term(float dot, const float* rf, float xs, float) {
+    return xs * rf[0] * dot;
+  }
+};
+
+template <> struct PQ<Q2_K> {
+  static constexpr int QT = Q2_K, SBW = 16, SWS = 16;
+  template <int C, int S>
+  static __device__ __forceinline__ half8 qfrag(const uint8_t* row, uint32_t h) {
+    constexpr int n = S / 8, j4 = (S % 8) / 2;
+    const u32x2 qs = ld8(pf_at<QT, C, 16 + 32 * n + 16 * (S % 2)>(row) + 8 * h);
+    u32x2 b;
+#pragma unroll
+    for (int d = 0; d < 2; d++) b[d] = (qs[d] >> (2 * j4)) & 0x03030303u;
+    return bytes_fma(b, h2s((_Float16)1.0f), h2s((_Float16)-1024.0f));
+  }
+  template <int C, int SB>
+  static __device__ __forceinline__ void rowf(const uint8_t* row, float* rf) {
+    const u32x4 scb = ld16(pf_at<QT, C, 0>(row));
+    const uint32_t dd = ld16(pf_at<QT, C, 80>(row)).x;
+    const uint32_t sc = (scb[SB / 4] >> (8 * (SB % 4))) & 0xffu;
+    rf[0] = f16v(dd) * (float)(sc & 15u);
+    rf[1] = f16v(dd >> 16) * (float)(sc >> 4);
+  }
+  static __device__ __forceinline__ float term(float dot, const float* rf, float xs, float s) {
+    return xs * (rf[0] * dot - rf[1] * s);
+  }
+};
+
+template <> struct PQ<Q8_0> {
+  static constexpr int QT = Q8_0, SBW = 32, SWS = 0;
+  template <int C, int S>
+  static __device__ __forceinline__ half8 qfrag(const uint8_t* row, uint32_t h) {
+    return Dec<Q8_0>::frag<C, S>(row, h);  // the int8 quants
+  }
+  template <int C, int SB>
+  static __device__ __forceinline__ void rowf(const uint8_t* row, float* rf) {
+    rf[0] = f16v(ld16(pf_at<QT, C, 0>(row))[SB / 2] >> (16 * (SB % 2)));
+  }
+  static __device__ __forceinline__ float term(float dot, const float* rf, float xs, float) {
+    return rf[0] * xs * dot;
+  }
+};
+
+template <int QT> constexpr bool pq_type() {
+  return QT == Q4_K || QT == Q5_K || QT == Q6_K || QT == Q3_K || QT == Q2_K || QT == Q8_0;
+}
+
+struct PqArgs {
+  const ExpertWork* work;
+  const uint32_t* ptile;
+  const _Float16* in;   // [nk][K] activation codes
+  const float* ins;     // [K/32][nkp] activation scales
+  const float* insum;   // [K/SWS][nkp] activation sums (types with SWS)
+  uint32_t nk, nkp, K, rows;
+  uint32_t upk;         // down: units of K per slice
+  // gate/up: h's codes, scales and sums (the down type's width, swo; 0 = none)
+  _Float16* out;
+  float* outs;
+  float* outsum;
+  uint32_t swo;
+  float* y;             // down: [slices][nk][rows]
+};
+
+template <int QT, bool GU>
+__global__ void __launch_bounds__(64 * PF<QT>::NW) k_pq(PqArgs a) {
+  using T = PF<QT>;
+  using Q = PQ<QT>;
+  constexpr int NW = T::NW, NT = 64 * NW;
+  constexpr int KC = T::KC, NCK = KC / 8, NPC = T::NPC, NCH = T::EU / KC, SPC = KC / 16;
+  constexpr int U = UT_<QT>::U, NP = U / 16;
+  constexpr int SPS = Q::SBW / 16;                       // K16 steps per sub-block
+  constexpr int NXS = KC / 32, NSM = Q::SWS ? KC / Q::SWS : 0;  // token factor rows per chunk
+  constexpr uint32_t WROWS = 32 * NW * (GU ? 1 : 2);
+  constexpr uint32_t WBYTES = NW * NPC * 1024, XBYTES = kPfTok * KC * 2, TBYTES = (NXS + NSM) * kPfTok * 4;
+  constexpr uint32_t BUF = WBYTES + XBYTES + TBYTES;
+  constexpr int NX = (int)kPfTok * NCK / NT;              // activation loads per thread per chunk
+  static_assert(NX >= 1 && (int)kPfTok * NCK % NT == 0, "activation staging");
+  static_assert(2 * BUF <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * BUF];
+
+  const uint32_t pt = a.ptile[blockIdx.y];
+  if (pt == ~0u) return;
+  const ExpertWork* W = a.work + (pt >> 16);
+  const uint32_t t0 = (pt & 0xffffu) * kPfTok;
+  const uint32_t m = min(kPfTok, W->m - t0), s0 = W->s0 + t0;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t K = a.K, nunit = K / T::EU;
+  const uint32_t u0 = GU ? 0 : blockIdx.z * a.upk, u1 = GU ? nunit : min(nunit, u0 + a.upk);
+
+  const size_t tile_bytes = (size_t)nunit * kTileRows * U;
+  const uint8_t* m_lo = GU ? W->w[0] + (NW / 2) * blockIdx.x * tile_bytes : W->w[2] + NW * blockIdx.x * tile_bytes;
+  const uint8_t* m_hi = GU ? W->w[1] + (NW / 2) * blockIdx.x * tile_bytes : m_lo + (NW / 2) * tile_bytes;
+  uint32_t row[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; rt++) {
+    const uint32_t tm = GU ? rt * (NW / 2) + wave / 2 : wave, i = GU ? 32 * (wave % 2) + l32 : 32 * rt + l32;
+    row[rt] = (tm * NPC * 64 + i) * 16;
+  }
+  const uint32_t xrow = l32 * NCK * 16;
+  uint32_t tsw = (l32 % NCK) * 16;
+
+  auto stage = [&](uint32_t u, auto cc, uint32_t b) {
+    constexpr int C = decltype(cc)::value;
+    uint8_t* wb = lds + b * BUF;
+    uint8_t* xb = wb + WBYTES;
+    uint8_t* tb = xb + XBYTES;
+#pragma unroll
+    for (int j = 0; j < NPC; j++) {
+      const uint32_t wq = NW * j + wave, tm = wq / NPC, pc = wq % NPC;
+      const uint8_t* src = (tm < NW / 2 ? m_lo : m_hi) + (tm % (NW / 2)) * tile_bytes;
+      lds_load16(src + ((size_t)u * NP + (uint32_t)T::piece(C, (int)pc)) * 1024 + lane * 16, wb + 1024 * wq);
+    }
+    // activation codes: item (token t, 16-byte column c at position c ^ (t % NCK))
+    constexpr uint32_t RW = 64 / NCK;
+    const uint32_t k0 = u * T::EU + C * KC;
+#pragma unroll
+    for (int j = 0; j < NX; j++) {
+      const uint32_t wq = NW * j + wave;
+      const uint32_t t = (RW * wq) % kPfTok + lane / NCK, c = (lane % NCK) ^ (t % NCK), tc = min(t, m - 1);
+      lds_load16(a.in + ((size_t)(s0 + tc) * K + k0 + 8 * c), xb + 1024 * wq);
+    }
+    // token factors: row r of the chunk (scales, then sums) = 64 floats of slots s0..
+#pragma unroll
+    for (int j = 0; j < (NXS + NSM + NW - 1) / NW; j++) {
+      const uint32_t r = NW * j + wave;
+      if (r < (uint32_t)(NXS + NSM)) {
+        const float* src = r < (uint32_t)NXS ? a.ins + (size_t)(k0 / 32 + r) * a.nkp
+                                             : a.insum + (size_t)(k0 / (Q::SWS ? Q::SWS : 1) + r - NXS) * a.nkp;
+        __builtin_amdgcn_global_load_lds(src + s0 + lane, (__attribute__((address_space(3))) void*)(tb + 256 * r), 4,
+                                         0, 0);
+      }
+    }
+  };
+
+  f32x16 acc[2][2], P[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = P[i][j][r] = 0.0f;
+  const f32x16 zero = acc[0][0];
+  const bool two = m > 32;  // the second 32-token tile holds tokens
+
+  if (u0 < u1) stage(u0, std::integral_constant<int, 0>{}, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (uint32_t u = u0; u < u1; u++) {
+    static_for<NCH>([&](auto cc) {
+      constexpr int C = decltype(cc)::value;
+      const uint32_t b = (NCH % 2 == 0) ? (uint32_t)(C % 2) : ((u - u0) * NCH + C) % 2;
+      if constexpr (C + 1 < NCH) {
+        stage(u, std::integral_constant<int, C + 1>{}, b ^ 1);
+      } else {
+        if (u + 1 < u1) stage(u + 1, std::integral_constant<int, 0>{}, b ^ 1);
+      }
+      const uint8_t* wb = lds + b * BUF;
+      const uint8_t* xb = wb + WBYTES;
+      const float* tf = reinterpret_cast<const float*>(xb + XBYTES);
+      asm volatile("" : "+v"(tsw));
+      static_for<SPC>([&](auto ss) {
+        constexpr int SL = decltype(ss)::value, S = C * SPC + SL;
+        half8 bw[2], ax[2];
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++) bw[rt] = Q::template qfrag<C, S>(wb + row[rt], h);
+        const uint32_t pos = ((2 * SL + h) * 16) ^ tsw;
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) ax[tt] = *reinterpret_cast<const half8*>(xb + xrow + pos + 32 * tt * NCK * 16);
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++) {
+          P[rt][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[0], bw[rt], S % SPS == 0 ? zero : P[rt][0], 0, 0, 0);
+          if (two)
+            P[rt][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[1], bw[rt], S % SPS == 0 ? zero : P[rt][1], 0, 0, 0);
+        }
+        if constexpr ((S + 1) % SPS == 0) {
+          // sub-block SB closes: its term for every (row, token), added in K order
+          constexpr int SB = S / SPS;
+          constexpr int EX = SL * 16 / 32, ES = Q::SWS ? SL * 16 / (Q::SWS ? Q::SWS : 1) : 0;
+          float rf[2][2];
+#pragma unroll
+          for (int rt = 0; rt < 2; rt++) Q::template rowf<C, SB>(wb + row[rt], rf[rt]);
+#pragma unroll
+          for (int tt = 0; tt < 2; tt++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              if (32 * tt + 8 * j < m) {
+                const uint32_t t4 = 32 * tt + 8 * j + 4 * h;
+                const float4 xs4 = *reinterpret_cast<const float4*>(tf + EX * kPfTok + t4);
+                float4 s4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if constexpr (Q::SWS != 0) s4 = *reinterpret_cast<const float4*>(tf + (NXS + ES) * kPfTok + t4);
+                const float xv[4] = {xs4.x, xs4.y, xs4.z, xs4.w}, sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                  for (int rt = 0; rt < 2; rt++) {
+                    const int r = 4 * j + i;
+                    acc[rt][tt][r] = acc[rt][tt][r] + Q::term(P[rt][tt][r], rf[rt], xv[i], sv[i]);
+                  }
+              }
+            }
+          }
+        }
+      });
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    });
+  }
+
+  // epilogue
+#pragma unroll
+  for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const uint32_t t = 32 * tt + 8 * (r / 4) + 4 * h + (r % 4);
+      if constexpr (GU) {
+        // h = silu(g) * u, then quantised per 32 rows (the 32 lanes of this half) with
+        // quant_wave's arithmetic (quant/mod.rs:331-345)
+        const uint32_t fr = blockIdx.x * WROWS + 32 * wave + l32;
+        const float hv = swiglu(acc[0][tt][r], acc[1][tt][r]);
+        float am = fmaxf(0.0f, fabsf(hv));
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+        const float scale = fdiv(am, 127.0f);
+        const float inv = scale > 0.0f ? fdiv(1.0f, scale) : 0.0f;
+        const float rq = roundf(hv * inv);
+        const int qi = (rq != rq) ? 0 : rq < -127.0f ? -127 : rq > 127.0f ? 127 : (int)rq;
+        int sm = qi;
+        if (a.swo) {
+#pragma unroll
+          for (int o = 8; o >= 1; o >>= 1) sm += __shfl_xor(sm, o, 64);
+          if (a.swo == 32) sm += __shfl_xor(sm, 16, 64);
+        }
+        if (t < m) {
+          a.out[(size_t)(s0 + t) * a.rows + fr] = (_Float16)(float)qi;
+          if (l32 == 0) a.outs[(size_t)(fr / 32) * a.nkp + s0 + t] = scale;
+          if (a.swo && (l32 % a.swo) == 0) a.outsum[(size_t)(fr / a.swo) * a.nkp + s0 + t] = (float)sm;
+        }
+      } else {
+        float* y = a.y + (size_t)blockIdx.z * a.nk * a.rows;
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++) {
+          const uint32_t dr = blockIdx.x * WROWS + 64 * wave + 32 * rt + l32;
+          if (t < m) y[(size_t)(s0 + t) * a.rows + dr] = acc[rt][tt][r];
+        }
+      }
+    }
+}
+
 template <int QT>
 uint32_t pf_rows(bool gu) {
   if constexpr (QT == F32) {
     return 0;
   } else {
     return 32u * PF<QT>::NW * (gu ? 1u : 2u);
+  }
+}
+
+// Packed-math prefill products (k_pq) of this block type.
+template <int QT>
+hipError_t pq_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  if constexpr (!pq_type<QT>()) {
+    return hipErrorNotSupported;
+  } else {
+    if (L.f % pf_rows<QT>(true) || L.d % PF<QT>::EU) return hipErrorInvalidValue;
+    PqArgs a{};
+    a.work = B.work;
+    a.ptile = B.ptile;
+    a.in = B.xh;
+    a.ins = B.qxs;
+    a.insum = B.qxsum;
+    a.nk = n * L.k;
+    a.nkp = B.nkp;
+    a.K = L.d;
+    a.rows = L.f;
+    a.out = B.hh;
+    a.outs = B.qhs;
+    a.outsum = B.qhsum;
+    a.swo = pq_sum_width(L.qt_down);
+    hipLaunchKernelGGL((k_pq<QT, true>), dim3(L.f / pf_rows<QT>(true), B.ptile_cap), dim3(64 * PF<QT>::NW), 0, st, a);
+    return hipGetLastError();
+  }
+}
+
+template <int QT>
+hipError_t pq_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st) {
+  if constexpr (!pq_type<QT>()) {
+    return hipErrorNotSupported;
+  } else {
+    if (L.d % pf_rows<QT>(false) || L.f % PF<QT>::EU || ksg < 1 || ksg > kMaxKsg) return hipErrorInvalidValue;
+    PqArgs a{};
+    a.work = B.work;
+    a.ptile = B.ptile;
+    a.in = B.hh;
+    a.ins = B.qhs;
+    a.insum = B.qhsum;
+    a.nk = n * L.k;
+    a.nkp = B.nkp;
+    a.K = L.f;
+    a.rows = L.d;
+    a.upk = (L.f / PF<QT>::EU + ksg - 1) / ksg;
+    a.y = B.y;
+    hipLaunchKernelGGL((k_pq<QT, false>), dim3(L.d / pf_rows<QT>(false), B.ptile_cap, ksg), dim3(64 * PF<QT>::NW), 0,
+                       st, a);
+    return hipGetLastError();
   }
 }
 
@@ -688,5 +1112,7 @@ hipError_t prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_
 template uint32_t prefill_down_slices<GMOE_QT>(const LayerDev&, const FwdBufs&);
 template hipError_t prefill_gateup<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, hipStream_t);
 template hipError_t prefill_down<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, uint32_t, hipStream_t);
+template hipError_t pq_gateup<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, hipStream_t);
+template hipError_t pq_down<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, uint32_t, hipStream_t);
 
 }  // namespace gmoe
