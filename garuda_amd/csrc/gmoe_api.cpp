@@ -629,6 +629,8 @@ gmoe_status run_layer(gmoe_ctx* c, Layer& L, FwdBufs B, uint32_t n, hipStream_t 
     HIP_TRY(launch_spec_front(D, B, n, quant ? 1 : 0, st));
   } else if (front_small_ok(D, n)) {
     HIP_TRY(launch_front_small(D, B, n, quant ? 1 : 0, true, st));
+  } else if (front_wide_ok(D, n)) {
+    HIP_TRY(launch_front_wide(D, B, n, quant ? 1 : 0, st));
   } else {
     HIP_TRY(launch_route(D, B, n, st));
     HIP_TRY(launch_dispatch(D, B, n, st));

@@ -595,6 +595,134 @@ __device__ __forceinline__ uint32_t lane_u(uint32_t v, uint32_t l) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l);
 }
 
+// The top-k weights after ranking: lane i < k holds the i-th ranked expert's value w
+// (probability, or logit under Mixtral gating); returns its final weight
+// (llama/mod.rs:945-949, router/mod.rs:91-115).
+__device__ __forceinline__ float gate_topk_weights(uint32_t gating, uint32_t k, float w) {
+  if (gating == 0) {  // llama/mod.rs:945-949
+    float sum = -0.0f;
+    for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
+    w *= sum > 0.0f ? fdiv(1.0f, sum) : fdiv(1.0f, (float)k);
+  } else if (gating == 1) {  // router/mod.rs:91-97: softmax over the k kept logits
+    float mx = -INFINITY;
+    for (uint32_t i = 0; i < k; i++) mx = fmaxf(mx, lane_f(w, i));
+    if (!isfinite(mx)) {
+      w = fdiv(1.0f, (float)k);
+    } else {
+      w = gm_expf(w - mx);
+      float sum = 0.0f;
+      for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
+      w = (isfinite(sum) && sum > 0.0f) ? w * fdiv(1.0f, sum) : fdiv(1.0f, (float)k);
+    }
+  } else if (gating == 3) {  // router/mod.rs:102-115
+    float sum = -0.0f;
+    for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
+    w = sum > 0.0f ? fdiv(w, sum) : fdiv(1.0f, (float)k);
+  }
+  return w;
+}
+
+// gate_wave for up to 64*EPL experts: lane l holds experts l, l + 64, ... in x[0..EPL).
+// Every ordered sum still runs over the experts in index order (readlane), so the
+// arithmetic is gate_wave's. Lanes r < k receive the r-th ranked expert and its weight.
+// `scratch` holds 2*k words of LDS.
+template <int EPL>
+__device__ void gate_wave_wide(uint32_t gating, uint32_t ne, uint32_t k, const float* x, uint32_t lane,
+                               uint32_t* id_out, float* w_out, uint32_t* scratch) {
+  const bool llama = gating == 0;
+  float v[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; j++) v[j] = x[j];
+  if (gating == 0 || gating == 2 || gating == 3) {  // softmax over all experts (simd/mod.rs:132-158)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < EPL; j++)
+      if (64 * j + lane < ne) mx = fmaxf(mx, x[j]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    float inv = -1.0f;  // uniform
+    if (isfinite(mx)) {
+#pragma unroll
+      for (int j = 0; j < EPL; j++) v[j] = gm_expf(x[j] - mx);
+      float sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < EPL; j++)
+        for (uint32_t l = 0; l < 64 && 64 * j + l < ne; l++) sum += lane_f(v[j], l);
+      if (isfinite(sum) && sum > 0.0f) inv = fdiv(1.0f, sum);
+    }
+#pragma unroll
+    for (int j = 0; j < EPL; j++) v[j] = inv < 0.0f ? fdiv(1.0f, (float)ne) : v[j] * inv;
+  }
+  float* tw = reinterpret_cast<float*>(scratch);
+  uint32_t* ti = scratch + k;
+  // When the rank order is a strict total order (always under total_cmp; under
+  // partial_cmp when no value is NaN, +0 and -0 then being equal), the r-th ranked expert
+  // is the r-th pick of k rounds of a wave-wide maximum over the key (value key, then
+  // ~id, so that ties go to the lower id). Otherwise the ranks are counted as gate_wave
+  // counts them.
+  bool nan = false;
+#pragma unroll
+  for (int j = 0; j < EPL; j++) nan |= (64 * j + lane < ne) && (v[j] != v[j]);
+  if (llama || __ballot(nan) == 0ull) {
+    uint64_t key[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+      const uint32_t e = 64 * j + lane;
+      // order-preserving unsigned image of the rank order's value key
+      const uint32_t vk = llama ? (uint32_t)total_key(v[j]) ^ 0x80000000u
+                                : (uint32_t)total_key(v[j] == 0.0f ? 0.0f : v[j]) ^ 0x80000000u;
+      key[j] = e < ne ? ((uint64_t)vk << 32) | (uint64_t)(0xffffffffu - e) : 0ull;
+    }
+    for (uint32_t r = 0; r < k; r++) {
+      uint64_t best = 0ull;
+#pragma unroll
+      for (int j = 0; j < EPL; j++) best = key[j] > best ? key[j] : best;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        const uint64_t b = (uint64_t)__shfl_xor((long long)best, o, 64);
+        best = b > best ? b : best;
+      }
+      const uint32_t e = 0xffffffffu - (uint32_t)best;
+#pragma unroll
+      for (int j = 0; j < EPL; j++)
+        if (key[j] == best && best != 0ull) {  // the owner records the pick
+          tw[r] = v[j];
+          ti[r] = e;
+          key[j] = 0ull;
+        }
+    }
+  } else {
+    // rank = how many experts come before this one
+    uint32_t r[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) r[j] = 0;
+#pragma unroll
+    for (int jo = 0; jo < EPL; jo++)
+      for (uint32_t l = 0; l < 64 && 64 * jo + l < ne; l++) {
+        const uint32_t o = 64 * jo + l;
+        const float vo = lane_f(v[jo], l);
+#pragma unroll
+        for (int j = 0; j < EPL; j++) {
+          const uint32_t e = 64 * j + lane;
+          if (o != e && ranks_before(llama, vo, o, v[j], e)) r[j]++;
+        }
+      }
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+      const uint32_t e = 64 * j + lane;
+      if (e < ne && r[j] < k) {
+        tw[r[j]] = v[j];
+        ti[r[j]] = e;
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");  // one wave: its DS writes land before these reads
+  const float w = lane < k ? tw[lane] : 0.0f;
+  *id_out = lane < k ? ti[lane] : 0u;
+  *w_out = gate_topk_weights(gating, k, w);
+}
+
 // One token's routing from its logit x (lane e < ne). Lanes r < k receive the r-th
 // ranked expert and its weight. `scratch` holds 2*k words of LDS.
 __device__ void gate_wave(uint32_t gating, uint32_t ne, uint32_t k, float x, uint32_t lane, uint32_t* id_out,
@@ -625,30 +753,9 @@ __device__ void gate_wave(uint32_t gating, uint32_t ne, uint32_t k, float x, uin
   }
   __builtin_amdgcn_wave_barrier();
   asm volatile("" ::: "memory");  // one wave: its DS writes land before these reads
-  float w = lane < k ? tw[lane] : 0.0f;
-  const uint32_t id = lane < k ? ti[lane] : 0u;
-  if (gating == 0) {  // llama/mod.rs:945-949
-    float sum = -0.0f;
-    for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
-    w *= sum > 0.0f ? fdiv(1.0f, sum) : fdiv(1.0f, (float)k);
-  } else if (gating == 1) {  // router/mod.rs:91-97: softmax over the k kept logits
-    float mx = -INFINITY;
-    for (uint32_t i = 0; i < k; i++) mx = fmaxf(mx, lane_f(w, i));
-    if (!isfinite(mx)) {
-      w = fdiv(1.0f, (float)k);
-    } else {
-      w = gm_expf(w - mx);
-      float sum = 0.0f;
-      for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
-      w = (isfinite(sum) && sum > 0.0f) ? w * fdiv(1.0f, sum) : fdiv(1.0f, (float)k);
-    }
-  } else if (gating == 3) {  // router/mod.rs:102-115
-    float sum = -0.0f;
-    for (uint32_t i = 0; i < k; i++) sum += lane_f(w, i);
-    w = sum > 0.0f ? fdiv(w, sum) : fdiv(1.0f, (float)k);
-  }
-  *id_out = id;
-  *w_out = w;
+  const float w = lane < k ? tw[lane] : 0.0f;
+  *id_out = lane < k ? ti[lane] : 0u;
+  *w_out = gate_topk_weights(gating, k, w);
 }
 
 

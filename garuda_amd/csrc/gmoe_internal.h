@@ -265,6 +265,10 @@ bool front_small_ok(const LayerDev& L, uint32_t n);
 // dispatch = false: logits, ids and weights only (the exact half of the speculative front end)
 hipError_t launch_front_small(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, bool dispatch,
                               hipStream_t st);
+// Front end for 64 < ne <= 256 experts: one wave per token gates it (given logits or the
+// sequential dots) and quantises its activations; the last workgroup dispatches.
+bool front_wide_ok(const LayerDev& L, uint32_t n);
+hipError_t launch_front_wide(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st);
 // Speculative front end: router logits by a parallel dot with a rigorous bound on their
 // distance to the sequential dot, every expert that can be among a token's top k, the
 // int8 activation quantiser, and the dispatch of all (token, candidate) pairs.

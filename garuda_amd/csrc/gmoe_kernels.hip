@@ -364,6 +364,217 @@ __device__ void dispatch_block(const LayerDev& L, const FwdBufs& B, uint32_t n, 
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Wide front end (64 < ne <= 64 * kWideEPL experts): one wave per token gates it (lane l
+// holds experts l, l + 64, ...: gate_wave_wide) from the given logits or the reference's
+// sequential dots, and quantises its activations; the workgroup that finishes last
+// dispatches every pair (dispatch_par).
+// ---------------------------------------------------------------------------------
+constexpr int kWideEPL = 4, kWideWaves = 8, kWideThreads = 64 * kWideWaves;
+
+// The stable counting sort of dispatch_block by one workgroup of W waves, each pair's
+// position found without a scan over the pairs before it: per chunk of 64 pairs (a wave)
+// the experts present are peeled one at a time by ballot, which gives each pair its rank
+// among its expert's pairs in the chunk and the chunk's count per expert; the chunks of
+// a round (W of them, in pair order) then add their counts per expert in chunk order to
+// the running position. sm holds (4 + W) * ne + 2 words. Every thread must call this.
+__device__ void dispatch_par(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t* sm) {
+  const uint32_t ne = L.ne, k = L.k, nk = n * k, tid = threadIdx.x, T = blockDim.x, W = T / 64;
+  const uint32_t wave = tid >> 6, lane = tid & 63;
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint32_t* cnt = sm;             // [ne]
+  uint32_t* start = cnt + ne;     // [ne]
+  uint32_t* aidx = start + ne;    // [ne]
+  uint32_t* run = aidx + ne;      // [ne] next position per expert
+  uint32_t* lh = run + ne;        // [W][ne] a round's per-chunk counts, then bases
+  uint32_t* tot = lh + W * ne;    // [2]
+  for (uint32_t e = tid; e < ne; e += T) cnt[e] = 0;
+  __syncthreads();
+  for (uint32_t p = tid; p < nk; p += T) atomicAdd(&cnt[B.ids[p]], 1u);
+  __syncthreads();
+  for (uint32_t e = tid; e < ne; e += T) {  // active slot: descending count, then id
+    const uint32_t c = cnt[e];
+    uint32_t r = 0;
+    if (c)
+#pragma unroll 8
+      for (uint32_t j = 0; j < ne; j++) {
+        const uint32_t cj = cnt[j];
+        r += (cj > c || (cj == c && j < e)) ? 1u : 0u;
+      }
+    aidx[e] = c ? r : ~0u;
+  }
+  __syncthreads();
+  if (wave == 0) {  // running scans over the experts, 64 at a time
+    uint32_t off = 0, na = 0, nt = 0;
+    for (uint32_t e0 = 0; e0 < ne; e0 += 64) {
+      const uint32_t e = e0 + lane;
+      const uint32_t c = e < ne ? cnt[e] : 0u, act = c ? 1u : 0u;
+      const uint32_t tl = B.ptile ? (c + kPfTok - 1) / kPfTok : 0u;
+      uint32_t ic = c, ia = act, it = tl;
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t vc = __shfl_up(ic, o, 64), va = __shfl_up(ia, o, 64), vt = __shfl_up(it, o, 64);
+        if (lane >= (uint32_t)o) {
+          ic += vc;
+          ia += va;
+          it += vt;
+        }
+      }
+      if (e < ne) {
+        start[e] = off + ic - c;
+        if (act && B.ptile) {
+          const uint32_t a = aidx[e], t0 = nt + it - tl;
+          for (uint32_t t = 0; t < tl; t++) B.ptile[t0 + t] = (a << 16) | t;
+        }
+      }
+      off += __shfl(ic, 63, 64);
+      na += __shfl(ia, 63, 64);
+      nt += __shfl(it, 63, 64);
+    }
+    if (lane == 0) {
+      tot[0] = na;
+      tot[1] = nt;
+      B.offsets[ne] = off;
+      B.active[0] = na;
+    }
+  }
+  __syncthreads();
+  const uint32_t na = tot[0], nt = tot[1];
+  for (uint32_t e = tid; e < ne; e += T) {
+    B.offsets[e] = start[e];
+    run[e] = start[e];
+    const uint32_t a = aidx[e];
+    if (a != ~0u) {
+      B.active[1 + a] = e;
+      if (B.work) {
+        ExpertWork& Wk = B.work[a];
+        for (int q = 0; q < 3; q++) Wk.w[q] = L.eptr[q * ne + e];
+        Wk.e = e;
+        Wk.s0 = start[e];
+        Wk.m = cnt[e];
+      }
+    }
+  }
+  if (B.work)
+    for (uint32_t a = na + tid; a < ne; a += T) B.work[a].m = 0;
+  if (B.ptile)
+    for (uint32_t i = nt + tid; i < B.ptile_cap; i += T) B.ptile[i] = ~0u;
+  for (uint32_t c0 = 0; c0 < nk; c0 += T) {
+    for (uint32_t e = lane; e < ne; e += 64) lh[wave * ne + e] = 0;
+    const uint32_t p = c0 + tid;
+    const uint32_t id = p < nk ? B.ids[p] : ~0u;
+    const float w = p < nk ? B.w[p] : 0.0f;
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");  // the wave's zeros land before its counts
+    uint32_t lrank = 0;
+    uint64_t todo = __ballot(id != ~0u);
+    while (todo) {
+      const uint32_t lead = (uint32_t)__builtin_ctzll(todo);
+      const uint32_t e = lane_u(id, lead);
+      const uint64_t m = __ballot(id == e);
+      if (id == e) lrank = (uint32_t)__popcll(m & below);
+      if (lane == lead) lh[wave * ne + e] = (uint32_t)__popcll(m);
+      todo &= ~m;
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < ne; e += T) {  // chunk bases in pair order
+      uint32_t r = run[e];
+      for (uint32_t v = 0; v < W; v++) {
+        const uint32_t c = lh[v * ne + e];
+        lh[v * ne + e] = r;
+        r += c;
+      }
+      run[e] = r;
+    }
+    __syncthreads();
+    if (id != ~0u) {
+      const uint32_t pos = lh[wave * ne + id] + lrank;
+      B.slot_tok[pos] = p / k;
+      B.slot_w[pos] = w;
+      B.slot_rank[pos] = p % k;
+      B.slot_of[p] = pos;
+    }
+    __syncthreads();
+  }
+}
+
+__global__ void __launch_bounds__(kWideThreads) k_front_wide(LayerDev L, FwdBufs B, uint32_t n, int quant) {
+  extern __shared__ uint32_t wsm[];  // [kWideWaves][2k] gating scratch, then dispatch_par's words
+  const uint32_t ne = L.ne, k = L.k, d = L.d;
+  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const uint32_t t = blockIdx.x * kWideWaves + wave;
+  if (t < n) {
+    const float* hs = B.hs + (size_t)t * d;
+    float x[kWideEPL];
+#pragma unroll
+    for (int j = 0; j < kWideEPL; j++) {
+      const uint32_t e = 64 * j + lane;
+      float acc = 0.0f;
+      if (e < ne) {
+        if (B.logits_in) {
+          acc = B.logits_in[(size_t)t * ne + e];
+        } else {  // simd/mod.rs:13-16: products added left to right from -0.0
+          const float4* wr = reinterpret_cast<const float4*>(L.router + (size_t)e * d);
+          const float4* hr = reinterpret_cast<const float4*>(hs);
+          acc = -0.0f;
+          for (uint32_t i = 0; i < d / 4; i++) {
+            const float4 a = wr[i], h = hr[i];
+            const float p0 = a.x * h.x, p1 = a.y * h.y, p2 = a.z * h.z, p3 = a.w * h.w;
+            acc = acc + p0;
+            acc = acc + p1;
+            acc = acc + p2;
+            acc = acc + p3;
+          }
+        }
+        B.logits[(size_t)t * ne + e] = acc;
+      }
+      x[j] = acc;
+    }
+    uint32_t id;
+    float w;
+    gate_wave_wide<kWideEPL>(L.gating, ne, k, x, lane, &id, &w, wsm + wave * 2 * k);
+    if (lane < k) {
+      B.ids[(size_t)t * k + lane] = id;
+      B.w[(size_t)t * k + lane] = w;
+    }
+    if (quant) {
+      const uint32_t nblk = d / 32;
+      for (uint32_t b = lane; b < nblk; b += 64) {
+        float v[32];
+        const float4* src = reinterpret_cast<const float4*>(hs + (size_t)b * 32);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const float4 t4 = src[i];
+          v[4 * i] = t4.x; v[4 * i + 1] = t4.y; v[4 * i + 2] = t4.z; v[4 * i + 3] = t4.w;
+        }
+        const size_t gb = (size_t)t * nblk + b;
+        quant32(v, B.xq + gb * 32, B.xs + gb, B.xsum, gb, sum_kind_of(L.qt_gate), sum_offset_of(L.qt_gate));
+      }
+    }
+  }
+  // every workgroup's ids and weights are in memory before its count is taken; the last
+  // one to count dispatches
+  __threadfence();
+  __syncthreads();
+  __shared__ uint32_t last;
+  if (tid == 0) last = atomicAdd(B.done, 1u) == gridDim.x - 1 ? 1u : 0u;
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  dispatch_par(L, B, n, wsm + kWideWaves * 2 * k);
+  if (tid == 0) *B.done = 0;
+}
+
+bool front_wide_ok(const LayerDev& L, uint32_t n) {
+  return n >= 1 && L.ne > 64u && L.ne <= 64u * kWideEPL && L.k <= 32 && L.d % 32 == 0;
+}
+
+hipError_t launch_front_wide(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st) {
+  const size_t shm = ((size_t)kWideWaves * 2 * L.k + (4 + kWideWaves) * (size_t)L.ne + 2) * 4;
+  hipLaunchKernelGGL(k_front_wide, dim3((n + kWideWaves - 1) / kWideWaves), dim3(kWideThreads), shm, st, L, B, n,
+                     quant);
+  return hipGetLastError();
+}
+
 constexpr uint32_t kDispatchThreads = 256;
 
 __global__ void __launch_bounds__(kDispatchThreads) k_dispatch(LayerDev L, FwdBufs B, uint32_t n) {
@@ -379,21 +590,48 @@ __global__ void __launch_bounds__(kDispatchThreads) k_dispatch(LayerDev L, FwdBu
 // Stable counting sort of the nk (token, rank) pairs by expert: members[e] of
 // llama/mod.rs:967-972 laid end to end, as dispatch_block makes it. pair(p, &id, &w)
 // reads pair p. Pairs go 64 at a time; per expert a ballot finds its pairs in the chunk
-// and lane e keeps expert e's count, then its next free slot.
+// and lane e keeps expert e's count, then its next free slot. Up to kWaveChunks chunks
+// are read once, all loads issued together, and kept in registers for both passes (one
+// memory round trip instead of two per chunk); longer lists are read chunk by chunk.
+constexpr uint32_t kWaveChunks = 16;
+
 template <class Ptr, class Pair>
 __device__ void dispatch_wave(const FwdBufs& B, Ptr eptr, uint32_t ne, uint32_t k, uint32_t nk,
                               uint32_t lane, Pair pair, bool meta = true) {
   const uint64_t below = (1ull << lane) - 1ull;
+  const bool cached = nk <= 64 * kWaveChunks;
+  uint32_t cid[kWaveChunks];
+  float cw[kWaveChunks];
+  if (cached) {
+#pragma unroll
+    for (uint32_t c = 0; c < kWaveChunks; c++) {
+      cid[c] = ~0u;
+      cw[c] = 0.0f;
+      if (64 * c + lane < nk) pair(64 * c + lane, &cid[c], &cw[c]);
+    }
+  }
+  // f(c0, id, w) for every chunk in order, pair c0 + lane in (id, w) (id ~0u past the end)
+  auto chunks = [&](auto f) {
+    if (cached) {
+#pragma unroll
+      for (uint32_t c = 0; c < kWaveChunks; c++)
+        if (64 * c < nk) f(64 * c, cid[c], cw[c]);
+    } else {
+      for (uint32_t c0 = 0; c0 < nk; c0 += 64) {
+        uint32_t id = ~0u;
+        float w = 0.0f;
+        if (c0 + lane < nk) pair(c0 + lane, &id, &w);
+        f(c0, id, w);
+      }
+    }
+  };
   uint32_t cnt = 0;
-  for (uint32_t c0 = 0; c0 < nk; c0 += 64) {
-    uint32_t id = ~0u;
-    float w;
-    if (c0 + lane < nk) pair(c0 + lane, &id, &w);
+  chunks([&](uint32_t, uint32_t id, float) {
     for (uint32_t e = 0; e < ne; e++) {
       const uint32_t c = (uint32_t)__popcll(__ballot(id == e));
       if (lane == e) cnt += c;
     }
-  }
+  });
   uint32_t off = 0, run = 0;
   for (uint32_t e = 0; e < ne; e++) {
     if (lane == e) off = run;
@@ -401,9 +639,9 @@ __device__ void dispatch_wave(const FwdBufs& B, Ptr eptr, uint32_t ne, uint32_t 
   }
   const uint64_t act = __ballot(lane < ne && cnt > 0);
   const uint32_t na = (uint32_t)__popcll(act);
-  // active slot: experts by descending pair count, then ascending id. The expert kernels'
-  // grids run the active slots in this order, so the experts with the most tokens (the
-  // longest workgroups) start first and the short ones fill in behind them.
+  // active slot: experts by descending pair count, then ascending id. The expert
+  // kernels' grids run the active slots in this order, so the experts with the most
+  // tokens (the longest workgroups) start first and the short ones fill in behind them.
   uint32_t arank = 0;
   for (uint32_t e = 0; e < ne; e++) {
     const uint32_t ce = lane_u(cnt, e);
@@ -441,11 +679,9 @@ __device__ void dispatch_wave(const FwdBufs& B, Ptr eptr, uint32_t ne, uint32_t 
     }
     for (uint32_t i = tr + lane; i < B.ptile_cap; i += 64) B.ptile[i] = ~0u;
   }
-  for (uint32_t c0 = 0; c0 < nk; c0 += 64) {
-    uint32_t id = ~0u, pos = 0;
-    float w = 0.0f;
+  chunks([&](uint32_t c0, uint32_t id, float w) {
+    uint32_t pos = 0;
     const uint32_t p = c0 + lane;
-    if (p < nk) pair(p, &id, &w);
     for (uint32_t e = 0; e < ne; e++) {
       const uint64_t m = __ballot(id == e);
       if (id == e) pos = lane_u(off, e) + (uint32_t)__popcll(m & below);
@@ -459,7 +695,7 @@ __device__ void dispatch_wave(const FwdBufs& B, Ptr eptr, uint32_t ne, uint32_t 
         B.slot_of[p] = pos;
       }
     }
-  }
+  });
 }
 
 // ---------------------------------------------------------------------------------
@@ -874,10 +1110,92 @@ hipError_t launch_tile_rows(uint32_t qt, const uint8_t* raw, uint32_t r0, uint32
 // then adds, starting from the zeroed output.
 // ---------------------------------------------------------------------------------
 
+// Decode-sized combines (k <= kCombK pairs a token): every slot, weight and slice value
+// is loaded before the first add, so the kernel waits on two memory round trips (the
+// slots, then the slices) instead of one per slice.
+constexpr uint32_t kCombK = 8;
+
+template <uint32_t KS>
+__device__ __forceinline__ void combine_fast(const LayerDev& L, const FwdBufs& B, uint32_t t, uint32_t c,
+                                             uint32_t ksg) {
+  const uint32_t k = L.k, d = L.d;
+  const size_t part = (size_t)B.nslot * d;
+  uint32_t slot[kCombK], rk[kCombK];
+  float wv[kCombK];
+  if (B.spec) {
+#pragma unroll
+    for (uint32_t i = 0; i < kCombK; i++)
+      if (i < k) {
+        slot[i] = B.slot_of[(size_t)t * k + i];
+        wv[i] = B.slot_w[(size_t)t * k + i];
+      }
+  } else {
+    uint32_t id[kCombK];
+#pragma unroll
+    for (uint32_t i = 0; i < kCombK; i++)
+      if (i < k) {
+        id[i] = B.ids[(size_t)t * k + i];
+        wv[i] = B.w[(size_t)t * k + i];
+        slot[i] = B.slot_of[(size_t)t * k + i];
+        rk[i] = i;
+      }
+    if (L.combine == 0) {  // ascending expert id: each rank's position among the token's ids
+#pragma unroll
+      for (uint32_t i = 0; i < kCombK; i++)
+        if (i < k) {
+          uint32_t pos = 0;
+#pragma unroll
+          for (uint32_t j = 0; j < kCombK; j++)
+            if (j < k) pos += (id[j] < id[i] || (id[j] == id[i] && j < i)) ? 1u : 0u;
+          rk[i] = pos;
+        }
+    }
+  }
+  float yv[kCombK][KS];
+#pragma unroll
+  for (uint32_t i = 0; i < kCombK; i++)
+    if (i < k) {
+      const bool ok = slot[i] != ~0u;
+      const float* yp = B.y + (size_t)(ok ? slot[i] : 0u) * d + c;
+#pragma unroll
+      for (uint32_t g = 0; g < KS; g++) yv[i][g] = g < ksg ? yp[g * part] : 0.0f;
+      if (!ok) yv[i][0] = __int_as_float(0x7fc00000);  // a pair the candidates missed: NaN
+    }
+  float ys[kCombK];  // each pair's down row: its slices added in order
+#pragma unroll
+  for (uint32_t i = 0; i < kCombK; i++)
+    if (i < k) {
+      float s = yv[i][0];
+#pragma unroll
+      for (uint32_t g = 1; g < KS; g++)
+        if (g < ksg) s += yv[i][g];
+      ys[i] = s;
+    }
+  float acc = 0.0f;
+  // in combine order: position r holds the pair whose rank is r
+#pragma unroll
+  for (uint32_t r = 0; r < kCombK; r++)
+    if (r < k) {
+      float y = 0.0f, w = 0.0f;
+#pragma unroll
+      for (uint32_t i = 0; i < kCombK; i++)
+        if (i < k && (B.spec ? i == r : rk[i] == r)) {
+          y = ys[i];
+          w = wv[i];
+        }
+      acc = acc + y * w;
+    }
+  B.out[(size_t)t * d + c] = acc;
+}
+
 __global__ void __launch_bounds__(256) k_combine(LayerDev L, FwdBufs B, uint32_t n, uint32_t ksg) {
   const uint32_t t = blockIdx.y, k = L.k, d = L.d;
   const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n || c >= d) return;
+  if (k <= kCombK && ksg <= kMaxKsg) {
+    combine_fast<kMaxKsg>(L, B, t, c, ksg);
+    return;
+  }
   const size_t part = (size_t)B.nslot * d;
   float acc = 0.0f;
   if (B.spec) {
