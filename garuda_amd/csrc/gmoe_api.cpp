@@ -628,7 +628,9 @@ gmoe_status run_layer(gmoe_ctx* c, Layer& L, FwdBufs B, uint32_t n, hipStream_t 
     ra.combine = D.combine;
     HIP_TRY(launch_spec_front(D, B, n, quant ? 1 : 0, st));
   } else if (front_small_ok(D, n)) {
-    HIP_TRY(launch_front_small(D, B, n, quant ? 1 : 0, true, st));
+    const bool split = n >= kFrontSplitTokens;
+    HIP_TRY(launch_front_small(D, B, n, quant ? 1 : 0, !split, st));
+    if (split) HIP_TRY(launch_dispatch_par(D, B, n, st));
   } else if (front_wide_ok(D, n)) {
     HIP_TRY(launch_front_wide(D, B, n, quant ? 1 : 0, st));
   } else {

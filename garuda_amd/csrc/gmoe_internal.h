@@ -265,6 +265,14 @@ bool front_small_ok(const LayerDev& L, uint32_t n);
 // dispatch = false: logits, ids and weights only (the exact half of the speculative front end)
 hipError_t launch_front_small(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, bool dispatch,
                               hipStream_t st);
+// The dispatch alone by one workgroup of eight waves (ne <= kParExperts: its LDS holds
+// 12 words an expert), after a front end launched without it.
+constexpr uint32_t kParExperts = 1024;
+hipError_t launch_dispatch_par(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
+// Calls of at least this many tokens run the small front end and its dispatch as two
+// launches: the launch boundary orders the routing for the dispatch, where one launch
+// needs a release fence per workgroup (measured: 56 us at 512 tokens).
+constexpr uint32_t kFrontSplitTokens = 64;
 // Front end for 64 < ne <= 256 experts: one wave per token gates it (given logits or the
 // sequential dots) and quantises its activations; the last workgroup dispatches.
 bool front_wide_ok(const LayerDev& L, uint32_t n);

@@ -365,9 +365,9 @@ __device__ void dispatch_block(const LayerDev& L, const FwdBufs& B, uint32_t n, 
 }
 
 // ---------------------------------------------------------------------------------
-// Wide front end (64 < ne <= 64 * kWideEPL experts): one wave per token gates it (lane l
-// holds experts l, l + 64, ...: gate_wave_wide) from the given logits or the reference's
-// sequential dots, and quantises its activations; the workgroup that finishes last
+// Wide front end (64 < ne <= 64 * kWideEPL experts): one workgroup of one wave per token
+// gates it (lane l holds experts l, l + 64, ...: gate_wave_wide) from the given logits or
+// the reference's sequential dots and quantises its activations; a second launch
 // dispatches every pair (dispatch_par).
 // ---------------------------------------------------------------------------------
 constexpr int kWideEPL = 4, kWideWaves = 8, kWideThreads = 64 * kWideWaves;
@@ -388,9 +388,23 @@ __device__ void dispatch_par(const LayerDev& L, const FwdBufs& B, uint32_t n, ui
   uint32_t* run = aidx + ne;      // [ne] next position per expert
   uint32_t* lh = run + ne;        // [W][ne] a round's per-chunk counts, then bases
   uint32_t* tot = lh + W * ne;    // [2]
+  // the first kParRounds rounds' pairs are read once, all loads issued together, and kept
+  // for both the counts and the placement
+  constexpr uint32_t kParRounds = 4;
+  uint32_t cid[kParRounds];
+  float cwt[kParRounds];
+#pragma unroll
+  for (uint32_t r = 0; r < kParRounds; r++) {
+    const uint32_t p = r * T + tid;
+    cid[r] = p < nk ? B.ids[p] : ~0u;
+    cwt[r] = p < nk ? B.w[p] : 0.0f;
+  }
   for (uint32_t e = tid; e < ne; e += T) cnt[e] = 0;
   __syncthreads();
-  for (uint32_t p = tid; p < nk; p += T) atomicAdd(&cnt[B.ids[p]], 1u);
+#pragma unroll
+  for (uint32_t r = 0; r < kParRounds; r++)
+    if (cid[r] != ~0u) atomicAdd(&cnt[cid[r]], 1u);
+  for (uint32_t p = kParRounds * T + tid; p < nk; p += T) atomicAdd(&cnt[B.ids[p]], 1u);
   __syncthreads();
   for (uint32_t e = tid; e < ne; e += T) {  // active slot: descending count, then id
     const uint32_t c = cnt[e];
@@ -458,23 +472,34 @@ __device__ void dispatch_par(const LayerDev& L, const FwdBufs& B, uint32_t n, ui
     for (uint32_t a = na + tid; a < ne; a += T) B.work[a].m = 0;
   if (B.ptile)
     for (uint32_t i = nt + tid; i < B.ptile_cap; i += T) B.ptile[i] = ~0u;
-  for (uint32_t c0 = 0; c0 < nk; c0 += T) {
+  for (uint32_t c0 = 0, rd = 0; c0 < nk; c0 += T, rd++) {
     for (uint32_t e = lane; e < ne; e += 64) lh[wave * ne + e] = 0;
     const uint32_t p = c0 + tid;
-    const uint32_t id = p < nk ? B.ids[p] : ~0u;
-    const float w = p < nk ? B.w[p] : 0.0f;
+    uint32_t id = ~0u;
+    float w = 0.0f;
+    if (rd < kParRounds) {
+#pragma unroll
+      for (uint32_t r = 0; r < kParRounds; r++)
+        if (r == rd) {
+          id = cid[r];
+          w = cwt[r];
+        }
+    } else if (p < nk) {
+      id = B.ids[p];
+      w = B.w[p];
+    }
     __builtin_amdgcn_wave_barrier();
     asm volatile("" ::: "memory");  // the wave's zeros land before its counts
-    uint32_t lrank = 0;
-    uint64_t todo = __ballot(id != ~0u);
-    while (todo) {
-      const uint32_t lead = (uint32_t)__builtin_ctzll(todo);
-      const uint32_t e = lane_u(id, lead);
-      const uint64_t m = __ballot(id == e);
-      if (id == e) lrank = (uint32_t)__popcll(m & below);
-      if (lane == lead) lh[wave * ne + e] = (uint32_t)__popcll(m);
-      todo &= ~m;
+    // the lanes holding this lane's expert: one ballot per bit of the id (ids past the end
+    // are ~0u and match only each other)
+    uint64_t m = __ballot(id != ~0u);
+    if (id == ~0u) m = ~m;
+    for (uint32_t bit = 1; bit < ne; bit <<= 1) {
+      const uint64_t b = __ballot((id & bit) != 0);
+      m &= (id & bit) ? b : ~b;
     }
+    const uint32_t lrank = (uint32_t)__popcll(m & below);
+    if (id != ~0u && lrank == 0) lh[wave * ne + id] = (uint32_t)__popcll(m);
     __syncthreads();
     for (uint32_t e = tid; e < ne; e += T) {  // chunk bases in pair order
       uint32_t r = run[e];
@@ -497,71 +522,73 @@ __device__ void dispatch_par(const LayerDev& L, const FwdBufs& B, uint32_t n, ui
   }
 }
 
-__global__ void __launch_bounds__(kWideThreads) k_front_wide(LayerDev L, FwdBufs B, uint32_t n, int quant) {
-  extern __shared__ uint32_t wsm[];  // [kWideWaves][2k] gating scratch, then dispatch_par's words
-  const uint32_t ne = L.ne, k = L.k, d = L.d;
-  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const uint32_t t = blockIdx.x * kWideWaves + wave;
-  if (t < n) {
-    const float* hs = B.hs + (size_t)t * d;
-    float x[kWideEPL];
+__global__ void __launch_bounds__(64) k_front_wide(LayerDev L, FwdBufs B, uint32_t n, int quant) {
+  __shared__ uint32_t gsc[64];  // gating scratch: 2k words (k <= 32)
+  const uint32_t ne = L.ne, k = L.k, d = L.d, lane = threadIdx.x, t = blockIdx.x;
+  const float* hs = B.hs + (size_t)t * d;
+  float x[kWideEPL];
 #pragma unroll
-    for (int j = 0; j < kWideEPL; j++) {
-      const uint32_t e = 64 * j + lane;
-      float acc = 0.0f;
-      if (e < ne) {
-        if (B.logits_in) {
-          acc = B.logits_in[(size_t)t * ne + e];
-        } else {  // simd/mod.rs:13-16: products added left to right from -0.0
-          const float4* wr = reinterpret_cast<const float4*>(L.router + (size_t)e * d);
-          const float4* hr = reinterpret_cast<const float4*>(hs);
-          acc = -0.0f;
-          for (uint32_t i = 0; i < d / 4; i++) {
-            const float4 a = wr[i], h = hr[i];
-            const float p0 = a.x * h.x, p1 = a.y * h.y, p2 = a.z * h.z, p3 = a.w * h.w;
-            acc = acc + p0;
-            acc = acc + p1;
-            acc = acc + p2;
-            acc = acc + p3;
-          }
+  for (int j = 0; j < kWideEPL; j++) {
+    const uint32_t e = 64 * j + lane;
+    float acc = 0.0f;
+    if (e < ne) {
+      if (B.logits_in) {
+        acc = B.logits_in[(size_t)t * ne + e];
+      } else {  // simd/mod.rs:13-16: products added left to right from -0.0
+        const float4* wr = reinterpret_cast<const float4*>(L.router + (size_t)e * d);
+        const float4* hr = reinterpret_cast<const float4*>(hs);
+        acc = -0.0f;
+        for (uint32_t i = 0; i < d / 4; i++) {
+          const float4 a = wr[i], h = hr[i];
+          const float p0 = a.x * h.x, p1 = a.y * h.y, p2 = a.z * h.z, p3 = a.w * h.w;
+          acc = acc + p0;
+          acc = acc + p1;
+          acc = acc + p2;
+          acc = acc + p3;
         }
-        B.logits[(size_t)t * ne + e] = acc;
       }
-      x[j] = acc;
+      B.logits[(size_t)t * ne + e] = acc;
     }
-    uint32_t id;
-    float w;
-    gate_wave_wide<kWideEPL>(L.gating, ne, k, x, lane, &id, &w, wsm + wave * 2 * k);
-    if (lane < k) {
-      B.ids[(size_t)t * k + lane] = id;
-      B.w[(size_t)t * k + lane] = w;
-    }
-    if (quant) {
-      const uint32_t nblk = d / 32;
-      for (uint32_t b = lane; b < nblk; b += 64) {
-        float v[32];
-        const float4* src = reinterpret_cast<const float4*>(hs + (size_t)b * 32);
+    x[j] = acc;
+  }
+  uint32_t id;
+  float w;
+  gate_wave_wide<kWideEPL>(L.gating, ne, k, x, lane, &id, &w, gsc);
+  if (lane < k) {
+    B.ids[(size_t)t * k + lane] = id;
+    B.w[(size_t)t * k + lane] = w;
+  }
+  if (quant) {
+    const uint32_t nblk = d / 32;
+    for (uint32_t b = lane; b < nblk; b += 64) {
+      float v[32];
+      const float4* src = reinterpret_cast<const float4*>(hs + (size_t)b * 32);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const float4 t4 = src[i];
-          v[4 * i] = t4.x; v[4 * i + 1] = t4.y; v[4 * i + 2] = t4.z; v[4 * i + 3] = t4.w;
-        }
-        const size_t gb = (size_t)t * nblk + b;
-        quant32(v, B.xq + gb * 32, B.xs + gb, B.xsum, gb, sum_kind_of(L.qt_gate), sum_offset_of(L.qt_gate));
+      for (int i = 0; i < 8; i++) {
+        const float4 t4 = src[i];
+        v[4 * i] = t4.x; v[4 * i + 1] = t4.y; v[4 * i + 2] = t4.z; v[4 * i + 3] = t4.w;
       }
+      const size_t gb = (size_t)t * nblk + b;
+      quant32(v, B.xq + gb * 32, B.xs + gb, B.xsum, gb, sum_kind_of(L.qt_gate), sum_offset_of(L.qt_gate));
     }
   }
-  // every workgroup's ids and weights are in memory before its count is taken; the last
-  // one to count dispatches
-  __threadfence();
-  __syncthreads();
-  __shared__ uint32_t last;
-  if (tid == 0) last = atomicAdd(B.done, 1u) == gridDim.x - 1 ? 1u : 0u;
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  dispatch_par(L, B, n, wsm + kWideWaves * 2 * k);
-  if (tid == 0) *B.done = 0;
+}
+
+// The dispatch alone (dispatch_par over the routing in memory), for ne <= kParExperts.
+__global__ void __launch_bounds__(kWideThreads) k_dispatch_par(LayerDev L, FwdBufs B, uint32_t n) {
+  extern __shared__ uint32_t dsm_par[];  // [(4 + kWideWaves) * ne + 2]
+  dispatch_par(L, B, n, dsm_par);
+}
+
+hipError_t launch_dispatch_par(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  if (L.ne > kParExperts) return hipErrorInvalidValue;
+  const size_t shm = ((4 + kWideWaves) * (size_t)L.ne + 2) * 4;
+  static const bool attr =
+      hipFuncSetAttribute((const void*)k_dispatch_par, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024) ==
+      hipSuccess;
+  (void)attr;
+  hipLaunchKernelGGL(k_dispatch_par, dim3(1), dim3(kWideThreads), shm, st, L, B, n);
+  return hipGetLastError();
 }
 
 bool front_wide_ok(const LayerDev& L, uint32_t n) {
@@ -569,10 +596,9 @@ bool front_wide_ok(const LayerDev& L, uint32_t n) {
 }
 
 hipError_t launch_front_wide(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st) {
-  const size_t shm = ((size_t)kWideWaves * 2 * L.k + (4 + kWideWaves) * (size_t)L.ne + 2) * 4;
-  hipLaunchKernelGGL(k_front_wide, dim3((n + kWideWaves - 1) / kWideWaves), dim3(kWideThreads), shm, st, L, B, n,
-                     quant);
-  return hipGetLastError();
+  hipLaunchKernelGGL(k_front_wide, dim3(n), dim3(64), 0, st, L, B, n, quant);
+  if (hipError_t e = hipGetLastError()) return e;
+  return launch_dispatch_par(L, B, n, st);
 }
 
 constexpr uint32_t kDispatchThreads = 256;
@@ -700,49 +726,58 @@ __device__ void dispatch_wave(const FwdBufs& B, Ptr eptr, uint32_t ne, uint32_t 
 
 // ---------------------------------------------------------------------------------
 // Fused front end: router logits, gating, the int8 activation quantiser and the
-// dispatch in one launch of one workgroup per token (ne <= 64 experts).
+// dispatch in one launch (ne <= 64 experts), tpw tokens a workgroup (front_tokens).
 //
 // A logit is the reference's sequential f32 dot (simd/mod.rs:13-16): products w*h, each
 // rounded, added left to right from -0.0. Its latency is its d dependent adds, so wave
-// 0 (lane e = expert e) does only those adds while eight producer waves make the
-// products into LDS ahead of it. K is cut into sections as long as two LDS halves of
-// [ne][section] allow (2432 values for 8 experts), and the two sides meet at a barrier
-// once per section: while wave 0 adds section s from one half, the producers fill the
-// other with section s+1 (and quantise the token's activations during the last one).
-// Wave 0 reads its products 32 at a time from two fixed register buffers, each batch
-// fetched one batch ahead by an unconditional load, so it waits only for the batch it
-// adds. Gating follows per token. The workgroup that finishes last (a device-wide
+// 0 (lane l = token l / ne, expert l % ne: one chain per lane) does only those adds while
+// eight producer waves make the products into LDS ahead of it. K is cut into sections as
+// long as two LDS halves of [tpw * ne][section] allow, and the two sides meet at a
+// barrier once per section: while wave 0 adds section s from one half, the producers
+// fill the other with section s+1 (and quantise the tokens' activations during the last
+// one). Wave 0 reads its products 32 at a time from two fixed register buffers, each
+// batch fetched one batch ahead by an unconditional load, so it waits only for the batch
+// it adds. Then wave w gates token w. The workgroup that finishes last (a device-wide
 // counter taken after a release fence) does the dispatch over every token's routing and
 // puts the counter back to zero.
 // ---------------------------------------------------------------------------------
 
 constexpr int kFrontExperts = 64, kFrontProdWaves = 8, kFrontThreads = 64 * (1 + kFrontProdWaves);
-constexpr uint32_t kFrontProdBytes = 156 * 1024;  // both LDS halves of products (the rest: < 1 KB)
+constexpr uint32_t kFrontProdBytes = 150 * 1024;  // both LDS halves of products (the rest: < 4 KB)
 constexpr int kFrontItems = 12;                   // float4 products a producer lane has in flight
+constexpr uint32_t kFrontMaxTok = 8;
 
-// Section length for ne experts: the longest multiple of 128 whose two halves fit.
-static inline uint32_t front_section(uint32_t ne, uint32_t d) {
-  const uint32_t sec = (kFrontProdBytes / (8 * ne) - 4) & ~127u;
+// Tokens a workgroup: one until the workgroups would outnumber the CUs (the chains are
+// latency-bound, so spreading them wins), then as many as keep about 256 workgroups,
+// within the 64 lanes of the chain wave.
+static inline uint32_t front_tokens(uint32_t ne, uint32_t n) {
+  return min(min(kFrontMaxTok, max(1u, 64u / ne)), max(1u, n / 256u));
+}
+
+// Section length for `rows` chains: the longest multiple of 128 whose two halves fit.
+static inline uint32_t front_section(uint32_t rows, uint32_t d) {
+  const uint32_t sec = (kFrontProdBytes / (8 * rows) - 4) & ~127u;
   return sec < d ? sec : d;
 }
 
 __global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, uint32_t n, int quant, int dispatch,
-                                                          uint32_t sec) {
+                                                          uint32_t sec, uint32_t tpw) {
   extern __shared__ float fs[];
-  const uint32_t ne = L.ne, d = L.d, k = L.k, t = blockIdx.x, row = sec + 4;  // padded row of one expert
-  float* prod = fs;                                                 // [2][ne][row]
-  uint32_t* scratch = reinterpret_cast<uint32_t*>(prod + 2 * ne * row);  // [2k] gating
+  const uint32_t ne = L.ne, d = L.d, k = L.k, nr = tpw * ne, row = sec + 4;  // padded row of one chain
+  const uint32_t t0 = blockIdx.x * tpw, ntok = min(tpw, n - t0);             // this workgroup's tokens
+  float* prod = fs;                                                          // [2][nr][row]
+  float* lg = prod + 2 * nr * row;                                           // [nr] logits
+  uint32_t* scratch = reinterpret_cast<uint32_t*>(lg + nr);                  // [tpw][2k] gating
+  uint32_t* last = scratch + tpw * 2 * k;                                     // [1] the last workgroup
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const uint32_t nsec = (d + sec - 1) / sec;
-  const float* hs = B.hs + (size_t)t * d;
-  // producer wave pw (1..8) makes the rows of experts pw-1, pw-1+8, ...; its items are
-  // (expert, float4 column) pairs, kFrontItems of them in flight per lane
+  // producer wave pw (1..8) makes the chains pw-1, pw-1+8, ... of the workgroup's valid
+  // tokens; its items are (chain, float4 column) pairs, kFrontItems of them in flight per lane
   auto produce = [&](uint32_t s) {
-    const uint32_t k0 = s * sec, len4 = min(sec, d - k0) / 4, e0 = wave - 1;
-    const uint32_t nexp = e0 < ne ? (ne - e0 + kFrontProdWaves - 1) / kFrontProdWaves : 0;
-    const uint32_t total = nexp * len4;
-    const float4* xr = reinterpret_cast<const float4*>(hs + k0);
-    float* half = prod + (s & 1) * ne * row;
+    const uint32_t k0 = s * sec, len4 = min(sec, d - k0) / 4, c0 = wave - 1, nrv = ntok * ne;
+    const uint32_t nch = c0 < nrv ? (nrv - c0 + kFrontProdWaves - 1) / kFrontProdWaves : 0;
+    const uint32_t total = nch * len4;
+    float* half = prod + (s & 1) * nr * row;
     for (uint32_t base = 0; base < total; base += 64 * kFrontItems) {
       float4 wv[kFrontItems], xv[kFrontItems];
       uint32_t off[kFrontItems];
@@ -750,10 +785,11 @@ __global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, 
       for (int i = 0; i < kFrontItems; i++) {
         const uint32_t q = base + lane + 64 * i;
         if (q < total) {
-          const uint32_t el = q / len4, j = q - el * len4, e = e0 + kFrontProdWaves * el;
+          const uint32_t cl = q / len4, j = q - cl * len4, ch = c0 + kFrontProdWaves * cl;
+          const uint32_t tt = ch / ne, e = ch - tt * ne;
           wv[i] = reinterpret_cast<const float4*>(L.router + (size_t)e * d + k0)[j];
-          xv[i] = xr[j];
-          off[i] = e * row + 4 * j;
+          xv[i] = reinterpret_cast<const float4*>(B.hs + (size_t)(t0 + tt) * d + k0)[j];
+          off[i] = ch * row + 4 * j;
         }
       }
 #pragma unroll
@@ -765,22 +801,22 @@ __global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, 
     }
   };
   auto quantise = [&] {
-    const uint32_t nblk = d / 32;
-    for (uint32_t b = tid - 64; b < nblk; b += 64 * kFrontProdWaves) {
+    const uint32_t nblk = d / 32, items = ntok * nblk;
+    for (uint32_t q = tid - 64; q < items; q += 64 * kFrontProdWaves) {
+      const uint32_t tt = q / nblk, b = q - tt * nblk;
       float v[32];
-      const float4* src = reinterpret_cast<const float4*>(hs + (size_t)b * 32);
+      const float4* src = reinterpret_cast<const float4*>(B.hs + (size_t)(t0 + tt) * d + (size_t)b * 32);
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         float4 t4 = src[i];
         v[4 * i] = t4.x; v[4 * i + 1] = t4.y; v[4 * i + 2] = t4.z; v[4 * i + 3] = t4.w;
       }
-      const size_t gb = (size_t)t * nblk + b;
+      const size_t gb = (size_t)(t0 + tt) * nblk + b;
       quant32(v, B.xq + gb * 32, B.xs + gb, B.xsum, gb, sum_kind_of(L.qt_gate), sum_offset_of(L.qt_gate));
     }
   };
-  float x = 0.0f;  // wave 0, lane e < ne: the logit of expert e
   if (B.logits_in) {
-    if (wave == 0 && lane < ne) x = B.logits_in[(size_t)t * ne + lane];
+    if (wave == 0 && lane < ntok * ne) lg[lane] = B.logits_in[(size_t)t0 * ne + lane];
     if (quant && wave != 0) quantise();
   } else {
     if (wave != 0) produce(0);
@@ -788,10 +824,10 @@ __global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, 
     float acc = -0.0f;
     for (uint32_t s = 0; s < nsec; s++) {
       if (wave == 0) {
-        if (lane < ne) {
+        if (lane < nr) {
           // nb batches of 8 float4; sections are multiples of 128 values, so nb is even
           const uint32_t nb = min(sec, d - s * sec) / 32;
-          const float4* src = reinterpret_cast<const float4*>(prod + (s & 1) * ne * row + lane * row);
+          const float4* src = reinterpret_cast<const float4*>(prod + (s & 1) * nr * row + lane * row);
           float4 ba[8], bb[8];
           auto fetch = [&](float4* dst, uint32_t b) {
 #pragma unroll
@@ -821,38 +857,44 @@ __global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, 
       }
       __syncthreads();
     }
-    if (wave == 0) x = acc;
+    if (wave == 0 && lane < nr) lg[lane] = acc;
   }
-  // the producer waves are done (their last stores were the quantised activations)
-  if (wave != 0) return;
-  if (lane < ne) B.logits[(size_t)t * ne + lane] = x;
-  uint32_t id;
-  float w;
-  gate_wave(L.gating, ne, k, x, lane, &id, &w, scratch);
-  if (lane < k) {
-    B.ids[(size_t)t * k + lane] = id;
-    B.w[(size_t)t * k + lane] = w;
+  __syncthreads();
+  // wave w gates token t0 + w
+  if (wave < ntok) {
+    const uint32_t t = t0 + wave;
+    const float x = lane < ne ? lg[wave * ne + lane] : 0.0f;
+    if (lane < ne) B.logits[(size_t)t * ne + lane] = x;
+    uint32_t id;
+    float w;
+    gate_wave(L.gating, ne, k, x, lane, &id, &w, scratch + wave * 2 * k);
+    if (lane < k) {
+      B.ids[(size_t)t * k + lane] = id;
+      B.w[(size_t)t * k + lane] = w;
+    }
   }
   if (!dispatch) return;
-  if (n == 1) {  // the only workgroup: pair p (< k) is rank p, which lane p holds
-    dispatch_wave(B, [&](int p) { return L.eptr[p * ne + lane]; }, ne, k, k, lane, [&](uint32_t, uint32_t* pid, float* pw) {
-      *pid = id;
-      *pw = w;
-    });
+  const auto pair = [&](uint32_t p, uint32_t* pid, float* pw) {
+    *pid = B.ids[p];
+    *pw = B.w[p];
+  };
+  if (gridDim.x == 1) {  // the only workgroup: its routing is in memory after the barrier
+    __syncthreads();
+    if (wave == 0) dispatch_wave(B, [&](int p) { return L.eptr[p * ne + lane]; }, ne, k, n * k, lane, pair);
     return;
   }
-  // every workgroup's ids and weights are in memory before its count is taken
-  __threadfence();
-  uint32_t prev = 0;
-  if (lane == 0) prev = atomicAdd(B.done, 1u);
-  if (lane_u(prev, 0) == n - 1) {
+  // every workgroup's ids, weights and activation codes are in memory before its count
+  // is taken: the barrier orders the waves' stores before thread 0's release fence
+  __syncthreads();
+  if (tid == 0) {
     __threadfence();
-    dispatch_wave(B, [&](int p) { return L.eptr[p * ne + lane]; }, ne, k, n * k, lane, [&](uint32_t p, uint32_t* pid, float* pw) {
-      *pid = B.ids[p];
-      *pw = B.w[p];
-    });
-    if (lane == 0) *B.done = 0;
+    *last = atomicAdd(B.done, 1u) == gridDim.x - 1 ? 1u : 0u;
   }
+  __syncthreads();
+  if (!*last || wave != 0) return;
+  __threadfence();
+  dispatch_wave(B, [&](int p) { return L.eptr[p * ne + lane]; }, ne, k, n * k, lane, pair);
+  if (lane == 0) *B.done = 0;
 }
 
 bool front_small_ok(const LayerDev& L, uint32_t n) {
@@ -861,12 +903,13 @@ bool front_small_ok(const LayerDev& L, uint32_t n) {
 
 hipError_t launch_front_small(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, bool dispatch,
                               hipStream_t st) {
-  const uint32_t sec = front_section(L.ne, L.d);
-  const size_t shm = ((size_t)2 * L.ne * (sec + 4) + 2 * L.k) * 4;
+  const uint32_t tpw = front_tokens(L.ne, n), sec = front_section(tpw * L.ne, L.d);
+  const size_t shm = ((size_t)2 * tpw * L.ne * (sec + 4) + tpw * L.ne + (size_t)tpw * 2 * L.k + 1) * 4;
   static const bool attr =
       hipFuncSetAttribute((const void*)k_front, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
   (void)attr;
-  hipLaunchKernelGGL(k_front, dim3(n), dim3(kFrontThreads), shm, st, L, B, n, quant, dispatch ? 1 : 0, sec);
+  hipLaunchKernelGGL(k_front, dim3((n + tpw - 1) / tpw), dim3(kFrontThreads), shm, st, L, B, n, quant,
+                     dispatch ? 1 : 0, sec, tpw);
   return hipGetLastError();
 }
 
@@ -1049,6 +1092,7 @@ hipError_t launch_route(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStre
 }
 
 hipError_t launch_dispatch(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  if (L.ne <= kParExperts) return launch_dispatch_par(L, B, n, st);
   const size_t shm = (kDispatchThreads + 3 * (size_t)L.ne + 2) * 4;
   if (shm > 160 * 1024) return hipErrorInvalidValue;  // registration bounds ne far below this
   static const bool attr =

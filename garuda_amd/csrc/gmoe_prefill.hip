@@ -495,6 +495,7 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = P[i][j][r] = 0.0f;
   const f32x16 zero = acc[0][0];
+  const bool two = m > 32;  // the second 32-token tile holds tokens
 
   // one barrier per chunk: chunk k computes from buffer k % 2 while chunk k+1 loads into
   // the other; the barrier after it says both that every wave is done reading buffer
@@ -529,6 +530,7 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
         for (int rt = 0; rt < 2; rt++)
 #pragma unroll
           for (int tt = 0; tt < 2; tt++) {
+            if (tt == 1 && !two) continue;  // a tile of at most 32 tokens: its second half is padding
             if constexpr (T::SU16 == 0) {
               acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[tt][0], bw[rt], acc[rt][tt], 0, 0, 0);
               acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[tt][1], bw[rt], acc[rt][tt], 0, 0, 0);
@@ -545,8 +547,9 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
               const float sc = D::template scale<C, S>(wb + row[rt]);
 #pragma unroll
               for (int tt = 0; tt < 2; tt++)
+                if (tt == 0 || two)
 #pragma unroll
-                for (int r = 0; r < 16; r++) acc[rt][tt][r] = __builtin_fmaf(sc, P[rt][tt][r], acc[rt][tt][r]);
+                  for (int r = 0; r < 16; r++) acc[rt][tt][r] = __builtin_fmaf(sc, P[rt][tt][r], acc[rt][tt][r]);
             }
           }
           // short scale groups: keep the scheduler from overlapping the next group's
@@ -562,6 +565,7 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
         const uint8_t* sb = xb + XBYTES;
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
+          if (tt == 1 && !two) continue;
           // sums 8h'.. of token t (h' = h with 16 sub-blocks; with 8 the upper lanes' B is zero)
           const uint32_t t = 32 * tt + l32, e = NS == 16 ? h : 0;
           const half8 sh = *reinterpret_cast<const half8*>(sb + ((0 * kPfTok + t) * (NS / 8) + e) * 16);
