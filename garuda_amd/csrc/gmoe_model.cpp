@@ -198,8 +198,30 @@ void gmoe_model_destroy(gmoe_model* m) {
   delete m;
 }
 
+size_t gmoe_model_trace_floats(const gmoe_model* m, uint32_t n) {
+  if (!m) return 0;
+  const size_t per_layer = 7 * (size_t)m->d + 2 * (size_t)m->qd + 2 * (size_t)m->kvd;
+  return (size_t)n * (m->n_layers * per_layer + 2 * (size_t)m->d);
+}
+
+static gmoe_status model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs, const uint32_t* tokens,
+                                uint32_t* next, float* logits, float* trace);
+
 gmoe_status gmoe_model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs, const uint32_t* tokens, uint32_t* next,
                               float* logits) {
+  return model_decode(m, n, seqs, tokens, next, logits, nullptr);
+}
+
+gmoe_status gmoe_model_decode_trace(gmoe_model* m, uint32_t n, const uint32_t* seqs, const uint32_t* tokens,
+                                    uint32_t* next, float* logits, float* trace) {
+  if (!trace) return mfail(GMOE_ERR_INFERENCE, "null trace buffer");
+  return model_decode(m, n, seqs, tokens, next, logits, trace);
+}
+
+}  // extern "C"
+
+static gmoe_status model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs, const uint32_t* tokens,
+                                uint32_t* next, float* logits, float* trace) {
   if (!m || !seqs || !tokens || !next) return mfail(GMOE_ERR_INFERENCE, "null model, sequences, tokens or output");
   if (n == 0 || n > kModelMaxBatch)
     return mfail(GMOE_ERR_INFERENCE, "a decode step takes 1 to %u sequences, not %u", kModelMaxBatch, n);
@@ -222,25 +244,50 @@ gmoe_status gmoe_model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs, c
   M_TRY(hipSetDevice(ctx_device(m->ctx)));
   hipStream_t st = ctx_stream(m->ctx);
   const uint32_t d = m->d;
+  // trace: n rows of `width` floats from `src` (rows `pitch` floats apart) at the trace's
+  // running offset
+  size_t at = 0;
+  auto rec = [&](const float* src, uint32_t width, uint32_t pitch) -> hipError_t {
+    if (!trace) return hipSuccess;
+    const hipError_t e = hipMemcpy2DAsync(trace + at, (size_t)width * 4, src, (size_t)pitch * 4, (size_t)width * 4,
+                                          n, hipMemcpyDeviceToHost, st);
+    at += (size_t)n * width;
+    return e;
+  };
   M_TRY(launch_embed(tk, n, m->table, d, m->x, st));
   for (uint32_t l = 0; l < m->n_layers; l++) {
     // h = norm(x + previous layer's MoE output, attn_norm)
     M_TRY(launch_add_norm(m->x, l ? m->y : nullptr, m->norms + (2 * (size_t)l) * d, n, d, m->eps, m->h, st));
+    M_TRY(rec(m->x, d, d));
+    M_TRY(rec(m->h, d, d));
     if (!m->wqkv.empty()) {
       const uint32_t row = m->qd + 2 * m->kvd;
       S_TRY(gmoe_dense_forward_async(m->ctx, m->wqkv[l], m->h, n, m->qkv, st));
+      M_TRY(rec(m->qkv, m->qd, row));
+      M_TRY(rec(m->qkv + m->qd, m->kvd, row));
+      M_TRY(rec(m->qkv + m->qd + m->kvd, m->kvd, row));
       S_TRY(kv_attend(m->kv, l, seqs, n, m->qkv, m->qkv + m->qd, m->qkv + m->qd + m->kvd, row, row, m->cx, st));
     } else {
       S_TRY(gmoe_dense_forward_async(m->ctx, m->wq[l], m->h, n, m->q, st));
       S_TRY(gmoe_dense_forward_async(m->ctx, m->wk[l], m->h, n, m->k, st));
       S_TRY(gmoe_dense_forward_async(m->ctx, m->wv[l], m->h, n, m->v, st));
+      M_TRY(rec(m->q, m->qd, m->qd));
+      M_TRY(rec(m->k, m->kvd, m->kvd));
+      M_TRY(rec(m->v, m->kvd, m->kvd));
       S_TRY(gmoe_attention_async(m->kv, l, seqs, n, m->q, m->k, m->v, m->cx, st));
     }
+    M_TRY(rec(m->cx, m->qd, m->qd));
     S_TRY(gmoe_dense_forward_async(m->ctx, m->wo[l], m->cx, n, m->ao, st));
+    M_TRY(rec(m->ao, d, d));
     M_TRY(launch_add_norm(m->x, m->ao, m->norms + (2 * (size_t)l + 1) * d, n, d, m->eps, m->h, st));
+    M_TRY(rec(m->x, d, d));
+    M_TRY(rec(m->h, d, d));
     S_TRY(gmoe_ffn_forward_async(m->ctx, m->moe[l], m->h, nullptr, n, m->y, nullptr, nullptr, st));
+    M_TRY(rec(m->y, d, d));
   }
   M_TRY(launch_add_norm(m->x, m->y, m->norms + 2 * (size_t)m->n_layers * d, n, d, m->eps, m->h, st));
+  M_TRY(rec(m->x, d, d));
+  M_TRY(rec(m->h, d, d));
   S_TRY(gmoe_dense_forward_async(m->ctx, m->out_id, m->h, n, m->logits, st));
   M_TRY(launch_argmax(m->logits, n, m->vocab, m->next, st));
   M_TRY(hipMemcpyAsync(m->pin_next, m->next, n * 4, hipMemcpyDeviceToHost, st));
@@ -249,5 +296,3 @@ gmoe_status gmoe_model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs, c
   std::memcpy(next, m->pin_next, n * 4);
   return GMOE_OK;
 }
-
-}  // extern "C"

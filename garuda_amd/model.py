@@ -73,6 +73,34 @@ class DecodeModel:
                                        nxt.ctypes.data_as(u32p), _fp(logits) if logits is not None else None))
         return (nxt, logits) if want_logits else nxt
 
+    TRACE_KEYS = ("x", "h_attn", "q", "k", "v", "context", "attn_out", "x_mid", "h_ffn", "moe_out")
+
+    def decode_step_trace(self, seqs, tokens):
+        """decode_step that also returns every layer's activations (gmoe_model_decode_trace):
+        (next, logits, layers, final), layers[l] a dict of TRACE_KEYS -> [n, width] arrays,
+        final a dict of x (the last residual) and h (its output norm)."""
+        seqs, tokens = _u32(seqs), _u32(tokens)
+        n = seqs.size
+        if tokens.size != n:
+            raise ValueError("one token per sequence")
+        nxt = np.zeros(n, dtype=np.uint32)
+        logits = np.empty((n, self.vocab), dtype=np.float32)
+        trace = np.empty(lib().gmoe_model_trace_floats(self._h, n), dtype=np.float32)
+        u32p = C.POINTER(C.c_uint32)
+        _check(lib().gmoe_model_decode_trace(self._h, n, seqs.ctypes.data_as(u32p), tokens.ctypes.data_as(u32p),
+                                             nxt.ctypes.data_as(u32p), _fp(logits), _fp(trace)))
+        qd, kvd, d = self.kv.n_heads * self.kv.hd, self.kv.kv_dim, self.d
+        widths = (d, d, qd, kvd, kvd, qd, d, d, d, d)
+        at, layers = 0, []
+        for _ in range(self.n_layers):
+            rec = {}
+            for key, w in zip(self.TRACE_KEYS, widths):
+                rec[key] = trace[at:at + n * w].reshape(n, w)
+                at += n * w
+            layers.append(rec)
+        final = {"x": trace[at:at + n * d].reshape(n, d), "h": trace[at + n * d:at + 2 * n * d].reshape(n, d)}
+        return nxt, logits, layers, final
+
     def close(self) -> None:
         if getattr(self, "_h", None):
             lib().gmoe_model_destroy(self._h)

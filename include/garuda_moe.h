@@ -438,6 +438,16 @@ void gmoe_model_destroy(gmoe_model* model);
  * expert is not resident. Synchronous: returns when next (and logits) are written. */
 gmoe_status gmoe_model_decode(gmoe_model* model, uint32_t n, const uint32_t* seqs, const uint32_t* tokens,
                               uint32_t* next, float* logits);
+/* Diagnostic, with no counterpart in the reference: gmoe_model_decode that also copies
+ * every layer's activations into trace (host, gmoe_model_trace_floats(model, n) floats),
+ * for checks of each layer against a restatement fed the device's own inputs. Per layer,
+ * each block n rows: the residual x entering it, h = rmsnorm(x) * attn_norm, q [q_dim],
+ * k [kv_dim], v [kv_dim] (before rotation), the attention context [q_dim], wo(context),
+ * x after the attention's residual add, h = rmsnorm(x) * ffn_norm, the MoE layer's output;
+ * then the final residual and rmsnorm(x) * output_norm. */
+size_t gmoe_model_trace_floats(const gmoe_model* model, uint32_t n);
+gmoe_status gmoe_model_decode_trace(gmoe_model* model, uint32_t n, const uint32_t* seqs, const uint32_t* tokens,
+                                    uint32_t* next, float* logits, float* trace);
 
 /* ---- single steps of the path, for parity tests (host pointers, synchronous) ---- */
 
