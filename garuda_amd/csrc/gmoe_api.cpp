@@ -606,6 +606,10 @@ gmoe_status run_layer(gmoe_ctx* c, Layer& L, FwdBufs B, uint32_t n, hipStream_t 
   for (uint32_t e = 0; e < L.ne; e++) resident &= L.slot[e] >= 0;
   const bool spec = !pf && !pq && !B.logits_in && resident && spec_ok(D, n);
   B.spec = spec ? 1u : 0u;
+  // top-k <= 2 at one or two tokens: the down product adds into the output (zeroed by the
+  // front end), no combine launch
+  const bool fuse = !pf && !pq && down_atomic_ok(D, n) && (spec || front_small_ok(D, n));
+  B.fuse_out = fuse ? 1u : 0u;
   if (!spec) B.nslot = n * L.k;
   RouteArgs ra{};
   if (spec) {
@@ -649,12 +653,14 @@ gmoe_status run_layer(gmoe_ctx* c, Layer& L, FwdBufs B, uint32_t n, hipStream_t 
   }
   HIP_TRY(pf ? launch_prefill_gateup(D, B, n, st) : pq ? launch_pq_gateup(D, B, n, st) : launch_gateup(D, B, n, ra, st));
   if (timed) HIP_TRY(hipEventRecord(tm.b, st));
-  HIP_TRY(pf ? launch_prefill_down(D, B, n, ksg, st) : pq ? launch_pq_down(D, B, n, ksg, st) : launch_down(D, B, n, st));
+  HIP_TRY(pf ? launch_prefill_down(D, B, n, ksg, st)
+             : pq ? launch_pq_down(D, B, n, ksg, st)
+                  : fuse ? launch_down_atomic(D, B, n, st) : launch_down(D, B, n, st));
   if (timed) {
     HIP_TRY(hipEventRecord(tm.c, st));
     c->pending.push_back(tm);
   }
-  HIP_TRY(launch_combine(D, B, n, ksg, st));
+  if (!fuse) HIP_TRY(launch_combine(D, B, n, ksg, st));
   L.last_stream = st;
   return GMOE_OK;
 }

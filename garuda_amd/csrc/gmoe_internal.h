@@ -173,6 +173,8 @@ struct FwdBufs {
   uint32_t* done;        // [1] workgroups of the front end that have finished; 0 between calls
   uint32_t nslot;        // rows of the slot-indexed arrays; y slices are nslot*d apart
   uint32_t* cand;        // [n][ne] speculative front end: each token's candidate experts, ~0u-padded
+  uint32_t fuse_out;     // 1: the front end zeroes out and the down product adds into it
+                         // (launch_down_atomic); no combine launch
   uint32_t spec;         // 1: slots hold candidate pairs; slot_of / slot_w hold the combine's
                          // (slot, weight) per (token, position in combine order), written by
                          // the exact routing (RouteArgs::comb_slot, comb_w)
@@ -223,6 +225,8 @@ constexpr int kDnKS = 2;
 template <int QT> hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra,
                                           hipStream_t st);
 template <int QT> hipError_t units_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
+// Down with the combine folded in (top-k <= 2, out zeroed by the front end beforehand).
+template <int QT> hipError_t units_down_atomic(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 
 // Prefill products (f32 math) on MFMA over token tiles of kPfTok (gmoe_prefill.hip,
 // built once per type; F32 weights are not supported). prefill_ok says when the path
@@ -288,6 +292,11 @@ hipError_t launch_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const 
 hipError_t launch_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st, uint32_t ksg = 0);
 uint32_t dense_ksg(const LayerDev& L);
 hipError_t launch_combine(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
+// The down product adding its weighted rows into the zeroed output (launch_down_atomic)
+// applies for top-k <= 2 while no expert takes more tokens than a workgroup stages at once.
+constexpr uint32_t kFuseMaxTokens = 2;
+bool down_atomic_ok(const LayerDev& L, uint32_t n);
+hipError_t launch_down_atomic(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 // Prefill path: whether it applies (f32 math, at least kPfMinSlots slots, supported
 // types and shapes), the per-slot fp16 gather of the activations, and the products.
 bool prefill_ok(const LayerDev& L, uint32_t n);

@@ -815,6 +815,8 @@ __global__ void __launch_bounds__(kFrontThreads) k_front(LayerDev L, FwdBufs B, 
       quant32(v, B.xq + gb * 32, B.xs + gb, B.xsum, gb, sum_kind_of(L.qt_gate), sum_offset_of(L.qt_gate));
     }
   };
+  if (B.fuse_out)  // the down product adds into the tokens' output rows
+    for (uint32_t c = tid; c < ntok * d; c += kFrontThreads) B.out[(size_t)t0 * d + c] = 0.0f;
   if (B.logits_in) {
     if (wave == 0 && lane < ntok * ne) lg[lane] = B.logits_in[(size_t)t0 * ne + lane];
     if (quant && wave != 0) quantise();
@@ -958,6 +960,8 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
   const uint8_t* ep[3] = {nullptr, nullptr, nullptr};
   if (wave == 0 && lane < ne)
     for (int p = 0; p < 3; p++) ep[p] = L.eptr[p * ne + lane];
+  if (B.fuse_out)  // the down product adds into the token's output row
+    for (uint32_t c = tid; c < d; c += kSpecThreads) B.out[(size_t)t * d + c] = 0.0f;
   const uint32_t nblk = d / 32, qb = tid - 64;  // block of thread tid >= 64
   float qv[32];
   const bool qown = quant && tid >= 64 && qb < nblk && nblk <= kSpecThreads - 64;
@@ -1547,6 +1551,17 @@ uint32_t dense_ksg(const LayerDev& L) {
   const uint32_t ksg = (960 + tiles - 1) / tiles;
   const uint32_t cap = max(1u, row_units(un, L.f) / kDnKS);
   return max(1u, min(min(ksg, cap), kMaxKsg));
+}
+
+bool down_atomic_ok(const LayerDev& L, uint32_t n) { return L.k <= 2 && n >= 1 && n <= kFuseMaxTokens; }
+
+hipError_t launch_down_atomic(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  switch (L.qt_down) {
+#define DN(T) case T: return units_down_atomic<T>(L, B, n, st);
+    DN(Q4_K) DN(Q5_K) DN(Q6_K) DN(Q3_K) DN(Q2_K) DN(Q8_0) DN(Q4_0) DN(F16) DN(F32)
+#undef DN
+  }
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st, uint32_t ksg_in) {

@@ -331,6 +331,82 @@ k_dn_units(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32_
   }
 }
 
+// Down with the combine folded in, for layers of top-k <= 2: a workgroup of KS waves takes
+// one 64-row tile of one expert over the whole K range (wave w its w-th share of the
+// units), adds the waves' row sums in wave order, and adds y * w into the zeroed output
+// with an atomic add. A token's output element then receives exactly k <= 2 terms; float
+// addition is commutative, so 0 + p1 + p2 is the same in either arrival order and the
+// result is the combine's (llama/mod.rs:974-997, moe/mod.rs:104-109) bit for bit, run
+// to run. Weights: slot_w[slot], or with spec set the exact routing's (slot, weight)
+// per (token, position), a candidate slot no routed pair names adding nothing and a
+// routed pair the candidates missed giving NaN, as the combine does.
+// grid.x = row tiles of d, grid.z = active-expert slot.
+template <int QT, bool PACKED, int KS>
+__global__ void __launch_bounds__(64 * KS, 2)
+k_dn_atomic(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32_t d, uint32_t mt,
+            const uint32_t* __restrict__ slot_tok, const uint32_t* __restrict__ slot_of,
+            const float* __restrict__ slot_w, uint32_t k, uint32_t spec, const int8_t* __restrict__ hq,
+            const float* __restrict__ hsc, const uint32_t* __restrict__ hsum, const float* __restrict__ hf,
+            float* __restrict__ out) {
+  constexpr int U = UT_<QT>::U;
+  extern __shared__ uint4 dsm[];
+  float* accs = reinterpret_cast<float*>(dsm);  // [KS][mt][64]
+  uint32_t* rows = reinterpret_cast<uint32_t*>(accs + KS * mt * 64);  // [mt] slot of each chunk member
+  uint8_t* acts = reinterpret_cast<uint8_t*>(rows + ((mt + 3) & ~3u));
+  for (uint32_t a = blockIdx.z; a < ne; a += gridDim.z) {
+  const ExpertWork* W = work + a;
+  const uint32_t m_all = W->m;
+  if (m_all == 0) break;
+  const uint32_t s0 = W->s0;
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t r0 = blockIdx.x * kTileRows;
+  const uint32_t nblk = unit_blocks<QT>(f), nunit = unit_count<QT>(f);
+  const uint32_t u0 = (nunit * wave) / KS, u1 = (nunit * (wave + 1)) / KS;
+  const uint32_t per = ActLds<QT, PACKED>::per_token(f);
+  float* my = accs + wave * mt * 64 + lane;
+  UnitStream<QT> st(W->w[2] + (size_t)blockIdx.x * nunit * kTileRows * U, u0, u1, lane);
+  for (uint32_t c0 = 0; c0 < m_all; c0 += mt) {
+    const uint32_t m = min(mt, m_all - c0);
+    st.prime();
+    for (uint32_t t = threadIdx.x; t < m; t += blockDim.x) rows[t] = s0 + c0 + t;
+    for (uint32_t t = 0; t < m; t++) my[t * 64] = 0.0f;
+    __syncthreads();
+    stage_acts<QT, PACKED>(acts, f, m, rows, f, 0, hq, hsc, hsum, hf);
+    __syncthreads();
+    st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED>(w, acts, per, f, u, 0, nblk, my, m); });
+    __syncthreads();
+    if (wave == 0) {
+      const uint32_t row = r0 + lane;
+      for (uint32_t t = 0; t < m; t++) {
+        float y = accs[t * 64 + lane];
+#pragma unroll
+        for (int w2 = 1; w2 < KS; w2++) y += accs[(w2 * mt + t) * 64 + lane];
+        const uint32_t slot = s0 + c0 + t, tok = slot_tok[slot];
+        float wt = 0.0f, miss = 0.0f;
+        bool routed = !spec;
+        if (spec) {
+          for (uint32_t i = 0; i < k; i++) {
+            const uint32_t sl = slot_of[(size_t)tok * k + i];
+            if (sl == slot) {
+              routed = true;
+              wt = slot_w[(size_t)tok * k + i];
+            }
+            if (sl == ~0u) miss = __int_as_float(0x7fc00000);
+          }
+        } else {
+          wt = slot_w[slot];
+        }
+        if (row < d) {
+          if (routed) atomicAdd(out + (size_t)tok * d + row, y * wt);
+          if (miss != 0.0f || miss != miss) atomicAdd(out + (size_t)tok * d + row, miss);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  }
+}
+
 // ---------------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------------
@@ -394,6 +470,30 @@ static hipError_t go_dn(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_
   return hipGetLastError();
 }
 
+constexpr int kDnAtomicKS = 8;
+
+template <int QT, bool PACKED>
+static hipError_t go_dn_atomic(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  const uint32_t per = kDnAtomicKS * 64 * 4 + ActLds<QT, PACKED>::per_token(L.f) + 4;
+  const uint32_t mt = min(n, (kLdsBudget - 16) / per);
+  if (mt == 0) return hipErrorInvalidValue;
+  static const bool once = allow_lds(k_dn_atomic<QT, PACKED, kDnAtomicKS>);
+  (void)once;
+  const dim3 g((L.d + kTileRows - 1) / kTileRows, 1, min(L.ne, n * L.k));
+  hipLaunchKernelGGL((k_dn_atomic<QT, PACKED, kDnAtomicKS>), g, dim3(64 * kDnAtomicKS), mt * per + 16, st, B.work,
+                     L.ne, L.f, L.d, mt, B.slot_tok, B.slot_of, B.slot_w, L.k, B.spec, B.hq, B.hsc, B.hsum, B.hf,
+                     B.out);
+  return hipGetLastError();
+}
+
+template <int QT>
+hipError_t units_down_atomic(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  if constexpr (has_int8_kernel(QT)) {
+    if (L.math == 0) return go_dn_atomic<QT, true>(L, B, n, st);
+  }
+  return go_dn_atomic<QT, false>(L, B, n, st);
+}
+
 template <int QT>
 hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
   if constexpr (has_int8_kernel(QT)) {
@@ -412,5 +512,6 @@ hipError_t units_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t 
 
 template hipError_t units_gateup<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, const RouteArgs&, hipStream_t);
 template hipError_t units_down<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, uint32_t, hipStream_t);
+template hipError_t units_down_atomic<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, hipStream_t);
 
 }  // namespace gmoe
