@@ -606,7 +606,7 @@ gmoe_status run_layer(gmoe_ctx* c, Layer& L, FwdBufs B, uint32_t n, hipStream_t 
   for (uint32_t e = 0; e < L.ne; e++) resident &= L.slot[e] >= 0;
   const bool spec = !pf && !pq && !B.logits_in && resident && spec_ok(D, n);
   B.spec = spec ? 1u : 0u;
-  // top-k <= 2 at one or two tokens: the down product adds into the output (zeroed by the
+  // top-k <= 2 at decode batches: the down product adds into the output (zeroed by the
   // front end), no combine launch
   const bool fuse = !pf && !pq && down_atomic_ok(D, n) && (spec || front_small_ok(D, n));
   B.fuse_out = fuse ? 1u : 0u;
