@@ -158,12 +158,10 @@ struct FwdBufs {
   _Float16* xsh;         // [2][n*k][d/16]
   _Float16* hh;          // [2][n*k][f]
   _Float16* hsh;         // [2][n*k][f/16]
-  // packed-math prefill (k_pq): the codes in slot order as fp16 in xh / hh (one plane),
-  // per-token scales and sums transposed to [K/32][nkp] and [K/sum width][nkp]
+  // packed-math prefill (k_pq): the activation codes in slot order as fp16 in xh (one
+  // plane), their per-token scales and sums transposed to [d/32][nkp] and [d/w][nkp]
   float* qxs;
   float* qxsum;
-  float* qhs;
-  float* qhsum;
   uint32_t nkp;          // >= n*k + 64
   int8_t* hq;            // [n*k][f]
   float* hsc;            // [n*k][f/32]
@@ -244,7 +242,6 @@ __host__ __device__ constexpr uint32_t pq_sum_width(uint32_t qt) {
   return (qt == Q4_K || qt == Q5_K) ? 32u : qt == Q2_K ? 16u : 0u;
 }
 template <int QT> hipError_t pq_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
-template <int QT> hipError_t pq_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
 template <int QT> hipError_t prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 template <int QT> hipError_t prefill_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg,
                                           hipStream_t st);
@@ -303,13 +300,12 @@ hipError_t launch_down_atomic(const LayerDev& L, const FwdBufs& B, uint32_t n, h
 // Prefill path: whether it applies (f32 math, at least kPfMinSlots slots, supported
 // types and shapes), the per-slot fp16 gather of the activations, and the products.
 bool prefill_ok(const LayerDev& L, uint32_t n);
-// Packed-math calls with enough tokens per expert run the products on MFMA (k_pq): the
-// activation codes gathered in slot order, then gate/up and down.
+// Packed-math calls with enough tokens per expert run the products on MFMA: the
+// activation codes gathered in slot order, gate/up by k_pq (bit-exact h and codes), the
+// down product by k_pf on the dequantised h.
 bool prefill_packed_ok(const LayerDev& L, uint32_t n);
 hipError_t launch_gather_codes(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 hipError_t launch_pq_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
-hipError_t launch_pq_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
-uint32_t pq_ksg(const LayerDev& L, const FwdBufs& B);
 bool prefill_dense_ok(const LayerDev& L, uint32_t n);
 hipError_t launch_dense_setup(ExpertWork* work, uint32_t* offsets, uint32_t* active, uint32_t* ptile,
                               uint32_t ptile_cap, uint32_t* slot_tok, const uint8_t* w, uint32_t n, hipStream_t st);

@@ -1503,18 +1503,6 @@ hipError_t launch_pq_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hip
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_pq_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st) {
-  switch (L.qt_down) {
-#define DN(T) case T: return pq_down<T>(L, B, n, ksg, st);
-    DN(Q4_K) DN(Q5_K) DN(Q6_K) DN(Q3_K) DN(Q2_K) DN(Q8_0)
-#undef DN
-  }
-  return hipErrorInvalidValue;
-}
-
-// k_pq's down workgroups cover the same rows as k_pf's, so the slices are sized alike.
-uint32_t pq_ksg(const LayerDev& L, const FwdBufs& B) { return prefill_ksg(L, B); }
-
 hipError_t launch_prefill_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
   switch (L.qt_gate) {
 #define GU(T) case T: return prefill_gateup<T>(L, B, n, st);

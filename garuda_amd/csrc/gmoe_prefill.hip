@@ -599,8 +599,10 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
           a.out[o + (size_t)a.nk * a.rows] = lo;
         }
         if (a.swo) {  // sums of h over swo consecutive rows (lanes): the down min term's S
-          float sm = hv;
-          for (uint32_t o = 1; o < a.swo; o <<= 1) sm += __shfl_xor(sm, (int)o, 64);
+          float sm = hv;  // offsets fixed at compile time, so the 32 reductions overlap
+#pragma unroll
+          for (int o = 1; o <= 8; o <<= 1) sm += __shfl_xor(sm, o, 64);
+          if (a.swo == 32) sm += __shfl_xor(sm, 16, 64);
           if (t < m && (l32 % a.swo) == 0) {
             const uint32_t ns = a.rows / a.swo;
             const size_t o = (size_t)(s0 + t) * ns + fr / a.swo;
@@ -799,16 +801,15 @@ struct PqArgs {
   const float* ins;     // [K/32][nkp] activation scales
   const float* insum;   // [K/SWS][nkp] activation sums (types with SWS)
   uint32_t nk, nkp, K, rows;
-  uint32_t upk;         // down: units of K per slice
-  // gate/up: h's codes, scales and sums (the down type's width, swo; 0 = none)
-  _Float16* out;
-  float* outs;
-  float* outsum;
-  uint32_t swo;
-  float* y;             // down: [slices][nk][rows]
+  // h dequantised (scale * q of its int8 requantisation) as fp16 hi/lo planes [2][nk][rows],
+  // and its sums over swf rows as hi/lo planes [2][nk][rows/swf] (swf 0: none): the input
+  // of the f32-math down product (k_pf)
+  _Float16* outf;
+  _Float16* outfs;
+  uint32_t swf;
 };
 
-template <int QT, bool GU>
+template <int QT>
 __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pq(PqArgs a) {
   using T = PF<QT>;
   using Q = PQ<QT>;
@@ -817,7 +818,7 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pq(PqArgs a) {
   constexpr int U = UT_<QT>::U, NP = U / 16;
   constexpr int SPS = Q::SBW / 16;                       // K16 steps per sub-block
   constexpr int NXS = KC / 32, NSM = Q::SWS ? KC / Q::SWS : 0;  // token factor rows per chunk
-  constexpr uint32_t WROWS = 32 * NW * (GU ? 1 : 2);
+  constexpr uint32_t WROWS = 32 * NW;
   constexpr uint32_t WBYTES = NW * NPC * 1024, XBYTES = kPfTok * KC * 2, TBYTES = (NXS + NSM) * kPfTok * 4;
   constexpr uint32_t BUF = WBYTES + XBYTES + TBYTES;
   constexpr int NX = (int)kPfTok * NCK / NT;              // activation loads per thread per chunk
@@ -833,15 +834,17 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pq(PqArgs a) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t K = a.K, nunit = K / T::EU;
-  const uint32_t u0 = GU ? 0 : blockIdx.z * a.upk, u1 = GU ? nunit : min(nunit, u0 + a.upk);
+  const uint32_t u0 = 0, u1 = nunit;
 
+  // NW/2 gate tiles then NW/2 up tiles of 64 rows; wave w owns rows 32 (w % 2) .. of gate
+  // tile w / 2 (rt = 0) and of the same up tile (rt = 1)
   const size_t tile_bytes = (size_t)nunit * kTileRows * U;
-  const uint8_t* m_lo = GU ? W->w[0] + (NW / 2) * blockIdx.x * tile_bytes : W->w[2] + NW * blockIdx.x * tile_bytes;
-  const uint8_t* m_hi = GU ? W->w[1] + (NW / 2) * blockIdx.x * tile_bytes : m_lo + (NW / 2) * tile_bytes;
+  const uint8_t* m_lo = W->w[0] + (NW / 2) * blockIdx.x * tile_bytes;
+  const uint8_t* m_hi = W->w[1] + (NW / 2) * blockIdx.x * tile_bytes;
   uint32_t row[2];
 #pragma unroll
   for (int rt = 0; rt < 2; rt++) {
-    const uint32_t tm = GU ? rt * (NW / 2) + wave / 2 : wave, i = GU ? 32 * (wave % 2) + l32 : 32 * rt + l32;
+    const uint32_t tm = rt * (NW / 2) + wave / 2, i = 32 * (wave % 2) + l32;
     row[rt] = (tm * NPC * 64 + i) * 16;
   }
   const uint32_t xrow = l32 * NCK * 16;
@@ -960,7 +963,7 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pq(PqArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const uint32_t t = 32 * tt + 8 * (r / 4) + 4 * h + (r % 4);
-      if constexpr (GU) {
+      {
         // h = silu(g) * u, then quantised per 32 rows (the 32 lanes of this half) with
         // quant_wave's arithmetic (quant/mod.rs:331-345)
         const uint32_t fr = blockIdx.x * WROWS + 32 * wave + l32;
@@ -972,23 +975,27 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pq(PqArgs a) {
         const float inv = scale > 0.0f ? fdiv(1.0f, scale) : 0.0f;
         const float rq = roundf(hv * inv);
         const int qi = (rq != rq) ? 0 : rq < -127.0f ? -127 : rq > 127.0f ? 127 : (int)rq;
-        int sm = qi;
-        if (a.swo) {
+        // the dequantised activation the reference's down dot sees, scale * q, as fp16
+        // hi/lo planes for the f32-math MFMA product (k_pf), and its sums over swf rows
+        const float xv = scale * (float)qi;
+        const _Float16 hi = (_Float16)xv, lo = (_Float16)(xv - (float)hi);
+        float sf = xv;  // offsets fixed at compile time, so the 32 reductions overlap
+        if (a.swf) {
 #pragma unroll
-          for (int o = 8; o >= 1; o >>= 1) sm += __shfl_xor(sm, o, 64);
-          if (a.swo == 32) sm += __shfl_xor(sm, 16, 64);
+          for (int o = 1; o <= 8; o <<= 1) sf += __shfl_xor(sf, o, 64);
+          if (a.swf == 32) sf += __shfl_xor(sf, 16, 64);
         }
         if (t < m) {
-          a.out[(size_t)(s0 + t) * a.rows + fr] = (_Float16)(float)qi;
-          if (l32 == 0) a.outs[(size_t)(fr / 32) * a.nkp + s0 + t] = scale;
-          if (a.swo && (l32 % a.swo) == 0) a.outsum[(size_t)(fr / a.swo) * a.nkp + s0 + t] = (float)sm;
-        }
-      } else {
-        float* y = a.y + (size_t)blockIdx.z * a.nk * a.rows;
-#pragma unroll
-        for (int rt = 0; rt < 2; rt++) {
-          const uint32_t dr = blockIdx.x * WROWS + 64 * wave + 32 * rt + l32;
-          if (t < m) y[(size_t)(s0 + t) * a.rows + dr] = acc[rt][tt][r];
+          const size_t o = (size_t)(s0 + t) * a.rows + fr;
+          a.outf[o] = hi;
+          a.outf[o + (size_t)a.nk * a.rows] = lo;
+          if (a.swf && (l32 % a.swf) == 0) {
+            const uint32_t ns = a.rows / a.swf;
+            const size_t os = (size_t)(s0 + t) * ns + fr / a.swf;
+            const _Float16 shi = (_Float16)sf;
+            a.outfs[os] = shi;
+            a.outfs[os + (size_t)a.nk * ns] = (_Float16)(sf - (float)shi);
+          }
         }
       }
     }
@@ -1003,7 +1010,7 @@ uint32_t pf_rows(bool gu) {
   }
 }
 
-// Packed-math prefill products (k_pq) of this block type.
+// The packed-math gate/up product (k_pq) of this block type; its down product is k_pf's.
 template <int QT>
 hipError_t pq_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
   if constexpr (!pq_type<QT>()) {
@@ -1020,35 +1027,10 @@ hipError_t pq_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_
     a.nkp = B.nkp;
     a.K = L.d;
     a.rows = L.f;
-    a.out = B.hh;
-    a.outs = B.qhs;
-    a.outsum = B.qhsum;
-    a.swo = pq_sum_width(L.qt_down);
-    hipLaunchKernelGGL((k_pq<QT, true>), dim3(L.f / pf_rows<QT>(true), B.ptile_cap), dim3(64 * PF<QT>::NW), 0, st, a);
-    return hipGetLastError();
-  }
-}
-
-template <int QT>
-hipError_t pq_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st) {
-  if constexpr (!pq_type<QT>()) {
-    return hipErrorNotSupported;
-  } else {
-    if (L.d % pf_rows<QT>(false) || L.f % PF<QT>::EU || ksg < 1 || ksg > kMaxKsg) return hipErrorInvalidValue;
-    PqArgs a{};
-    a.work = B.work;
-    a.ptile = B.ptile;
-    a.in = B.hh;
-    a.ins = B.qhs;
-    a.insum = B.qhsum;
-    a.nk = n * L.k;
-    a.nkp = B.nkp;
-    a.K = L.f;
-    a.rows = L.d;
-    a.upk = (L.f / PF<QT>::EU + ksg - 1) / ksg;
-    a.y = B.y;
-    hipLaunchKernelGGL((k_pq<QT, false>), dim3(L.d / pf_rows<QT>(false), B.ptile_cap, ksg), dim3(64 * PF<QT>::NW), 0,
-                       st, a);
+    a.outf = B.hh;
+    a.outfs = B.hsh;
+    a.swf = pf_sum_width(L.qt_down);
+    hipLaunchKernelGGL((k_pq<QT>), dim3(L.f / pf_rows<QT>(true), B.ptile_cap), dim3(64 * PF<QT>::NW), 0, st, a);
     return hipGetLastError();
   }
 }
@@ -1117,6 +1099,5 @@ template uint32_t prefill_down_slices<GMOE_QT>(const LayerDev&, const FwdBufs&);
 template hipError_t prefill_gateup<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, hipStream_t);
 template hipError_t prefill_down<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, uint32_t, hipStream_t);
 template hipError_t pq_gateup<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, hipStream_t);
-template hipError_t pq_down<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, uint32_t, hipStream_t);
 
 }  // namespace gmoe
