@@ -401,6 +401,22 @@ struct PfArgs {
   float* y;               // down: [slices][nk][rows]
 };
 
+// The (row block, token tile) of a workgroup of a gate/up grid (gridDim.x row blocks,
+// gridDim.y token tiles). Workgroups go round-robin over the 8 XCDs, each with its own L2,
+// and the token tiles of one expert read the same weight rows. With gridDim.x a multiple
+// of 8, XCD c's sequence of workgroups is remapped to take one row block's token tiles one
+// after another, so an expert's tiles of a row block run side by side on one XCD and the
+// weights come from its L2 after the first; otherwise the launch's own order.
+__device__ __forceinline__ void pf_block(uint32_t& bx, uint32_t& by) {
+  bx = blockIdx.x;
+  by = blockIdx.y;
+  if (gridDim.x % 8 == 0) {
+    const uint32_t L = blockIdx.y * gridDim.x + blockIdx.x, j = L / 8;
+    bx = (j / gridDim.y) * 8 + L % 8;
+    by = j % gridDim.y;
+  }
+}
+
 template <int QT, bool GU>
 __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
   using T = PF<QT>;
@@ -417,7 +433,9 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
   static_assert(2 * BUF <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * BUF];
 
-  const uint32_t pt = a.ptile[blockIdx.y];
+  uint32_t bx = blockIdx.x, by = blockIdx.y;
+  if constexpr (GU) pf_block(bx, by);
+  const uint32_t pt = a.ptile[by];
   if (pt == ~0u) return;
   const ExpertWork* W = a.work + (pt >> 16);
   const uint32_t t0 = (pt & 0xffffu) * kPfTok;
@@ -431,8 +449,8 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
   // slab tiles of the workgroup's NW (matrix, tile) pairs: NW/2 gate tiles then NW/2 up
   // tiles (GU), or NW down tiles
   const size_t tile_bytes = (size_t)nunit * kTileRows * U;
-  const uint8_t* m_lo = GU ? W->w[0] + (NW / 2) * blockIdx.x * tile_bytes : W->w[2] + NW * blockIdx.x * tile_bytes;
-  const uint8_t* m_hi = GU ? W->w[1] + (NW / 2) * blockIdx.x * tile_bytes : m_lo + (NW / 2) * tile_bytes;
+  const uint8_t* m_lo = GU ? W->w[0] + (NW / 2) * bx * tile_bytes : W->w[2] + NW * bx * tile_bytes;
+  const uint8_t* m_hi = GU ? W->w[1] + (NW / 2) * bx * tile_bytes : m_lo + (NW / 2) * tile_bytes;
   // the lane's row in each of its two row tiles (offsets into a weight buffer)
   uint32_t row[2];
 #pragma unroll
@@ -590,7 +608,7 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
     for (int r = 0; r < 16; r++) {
       const uint32_t t = 32 * tt + 8 * (r / 4) + 4 * h + (r % 4);
       if constexpr (GU) {
-        const uint32_t fr = blockIdx.x * WROWS + 32 * wave + l32;
+        const uint32_t fr = bx * WROWS + 32 * wave + l32;
         const float hv = swiglu(acc[0][tt][r], acc[1][tt][r]);
         const _Float16 hi = (_Float16)hv, lo = (_Float16)(hv - (float)hi);
         if (t < m) {
@@ -615,7 +633,7 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
         float* y = a.y + (size_t)blockIdx.z * a.nk * a.rows;
 #pragma unroll
         for (int rt = 0; rt < 2; rt++) {
-          const uint32_t dr = blockIdx.x * WROWS + 64 * wave + 32 * rt + l32;
+          const uint32_t dr = bx * WROWS + 64 * wave + 32 * rt + l32;
           if (t < m) y[(size_t)(s0 + t) * a.rows + dr] = acc[rt][tt][r];
         }
       }
@@ -826,7 +844,9 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pq(PqArgs a) {
   static_assert(2 * BUF <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * BUF];
 
-  const uint32_t pt = a.ptile[blockIdx.y];
+  uint32_t bx, by;
+  pf_block(bx, by);
+  const uint32_t pt = a.ptile[by];
   if (pt == ~0u) return;
   const ExpertWork* W = a.work + (pt >> 16);
   const uint32_t t0 = (pt & 0xffffu) * kPfTok;
@@ -839,8 +859,8 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pq(PqArgs a) {
   // NW/2 gate tiles then NW/2 up tiles of 64 rows; wave w owns rows 32 (w % 2) .. of gate
   // tile w / 2 (rt = 0) and of the same up tile (rt = 1)
   const size_t tile_bytes = (size_t)nunit * kTileRows * U;
-  const uint8_t* m_lo = W->w[0] + (NW / 2) * blockIdx.x * tile_bytes;
-  const uint8_t* m_hi = W->w[1] + (NW / 2) * blockIdx.x * tile_bytes;
+  const uint8_t* m_lo = W->w[0] + (NW / 2) * bx * tile_bytes;
+  const uint8_t* m_hi = W->w[1] + (NW / 2) * bx * tile_bytes;
   uint32_t row[2];
 #pragma unroll
   for (int rt = 0; rt < 2; rt++) {
@@ -966,7 +986,7 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pq(PqArgs a) {
       {
         // h = silu(g) * u, then quantised per 32 rows (the 32 lanes of this half) with
         // quant_wave's arithmetic (quant/mod.rs:331-345)
-        const uint32_t fr = blockIdx.x * WROWS + 32 * wave + l32;
+        const uint32_t fr = bx * WROWS + 32 * wave + l32;
         const float hv = swiglu(acc[0][tt][r], acc[1][tt][r]);
         float am = fmaxf(0.0f, fabsf(hv));
 #pragma unroll
