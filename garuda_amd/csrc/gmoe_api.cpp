@@ -606,7 +606,10 @@ gmoe_status run_layer(gmoe_ctx* c, Layer& L, FwdBufs B, uint32_t n, hipStream_t 
   B.spec = spec ? 1u : 0u;
   // top-k <= 2 at decode batches: the down product adds into the output (zeroed by the
   // front end), no combine launch
-  const bool fuse = !pf && !pq && down_atomic_ok(D, n) && (spec || front_small_ok(D, n));
+  // (the front end zeroes out while it reads hs: not when they overlap, as in place)
+  const uintptr_t ob = (uintptr_t)B.out, oe = ob + (size_t)n * L.d * 4, hb = (uintptr_t)B.hs,
+                  he = hb + (size_t)n * L.d * 4;
+  const bool fuse = !pf && !pq && down_atomic_ok(D, n) && (spec || front_small_ok(D, n)) && (oe <= hb || he <= ob);
   B.fuse_out = fuse ? 1u : 0u;
   if (!spec) B.nslot = n * L.k;
   RouteArgs ra{};
