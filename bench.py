@@ -185,8 +185,9 @@ def extra_leg(name, a, dev, threads, stream, timed, cpu):
 def prefill_leg(a, dev, mats, threads, stream, timed, cpu, packed=False):
     """the same Q4_K layer at a prefill of `a.prefill_tokens` tokens,
     routing skewed to Zipf(1.1) expert loads through one shared activation direction.
-    f32 math (Weight::Full) runs k_pf, packed math (Weight::Packed, mmap = true) k_pq;
-    both on MFMA. Returns the JSON object of the leg."""
+    f32 math (Weight::Full) runs k_pf for gate/up and down; packed math (Weight::Packed,
+    mmap = true) runs k_pq for gate/up and k_pf for down over the dequantised h; all on
+    MFMA. Returns the JSON object of the leg."""
     import torch
     import garuda_amd as G
     from garuda_amd import moe as M
@@ -254,10 +255,10 @@ def prefill_leg(a, dev, mats, threads, stream, timed, cpu, packed=False):
         log(f"prefill cpu (f32 Full path): {sample / med:.1f} tok/s")
     for l in layers:
         l.release()
-    kname = "k_pq" if packed else "k_pf"
+    kernels = "k_pq<Q4_K> (gate/up) + k_pf<Q4_K, down>" if packed else "k_pf<Q4_K, gate/up> + k_pf<Q4_K, down>"
     note = ("algorithmic flops (sum of expert tokens x 6 d f) over the two MFMA launches' time; the reference's "
-            "packed arithmetic adds one float term per 32-value sub-block per (row, token), five VALU operations "
-            "evaluated in K order, which bound the kernel" if packed else
+            "packed arithmetic adds one float term per 32-value sub-block per (row, token) of gate/up, five VALU "
+            "operations evaluated in K order, which bound k_pq near 20% of peak" if packed else
             "algorithmic flops (sum of expert tokens x 6 d f) over the two MFMA launches' "
             "time; the exact-product scheme issues two fp16 MFMA passes per product")
     return {
@@ -267,7 +268,7 @@ def prefill_leg(a, dev, mats, threads, stream, timed, cpu, packed=False):
         "tokens_per_s": n / step_s, "ms_per_call": step_s * 1e3, "steps": a.prefill_steps,
         "expert_loads": [int(x) for x in loads[0]],
         "gateup_us": gu_ms * 1e3, "down_us": dn_ms * 1e3,
-        "roofline": {"bound": "mfma", "kernels": f"{kname}<Q4_K, gate/up> + {kname}<Q4_K, down>",
+        "roofline": {"bound": "mfma", "kernels": kernels,
                      "achieved": tflops, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": tflops / MFMA_PEAK_TFLOPS,
                      "flops_per_call": flops, "note": note},
     }
