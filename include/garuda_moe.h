@@ -131,7 +131,8 @@ gmoe_status gmoe_ffn_forward_logits(gmoe_ctx* ctx, uint32_t layer_id, const floa
  * (a hipStream_t; NULL = the context's own stream) and the call returns without
  * waiting. Requires every expert of the layer to be resident (GMOE_ERR_CACHE
  * otherwise). Calls on one context share its scratch, so they must be ordered on
- * one stream. d_logits may be NULL. */
+ * one stream. d_logits may be NULL. d_out may equal d_hs (the output overwrites the
+ * input); otherwise the output must not overlap an input. */
 gmoe_status gmoe_ffn_forward_async(gmoe_ctx* ctx, uint32_t layer_id, const float* d_hs,
                                    const float* d_logits, uint32_t n, float* d_out,
                                    uint32_t* d_routed_ids, float* d_routed_w, void* stream);
