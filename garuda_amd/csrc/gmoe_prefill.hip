@@ -521,85 +521,93 @@ __global__ void __launch_bounds__(64 * PF<QT>::NW) k_pf(PfArgs a) {
   if (u0 < u1) stage(u0, std::integral_constant<int, 0>{}, 0);  // a slice past the end writes zeros
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (uint32_t u = u0; u < u1; u++) {
-    static_for<NCH>([&](auto cc) {
-      constexpr int C = decltype(cc)::value;
-      const uint32_t b = (NCH % 2 == 0) ? (uint32_t)(C % 2) : ((u - u0) * NCH + C) % 2;
-      if constexpr (C + 1 < NCH) {
-        stage(u, std::integral_constant<int, C + 1>{}, b ^ 1);
-      } else {
-        if (u + 1 < u1) stage(u + 1, std::integral_constant<int, 0>{}, b ^ 1);
-      }
-      const uint8_t* wb = lds + b * BUF;
-      const uint8_t* xb = wb + WBYTES;
-      asm volatile("" : "+v"(tsw));  // per-step addresses are made here, not kept across chunks
-      static_for<SPC>([&](auto ss) {
-        constexpr int SL = decltype(ss)::value, S = C * SPC + SL;
-        half8 bw[2], ax[2][2];
-#pragma unroll
-        for (int rt = 0; rt < 2; rt++) bw[rt] = D::template frag<C, S>(wb + row[rt], h);
-        const uint32_t pos = ((2 * SL + h) * 16) ^ tsw;
-#pragma unroll
-        for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-          for (int pl = 0; pl < 2; pl++)
-            ax[tt][pl] = *reinterpret_cast<const half8*>(xb + xrow + pos + (pl * kPfTok + 32 * tt) * NCK * 16);
-#pragma unroll
-        for (int rt = 0; rt < 2; rt++)
-#pragma unroll
+  // the main loop compiled twice, with and without the second 32-token tile, so that no
+  // branch splits a chunk's steps and the scheduler can overlap one step's LDS reads and
+  // weight decode with the previous step's MFMAs
+  auto main_loop = [&](auto twoc) {
+    constexpr bool TWO = decltype(twoc)::value;
+    for (uint32_t u = u0; u < u1; u++) {
+      static_for<NCH>([&](auto cc) {
+        constexpr int C = decltype(cc)::value;
+        const uint32_t b = (NCH % 2 == 0) ? (uint32_t)(C % 2) : ((u - u0) * NCH + C) % 2;
+        if constexpr (C + 1 < NCH) {
+          stage(u, std::integral_constant<int, C + 1>{}, b ^ 1);
+        } else {
+          if (u + 1 < u1) stage(u + 1, std::integral_constant<int, 0>{}, b ^ 1);
+        }
+        const uint8_t* wb = lds + b * BUF;
+        const uint8_t* xb = wb + WBYTES;
+        asm volatile("" : "+v"(tsw));  // per-step addresses are made here, not kept across chunks
+        static_for<SPC>([&](auto ss) {
+          constexpr int SL = decltype(ss)::value, S = C * SPC + SL;
+          half8 bw[2], ax[2][2];
+  #pragma unroll
+          for (int rt = 0; rt < 2; rt++) bw[rt] = D::template frag<C, S>(wb + row[rt], h);
+          const uint32_t pos = ((2 * SL + h) * 16) ^ tsw;
+  #pragma unroll
+          for (int tt = 0; tt < 2; tt++)
+  #pragma unroll
+            for (int pl = 0; pl < 2; pl++)
+              ax[tt][pl] = *reinterpret_cast<const half8*>(xb + xrow + pos + (pl * kPfTok + 32 * tt) * NCK * 16);
+  #pragma unroll
+          for (int rt = 0; rt < 2; rt++)
+  #pragma unroll
+            for (int tt = 0; tt < 2; tt++) {
+              if (tt == 1 && !TWO) continue;  // a tile of at most 32 tokens: its second half is padding
+              if constexpr (T::SU16 == 0) {
+                acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[tt][0], bw[rt], acc[rt][tt], 0, 0, 0);
+                acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[tt][1], bw[rt], acc[rt][tt], 0, 0, 0);
+              } else {
+                const f32x16 c0 = (S % T::SU16 == 0) ? zero : P[rt][tt];
+                P[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[tt][0], bw[rt], c0, 0, 0, 0);
+                P[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[tt][1], bw[rt], P[rt][tt], 0, 0, 0);
+              }
+            }
+          if constexpr (T::SU16 != 0) {
+            if constexpr ((S + 1) % T::SU16 == 0) {
+  #pragma unroll
+              for (int rt = 0; rt < 2; rt++) {
+                const float sc = D::template scale<C, S>(wb + row[rt]);
+  #pragma unroll
+                for (int tt = 0; tt < 2; tt++)
+                  if (tt == 0 || TWO)
+  #pragma unroll
+                    for (int r = 0; r < 16; r++) acc[rt][tt][r] = __builtin_fmaf(sc, P[rt][tt][r], acc[rt][tt][r]);
+              }
+            }
+            // short scale groups: keep the scheduler from overlapping the next group's
+            // partial sums with these (two live sets of P do not fit the registers)
+            if constexpr (T::SU16 <= 2) __builtin_amdgcn_sched_barrier(0);
+          }
+        });
+        if constexpr (T::SW != 0 && C == NCH - 1) {
+          // min term of unit u: -sum over its sub-blocks of (dmin*m) * S, three MFMA passes
+          half8 bh[2], bl[2];
+  #pragma unroll
+          for (int rt = 0; rt < 2; rt++) D::template mins<C>(wb + row[rt], h, bh[rt], bl[rt]);
+          const uint8_t* sb = xb + XBYTES;
+  #pragma unroll
           for (int tt = 0; tt < 2; tt++) {
-            if (tt == 1 && !two) continue;  // a tile of at most 32 tokens: its second half is padding
-            if constexpr (T::SU16 == 0) {
-              acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[tt][0], bw[rt], acc[rt][tt], 0, 0, 0);
-              acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[tt][1], bw[rt], acc[rt][tt], 0, 0, 0);
-            } else {
-              const f32x16 c0 = (S % T::SU16 == 0) ? zero : P[rt][tt];
-              P[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[tt][0], bw[rt], c0, 0, 0, 0);
-              P[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[tt][1], bw[rt], P[rt][tt], 0, 0, 0);
-            }
-          }
-        if constexpr (T::SU16 != 0) {
-          if constexpr ((S + 1) % T::SU16 == 0) {
-#pragma unroll
+            if (tt == 1 && !TWO) continue;
+            // sums 8h'.. of token t (h' = h with 16 sub-blocks; with 8 the upper lanes' B is zero)
+            const uint32_t t = 32 * tt + l32, e = NS == 16 ? h : 0;
+            const half8 sh = *reinterpret_cast<const half8*>(sb + ((0 * kPfTok + t) * (NS / 8) + e) * 16);
+            const half8 sl = *reinterpret_cast<const half8*>(sb + ((1 * kPfTok + t) * (NS / 8) + e) * 16);
+  #pragma unroll
             for (int rt = 0; rt < 2; rt++) {
-              const float sc = D::template scale<C, S>(wb + row[rt]);
-#pragma unroll
-              for (int tt = 0; tt < 2; tt++)
-                if (tt == 0 || two)
-#pragma unroll
-                  for (int r = 0; r < 16; r++) acc[rt][tt][r] = __builtin_fmaf(sc, P[rt][tt][r], acc[rt][tt][r]);
+              acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh, bh[rt], acc[rt][tt], 0, 0, 0);
+              acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sl, bh[rt], acc[rt][tt], 0, 0, 0);
+              acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh, bl[rt], acc[rt][tt], 0, 0, 0);
             }
           }
-          // short scale groups: keep the scheduler from overlapping the next group's
-          // partial sums with these (two live sets of P do not fit the registers)
-          if constexpr (T::SU16 <= 2) __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
       });
-      if constexpr (T::SW != 0 && C == NCH - 1) {
-        // min term of unit u: -sum over its sub-blocks of (dmin*m) * S, three MFMA passes
-        half8 bh[2], bl[2];
-#pragma unroll
-        for (int rt = 0; rt < 2; rt++) D::template mins<C>(wb + row[rt], h, bh[rt], bl[rt]);
-        const uint8_t* sb = xb + XBYTES;
-#pragma unroll
-        for (int tt = 0; tt < 2; tt++) {
-          if (tt == 1 && !two) continue;
-          // sums 8h'.. of token t (h' = h with 16 sub-blocks; with 8 the upper lanes' B is zero)
-          const uint32_t t = 32 * tt + l32, e = NS == 16 ? h : 0;
-          const half8 sh = *reinterpret_cast<const half8*>(sb + ((0 * kPfTok + t) * (NS / 8) + e) * 16);
-          const half8 sl = *reinterpret_cast<const half8*>(sb + ((1 * kPfTok + t) * (NS / 8) + e) * 16);
-#pragma unroll
-          for (int rt = 0; rt < 2; rt++) {
-            acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh, bh[rt], acc[rt][tt], 0, 0, 0);
-            acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sl, bh[rt], acc[rt][tt], 0, 0, 0);
-            acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh, bl[rt], acc[rt][tt], 0, 0, 0);
-          }
-        }
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-    });
-  }
+    }
+  };
+  if (two) main_loop(std::true_type{});
+  else main_loop(std::false_type{});
 
   // epilogue
 #pragma unroll
