@@ -127,6 +127,8 @@ SIGNATURES = {
     "gmoe_model_decode": (i32, [vp, u32, u32p, u32p, u32p, f32p]),
     "gmoe_model_trace_floats": (C.c_size_t, [vp, u32]),
     "gmoe_model_decode_trace": (i32, [vp, u32, u32p, u32p, u32p, f32p, f32p]),
+    "gmoe_model_set_graphs": (i32, [vp, C.c_int]),
+    "gmoe_model_graph_ready": (C.c_int, [vp, u32]),
     "gmoe_set_kernel_timing": (i32, [vp, i32]),
     "gmoe_kernel_time": (i32, [vp, u32, C.POINTER(C.c_double), C.POINTER(u64)]),
 }

@@ -240,6 +240,11 @@ namespace gmoe {
 // for the other host modules (gmoe_kv.cpp)
 int ctx_device(gmoe_ctx* c) { return c->device; }
 hipStream_t ctx_stream(gmoe_ctx* c) { return c->stream; }
+// the scratch arena's current allocation (launches captured into a graph point into it)
+const void* ctx_scratch_id(gmoe_ctx* c) {
+  std::lock_guard<std::mutex> g(c->slab_mu);
+  return c->scratch;
+}
 }  // namespace gmoe
 
 namespace {
@@ -648,6 +653,10 @@ gmoe_status run_layer(gmoe_ctx* c, Layer& L, FwdBufs B, uint32_t n, hipStream_t 
   const uint32_t ksg = (pf || pq) ? prefill_ksg(D, B) : down_ksg(D, n * L.k);
   Timing tm{};
   timed = timed && c->timing;
+  if (timed) {  // no timing events inside a graph being captured
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) timed = false;
+  }
   if (timed) {
     tm = take_timing(c);
     HIP_TRY(hipEventRecord(tm.a, st));

@@ -34,6 +34,15 @@ __global__ void __launch_bounds__(256) k_embed(GlueTokens tk, const float* __res
   for (uint32_t c = threadIdx.x; c < d / 4; c += blockDim.x) dst[c] = src[c];
 }
 
+// The same with the tokens in device memory (a decode step replayed from a graph).
+__global__ void __launch_bounds__(256) k_embed_dev(const uint32_t* __restrict__ tok, const float* __restrict__ table,
+                                                   uint32_t d, float* __restrict__ x) {
+  const uint32_t i = blockIdx.x;
+  const float4* src = reinterpret_cast<const float4*>(table + (size_t)tok[i] * d);
+  float4* dst = reinterpret_cast<float4*>(x + (size_t)i * d);
+  for (uint32_t c = threadIdx.x; c < d / 4; c += blockDim.x) dst[c] = src[c];
+}
+
 // grid n, 256 threads: with y, x[i] += y[i] first (written back); then
 // h[i] = (x[i] * scale) * w with scale = 1 / sqrt(mean(x[i]^2) + eps). A thread holds its
 // kNormVec float4 of the row (d <= 4 * 256 * kNormVec, checked by the model) in
@@ -144,6 +153,11 @@ __global__ void __launch_bounds__(256) k_argmax(const float* __restrict__ logits
 
 hipError_t launch_embed(const GlueTokens& tk, uint32_t n, const float* table, uint32_t d, float* x, hipStream_t st) {
   hipLaunchKernelGGL(k_embed, dim3(n), dim3(256), 0, st, tk, table, d, x);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed_dev(const uint32_t* tok, uint32_t n, const float* table, uint32_t d, float* x, hipStream_t st) {
+  hipLaunchKernelGGL(k_embed_dev, dim3(n), dim3(256), 0, st, tok, table, d, x);
   return hipGetLastError();
 }
 

@@ -358,6 +358,7 @@ struct GlueTokens {
   uint32_t tok[kModelMaxBatch];
 };
 hipError_t launch_embed(const GlueTokens& tk, uint32_t n, const float* table, uint32_t d, float* x, hipStream_t st);
+hipError_t launch_embed_dev(const uint32_t* tok, uint32_t n, const float* table, uint32_t d, float* x, hipStream_t st);
 hipError_t launch_add_norm(float* x, const float* y, const float* w, uint32_t n, uint32_t d, float eps, float* h,
                            hipStream_t st);
 hipError_t launch_argmax(const float* logits, uint32_t n, uint32_t vocab, uint32_t* next, hipStream_t st);

@@ -108,17 +108,15 @@ gmoe_status grow_pinned(gmoe_kv* kv, uint32_t n) {
   return GMOE_OK;
 }
 
-// Plans the call's entries (positions, windows, pages) and commits them: lengths advance
-// and pages are taken only when the whole call fits. Then queues the three launches.
-gmoe_status attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, const float* q, const float* k,
-                   const float* v, float* out, hipStream_t st, uint32_t q_stride = 0, uint32_t kv_stride = 0) {
+// The call's entries (positions, windows, pages), checked against the window and the
+// free pages but not committed; maxspan receives the longest span attended.
+gmoe_status plan(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, AttnEntry* ent, uint32_t* maxspan) {
   const gmoe_kv_desc& D = kv->d;
   if (layer >= D.n_layers) return kfail(GMOE_ERR_INFERENCE, "layer %u of %u", layer, D.n_layers);
   if (n == 0 || !seqs) return kfail(GMOE_ERR_INFERENCE, "empty attention call");
-  std::vector<AttnEntry> ent(n);
   std::vector<uint32_t> extra(kv->seqs.size(), 0);  // this call's entries so far, per sequence
   uint32_t need_pages = 0;
-  uint32_t maxspan = 1;
+  *maxspan = 1;
   for (uint32_t i = 0; i < n; i++) {
     const uint32_t s = seqs[i];
     if (s >= kv->seqs.size() || !kv->seqs[s].open) return kfail(GMOE_ERR_INFERENCE, "sequence %u is not open", s);
@@ -127,7 +125,7 @@ gmoe_status attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n
       return kfail(GMOE_ERR_CACHE, "context window of %u positions is exhausted", D.max_positions);
     if (pos % D.block_size == 0) need_pages++;
     const uint32_t start = D.sliding_window && pos + 1 > D.sliding_window ? pos + 1 - D.sliding_window : 0;
-    maxspan = std::max(maxspan, pos + 1 - start);
+    *maxspan = std::max(*maxspan, pos + 1 - start);
     ent[i].pos = pos;
     ent[i].start = start;
     ent[i].pages = kv->tables + ((size_t)s * D.n_layers + layer) * kv->ppseq;
@@ -135,16 +133,12 @@ gmoe_status attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n
   if (need_pages > kv->free_pages.size())
     return kfail(GMOE_ERR_CACHE, "the KV pool has %zu free pages, the call needs %u", kv->free_pages.size(),
                  need_pages);
-  // scratch: entries, rotated q, partials
-  const uint32_t nchunk = (maxspan + kAttnChunk - 1) / kAttnChunk;
-  const size_t qn = (size_t)n * D.n_heads * D.head_dim;
-  const size_t o_ent = 0, o_qr = (n * sizeof(AttnEntry) + 255) & ~(size_t)255;
-  const size_t o_part = o_qr + ((qn * 4 + 255) & ~(size_t)255);
-  const size_t total = o_part + (size_t)n * D.n_heads * nchunk * (D.head_dim + 2) * 4;
-  if (gmoe_status s = grow_scratch(kv, total)) return s;
-  if (n > kAttnInline)
-    if (gmoe_status s = grow_pinned(kv, n)) return s;
-  // commit: pages and lengths
+  return GMOE_OK;
+}
+
+// Commits a planned call: lengths advance and pages are taken.
+void commit(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, AttnEntry* ent) {
+  const gmoe_kv_desc& D = kv->d;
   for (uint32_t i = 0; i < n; i++) {
     Seq& S = kv->seqs[seqs[i]];
     if (ent[i].pos % D.block_size == 0) {
@@ -158,20 +152,27 @@ gmoe_status attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n
     ent[i].page = S.pages[layer][ent[i].pos / D.block_size];
     S.len[layer] = ent[i].pos + 1;
   }
+}
+
+// Scratch of a call of n entries and nchunk chunks: entries, rotated q, partials.
+struct AttnLayout {
+  size_t o_ent, o_qr, o_part, total;
+};
+AttnLayout layout(const gmoe_kv* kv, uint32_t n, uint32_t nchunk) {
+  const gmoe_kv_desc& D = kv->d;
+  const size_t qn = (size_t)n * D.n_heads * D.head_dim;
+  AttnLayout l;
+  l.o_ent = 0;
+  l.o_qr = (n * sizeof(AttnEntry) + 255) & ~(size_t)255;
+  l.o_part = l.o_qr + ((qn * 4 + 255) & ~(size_t)255);
+  l.total = l.o_part + (size_t)n * D.n_heads * nchunk * (D.head_dim + 2) * 4;
+  return l;
+}
+
+AttnArgs args(const gmoe_kv* kv, uint32_t n, uint32_t nchunk, const AttnLayout& l, const float* q, const float* k,
+              const float* v, float* out, uint32_t q_stride, uint32_t kv_stride) {
+  const gmoe_kv_desc& D = kv->d;
   AttnArgs a{};
-  if (n <= kAttnInline) {  // a decode batch: the entries ride in the kernel arguments
-    std::copy(ent.begin(), ent.end(), a.inl);
-    a.ent = nullptr;
-  } else {
-    const int h = kv->pin_slot;
-    kv->pin_slot = (h + 1) % kPinSlots;
-    KV_TRY(hipEventSynchronize(kv->pin_ev[h]));  // the slot's previous copy has been read
-    AttnEntry* pin = kv->pin + (size_t)h * kv->pin_cap;
-    std::copy(ent.begin(), ent.end(), pin);
-    KV_TRY(hipMemcpyAsync(kv->scratch + o_ent, pin, n * sizeof(AttnEntry), hipMemcpyHostToDevice, st));
-    KV_TRY(hipEventRecord(kv->pin_ev[h], st));
-    a.ent = reinterpret_cast<const AttnEntry*>(kv->scratch + o_ent);
-  }
   a.n = n;
   a.n_heads = D.n_heads;
   a.n_kv = D.n_kv_heads;
@@ -184,12 +185,42 @@ gmoe_status attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n
   a.q = q;
   a.k = k;
   a.v = v;
-  a.qr = reinterpret_cast<float*>(kv->scratch + o_qr);
-  a.part = reinterpret_cast<float*>(kv->scratch + o_part);
+  a.qr = reinterpret_cast<float*>(kv->scratch + l.o_qr);
+  a.part = reinterpret_cast<float*>(kv->scratch + l.o_part);
   a.nchunk = nchunk;
   a.ctx = out;
   a.q_stride = q_stride ? q_stride : D.n_heads * D.head_dim;
   a.kv_stride = kv_stride ? kv_stride : kv->kvd;
+  return a;
+}
+
+// Plans the call's entries and commits them (lengths advance and pages are taken only when
+// the whole call fits), then queues the three launches.
+gmoe_status attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, const float* q, const float* k,
+                   const float* v, float* out, hipStream_t st, uint32_t q_stride = 0, uint32_t kv_stride = 0) {
+  std::vector<AttnEntry> ent(n ? n : 1);
+  uint32_t maxspan;
+  if (gmoe_status s = plan(kv, layer, seqs, n, ent.data(), &maxspan)) return s;
+  const uint32_t nchunk = (maxspan + kAttnChunk - 1) / kAttnChunk;
+  const AttnLayout l = layout(kv, n, nchunk);
+  if (gmoe_status s = grow_scratch(kv, l.total)) return s;
+  if (n > kAttnInline)
+    if (gmoe_status s = grow_pinned(kv, n)) return s;
+  commit(kv, layer, seqs, n, ent.data());
+  AttnArgs a = args(kv, n, nchunk, l, q, k, v, out, q_stride, kv_stride);
+  if (n <= kAttnInline) {  // a decode batch: the entries ride in the kernel arguments
+    std::copy(ent.begin(), ent.begin() + n, a.inl);
+    a.ent = nullptr;
+  } else {
+    const int h = kv->pin_slot;
+    kv->pin_slot = (h + 1) % kPinSlots;
+    KV_TRY(hipEventSynchronize(kv->pin_ev[h]));  // the slot's previous copy has been read
+    AttnEntry* pin = kv->pin + (size_t)h * kv->pin_cap;
+    std::copy(ent.begin(), ent.begin() + n, pin);
+    KV_TRY(hipMemcpyAsync(kv->scratch + l.o_ent, pin, n * sizeof(AttnEntry), hipMemcpyHostToDevice, st));
+    KV_TRY(hipEventRecord(kv->pin_ev[h], st));
+    a.ent = reinterpret_cast<const AttnEntry*>(kv->scratch + l.o_ent);
+  }
   KV_TRY(launch_attention(a, st));
   return GMOE_OK;
 }
@@ -235,6 +266,45 @@ gmoe_status kv_check_step(gmoe_kv* kv, const uint32_t* seqs, uint32_t n) {
   if (pages > kv->free_pages.size())
     return kfail(GMOE_ERR_CACHE, "the KV pool has %zu free pages, the step needs %llu", kv->free_pages.size(),
                  (unsigned long long)pages);
+  return GMOE_OK;
+}
+
+// For decode steps replayed from a HIP graph (gmoe_model.cpp): the host plans and commits
+// each layer's entries (kv_plan_commit) and copies them to device memory the graph's
+// attention launches read (kv_attend_dev). Those launches span kv_graph_chunks chunks,
+// every position a sequence can reach; chunks past an entry's span are empty and merge as
+// nothing, so the result is the same as over the entry's own chunks.
+uint32_t kv_graph_chunks(gmoe_kv* kv) {
+  const gmoe_kv_desc& D = kv->d;
+  const uint32_t span = D.sliding_window ? std::min(D.sliding_window, D.max_positions) : D.max_positions;
+  return (span + kAttnChunk - 1) / kAttnChunk;
+}
+
+gmoe_status kv_reserve(gmoe_kv* kv, uint32_t n, uint32_t nchunk) {
+  std::lock_guard<std::mutex> g(kv->mu);
+  KV_TRY(hipSetDevice(ctx_device(kv->ctx)));
+  return grow_scratch(kv, layout(kv, n, nchunk).total);
+}
+
+const void* kv_scratch_id(gmoe_kv* kv) { return kv->scratch; }
+
+gmoe_status kv_plan_commit(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, AttnEntry* ent) {
+  std::lock_guard<std::mutex> g(kv->mu);
+  uint32_t maxspan;
+  if (gmoe_status s = plan(kv, layer, seqs, n, ent, &maxspan)) return s;
+  commit(kv, layer, seqs, n, ent);
+  return GMOE_OK;
+}
+
+gmoe_status kv_attend_dev(gmoe_kv* kv, uint32_t n, const AttnEntry* d_ent, uint32_t nchunk, const float* q,
+                          const float* k, const float* v, uint32_t q_stride, uint32_t kv_stride, float* out,
+                          hipStream_t st) {
+  std::lock_guard<std::mutex> g(kv->mu);
+  const AttnLayout l = layout(kv, n, nchunk);
+  if (l.total > kv->scratch_bytes) return kfail(GMOE_ERR_INFERENCE, "attention scratch not reserved");
+  AttnArgs a = args(kv, n, nchunk, l, q, k, v, out, q_stride, kv_stride);
+  a.ent = d_ent;
+  KV_TRY(launch_attention(a, st));
   return GMOE_OK;
 }
 

@@ -28,6 +28,14 @@ bool dense_shape(gmoe_ctx* c, uint32_t id, uint32_t* rows, uint32_t* cols);
 bool layer_width(gmoe_ctx* c, uint32_t id, uint32_t* d, uint32_t* ne);
 void kv_dims(gmoe_kv* kv, uint32_t* n_layers, uint32_t* q_dim, uint32_t* kv_dim);
 gmoe_status kv_check_step(gmoe_kv* kv, const uint32_t* seqs, uint32_t n);
+uint32_t kv_graph_chunks(gmoe_kv* kv);
+gmoe_status kv_reserve(gmoe_kv* kv, uint32_t n, uint32_t nchunk);
+const void* kv_scratch_id(gmoe_kv* kv);
+gmoe_status kv_plan_commit(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, AttnEntry* ent);
+gmoe_status kv_attend_dev(gmoe_kv* kv, uint32_t n, const AttnEntry* d_ent, uint32_t nchunk, const float* q,
+                          const float* k, const float* v, uint32_t q_stride, uint32_t kv_stride, float* out,
+                          hipStream_t st);
+const void* ctx_scratch_id(gmoe_ctx* c);
 gmoe_status kv_attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, const float* q, const float* k,
                       const float* v, uint32_t q_stride, uint32_t kv_stride, float* out, hipStream_t st);
 gmoe_status dense_stack(gmoe_ctx* c, const uint32_t* ids, uint32_t count, uint32_t* out);
@@ -54,18 +62,36 @@ struct gmoe_model {
         *y = nullptr, *logits = nullptr;
   uint32_t* next = nullptr;
   uint32_t* pin_next = nullptr;
+  // Decode steps replayed from a HIP graph: the step's launches are captured once per
+  // batch size and read the step's parameters from device memory (par: the tokens, then
+  // every layer's attention entries; pin_par its pinned host copy). The graph is kept
+  // while the scratch allocations its launches point into stay where they were.
+  bool graphs = true, graph_failed = false;
+  hipGraphExec_t gexec = nullptr;
+  uint32_t gn = 0;
+  const void* g_ctx = nullptr;
+  const void* g_kv = nullptr;
+  uint8_t* par = nullptr;
+  uint8_t* pin_par = nullptr;
   std::mutex mu;
 
   ~gmoe_model() {
+    if (gexec) hipGraphExecDestroy(gexec);
+    if (pin_par) hipHostFree(pin_par);
     for (uint32_t id : wqkv) gmoe_dense_release(ctx, id);
     for (void* p : {(void*)table, (void*)norms, (void*)x, (void*)h, (void*)q, (void*)k, (void*)v, (void*)cx,
-                    (void*)ao, (void*)y, (void*)logits, (void*)next, (void*)qkv})
+                    (void*)ao, (void*)y, (void*)logits, (void*)next, (void*)qkv, (void*)par})
       if (p) hipFree(p);
     if (pin_next) hipHostFree(pin_next);
   }
 };
 
 namespace {
+
+// Step parameters in device memory: tokens [kModelMaxBatch], then the attention entries
+// [n_layers][kModelMaxBatch].
+constexpr size_t kParEnt = kModelMaxBatch * 4;
+size_t par_bytes(uint32_t n_layers) { return kParEnt + (size_t)n_layers * kModelMaxBatch * sizeof(AttnEntry); }
 
 gmoe_status mfail(gmoe_status s, const char* fmt, ...) {
   char buf[512];
@@ -160,12 +186,14 @@ gmoe_status gmoe_model_create(gmoe_ctx* ctx, const gmoe_model_desc* desc, gmoe_m
                 {(void**)&m->v, B * kvd * 4},         {(void**)&m->cx, B * qd * 4},
                 {(void**)&m->ao, B * d * 4},          {(void**)&m->y, B * d * 4},
                 {(void**)&m->logits, B * D.vocab * 4}, {(void**)&m->next, B * 4},
-                {(void**)&m->qkv, B * (qd + 2 * (size_t)kvd) * 4}};
+                {(void**)&m->qkv, B * (qd + 2 * (size_t)kvd) * 4},
+                {(void**)&m->par, par_bytes(D.n_layers)}};
   for (auto& a : allocs) {
     const hipError_t e = hipMalloc(a.p, a.bytes);
     if (e != hipSuccess) return fail(mfail(GMOE_ERR_CACHE, "device memory for the model: %s", hipGetErrorString(e)));
   }
   hipError_t e = hipHostMalloc((void**)&m->pin_next, B * 4, hipHostMallocDefault);
+  if (e == hipSuccess) e = hipHostMalloc((void**)&m->pin_par, par_bytes(D.n_layers), hipHostMallocDefault);
   if (e == hipSuccess) e = hipMemcpy(m->table, D.token_embd, table_bytes, hipMemcpyHostToDevice);
   for (uint32_t l = 0; l < D.n_layers && e == hipSuccess; l++) {
     e = hipMemcpy(m->norms + (2 * (size_t)l) * d, D.attn_norm + (size_t)l * d, d * 4, hipMemcpyHostToDevice);
@@ -212,6 +240,26 @@ gmoe_status gmoe_model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs, c
   return model_decode(m, n, seqs, tokens, next, logits, nullptr);
 }
 
+gmoe_status gmoe_model_set_graphs(gmoe_model* m, int enable) {
+  if (!m) return mfail(GMOE_ERR_INFERENCE, "null model");
+  std::lock_guard<std::mutex> g(m->mu);
+  m->graphs = enable != 0;
+  if (!m->graphs && m->gexec) {
+    hipSetDevice(ctx_device(m->ctx));
+    hipStreamSynchronize(ctx_stream(m->ctx));
+    hipGraphExecDestroy(m->gexec);
+    m->gexec = nullptr;
+  }
+  m->graph_failed = false;
+  return GMOE_OK;
+}
+
+int gmoe_model_graph_ready(gmoe_model* m, uint32_t n) {
+  if (!m) return 0;
+  std::lock_guard<std::mutex> g(m->mu);
+  return m->gexec && m->gn == n ? 1 : 0;
+}
+
 gmoe_status gmoe_model_decode_trace(gmoe_model* m, uint32_t n, const uint32_t* seqs, const uint32_t* tokens,
                                     uint32_t* next, float* logits, float* trace) {
   if (!trace) return mfail(GMOE_ERR_INFERENCE, "null trace buffer");
@@ -219,6 +267,98 @@ gmoe_status gmoe_model_decode_trace(gmoe_model* m, uint32_t n, const uint32_t* s
 }
 
 }  // extern "C"
+
+// The launches of one decode step on st, up to the greedy tokens in m->next. With tk,
+// the tokens ride in the embedding's arguments and each layer's attention plans and
+// commits its entries as it is queued; without, the tokens and every layer's entries are
+// read from the step parameters in device memory (m->par, already committed), so the
+// same launches serve every step: the form a graph captures. trace (eager only): every
+// layer's activations copied to the host.
+static gmoe_status step_launches(gmoe_model* m, uint32_t n, const uint32_t* seqs, const GlueTokens* tk, float* trace,
+                                 hipStream_t st) {
+  const uint32_t d = m->d;
+  const uint32_t* dtok = reinterpret_cast<const uint32_t*>(m->par);
+  const AttnEntry* dent = reinterpret_cast<const AttnEntry*>(m->par + kParEnt);
+  const uint32_t nchunk = tk ? 0u : kv_graph_chunks(m->kv);
+  // trace: n rows of `width` floats from `src` (rows `pitch` floats apart) at the trace's
+  // running offset
+  size_t at = 0;
+  auto rec = [&](const float* src, uint32_t width, uint32_t pitch) -> hipError_t {
+    if (!trace) return hipSuccess;
+    const hipError_t e = hipMemcpy2DAsync(trace + at, (size_t)width * 4, src, (size_t)pitch * 4, (size_t)width * 4,
+                                          n, hipMemcpyDeviceToHost, st);
+    at += (size_t)n * width;
+    return e;
+  };
+  M_TRY(tk ? launch_embed(*tk, n, m->table, d, m->x, st) : launch_embed_dev(dtok, n, m->table, d, m->x, st));
+  for (uint32_t l = 0; l < m->n_layers; l++) {
+    // h = norm(x + previous layer's MoE output, attn_norm)
+    M_TRY(launch_add_norm(m->x, l ? m->y : nullptr, m->norms + (2 * (size_t)l) * d, n, d, m->eps, m->h, st));
+    M_TRY(rec(m->x, d, d));
+    M_TRY(rec(m->h, d, d));
+    const AttnEntry* le = dent + (size_t)l * kModelMaxBatch;
+    if (!m->wqkv.empty()) {
+      const uint32_t row = m->qd + 2 * m->kvd;
+      S_TRY(gmoe_dense_forward_async(m->ctx, m->wqkv[l], m->h, n, m->qkv, st));
+      M_TRY(rec(m->qkv, m->qd, row));
+      M_TRY(rec(m->qkv + m->qd, m->kvd, row));
+      M_TRY(rec(m->qkv + m->qd + m->kvd, m->kvd, row));
+      if (tk)
+        S_TRY(kv_attend(m->kv, l, seqs, n, m->qkv, m->qkv + m->qd, m->qkv + m->qd + m->kvd, row, row, m->cx, st));
+      else
+        S_TRY(kv_attend_dev(m->kv, n, le, nchunk, m->qkv, m->qkv + m->qd, m->qkv + m->qd + m->kvd, row, row, m->cx,
+                            st));
+    } else {
+      S_TRY(gmoe_dense_forward_async(m->ctx, m->wq[l], m->h, n, m->q, st));
+      S_TRY(gmoe_dense_forward_async(m->ctx, m->wk[l], m->h, n, m->k, st));
+      S_TRY(gmoe_dense_forward_async(m->ctx, m->wv[l], m->h, n, m->v, st));
+      M_TRY(rec(m->q, m->qd, m->qd));
+      M_TRY(rec(m->k, m->kvd, m->kvd));
+      M_TRY(rec(m->v, m->kvd, m->kvd));
+      if (tk) S_TRY(gmoe_attention_async(m->kv, l, seqs, n, m->q, m->k, m->v, m->cx, st));
+      else S_TRY(kv_attend_dev(m->kv, n, le, nchunk, m->q, m->k, m->v, 0, 0, m->cx, st));
+    }
+    M_TRY(rec(m->cx, m->qd, m->qd));
+    S_TRY(gmoe_dense_forward_async(m->ctx, m->wo[l], m->cx, n, m->ao, st));
+    M_TRY(rec(m->ao, d, d));
+    M_TRY(launch_add_norm(m->x, m->ao, m->norms + (2 * (size_t)l + 1) * d, n, d, m->eps, m->h, st));
+    M_TRY(rec(m->x, d, d));
+    M_TRY(rec(m->h, d, d));
+    S_TRY(gmoe_ffn_forward_async(m->ctx, m->moe[l], m->h, nullptr, n, m->y, nullptr, nullptr, st));
+    M_TRY(rec(m->y, d, d));
+  }
+  M_TRY(launch_add_norm(m->x, m->y, m->norms + 2 * (size_t)m->n_layers * d, n, d, m->eps, m->h, st));
+  M_TRY(rec(m->x, d, d));
+  M_TRY(rec(m->h, d, d));
+  S_TRY(gmoe_dense_forward_async(m->ctx, m->out_id, m->h, n, m->logits, st));
+  M_TRY(launch_argmax(m->logits, n, m->vocab, m->next, st));
+  return GMOE_OK;
+}
+
+// Captures the parameter-reading form of the step for batch n into m->gexec (nothing
+// runs). A capture or instantiation that fails leaves the model on eager steps.
+static void capture_step(gmoe_model* m, uint32_t n, hipStream_t st) {
+  if (m->gexec) hipGraphExecDestroy(m->gexec);
+  m->gexec = nullptr;
+  hipGraph_t g = nullptr;
+  gmoe_status s = GMOE_ERR_DEVICE;
+  hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+  if (e == hipSuccess) {
+    s = step_launches(m, n, nullptr, nullptr, nullptr, st);
+    e = hipStreamEndCapture(st, &g);
+  }
+  if (e == hipSuccess && s == GMOE_OK) e = hipGraphInstantiate(&m->gexec, g, nullptr, nullptr, 0);
+  if (g) hipGraphDestroy(g);
+  if (e != hipSuccess || s != GMOE_OK) {
+    (void)hipGetLastError();
+    m->gexec = nullptr;
+    m->graph_failed = true;
+    return;
+  }
+  m->gn = n;
+  m->g_ctx = ctx_scratch_id(m->ctx);
+  m->g_kv = kv_scratch_id(m->kv);
+}
 
 static gmoe_status model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs, const uint32_t* tokens,
                                 uint32_t* next, float* logits, float* trace) {
@@ -243,56 +383,30 @@ static gmoe_status model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs,
   }
   M_TRY(hipSetDevice(ctx_device(m->ctx)));
   hipStream_t st = ctx_stream(m->ctx);
-  const uint32_t d = m->d;
-  // trace: n rows of `width` floats from `src` (rows `pitch` floats apart) at the trace's
-  // running offset
-  size_t at = 0;
-  auto rec = [&](const float* src, uint32_t width, uint32_t pitch) -> hipError_t {
-    if (!trace) return hipSuccess;
-    const hipError_t e = hipMemcpy2DAsync(trace + at, (size_t)width * 4, src, (size_t)pitch * 4, (size_t)width * 4,
-                                          n, hipMemcpyDeviceToHost, st);
-    at += (size_t)n * width;
-    return e;
-  };
-  M_TRY(launch_embed(tk, n, m->table, d, m->x, st));
-  for (uint32_t l = 0; l < m->n_layers; l++) {
-    // h = norm(x + previous layer's MoE output, attn_norm)
-    M_TRY(launch_add_norm(m->x, l ? m->y : nullptr, m->norms + (2 * (size_t)l) * d, n, d, m->eps, m->h, st));
-    M_TRY(rec(m->x, d, d));
-    M_TRY(rec(m->h, d, d));
-    if (!m->wqkv.empty()) {
-      const uint32_t row = m->qd + 2 * m->kvd;
-      S_TRY(gmoe_dense_forward_async(m->ctx, m->wqkv[l], m->h, n, m->qkv, st));
-      M_TRY(rec(m->qkv, m->qd, row));
-      M_TRY(rec(m->qkv + m->qd, m->kvd, row));
-      M_TRY(rec(m->qkv + m->qd + m->kvd, m->kvd, row));
-      S_TRY(kv_attend(m->kv, l, seqs, n, m->qkv, m->qkv + m->qd, m->qkv + m->qd + m->kvd, row, row, m->cx, st));
+  bool capture = false;
+  if (trace || !m->graphs || m->graph_failed) {
+    S_TRY(step_launches(m, n, seqs, &tk, trace, st));
+  } else {
+    // the step's parameters: tokens, and every layer's attention entries, planned and
+    // committed here (kv_check_step has refused any step that would not fit)
+    std::memcpy(m->pin_par, tk.tok, n * 4);
+    AttnEntry* pent = reinterpret_cast<AttnEntry*>(m->pin_par + kParEnt);
+    for (uint32_t l = 0; l < m->n_layers; l++) S_TRY(kv_plan_commit(m->kv, l, seqs, n, pent + (size_t)l * kModelMaxBatch));
+    M_TRY(hipMemcpyAsync(m->par, m->pin_par, par_bytes(m->n_layers), hipMemcpyHostToDevice, st));
+    if (m->gexec && m->gn == n && m->g_ctx == ctx_scratch_id(m->ctx) && m->g_kv == kv_scratch_id(m->kv)) {
+      M_TRY(hipGraphLaunch(m->gexec, st));
     } else {
-      S_TRY(gmoe_dense_forward_async(m->ctx, m->wq[l], m->h, n, m->q, st));
-      S_TRY(gmoe_dense_forward_async(m->ctx, m->wk[l], m->h, n, m->k, st));
-      S_TRY(gmoe_dense_forward_async(m->ctx, m->wv[l], m->h, n, m->v, st));
-      M_TRY(rec(m->q, m->qd, m->qd));
-      M_TRY(rec(m->k, m->kvd, m->kvd));
-      M_TRY(rec(m->v, m->kvd, m->kvd));
-      S_TRY(gmoe_attention_async(m->kv, l, seqs, n, m->q, m->k, m->v, m->cx, st));
+      // this step runs its launches directly (sizing every scratch it needs); the graph is
+      // captured after it, for the steps that follow
+      S_TRY(kv_reserve(m->kv, n, kv_graph_chunks(m->kv)));
+      S_TRY(step_launches(m, n, seqs, nullptr, nullptr, st));
+      capture = true;
     }
-    M_TRY(rec(m->cx, m->qd, m->qd));
-    S_TRY(gmoe_dense_forward_async(m->ctx, m->wo[l], m->cx, n, m->ao, st));
-    M_TRY(rec(m->ao, d, d));
-    M_TRY(launch_add_norm(m->x, m->ao, m->norms + (2 * (size_t)l + 1) * d, n, d, m->eps, m->h, st));
-    M_TRY(rec(m->x, d, d));
-    M_TRY(rec(m->h, d, d));
-    S_TRY(gmoe_ffn_forward_async(m->ctx, m->moe[l], m->h, nullptr, n, m->y, nullptr, nullptr, st));
-    M_TRY(rec(m->y, d, d));
   }
-  M_TRY(launch_add_norm(m->x, m->y, m->norms + 2 * (size_t)m->n_layers * d, n, d, m->eps, m->h, st));
-  M_TRY(rec(m->x, d, d));
-  M_TRY(rec(m->h, d, d));
-  S_TRY(gmoe_dense_forward_async(m->ctx, m->out_id, m->h, n, m->logits, st));
-  M_TRY(launch_argmax(m->logits, n, m->vocab, m->next, st));
   M_TRY(hipMemcpyAsync(m->pin_next, m->next, n * 4, hipMemcpyDeviceToHost, st));
   if (logits) M_TRY(hipMemcpyAsync(logits, m->logits, (size_t)n * m->vocab * 4, hipMemcpyDeviceToHost, st));
   M_TRY(hipStreamSynchronize(st));
   std::memcpy(next, m->pin_next, n * 4);
+  if (capture) capture_step(m, n, st);
   return GMOE_OK;
 }

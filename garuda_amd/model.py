@@ -73,6 +73,15 @@ class DecodeModel:
                                        nxt.ctypes.data_as(u32p), _fp(logits) if logits is not None else None))
         return (nxt, logits) if want_logits else nxt
 
+    def set_graphs(self, enable: bool) -> None:
+        """Replay decode steps from a HIP graph (the default) or issue every launch of every
+        step (gmoe_model_set_graphs)."""
+        _check(lib().gmoe_model_set_graphs(self._h, 1 if enable else 0))
+
+    def graph_ready(self, n: int) -> bool:
+        """Whether a graph of the step at batch size n is held."""
+        return bool(lib().gmoe_model_graph_ready(self._h, n))
+
     TRACE_KEYS = ("x", "h_attn", "q", "k", "v", "context", "attn_out", "x_mid", "h_ffn", "moe_out")
 
     def decode_step_trace(self, seqs, tokens):

@@ -436,9 +436,17 @@ void gmoe_model_destroy(gmoe_model* model);
  * the greedy next token; logits ([n x vocab], host) may be NULL. 1 <= n <= 64. Refused
  * before any device work when a token is outside the vocabulary (GMOE_ERR_INVALID_TOKEN),
  * a sequence's window is exhausted or the pool lacks pages (GMOE_ERR_CACHE), or an
- * expert is not resident. Synchronous: returns when next (and logits) are written. */
+ * expert is not resident. Synchronous: returns when next (and logits) are written.
+ * The step's launches are replayed from a HIP graph captured after the first step of each
+ * batch size (the tokens and the attention entries are then read from device memory);
+ * the results are those of the launches issued one by one. */
 gmoe_status gmoe_model_decode(gmoe_model* model, uint32_t n, const uint32_t* seqs, const uint32_t* tokens,
                               uint32_t* next, float* logits);
+/* No counterpart in the reference (the execution strategy of gmoe_model_decode):
+ * enable != 0 replays decode steps from a graph (the default), 0 issues every launch of
+ * every step. gmoe_model_graph_ready says whether a graph for batch size n is held. */
+gmoe_status gmoe_model_set_graphs(gmoe_model* model, int enable);
+int gmoe_model_graph_ready(gmoe_model* model, uint32_t n);
 /* Diagnostic, with no counterpart in the reference: gmoe_model_decode that also copies
  * every layer's activations into trace (host, gmoe_model_trace_floats(model, n) floats),
  * for checks of each layer against a restatement fed the device's own inputs. Per layer,

@@ -178,6 +178,39 @@ def test_decode_layers_teacher_forced(dev, weights, math):
         release(*parts)
 
 
+def test_graph_steps_equal_eager_steps(dev, weights):
+    """Decode steps replayed from the captured graph (the default) against the same steps
+    issued launch by launch, on two models of the same weights: next tokens and logits
+    bit for bit at every step. The batch goes 3, 2, 3 (a graph per batch size, the second
+    3-graph recaptured or kept), positions cross page boundaries (pages of 16), and every
+    replay follows the other model's eager work and a synchronisation."""
+    a, b = gpu_model(dev, weights), gpu_model(dev, weights)
+    ma, kva, mb, kvb = a[0], a[1], b[0], b[1]
+    try:
+        ma.set_graphs(False)
+        sa = [kva.open_seq() for _ in range(3)]
+        sb = [kvb.open_seq() for _ in range(3)]
+        rng = np.random.default_rng(5)
+        toks = rng.integers(0, VOCAB, 3).astype(np.uint32)
+        replays = 0
+        for step in range(40):
+            live = [0, 1, 2] if step < 12 or step >= 20 else [0, 2]
+            say(f"graph step {step}, batch {len(live)}")
+            ready = mb.graph_ready(len(live))
+            na, la = ma.decode_step([sa[i] for i in live], toks[live], want_logits=True)
+            nb, lb = mb.decode_step([sb[i] for i in live], toks[live], want_logits=True)
+            replays += ready
+            assert np.array_equal(na, nb), f"step {step}: next tokens differ"
+            assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)), f"step {step}: logits differ"
+            toks[live] = na
+        assert mb.graph_ready(3) and replays >= 30, f"{replays} steps replayed from a graph"
+        for i in range(3):
+            assert kva.seq_len(sa[i], NL - 1) == kvb.seq_len(sb[i], NL - 1)
+    finally:
+        release(*a)
+        release(*b)
+
+
 def test_refusals_leave_the_sequences_unchanged(dev, weights):
     parts = gpu_model(dev, weights, max_positions=3)
     model, kv, moe = parts[0], parts[1], parts[2]
