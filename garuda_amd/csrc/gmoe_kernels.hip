@@ -235,13 +235,28 @@ __global__ void __launch_bounds__(kRouteThreads) k_route(LayerDev L, FwdBufs B, 
         const float4* wr = reinterpret_cast<const float4*>(L.router + (size_t)e * d);
         const float4* hr = reinterpret_cast<const float4*>(B.hs + (size_t)t * d);
         acc = -0.0f;
-        for (uint32_t j = 0; j < d / 4; j++) {
-          float4 a = wr[j], h = hr[j];
-          float p0 = a.x * h.x, p1 = a.y * h.y, p2 = a.z * h.z, p3 = a.w * h.w;
-          acc = acc + p0;
-          acc = acc + p1;
-          acc = acc + p2;
-          acc = acc + p3;
+        // the products of 16 float4 columns at a time, their loads issued together, then
+        // added to the chain in order (the same sequential sum)
+        constexpr uint32_t kRB = 16;
+        const uint32_t n4 = d / 4;
+        for (uint32_t j0 = 0; j0 < n4; j0 += kRB) {
+          float4 a[kRB], h[kRB];
+#pragma unroll
+          for (uint32_t i = 0; i < kRB; i++) {
+            const uint32_t j = min(j0 + i, n4 - 1);
+            a[i] = wr[j];
+            h[i] = hr[j];
+          }
+#pragma unroll
+          for (uint32_t i = 0; i < kRB; i++) {
+            if (j0 + i < n4) {
+              const float p0 = a[i].x * h[i].x, p1 = a[i].y * h[i].y, p2 = a[i].z * h[i].z, p3 = a[i].w * h[i].w;
+              acc = acc + p0;
+              acc = acc + p1;
+              acc = acc + p2;
+              acc = acc + p3;
+            }
+          }
         }
       }
       B.logits[(size_t)t * ne + e] = acc;
