@@ -245,6 +245,15 @@ const void* ctx_scratch_id(gmoe_ctx* c) {
   std::lock_guard<std::mutex> g(c->slab_mu);
   return c->scratch;
 }
+// A graph launched on st uses the scratch arena and the given layers' experts: growing the
+// arena or evicting one of those experts waits for st, as after the calls themselves.
+void ctx_note_graph(gmoe_ctx* c, const uint32_t* layers, uint32_t n, hipStream_t st) {
+  CtxLock g(c);
+  c->scratch_stream = st;
+  for (uint32_t i = 0; i < n; i++)
+    if (layers[i] < c->layers.size() && c->layers[layers[i]] && c->layers[layers[i]]->alive)
+      c->layers[layers[i]]->last_stream = st;
+}
 }  // namespace gmoe
 
 namespace {

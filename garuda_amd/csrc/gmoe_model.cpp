@@ -36,6 +36,7 @@ gmoe_status kv_attend_dev(gmoe_kv* kv, uint32_t n, const AttnEntry* d_ent, uint3
                           const float* k, const float* v, uint32_t q_stride, uint32_t kv_stride, float* out,
                           hipStream_t st);
 const void* ctx_scratch_id(gmoe_ctx* c);
+void ctx_note_graph(gmoe_ctx* c, const uint32_t* layers, uint32_t n, hipStream_t st);
 gmoe_status kv_attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, const float* q, const float* k,
                       const float* v, uint32_t q_stride, uint32_t kv_stride, float* out, hipStream_t st);
 gmoe_status dense_stack(gmoe_ctx* c, const uint32_t* ids, uint32_t count, uint32_t* out);
@@ -67,6 +68,7 @@ struct gmoe_model {
   // every layer's attention entries; pin_par its pinned host copy). The graph is kept
   // while the scratch allocations its launches point into stay where they were.
   bool graphs = true, graph_failed = false;
+  hipStream_t cap = nullptr;  // captures run on a stream of the model's own, which no other caller queues on
   hipGraphExec_t gexec = nullptr;
   uint32_t gn = 0;
   const void* g_ctx = nullptr;
@@ -77,6 +79,7 @@ struct gmoe_model {
 
   ~gmoe_model() {
     if (gexec) hipGraphExecDestroy(gexec);
+    if (cap) hipStreamDestroy(cap);
     if (pin_par) hipHostFree(pin_par);
     for (uint32_t id : wqkv) gmoe_dense_release(ctx, id);
     for (void* p : {(void*)table, (void*)norms, (void*)x, (void*)h, (void*)q, (void*)k, (void*)v, (void*)cx,
@@ -194,6 +197,7 @@ gmoe_status gmoe_model_create(gmoe_ctx* ctx, const gmoe_model_desc* desc, gmoe_m
   }
   hipError_t e = hipHostMalloc((void**)&m->pin_next, B * 4, hipHostMallocDefault);
   if (e == hipSuccess) e = hipHostMalloc((void**)&m->pin_par, par_bytes(D.n_layers), hipHostMallocDefault);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&m->cap, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipMemcpy(m->table, D.token_embd, table_bytes, hipMemcpyHostToDevice);
   for (uint32_t l = 0; l < D.n_layers && e == hipSuccess; l++) {
     e = hipMemcpy(m->norms + (2 * (size_t)l) * d, D.attn_norm + (size_t)l * d, d * 4, hipMemcpyHostToDevice);
@@ -336,8 +340,11 @@ static gmoe_status step_launches(gmoe_model* m, uint32_t n, const uint32_t* seqs
 }
 
 // Captures the parameter-reading form of the step for batch n into m->gexec (nothing
-// runs). A capture or instantiation that fails leaves the model on eager steps.
-static void capture_step(gmoe_model* m, uint32_t n, hipStream_t st) {
+// runs), on the model's own stream, so that no other caller's work on the context's
+// stream joins the graph; the graph is launched on the context's stream. A capture or
+// instantiation that fails leaves the model on eager steps.
+static void capture_step(gmoe_model* m, uint32_t n) {
+  hipStream_t st = m->cap;
   if (m->gexec) hipGraphExecDestroy(m->gexec);
   m->gexec = nullptr;
   hipGraph_t g = nullptr;
@@ -353,11 +360,13 @@ static void capture_step(gmoe_model* m, uint32_t n, hipStream_t st) {
     (void)hipGetLastError();
     m->gexec = nullptr;
     m->graph_failed = true;
+    ctx_note_graph(m->ctx, m->moe.data(), m->n_layers, ctx_stream(m->ctx));
     return;
   }
   m->gn = n;
   m->g_ctx = ctx_scratch_id(m->ctx);
   m->g_kv = kv_scratch_id(m->kv);
+  ctx_note_graph(m->ctx, m->moe.data(), m->n_layers, ctx_stream(m->ctx));
 }
 
 static gmoe_status model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs, const uint32_t* tokens,
@@ -395,6 +404,7 @@ static gmoe_status model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs,
     M_TRY(hipMemcpyAsync(m->par, m->pin_par, par_bytes(m->n_layers), hipMemcpyHostToDevice, st));
     if (m->gexec && m->gn == n && m->g_ctx == ctx_scratch_id(m->ctx) && m->g_kv == kv_scratch_id(m->kv)) {
       M_TRY(hipGraphLaunch(m->gexec, st));
+      ctx_note_graph(m->ctx, m->moe.data(), m->n_layers, st);
     } else {
       // this step runs its launches directly (sizing every scratch it needs); the graph is
       // captured after it, for the steps that follow
@@ -407,6 +417,6 @@ static gmoe_status model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs,
   if (logits) M_TRY(hipMemcpyAsync(logits, m->logits, (size_t)n * m->vocab * 4, hipMemcpyDeviceToHost, st));
   M_TRY(hipStreamSynchronize(st));
   std::memcpy(next, m->pin_next, n * 4);
-  if (capture) capture_step(m, n, st);
+  if (capture) capture_step(m, n);
   return GMOE_OK;
 }
