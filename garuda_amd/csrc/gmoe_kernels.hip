@@ -963,6 +963,7 @@ __device__ __forceinline__ double sum_gamma(double m) {
 __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs B, uint32_t n, int quant) {
   __shared__ float lt[kFrontExperts], la[kFrontExperts];
   __shared__ uint32_t cl[kFrontExperts];
+  __shared__ double sb[2 * kFrontExperts];  // candidate test: lo, then hi, of each expert
   const uint32_t ne = L.ne, d = L.d, k = L.k, t = blockIdx.x;
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const float* hs = B.hs + (size_t)t * d;
@@ -1054,18 +1055,40 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
   const double delta = (sum_gamma(m_seq) + sum_gamma(m_tree)) * A * (1.0 + 0x1p-20);
   const bool fin = !valid || (isfinite(Lt) && isfinite(delta));
   const double lo = Lt - delta, hi = Lt + delta;
-  double maxhi = valid ? hi : -INFINITY;
-  for (int o = 32; o >= 1; o >>= 1) maxhi = fmax(maxhi, __shfl_xor(maxhi, o, 64));
+  // every lane reads every expert's bounds from LDS, eight at a time with their loads
+  // issued together (a shuffle per expert would wait out one LDS round trip each)
+  if (valid) {
+    sb[lane] = lo;
+    sb[kFrontExperts + lane] = hi;
+  }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");  // one wave: its DS writes land before these reads
+  // f(j, lo_j, hi_j) for j = 0 .. ne-1 in order
+  auto each = [&](auto f) {
+    for (uint32_t j0 = 0; j0 < ne; j0 += 8) {
+      double l8[8], h8[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const uint32_t j = min(j0 + i, ne - 1);
+        l8[i] = sb[j];
+        h8[i] = sb[kFrontExperts + j];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        if (j0 + i < ne) f(j0 + i, l8[i], h8[i]);
+    }
+  };
+  double maxhi = -INFINITY;
+  each([&](uint32_t, double, double hj) { maxhi = fmax(maxhi, hj); });
   const bool all_fin = __ballot(!fin) == 0ull;
   // experts certainly clear of expf's underflow relative to the largest logit
   const uint32_t safe = (uint32_t)__popcll(__ballot(valid && lo - maxhi > -80.0));
   const bool all = !all_fin || (L.gating != 1 && safe < k);
   const double eps = 4e-6 * (1.0 + fabs(Lt) + fabs(maxhi));
   uint32_t above = 0;
-  for (uint32_t j = 0; j < ne; j++) {
-    const double loj = __shfl(lo, (int)j, 64);
+  each([&](uint32_t j, double loj, double) {
     if (j != lane && loj > hi + eps) above++;
-  }
+  });
   const bool cand = valid && (all || above < k);
   const uint64_t cm = __ballot(cand);
   const uint32_t pos = (uint32_t)__popcll(cm & ((1ull << lane) - 1ull)), nc = (uint32_t)__popcll(cm);
@@ -1075,10 +1098,33 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
   const uint32_t my = lane < nc ? cl[lane] : ~0u;
   if (lane < ne) B.cand[(size_t)t * ne + lane] = my;
   if (n == 1) {
-    dispatch_wave(B, [&](int p) { return ep[p]; }, ne, ne, ne, lane, [&](uint32_t, uint32_t* pid, float* pw) {
-      *pid = my;
-      *pw = 0.0f;
-    }, false);
+    // one token: what dispatch_wave makes of its candidate list, written directly. Every
+    // candidate has one pair, so the experts of equal count go in ascending id order:
+    // candidate e's active slot, first pair slot and token tile are all its rank pos
+    // among the candidates, and its one pair is token 0's.
+    if (valid) {
+      B.offsets[lane] = pos;
+      if (cand) {
+        B.active[1 + pos] = lane;
+        if (B.work) {
+          ExpertWork& W = B.work[pos];
+          for (int p = 0; p < 3; p++) W.w[p] = ep[p];
+          W.e = lane;
+          W.s0 = pos;
+          W.m = 1;
+        }
+        B.slot_tok[pos] = 0;
+      }
+      if (B.work && lane >= nc) B.work[lane].m = 0;
+    }
+    if (lane == 0) {
+      B.offsets[ne] = nc;
+      B.active[0] = nc;
+    }
+    if (B.ptile) {
+      if (cand) B.ptile[pos] = pos << 16;
+      for (uint32_t i = nc + lane; i < B.ptile_cap; i += 64) B.ptile[i] = ~0u;
+    }
     return;
   }
   __threadfence();
