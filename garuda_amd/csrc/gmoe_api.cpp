@@ -787,6 +787,7 @@ size_t plan_dense(const gmoe_ctx* c, const Dense& W, uint32_t n, uint8_t* base, 
   return P.total;
 }
 
+// out null: the K slices are left in cv.B.y ([cv.ksg][n][rows]) for the caller to add.
 gmoe_status run_dense(const Dense& W, const DenseCarve& cv, const float* x, uint32_t n, float* out, hipStream_t st) {
   const LayerDev D = dense_dev(W);
   FwdBufs B = cv.B;
@@ -809,7 +810,7 @@ gmoe_status run_dense(const Dense& W, const DenseCarve& cv, const float* x, uint
     }
     HIP_TRY(launch_down(D, B, n, st, cv.ksg));
   }
-  HIP_TRY(launch_reduce_parts(B.y, cv.ksg, (size_t)n * W.rows, out, st));
+  if (out) HIP_TRY(launch_reduce_parts(B.y, cv.ksg, (size_t)n * W.rows, out, st));
   return GMOE_OK;
 }
 
@@ -823,6 +824,27 @@ gmoe_status get_dense(gmoe_ctx* c, uint32_t id, Dense** out) {
     return fail(GMOE_ERR_INFERENCE, "unknown dense weight id %u", id);
   *out = c->dense[id].get();
   return GMOE_OK;
+}
+
+// A dense call without its slice sum: *parts holds [*nsl][n][rows] K slices in the
+// context's scratch, which the caller's next launch on st adds in slice order (the sum
+// k_reduce_parts makes), before any other call on the context reuses the scratch.
+gmoe_status dense_slices(gmoe_ctx* c, uint32_t id, const float* d_xs, uint32_t n, hipStream_t st, const float** parts,
+                         uint32_t* nsl) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (!d_xs || !parts || !nsl) return fail(GMOE_ERR_INFERENCE, "null activation or output pointer");
+  if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
+  CtxLock g(c);
+  Dense* W;
+  if (gmoe_status s = get_dense(c, id, &W)) return s;
+  HIP_TRY(hipSetDevice(c->device));
+  if (gmoe_status s = ensure_scratch(c, plan_dense(c, *W, n, nullptr, nullptr))) return s;
+  DenseCarve cv;
+  plan_dense(c, *W, n, c->scratch, &cv);
+  if (gmoe_status s = run_dense(*W, cv, d_xs, n, nullptr, st)) return s;
+  *parts = cv.B.y;
+  *nsl = cv.ksg;
+  return mark_scratch(c, st);
 }
 
 gmoe_status get_layer(gmoe_ctx* c, uint32_t id, Layer** out) {
@@ -954,6 +976,12 @@ gmoe_status dense_tables(gmoe_ctx* c, Dense* W) {
 }  // namespace
 
 namespace gmoe {
+
+// The dense call without its slice sum, for the model step (dense_slices).
+gmoe_status dense_forward_slices(gmoe_ctx* c, uint32_t id, const float* d_xs, uint32_t n, hipStream_t st,
+                                 const float** parts, uint32_t* nsl) {
+  return dense_slices(c, id, d_xs, n, st, parts, nsl);
+}
 
 // One dense weight made of registered ones laid end to end: its rows are theirs in order
 // (out = [W0 x; W1 x; ...]). They share type, width and math, and every one but the last

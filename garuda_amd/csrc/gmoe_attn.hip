@@ -39,6 +39,32 @@ __device__ __forceinline__ const float* key_row(const AttnArgs& a, const AttnEnt
 }
 
 // grid (n, ceil(pairs / 256)), pairs = (n_heads + n_kv) * hd / 2
+// (x, y) = elements 2j, 2j+1 from p, each the sum of nsl K slices `stride` floats apart in
+// slice order when nsl > 1 (k_reduce_parts's sum); the slice loads are issued together
+// (indices clamped, the surplus ones not added)
+__device__ __forceinline__ void ld_pair(const float* p, uint32_t j, uint32_t nsl, uint64_t stride, float& x, float& y) {
+  if (nsl <= 1) {
+    x = p[2 * j];
+    y = p[2 * j + 1];
+    return;
+  }
+  float vx[kMaxKsg], vy[kMaxKsg];
+#pragma unroll
+  for (uint32_t g = 0; g < kMaxKsg; g++) {
+    const float* s = p + min(g, nsl - 1) * stride;
+    vx[g] = s[2 * j];
+    vy[g] = s[2 * j + 1];
+  }
+  x = vx[0];
+  y = vy[0];
+#pragma unroll
+  for (uint32_t g = 1; g < kMaxKsg; g++)
+    if (g < nsl) {
+      x += vx[g];
+      y += vy[g];
+    }
+}
+
 __global__ void __launch_bounds__(256) k_rope_append(AttnArgs a) {
   const uint32_t i = blockIdx.x, half = a.hd / 2, kvd = a.n_kv * a.hd;
   const uint32_t pr = blockIdx.y * 256 + threadIdx.x, qpairs = a.n_heads * half;
@@ -50,7 +76,8 @@ __global__ void __launch_bounds__(256) k_rope_append(AttnArgs a) {
   if (pr < qpairs) {
     const uint32_t h = pr / half, j = pr % half;
     const float* src = a.q + (size_t)i * a.q_stride + h * a.hd;
-    float x = src[2 * j], y = src[2 * j + 1];
+    float x, y;
+    ld_pair(src, j, a.nsl, a.sl_stride, x, y);
     rope_pair(x, y, j, a.hd, e.pos, a.theta);
     float* dst = a.qr + (size_t)i * a.n_heads * a.hd + h * a.hd;
     dst[2 * j] = x;
@@ -58,14 +85,17 @@ __global__ void __launch_bounds__(256) k_rope_append(AttnArgs a) {
   } else if (pr < qpairs + a.n_kv * half) {
     const uint32_t p2 = pr - qpairs, h = p2 / half, j = p2 % half;
     const float* src = a.k + (size_t)i * a.kv_stride + h * a.hd;
-    float x = src[2 * j], y = src[2 * j + 1];
+    float x, y;
+    ld_pair(src, j, a.nsl, a.sl_stride, x, y);
     rope_pair(x, y, j, a.hd, e.pos, a.theta);
     const size_t hoff = (size_t)h * a.bs * a.hd;
     kp[hoff + 2 * j] = x;
     kp[hoff + 2 * j + 1] = y;
     const float* vs = a.v + (size_t)i * a.kv_stride + h * a.hd;
-    vp[hoff + 2 * j] = vs[2 * j];
-    vp[hoff + 2 * j + 1] = vs[2 * j + 1];
+    float vx, vy;
+    ld_pair(vs, j, a.nsl, a.sl_stride, vx, vy);
+    vp[hoff + 2 * j] = vx;
+    vp[hoff + 2 * j + 1] = vy;
   }
 }
 

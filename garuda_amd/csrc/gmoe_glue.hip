@@ -46,10 +46,14 @@ __global__ void __launch_bounds__(256) k_embed_dev(const uint32_t* __restrict__ 
 // grid n, 256 threads: with y, x[i] += y[i] first (written back); then
 // h[i] = (x[i] * scale) * w with scale = 1 / sqrt(mean(x[i]^2) + eps). A thread holds its
 // kNormVec float4 of the row (d <= 4 * 256 * kNormVec, checked by the model) in
-// registers, every load issued before any use.
+// registers, every load issued before any use. SL: y is the sum of nsl K slices of a
+// dense product, `stride` floats apart, added in slice order (k_reduce_parts's sum) before
+// it is added to x; a float4's slice loads are issued together (slice indices clamped,
+// the surplus ones not added).
+template <bool SL>
 __global__ void __launch_bounds__(256) k_add_norm(float* __restrict__ x, const float* __restrict__ y,
                                                   const float* __restrict__ w, uint32_t d, float eps,
-                                                  float* __restrict__ h) {
+                                                  float* __restrict__ h, uint32_t nsl, size_t stride) {
   __shared__ float part[4];
   const uint32_t i = blockIdx.x, t = threadIdx.x, nv = d / 4;
   float4* xr = reinterpret_cast<float4*>(x + (size_t)i * d);
@@ -66,7 +70,20 @@ __global__ void __launch_bounds__(256) k_add_norm(float* __restrict__ x, const f
 #pragma unroll
     for (int r = 0; r < kNormVec; r++) {
       const uint32_t c = t + 256 * r;
-      if (c < nv) yv[r] = yr[c];
+      if (c < nv) {
+        if constexpr (SL) {
+          float4 p[kMaxKsg];
+#pragma unroll
+          for (uint32_t g = 0; g < kMaxKsg; g++) p[g] = yr[c + (size_t)min(g, nsl - 1) * (stride / 4)];
+          float4 a = p[0];
+#pragma unroll
+          for (uint32_t g = 1; g < kMaxKsg; g++)
+            if (g < nsl) a = make_float4(a.x + p[g].x, a.y + p[g].y, a.z + p[g].z, a.w + p[g].w);
+          yv[r] = a;
+        } else {
+          yv[r] = yr[c];
+        }
+      }
     }
 #pragma unroll
     for (int r = 0; r < kNormVec; r++) {
@@ -163,7 +180,14 @@ hipError_t launch_embed_dev(const uint32_t* tok, uint32_t n, const float* table,
 
 hipError_t launch_add_norm(float* x, const float* y, const float* w, uint32_t n, uint32_t d, float eps, float* h,
                            hipStream_t st) {
-  hipLaunchKernelGGL(k_add_norm, dim3(n), dim3(256), 0, st, x, y, w, d, eps, h);
+  hipLaunchKernelGGL(k_add_norm<false>, dim3(n), dim3(256), 0, st, x, y, w, d, eps, h, 1u, (size_t)0);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_norm_slices(float* x, const float* parts, uint32_t nsl, const float* w, uint32_t n, uint32_t d,
+                                  float eps, float* h, hipStream_t st) {
+  if (nsl == 0 || nsl > kMaxKsg || d % 4) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_add_norm<true>, dim3(n), dim3(256), 0, st, x, parts, w, d, eps, h, nsl, (size_t)n * d);
   return hipGetLastError();
 }
 

@@ -345,6 +345,8 @@ struct AttnArgs {
   uint32_t nchunk;       // chunks of kAttnChunk positions per entry
   float* ctx;            // [n][n_heads * hd]
   uint32_t q_stride, kv_stride;  // floats between consecutive rows of q, and of k and v
+  uint32_t nsl;                  // > 1: q, k and v are each the sum of nsl K slices of a dense
+  uint64_t sl_stride;            //   product, sl_stride floats apart (added in slice order)
 };
 
 constexpr uint32_t kAttnChunk = 64, kAttnMaxGroup = 16, kAttnMaxHd = 256;
@@ -361,6 +363,9 @@ hipError_t launch_embed(const GlueTokens& tk, uint32_t n, const float* table, ui
 hipError_t launch_embed_dev(const uint32_t* tok, uint32_t n, const float* table, uint32_t d, float* x, hipStream_t st);
 hipError_t launch_add_norm(float* x, const float* y, const float* w, uint32_t n, uint32_t d, float eps, float* h,
                            hipStream_t st);
+// the same with y the sum of nsl K slices [nsl][n][d] of a dense product (k_reduce_parts's sum)
+hipError_t launch_add_norm_slices(float* x, const float* parts, uint32_t nsl, const float* w, uint32_t n, uint32_t d,
+                                  float eps, float* h, hipStream_t st);
 hipError_t launch_argmax(const float* logits, uint32_t n, uint32_t vocab, uint32_t* next, hipStream_t st);
 
 hipError_t launch_tile_rows(uint32_t qtype, const uint8_t* raw, uint32_t r0, uint32_t nrows, uint32_t rows,

@@ -298,12 +298,15 @@ gmoe_status kv_plan_commit(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, ui
 
 gmoe_status kv_attend_dev(gmoe_kv* kv, uint32_t n, const AttnEntry* d_ent, uint32_t nchunk, const float* q,
                           const float* k, const float* v, uint32_t q_stride, uint32_t kv_stride, float* out,
-                          hipStream_t st) {
+                          hipStream_t st, uint32_t nsl, uint64_t sl_stride) {
   std::lock_guard<std::mutex> g(kv->mu);
   const AttnLayout l = layout(kv, n, nchunk);
   if (l.total > kv->scratch_bytes) return kfail(GMOE_ERR_INFERENCE, "attention scratch not reserved");
+  if (nsl > kMaxKsg) return kfail(GMOE_ERR_INFERENCE, "%u K slices exceed %u", nsl, kMaxKsg);
   AttnArgs a = args(kv, n, nchunk, l, q, k, v, out, q_stride, kv_stride);
   a.ent = d_ent;
+  a.nsl = nsl;
+  a.sl_stride = sl_stride;
   KV_TRY(launch_attention(a, st));
   return GMOE_OK;
 }

@@ -34,7 +34,9 @@ const void* kv_scratch_id(gmoe_kv* kv);
 gmoe_status kv_plan_commit(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, AttnEntry* ent);
 gmoe_status kv_attend_dev(gmoe_kv* kv, uint32_t n, const AttnEntry* d_ent, uint32_t nchunk, const float* q,
                           const float* k, const float* v, uint32_t q_stride, uint32_t kv_stride, float* out,
-                          hipStream_t st);
+                          hipStream_t st, uint32_t nsl = 1, uint64_t sl_stride = 0);
+gmoe_status dense_forward_slices(gmoe_ctx* c, uint32_t id, const float* d_xs, uint32_t n, hipStream_t st,
+                                 const float** parts, uint32_t* nsl);
 const void* ctx_scratch_id(gmoe_ctx* c);
 void ctx_note_graph(gmoe_ctx* c, const uint32_t* layers, uint32_t n, hipStream_t st);
 gmoe_status kv_attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, const float* q, const float* k,
@@ -303,15 +305,21 @@ static gmoe_status step_launches(gmoe_model* m, uint32_t n, const uint32_t* seqs
     const AttnEntry* le = dent + (size_t)l * kModelMaxBatch;
     if (!m->wqkv.empty()) {
       const uint32_t row = m->qd + 2 * m->kvd;
-      S_TRY(gmoe_dense_forward_async(m->ctx, m->wqkv[l], m->h, n, m->qkv, st));
-      M_TRY(rec(m->qkv, m->qd, row));
-      M_TRY(rec(m->qkv + m->qd, m->kvd, row));
-      M_TRY(rec(m->qkv + m->qd + m->kvd, m->kvd, row));
-      if (tk)
+      if (tk) {
+        S_TRY(gmoe_dense_forward_async(m->ctx, m->wqkv[l], m->h, n, m->qkv, st));
+        M_TRY(rec(m->qkv, m->qd, row));
+        M_TRY(rec(m->qkv + m->qd, m->kvd, row));
+        M_TRY(rec(m->qkv + m->qd + m->kvd, m->kvd, row));
         S_TRY(kv_attend(m->kv, l, seqs, n, m->qkv, m->qkv + m->qd, m->qkv + m->qd + m->kvd, row, row, m->cx, st));
-      else
-        S_TRY(kv_attend_dev(m->kv, n, le, nchunk, m->qkv, m->qkv + m->qd, m->qkv + m->qd + m->kvd, row, row, m->cx,
-                            st));
+      } else {
+        // the projection's K slices go straight to the attention's first launch, which
+        // adds them in slice order as it reads q, k and v (no k_reduce_parts launch)
+        const float* qkv;
+        uint32_t nsl;
+        S_TRY(dense_forward_slices(m->ctx, m->wqkv[l], m->h, n, st, &qkv, &nsl));
+        S_TRY(kv_attend_dev(m->kv, n, le, nchunk, qkv, qkv + m->qd, qkv + m->qd + m->kvd, row, row, m->cx, st, nsl,
+                            (uint64_t)n * row));
+      }
     } else {
       S_TRY(gmoe_dense_forward_async(m->ctx, m->wq[l], m->h, n, m->q, st));
       S_TRY(gmoe_dense_forward_async(m->ctx, m->wk[l], m->h, n, m->k, st));
@@ -323,9 +331,16 @@ static gmoe_status step_launches(gmoe_model* m, uint32_t n, const uint32_t* seqs
       else S_TRY(kv_attend_dev(m->kv, n, le, nchunk, m->q, m->k, m->v, 0, 0, m->cx, st));
     }
     M_TRY(rec(m->cx, m->qd, m->qd));
-    S_TRY(gmoe_dense_forward_async(m->ctx, m->wo[l], m->cx, n, m->ao, st));
-    M_TRY(rec(m->ao, d, d));
-    M_TRY(launch_add_norm(m->x, m->ao, m->norms + (2 * (size_t)l + 1) * d, n, d, m->eps, m->h, st));
+    if (tk) {
+      S_TRY(gmoe_dense_forward_async(m->ctx, m->wo[l], m->cx, n, m->ao, st));
+      M_TRY(rec(m->ao, d, d));
+      M_TRY(launch_add_norm(m->x, m->ao, m->norms + (2 * (size_t)l + 1) * d, n, d, m->eps, m->h, st));
+    } else {  // the output projection's K slices added by the residual add (no k_reduce_parts launch)
+      const float* ao;
+      uint32_t nsl;
+      S_TRY(dense_forward_slices(m->ctx, m->wo[l], m->cx, n, st, &ao, &nsl));
+      M_TRY(launch_add_norm_slices(m->x, ao, nsl, m->norms + (2 * (size_t)l + 1) * d, n, d, m->eps, m->h, st));
+    }
     M_TRY(rec(m->x, d, d));
     M_TRY(rec(m->h, d, d));
     S_TRY(gmoe_ffn_forward_async(m->ctx, m->moe[l], m->h, nullptr, n, m->y, nullptr, nullptr, st));

@@ -30,6 +30,20 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.gmoe_last_invalid_token() == 0xFFFFFFFF  # none yet on this thread
 
 
+def test_library_leaves_no_internal_symbol_undefined():
+    """A shared library links with undefined symbols; one of the library's own (namespace
+    gmoe) would only fail when the library is loaded on the GPU box."""
+    import shutil
+    import subprocess
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm is not installed")
+    out = subprocess.run([nm, "-D", "--undefined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    own = [l.split()[-1] for l in out.splitlines() if l.split() and l.split()[-1].startswith("_ZN4gmoe")]
+    assert not own, own
+
+
 @pytest.mark.parametrize("qtype", [M.Q4_K, M.Q5_K, M.Q6_K, M.Q3_K, M.Q2_K, M.Q8_0, M.Q4_0, M.F16, M.F32])
 def test_quantiser_round_trips_through_the_reference_decoder(qtype):
     x = M.fill_gaussian(1234 + qtype, 256 * 64, 0.0, 0.02)
