@@ -325,21 +325,45 @@ __device__ __forceinline__ void quant32(const float* v, int8_t* q, float* s, uin
 // `sums` of which the wave holds values r0 .. r0 + 63. `valid` (uniform over each 32-lane
 // half) leaves blocks past the end of the row unwritten; every lane of the wave must call
 // this.
+// Cross-lane moves within a row of 16 lanes as DPP operand modifiers (a VALU operand, no
+// LDS round trip as __shfl's ds_bpermute takes): lane i reads lane i ^ 1 (quad_perm
+// [1,0,3,2]), i ^ 2 (quad_perm [2,3,0,1]), 7 - i within its 8 (row_half_mirror), 15 - i
+// within its 16 (row_mirror), i + n within its row (row_shl:n; lanes past the row's end
+// read 0).
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140, kDppShl1 = 0x101;
+
 __device__ __forceinline__ void quant_wave(float v, uint32_t lane, bool valid, int8_t* q, float* s, uint32_t* sums,
                                            uint32_t r0, int kind, int32_t off) {
+  // the max over the lane's 32 (16 by DPP, then the other 16): after the two quad steps
+  // every lane holds its quad's value, after the half mirror its 8's, after the mirror its 16's
   float a = fmaxf(0.0f, fabsf(v));
-#pragma unroll
-  for (int o = 16; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+  a = fmaxf(a, dpp_f<kDppXor1>(a));
+  a = fmaxf(a, dpp_f<kDppXor2>(a));
+  a = fmaxf(a, dpp_f<kDppHalfMirror>(a));
+  a = fmaxf(a, dpp_f<kDppMirror>(a));
+  a = fmaxf(a, __shfl_xor(a, 16, 64));
   const float scale = fdiv(a, 127.0f);
   const float inv = scale > 0.0f ? fdiv(1.0f, scale) : 0.0f;
   const float r = roundf(v * inv);
   const int qi = (r != r) ? 0 : r < -127.0f ? -127 : r > 127.0f ? 127 : (int)r;
-  int sum = qi;
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  int sum = qi;  // over the lane's 16, the same way (integer: any order is exact)
+  sum += dpp_i<kDppXor1>(sum);
+  sum += dpp_i<kDppXor2>(sum);
+  sum += dpp_i<kDppHalfMirror>(sum);
+  sum += dpp_i<kDppMirror>(sum);
   const int sum32 = sum + __shfl_xor(sum, 16, 64);
+  // lanes 4j pack lanes 4j .. 4j+3 (all in one row)
   const uint32_t b = (uint32_t)qi & 0xffu;
-  const uint32_t word = b | (__shfl_down(b, 1, 64) << 8) | (__shfl_down(b, 2, 64) << 16) | (__shfl_down(b, 3, 64) << 24);
+  const uint32_t word = b | ((uint32_t)dpp_i<kDppShl1>((int)b) << 8) | ((uint32_t)dpp_i<kDppShl1 + 1>((int)b) << 16) |
+                        ((uint32_t)dpp_i<kDppShl1 + 2>((int)b) << 24);
   if (valid) {
     if ((lane & 3) == 0) reinterpret_cast<uint32_t*>(q)[lane / 4] = word;
     if ((lane & 31) == 0) s[lane / 32] = scale;
