@@ -99,14 +99,8 @@ __global__ void __launch_bounds__(256) k_rope_append(AttnArgs a) {
   }
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+__device__ __forceinline__ float wave_max(float v) { return wave64_max(v); }
+__device__ __forceinline__ float wave_sum(float v) { return wave64_sum(v); }
 
 // grid (n, n_kv, nchunk), 256 threads: one chunk of kAttnChunk positions for the
 // `group` query heads of one kv head. Thread t takes position j = t / 4 of the chunk and
@@ -197,8 +191,8 @@ __global__ void __launch_bounds__(256) k_attn_partial(AttnArgs a) {
   for (int g = 0; g < kAttnMaxGroup; g++) {
     if ((uint32_t)g < G) {
       float v = acc[g];
-      v += __shfl_xor(v, 1, 64);
-      v += __shfl_xor(v, 2, 64);
+      v += dpp_f<kDppXor1>(v);
+      v += dpp_f<kDppXor2>(v);
       if (qq == 0) ps(g, j) = rowok ? v * a.scale : -INFINITY;
     }
   }

@@ -340,6 +340,27 @@ __device__ __forceinline__ float dpp_f(float v) {
 }
 constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140, kDppShl1 = 0x101;
 
+// Butterfly sum and maximum over a wave: every lane ends with the result. Each level
+// combines two halves that hold the same bits in every lane (a + b and b + a are equal),
+// so within a row of 16 the DPP mirrors stand in for xor 4 and xor 8; xor 16 and xor 32
+// go through ds_bpermute. Levels run from distance 1 up.
+__device__ __forceinline__ float wave64_sum(float v) {
+  v += dpp_f<kDppXor1>(v);
+  v += dpp_f<kDppXor2>(v);
+  v += dpp_f<kDppHalfMirror>(v);
+  v += dpp_f<kDppMirror>(v);
+  v += __shfl_xor(v, 16, 64);
+  return v + __shfl_xor(v, 32, 64);
+}
+__device__ __forceinline__ float wave64_max(float v) {
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+
 __device__ __forceinline__ void quant_wave(float v, uint32_t lane, bool valid, int8_t* q, float* s, uint32_t* sums,
                                            uint32_t r0, int kind, int32_t off) {
   // the max over the lane's 32 (16 by DPP, then the other 16): after the two quad steps

@@ -18,10 +18,7 @@ namespace gmoe {
 
 namespace {
 
-__device__ __forceinline__ float glue_wave_sum(float v) {
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+__device__ __forceinline__ float glue_wave_sum(float v) { return wave64_sum(v); }
 
 }  // namespace
 

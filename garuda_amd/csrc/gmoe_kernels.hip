@@ -1015,10 +1015,8 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
         ab = ab + fabsf(p0); ab = ab + fabsf(p1); ab = ab + fabsf(p2); ab = ab + fabsf(p3);
       }
     }
-    for (int o = 32; o >= 1; o >>= 1) {
-      sm += __shfl_xor(sm, o, 64);
-      ab += __shfl_xor(ab, o, 64);
-    }
+    sm = wave64_sum(sm);  // a tree of 6 levels, as the bound below counts
+    ab = wave64_sum(ab);
     if (lane == 0) {
       lt[e] = sm;
       la[e] = ab;
