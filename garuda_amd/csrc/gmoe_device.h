@@ -340,25 +340,44 @@ __device__ __forceinline__ float dpp_f(float v) {
 }
 constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140, kDppShl1 = 0x101;
 
+// A lane's value and its xor-16 (xor-32) partner's: v_permlane16_swap (v_permlane32_swap)
+// of v with itself leaves the two in the pair's halves, own and partner's in some order
+// (checked on the device).
+struct LanePair {
+  float a, b;
+};
+__device__ __forceinline__ LanePair xor16_pair(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return {__int_as_float(p[0]), __int_as_float(p[1])};
+}
+__device__ __forceinline__ LanePair xor32_pair(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return {__int_as_float(p[0]), __int_as_float(p[1])};
+}
+
 // Butterfly sum and maximum over a wave: every lane ends with the result. Each level
 // combines two halves that hold the same bits in every lane (a + b and b + a are equal),
-// so within a row of 16 the DPP mirrors stand in for xor 4 and xor 8; xor 16 and xor 32
-// go through ds_bpermute. Levels run from distance 1 up.
+// so within a row of 16 the DPP mirrors stand in for xor 4 and xor 8, and the permlane
+// swaps give xor 16 and xor 32: no level goes through LDS. Levels run from distance 1 up.
 __device__ __forceinline__ float wave64_sum(float v) {
   v += dpp_f<kDppXor1>(v);
   v += dpp_f<kDppXor2>(v);
   v += dpp_f<kDppHalfMirror>(v);
   v += dpp_f<kDppMirror>(v);
-  v += __shfl_xor(v, 16, 64);
-  return v + __shfl_xor(v, 32, 64);
+  LanePair p = xor16_pair(v);
+  v = p.a + p.b;
+  p = xor32_pair(v);
+  return p.a + p.b;
 }
 __device__ __forceinline__ float wave64_max(float v) {
   v = fmaxf(v, dpp_f<kDppXor1>(v));
   v = fmaxf(v, dpp_f<kDppXor2>(v));
   v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
   v = fmaxf(v, dpp_f<kDppMirror>(v));
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return fmaxf(v, __shfl_xor(v, 32, 64));
+  LanePair p = xor16_pair(v);
+  v = fmaxf(p.a, p.b);
+  p = xor32_pair(v);
+  return fmaxf(p.a, p.b);
 }
 
 __device__ __forceinline__ void quant_wave(float v, uint32_t lane, bool valid, int8_t* q, float* s, uint32_t* sums,
@@ -370,7 +389,8 @@ __device__ __forceinline__ void quant_wave(float v, uint32_t lane, bool valid, i
   a = fmaxf(a, dpp_f<kDppXor2>(a));
   a = fmaxf(a, dpp_f<kDppHalfMirror>(a));
   a = fmaxf(a, dpp_f<kDppMirror>(a));
-  a = fmaxf(a, __shfl_xor(a, 16, 64));
+  const LanePair ap = xor16_pair(a);
+  a = fmaxf(ap.a, ap.b);
   const float scale = fdiv(a, 127.0f);
   const float inv = scale > 0.0f ? fdiv(1.0f, scale) : 0.0f;
   const float r = roundf(v * inv);
@@ -380,7 +400,8 @@ __device__ __forceinline__ void quant_wave(float v, uint32_t lane, bool valid, i
   sum += dpp_i<kDppXor2>(sum);
   sum += dpp_i<kDppHalfMirror>(sum);
   sum += dpp_i<kDppMirror>(sum);
-  const int sum32 = sum + __shfl_xor(sum, 16, 64);
+  const auto sp = __builtin_amdgcn_permlane16_swap(sum, sum, false, false);
+  const int sum32 = sp[0] + sp[1];
   // lanes 4j pack lanes 4j .. 4j+3 (all in one row)
   const uint32_t b = (uint32_t)qi & 0xffu;
   const uint32_t word = b | ((uint32_t)dpp_i<kDppShl1>((int)b) << 8) | ((uint32_t)dpp_i<kDppShl1 + 1>((int)b) << 16) |
