@@ -618,6 +618,10 @@ gmoe_status run_layer(gmoe_ctx* c, Layer& L, FwdBufs B, uint32_t n, hipStream_t 
   for (uint32_t e = 0; e < L.ne; e++) resident &= L.slot[e] >= 0;
   const bool spec = !pf && !pq && !B.logits_in && resident && spec_ok(D, n);
   B.spec = spec ? 1u : 0u;
+  if (B.nx && !spec) {  // hs made by its own launch, as the speculative front end would
+    HIP_TRY(launch_add_norm_slices(B.nx, B.ny, B.nsl_y, B.nw, n, L.d, B.neps, B.nh, st));
+    B.nx = nullptr;
+  }
   // top-k <= 2 at decode batches: the down product adds into the output (zeroed by the
   // front end), no combine launch
   // (the front end zeroes out while it reads hs: not when they overlap, as in place)
@@ -827,10 +831,11 @@ gmoe_status get_dense(gmoe_ctx* c, uint32_t id, Dense** out) {
 }
 
 // A dense call without its slice sum: *parts holds [*nsl][n][rows] K slices in the
-// context's scratch, which the caller's next launch on st adds in slice order (the sum
-// k_reduce_parts makes), before any other call on the context reuses the scratch.
+// context's scratch (or in y_out, kMaxKsg * n * rows floats), which the caller's next
+// launch on st adds in slice order (the sum k_reduce_parts makes), before any other call
+// on the context reuses the scratch.
 gmoe_status dense_slices(gmoe_ctx* c, uint32_t id, const float* d_xs, uint32_t n, hipStream_t st, const float** parts,
-                         uint32_t* nsl) {
+                         uint32_t* nsl, float* y_out) {
   if (gmoe_status s = check_ctx(c)) return s;
   if (!d_xs || !parts || !nsl) return fail(GMOE_ERR_INFERENCE, "null activation or output pointer");
   if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
@@ -841,6 +846,7 @@ gmoe_status dense_slices(gmoe_ctx* c, uint32_t id, const float* d_xs, uint32_t n
   if (gmoe_status s = ensure_scratch(c, plan_dense(c, *W, n, nullptr, nullptr))) return s;
   DenseCarve cv;
   plan_dense(c, *W, n, c->scratch, &cv);
+  if (y_out) cv.B.y = y_out;  // [kMaxKsg][n][rows] floats of the caller's
   if (gmoe_status s = run_dense(*W, cv, d_xs, n, nullptr, st)) return s;
   *parts = cv.B.y;
   *nsl = cv.ksg;
@@ -979,8 +985,46 @@ namespace gmoe {
 
 // The dense call without its slice sum, for the model step (dense_slices).
 gmoe_status dense_forward_slices(gmoe_ctx* c, uint32_t id, const float* d_xs, uint32_t n, hipStream_t st,
-                                 const float** parts, uint32_t* nsl) {
-  return dense_slices(c, id, d_xs, n, st, parts, nsl);
+                                 const float** parts, uint32_t* nsl, float* y_out) {
+  return dense_slices(c, id, d_xs, n, st, parts, nsl, y_out);
+}
+
+// The MoE feed-forward of a model step with its input made by its own front end: hs =
+// RMSNorm(x + the sum of y's nsl K slices) * w, written to h (and x updated), as
+// k_add_norm<true> makes it; calls that take another front end run that launch first.
+gmoe_status ffn_forward_normed(gmoe_ctx* c, uint32_t lid, float* d_x, const float* d_y, uint32_t nsl,
+                               uint64_t y_stride, const float* d_w, float eps, float* d_h, uint32_t n, float* d_out,
+                               hipStream_t st) {
+  if (gmoe_status s = check_ctx(c)) return s;
+  if (!d_x || !d_y || !d_w || !d_h || !d_out) return fail(GMOE_ERR_INFERENCE, "null activation pointer");
+  if (n == 0) return fail(GMOE_ERR_INFERENCE, "empty batch");
+  CtxLock g(c);
+  Layer* L;
+  if (gmoe_status s = get_layer(c, lid, &L)) return s;
+  for (uint32_t e = 0; e < L->ne; e++)
+    if (L->slot[e] < 0) return fail(GMOE_ERR_CACHE, "expert %u of layer %u is not resident", e, lid);
+  HIP_TRY(hipSetDevice(c->device));
+  const uint32_t per = call_tokens(*L);
+  if (gmoe_status s = ensure_scratch(c, call_scratch(*L, n))) return s;
+  for (uint32_t t0 = 0; t0 < n; t0 += per) {
+    const uint32_t m = std::min(per, n - t0);
+    Carved cv;
+    plan_scratch(*L, m, &cv, c->scratch);
+    FwdBufs B = cv.B;
+    B.hs = d_h + (size_t)t0 * L->d;
+    B.logits_in = nullptr;
+    B.out = d_out + (size_t)t0 * L->d;
+    B.nx = d_x + (size_t)t0 * L->d;
+    B.ny = d_y + (size_t)t0 * L->d;
+    B.nw = d_w;
+    B.nh = d_h + (size_t)t0 * L->d;
+    B.neps = eps;
+    B.nsl_y = nsl;
+    B.ny_stride = y_stride;
+    if (gmoe_status s = run_layer(c, *L, B, m, st)) return s;
+    c->scratch_stream = st;
+  }
+  return GMOE_OK;
 }
 
 // One dense weight made of registered ones laid end to end: its rows are theirs in order

@@ -380,6 +380,87 @@ __device__ __forceinline__ float wave64_max(float v) {
   return fmaxf(p.a, p.b);
 }
 
+// One row's residual add and RMSNorm by the block's first 256 threads; every thread of
+// the block calls it (it holds one barrier). With y, x += y first (written back); with SL,
+// y is the sum of nsl K slices of a dense product `stride` floats apart, added in slice
+// order (k_reduce_parts's sum), each float4's slice loads issued together. Then
+// h = (x * scale) * w with scale = 1 / sqrt(mean(x^2) + eps), written to h and, when hl is
+// given, to hl as well. A thread holds its kNormVec float4 of the row (d <= 4 * 256 *
+// kNormVec) in registers, every load issued before any use. part: 4 floats of LDS.
+template <bool SL>
+__device__ __forceinline__ void add_norm_row(float* __restrict__ x, const float* __restrict__ y,
+                                             const float* __restrict__ w, uint32_t d, float eps,
+                                             float* __restrict__ h, float* hl, uint32_t nsl, size_t stride,
+                                             float* part) {
+  const uint32_t t = threadIdx.x, nv = t < 256 ? d / 4 : 0u;  // threads past 256 only meet the barrier
+  float4* xr = reinterpret_cast<float4*>(x);
+  const float4* yr = reinterpret_cast<const float4*>(y);
+  const float4* wr = reinterpret_cast<const float4*>(w);
+  float4* hr = reinterpret_cast<float4*>(h);
+  float4 xv[kNormVec], yv[kNormVec];
+#pragma unroll
+  for (int r = 0; r < kNormVec; r++) {
+    const uint32_t c = t + 256 * r;
+    if (c < nv) xv[r] = xr[c];
+  }
+  if (yr) {
+#pragma unroll
+    for (int r = 0; r < kNormVec; r++) {
+      const uint32_t c = t + 256 * r;
+      if (c < nv) {
+        if constexpr (SL) {
+          float4 p[kMaxKsg];
+#pragma unroll
+          for (uint32_t g = 0; g < kMaxKsg; g++) p[g] = yr[c + (size_t)min(g, nsl - 1) * (stride / 4)];
+          float4 a = p[0];
+#pragma unroll
+          for (uint32_t g = 1; g < kMaxKsg; g++)
+            if (g < nsl) a = make_float4(a.x + p[g].x, a.y + p[g].y, a.z + p[g].z, a.w + p[g].w);
+          yv[r] = a;
+        } else {
+          yv[r] = yr[c];
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kNormVec; r++) {
+      const uint32_t c = t + 256 * r;
+      if (c < nv) {
+        xv[r] = make_float4(xv[r].x + yv[r].x, xv[r].y + yv[r].y, xv[r].z + yv[r].z, xv[r].w + yv[r].w);
+        xr[c] = xv[r];
+      }
+    }
+  }
+  float sq = 0.0f;
+#pragma unroll
+  for (int r = 0; r < kNormVec; r++) {
+    const uint32_t c = t + 256 * r;
+    if (c < nv) {
+      sq = sq + xv[r].x * xv[r].x;
+      sq = sq + xv[r].y * xv[r].y;
+      sq = sq + xv[r].z * xv[r].z;
+      sq = sq + xv[r].w * xv[r].w;
+    }
+  }
+  if (t < 256) {
+    sq = wave64_sum(sq);
+    if ((t & 63) == 0) part[t >> 6] = sq;
+  }
+  __syncthreads();
+  const float mean = (part[0] + part[1] + part[2] + part[3]) / (float)d;
+  const float scale = fdiv(1.0f, __fsqrt_rn(mean + eps));
+#pragma unroll
+  for (int r = 0; r < kNormVec; r++) {
+    const uint32_t c = t + 256 * r;
+    if (c < nv) {
+      const float4 v = xv[r], g = wr[c];
+      const float4 o = make_float4((v.x * scale) * g.x, (v.y * scale) * g.y, (v.z * scale) * g.z, (v.w * scale) * g.w);
+      hr[c] = o;
+      if (hl) reinterpret_cast<float4*>(hl)[c] = o;
+    }
+  }
+}
+
 __device__ __forceinline__ void quant_wave(float v, uint32_t lane, bool valid, int8_t* q, float* s, uint32_t* sums,
                                            uint32_t r0, int kind, int32_t off) {
   // the max over the lane's 32 (16 by DPP, then the other 16): after the two quad steps

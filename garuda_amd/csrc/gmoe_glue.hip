@@ -52,69 +52,9 @@ __global__ void __launch_bounds__(256) k_add_norm(float* __restrict__ x, const f
                                                   const float* __restrict__ w, uint32_t d, float eps,
                                                   float* __restrict__ h, uint32_t nsl, size_t stride) {
   __shared__ float part[4];
-  const uint32_t i = blockIdx.x, t = threadIdx.x, nv = d / 4;
-  float4* xr = reinterpret_cast<float4*>(x + (size_t)i * d);
-  const float4* yr = y ? reinterpret_cast<const float4*>(y + (size_t)i * d) : nullptr;
-  const float4* wr = reinterpret_cast<const float4*>(w);
-  float4* hr = reinterpret_cast<float4*>(h + (size_t)i * d);
-  float4 xv[kNormVec], yv[kNormVec];
-#pragma unroll
-  for (int r = 0; r < kNormVec; r++) {
-    const uint32_t c = t + 256 * r;
-    if (c < nv) xv[r] = xr[c];
-  }
-  if (yr) {
-#pragma unroll
-    for (int r = 0; r < kNormVec; r++) {
-      const uint32_t c = t + 256 * r;
-      if (c < nv) {
-        if constexpr (SL) {
-          float4 p[kMaxKsg];
-#pragma unroll
-          for (uint32_t g = 0; g < kMaxKsg; g++) p[g] = yr[c + (size_t)min(g, nsl - 1) * (stride / 4)];
-          float4 a = p[0];
-#pragma unroll
-          for (uint32_t g = 1; g < kMaxKsg; g++)
-            if (g < nsl) a = make_float4(a.x + p[g].x, a.y + p[g].y, a.z + p[g].z, a.w + p[g].w);
-          yv[r] = a;
-        } else {
-          yv[r] = yr[c];
-        }
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < kNormVec; r++) {
-      const uint32_t c = t + 256 * r;
-      if (c < nv) {
-        xv[r] = make_float4(xv[r].x + yv[r].x, xv[r].y + yv[r].y, xv[r].z + yv[r].z, xv[r].w + yv[r].w);
-        xr[c] = xv[r];
-      }
-    }
-  }
-  float sq = 0.0f;
-#pragma unroll
-  for (int r = 0; r < kNormVec; r++) {
-    const uint32_t c = t + 256 * r;
-    if (c < nv) {
-      sq = sq + xv[r].x * xv[r].x;
-      sq = sq + xv[r].y * xv[r].y;
-      sq = sq + xv[r].z * xv[r].z;
-      sq = sq + xv[r].w * xv[r].w;
-    }
-  }
-  sq = glue_wave_sum(sq);
-  if ((t & 63) == 0) part[t >> 6] = sq;
-  __syncthreads();
-  const float mean = (part[0] + part[1] + part[2] + part[3]) / (float)d;
-  const float scale = fdiv(1.0f, __fsqrt_rn(mean + eps));
-#pragma unroll
-  for (int r = 0; r < kNormVec; r++) {
-    const uint32_t c = t + 256 * r;
-    if (c < nv) {
-      const float4 v = xv[r], g = wr[c];
-      hr[c] = make_float4((v.x * scale) * g.x, (v.y * scale) * g.y, (v.z * scale) * g.z, (v.w * scale) * g.w);
-    }
-  }
+  const uint32_t i = blockIdx.x;
+  add_norm_row<SL>(x + (size_t)i * d, y ? y + (size_t)i * d : nullptr, w, d, eps, h + (size_t)i * d, nullptr, nsl,
+                   stride, part);
 }
 
 // grid n, 256 threads: next[i] = the first index of row i's largest value

@@ -176,6 +176,15 @@ struct FwdBufs {
   uint32_t spec;         // 1: slots hold candidate pairs; slot_of / slot_w hold the combine's
                          // (slot, weight) per (token, position in combine order), written by
                          // the exact routing (RouteArgs::comb_slot, comb_w)
+  // speculative front end with nx: it first makes hs itself, as k_add_norm<true> does:
+  // nx += the sum of ny's nsl_y K slices (ny_stride floats apart), hs = RMSNorm(nx) * nw
+  float* nx;             // [n][d] residual, updated
+  const float* ny;       // [nsl_y][..][d] slices, row t at ny + t * d
+  const float* nw;       // [d]
+  float* nh;             // [n][d] where hs is written (hs points there too)
+  float neps;
+  uint32_t nsl_y;
+  uint64_t ny_stride;
 };
 
 // Exact routing carried by the gate/up launch of a speculative decode call: one extra

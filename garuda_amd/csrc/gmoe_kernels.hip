@@ -960,13 +960,23 @@ __device__ __forceinline__ double sum_gamma(double m) {
   return m * u / (1.0 - m * u);
 }
 
+// NORM: the token's row of hs is made first, by the residual add and RMSNorm of
+// add_norm_row (FwdBufs::nx ...), written to nh and kept in LDS, from where the logits
+// and the quantiser read it.
+template <bool NORM>
 __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs B, uint32_t n, int quant) {
   __shared__ float lt[kFrontExperts], la[kFrontExperts];
   __shared__ uint32_t cl[kFrontExperts];
   __shared__ double sb[2 * kFrontExperts];  // candidate test: lo, then hi, of each expert
+  extern __shared__ float4 hrow[];          // NORM: the token's row of hs
   const uint32_t ne = L.ne, d = L.d, k = L.k, t = blockIdx.x;
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const float* hs = B.hs + (size_t)t * d;
+  if constexpr (NORM) {
+    add_norm_row<true>(B.nx + (size_t)t * d, B.ny + (size_t)t * d, B.nw, d, B.neps, B.nh + (size_t)t * d,
+                       reinterpret_cast<float*>(hrow), B.nsl_y, B.ny_stride, lt);
+    __syncthreads();
+  }
+  const float* hs = NORM ? reinterpret_cast<const float*>(hrow) : B.hs + (size_t)t * d;
   const float4* xr = reinterpret_cast<const float4*>(hs);
   // loads whose use comes late, issued first: wave 0's slab pointers for the dispatch
   // (lane e: expert e's gate, up, down) and, for the threads of waves 1 on, the
@@ -1143,7 +1153,12 @@ bool spec_ok(const LayerDev& L, uint32_t n) {
 }
 
 hipError_t launch_spec_front(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st) {
-  hipLaunchKernelGGL(k_spec_front, dim3(n), dim3(kSpecThreads), 0, st, L, B, n, quant);
+  if (B.nx) {
+    if (B.nsl_y == 0 || B.nsl_y > kMaxKsg || L.d > 4 * 256 * kNormVec) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_spec_front<true>, dim3(n), dim3(kSpecThreads), L.d * 4, st, L, B, n, quant);
+  } else {
+    hipLaunchKernelGGL(k_spec_front<false>, dim3(n), dim3(kSpecThreads), 0, st, L, B, n, quant);
+  }
   return hipGetLastError();
 }
 

@@ -36,7 +36,10 @@ gmoe_status kv_attend_dev(gmoe_kv* kv, uint32_t n, const AttnEntry* d_ent, uint3
                           const float* k, const float* v, uint32_t q_stride, uint32_t kv_stride, float* out,
                           hipStream_t st, uint32_t nsl = 1, uint64_t sl_stride = 0);
 gmoe_status dense_forward_slices(gmoe_ctx* c, uint32_t id, const float* d_xs, uint32_t n, hipStream_t st,
-                                 const float** parts, uint32_t* nsl);
+                                 const float** parts, uint32_t* nsl, float* y_out = nullptr);
+gmoe_status ffn_forward_normed(gmoe_ctx* c, uint32_t lid, float* d_x, const float* d_y, uint32_t nsl,
+                               uint64_t y_stride, const float* d_w, float eps, float* d_h, uint32_t n, float* d_out,
+                               hipStream_t st);
 const void* ctx_scratch_id(gmoe_ctx* c);
 void ctx_note_graph(gmoe_ctx* c, const uint32_t* layers, uint32_t n, hipStream_t st);
 gmoe_status kv_attend(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, const float* q, const float* k,
@@ -189,7 +192,7 @@ gmoe_status gmoe_model_create(gmoe_ctx* ctx, const gmoe_model_desc* desc, gmoe_m
                 {(void**)&m->x, B * d * 4},           {(void**)&m->h, B * d * 4},
                 {(void**)&m->q, B * qd * 4},          {(void**)&m->k, B * kvd * 4},
                 {(void**)&m->v, B * kvd * 4},         {(void**)&m->cx, B * qd * 4},
-                {(void**)&m->ao, B * d * 4},          {(void**)&m->y, B * d * 4},
+                {(void**)&m->ao, kMaxKsg * B * d * 4}, {(void**)&m->y, B * d * 4},
                 {(void**)&m->logits, B * D.vocab * 4}, {(void**)&m->next, B * 4},
                 {(void**)&m->qkv, B * (qd + 2 * (size_t)kvd) * 4},
                 {(void**)&m->par, par_bytes(D.n_layers)}};
@@ -331,19 +334,23 @@ static gmoe_status step_launches(gmoe_model* m, uint32_t n, const uint32_t* seqs
       else S_TRY(kv_attend_dev(m->kv, n, le, nchunk, m->q, m->k, m->v, 0, 0, m->cx, st));
     }
     M_TRY(rec(m->cx, m->qd, m->qd));
+    const float* ffn_norm = m->norms + (2 * (size_t)l + 1) * d;
     if (tk) {
       S_TRY(gmoe_dense_forward_async(m->ctx, m->wo[l], m->cx, n, m->ao, st));
       M_TRY(rec(m->ao, d, d));
-      M_TRY(launch_add_norm(m->x, m->ao, m->norms + (2 * (size_t)l + 1) * d, n, d, m->eps, m->h, st));
-    } else {  // the output projection's K slices added by the residual add (no k_reduce_parts launch)
+      M_TRY(launch_add_norm(m->x, m->ao, ffn_norm, n, d, m->eps, m->h, st));
+      M_TRY(rec(m->x, d, d));
+      M_TRY(rec(m->h, d, d));
+      S_TRY(gmoe_ffn_forward_async(m->ctx, m->moe[l], m->h, nullptr, n, m->y, nullptr, nullptr, st));
+    } else {
+      // the output projection leaves its K slices in m->ao and the MoE front end adds them
+      // to the residual and norms it (no k_reduce_parts and no k_add_norm launch)
       const float* ao;
       uint32_t nsl;
-      S_TRY(dense_forward_slices(m->ctx, m->wo[l], m->cx, n, st, &ao, &nsl));
-      M_TRY(launch_add_norm_slices(m->x, ao, nsl, m->norms + (2 * (size_t)l + 1) * d, n, d, m->eps, m->h, st));
+      S_TRY(dense_forward_slices(m->ctx, m->wo[l], m->cx, n, st, &ao, &nsl, m->ao));
+      S_TRY(ffn_forward_normed(m->ctx, m->moe[l], m->x, ao, nsl, (uint64_t)n * d, ffn_norm, m->eps, m->h, n, m->y,
+                               st));
     }
-    M_TRY(rec(m->x, d, d));
-    M_TRY(rec(m->h, d, d));
-    S_TRY(gmoe_ffn_forward_async(m->ctx, m->moe[l], m->h, nullptr, n, m->y, nullptr, nullptr, st));
     M_TRY(rec(m->y, d, d));
   }
   M_TRY(launch_add_norm(m->x, m->y, m->norms + 2 * (size_t)m->n_layers * d, n, d, m->eps, m->h, st));
