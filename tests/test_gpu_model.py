@@ -211,6 +211,34 @@ def test_graph_steps_equal_eager_steps(dev, weights):
         release(*b)
 
 
+def test_graph_steps_equal_eager_steps_wide_router(dev):
+    """The same comparison on a model of 72 experts, past the speculative front end's 64:
+    its graph steps run the FFN's add-norm as a launch of its own (the output projection's
+    K slices added there) and the wide front end, and must still match the eager steps
+    (reduced output projection, separate add-norm) bit for bit."""
+    w = tiny_model(13, n_layers=2, d=D, nh=NH, nkv=NKV, hd=HD, f=F, ne=72, k=K, vocab=VOCAB)
+    a, b = gpu_model(dev, w), gpu_model(dev, w)
+    ma, kva, mb, kvb = a[0], a[1], b[0], b[1]
+    try:
+        ma.set_graphs(False)
+        sa = [kva.open_seq() for _ in range(3)]
+        sb = [kvb.open_seq() for _ in range(3)]
+        toks = np.random.default_rng(7).integers(0, VOCAB, 3).astype(np.uint32)
+        replays = 0
+        for step in range(10):
+            say(f"wide-router graph step {step}")
+            replays += mb.graph_ready(3)
+            na, la = ma.decode_step(sa, toks, want_logits=True)
+            nb, lb = mb.decode_step(sb, toks, want_logits=True)
+            assert np.array_equal(na, nb), f"step {step}: next tokens differ"
+            assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)), f"step {step}: logits differ"
+            toks = na
+        assert replays >= 8, f"{replays} steps replayed from a graph"
+    finally:
+        release(*a)
+        release(*b)
+
+
 def test_refusals_leave_the_sequences_unchanged(dev, weights):
     parts = gpu_model(dev, weights, max_positions=3)
     model, kv, moe = parts[0], parts[1], parts[2]
