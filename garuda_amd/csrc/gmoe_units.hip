@@ -373,6 +373,37 @@ k_dn_atomic(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32
     __syncthreads();
     stage_acts<QT, PACKED>(acts, f, m, rows, f, 0, hq, hsc, hsum, hf);
     __syncthreads();
+    // wave 0, lane t < m: chunk member t's token and combine weight, loaded here so that
+    // their latency hides behind the stream (m <= kFuseMaxTokens <= 64, k <= 2). fl: 1 the
+    // slot is a routed pair's, 2 a routed pair of the token has no candidate slot (NaN).
+    uint32_t rtok = 0, rfl = 0;
+    float rwt = 0.0f;
+    if (wave == 0 && lane < m) {
+      const uint32_t slot = s0 + c0 + lane;
+      rtok = slot_tok[slot];
+      if (spec) {
+        uint32_t sl[2];
+        float wv[2];
+#pragma unroll
+        for (uint32_t i = 0; i < 2; i++)
+          if (i < k) {
+            sl[i] = slot_of[(size_t)rtok * k + i];
+            wv[i] = slot_w[(size_t)rtok * k + i];
+          }
+#pragma unroll
+        for (uint32_t i = 0; i < 2; i++)
+          if (i < k) {
+            if (sl[i] == slot) {
+              rfl |= 1u;
+              rwt = wv[i];
+            }
+            if (sl[i] == ~0u) rfl |= 2u;
+          }
+      } else {
+        rfl = 1u;
+        rwt = slot_w[slot];
+      }
+    }
     st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED>(w, acts, per, f, u, 0, nblk, my, m); });
     __syncthreads();
     if (wave == 0) {
@@ -381,24 +412,11 @@ k_dn_atomic(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32
         float y = accs[t * 64 + lane];
 #pragma unroll
         for (int w2 = 1; w2 < KS; w2++) y += accs[(w2 * mt + t) * 64 + lane];
-        const uint32_t slot = s0 + c0 + t, tok = slot_tok[slot];
-        float wt = 0.0f, miss = 0.0f;
-        bool routed = !spec;
-        if (spec) {
-          for (uint32_t i = 0; i < k; i++) {
-            const uint32_t sl = slot_of[(size_t)tok * k + i];
-            if (sl == slot) {
-              routed = true;
-              wt = slot_w[(size_t)tok * k + i];
-            }
-            if (sl == ~0u) miss = __int_as_float(0x7fc00000);
-          }
-        } else {
-          wt = slot_w[slot];
-        }
+        const uint32_t tok = lane_u(rtok, t), fl = lane_u(rfl, t);
+        const float wt = __uint_as_float(lane_u(__float_as_uint(rwt), t));
         if (row < d) {
-          if (routed) atomicAdd(out + (size_t)tok * d + row, y * wt);
-          if (miss != 0.0f || miss != miss) atomicAdd(out + (size_t)tok * d + row, miss);
+          if (fl & 1u) atomicAdd(out + (size_t)tok * d + row, y * wt);
+          if (fl & 2u) atomicAdd(out + (size_t)tok * d + row, __int_as_float(0x7fc00000));
         }
       }
     }
@@ -472,8 +490,11 @@ static hipError_t go_dn(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_
 
 constexpr int kDnAtomicKS = 8;
 
+static_assert(kFuseMaxTokens <= 64, "k_dn_atomic keeps a chunk's tokens one a lane");
+
 template <int QT, bool PACKED>
 static hipError_t go_dn_atomic(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  if (L.k > 2 || n > kFuseMaxTokens) return hipErrorInvalidValue;
   const uint32_t per = kDnAtomicKS * 64 * 4 + ActLds<QT, PACKED>::per_token(L.f) + 4;
   const uint32_t mt = min(n, (kLdsBudget - 16) / per);
   if (mt == 0) return hipErrorInvalidValue;
