@@ -978,27 +978,15 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
   }
   const float* hs = NORM ? reinterpret_cast<const float*>(hrow) : B.hs + (size_t)t * d;
   const float4* xr = reinterpret_cast<const float4*>(hs);
-  // loads whose use comes late, issued first: wave 0's slab pointers for the dispatch
-  // (lane e: expert e's gate, up, down) and, for the threads of waves 1 on, the
-  // activations of their 32-value block for the int8 quantiser. Only the expert kernels
-  // read the quantised activations, so those waves quantise after the barrier while
-  // wave 0 runs the candidate test and the dispatch.
+  // wave 0's slab pointers for the dispatch (lane e: expert e's gate, up, down), loaded
+  // first; the output rows' zeroing and the quantiser's loads (threads of waves 1 on, the
+  // activations of their 32-value block) follow the router dots' loads, whose results
+  // the barrier waits for. Only the expert kernels read the quantised activations, so
+  // those waves quantise after the barrier while wave 0 runs the candidate test and the
+  // dispatch.
   const uint8_t* ep[3] = {nullptr, nullptr, nullptr};
   if (wave == 0 && lane < ne)
     for (int p = 0; p < 3; p++) ep[p] = L.eptr[p * ne + lane];
-  if (B.fuse_out)  // the down product adds into the token's output row
-    for (uint32_t c = tid; c < d; c += kSpecThreads) B.out[(size_t)t * d + c] = 0.0f;
-  const uint32_t nblk = d / 32, qb = tid - 64;  // block of thread tid >= 64
-  float qv[32];
-  const bool qown = quant && tid >= 64 && qb < nblk && nblk <= kSpecThreads - 64;
-  if (qown) {
-    const float4* src = reinterpret_cast<const float4*>(hs + (size_t)qb * 32);
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float4 t4 = src[i];
-      qv[4 * i] = t4.x; qv[4 * i + 1] = t4.y; qv[4 * i + 2] = t4.z; qv[4 * i + 3] = t4.w;
-    }
-  }
   // wave w: experts w, w + 8, ...; lane j: float4 columns j, j + 64, ..., 16 loads in flight
   constexpr int kB = 16;
   const uint32_t n4 = d / 4;
@@ -1030,6 +1018,19 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
     if (lane == 0) {
       lt[e] = sm;
       la[e] = ab;
+    }
+  }
+  if (B.fuse_out)  // the down product adds into the token's output row
+    for (uint32_t c = tid; c < d; c += kSpecThreads) B.out[(size_t)t * d + c] = 0.0f;
+  const uint32_t nblk = d / 32, qb = tid - 64;  // block of thread tid >= 64
+  float qv[32];
+  const bool qown = quant && tid >= 64 && qb < nblk && nblk <= kSpecThreads - 64;
+  if (qown) {
+    const float4* src = reinterpret_cast<const float4*>(hs + (size_t)qb * 32);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float4 t4 = src[i];
+      qv[4 * i] = t4.x; qv[4 * i + 1] = t4.y; qv[4 * i + 2] = t4.z; qv[4 * i + 3] = t4.w;
     }
   }
   if (quant && nblk > kSpecThreads - 64) {  // (wide rows: every thread, before the barrier)
