@@ -463,7 +463,9 @@ def e2e_leg(a, threads, cpu):
     dense = {nm: [G.DenseWeight(dev, G.Q4_K, r, cc, att[nm]) for _ in range(copies)]
              for nm, r, cc in (("wq", nh * hd, d), ("wk", nkv * hd, d), ("wv", nkv * hd, d), ("wo", d, nh * hd))}
     head = G.DenseWeight(dev, G.Q6_K, vocab, d, head_raw)
-    kv = KvCache(dev, nl, nh, nkv, hd, block_size=16, max_positions=prompt + steps + 8, max_seqs=nseq,
+    # the window is C5's context (2048): graph-replayed steps attend over the live
+    # context's chunk bucket, whatever the window
+    kv = KvCache(dev, nl, nh, nkv, hd, block_size=16, max_positions=max(2048, prompt + steps + 8), max_seqs=nseq,
                  rope_theta=1e6)
     pick = [l % copies for l in range(nl)]
     model = G.DecodeModel(dev, kv, [moe[c] for c in pick], *[[dense[nm][c] for c in pick] for nm in ("wq", "wk", "wv", "wo")],
@@ -557,7 +559,7 @@ def c1_leg(a, dev, threads, cpu):
             nxt = step(seq, int(nxt))
         return toks, t1 - t0, time.perf_counter() - t1
 
-    with tempfile.TemporaryDirectory() as td, SyntheticEngine(dev, td, max_positions=256, **dims) as eng:
+    with tempfile.TemporaryDirectory() as td, SyntheticEngine(dev, td, max_positions=2048, **dims) as eng:
         gstep = lambda seq, t: eng.step([seq], [t])[0]
         run(gstep, eng.open_seq)  # warm-up pass (its own sequence)
         gtoks, gp, gd = run(gstep, eng.open_seq)

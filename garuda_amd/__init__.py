@@ -11,5 +11,5 @@ from .moe import (  # noqa: F401
     DenseWeight, InvalidTokenError, MoeLayer, NotFoundError, block_layout, byte_size, fill_gaussian, quantize,
 )
 from .model import DecodeModel  # noqa: F401
-from .tiers import ExpertTier, engine_weights, fill_seeded  # noqa: F401
+from .tiers import TIER_L2, TIER_L3, TIER_SYNTHESISED, ExpertTier, engine_weights, fill_seeded  # noqa: F401
 from .gguf import Gguf, TensorInfo, Value, write_gguf  # noqa: F401

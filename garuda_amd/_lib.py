@@ -52,7 +52,7 @@ class GmoeGgufTensorInfo(C.Structure):
 
 
 class GmoeL2Counts(C.Structure):
-    _fields_ = [("l2", u64), ("synthesised", u64), ("written", u64)]
+    _fields_ = [("l2", u64), ("synthesised", u64), ("written", u64), ("l3", u64), ("promoted", u64)]
 
 
 class GmoePredictStats(C.Structure):
@@ -67,6 +67,7 @@ SIGNATURES = {
     "gmoe_init": (i32, [i32, u64, C.POINTER(vp)]),
     "gmoe_shutdown": (None, [vp]),
     "gmoe_layer_register": (i32, [vp, C.POINTER(GmoeLayerDesc), u32p]),
+    "gmoe_layer_register_fetch": (i32, [vp, C.POINTER(GmoeLayerDesc), vp, vp, u32p]),
     "gmoe_layer_release": (i32, [vp, u32]),
     "gmoe_ffn_forward": (i32, [vp, u32, f32p, u32, f32p, u32p, f32p]),
     "gmoe_ffn_forward_logits": (i32, [vp, u32, f32p, f32p, u32, f32p, u32p, f32p]),
@@ -91,6 +92,10 @@ SIGNATURES = {
     "gmoe_l2_close": (None, [vp]),
     "gmoe_l2_get_counts": (i32, [vp, C.POINTER(GmoeL2Counts)]),
     "gmoe_l2_layer_desc": (i32, [vp, f32p, u32, u32, u32, C.POINTER(GmoeLayerDesc)]),
+    "gmoe_tiers_open": (i32, [C.c_char_p, C.c_char_p, u32, u32, u32, u32, C.POINTER(vp)]),
+    "gmoe_l2_fetch": (i32, [vp, u32, C.POINTER(vp)]),
+    "gmoe_l2_locate": (i32, [vp, u32]),
+    "gmoe_l2_layer_register": (i32, [vp, vp, f32p, u32, u32, u32, u32p]),
     "gmoe_dense_register": (i32, [vp, C.POINTER(GmoeDenseDesc), u32p]),
     "gmoe_dense_release": (i32, [vp, u32]),
     "gmoe_dense_forward": (i32, [vp, u32, f32p, u32, f32p]),
@@ -109,6 +114,8 @@ SIGNATURES = {
     "gmoe_kv_seq_open": (i32, [vp, u32p]),
     "gmoe_kv_seq_close": (i32, [vp, u32]),
     "gmoe_kv_seq_len": (i32, [vp, u32, u32, u32p]),
+    "gmoe_kv_free_pages": (i32, [vp, C.POINTER(u64)]),
+    "gmoe_kv_fail_reserves": (i32, [vp, u32]),
     "gmoe_attention": (i32, [vp, u32, u32p, u32, f32p, f32p, f32p, f32p]),
     "gmoe_attention_async": (i32, [vp, u32, u32p, u32, vp, vp, vp, vp, vp]),
     "gmoe_gguf_open": (i32, [C.c_char_p, C.POINTER(vp)]),

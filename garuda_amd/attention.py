@@ -53,6 +53,16 @@ class KvCache:
         _check(lib().gmoe_kv_seq_len(self._h, seq, layer, C.byref(n)))
         return n.value
 
+    def free_pages(self) -> int:
+        n = C.c_uint64()
+        _check(lib().gmoe_kv_free_pages(self._h, C.byref(n)))
+        return n.value
+
+    def fail_reserves(self, count: int) -> None:
+        """Test hook: the next `count` attention-scratch reservations of graph-replayed
+        model steps fail as a device allocation would."""
+        _check(lib().gmoe_kv_fail_reserves(self._h, count))
+
     def attention(self, layer: int, seqs, q: np.ndarray, k: np.ndarray, v: np.ndarray) -> np.ndarray:
         seqs = np.ascontiguousarray(np.asarray(seqs, dtype=np.uint32).reshape(-1))
         n = seqs.size

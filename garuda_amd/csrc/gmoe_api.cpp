@@ -154,6 +154,13 @@ struct Layer {
   // free once that stream has drained. An event recorded per call would say exactly when,
   // but each record puts a marker on the GPU timeline (about 4 us a call).
   hipStream_t last_stream = nullptr;
+  // experts pulled from a lower tier when staged (gmoe_layer_register_fetch) instead of
+  // from host pointers given at registration
+  gmoe_expert_fetch fetch = nullptr;
+  void* fetch_user = nullptr;
+  // model steps in flight that read every expert of the layer (ctx_pin_layers): while
+  // non-zero no expert of the layer is chosen for eviction, nor evicted on request
+  uint32_t pins = 0;
   bool alive = true;
 };
 
@@ -254,6 +261,31 @@ void ctx_note_graph(gmoe_ctx* c, const uint32_t* layers, uint32_t n, hipStream_t
     if (layers[i] < c->layers.size() && c->layers[layers[i]] && c->layers[layers[i]]->alive)
       c->layers[layers[i]]->last_stream = st;
 }
+// A model step reads every expert of its layers from the device pointer tables (a graph
+// replay, or the speculative front end): check that all are resident and keep them so,
+// in one hold of the slab lock, until ctx_unpin_layers. Neither the staging thread nor
+// another call can evict them meanwhile (reserve() passes them over, evict refuses).
+gmoe_status ctx_pin_layers(gmoe_ctx* c, const uint32_t* layers, uint32_t n) {
+  CtxLock g(c);
+  for (uint32_t i = 0; i < n; i++) {
+    const uint32_t l = layers[i];
+    if (l >= c->layers.size() || !c->layers[l] || !c->layers[l]->alive)
+      return fail(GMOE_ERR_INFERENCE, "MoE layer %u was released", l);
+    const Layer& L = *c->layers[l];
+    for (uint32_t e = 0; e < L.ne; e++)
+      if (L.slot[e] < 0 || L.pending[e] == kStaging)
+        return fail(GMOE_ERR_CACHE, "expert %u of layer %u is not resident", e, l);
+  }
+  for (uint32_t i = 0; i < n; i++) c->layers[layers[i]]->pins++;
+  return GMOE_OK;
+}
+void ctx_unpin_layers(gmoe_ctx* c, const uint32_t* layers, uint32_t n) {
+  CtxLock g(c);
+  for (uint32_t i = 0; i < n; i++)
+    if (layers[i] < c->layers.size() && c->layers[layers[i]] && c->layers[layers[i]]->pins)
+      c->layers[layers[i]]->pins--;
+  c->cv.notify_all();
+}
 }  // namespace gmoe
 
 namespace {
@@ -308,9 +340,17 @@ gmoe_status stage_proj(gmoe_ctx* c, const Proj& P, const uint8_t* src, uint8_t* 
 // Runs under stage_mu; reads only what registration fixed.
 gmoe_status stage_expert(gmoe_ctx* c, const Layer& L, uint32_t e, uint64_t off, uint8_t* ptrs[3]) {
   uint8_t* base = c->slab.base + off;
+  const void* src[3] = {nullptr, nullptr, nullptr};
+  if (L.fetch) {  // MemoryManager::load_uncached (memory/mod.rs:114-146) behind the callback
+    if (gmoe_status s = L.fetch(L.fetch_user, e, src)) return s;
+    for (int p = 0; p < 3; p++)
+      if (!src[p]) return fail(GMOE_ERR_MODEL, "expert %u: the tier returned no weights for tensor %d", e, p);
+  } else {
+    for (int p = 0; p < 3; p++) src[p] = L.p[p].host[e];
+  }
   uint64_t o = 0;
   for (int p = 0; p < 3; p++) {
-    if (gmoe_status s = stage_proj(c, L.p[p], L.p[p].host[e], base + o)) return s;
+    if (gmoe_status s = stage_proj(c, L.p[p], static_cast<const uint8_t*>(src[p]), base + o)) return s;
     ptrs[p] = base + o;
     o += (L.p[p].bytes_dev + 255) & ~uint64_t(255);
   }
@@ -358,7 +398,7 @@ gmoe_status reserve(gmoe_ctx* c, uint32_t l, bool evict_ok, const Keep* keep, ui
     if (!evict_ok) return fail(GMOE_ERR_CACHE, "HBM slab is full");
     auto victim = c->lru.end();
     for (auto it = c->lru.begin(); it != c->lru.end(); ++it) {
-      bool kept = false;
+      bool kept = c->layers[it->first]->pins > 0;  // read by a model step in flight
       if (keep)
         for (auto& kp : *keep) kept |= (kp == *it);
       if (!kept) {
@@ -1181,7 +1221,15 @@ void gmoe_shutdown(gmoe_ctx* c) {
   delete c;
 }
 
-gmoe_status gmoe_layer_register(gmoe_ctx* c, const gmoe_layer_desc* desc, uint32_t* layer_id) {
+}  // extern "C"
+
+namespace {
+
+// gmoe_layer_register and gmoe_layer_register_fetch: with `fetch` set the tensors' host
+// pointers are not read (each expert comes from fetch when it is staged) and nothing is
+// staged here, so every expert is loaded when first routed, as MoeEngine loads it.
+gmoe_status register_layer(gmoe_ctx* c, const gmoe_layer_desc* desc, gmoe_expert_fetch fetch, void* user,
+                           uint32_t* layer_id) {
   if (gmoe_status s = check_ctx(c)) return s;
   if (!desc || !layer_id) return fail(GMOE_ERR_INFERENCE, "null descriptor");
   const gmoe_layer_desc& D = *desc;
@@ -1211,6 +1259,7 @@ gmoe_status gmoe_layer_register(gmoe_ctx* c, const gmoe_layer_desc* desc, uint32
     Unit un;
     if (!unit_of(P.qtype, &un)) return fail(GMOE_ERR_MODEL, "unsupported tensor type %u", P.qtype);
     P.bytes_dev = tiled_bytes(un, P.rows, P.cols);
+    if (fetch) continue;
     P.host.resize(L->ne);
     if (T[p]->layout == GMOE_LAYOUT_STACKED) {
       if (!T[p]->data) return fail(GMOE_ERR_MODEL, "stacked tensor %d has no data", p);
@@ -1243,10 +1292,12 @@ gmoe_status gmoe_layer_register(gmoe_ctx* c, const gmoe_layer_desc* desc, uint32
   L->slot.assign(L->ne, -1);
   L->lru_pos.resize(L->ne);
   L->pending.assign(L->ne, kAbsent);
+  L->fetch = fetch;
+  L->fetch_user = user;
   uint32_t id = (uint32_t)c->layers.size();
   c->layers.push_back(std::move(L));
   Layer& LL = *c->layers.back();
-  for (uint32_t e = 0; e < LL.ne; e++) {
+  for (uint32_t e = 0; e < LL.ne && !fetch; e++) {
     gmoe_status s = make_resident(c, g.slab, id, e, false, nullptr);
     if (s == GMOE_ERR_CACHE) break;  // the rest stays on the host tier
     if (s) return s;
@@ -1255,11 +1306,26 @@ gmoe_status gmoe_layer_register(gmoe_ctx* c, const gmoe_layer_desc* desc, uint32
   return GMOE_OK;
 }
 
+}  // namespace
+
+extern "C" {
+
+gmoe_status gmoe_layer_register(gmoe_ctx* c, const gmoe_layer_desc* desc, uint32_t* layer_id) {
+  return register_layer(c, desc, nullptr, nullptr, layer_id);
+}
+
+gmoe_status gmoe_layer_register_fetch(gmoe_ctx* c, const gmoe_layer_desc* desc, gmoe_expert_fetch fetch, void* user,
+                                      uint32_t* layer_id) {
+  if (!fetch) return fail(GMOE_ERR_INFERENCE, "null fetch callback");
+  return register_layer(c, desc, fetch, user, layer_id);
+}
+
 gmoe_status gmoe_layer_release(gmoe_ctx* c, uint32_t id) {
   if (gmoe_status s = check_ctx(c)) return s;
   CtxLock g(c);
   Layer* L;
   if (gmoe_status s = get_layer(c, id, &L)) return s;
+  if (L->pins) return fail(GMOE_ERR_CACHE, "layer %u is in use by a model step", id);
   HIP_TRY(hipSetDevice(c->device));
   // its queued experts leave the staging queue; the one being staged is waited for
   c->queue.erase(std::remove_if(c->queue.begin(), c->queue.end(), [&](const auto& q) { return q.first == id; }),
@@ -1382,6 +1448,7 @@ gmoe_status gmoe_expert_evict(gmoe_ctx* c, uint32_t lid, uint32_t e) {
   Layer* L;
   if (gmoe_status s = get_layer(c, lid, &L)) return s;
   if (e >= L->ne) return fail(GMOE_ERR_INFERENCE, "expert %u out of range", e);
+  if (L->pins) return fail(GMOE_ERR_CACHE, "layer %u is in use by a model step", lid);
   HIP_TRY(hipSetDevice(c->device));
   c->cv.wait(g.slab, [&] { return L->pending[e] != kStaging; });
   if (L->pending[e] == kQueued) {

@@ -71,6 +71,7 @@ struct gmoe_kv {
   uint32_t pin_cap = 0;       // entries per slot
   hipEvent_t pin_ev[kPinSlots]{};
   int pin_slot = 0;
+  uint32_t fail_reserves = 0;  // test hook: reservations still to refuse (gmoe_kv_fail_reserves)
   std::mutex mu;
 
   ~gmoe_kv() {
@@ -269,20 +270,86 @@ gmoe_status kv_check_step(gmoe_kv* kv, const uint32_t* seqs, uint32_t n) {
   return GMOE_OK;
 }
 
-// For decode steps replayed from a HIP graph (gmoe_model.cpp): the host plans and commits
-// each layer's entries (kv_plan_commit) and copies them to device memory the graph's
-// attention launches read (kv_attend_dev). Those launches span kv_graph_chunks chunks,
-// every position a sequence can reach; chunks past an entry's span are empty and merge as
-// nothing, so the result is the same as over the entry's own chunks.
+// For decode steps replayed from a HIP graph (gmoe_model.cpp): the host plans every
+// layer's entries (kv_plan_step), reserves the attention scratch, then commits them
+// (kv_commit_step) and copies them to device memory the graph's attention launches read
+// (kv_attend_dev). Those launches span a fixed number of chunks, the step's longest span
+// rounded up to a power of two (kv_step_chunks), so one graph serves every step until a
+// sequence outgrows the bucket; chunks past an entry's span are empty and merge as
+// nothing, so the result is the same as over the entry's own chunks. kv_graph_chunks is
+// the most a sequence can reach.
 uint32_t kv_graph_chunks(gmoe_kv* kv) {
   const gmoe_kv_desc& D = kv->d;
   const uint32_t span = D.sliding_window ? std::min(D.sliding_window, D.max_positions) : D.max_positions;
   return (span + kAttnChunk - 1) / kAttnChunk;
 }
 
+uint32_t kv_step_chunks(gmoe_kv* kv, uint32_t maxspan) {
+  const uint32_t need = (maxspan + kAttnChunk - 1) / kAttnChunk;
+  uint32_t b = 1;
+  while (b < need) b *= 2;
+  return std::min(b, kv_graph_chunks(kv));
+}
+
+// Every layer's entries of a step (ents[l * stride + i]), planned but not committed, and
+// the longest span any of them attends.
+gmoe_status kv_plan_step(gmoe_kv* kv, const uint32_t* seqs, uint32_t n, AttnEntry* ents, size_t stride,
+                         uint32_t* maxspan) {
+  std::lock_guard<std::mutex> g(kv->mu);
+  *maxspan = 1;
+  for (uint32_t l = 0; l < kv->d.n_layers; l++) {
+    uint32_t ms;
+    if (gmoe_status s = plan(kv, l, seqs, n, ents + (size_t)l * stride, &ms)) return s;
+    *maxspan = std::max(*maxspan, ms);
+  }
+  return GMOE_OK;
+}
+
+void kv_commit_step(gmoe_kv* kv, const uint32_t* seqs, uint32_t n, AttnEntry* ents, size_t stride) {
+  std::lock_guard<std::mutex> g(kv->mu);
+  for (uint32_t l = 0; l < kv->d.n_layers; l++) commit(kv, l, seqs, n, ents + (size_t)l * stride);
+}
+
+// The step's sequences as they stand (every layer's length and page count), and their
+// return to it: pages taken since go back to the free list, lengths go back. A step that
+// fails after committing positions restores them, so a refused step leaves every sequence
+// where it was.
+void kv_snapshot(gmoe_kv* kv, const uint32_t* seqs, uint32_t n, std::vector<uint32_t>& snap) {
+  std::lock_guard<std::mutex> g(kv->mu);
+  snap.clear();
+  for (uint32_t i = 0; i < n; i++) {
+    const Seq& S = kv->seqs[seqs[i]];
+    for (uint32_t l = 0; l < kv->d.n_layers; l++) {
+      snap.push_back(S.len[l]);
+      snap.push_back((uint32_t)S.pages[l].size());
+    }
+  }
+}
+
+void kv_restore(gmoe_kv* kv, const uint32_t* seqs, uint32_t n, const std::vector<uint32_t>& snap) {
+  std::lock_guard<std::mutex> g(kv->mu);
+  size_t at = 0;
+  for (uint32_t i = 0; i < n && at + 2 * kv->d.n_layers <= snap.size(); i++) {
+    Seq& S = kv->seqs[seqs[i]];
+    for (uint32_t l = 0; l < kv->d.n_layers; l++, at += 2) {
+      S.len[l] = snap[at];
+      while (S.pages[l].size() > snap[at + 1]) {
+        kv->free_pages.push_back(S.pages[l].back());
+        S.pages[l].pop_back();
+      }
+    }
+  }
+}
+
+
 gmoe_status kv_reserve(gmoe_kv* kv, uint32_t n, uint32_t nchunk) {
   std::lock_guard<std::mutex> g(kv->mu);
   KV_TRY(hipSetDevice(ctx_device(kv->ctx)));
+  if (kv->fail_reserves) {
+    kv->fail_reserves--;
+    return kfail(GMOE_ERR_DEVICE, "attention scratch of %zu bytes: allocation refused (test hook)",
+                 layout(kv, n, nchunk).total);
+  }
   return grow_scratch(kv, layout(kv, n, nchunk).total);
 }
 
@@ -385,6 +452,20 @@ gmoe_status gmoe_kv_seq_len(const gmoe_kv* kv, uint32_t seq, uint32_t layer, uin
   if (seq >= kv->seqs.size() || !kv->seqs[seq].open) return kfail(GMOE_ERR_INFERENCE, "sequence %u is not open", seq);
   if (layer >= kv->d.n_layers) return kfail(GMOE_ERR_INFERENCE, "layer %u of %u", layer, kv->d.n_layers);
   *len = kv->seqs[seq].len[layer];
+  return GMOE_OK;
+}
+
+gmoe_status gmoe_kv_free_pages(gmoe_kv* kv, uint64_t* pages) {
+  if (!kv || !pages) return kfail(GMOE_ERR_INFERENCE, "null cache or output");
+  std::lock_guard<std::mutex> g(kv->mu);
+  *pages = kv->free_pages.size();
+  return GMOE_OK;
+}
+
+gmoe_status gmoe_kv_fail_reserves(gmoe_kv* kv, uint32_t count) {
+  if (!kv) return kfail(GMOE_ERR_INFERENCE, "null cache");
+  std::lock_guard<std::mutex> g(kv->mu);
+  kv->fail_reserves = count;
   return GMOE_OK;
 }
 

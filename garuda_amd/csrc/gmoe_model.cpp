@@ -12,6 +12,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -28,10 +29,16 @@ bool dense_shape(gmoe_ctx* c, uint32_t id, uint32_t* rows, uint32_t* cols);
 bool layer_width(gmoe_ctx* c, uint32_t id, uint32_t* d, uint32_t* ne);
 void kv_dims(gmoe_kv* kv, uint32_t* n_layers, uint32_t* q_dim, uint32_t* kv_dim);
 gmoe_status kv_check_step(gmoe_kv* kv, const uint32_t* seqs, uint32_t n);
-uint32_t kv_graph_chunks(gmoe_kv* kv);
+uint32_t kv_step_chunks(gmoe_kv* kv, uint32_t maxspan);
 gmoe_status kv_reserve(gmoe_kv* kv, uint32_t n, uint32_t nchunk);
 const void* kv_scratch_id(gmoe_kv* kv);
-gmoe_status kv_plan_commit(gmoe_kv* kv, uint32_t layer, const uint32_t* seqs, uint32_t n, AttnEntry* ent);
+gmoe_status kv_plan_step(gmoe_kv* kv, const uint32_t* seqs, uint32_t n, AttnEntry* ents, size_t stride,
+                         uint32_t* maxspan);
+void kv_commit_step(gmoe_kv* kv, const uint32_t* seqs, uint32_t n, AttnEntry* ents, size_t stride);
+void kv_snapshot(gmoe_kv* kv, const uint32_t* seqs, uint32_t n, std::vector<uint32_t>& snap);
+void kv_restore(gmoe_kv* kv, const uint32_t* seqs, uint32_t n, const std::vector<uint32_t>& snap);
+gmoe_status ctx_pin_layers(gmoe_ctx* c, const uint32_t* layers, uint32_t n);
+void ctx_unpin_layers(gmoe_ctx* c, const uint32_t* layers, uint32_t n);
 gmoe_status kv_attend_dev(gmoe_kv* kv, uint32_t n, const AttnEntry* d_ent, uint32_t nchunk, const float* q,
                           const float* k, const float* v, uint32_t q_stride, uint32_t kv_stride, float* out,
                           hipStream_t st, uint32_t nsl = 1, uint64_t sl_stride = 0);
@@ -68,22 +75,38 @@ struct gmoe_model {
         *y = nullptr, *logits = nullptr;
   uint32_t* next = nullptr;
   uint32_t* pin_next = nullptr;
-  // Decode steps replayed from a HIP graph: the step's launches are captured once per
-  // batch size and read the step's parameters from device memory (par: the tokens, then
-  // every layer's attention entries; pin_par its pinned host copy). The graph is kept
-  // while the scratch allocations its launches point into stay where they were.
+  // Decode steps replayed from HIP graphs: a step's launches are captured once per (batch
+  // size, attention chunks) and read the step's parameters from device memory (par: the
+  // tokens, then every layer's attention entries; pin_par its pinned host copy). The
+  // chunks are the step's longest span rounded up to a power of two, so a graph serves
+  // until a sequence outgrows its bucket. Up to kGraphCache graphs are kept (least
+  // recently replayed out), each while the scratch allocations its launches point into
+  // stay where they were, so continuous batching whose batch size drifts replays instead
+  // of capturing again.
+  struct Graph {
+    hipGraphExec_t exec = nullptr;
+    uint32_t n = 0, nchunk = 0;
+    const void* g_ctx = nullptr;
+    const void* g_kv = nullptr;
+    uint64_t used = 0;
+  };
+  static constexpr size_t kGraphCache = 8;
   bool graphs = true, graph_failed = false;
   hipStream_t cap = nullptr;  // captures run on a stream of the model's own, which no other caller queues on
-  hipGraphExec_t gexec = nullptr;
-  uint32_t gn = 0;
-  const void* g_ctx = nullptr;
-  const void* g_kv = nullptr;
+  std::vector<Graph> gcache;
+  uint64_t gclock = 0;
   uint8_t* par = nullptr;
   uint8_t* pin_par = nullptr;
   std::mutex mu;
 
+  void drop_graphs() {
+    for (auto& g : gcache)
+      if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    gcache.clear();
+  }
+
   ~gmoe_model() {
-    if (gexec) hipGraphExecDestroy(gexec);
+    drop_graphs();
     if (cap) hipStreamDestroy(cap);
     if (pin_par) hipHostFree(pin_par);
     for (uint32_t id : wqkv) gmoe_dense_release(ctx, id);
@@ -253,11 +276,10 @@ gmoe_status gmoe_model_set_graphs(gmoe_model* m, int enable) {
   if (!m) return mfail(GMOE_ERR_INFERENCE, "null model");
   std::lock_guard<std::mutex> g(m->mu);
   m->graphs = enable != 0;
-  if (!m->graphs && m->gexec) {
-    hipSetDevice(ctx_device(m->ctx));
-    hipStreamSynchronize(ctx_stream(m->ctx));
-    hipGraphExecDestroy(m->gexec);
-    m->gexec = nullptr;
+  if (!m->graphs && !m->gcache.empty()) {
+    (void)hipSetDevice(ctx_device(m->ctx));
+    (void)hipStreamSynchronize(ctx_stream(m->ctx));
+    m->drop_graphs();
   }
   m->graph_failed = false;
   return GMOE_OK;
@@ -266,7 +288,9 @@ gmoe_status gmoe_model_set_graphs(gmoe_model* m, int enable) {
 int gmoe_model_graph_ready(gmoe_model* m, uint32_t n) {
   if (!m) return 0;
   std::lock_guard<std::mutex> g(m->mu);
-  return m->gexec && m->gn == n ? 1 : 0;
+  for (const auto& e : m->gcache)
+    if (e.n == n && e.exec) return 1;
+  return 0;
 }
 
 gmoe_status gmoe_model_decode_trace(gmoe_model* m, uint32_t n, const uint32_t* seqs, const uint32_t* tokens,
@@ -284,11 +308,10 @@ gmoe_status gmoe_model_decode_trace(gmoe_model* m, uint32_t n, const uint32_t* s
 // same launches serve every step: the form a graph captures. trace (eager only): every
 // layer's activations copied to the host.
 static gmoe_status step_launches(gmoe_model* m, uint32_t n, const uint32_t* seqs, const GlueTokens* tk, float* trace,
-                                 hipStream_t st) {
+                                 hipStream_t st, uint32_t nchunk) {
   const uint32_t d = m->d;
   const uint32_t* dtok = reinterpret_cast<const uint32_t*>(m->par);
   const AttnEntry* dent = reinterpret_cast<const AttnEntry*>(m->par + kParEnt);
-  const uint32_t nchunk = tk ? 0u : kv_graph_chunks(m->kv);
   // trace: n rows of `width` floats from `src` (rows `pitch` floats apart) at the trace's
   // running offset
   size_t at = 0;
@@ -361,34 +384,95 @@ static gmoe_status step_launches(gmoe_model* m, uint32_t n, const uint32_t* seqs
   return GMOE_OK;
 }
 
-// Captures the parameter-reading form of the step for batch n into m->gexec (nothing
-// runs), on the model's own stream, so that no other caller's work on the context's
-// stream joins the graph; the graph is launched on the context's stream. A capture or
-// instantiation that fails leaves the model on eager steps.
-static void capture_step(gmoe_model* m, uint32_t n) {
+// Captures the parameter-reading form of the step for batch n and nchunk attention
+// chunks into the graph cache (nothing runs), on the model's own stream, so that no other
+// caller's work on the context's stream joins the graph; the graph is launched on the
+// context's stream. A capture or instantiation that fails leaves the model on eager steps.
+static void capture_step(gmoe_model* m, uint32_t n, uint32_t nchunk) {
   hipStream_t st = m->cap;
-  if (m->gexec) hipGraphExecDestroy(m->gexec);
-  m->gexec = nullptr;
   hipGraph_t g = nullptr;
+  hipGraphExec_t exec = nullptr;
   gmoe_status s = GMOE_ERR_DEVICE;
   hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
   if (e == hipSuccess) {
-    s = step_launches(m, n, nullptr, nullptr, nullptr, st);
+    s = step_launches(m, n, nullptr, nullptr, nullptr, st, nchunk);
     e = hipStreamEndCapture(st, &g);
   }
-  if (e == hipSuccess && s == GMOE_OK) e = hipGraphInstantiate(&m->gexec, g, nullptr, nullptr, 0);
-  if (g) hipGraphDestroy(g);
+  if (e == hipSuccess && s == GMOE_OK) e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  if (g) (void)hipGraphDestroy(g);
   if (e != hipSuccess || s != GMOE_OK) {
     (void)hipGetLastError();
-    m->gexec = nullptr;
     m->graph_failed = true;
     ctx_note_graph(m->ctx, m->moe.data(), m->n_layers, ctx_stream(m->ctx));
     return;
   }
-  m->gn = n;
-  m->g_ctx = ctx_scratch_id(m->ctx);
-  m->g_kv = kv_scratch_id(m->kv);
+  // one graph per (n, nchunk): a stale one of the same key, or the least recently
+  // replayed when the cache is full, makes room (every step synchronises its stream before
+  // it returns, so none of them is running)
+  auto victim = m->gcache.end();
+  for (auto it = m->gcache.begin(); it != m->gcache.end(); ++it)
+    if (it->n == n && it->nchunk == nchunk) victim = it;
+  if (victim == m->gcache.end() && m->gcache.size() >= gmoe_model::kGraphCache)
+    victim = std::min_element(m->gcache.begin(), m->gcache.end(),
+                              [](const auto& a, const auto& b) { return a.used < b.used; });
+  if (victim != m->gcache.end()) {
+    (void)hipGraphExecDestroy(victim->exec);
+    m->gcache.erase(victim);
+  }
+  gmoe_model::Graph ent;
+  ent.exec = exec;
+  ent.n = n;
+  ent.nchunk = nchunk;
+  ent.g_ctx = ctx_scratch_id(m->ctx);
+  ent.g_kv = kv_scratch_id(m->kv);
+  ent.used = ++m->gclock;
+  m->gcache.push_back(ent);
   ctx_note_graph(m->ctx, m->moe.data(), m->n_layers, ctx_stream(m->ctx));
+}
+
+// The step's device work and the chosen tokens' return, with the sequences' positions
+// committed as it goes; a failure may leave some committed (the caller restores them).
+// *capture: the step ran the graph form directly and a graph of it is to be captured
+// for *cap_chunks attention chunks.
+static gmoe_status decode_body(gmoe_model* m, uint32_t n, const uint32_t* seqs, const GlueTokens& tk, uint32_t* next,
+                               float* logits, float* trace, bool* capture, uint32_t* cap_chunks) {
+  M_TRY(hipSetDevice(ctx_device(m->ctx)));
+  hipStream_t st = ctx_stream(m->ctx);
+  if (trace || !m->graphs || m->graph_failed) {
+    S_TRY(step_launches(m, n, seqs, &tk, trace, st, 0));
+  } else {
+    // the step's parameters: tokens, and every layer's attention entries, planned, then
+    // the scratch they need reserved, then committed (kv_check_step has refused any step
+    // that would not fit), so a failed reservation commits nothing
+    std::memcpy(m->pin_par, tk.tok, n * 4);
+    AttnEntry* pent = reinterpret_cast<AttnEntry*>(m->pin_par + kParEnt);
+    uint32_t maxspan;
+    S_TRY(kv_plan_step(m->kv, seqs, n, pent, kModelMaxBatch, &maxspan));
+    const uint32_t nchunk = kv_step_chunks(m->kv, maxspan);
+    gmoe_model::Graph* g = nullptr;
+    for (auto& e : m->gcache)
+      if (e.n == n && e.nchunk == nchunk && e.g_ctx == ctx_scratch_id(m->ctx) && e.g_kv == kv_scratch_id(m->kv))
+        g = &e;
+    if (!g) S_TRY(kv_reserve(m->kv, n, nchunk));
+    kv_commit_step(m->kv, seqs, n, pent, kModelMaxBatch);
+    M_TRY(hipMemcpyAsync(m->par, m->pin_par, par_bytes(m->n_layers), hipMemcpyHostToDevice, st));
+    if (g) {
+      M_TRY(hipGraphLaunch(g->exec, st));
+      g->used = ++m->gclock;
+      ctx_note_graph(m->ctx, m->moe.data(), m->n_layers, st);
+    } else {
+      // this step runs its launches directly (sizing every scratch it needs); the graph is
+      // captured after it, for the steps that follow
+      S_TRY(step_launches(m, n, seqs, nullptr, nullptr, st, nchunk));
+      *capture = true;
+      *cap_chunks = nchunk;
+    }
+  }
+  M_TRY(hipMemcpyAsync(m->pin_next, m->next, n * 4, hipMemcpyDeviceToHost, st));
+  if (logits) M_TRY(hipMemcpyAsync(logits, m->logits, (size_t)n * m->vocab * 4, hipMemcpyDeviceToHost, st));
+  M_TRY(hipStreamSynchronize(st));
+  std::memcpy(next, m->pin_next, n * 4);
+  return GMOE_OK;
 }
 
 static gmoe_status model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs, const uint32_t* tokens,
@@ -405,40 +489,21 @@ static gmoe_status model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs,
     tk.tok[i] = tokens[i];
   }
   S_TRY(kv_check_step(m->kv, seqs, n));
-  for (uint32_t l = 0; l < m->n_layers; l++) {  // the MoE layers run from the slab: all resident
-    uint32_t w, ne;
-    if (!layer_width(m->ctx, m->moe[l], &w, &ne)) return mfail(GMOE_ERR_INFERENCE, "MoE layer %u was released", m->moe[l]);
-    for (uint32_t e = 0; e < ne; e++)
-      if (gmoe_expert_is_resident(m->ctx, m->moe[l], e) != 1)
-        return mfail(GMOE_ERR_CACHE, "expert %u of layer %u is not resident", e, l);
-  }
-  M_TRY(hipSetDevice(ctx_device(m->ctx)));
-  hipStream_t st = ctx_stream(m->ctx);
+  // the MoE layers run from the slab: every expert resident, and kept so until the step's
+  // device work has finished
+  S_TRY(ctx_pin_layers(m->ctx, m->moe.data(), m->n_layers));
+  std::vector<uint32_t> snap;
+  kv_snapshot(m->kv, seqs, n, snap);
   bool capture = false;
-  if (trace || !m->graphs || m->graph_failed) {
-    S_TRY(step_launches(m, n, seqs, &tk, trace, st));
-  } else {
-    // the step's parameters: tokens, and every layer's attention entries, planned and
-    // committed here (kv_check_step has refused any step that would not fit)
-    std::memcpy(m->pin_par, tk.tok, n * 4);
-    AttnEntry* pent = reinterpret_cast<AttnEntry*>(m->pin_par + kParEnt);
-    for (uint32_t l = 0; l < m->n_layers; l++) S_TRY(kv_plan_commit(m->kv, l, seqs, n, pent + (size_t)l * kModelMaxBatch));
-    M_TRY(hipMemcpyAsync(m->par, m->pin_par, par_bytes(m->n_layers), hipMemcpyHostToDevice, st));
-    if (m->gexec && m->gn == n && m->g_ctx == ctx_scratch_id(m->ctx) && m->g_kv == kv_scratch_id(m->kv)) {
-      M_TRY(hipGraphLaunch(m->gexec, st));
-      ctx_note_graph(m->ctx, m->moe.data(), m->n_layers, st);
-    } else {
-      // this step runs its launches directly (sizing every scratch it needs); the graph is
-      // captured after it, for the steps that follow
-      S_TRY(kv_reserve(m->kv, n, kv_graph_chunks(m->kv)));
-      S_TRY(step_launches(m, n, seqs, nullptr, nullptr, st));
-      capture = true;
-    }
+  uint32_t cap_chunks = 0;
+  const gmoe_status s = decode_body(m, n, seqs, tk, next, logits, trace, &capture, &cap_chunks);
+  if (s != GMOE_OK) {
+    // a refused step leaves every sequence where it was: its queued work has finished
+    // before the positions and pages it committed are given back
+    (void)hipStreamSynchronize(ctx_stream(m->ctx));
+    kv_restore(m->kv, seqs, n, snap);
   }
-  M_TRY(hipMemcpyAsync(m->pin_next, m->next, n * 4, hipMemcpyDeviceToHost, st));
-  if (logits) M_TRY(hipMemcpyAsync(logits, m->logits, (size_t)n * m->vocab * 4, hipMemcpyDeviceToHost, st));
-  M_TRY(hipStreamSynchronize(st));
-  std::memcpy(next, m->pin_next, n * 4);
-  if (capture) capture_step(m, n);
-  return GMOE_OK;
+  ctx_unpin_layers(m->ctx, m->moe.data(), m->n_layers);
+  if (s == GMOE_OK && capture) capture_step(m, n, cap_chunks);
+  return s;
 }

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GMOE_ABI_VERSION 4u
+#define GMOE_ABI_VERSION 5u
 
 /* Status codes. Mirrors the GarudaError variants the reference returns on this
  * path (garuda/src/core/mod.rs:10-47). */
@@ -111,6 +111,20 @@ uint32_t gmoe_abi_version(void);
  * expert is staged again from them. */
 gmoe_status gmoe_layer_register(gmoe_ctx* ctx, const gmoe_layer_desc* desc, uint32_t* layer_id);
 gmoe_status gmoe_layer_release(gmoe_ctx* ctx, uint32_t layer_id);
+
+/* The expert loader under the slab (core::ExpertLoader::load on an L1 miss,
+ * core/mod.rs:215-223; MemoryManager::load_uncached, memory/mod.rs:114-146): fills
+ * weights[0..2] with expert `expert`'s gate, up and down bytes in the descriptor's types,
+ * row-major as in a split tensor, valid until the same expert is fetched again or the
+ * source closes. A non-zero status fails the call that needed the expert. */
+typedef gmoe_status (*gmoe_expert_fetch)(void* user, uint32_t expert, const void* weights[3]);
+/* Register a layer whose experts come from `fetch` each time one is staged into the slab
+ * (first routing, or again after an eviction). The descriptor's dims, types and router are
+ * used as gmoe_layer_register uses them; its tensors' data and expert pointers are not
+ * read, and nothing is staged until an expert is routed, prefetched or asked for. `user`
+ * must stay valid until gmoe_layer_release. */
+gmoe_status gmoe_layer_register_fetch(gmoe_ctx* ctx, const gmoe_layer_desc* desc, gmoe_expert_fetch fetch,
+                                      void* user, uint32_t* layer_id);
 
 /* ---- the hot path ---- */
 
@@ -284,19 +298,24 @@ gmoe_status gmoe_gguf_expert_ranges(gmoe_gguf* g, uint32_t layer, uint32_t exper
 /* ---- the synthetic engine's expert tiers (memory/mod.rs:114-184, weights/mod.rs:17-164) ----
  *
  * garuda's MoeEngine (moe/mod.rs:67-112) pulls each routed expert through MemoryManager:
- * the L1 cache, else `expert_{id}.bin` in the L2 directory, else a deterministic synthesis
- * written back to L2. Here the HBM slab is L1 and a gmoe_l2 handle is the L2 side. Each
- * file is read as weights::expert_from_bytes reads it: little-endian f32, gate [f x d],
- * up [f x d], down [d x f], exactly 3*f*d*4 bytes, every value finite (GMOE_ERR_MODEL with
- * the reference's message otherwise). An expert with no file is synthesised as
- * weights::synthesize_expert does and written to the directory (a failed write is not an
- * error). Host code; the files stay mapped while the handle lives. */
+ * the L1 cache, else `expert_{id}.bin` in the L2 directory, else the same file in the L3
+ * directory (promoted into L2), else a deterministic synthesis written to L2. Here the
+ * HBM slab is L1 and a gmoe_l2 handle is the L2/L3 side. Each file is read as
+ * weights::expert_from_bytes reads it: little-endian f32, gate [f x d], up [f x d], down
+ * [d x f], exactly 3*f*d*4 bytes, every value finite (GMOE_ERR_MODEL with the reference's
+ * message otherwise). An expert with no file is synthesised as weights::synthesize_expert
+ * does and written to L2; a failed write or promotion is not an error (the weights are
+ * held). Host code. */
 typedef struct gmoe_l2 gmoe_l2;
 typedef struct gmoe_l2_counts {
-  uint64_t l2;           /* experts read from their file (TierCounts::l2) */
+  uint64_t l2;           /* loads from an L2 file (TierCounts::l2) */
   uint64_t synthesised;  /* experts synthesised (TierCounts::synthesised) */
-  uint64_t written;      /* synthesised experts materialised into the directory */
+  uint64_t written;      /* synthesised experts materialised into L2 */
+  uint64_t l3;           /* loads from an L3 file (TierCounts::l3) */
+  uint64_t promoted;     /* L3 loads copied into L2 */
 } gmoe_l2_counts;
+/* MemoryTier below L1 (memory/mod.rs:17-24, locate :99-111): where a load would find it */
+enum { GMOE_TIER_L2 = 1, GMOE_TIER_L3 = 2, GMOE_TIER_SYNTHESISED = 3 };
 
 /* weights::seeded (weights/mod.rs:26-35): n values uniform in [-bound, bound] from the
  * splitmix64 stream of `seed`; the engine's shared weights use it with bound(fan_in) =
@@ -304,17 +323,36 @@ typedef struct gmoe_l2_counts {
 gmoe_status gmoe_fill_seeded(uint64_t seed, uint64_t n, float bound, float* out);
 /* Experts id_base .. id_base + n_experts - 1 of the directory `dir` (expert e of the layer
  * is file expert_{id_base + e}.bin). */
+/* Every expert is loaded at open (the files stay mapped while the handle lives). */
 gmoe_status gmoe_l2_open(const char* dir, uint32_t d_model, uint32_t d_ff, uint32_t n_experts, uint32_t id_base,
                          gmoe_l2** out);
+/* MemoryManager::new with an L2 directory and an optional L3 one (l3_dir may be NULL:
+ * no L3 tier): nothing is loaded at open; each gmoe_l2_fetch is one load_uncached. */
+gmoe_status gmoe_tiers_open(const char* l2_dir, const char* l3_dir, uint32_t d_model, uint32_t d_ff,
+                            uint32_t n_experts, uint32_t id_base, gmoe_l2** out);
 void gmoe_l2_close(gmoe_l2* l2);
 gmoe_status gmoe_l2_get_counts(const gmoe_l2* l2, gmoe_l2_counts* out);
+/* MemoryManager::load_uncached (memory/mod.rs:114-146) for expert `expert` of the handle:
+ * an L2 file, else an L3 file (written into L2), else a synthesis (written into L2),
+ * counted per load. weights[0..2] receive its gate, up and down f32 values, valid until
+ * the expert is fetched again or the handle closes. An expert outside the handle is
+ * GMOE_ERR_MODEL, as ExpertLoader::load refuses it (:151-157). Thread-safe: concurrent
+ * fetches of one expert load it one after another, so it is synthesised once. */
+gmoe_status gmoe_l2_fetch(gmoe_l2* l2, uint32_t expert, const void* weights[3]);
+/* MemoryManager::locate below L1: GMOE_TIER_L2, _L3 or _SYNTHESISED; -1 outside the handle */
+int gmoe_l2_locate(const gmoe_l2* l2, uint32_t expert);
 /* The tier's experts as a layer descriptor: split F32 tensors pointing into the handle
  * (valid until gmoe_l2_close, so a layer registered from it is released first), the
  * given router [n_experts x d_model], top_k, gating (the engine's Router types: MIXTRAL,
  * DEEPSEEK, QWEN) and combine order (the engine's is RANK_ORDER, moe/mod.rs:104-109),
- * math F32 (simd::matvec, moe/mod.rs:82-90). */
+ * math F32 (simd::matvec, moe/mod.rs:82-90). For a handle from gmoe_l2_open only. */
 gmoe_status gmoe_l2_layer_desc(const gmoe_l2* l2, const float* router, uint32_t top_k, uint32_t gating,
                                uint32_t combine, gmoe_layer_desc* out);
+/* The same layer registered with its experts fetched from the tiers when staged
+ * (gmoe_layer_register_fetch over gmoe_l2_fetch): MoeEngine's lazy loads, an eviction
+ * followed by a reload from L2. Any handle; it must outlive the layer. */
+gmoe_status gmoe_l2_layer_register(gmoe_ctx* ctx, gmoe_l2* l2, const float* router, uint32_t top_k,
+                                   uint32_t gating, uint32_t combine, uint32_t* layer_id);
 
 /* ---- decode attention over a paged KV cache (llama/mod.rs:766-821, cache/mod.rs:143-600) ----
  *
@@ -346,6 +384,12 @@ gmoe_status gmoe_kv_seq_open(gmoe_kv* kv, uint32_t* seq);
 /* Frees the sequence's pages (after queued device work has finished). */
 gmoe_status gmoe_kv_seq_close(gmoe_kv* kv, uint32_t seq);
 gmoe_status gmoe_kv_seq_len(const gmoe_kv* kv, uint32_t seq, uint32_t layer, uint32_t* len);
+/* Pages of the pool no sequence holds (CacheStats-like accounting of the paged pool). */
+gmoe_status gmoe_kv_free_pages(gmoe_kv* kv, uint64_t* pages);
+/* Test entry (no counterpart in the reference): the next `count` reservations of attention
+ * scratch for graph-replayed model steps fail with GMOE_ERR_DEVICE, as a failed device
+ * allocation would, so that tests can check a failed step leaves every sequence as it was. */
+gmoe_status gmoe_kv_fail_reserves(gmoe_kv* kv, uint32_t count);
 /* Attention for n tokens in layer `layer`: q [n x n_heads*head_dim], k and v
  * [n x kv_dim] (projected, not yet rotated), context [n x n_heads*head_dim] out.
  * Synchronous; host pointers. */

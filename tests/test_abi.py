@@ -16,6 +16,7 @@ ROOT = Path(__file__).resolve().parents[1]
 def declared_symbols():
     text = (ROOT / "include" / "garuda_moe.h").read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"typedef[^;]*\(\s*\*[^;]*;", "", text)  # function-pointer types (callbacks)
     return sorted(set(re.findall(r"\b(gmoe_[a-z_0-9]+)\s*\(", text)))
 
 
@@ -26,7 +27,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     for s in syms:
         assert hasattr(lib, s), s
     assert set(syms) == set(_lib.SIGNATURES), "ctypes table and header disagree"
-    assert lib.gmoe_abi_version() == 4
+    assert lib.gmoe_abi_version() == 5
     assert lib.gmoe_last_invalid_token() == 0xFFFFFFFF  # none yet on this thread
 
 

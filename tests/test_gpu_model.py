@@ -276,3 +276,121 @@ def test_refusals_leave_the_sequences_unchanged(dev, weights):
                           np.zeros((VOCAB, wide), np.float32))
     finally:
         release(*parts)
+
+
+def test_failed_graph_step_leaves_the_sequences_unchanged(dev, weights):
+    """A graph-replayed step plans every layer's positions, reserves the attention scratch
+    they need and only then commits them; a step that fails after committing gives them
+    back. With the reservation refused (a test hook standing in for an allocation failure)
+    the step is an error and every sequence keeps its length and the pool its free pages;
+    the next steps then match a model that never failed, bit for bit."""
+    a, b = gpu_model(dev, weights, max_positions=256), gpu_model(dev, weights, max_positions=256)
+    ma, kva, mb, kvb = a[0], a[1], b[0], b[1]
+    try:
+        sa = [kva.open_seq() for _ in range(2)]
+        sb = [kvb.open_seq() for _ in range(2)]
+        toks = np.array([5, 9], np.uint32)
+        for step in range(3):
+            na = ma.decode_step(sa, toks)
+            nb = mb.decode_step(sb, toks)
+            assert np.array_equal(na, nb)
+            toks = na
+        # a batch size of a new graph: its scratch is reserved before anything commits
+        lens = [kva.seq_len(s, l) for s in sa for l in range(NL)]
+        free = kva.free_pages()
+        kva.fail_reserves(1)
+        with pytest.raises(G.DeviceError):
+            ma.decode_step(sa[:1], toks[:1])
+        assert [kva.seq_len(s, l) for s in sa for l in range(NL)] == lens
+        assert kva.free_pages() == free
+        for step in range(66):  # past pages (16 positions) and a chunk bucket (64 positions)
+            say(f"after a failed step: step {step}")
+            na, la = ma.decode_step(sa, toks, want_logits=True)
+            nb, lb = mb.decode_step(sb, toks, want_logits=True)
+            assert np.array_equal(na, nb) and np.array_equal(la.view(np.uint32), lb.view(np.uint32)), step
+            toks = na
+        assert kva.free_pages() == kvb.free_pages()
+    finally:
+        release(*a)
+        release(*b)
+
+
+def test_graph_cache_serves_drifting_batches_over_a_long_window(dev):
+    """Continuous batching: the batch size drifts between 1 and 3 as sequences join and
+    leave, over a 32768-position window. Graphs are kept per (batch, chunk bucket) and
+    replayed; each replayed step's attention spans the live context's bucket, not the
+    window. Every step matches a model issuing every launch, bit for bit."""
+    w = tiny_model(17, n_layers=2, d=D, nh=NH, nkv=NKV, hd=HD, f=F, ne=NE, k=K, vocab=VOCAB)
+    a, b = gpu_model(dev, w, max_positions=32768), gpu_model(dev, w, max_positions=32768)
+    ma, kva, mb, kvb = a[0], a[1], b[0], b[1]
+    try:
+        ma.set_graphs(False)
+        sa = [kva.open_seq() for _ in range(3)]
+        sb = [kvb.open_seq() for _ in range(3)]
+        rng = np.random.default_rng(5)
+        toks = rng.integers(0, VOCAB, 3).astype(np.uint32)
+        pattern = [3, 2, 3, 1, 3, 2, 2, 3, 1, 1]
+        replays = 0
+        for step in range(40):
+            n = pattern[step % len(pattern)]
+            live = list(range(n))
+            replays += mb.graph_ready(n)
+            say(f"drifting batch step {step}, n={n}")
+            na, la = ma.decode_step([sa[i] for i in live], toks[live], want_logits=True)
+            nb, lb = mb.decode_step([sb[i] for i in live], toks[live], want_logits=True)
+            assert np.array_equal(na, nb), f"step {step}: next tokens differ"
+            assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)), f"step {step}: logits differ"
+            toks[live] = na
+        assert replays >= 30, f"{replays} steps replayed from a graph"
+    finally:
+        release(*a)
+        release(*b)
+
+
+def test_model_layers_are_kept_resident_during_a_step(dev, weights):
+    """A model step reads every expert of its layers through the device pointer tables,
+    so they are held in the slab from the residency check until the step's device work is
+    done: an eviction requested meanwhile is refused, and after the step it goes through.
+    (Between steps, the staging thread or another call may evict them; the next step then
+    refuses cleanly.)"""
+    parts = gpu_model(dev, weights)
+    model, kv, moe = parts[0], parts[1], parts[2]
+    try:
+        s = kv.open_seq()
+        model.decode_step([s], [1])
+        import threading
+        errs, done = [], threading.Event()
+
+        import time
+        held = [0]
+
+        def evictor():
+            while not done.is_set():
+                try:
+                    moe[0].evict(0)
+                    moe[0].prefetch(0)
+                    time.sleep(0.002)
+                except G.CacheError as e:
+                    held[0] += "in use by a model step" in str(e)  # refused while a step held the layer
+                except Exception as e:  # noqa: BLE001 - reported below
+                    errs.append(e)
+                    return
+
+        t = threading.Thread(target=evictor)
+        t.start()
+        ok = 0
+        try:
+            for step in range(30):
+                try:
+                    model.decode_step([s], [step % VOCAB])
+                    ok += 1
+                except G.CacheError:
+                    pass  # the expert was out between steps: refused before any device work
+        finally:
+            done.set()
+            t.join()
+        say(f"{ok} of 30 steps ran; {held[0]} evictions refused while a step held the layer")
+        assert not errs, errs
+        assert ok > 0
+    finally:
+        release(*parts)

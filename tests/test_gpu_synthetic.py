@@ -116,3 +116,53 @@ def test_c1_engine_decodes_as_the_oracle(dev, tmp_path):
             nxt = prompt[:, step + 1] if step + 1 < prompt.shape[1] else on
             toks = np.asarray(nxt, np.uint32)
         assert len(ambiguous) < 2
+
+
+def test_engine_layer_over_lazy_l2_l3_tiers(tmp_path):
+    """MemoryManager's full path under the slab (memory/mod.rs:114-146): a layer whose
+    experts are fetched when routed. Experts 0, 3, 6 and 7 sit in L3 only, the others
+    nowhere: a routed L3 expert is promoted into L2, a routed absent one synthesised into
+    L2, an unrouted one never loaded; after an eviction the expert comes back from L2.
+    Outputs and routing as the oracle's, bit-exact routing."""
+    l2, l3 = tmp_path / "l2", tmp_path / "l3"
+    l2.mkdir()
+    l3.mkdir()
+    write_reference_fixtures(l3)
+    router = O.seeded(SEED_ROUTER, NE * D, O.lib().or_bound(D))
+    gate, up, down = oracle_experts(D, F, range(NE))
+    L = dict(d=D, f=F, ne=NE, k=K, gating=G.GATING_MIXTRAL, combine=1, packed=0, router=router,
+             qtypes=(O.F32,) * 3, gate=gate, up=up, down=down)
+    per = 3 * F * D * 4
+    rng = np.random.default_rng(11)
+    # room for two experts: a one-token call at top-2, so every call evicts
+    with G.Device(0, slab_bytes=2 * per + (1 << 16)) as small, ExpertTier(l2, D, F, NE, l3=l3) as tier:
+        layer = tier.layer(small, router, K, G.GATING_MIXTRAL, G.COMBINE_RANK_ORDER)
+        try:
+            assert not any(layer.is_resident(e) for e in range(NE))  # nothing loaded at registration
+            assert tier.counts().l2 + tier.counts().l3 + tier.counts().synthesised == 0
+            seen = []
+            for step in range(10):
+                say(f"lazy tiers step {step}")
+                hs = rng.normal(0, 1, (1, D)).astype(np.float32)
+                before = {e: tier.locate(e) for e in range(NE)}
+                c0 = tier.counts()
+                resident = [e for e in range(NE) if layer.is_resident(e)]
+                out, ids, w = layer.feed_forward_batch(hs)
+                wout, wids, ww = O.feed_forward_batch(L, hs)
+                assert np.array_equal(ids, wids) and np.array_equal(bits(w), bits(ww))
+                assert np.allclose(out, wout, rtol=RTOL, atol=ATOL), np.abs(out - wout).max()
+                c1 = tier.counts()
+                loaded = [int(e) for e in ids.reshape(-1) if int(e) not in resident]
+                want = {G.TIER_L2: 0, G.TIER_L3: 0, G.TIER_SYNTHESISED: 0}
+                for e in loaded:
+                    want[before[e]] += 1
+                assert (c1.l2 - c0.l2, c1.l3 - c0.l3, c1.synthesised - c0.synthesised) == \
+                    (want[G.TIER_L2], want[G.TIER_L3], want[G.TIER_SYNTHESISED]), (step, loaded, before)
+                for e in loaded:
+                    assert tier.locate(e) == G.TIER_L2  # promoted or materialised into L2
+                seen += [int(e) for e in ids.reshape(-1)]
+            for e in set(range(NE)) - set(seen):
+                assert not (l2 / f"expert_{e}.bin").exists()  # never routed, never loaded
+            assert small.slab_stats().evictions > 0 and tier.counts().l2 > 0
+        finally:
+            layer.release()

@@ -86,3 +86,123 @@ def test_bad_files_are_model_errors(tmp_path):
     (tmp_path / "expert_2.bin").write_bytes(bad.tobytes())
     with pytest.raises(G.ModelError, match=r"expert 2: non-finite weight at index 1234"):
         ExpertTier(tmp_path, D, F, NE)
+
+
+# ---- the lazy tiers: one MemoryManager::load_uncached per fetch (memory/mod.rs:114-146),
+# restating the reference's own tier tests (memory/mod.rs:237-372) below L1 ----
+
+def _dirs(tmp_path):
+    l2, l3 = tmp_path / "l2", tmp_path / "l3"
+    l2.mkdir()
+    l3.mkdir()
+    return l2, l3
+
+
+def _synth_bytes(e):
+    return np.concatenate(O.synthesize_expert(e)).astype("<f4").tobytes()
+
+
+def test_first_fetch_synthesises_then_the_next_reads_l2(tmp_path):
+    # first_load_synthesises_then_second_load_hits_l1 (:238-257): below L1 the second load
+    # is the L2 file the synthesis materialised
+    l2, l3 = _dirs(tmp_path)
+    with ExpertTier(l2, D, F, NE, l3=l3) as tier:
+        assert (tier.counts().l2, tier.counts().synthesised) == (0, 0)  # nothing loaded at open
+        assert tier.locate(0) == G.TIER_SYNTHESISED
+        a = tier.fetch(0)
+        c = tier.counts()
+        assert (c.synthesised, c.written, c.l2, c.l3) == (1, 1, 0, 0)
+        assert (l2 / "expert_0.bin").exists() and tier.locate(0) == G.TIER_L2
+        b = tier.fetch(0)
+        assert tier.counts().l2 == 1 and tier.counts().synthesised == 1
+        for x, y in zip(a, b):
+            assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+        assert (l2 / "expert_0.bin").read_bytes() == _synth_bytes(0)
+
+
+def test_l3_hit_is_promoted_into_l2(tmp_path):
+    # l3_hit_is_promoted_into_l2 (:280-301)
+    l2, l3 = _dirs(tmp_path)
+    (l3 / "expert_5.bin").write_bytes(_synth_bytes(5))
+    with ExpertTier(l2, D, F, NE, l3=l3) as tier:
+        assert tier.locate(5) == G.TIER_L3
+        g, u, dn = tier.fetch(5)
+        c = tier.counts()
+        assert (c.l3, c.promoted, c.l2, c.synthesised) == (1, 1, 0, 0)
+        want = O.synthesize_expert(5)
+        assert np.array_equal(dn.reshape(-1).view(np.uint32), np.asarray(want[2], np.float32).view(np.uint32))
+        assert (l2 / "expert_5.bin").read_bytes() == _synth_bytes(5)
+        assert tier.locate(5) == G.TIER_L2
+        tier.fetch(5)  # one tier shallower the next time
+        assert (tier.counts().l2, tier.counts().l3) == (1, 1)
+
+
+def test_l2_shadows_l3(tmp_path):
+    # load_uncached looks in L2 first (:118-123): an L3 file under an L2 one is never read
+    l2, l3 = _dirs(tmp_path)
+    other = np.random.default_rng(1).normal(0, 0.1, 3 * F * D).astype("<f4")
+    (l2 / "expert_2.bin").write_bytes(other.tobytes())
+    (l3 / "expert_2.bin").write_bytes(_synth_bytes(2))
+    with ExpertTier(l2, D, F, NE, l3=l3) as tier:
+        g, _, _ = tier.fetch(2)
+        assert np.array_equal(g.reshape(-1), other[:F * D])
+        assert (tier.counts().l2, tier.counts().l3) == (1, 0)
+
+
+def test_a_corrupt_file_fails_its_load_not_the_open(tmp_path):
+    # a_corrupt_expert_file_is_an_error_not_a_panic (:303-314): the error comes when the
+    # expert is loaded, as GarudaError::Model; the other experts still load
+    l2, l3 = _dirs(tmp_path)
+    (l2 / "expert_3.bin").write_bytes(bytes([0, 1]))
+    bad = np.zeros(3 * F * D, "<f4")
+    bad[77] = np.inf
+    (l3 / "expert_4.bin").write_bytes(bad.tobytes())
+    with ExpertTier(l2, D, F, NE, l3=l3) as tier:
+        with pytest.raises(G.ModelError, match=r"expert 3: expected 393216 bytes for dims 128x256, found 2"):
+            tier.fetch(3)
+        with pytest.raises(G.ModelError, match=r"expert 4: non-finite weight at index 77"):
+            tier.fetch(4)
+        assert not (l2 / "expert_4.bin").exists()  # a failed L3 load promotes nothing
+        tier.fetch(1)
+        assert tier.counts().synthesised == 1
+
+
+def test_out_of_range_expert_is_rejected(tmp_path):
+    # out_of_range_expert_is_rejected (:316-322)
+    l2, l3 = _dirs(tmp_path)
+    with ExpertTier(l2, D, F, NE, l3=l3) as tier:
+        with pytest.raises(G.ModelError, match=rf"expert {NE} does not exist \(model has {NE}\)"):
+            tier.fetch(NE)
+        assert tier.locate(NE) == -1
+
+
+def test_concurrent_misses_on_one_expert_synthesise_it_once(tmp_path):
+    # concurrent_misses_on_one_expert_do_a_single_load (:324-345)
+    import threading
+    l2, l3 = _dirs(tmp_path)
+    with ExpertTier(l2, D, F, NE, l3=l3) as tier:
+        errs = []
+
+        def go():
+            try:
+                tier.fetch(2)
+            except Exception as e:  # noqa: BLE001 - reported below
+                errs.append(e)
+
+        ts = [threading.Thread(target=go) for _ in range(8)]
+        for t in ts:
+            t.start()
+        for t in ts:
+            t.join()
+        assert not errs
+        c = tier.counts()
+        assert c.synthesised == 1, "expert was built more than once"
+        assert c.synthesised + c.l2 == 8
+
+
+def test_works_without_an_l3_tier(tmp_path):
+    # works_without_an_l3_tier (:365-383)
+    with ExpertTier(tmp_path, D, F, NE, lazy=True) as tier:
+        tier.fetch(0)
+        assert (tmp_path / "expert_0.bin").exists()
+        assert tier.locate(1) == G.TIER_SYNTHESISED
