@@ -718,12 +718,19 @@ __device__ __forceinline__ int total_key(float f) {
 }
 
 // rank order: llama = total_cmp descending, stable (llama/mod.rs:943);
-// router = partial_cmp descending, unordered/equal -> lower id first (router/mod.rs:83-88).
+// router = partial_cmp descending, equal -> lower id first (router/mod.rs:83-88). The
+// router's comparator is no order once a logit is NaN (NaN compares Equal to every value,
+// which is not transitive; Rust's sort_by then gives an unspecified order and may panic),
+// so this build ranks a NaN logit after every number and NaNs among themselves by id: a
+// strict total order that agrees with partial_cmp wherever that is one, so the counted
+// ranks below are always a permutation.
 __device__ __forceinline__ bool ranks_before(bool llama, float a, uint32_t ia, float b, uint32_t ib) {
   if (llama) {
     int ka = total_key(a), kb = total_key(b);
     return ka > kb || (ka == kb && ia < ib);
   }
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return na == nb ? ia < ib : nb;
   if (a > b) return true;
   if (a < b) return false;
   return ia < ib;
@@ -802,22 +809,19 @@ __device__ void gate_wave_wide(uint32_t gating, uint32_t ne, uint32_t k, const f
   }
   float* tw = reinterpret_cast<float*>(scratch);
   uint32_t* ti = scratch + k;
-  // When the rank order is a strict total order (always under total_cmp; under
-  // partial_cmp when no value is NaN, +0 and -0 then being equal), the r-th ranked expert
-  // is the r-th pick of k rounds of a wave-wide maximum over the key (value key, then
-  // ~id, so that ties go to the lower id). Otherwise the ranks are counted as gate_wave
-  // counts them.
-  bool nan = false;
-#pragma unroll
-  for (int j = 0; j < EPL; j++) nan |= (64 * j + lane < ne) && (v[j] != v[j]);
-  if (llama || __ballot(nan) == 0ull) {
+  // The rank order (ranks_before) is a strict total order, so the r-th ranked expert is
+  // the r-th pick of k rounds of a wave-wide maximum over the key (value key, then ~id,
+  // so that ties go to the lower id).
+  {
     uint64_t key[EPL];
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
       const uint32_t e = 64 * j + lane;
-      // order-preserving unsigned image of the rank order's value key
+      // order-preserving unsigned image of the rank order's value key: under partial_cmp
+      // +0 and -0 are one value and a NaN comes after every number (0, below -inf's key)
       const uint32_t vk = llama ? (uint32_t)total_key(v[j]) ^ 0x80000000u
-                                : (uint32_t)total_key(v[j] == 0.0f ? 0.0f : v[j]) ^ 0x80000000u;
+                          : v[j] != v[j] ? 0u
+                                         : (uint32_t)total_key(v[j] == 0.0f ? 0.0f : v[j]) ^ 0x80000000u;
       key[j] = e < ne ? ((uint64_t)vk << 32) | (uint64_t)(0xffffffffu - e) : 0ull;
     }
     for (uint32_t r = 0; r < k; r++) {
@@ -837,30 +841,6 @@ __device__ void gate_wave_wide(uint32_t gating, uint32_t ne, uint32_t k, const f
           ti[r] = e;
           key[j] = 0ull;
         }
-    }
-  } else {
-    // rank = how many experts come before this one
-    uint32_t r[EPL];
-#pragma unroll
-    for (int j = 0; j < EPL; j++) r[j] = 0;
-#pragma unroll
-    for (int jo = 0; jo < EPL; jo++)
-      for (uint32_t l = 0; l < 64 && 64 * jo + l < ne; l++) {
-        const uint32_t o = 64 * jo + l;
-        const float vo = lane_f(v[jo], l);
-#pragma unroll
-        for (int j = 0; j < EPL; j++) {
-          const uint32_t e = 64 * j + lane;
-          if (o != e && ranks_before(llama, vo, o, v[j], e)) r[j]++;
-        }
-      }
-#pragma unroll
-    for (int j = 0; j < EPL; j++) {
-      const uint32_t e = 64 * j + lane;
-      if (e < ne && r[j] < k) {
-        tw[r[j]] = v[j];
-        ti[r[j]] = e;
-      }
     }
   }
   __builtin_amdgcn_wave_barrier();

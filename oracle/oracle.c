@@ -714,13 +714,19 @@ static inline int32_t total_key(float f) {
 }
 
 /* Stable sort descending. llama: by total_cmp (llama/mod.rs:943, slice::sort_by is
- * stable so equal keys keep ascending id). Router: partial_cmp with NaN as Equal,
- * then id ascending (router/mod.rs:83-88). Insertion sort is stable and ne is small. */
+ * stable so equal keys keep ascending id). Router: partial_cmp, equal values by id
+ * ascending (router/mod.rs:83-88). The reference's comparator maps an unordered pair to
+ * Equal, which is no order once a logit is NaN (Rust's sort_by then gives an unspecified
+ * order, or panics): this restatement, like the device code, ranks a NaN after every
+ * number and NaNs among themselves by id. That case is parity unpinned: nothing in the
+ * reference fixes it. Insertion sort is stable and ne is small. */
 static int before_llama(float a_s, float b_s) { return total_key(a_s) > total_key(b_s); }
 static int before_router(uint32_t a_id, float a_s, uint32_t b_id, float b_s) {
+  const int na = a_s != a_s, nb = b_s != b_s;
+  if (na || nb) return na == nb ? a_id < b_id : nb;
   if (a_s > b_s) return 1;
   if (a_s < b_s) return 0;
-  return a_id < b_id;  /* equal or unordered: id ascending */
+  return a_id < b_id;  /* equal: id ascending */
 }
 
 void or_gate(int kind, float* scores, int ne, int k, uint32_t* ids, float* w) {

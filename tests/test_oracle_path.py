@@ -288,3 +288,54 @@ def test_q4k_packed_layer_tracks_full_layer_within_int8_error():
     assert (ia == ib).all()
     rel = np.linalg.norm(a - b) / np.linalg.norm(b)
     assert 1e-5 < rel < 0.05
+
+
+# ---- gating on non-finite logits ----
+# simd::softmax falls back to uniform when the maximum or the sum is not finite
+# (simd/mod.rs:132-158), which fixes llama, DeepSeek and Qwen gating on NaN and +-inf:
+# uniform probabilities, ranked by id. Mixtral ranks the raw logits with partial_cmp,
+# which is no order once a value is NaN (router/mod.rs:83-88: Rust's sort_by then gives
+# an unspecified order or panics): this build ranks a NaN after every number, NaNs among
+# themselves by id (parity unpinned: nothing in the reference fixes that case).
+
+def _brute_router_topk(scores, k):
+    s = np.asarray(scores, np.float32)
+    order = sorted(range(s.size), key=lambda i: (bool(np.isnan(s[i])), 0.0 if np.isnan(s[i]) else -float(s[i]), i))
+    return order[:k]
+
+
+def test_softmax_gatings_are_uniform_on_nan_or_infinity():
+    for bad in (np.nan, np.inf):
+        scores = np.array([0.3, bad, -1.0, 2.0, 0.5], np.float32)
+        for kind in (0, 2, 3):  # llama, DeepSeek, Qwen
+            ids, w = O.gate(kind, scores, 2)
+            assert ids.tolist() == [0, 1], (kind, bad)  # equal probabilities: lower ids first
+            want = {0: 0.5, 2: 0.2, 3: 0.5}[kind]  # llama/Qwen renormalise, DeepSeek keeps 1/ne
+            assert np.allclose(w, want), (kind, bad, w)
+    # -inf beside finite values is an ordinary masked logit: exp(-inf) = 0
+    ids, w = O.gate(0, np.array([0.3, -np.inf, 2.0], np.float32), 2)
+    assert ids.tolist() == [2, 0] and w[1] > 0
+
+
+def test_mixtral_ranks_nan_after_every_number():
+    ids, w = O.gate(1, np.array([1.0, np.nan, 2.0], np.float32), 2)
+    assert ids.tolist() == [2, 0]
+    assert np.allclose(w, np.exp([0.0, -1.0]) / np.exp([0.0, -1.0]).sum())
+    # +-inf are numbers: +inf first, -inf after every finite value but before NaN
+    ids, w = O.gate(1, np.array([np.nan, -np.inf, 0.5, np.inf], np.float32), 3)
+    assert ids.tolist() == [3, 2, 1]
+    assert np.allclose(w, 1.0 / 3)  # softmax over [inf, 0.5, -inf]: the maximum is not finite
+    # fewer than k numbers: the NaNs follow by id, and the kept NaN makes softmax uniform
+    ids, w = O.gate(1, np.array([np.nan, 3.0, np.nan, np.nan], np.float32), 3)
+    assert ids.tolist() == [1, 0, 2] and np.allclose(w, 1.0 / 3)
+    rng = np.random.default_rng(8)
+    for _ in range(300):
+        ne = int(rng.integers(2, 40))
+        s = rng.normal(0, 2, ne).astype(np.float32)
+        s[rng.random(ne) < 0.3] = np.nan
+        s[rng.random(ne) < 0.1] = np.inf
+        s[rng.random(ne) < 0.1] = -np.inf
+        s[rng.random(ne) < 0.2] = s[0]  # ties
+        k = int(rng.integers(1, ne + 1))
+        ids, _ = O.gate(1, s, k)
+        assert ids.tolist() == _brute_router_topk(s, k)
