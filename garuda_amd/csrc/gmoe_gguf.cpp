@@ -359,11 +359,12 @@ gmoe_status moe_dims(const gmoe_gguf* g, MoeDims* m) {
   if (a == g->meta.end() || a->second.type != 8) return gfail(GMOE_ERR_MODEL, "no general.architecture");
   const char* arch = a->second.s.c_str();
   struct { const char* key; uint64_t* dst; } need[] = {
-      {"embedding_length", &m->d}, {"feed_forward_length", &m->f}, {"block_count", &m->layers},
-      {"expert_count", &m->ne}, {"expert_used_count", &m->k}};
+      {"embedding_length", &m->d}, {"feed_forward_length", &m->f}, {"block_count", &m->layers}};
   for (auto& n : need)
     if (!arch_u64(g, n.key, n.dst)) return gfail(GMOE_ERR_MODEL, "gguf is missing %s.%s", arch, n.key);
-  if (m->ne == 0) return gfail(GMOE_ERR_MODEL, "%s.expert_count is 0: a dense model has no MoE layers", arch);
+  // LlamaConfig::from_gguf (llama/mod.rs:462-463): absent expert counts are 0, a dense model
+  if (!arch_u64(g, "expert_count", &m->ne)) m->ne = 0;
+  if (!arch_u64(g, "expert_used_count", &m->k)) m->k = 0;
   if (m->d > UINT32_MAX || m->f > UINT32_MAX || m->ne > UINT32_MAX || m->k > UINT32_MAX)
     return gfail(GMOE_ERR_MODEL, "model dimensions do not fit in 32 bits");
   return GMOE_OK;
@@ -506,6 +507,52 @@ gmoe_status gmoe_gguf_find_tensor(const gmoe_gguf* g, const char* name, gmoe_ggu
   return GMOE_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Ffn::Dense (llama/mod.rs:608-613, :913-920): "a dense FFN is one expert spanning the
+// whole tensor". It is described as one expert, top-1, with a zero router: every gating
+// gives that expert weight 1 exactly (a softmax over one logit is 1, a renormalisation
+// divides by 1), so the combine adds y * 1 to zero and the layer's output is
+// expert_batch's, the dense arm's.
+gmoe_status dense_layer_desc(gmoe_gguf* g, const MoeDims& m, uint32_t layer, uint32_t math, gmoe_layer_desc* out) {
+  if (!find(g, blk(layer, "ffn_gate")))
+    return gfail(GMOE_ERR_MODEL,
+                 "layer %u has no feed-forward tensors (blk.%u.ffn_gate_exps, blk.%u.ffn_gate.0 or blk.%u.ffn_gate)",
+                 layer, layer, layer, layer);
+  auto bufs = std::make_unique<LayerBufs>();
+  bufs->router.assign(m.d, 0.0f);
+  gmoe_layer_desc D{};
+  D.d_model = (uint32_t)m.d;
+  D.d_ff = (uint32_t)m.f;
+  D.n_experts = 1;
+  D.top_k = 1;
+  D.gating = GMOE_GATING_LLAMA;
+  D.combine = GMOE_COMBINE_EXPERT_ORDER;
+  D.math = math;
+  D.router = bufs->router.data();
+  const char* base[3] = {"ffn_gate", "ffn_up", "ffn_down"};
+  const uint64_t rows[3] = {m.f, m.f, m.d}, cols[3] = {m.d, m.d, m.f};
+  gmoe_tensor* dst[3] = {&D.gate, &D.up, &D.down};
+  for (int w = 0; w < 3; w++) {
+    const Tensor* t;
+    uint64_t st;
+    if (gmoe_status s = weight(g, blk(layer, base[w]), rows[w], cols[w], &t, &st)) return s;
+    dst[w]->qtype = t->type;
+    dst[w]->layout = GMOE_LAYOUT_STACKED;
+    dst[w]->data = g->bytes + st;
+    dst[w]->experts = nullptr;
+  }
+  g->descs.push_back(std::move(bufs));
+  *out = D;
+  return GMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 gmoe_status gmoe_gguf_layer_desc(gmoe_gguf* g, uint32_t layer, uint32_t gating, uint32_t combine, uint32_t math,
                                  gmoe_layer_desc* out) {
   if (!g || !out) return gfail(GMOE_ERR_INFERENCE, "null handle or output");
@@ -514,10 +561,10 @@ gmoe_status gmoe_gguf_layer_desc(gmoe_gguf* g, uint32_t layer, uint32_t gating, 
   if (s != GMOE_OK) return s;
   if (layer >= m.layers)
     return gfail(GMOE_ERR_INFERENCE, "layer %u of a %llu-layer model", layer, (unsigned long long)m.layers);
-  const bool stacked = stacked_layer(g, layer);
-  if (!stacked && !split_layer(g, layer))
-    return gfail(GMOE_ERR_MODEL, "layer %u has no expert tensors (blk.%u.ffn_gate_exps or blk.%u.ffn_gate.0)", layer,
-                 layer, layer);
+  // llama/mod.rs:590-613: MoE when the model declares experts and the block has the
+  // stacked or the split expert tensors, else a dense FFN
+  const bool stacked = m.ne > 0 && stacked_layer(g, layer);
+  if (!stacked && !(m.ne > 0 && split_layer(g, layer))) return dense_layer_desc(g, m, layer, math, out);
   auto bufs = std::make_unique<LayerBufs>();
   gmoe_layer_desc D{};
   D.d_model = (uint32_t)m.d;

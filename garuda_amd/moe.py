@@ -300,7 +300,9 @@ class MoeLayer:
                   combine: int = COMBINE_EXPERT_ORDER, math: int = MATH_PACKED) -> "MoeLayer":
         """Layer `layer` of a GGUF checkpoint (garuda_amd.gguf.Gguf), registered straight
         from the file's bytes: the `Ffn::Moe` arm of LlamaBackend::from_gguf
-        (llama/mod.rs:569-607). The checkpoint stays open while this layer lives."""
+        (llama/mod.rs:569-607), or for a layer without expert tensors the `Ffn::Dense` arm
+        (:608-613) as one expert of weight 1, top-1. The checkpoint stays open while this
+        layer lives."""
         desc = GmoeLayerDesc()
         _check(lib().gmoe_gguf_layer_desc(gguf.handle, layer, gating, combine, math, C.byref(desc)))
         self = cls.__new__(cls)

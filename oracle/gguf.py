@@ -216,6 +216,8 @@ def moe_dims(g):
     for key in ("embedding_length", "feed_forward_length", "block_count", "expert_count", "expert_used_count"):
         v = g["metadata"].get(f"{arch[1]}.{key}")
         u = None if v is None else as_u64(v)
+        if u is None and key.startswith("expert"):
+            u = 0  # LlamaConfig::from_gguf, llama/mod.rs:462-463: absent counts are 0
         if u is None:
             raise _bad(f"gguf is missing {arch[1]}.{key}")
         out[key] = u
@@ -224,15 +226,25 @@ def moe_dims(g):
 
 
 def layer(g, file_len: int, l: int) -> dict:
-    """The MoE tensors of layer l (llama/mod.rs:569-607): {router: (type, start, nbytes),
-    layout: 'stacked'|'split', gate/up/down: (type, [start per expert], bytes per expert)}."""
+    """The feed-forward tensors of layer l (llama/mod.rs:569-613): {router: (type, start,
+    nbytes), layout: 'stacked'|'split', gate/up/down: (type, [start per expert], bytes per
+    expert)}; a dense FFN (Ffn::Dense) is layout 'dense', one expert, top-1, router None."""
     d, f, ne, k, nl = moe_dims(g)
     if l >= nl:
         raise _bad(f"layer {l} of a {nl}-layer model")
     p = lambda name: f"blk.{l}.{name}.weight"  # noqa: E731
     pe = lambda name, e: f"blk.{l}.{name}.{e}.weight"  # noqa: E731
-    out = {"d": d, "f": f, "ne": ne, "k": k, "router": _weight(g, file_len, p("ffn_gate_inp"), ne, d)}
     shapes = {"gate": ("ffn_gate", f, d), "up": ("ffn_up", f, d), "down": ("ffn_down", d, f)}
+    moe = ne > 0 and (_tensor(g, p("ffn_gate_exps")) is not None or _tensor(g, pe("ffn_gate", 0)) is not None)
+    if not moe:
+        if _tensor(g, p("ffn_gate")) is None:
+            raise _bad(f"layer {l} has no feed-forward tensors")
+        out = {"d": d, "f": f, "ne": 1, "k": 1, "router": None, "layout": "dense"}
+        for key, (base, rows, cols) in shapes.items():
+            t, start, nb = _weight(g, file_len, p(base), rows, cols)
+            out[key] = (t, [start], nb)
+        return out
+    out = {"d": d, "f": f, "ne": ne, "k": k, "router": _weight(g, file_len, p("ffn_gate_inp"), ne, d)}
     if ne > 0 and _tensor(g, p("ffn_gate_exps")) is not None:
         out["layout"] = "stacked"
         for key, (base, rows, cols) in shapes.items():

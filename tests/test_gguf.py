@@ -14,6 +14,7 @@ import pytest
 import garuda_amd as G
 from garuda_amd import gguf as gg
 from oracle import gguf as OG
+from oracle import oracle as O
 
 
 # ---- the reference test module's Builder (gguf/mod.rs:431-501), restated ----
@@ -424,7 +425,7 @@ def test_layer_desc_refusals():
         (moe_file(bad_elems="blk.0.ffn_down_exps.weight"), 0, "elements, expected"),
         (moe_file("split", split_types={(0, "ffn_up", 2): G.Q6_K}), 0, "one type per matrix"),
         (moe_file(), 2, "layer 2 of a 2-layer model"),
-        (moe_file(drop="blk.0.ffn_gate_exps.weight"), 0, "no expert tensors"),
+        (moe_file(drop="blk.0.ffn_gate_exps.weight"), 0, "no feed-forward tensors"),
         (moe_file(drop="blk.0.ffn_gate_inp.weight"), 0, "not found"),
     ]
     for data, layer, msg in cases:
@@ -465,3 +466,49 @@ def test_streamed_writer_matches(tmp_path):
     g = lib_parse(data)
     assert g.data_offset % 64 == 0 and all(t.offset % 64 == 0 for t in g.tensors)
     assert g.tensor("c").bytes().tobytes() == tensors[2][3].tobytes()
+
+
+# ---- dense feed-forward layers (Ffn::Dense, llama/mod.rs:590-613, :913-920) ----
+
+def dense_file(d=256, f=512, ne=4, with_counts=True, seed=1):
+    """Layer 0 MoE (stacked), layer 1 dense (blk.1.ffn_gate/up/down); with_counts False:
+    no expert counts at all, every layer dense."""
+    rng = np.random.default_rng(seed)
+    meta = [("general.architecture", gg.STRING, "llama"), ("llama.embedding_length", gg.U32, d),
+            ("llama.feed_forward_length", gg.U32, f), ("llama.block_count", gg.U32, 2)]
+    if with_counts:
+        meta += [("llama.expert_count", gg.U32, ne), ("llama.expert_used_count", gg.U32, 2)]
+    tensors = []
+    for l in range(2):
+        moe = with_counts and l == 0
+        if moe:
+            tensors.append((f"blk.{l}.ffn_gate_inp.weight", [d, ne], G.F32,
+                            rng.normal(0, 0.02, (ne, d)).astype(np.float32).tobytes()))
+        for base, rows, cols in (("ffn_gate", f, d), ("ffn_up", f, d), ("ffn_down", d, f)):
+            m = ne if moe else 1
+            raw = G.quantize(G.Q4_K, rng.normal(0, 0.02, m * rows * cols).astype(np.float32)).tobytes()
+            name = f"blk.{l}.{base}_exps.weight" if moe else f"blk.{l}.{base}.weight"
+            tensors.append((name, [cols, rows, ne] if moe else [cols, rows], G.Q4_K, raw))
+    return gg.write_gguf(meta, tensors)
+
+
+@pytest.mark.parametrize("with_counts", [True, False])
+def test_a_dense_layer_is_one_expert_of_weight_one(with_counts):
+    data = dense_file(with_counts=with_counts)
+    g = lib_parse(data)
+    base = g._keep.ctypes.data
+    o = OG.parse(data)
+    want = OG.layer(o, len(data), 1)
+    assert want["layout"] == "dense" and (want["ne"], want["k"]) == (1, 1) and want["router"] is None
+    desc = _desc(g, 1)
+    assert (desc.d_model, desc.d_ff, desc.n_experts, desc.top_k) == (256, 512, 1, 1)
+    assert not np.ctypeslib.as_array(desc.router, shape=(256,)).any()  # a zero router: weight 1 under any gating
+    for name in ("gate", "up", "down"):
+        t = getattr(desc, name)
+        qt, starts, per = want[name]
+        assert t.qtype == qt and t.layout == G.moe.LAYOUT_STACKED and t.data - base == starts[0]
+    if with_counts:
+        assert _desc(g, 0).n_experts == 4 and OG.layer(o, len(data), 0)["layout"] == "stacked"
+    for kind in range(4):  # every gating of a single logit gives weight 1 exactly
+        ids, w = O.gate(kind, np.array([0.0], np.float32), 1)
+        assert ids.tolist() == [0] and w.tolist() == [1.0]

@@ -107,3 +107,40 @@ def test_evicted_experts_restage_from_the_mapping(dev, tmp_path):
             assert np.array_equal(ids, ids2) and np.array_equal(bits(first), bits(again))
         finally:
             layer.release()
+
+
+def test_dense_ffn_layer_from_gguf_is_expert_batch(dev, tmp_path):
+    """Ffn::Dense (llama/mod.rs:913-920): `expert_batch` of the one dense expert over every
+    token, down(silu(gate h) * up h). A layer without expert tensors comes back from the
+    GGUF reader as one expert, top-1, zero router: weight 1, so the combine's y * 1 + 0 is
+    the dense arm's output. Checked against the oracle's quant::matmul chain written out
+    (packed) or simd::matmul over dequantised weights (f32)."""
+    from tests.test_gguf import dense_file
+    path = tmp_path / "dense.gguf"
+    path.write_bytes(dense_file())
+    data = path.read_bytes()
+    o = OG.layer(OG.parse(data), len(data), 1)
+    d, f = o["d"], o["f"]
+    w = {n: (o[n][0], np.frombuffer(data, np.uint8, o[n][2], o[n][1][0]).copy()) for n in ("gate", "up", "down")}
+    rng = np.random.default_rng(21)
+    with G.Gguf.open(path) as g:
+        for math in (G.MATH_PACKED, G.MATH_F32):
+            layer = G.MoeLayer.from_gguf(dev, g, 1, math=math)
+            try:
+                for n in (1, 6, 70):
+                    say(f"dense gguf layer math={math} n={n}")
+                    hs = rng.normal(0, 1, (n, d)).astype(np.float32)
+                    out, ids, wts = layer.feed_forward_batch(hs)
+                    assert not ids.any() and np.all(wts == 1.0)
+                    if math == G.MATH_PACKED:
+                        mm = lambda name, rows, cols, x: O.matmul(w[name][0], w[name][1], rows, cols, x, n, 8)  # noqa: E731
+                    else:
+                        deq = {k: O.dequantize(v[0], v[1], (f * d)) for k, v in w.items()}
+                        mm = lambda name, rows, cols, x: O.simd_matmul(deq[name], rows, cols, x, n, 8)  # noqa: E731
+                    gt = mm("gate", f, d, hs)
+                    up = mm("up", f, d, hs)
+                    h = O.silu(gt) * up
+                    want = mm("down", d, f, h).reshape(n, d)
+                    assert np.allclose(out, want, rtol=RTOL, atol=ATOL), np.abs(out - want).max()
+            finally:
+                layer.release()
