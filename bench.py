@@ -468,28 +468,38 @@ def e2e_leg(a, threads, cpu):
     kv = KvCache(dev, nl, nh, nkv, hd, block_size=16, max_positions=max(2048, prompt + steps + 8), max_seqs=nseq,
                  rope_theta=1e6)
     pick = [l % copies for l in range(nl)]
+    # the token table kept packed (Q6_K rows, 107 MB instead of 524 MB of f32), a row
+    # dequantised per token
+    embd_raw = M.quantize(G.Q6_K, table.reshape(-1), threads)
     model = G.DecodeModel(dev, kv, [moe[c] for c in pick], *[[dense[nm][c] for c in pick] for nm in ("wq", "wk", "wv", "wo")],
                           head, np.stack([norms[2 * c] for c in pick]), np.stack([norms[2 * c + 1] for c in pick]),
-                          norms[-1], table)
+                          norms[-1], (G.Q6_K, embd_raw, vocab, d))
     seqs = [kv.open_seq() for _ in range(nseq)]
     toks = np.random.default_rng(seed & 0xffffffff).integers(0, vocab, (nseq, prompt)).astype(np.uint32)
-    t0 = time.time()
-    for p in range(prompt):
-        nxt = model.decode_step(seqs, toks[:, p])
-    prompt_s = time.time() - t0
+    # the prompts through gmoe_model_prefill (forward_tail): one call a sequence, its 128
+    # tokens one chunk, every layer over the chunk at once (the MFMA/packed prefill paths)
+    model.prefill(seqs[0], toks[0, :8])  # warm-up (scratch sizing), on a sequence of its own
+    kv.close_seq(seqs[0])
+    seqs[0] = kv.open_seq()
+    t0 = time.perf_counter()
+    nxt = np.array([model.prefill(s, toks[i])[0] for i, s in enumerate(seqs)], np.uint32)
+    prompt_s = time.perf_counter() - t0
     t0 = time.perf_counter()
     for _ in range(steps):
         nxt = model.decode_step(seqs, nxt)
     dt = time.perf_counter() - t0
     tps = nseq * steps / dt
     log(f"c5 end to end: {tps:.0f} tok/s ({dt / steps * 1e3:.2f} ms per batch-{nseq} step of {nl} layers, "
-        f"contexts {prompt + 1}-{prompt + steps}); prompts fed in {prompt_s:.1f}s, weights made in {gen_s:.1f}s")
+        f"contexts {prompt + 1}-{prompt + steps}); prompts prefilled at {nseq * prompt / prompt_s:.0f} tok/s "
+        f"({prompt_s * 1e3 / nseq:.1f} ms per {prompt}-token prompt), weights made in {gen_s:.1f}s")
     res = {"workload": f"C5 end to end: {nl} Mixtral-shape layers (Q3_K gate/up, Q4_K down and attention "
-                       f"projections, Q6_K head, f32 token table, GQA 32/8 of 128, paged KV cache) cycling over "
-                       f"{copies} HBM copies of one synthetic layer; {nseq} sequences, {prompt}-token prompts fed "
-                       f"one token per step, then {steps} timed greedy decode steps",
+                       f"projections, Q6_K head, Q6_K token table kept packed, GQA 32/8 of 128, paged KV cache "
+                       f"with a 2048-position window) cycling over {copies} HBM copies of one synthetic layer; "
+                       f"{nseq} sequences, {prompt}-token prompts prefilled one sequence a call (chunks run "
+                       f"layer-major), then {steps} timed greedy decode steps of all {nseq}",
            "tokens_per_s": tps, "ms_per_step": dt / steps * 1e3, "layers": nl, "sequences": nseq,
-           "prompt": prompt, "steps": steps, "cpu": None}
+           "prompt": prompt, "steps": steps, "prefill_tokens_per_s": nseq * prompt / prompt_s,
+           "prefill_ms_per_prompt": prompt_s * 1e3 / nseq, "cpu": None}
     model.close()
     kv.close()
     for ws in dense.values():

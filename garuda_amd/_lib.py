@@ -132,6 +132,7 @@ SIGNATURES = {
     "gmoe_model_create": (i32, [vp, vp, C.POINTER(vp)]),
     "gmoe_model_destroy": (None, [vp]),
     "gmoe_model_decode": (i32, [vp, u32, u32p, u32p, u32p, f32p]),
+    "gmoe_model_prefill": (i32, [vp, u32, u32, u32p, u32, u32p, f32p]),
     "gmoe_model_trace_floats": (C.c_size_t, [vp, u32]),
     "gmoe_model_decode_trace": (i32, [vp, u32, u32p, u32p, u32p, f32p, f32p]),
     "gmoe_model_set_graphs": (i32, [vp, C.c_int]),

@@ -1117,6 +1117,17 @@ bool dense_shape(gmoe_ctx* c, uint32_t id, uint32_t* rows, uint32_t* cols) {
   return true;
 }
 
+// The tiled bytes of a dense weight and its type (a model's packed token table reads its
+// rows from them).
+bool dense_tiled(gmoe_ctx* c, uint32_t id, const uint8_t** tiled, uint32_t* qtype) {
+  CtxLock g(c);
+  Dense* W;
+  if (get_dense(c, id, &W) != GMOE_OK) return false;
+  *tiled = W->tiled;
+  *qtype = W->qtype;
+  return true;
+}
+
 bool layer_width(gmoe_ctx* c, uint32_t id, uint32_t* d, uint32_t* ne) {
   CtxLock g(c);
   Layer* L;

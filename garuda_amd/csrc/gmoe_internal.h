@@ -370,6 +370,12 @@ struct GlueTokens {
 };
 hipError_t launch_embed(const GlueTokens& tk, uint32_t n, const float* table, uint32_t d, float* x, hipStream_t st);
 hipError_t launch_embed_dev(const uint32_t* tok, uint32_t n, const float* table, uint32_t d, float* x, hipStream_t st);
+// rows of a tiled dense weight of type qtype, dequantised (tokens from tk, or dtok when tk is null)
+template <int QT>
+hipError_t units_embed(const uint8_t* tiled, uint32_t cols, const GlueTokens* tk, const uint32_t* dtok, uint32_t n,
+                       float* x, hipStream_t st);
+hipError_t launch_embed_tiled(uint32_t qtype, const uint8_t* tiled, uint32_t cols, const GlueTokens* tk,
+                              const uint32_t* dtok, uint32_t n, float* x, hipStream_t st);
 hipError_t launch_add_norm(float* x, const float* y, const float* w, uint32_t n, uint32_t d, float eps, float* h,
                            hipStream_t st);
 // the same with y the sum of nsl K slices [nsl][n][d] of a dense product (k_reduce_parts's sum)

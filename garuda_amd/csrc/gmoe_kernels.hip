@@ -1627,6 +1627,16 @@ hipError_t launch_down_atomic(const LayerDev& L, const FwdBufs& B, uint32_t n, h
   return hipErrorInvalidValue;
 }
 
+hipError_t launch_embed_tiled(uint32_t qtype, const uint8_t* tiled, uint32_t cols, const GlueTokens* tk,
+                              const uint32_t* dtok, uint32_t n, float* x, hipStream_t st) {
+  switch (qtype) {
+#define EM(T) case T: return units_embed<T>(tiled, cols, tk, dtok, n, x, st);
+    EM(Q4_K) EM(Q5_K) EM(Q6_K) EM(Q3_K) EM(Q2_K) EM(Q8_0) EM(Q4_0) EM(F16) EM(F32)
+#undef EM
+  }
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st, uint32_t ksg_in) {
   const uint32_t ksg = ksg_in ? ksg_in : down_ksg(L, n * L.k);
   switch (L.qt_down) {

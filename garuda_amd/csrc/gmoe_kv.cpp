@@ -270,6 +270,27 @@ gmoe_status kv_check_step(gmoe_kv* kv, const uint32_t* seqs, uint32_t n) {
   return GMOE_OK;
 }
 
+// A prefill of n positions of one sequence (forward_tail, llama/mod.rs:1058-1066): the
+// window and the pool checked for every layer before any layer runs.
+gmoe_status kv_check_prefill(gmoe_kv* kv, uint32_t seq, uint32_t n) {
+  std::lock_guard<std::mutex> g(kv->mu);
+  const gmoe_kv_desc& D = kv->d;
+  if (seq >= kv->seqs.size() || !kv->seqs[seq].open) return kfail(GMOE_ERR_INFERENCE, "sequence %u is not open", seq);
+  uint64_t pages = 0;
+  for (uint32_t l = 0; l < D.n_layers; l++) {
+    const uint32_t len = kv->seqs[seq].len[l];
+    if ((uint64_t)len + n > D.max_positions)
+      return kfail(GMOE_ERR_CACHE, "%u tokens do not fit the %u-position context window (%u used)", n,
+                   D.max_positions, len);
+    for (uint64_t p = len; p < (uint64_t)len + n; p++)
+      if (p % D.block_size == 0) pages++;
+  }
+  if (pages > kv->free_pages.size())
+    return kfail(GMOE_ERR_CACHE, "the KV pool has %zu free pages, the prefill needs %llu", kv->free_pages.size(),
+                 (unsigned long long)pages);
+  return GMOE_OK;
+}
+
 // For decode steps replayed from a HIP graph (gmoe_model.cpp): the host plans every
 // layer's entries (kv_plan_step), reserves the attention scratch, then commits them
 // (kv_commit_step) and copies them to device memory the graph's attention launches read

@@ -39,6 +39,8 @@ void kv_snapshot(gmoe_kv* kv, const uint32_t* seqs, uint32_t n, std::vector<uint
 void kv_restore(gmoe_kv* kv, const uint32_t* seqs, uint32_t n, const std::vector<uint32_t>& snap);
 gmoe_status ctx_pin_layers(gmoe_ctx* c, const uint32_t* layers, uint32_t n);
 void ctx_unpin_layers(gmoe_ctx* c, const uint32_t* layers, uint32_t n);
+bool dense_tiled(gmoe_ctx* c, uint32_t id, const uint8_t** tiled, uint32_t* qtype);
+gmoe_status kv_check_prefill(gmoe_kv* kv, uint32_t seq, uint32_t n);
 gmoe_status kv_attend_dev(gmoe_kv* kv, uint32_t n, const AttnEntry* d_ent, uint32_t nchunk, const float* q,
                           const float* k, const float* v, uint32_t q_stride, uint32_t kv_stride, float* out,
                           hipStream_t st, uint32_t nsl = 1, uint64_t sl_stride = 0);
@@ -68,7 +70,20 @@ struct gmoe_model {
   std::vector<uint32_t> wqkv;
   uint32_t out_id = 0;
   float* qkv = nullptr;
-  float* table = nullptr;  // [vocab][d] token embeddings
+  float* table = nullptr;  // [vocab][d] token embeddings (f32 rows)
+  // or the token table kept packed: a dense weight of the model's own, its rows dequantised
+  // per token (and, when the checkpoint ties them, the output head itself)
+  uint32_t embd_id = kNoDense;
+  const uint8_t* embd_tiled = nullptr;
+  uint32_t embd_qt = 0;
+  static constexpr uint32_t kNoDense = 0xFFFFFFFFu;
+  // prompt chunks (gmoe_model_prefill): activations of up to kPrefillChunk tokens, the
+  // chunk's tokens (device, and their pinned staging), allocated on the first prefill
+  static constexpr uint32_t kPrefillChunk = 256;  // DEFAULT_PREFILL_CHUNK, llama/mod.rs:32
+  float *px = nullptr, *ph = nullptr, *pq = nullptr, *pk = nullptr, *pv = nullptr, *pqkv = nullptr, *pcx = nullptr,
+        *pao = nullptr, *py = nullptr;
+  uint32_t* ptok = nullptr;
+  uint32_t* pin_tok = nullptr;
   float* norms = nullptr;  // [2 n_layers + 1][d]: attn_norm, ffn_norm per layer, then output_norm
   // per-step activations for up to kModelMaxBatch tokens
   float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *cx = nullptr, *ao = nullptr,
@@ -110,10 +125,13 @@ struct gmoe_model {
     if (cap) hipStreamDestroy(cap);
     if (pin_par) hipHostFree(pin_par);
     for (uint32_t id : wqkv) gmoe_dense_release(ctx, id);
+    if (embd_id != kNoDense) gmoe_dense_release(ctx, embd_id);
     for (void* p : {(void*)table, (void*)norms, (void*)x, (void*)h, (void*)q, (void*)k, (void*)v, (void*)cx,
-                    (void*)ao, (void*)y, (void*)logits, (void*)next, (void*)qkv, (void*)par})
-      if (p) hipFree(p);
-    if (pin_next) hipHostFree(pin_next);
+                    (void*)ao, (void*)y, (void*)logits, (void*)next, (void*)qkv, (void*)par, (void*)px, (void*)ph,
+                    (void*)pq, (void*)pk, (void*)pv, (void*)pqkv, (void*)pcx, (void*)pao, (void*)py, (void*)ptok})
+      if (p) (void)hipFree(p);
+    if (pin_next) (void)hipHostFree(pin_next);
+    if (pin_tok) (void)hipHostFree(pin_tok);
   }
 };
 
@@ -169,7 +187,8 @@ gmoe_status gmoe_model_create(gmoe_ctx* ctx, const gmoe_model_desc* desc, gmoe_m
     return mfail(GMOE_ERR_CONFIG, "model dimensions must be positive, d_model a multiple of 4");
   if (D.d_model > 4u * 256u * kNormVec)
     return mfail(GMOE_ERR_CONFIG, "d_model %u is above the %u a norm workgroup holds", D.d_model, 4u * 256u * kNormVec);
-  if (D.token_embd_qtype != GMOE_F32) return mfail(GMOE_ERR_MODEL, "token embeddings must be F32 rows");
+  const bool tied = D.output == GMOE_OUTPUT_TIED;
+  if (tied && D.output_math > GMOE_MATH_F32) return mfail(GMOE_ERR_CONFIG, "unknown output_math %u", D.output_math);
   uint32_t kl, qd, kvd;
   kv_dims(D.kv, &kl, &qd, &kvd);
   if (kl != D.n_layers) return mfail(GMOE_ERR_INFERENCE, "the KV cache has %u layers, the model %u", kl, D.n_layers);
@@ -183,7 +202,7 @@ gmoe_status gmoe_model_create(gmoe_ctx* ctx, const gmoe_model_desc* desc, gmoe_m
     S_TRY(check_dense(ctx, D.wv[l], kvd, D.d_model, "wv", l));
     S_TRY(check_dense(ctx, D.wo[l], D.d_model, qd, "wo", l));
   }
-  S_TRY(check_dense(ctx, D.output, D.vocab, D.d_model, "output", D.n_layers));
+  if (!tied) S_TRY(check_dense(ctx, D.output, D.vocab, D.d_model, "output", D.n_layers));
   auto* m = new (std::nothrow) gmoe_model;
   if (!m) return mfail(GMOE_ERR_CONFIG, "out of host memory");
   m->ctx = ctx;
@@ -207,7 +226,24 @@ gmoe_status gmoe_model_create(gmoe_ctx* ctx, const gmoe_model_desc* desc, gmoe_m
   const hipError_t se = hipSetDevice(ctx_device(ctx));
   if (se != hipSuccess) return fail(mfail(GMOE_ERR_DEVICE, "hipSetDevice: %s", hipGetErrorString(se)));
   const size_t B = kModelMaxBatch, d = D.d_model;
-  const size_t table_bytes = (size_t)D.vocab * d * 4, norm_bytes = (2 * (size_t)D.n_layers + 1) * d * 4;
+  // the token table: f32 rows as they are; any other type, or a head tied to it, as a
+  // dense weight of the model's own (registered from the packed rows, which it copies)
+  const bool f32_table = D.token_embd_qtype == GMOE_F32 && !tied;
+  if (!f32_table) {
+    gmoe_dense_desc dd{};
+    dd.rows = D.vocab;
+    dd.cols = D.d_model;
+    dd.qtype = D.token_embd_qtype;
+    dd.math = tied ? D.output_math : GMOE_MATH_PACKED;
+    dd.data = D.token_embd;
+    uint32_t id;
+    if (gmoe_status s = gmoe_dense_register(ctx, &dd, &id)) return fail(s);
+    m->embd_id = id;
+    if (!dense_tiled(ctx, id, &m->embd_tiled, &m->embd_qt))
+      return fail(mfail(GMOE_ERR_INFERENCE, "token table registration lost"));
+    if (tied) m->out_id = id;
+  }
+  const size_t table_bytes = f32_table ? (size_t)D.vocab * d * 4 : 0, norm_bytes = (2 * (size_t)D.n_layers + 1) * d * 4;
   struct Alloc {
     void** p;
     size_t bytes;
@@ -220,13 +256,14 @@ gmoe_status gmoe_model_create(gmoe_ctx* ctx, const gmoe_model_desc* desc, gmoe_m
                 {(void**)&m->qkv, B * (qd + 2 * (size_t)kvd) * 4},
                 {(void**)&m->par, par_bytes(D.n_layers)}};
   for (auto& a : allocs) {
+    if (!a.bytes) continue;
     const hipError_t e = hipMalloc(a.p, a.bytes);
     if (e != hipSuccess) return fail(mfail(GMOE_ERR_CACHE, "device memory for the model: %s", hipGetErrorString(e)));
   }
   hipError_t e = hipHostMalloc((void**)&m->pin_next, B * 4, hipHostMallocDefault);
   if (e == hipSuccess) e = hipHostMalloc((void**)&m->pin_par, par_bytes(D.n_layers), hipHostMallocDefault);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&m->cap, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipMemcpy(m->table, D.token_embd, table_bytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess && table_bytes) e = hipMemcpy(m->table, D.token_embd, table_bytes, hipMemcpyHostToDevice);
   for (uint32_t l = 0; l < D.n_layers && e == hipSuccess; l++) {
     e = hipMemcpy(m->norms + (2 * (size_t)l) * d, D.attn_norm + (size_t)l * d, d * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess)
@@ -322,7 +359,10 @@ static gmoe_status step_launches(gmoe_model* m, uint32_t n, const uint32_t* seqs
     at += (size_t)n * width;
     return e;
   };
-  M_TRY(tk ? launch_embed(*tk, n, m->table, d, m->x, st) : launch_embed_dev(dtok, n, m->table, d, m->x, st));
+  if (m->embd_tiled)
+    M_TRY(launch_embed_tiled(m->embd_qt, m->embd_tiled, d, tk, tk ? nullptr : dtok, n, m->x, st));
+  else
+    M_TRY(tk ? launch_embed(*tk, n, m->table, d, m->x, st) : launch_embed_dev(dtok, n, m->table, d, m->x, st));
   for (uint32_t l = 0; l < m->n_layers; l++) {
     // h = norm(x + previous layer's MoE output, attn_norm)
     M_TRY(launch_add_norm(m->x, l ? m->y : nullptr, m->norms + (2 * (size_t)l) * d, n, d, m->eps, m->h, st));
@@ -505,5 +545,114 @@ static gmoe_status model_decode(gmoe_model* m, uint32_t n, const uint32_t* seqs,
   }
   ctx_unpin_layers(m->ctx, m->moe.data(), m->n_layers);
   if (s == GMOE_OK && capture) capture_step(m, n, cap_chunks);
+  return s;
+}
+
+// ---- prompt prefill: forward_tail (llama/mod.rs:1027-1116) ----
+
+namespace {
+
+gmoe_status ensure_prefill_buffers(gmoe_model* m) {
+  if (m->px) return GMOE_OK;
+  const size_t C = gmoe_model::kPrefillChunk, d = m->d;
+  struct Alloc {
+    void** p;
+    size_t bytes;
+  } allocs[] = {{(void**)&m->px, C * d * 4},        {(void**)&m->ph, C * d * 4},
+                {(void**)&m->pq, C * m->qd * 4},    {(void**)&m->pk, C * m->kvd * 4},
+                {(void**)&m->pv, C * m->kvd * 4},   {(void**)&m->pqkv, C * (m->qd + 2 * (size_t)m->kvd) * 4},
+                {(void**)&m->pcx, C * m->qd * 4},   {(void**)&m->pao, C * d * 4},
+                {(void**)&m->py, C * d * 4},        {(void**)&m->ptok, C * 4}};
+  for (auto& a : allocs) M_TRY(hipMalloc(a.p, a.bytes));
+  M_TRY(hipHostMalloc((void**)&m->pin_tok, C * 4, hipHostMallocDefault));
+  return GMOE_OK;
+}
+
+// One chunk of cn positions of sequence `seq`, layer-major (every layer over the chunk,
+// then the next): the launches of a decode step over the chunk's rows, attention taking
+// the chunk's positions as consecutive entries of the one sequence (each attending over
+// the positions before it and itself), then norm(x, output_norm) of every row into ph.
+gmoe_status chunk_launches(gmoe_model* m, uint32_t seq, uint32_t cn, hipStream_t st) {
+  const uint32_t d = m->d;
+  std::vector<uint32_t> seqs(cn, seq);
+  if (m->embd_tiled)
+    M_TRY(launch_embed_tiled(m->embd_qt, m->embd_tiled, d, nullptr, m->ptok, cn, m->px, st));
+  else
+    M_TRY(launch_embed_dev(m->ptok, cn, m->table, d, m->px, st));
+  for (uint32_t l = 0; l < m->n_layers; l++) {
+    M_TRY(launch_add_norm(m->px, l ? m->py : nullptr, m->norms + (2 * (size_t)l) * d, cn, d, m->eps, m->ph, st));
+    if (!m->wqkv.empty()) {
+      const uint32_t row = m->qd + 2 * m->kvd;
+      S_TRY(gmoe_dense_forward_async(m->ctx, m->wqkv[l], m->ph, cn, m->pqkv, st));
+      S_TRY(kv_attend(m->kv, l, seqs.data(), cn, m->pqkv, m->pqkv + m->qd, m->pqkv + m->qd + m->kvd, row, row,
+                      m->pcx, st));
+    } else {
+      S_TRY(gmoe_dense_forward_async(m->ctx, m->wq[l], m->ph, cn, m->pq, st));
+      S_TRY(gmoe_dense_forward_async(m->ctx, m->wk[l], m->ph, cn, m->pk, st));
+      S_TRY(gmoe_dense_forward_async(m->ctx, m->wv[l], m->ph, cn, m->pv, st));
+      S_TRY(kv_attend(m->kv, l, seqs.data(), cn, m->pq, m->pk, m->pv, m->qd, m->kvd, m->pcx, st));
+    }
+    S_TRY(gmoe_dense_forward_async(m->ctx, m->wo[l], m->pcx, cn, m->pao, st));
+    M_TRY(launch_add_norm(m->px, m->pao, m->norms + (2 * (size_t)l + 1) * d, cn, d, m->eps, m->ph, st));
+    S_TRY(gmoe_ffn_forward_async(m->ctx, m->moe[l], m->ph, nullptr, cn, m->py, nullptr, nullptr, st));
+  }
+  M_TRY(launch_add_norm(m->px, m->py, m->norms + 2 * (size_t)m->n_layers * d, cn, d, m->eps, m->ph, st));
+  return GMOE_OK;
+}
+
+gmoe_status prefill_body(gmoe_model* m, uint32_t seq, uint32_t n, const uint32_t* tokens, uint32_t n_last,
+                         uint32_t* next, float* logits) {
+  M_TRY(hipSetDevice(ctx_device(m->ctx)));
+  S_TRY(ensure_prefill_buffers(m));
+  hipStream_t st = ctx_stream(m->ctx);
+  // chunks of kPrefillChunk from the front; the last one holds at least n_last positions,
+  // whose normed states feed the head (forward_tail's `tail`)
+  const uint32_t C = gmoe_model::kPrefillChunk;
+  uint32_t lastc = n % C ? n % C : std::min(n, C);
+  if (lastc < n_last) lastc = n_last;
+  uint32_t cn = 0;
+  for (uint32_t c0 = 0; c0 < n; c0 += cn) {
+    const uint32_t rest = n - c0;
+    cn = rest == lastc ? lastc : std::min(C, rest - lastc);
+    M_TRY(hipStreamSynchronize(st));  // the pinned tokens of the previous chunk have been copied
+    std::memcpy(m->pin_tok, tokens + c0, (size_t)cn * 4);
+    M_TRY(hipMemcpyAsync(m->ptok, m->pin_tok, (size_t)cn * 4, hipMemcpyHostToDevice, st));
+    S_TRY(chunk_launches(m, seq, cn, st));
+  }
+  const float* tail = m->ph + (size_t)(cn - n_last) * m->d;
+  S_TRY(gmoe_dense_forward_async(m->ctx, m->out_id, tail, n_last, m->logits, st));
+  M_TRY(launch_argmax(m->logits, n_last, m->vocab, m->next, st));
+  M_TRY(hipMemcpyAsync(m->pin_next, m->next, n_last * 4, hipMemcpyDeviceToHost, st));
+  if (logits) M_TRY(hipMemcpyAsync(logits, m->logits, (size_t)n_last * m->vocab * 4, hipMemcpyDeviceToHost, st));
+  M_TRY(hipStreamSynchronize(st));
+  std::memcpy(next, m->pin_next, n_last * 4);
+  return GMOE_OK;
+}
+
+}  // namespace
+
+extern "C" gmoe_status gmoe_model_prefill(gmoe_model* m, uint32_t seq, uint32_t n, const uint32_t* tokens,
+                                          uint32_t n_last, uint32_t* next, float* logits) {
+  if (!m || !tokens || !next) return mfail(GMOE_ERR_INFERENCE, "null model, tokens or output");
+  if (n == 0) return mfail(GMOE_ERR_INFERENCE, "no new tokens to process for this context");
+  if (n_last == 0 || n_last > n || n_last > kModelMaxBatch)
+    return mfail(GMOE_ERR_INFERENCE, "asked for the last %u positions of %u (1 to %u)", n_last, n, kModelMaxBatch);
+  std::lock_guard<std::mutex> g(m->mu);
+  // refused before any layer runs: tokens outside the vocabulary, then the window and pool
+  for (uint32_t i = 0; i < n; i++)
+    if (tokens[i] >= m->vocab) {
+      set_invalid_token(tokens[i]);
+      return mfail(GMOE_ERR_INVALID_TOKEN, "token %u is outside the %u-entry vocabulary", tokens[i], m->vocab);
+    }
+  S_TRY(kv_check_prefill(m->kv, seq, n));
+  S_TRY(ctx_pin_layers(m->ctx, m->moe.data(), m->n_layers));
+  std::vector<uint32_t> snap;
+  kv_snapshot(m->kv, &seq, 1, snap);
+  const gmoe_status s = prefill_body(m, seq, n, tokens, n_last, next, logits);
+  if (s != GMOE_OK) {
+    (void)hipStreamSynchronize(ctx_stream(m->ctx));
+    kv_restore(m->kv, &seq, 1, snap);
+  }
+  ctx_unpin_layers(m->ctx, m->moe.data(), m->n_layers);
   return s;
 }

@@ -425,6 +425,50 @@ k_dn_atomic(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32
   }
 }
 
+// Token embeddings from a tiled dense weight (the token table kept packed): x[i] = row
+// tok[i] dequantised, Weight::row (llama/mod.rs:198-212) -> quant::dequantize, with the
+// same per-block arithmetic as every dequantiser here (bit for bit). Row t is lane t % 64
+// of tile t / 64; a thread takes one 32-value group of one unit (its unit's pieces are
+// read by every group of the unit, from L1 after the first). The tokens come from the
+// kernel arguments, or from device memory (dtok) in steps replayed from a graph.
+template <int QT>
+__global__ void __launch_bounds__(256) k_embed_tiled(const uint8_t* __restrict__ tiled, uint32_t cols, GlueTokens tk,
+                                                     const uint32_t* __restrict__ dtok, float* __restrict__ x) {
+  constexpr int U = UT_<QT>::U, NP = U / 16, NW = U / 4, EU = UT_<QT>::EU, G = UT_<QT>::G;
+  constexpr int NG = EU / 32, GPB = QT_<QT>::E / 32;
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const uint32_t i = blockIdx.x;
+  const uint32_t t = dtok ? dtok[i] : tk.tok[i];
+  const uint32_t nunit = unit_count<QT>(cols), nblk = unit_blocks<QT>(cols);
+  const uint8_t* row = tiled + (size_t)(t / kTileRows) * nunit * kTileRows * U + (t % kTileRows) * 16;
+  float* dst = x + (size_t)i * cols;
+  for (uint32_t j = threadIdx.x; j < nunit * NG; j += blockDim.x) {
+    const uint32_t u = j / NG, q = j % NG;
+    const uint32_t nvalid = G == 1 ? 1u : min((uint32_t)G, nblk - u * G);
+    if (G > 1 && q / GPB >= nvalid) continue;  // past the row's last block
+    uint32_t w[NW];
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(row + (size_t)u * NP * 1024 + p * 1024);
+      w[4 * p] = v.x; w[4 * p + 1] = v.y; w[4 * p + 2] = v.z; w[4 * p + 3] = v.w;
+    }
+    float v[32];
+    unit_deq32<QT>(w, (int)q, v);
+    float4* o = reinterpret_cast<float4*>(dst + (size_t)u * EU + 32 * q);
+#pragma unroll
+    for (int c = 0; c < 8; c++) o[c] = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
+  }
+}
+
+template <int QT>
+hipError_t units_embed(const uint8_t* tiled, uint32_t cols, const GlueTokens* tk, const uint32_t* dtok, uint32_t n,
+                       float* x, hipStream_t st) {
+  GlueTokens a{};
+  if (tk) a = *tk;
+  hipLaunchKernelGGL(k_embed_tiled<QT>, dim3(n), dim3(256), 0, st, tiled, cols, a, dtok, x);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------------
@@ -534,5 +578,7 @@ hipError_t units_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t 
 template hipError_t units_gateup<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, const RouteArgs&, hipStream_t);
 template hipError_t units_down<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, uint32_t, hipStream_t);
 template hipError_t units_down_atomic<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, hipStream_t);
+template hipError_t units_embed<GMOE_QT>(const uint8_t*, uint32_t, const GlueTokens*, const uint32_t*, uint32_t, float*,
+                                         hipStream_t);
 
 }  // namespace gmoe

@@ -25,7 +25,9 @@ class GmoeModelDesc(C.Structure):
                 ("wk", C.POINTER(C.c_uint32)), ("wv", C.POINTER(C.c_uint32)), ("wo", C.POINTER(C.c_uint32)),
                 ("output", C.c_uint32), ("attn_norm", C.POINTER(C.c_float)), ("ffn_norm", C.POINTER(C.c_float)),
                 ("output_norm", C.POINTER(C.c_float)), ("token_embd_qtype", C.c_uint32),
-                ("token_embd", C.POINTER(C.c_float))]
+                ("token_embd", C.c_void_p), ("output_math", C.c_uint32)]
+
+OUTPUT_TIED = 0xFFFFFFFF
 
 
 def _u32(a):
@@ -34,15 +36,23 @@ def _u32(a):
 
 class DecodeModel:
     """moe_layers / wq / wk / wv / wo: per layer, the registered MoeLayer and DenseWeight
-    objects; output: the head's DenseWeight; kv: a KvCache of n_layers layers;
-    attn_norm / ffn_norm: [n_layers, d]; output_norm: [d]; token_embd: [vocab, d] f32.
-    The objects must outlive the model (it keeps their ids, not copies)."""
+    objects; output: the head's DenseWeight, or None when the checkpoint ties the head to
+    the token table (llama/mod.rs:565-571; output_math then sets its arithmetic); kv: a
+    KvCache of n_layers layers; attn_norm / ffn_norm: [n_layers, d]; output_norm: [d];
+    token_embd: [vocab, d] f32, or (qtype, packed rows, vocab, d) to keep the table packed in
+    HBM, a row dequantised per token (Weight::row, llama/mod.rs:198-212). The objects must
+    outlive the model (it keeps their ids, not copies)."""
 
     def __init__(self, dev, kv, moe_layers, wq, wk, wv, wo, output, attn_norm, ffn_norm, output_norm, token_embd,
-                 rms_eps: float = 1e-5):
+                 rms_eps: float = 1e-5, output_math: int = 0):
         n_layers = len(moe_layers)
-        token_embd = np.ascontiguousarray(token_embd, dtype=np.float32)
-        vocab, d = token_embd.shape
+        if isinstance(token_embd, tuple):
+            embd_qt, raw, vocab, d = token_embd
+            table = np.ascontiguousarray(raw, dtype=np.uint8)
+        else:
+            table = np.ascontiguousarray(token_embd, dtype=np.float32)
+            embd_qt = 0
+            vocab, d = table.shape
         self.dev, self.kv, self.n_layers, self.d, self.vocab = dev, kv, n_layers, d, vocab
         self._keep = (moe_layers, wq, wk, wv, wo, output)
         ids = {name: _u32([o.id for o in objs]) for name, objs in
@@ -54,8 +64,8 @@ class DecodeModel:
         desc = GmoeModelDesc(n_layers, d, vocab, rms_eps, kv._h,
                              ids["moe"].ctypes.data_as(u32p), ids["wq"].ctypes.data_as(u32p),
                              ids["wk"].ctypes.data_as(u32p), ids["wv"].ctypes.data_as(u32p),
-                             ids["wo"].ctypes.data_as(u32p), output.id, _fp(an), _fp(fn), _fp(on), 0,
-                             _fp(token_embd))
+                             ids["wo"].ctypes.data_as(u32p), OUTPUT_TIED if output is None else output.id,
+                             _fp(an), _fp(fn), _fp(on), embd_qt, table.ctypes.data, output_math)
         h = C.c_void_p()
         _check(lib().gmoe_model_create(dev.handle, C.byref(desc), C.byref(h)))
         self._h = h
@@ -71,6 +81,19 @@ class DecodeModel:
         u32p = C.POINTER(C.c_uint32)
         _check(lib().gmoe_model_decode(self._h, n, seqs.ctypes.data_as(u32p), tokens.ctypes.data_as(u32p),
                                        nxt.ctypes.data_as(u32p), _fp(logits) if logits is not None else None))
+        return (nxt, logits) if want_logits else nxt
+
+    def prefill(self, seq: int, tokens, n_last: int = 1, want_logits: bool = False):
+        """A prompt through the model (gmoe_model_prefill, forward_tail + logits_multi):
+        the tokens take the sequence's next positions, in chunks of 256 run layer-major;
+        the greedy next token after each of the last n_last positions (and their [n_last,
+        vocab] logits if asked)."""
+        tokens = _u32(tokens)
+        nxt = np.zeros(n_last, dtype=np.uint32)
+        logits = np.empty((n_last, self.vocab), dtype=np.float32) if want_logits else None
+        u32p = C.POINTER(C.c_uint32)
+        _check(lib().gmoe_model_prefill(self._h, seq, tokens.size, tokens.ctypes.data_as(u32p), n_last,
+                                        nxt.ctypes.data_as(u32p), _fp(logits) if logits is not None else None))
         return (nxt, logits) if want_logits else nxt
 
     def set_graphs(self, enable: bool) -> None:

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GMOE_ABI_VERSION 5u
+#define GMOE_ABI_VERSION 6u
 
 /* Status codes. Mirrors the GarudaError variants the reference returns on this
  * path (garuda/src/core/mod.rs:10-47). */
@@ -466,13 +466,18 @@ typedef struct gmoe_model_desc {
   const uint32_t* wk;           /* [n_layers] kv_dim x d_model */
   const uint32_t* wv;           /* [n_layers] kv_dim x d_model */
   const uint32_t* wo;           /* [n_layers] d_model x q_dim */
-  uint32_t output;              /* dense id: vocab x d_model */
+  uint32_t output;              /* dense id: vocab x d_model, or GMOE_OUTPUT_TIED: the head is
+                                   token_embd itself (llama/mod.rs:565-571), under output_math */
   const float* attn_norm;       /* [n_layers][d_model] */
   const float* ffn_norm;        /* [n_layers][d_model] */
   const float* output_norm;     /* [d_model] */
-  uint32_t token_embd_qtype;    /* GMOE_F32 (rows of the table as f32) */
-  const float* token_embd;      /* [vocab][d_model] */
+  uint32_t token_embd_qtype;    /* ggml type id of the table's rows (any the slab takes) */
+  const void* token_embd;       /* [vocab] rows of d_model values, quant::byte_size each; copied.
+                                   F32 rows stay an f32 table; other types stay packed in HBM,
+                                   a row dequantised per token (Weight::row, llama/mod.rs:198-212) */
+  uint32_t output_math;         /* GMOE_MATH_* of a tied head */
 } gmoe_model_desc;
+#define GMOE_OUTPUT_TIED 0xFFFFFFFFu
 
 gmoe_status gmoe_model_create(gmoe_ctx* ctx, const gmoe_model_desc* desc, gmoe_model** out);
 void gmoe_model_destroy(gmoe_model* model);
@@ -486,6 +491,18 @@ void gmoe_model_destroy(gmoe_model* model);
  * the results are those of the launches issued one by one. */
 gmoe_status gmoe_model_decode(gmoe_model* model, uint32_t n, const uint32_t* seqs, const uint32_t* tokens,
                               uint32_t* next, float* logits);
+/* A prompt through the model: LlamaBackend::forward_tail + logits_multi
+ * (llama/mod.rs:1027-1116, :1223-1247) for sequence `seq`, whose n new tokens take its
+ * next positions. The tokens run in chunks of up to 256 (DEFAULT_PREFILL_CHUNK), each
+ * chunk layer-major: every layer over the whole chunk (its projections and MoE layer as
+ * batched products, the MFMA paths where the batch allows), its attention causal over the
+ * sequence. next[0..n_last) receive the greedy token after each of the last n_last
+ * positions and logits ([n_last x vocab], host) their logits when not NULL; 1 <= n_last <=
+ * min(n, 64). Refused before any layer runs when a token is outside the vocabulary, the
+ * window or pool cannot take the n positions, or an expert is not resident; a step that
+ * fails later leaves the sequence as it was. Synchronous. */
+gmoe_status gmoe_model_prefill(gmoe_model* model, uint32_t seq, uint32_t n, const uint32_t* tokens,
+                               uint32_t n_last, uint32_t* next, float* logits);
 /* No counterpart in the reference (the execution strategy of gmoe_model_decode):
  * enable != 0 replays decode steps from a graph (the default), 0 issues every launch of
  * every step. gmoe_model_graph_ready says whether a graph for batch size n is held. */

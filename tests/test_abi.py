@@ -27,7 +27,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     for s in syms:
         assert hasattr(lib, s), s
     assert set(syms) == set(_lib.SIGNATURES), "ctypes table and header disagree"
-    assert lib.gmoe_abi_version() == 5
+    assert lib.gmoe_abi_version() == 6
     assert lib.gmoe_last_invalid_token() == 0xFFFFFFFF  # none yet on this thread
 
 

@@ -23,6 +23,7 @@ import numpy as np
 import pytest
 
 import garuda_amd as G
+from garuda_amd import moe as M
 from garuda_amd.attention import KvCache
 from oracle import oracle as O
 from oracle.attention import KvOracle
@@ -392,5 +393,151 @@ def test_model_layers_are_kept_resident_during_a_step(dev, weights):
         say(f"{ok} of 30 steps ran; {held[0]} evictions refused while a step held the layer")
         assert not errs, errs
         assert ok > 0
+    finally:
+        release(*parts)
+
+
+def gpu_model_packed_table(dev, w, embd_qt, math, max_positions=64, tied=True):
+    """gpu_model with the token table kept packed (embd_qt rows) and, with tied, the head
+    taken from it (llama/mod.rs:565-571); returns the parts and the oracle's f32 table and
+    head."""
+    layers, out, onorm, embd, (nh, nkv, hd) = w
+    vocab, d = embd.shape
+    raw = M.quantize(embd_qt, embd.reshape(-1))
+    table = O.dequantize(embd_qt, raw, vocab * d).reshape(vocab, d)
+    kv = KvCache(dev, len(layers), nh, nkv, hd, block_size=16, max_positions=max_positions, max_seqs=4)
+    moe, dense = [], {n: [] for n in ("wq", "wk", "wv", "wo")}
+    for L in layers:
+        m = L["moe"]
+        moe.append(G.MoeLayer(dev, m["d"], m["f"], m["ne"], m["k"], m["router"], m["gate"], m["up"], m["down"],
+                              m["qtypes"], math=math))
+        for n in dense:
+            qt, r, rr, c = L[n]
+            dense[n].append(G.DenseWeight(dev, qt, rr, c, r, math))
+    qt, r, rr, c = out
+    head = None if tied else G.DenseWeight(dev, qt, rr, c, r, math)
+    model = G.DecodeModel(dev, kv, moe, dense["wq"], dense["wk"], dense["wv"], dense["wo"], head,
+                          np.stack([L["attn_norm"] for L in layers]), np.stack([L["ffn_norm"] for L in layers]),
+                          onorm, (embd_qt, raw, vocab, d), output_math=math)
+    ohead = (embd_qt, raw, vocab, d) if tied else out
+    return (model, kv, moe, dense, head), table, ohead
+
+
+@pytest.mark.parametrize("embd_qt", [G.Q6_K, G.Q8_0, G.Q4_K])
+def test_packed_token_table_with_tied_head(dev, weights, embd_qt):
+    """token_embd kept packed in HBM (Weight::Packed): each token's row is dequantised on the
+    device, bit for bit the reference's dequantize (the first layer's residual input is
+    compared bit for bit), and the head tied to the same table (has_tied_embeddings): f32
+    math end to end against the oracle's model over the same dequantised table and head."""
+    layers, out, onorm, embd, (nh, nkv, hd) = weights
+    parts, table, ohead = gpu_model_packed_table(dev, weights, embd_qt, G.MATH_F32)
+    model, kv = parts[0], parts[1]
+    try:
+        orc = ModelOracle(layers, ohead, onorm, table, nh, nkv, hd, max_positions=64, packed=False)
+        seqs = [kv.open_seq() for _ in range(2)]
+        toks = np.random.default_rng(31).integers(0, VOCAB, 2).astype(np.uint32)
+        ambiguous = set()
+        for step in range(8):
+            say(f"packed token table {embd_qt}, step {step}")
+            gn, gl, tr, _ = model.decode_step_trace(seqs, toks)
+            same_bits(f"step {step}: embedding rows", tr[0]["x"], table[toks])
+            on, ol = orc.decode_step(seqs, toks)
+            ambiguous |= {i for i, m in enumerate(orc.last_margins) if m < NEAR_TIE}
+            for i in range(2):
+                if i in ambiguous:
+                    continue
+                scale = float(np.abs(ol[i]).max())
+                assert float(np.abs(gl[i] - ol[i]).max()) <= 1e-3 * scale, (step, i)
+            toks = on
+        # graph-replayed steps read the tokens from device memory: same rows
+        for step in range(3):
+            nxt, lg = model.decode_step(seqs, toks, want_logits=True)
+            on, ol = orc.decode_step(seqs, toks)
+            for i in range(2):
+                if i not in ambiguous:
+                    assert float(np.abs(lg[i] - ol[i]).max()) <= 1e-3 * float(np.abs(ol[i]).max())
+            toks = on
+    finally:
+        _release_tied(*parts)
+
+
+def _release_tied(model, kv, moe, dense, head):
+    model.close()
+    for m in moe:
+        m.release()
+    for ws in dense.values():
+        for x in ws:
+            x.release()
+    if head is not None:
+        head.release()
+    kv.close()
+
+
+@pytest.fixture(scope="module")
+def wide_weights():
+    # d 512: the MoE layer, q, o and the head take the MFMA products at prefill sizes
+    return tiny_model(23, n_layers=2, d=512, nh=8, nkv=2, hd=64, f=512, ne=8, k=2, vocab=512)
+
+
+@pytest.mark.parametrize("n_prompt", [70, 300])
+def test_prefill_equals_the_prompt_token_by_token(dev, wide_weights, n_prompt):
+    """forward_tail (llama/mod.rs:1027-1116): a prompt through the model in chunks of up to
+    256 positions, layer-major (the projections and the MoE layer as batched products: the
+    MFMA paths at these sizes), against the oracle fed the same prompt one token per step
+    (the reference's layer-major and token-major passes are the same arithmetic). f32 math:
+    the last positions' logits within 1e-3 of their size, the same greedy tokens where the
+    top two are apart; the KV cache the prefill leaves is checked by decoding on from it."""
+    weights = wide_weights
+    layers, out, onorm, embd, (nh, nkv, hd) = weights
+    NL = len(layers)
+    VOCAB = embd.shape[0]
+    parts = gpu_model(dev, weights, max_positions=320, math=G.MATH_F32)
+    model, kv = parts[0], parts[1]
+    try:
+        orc = ModelOracle(layers, out, onorm, embd, nh, nkv, hd, max_positions=320, packed=False)
+        s = kv.open_seq()
+        prompt = np.random.default_rng(n_prompt).integers(0, VOCAB, n_prompt).astype(np.uint32)
+        say(f"prefill of {n_prompt} tokens")
+        gn, gl = model.prefill(s, prompt, n_last=3, want_logits=True)
+        assert all(kv.seq_len(s, l) == n_prompt for l in range(NL))
+        ol, margins = [], []
+        for t in prompt:
+            on, lo = orc.decode_step([s], [t])
+            ol.append(lo[0])
+            margins.append(orc.last_margins[0])
+        if min(margins) < NEAR_TIE:
+            pytest.skip("the oracle's router met a near-tie in this prompt")
+        for j in range(3):
+            want = ol[n_prompt - 3 + j]
+            scale = float(np.abs(want).max())
+            assert float(np.abs(gl[j] - want).max()) <= 1e-3 * scale, j
+            top = np.sort(want)[-2:]
+            if top[1] - top[0] > 4e-3 * scale:
+                assert gn[j] == int(np.argmax(want)), j
+        toks = np.array([on[0]], np.uint32)
+        for step in range(4):  # decoding on from the prefilled cache
+            gnd, gld = model.decode_step([s], toks, want_logits=True)
+            on, lo = orc.decode_step([s], toks)
+            assert float(np.abs(gld[0] - lo[0]).max()) <= 1e-3 * float(np.abs(lo[0]).max()), step
+            toks = np.array([on[0]], np.uint32)
+    finally:
+        release(*parts)
+
+
+def test_prefill_refusals_leave_the_sequence_unchanged(dev, weights):
+    parts = gpu_model(dev, weights, max_positions=40)
+    model, kv = parts[0], parts[1]
+    try:
+        s = kv.open_seq()
+        model.prefill(s, np.arange(10, dtype=np.uint32))
+        with pytest.raises(G.InvalidTokenError):
+            model.prefill(s, [1, 2, VOCAB])
+        with pytest.raises(G.CacheError):  # 10 + 31 positions exceed the window of 40
+            model.prefill(s, np.zeros(31, np.uint32))
+        with pytest.raises(G.InferenceError):
+            model.prefill(s, [1, 2], n_last=3)
+        assert all(kv.seq_len(s, l) == 10 for l in range(NL))
+        model.prefill(s, np.arange(30, dtype=np.uint32))
+        assert kv.seq_len(s, NL - 1) == 40
     finally:
         release(*parts)
