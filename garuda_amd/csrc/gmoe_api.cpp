@@ -1418,6 +1418,10 @@ gmoe_status gmoe_ffn_forward_noalloc(gmoe_ctx* c, uint32_t lid, const float* d_h
                 n, need, kNoAllocScratchBytes);
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+  // every call on this GPU shares the array: this one runs after the previous one's work
+  hipError_t oe;
+  auto order = noalloc_begin(c->device, st, &oe);
+  HIP_TRY(oe);
   const uint32_t per = call_tokens(*L);
   for (uint32_t t0 = 0; t0 < n; t0 += per) {
     const uint32_t m = std::min(per, n - t0);
@@ -1429,8 +1433,12 @@ gmoe_status gmoe_ffn_forward_noalloc(gmoe_ctx* c, uint32_t lid, const float* d_h
     B.out = d_out + (size_t)t0 * L->d;
     if (d_ids) B.ids = d_ids + (size_t)t0 * L->k;
     if (d_w) B.w = d_w + (size_t)t0 * L->k;
-    if (gmoe_status s = run_layer(c, *L, B, m, st, false)) return s;
+    if (gmoe_status s = run_layer(c, *L, B, m, st, false)) {
+      (void)noalloc_end(c->device, st);
+      return s;
+    }
   }
+  HIP_TRY(noalloc_end(c->device, st));
   return GMOE_OK;
 }
 

@@ -3,6 +3,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <mutex>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -222,6 +224,11 @@ struct LayerDev {
 constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
 // Its address on `device` (the current device), looked up once per device.
 hipError_t noalloc_scratch(int device, void** out);
+// Orders the calls that share a device's array: noalloc_begin waits (on st) for the previous
+// call's work and holds the device's lock until noalloc_end records this call's (neither
+// under graph capture).
+std::unique_lock<std::mutex> noalloc_begin(int device, hipStream_t st, hipError_t* err);
+hipError_t noalloc_end(int device, hipStream_t st);
 
 // The down product splits K over this many partial slices at most; FwdBufs::y holds
 // kMaxKsg slices of [n*k][d]. A down workgroup has kDnKS waves, each its own K range.

@@ -21,11 +21,12 @@
 // differs from the f32 reference by reordered f32 sums (~1e-6 relative).
 //
 // Work layout. The dispatch lists the call's token tiles (kPfTok = 64 tokens of one
-// expert, in slot order) in B.ptile; blockIdx.y is a token tile. Gate/up workgroups
-// take 128 rows of f (both matrices), down workgroups 256 rows of d. Each of the 4
-// waves owns two 32-row MFMA row tiles (gate and up of its 32 rows, or two 32-row
-// halves of its 64 down rows) and both 32-token tiles: 4 accumulators of 32x32, plus 4
-// of partial block sums. Per chunk of K (128 values, 64 for F16) the workgroup copies the
+// expert, in slot order) in B.ptile; blockIdx.y is a token tile. A workgroup has PF<QT>::NW
+// waves (8; 4 for Q6_K), each owning 32 rows: gate/up
+// workgroups take NW * 32 rows of f (both matrices: 256 for NW = 8), down workgroups NW *
+// 64 rows of d. Each wave owns two 32-row MFMA row tiles (gate and up of its 32 rows, or
+// two 32-row halves of its 64 down rows) and both 32-token tiles: 4 accumulators of 32x32,
+// plus 4 of partial block sums. Per chunk of K (128 values, 64 for F16) the workgroup copies the
 // chunk's raw 16-byte pieces of its rows (the slab's tiled layout makes each piece of 64
 // rows one 1 KiB run) and the tokens' hi/lo activations into LDS; a lane then decodes
 // its row's 8 values of each 16-value K step straight into the MFMA B operand.

@@ -159,9 +159,11 @@ gmoe_status gmoe_ffn_forward_async(gmoe_ctx* ctx, uint32_t layer_id, const float
  * A call whose scratch would exceed it is refused with GMOE_ERR_INFERENCE before any
  * device work (a Mixtral-shape layer, d 4096 / f 14336 / 8 experts, fits every batch of
  * up to 53 tokens; the 128-expert C4 layer fits 64). Every call on one GPU, from every
- * context, shares that array and leaves its contents behind: calls that overlap on one
- * GPU race, so order them on one stream. Same arguments and results as
- * gmoe_ffn_forward_async. */
+ * context and on every stream, shares that array: each call's stream waits (an event, no
+ * allocation) until the previous call on the GPU has finished with it, so calls never
+ * overlap on the array. A call made under stream capture does not take part in that
+ * ordering (its graph's launches are ordered by the caller): two graphs holding such calls
+ * must not run at the same time. Same arguments and results as gmoe_ffn_forward_async. */
 gmoe_status gmoe_ffn_forward_noalloc(gmoe_ctx* ctx, uint32_t layer_id, const float* d_hs,
                                      const float* d_logits, uint32_t n, float* d_out,
                                      uint32_t* d_routed_ids, float* d_routed_w, void* stream);
