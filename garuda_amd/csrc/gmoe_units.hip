@@ -280,7 +280,7 @@ k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __r
 // workgroup adds its waves' partial sums in wave order and writes them to its own
 // partial slice y[blockIdx.y]; the combine adds the slices in order.
 // grid.x = row tiles of d_model, grid.y = K groups, grid.z = active-expert slot.
-template <int QT, bool PACKED, int KS>
+template <int QT, bool PACKED, int KS, int RD = 2>
 __global__ void __launch_bounds__(64 * KS, 2)
 k_dn_units(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32_t d, uint32_t mt, uint32_t part_stride,
            const int8_t* __restrict__ hq, const float* __restrict__ hsc, const uint32_t* __restrict__ hsum,
@@ -306,7 +306,7 @@ k_dn_units(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32_
   const uint32_t per = ActLds<QT, PACKED>::per_token(nelem);
   float* y = ypart + (size_t)blockIdx.y * part_stride;
   float* my = accs + wave * mt * 64 + lane;
-  UnitStream<QT> st(W->w[2] + (size_t)blockIdx.x * nunit * kTileRows * U, u0, u1, lane);
+  UnitStream<QT, RD> st(W->w[2] + (size_t)blockIdx.x * nunit * kTileRows * U, u0, u1, lane);
   for (uint32_t c0 = 0; c0 < m_all; c0 += mt) {
     const uint32_t m = min(mt, m_all - c0);
     st.prime();  // the weights' first loads overlap the staging of the activations
@@ -341,7 +341,7 @@ k_dn_units(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32_
 // per (token, position), a candidate slot no routed pair names adding nothing and a
 // routed pair the candidates missed giving NaN, as the combine does.
 // grid.x = row tiles of d, grid.z = active-expert slot.
-template <int QT, bool PACKED, int KS>
+template <int QT, bool PACKED, int KS, int RD = 2>
 __global__ void __launch_bounds__(64 * KS, 2)
 k_dn_atomic(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32_t d, uint32_t mt,
             const uint32_t* __restrict__ slot_tok, const uint32_t* __restrict__ slot_of,
@@ -364,7 +364,7 @@ k_dn_atomic(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32
   const uint32_t u0 = (nunit * wave) / KS, u1 = (nunit * (wave + 1)) / KS;
   const uint32_t per = ActLds<QT, PACKED>::per_token(f);
   float* my = accs + wave * mt * 64 + lane;
-  UnitStream<QT> st(W->w[2] + (size_t)blockIdx.x * nunit * kTileRows * U, u0, u1, lane);
+  UnitStream<QT, RD> st(W->w[2] + (size_t)blockIdx.x * nunit * kTileRows * U, u0, u1, lane);
   for (uint32_t c0 = 0; c0 < m_all; c0 += mt) {
     const uint32_t m = min(mt, m_all - c0);
     st.prime();
@@ -476,7 +476,12 @@ hipError_t units_embed(const uint8_t* tiled, uint32_t cols, const GlueTokens* tk
 constexpr uint32_t kLdsBudget = 160 * 1024 - 2048;
 // Single-token calls stream gate/up with a ring of 4 unit sets: at one token the grid
 // has fewer waves than SIMDs, so the registers cost no occupancy, and on the C2 layer the
-// launch took 33.7 us instead of 35.4. At 2 or 4 tokens the deeper ring was slower.
+// launch took 33.7 us instead of 35.4 (a ring of 2) or 37.3 (a ring of 1). Calls of at
+// most one token an expert on average (n * k <= experts) take a ring of one set: 159
+// VGPRs instead of 209, three waves a SIMD, so that the grid (with those few tokens an
+// expert, chunks of LDS for six workgroups a CU) is resident in one round: C2 at batch 4
+// 88.6 -> 82.5 us. With more tokens an expert the ring of two stays (batch 8: 106.8 us
+// against 111.7-125 with a ring of one and chunks of 3-5 tokens).
 constexpr uint32_t kDeepRingTokens = 1;
 
 template <class K>
@@ -517,17 +522,29 @@ static hipError_t go_gu(const LayerDev& L, const FwdBufs& B, uint32_t n, const R
   return hipGetLastError();
 }
 
+template <int QT, bool PACKED, int RD>
+static hipError_t go_dn_rd(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
+
+// The K-sliced down product (and the dense projections it runs) streams through a ring of
+// one unit set, as the fused down does: C4 (Q8_0 down) 201 -> 189.6 us a call, the
+// attention projections at batch 8 64.3 -> 60.7 us, the 32000-row output head 55.0 ->
+// 52.9 us, against a ring of two on the same box.
 template <int QT, bool PACKED>
 static hipError_t go_dn(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st) {
+  return go_dn_rd<QT, PACKED, 1>(L, B, n, ksg, st);
+}
+
+template <int QT, bool PACKED, int RD>
+static hipError_t go_dn_rd(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st) {
   // a workgroup stages at most ceil(units / ksg) + 1 units
   const uint32_t span = min(((unit_count<QT>(L.f) + ksg - 1) / ksg + 1) * UT_<QT>::EU, L.f);
   const uint32_t per = kDnKS * 64 * 4 + ActLds<QT, PACKED>::per_token(span) + 4;
   const uint32_t mt = chunk_tokens(L, n, per + 16);
   if (mt == 0) return hipErrorInvalidValue;
-  static const bool once = allow_lds(k_dn_units<QT, PACKED, kDnKS>);
+  static const bool once = allow_lds(k_dn_units<QT, PACKED, kDnKS, RD>);
   (void)once;
   const dim3 g((L.d + kTileRows - 1) / kTileRows, ksg, min(L.ne, n * L.k));
-  hipLaunchKernelGGL((k_dn_units<QT, PACKED, kDnKS>), g, dim3(64 * kDnKS), mt * per + 16, st, B.work, L.ne, L.f, L.d, mt,
+  hipLaunchKernelGGL((k_dn_units<QT, PACKED, kDnKS, RD>), g, dim3(64 * kDnKS), mt * per + 16, st, B.work, L.ne, L.f, L.d, mt,
                      B.nslot * L.d, B.hq, B.hsc, B.hsum, B.hf, B.y);
   return hipGetLastError();
 }
@@ -536,19 +553,30 @@ constexpr int kDnAtomicKS = 8;
 
 static_assert(kFuseMaxTokens <= 64, "k_dn_atomic keeps a chunk's tokens one a lane");
 
-template <int QT, bool PACKED>
-static hipError_t go_dn_atomic(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+// The down product with the combine folded in streams its units through a ring of one set
+// (RD = 1): the loads of a unit are issued right after the previous unit's body. Measured
+// on the C2 layer against a ring of two: 22.6 -> 22.2 us at batch 1, 33.0 -> 31.8 at 2,
+// 48.4 -> 46.4 at 4, 57.6 -> 56.1 at 8, the C5 slice 175.1 -> 172.6 us. Its workgroups
+// carry 8 waves and the long K range of d_ff, so every SIMD holds several streams at once
+// and a deeper ring only lengthens the wait for each wave's next unit.
+template <int QT, bool PACKED, int RD>
+static hipError_t go_dn_atomic_rd(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
   if (L.k > 2 || n > kFuseMaxTokens) return hipErrorInvalidValue;
   const uint32_t per = kDnAtomicKS * 64 * 4 + ActLds<QT, PACKED>::per_token(L.f) + 4;
   const uint32_t mt = min(n, (kLdsBudget - 16) / per);
   if (mt == 0) return hipErrorInvalidValue;
-  static const bool once = allow_lds(k_dn_atomic<QT, PACKED, kDnAtomicKS>);
+  static const bool once = allow_lds(k_dn_atomic<QT, PACKED, kDnAtomicKS, RD>);
   (void)once;
   const dim3 g((L.d + kTileRows - 1) / kTileRows, 1, min(L.ne, n * L.k));
-  hipLaunchKernelGGL((k_dn_atomic<QT, PACKED, kDnAtomicKS>), g, dim3(64 * kDnAtomicKS), mt * per + 16, st, B.work,
+  hipLaunchKernelGGL((k_dn_atomic<QT, PACKED, kDnAtomicKS, RD>), g, dim3(64 * kDnAtomicKS), mt * per + 16, st, B.work,
                      L.ne, L.f, L.d, mt, B.slot_tok, B.slot_of, B.slot_w, L.k, B.spec, B.hq, B.hsc, B.hsum, B.hf,
                      B.out);
   return hipGetLastError();
+}
+
+template <int QT, bool PACKED>
+static hipError_t go_dn_atomic(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  return go_dn_atomic_rd<QT, PACKED, 1>(L, B, n, st);
 }
 
 template <int QT>
@@ -562,7 +590,11 @@ hipError_t units_down_atomic(const LayerDev& L, const FwdBufs& B, uint32_t n, hi
 template <int QT>
 hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
   if constexpr (has_int8_kernel(QT)) {
-    if (L.math == 0) return n <= kDeepRingTokens ? go_gu<QT, true, 4>(L, B, n, ra, st) : go_gu<QT, true, 2>(L, B, n, ra, st);
+    if (L.math == 0) {
+      if (n <= kDeepRingTokens) return go_gu<QT, true, 4>(L, B, n, ra, st);
+      if (n * L.k <= L.ne) return go_gu<QT, true, 1>(L, B, n, ra, st);
+      return go_gu<QT, true, 2>(L, B, n, ra, st);
+    }
   }
   return go_gu<QT, false, 2>(L, B, n, ra, st);
 }
