@@ -514,6 +514,18 @@ struct PkTok {
   const float* xs;
   const uint32_t* sm;
   float* acc;
+  // the block's i-th term (its sub-blocks in K order) is added to the running row sum
+  __device__ __forceinline__ void put(int, float v) const { *acc += v; }
+};
+
+// The same view whose terms are kept instead of added: term i goes to out[i * 64] (one
+// lane's column of a [term][64] array in LDS), to be added in K order later.
+struct PkTerms {
+  const int8_t* x;
+  const float* xs;
+  const uint32_t* sm;
+  float* out;
+  __device__ __forceinline__ void put(int i, float v) const { out[i * 64] = v; }
 };
 
 // The activation sums a packed dot reads: sum_kind_of / sum_offset_of (gmoe_internal.h).
@@ -539,7 +551,7 @@ __device__ __forceinline__ void pk_q4k(const uint32_t* w, uint32_t m, Tok tok) {
       hi[i] = (v >> 4) & 0x0f0f0f0fu;
     }
     for (uint32_t t = 0; t < m; t++) {
-      const PkTok a = tok(t);
+      const auto a = tok(t);
       const uint32_t* xa = reinterpret_cast<const uint32_t*>(a.x + 64 * c);
       int dl = 0, dh = 0;
 #pragma unroll
@@ -548,10 +560,8 @@ __device__ __forceinline__ void pk_q4k(const uint32_t* w, uint32_t m, Tok tok) {
         dh = sdot4(hi[i], xa[8 + i], dh);
       }
       const float s1 = __uint_as_float(a.sm[2 * c]), s2 = __uint_as_float(a.sm[2 * c + 1]);
-      float acc = *a.acc;
-      acc += a.xs[2 * c] * (d * (float)sc1 * (float)dl - dmin * (float)m1 * s1);
-      acc += a.xs[2 * c + 1] * (d * (float)sc2 * (float)dh - dmin * (float)m2 * s2);
-      *a.acc = acc;
+      a.put(2 * c, a.xs[2 * c] * (d * (float)sc1 * (float)dl - dmin * (float)m1 * s1));
+      a.put(2 * c + 1, a.xs[2 * c + 1] * (d * (float)sc2 * (float)dh - dmin * (float)m2 * s2));
     }
   }
 }
@@ -575,7 +585,7 @@ __device__ __forceinline__ void pk_q5k(const uint32_t* w, uint32_t m, Tok tok) {
       hi[i] = ((v >> 4) & 0x0f0f0f0fu) | (((h >> (2 * g + 1)) & 0x01010101u) << 4);
     }
     for (uint32_t t = 0; t < m; t++) {
-      const PkTok a = tok(t);
+      const auto a = tok(t);
       const uint32_t* xa = reinterpret_cast<const uint32_t*>(a.x + 64 * g);
       int dl = 0, dh = 0;
 #pragma unroll
@@ -584,10 +594,8 @@ __device__ __forceinline__ void pk_q5k(const uint32_t* w, uint32_t m, Tok tok) {
         dh = sdot4(hi[i], xa[8 + i], dh);
       }
       const float s1 = __uint_as_float(a.sm[2 * g]), s2 = __uint_as_float(a.sm[2 * g + 1]);
-      float acc = *a.acc;
-      acc += a.xs[2 * g] * (d * (float)sc1 * (float)dl - dmin * (float)m1 * s1);
-      acc += a.xs[2 * g + 1] * (d * (float)sc2 * (float)dh - dmin * (float)m2 * s2);
-      *a.acc = acc;
+      a.put(2 * g, a.xs[2 * g] * (d * (float)sc1 * (float)dl - dmin * (float)m1 * s1));
+      a.put(2 * g + 1, a.xs[2 * g + 1] * (d * (float)sc2 * (float)dh - dmin * (float)m2 * s2));
     }
   }
 }
@@ -611,12 +619,12 @@ __device__ __forceinline__ void pk_q6k(const uint32_t* w, uint32_t m, Tok tok) {
     }
     float sc = (float)(int8_t)byte_of(w, 192 + s);
     for (uint32_t t = 0; t < m; t++) {
-      const PkTok a = tok(t);
+      const auto a = tok(t);
       const uint32_t* xa = reinterpret_cast<const uint32_t*>(a.x + 16 * s);
       int dt = (int)a.sm[s];  // -32 * the sub-block's sum
 #pragma unroll
       for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
-      *a.acc += a.xs[s / 2] * d * sc * (float)dt;
+      a.put(s, a.xs[s / 2] * d * sc * (float)dt);
     }
   }
 }
@@ -640,12 +648,12 @@ __device__ __forceinline__ void pk_q3k(const uint32_t* w, uint32_t m, Tok tok) {
     }
     float dl = d_all * (float)((int)(int8_t)byte_of(sc4, s) - 32);
     for (uint32_t t = 0; t < m; t++) {
-      const PkTok a = tok(t);
+      const auto a = tok(t);
       const uint32_t* xa = reinterpret_cast<const uint32_t*>(a.x + 16 * s);
       int dt = (int)a.sm[s];  // -4 * the sub-block's sum
 #pragma unroll
       for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
-      *a.acc += a.xs[s / 2] * dl * (float)dt;
+      a.put(s, a.xs[s / 2] * dl * (float)dt);
     }
   }
 }
@@ -663,12 +671,12 @@ __device__ __forceinline__ void pk_q2k(const uint32_t* w, uint32_t m, Tok tok) {
     uint32_t sc = byte_of(w, s);
     float dl = d * (float)(sc & 15u), ml = dmin * (float)(sc >> 4);
     for (uint32_t t = 0; t < m; t++) {
-      const PkTok a = tok(t);
+      const auto a = tok(t);
       const uint32_t* xa = reinterpret_cast<const uint32_t*>(a.x + 16 * s);
       int dt = 0;
 #pragma unroll
       for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
-      *a.acc += a.xs[s / 2] * (dl * (float)dt - ml * __uint_as_float(a.sm[s]));
+      a.put(s, a.xs[s / 2] * (dl * (float)dt - ml * __uint_as_float(a.sm[s])));
     }
   }
 }
@@ -684,12 +692,12 @@ __device__ __forceinline__ void pk_q80_unit(const uint32_t* w, uint32_t nvalid, 
       const float ws = f16f(w[g / 2] >> (16 * (g % 2)));
       const uint32_t* q = w + 4 + 8 * g;
       for (uint32_t t = 0; t < m; t++) {
-        const PkTok a = tok(t);
+        const auto a = tok(t);
         const uint32_t* xa = reinterpret_cast<const uint32_t*>(a.x + 32 * g);
         int dt = 0;
 #pragma unroll
         for (int i = 0; i < 8; i++) dt = sdot4(q[i], xa[i], dt);
-        *a.acc += ws * a.xs[g] * (float)dt;
+        a.put(g, ws * a.xs[g] * (float)dt);
       }
     }
   }
@@ -886,6 +894,29 @@ __device__ void gate_wave(uint32_t gating, uint32_t ne, uint32_t k, float x, uin
 }
 
 
+// The combine's inputs of token t from its gating (id, w of lane < k): the pair's place in
+// the combine's order (among the token's k ids when the combine runs in expert order)
+// and its slot, found by binary search among the expert's candidate slots (~0u when the
+// candidates missed it).
+__device__ __forceinline__ void route_comb(const RouteArgs& r, uint32_t t, uint32_t id, float w, uint32_t lane) {
+  uint32_t pos = lane;
+  if (r.combine == 0) {
+    pos = 0;
+    for (uint32_t j = 0; j < r.k; j++) pos += lane_u(id, j) < id ? 1u : 0u;
+  }
+  if (lane < r.k) {
+    uint32_t lo = r.offsets[id], hi = r.offsets[id + 1];
+    const uint32_t end = hi;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) / 2;
+      if (r.slot_tok[mid] < t) lo = mid + 1;
+      else hi = mid;
+    }
+    r.comb_slot[(size_t)t * r.k + pos] = lo < end && r.slot_tok[lo] == t ? lo : ~0u;
+    r.comb_w[(size_t)t * r.k + pos] = w;
+  }
+}
+
 // ---------------------------------------------------------------------------------
 // Exact router logit of one (token, expert) pair by one workgroup of two or more waves,
 // then the token's gating by the last of its ne workgroups. Wave 1 puts the products w*h
@@ -962,25 +993,104 @@ __device__ __forceinline__ void route_logit(const RouteArgs& r, uint32_t x, floa
     r.ids[(size_t)t * r.k + lane] = id;
     r.w[(size_t)t * r.k + lane] = w;
   }
-  // the combine's order and slots: the pair's place among the token's k ids (experts are
-  // distinct), and its slot by search among the expert's candidate slots
-  uint32_t pos = lane;
-  if (r.combine == 0) {
-    pos = 0;
-    for (uint32_t j = 0; j < r.k; j++) pos += lane_u(id, j) < id ? 1u : 0u;
-  }
-  if (lane < r.k) {
-    uint32_t lo = r.offsets[id], hi = r.offsets[id + 1];
-    const uint32_t end = hi;
-    while (lo < hi) {
-      const uint32_t mid = (lo + hi) / 2;
-      if (r.slot_tok[mid] < t) lo = mid + 1;
-      else hi = mid;
-    }
-    r.comb_slot[(size_t)t * r.k + pos] = lo < end && r.slot_tok[lo] == t ? lo : ~0u;
-    r.comb_w[(size_t)t * r.k + pos] = w;
-  }
+  route_comb(r, t, id, w, lane);
   if (lane == 0) r.tok_done[t] = 0;
+}
+
+// ---------------------------------------------------------------------------------
+// Exact routing of one token by one workgroup of two or more waves: lane e of wave 0 runs
+// expert e's chain, the reference's sequential f32 dot from -0.0 (simd/mod.rs:13-16),
+// over the products w*h that the other waves put in LDS one section of d ahead (two
+// halves of [ne][sec + 4]); lane e reads its products 32 at a time from two register
+// buffers, each fetched one batch ahead. Then wave 0 gates the token (gate_wave), writes
+// its logits, ids and weights and the combine's (slot, weight) pairs, and bumps `routed`
+// (when given) after a release fence. sec: a multiple of 64 (d too), lds: route_token_lds floats.
+// Every thread of the workgroup calls this; ne <= 64.
+// ---------------------------------------------------------------------------------
+__host__ __device__ inline uint32_t route_token_lds(uint32_t ne, uint32_t k, uint32_t sec) {
+  return 2 * ne * (sec + 4) + 2 * k;
+}
+
+__device__ __forceinline__ void route_token(const RouteArgs& r, uint32_t t, float* lds, uint32_t sec,
+                                            uint32_t* routed) {
+  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, np = blockDim.x - 64;
+  const uint32_t ne = r.ne, d = r.d, row = sec + 4, nsec = (d + sec - 1) / sec;
+  float* prod = lds;  // [2][ne][row]
+  uint32_t* scratch = reinterpret_cast<uint32_t*>(lds + 2 * ne * row);
+  const float* hs = r.hs + (size_t)t * d;
+  constexpr int kItems = 4;  // float4 products a producer thread has in flight
+  auto produce = [&](uint32_t s) {
+    const uint32_t k0 = s * sec, len4 = min(sec, d - k0) / 4, total = ne * len4;
+    float* half = prod + (s & 1) * ne * row;
+    for (uint32_t base = tid - 64; base < total; base += np * kItems) {
+      float4 wv[kItems], xv[kItems];
+      uint32_t off[kItems];
+#pragma unroll
+      for (int i = 0; i < kItems; i++) {
+        const uint32_t q = base + np * i;
+        if (q < total) {
+          const uint32_t e = q / len4, j = q - e * len4;
+          wv[i] = reinterpret_cast<const float4*>(r.router + (size_t)e * d + k0)[j];
+          xv[i] = reinterpret_cast<const float4*>(hs + k0)[j];
+          off[i] = e * row + 4 * j;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kItems; i++)
+        if (base + np * i < total)
+          *reinterpret_cast<float4*>(half + off[i]) =
+              make_float4(wv[i].x * xv[i].x, wv[i].y * xv[i].y, wv[i].z * xv[i].z, wv[i].w * xv[i].w);
+    }
+  };
+  if (wave != 0) produce(0);
+  __syncthreads();
+  float acc = -0.0f;
+  for (uint32_t s = 0; s < nsec; s++) {
+    if (wave == 0) {
+      if (lane < ne) {
+        const uint32_t nb = min(sec, d - s * sec) / 32;  // even: sections and d are multiples of 64
+        const float4* src = reinterpret_cast<const float4*>(prod + (s & 1) * ne * row + lane * row);
+        float4 ba[8], bb[8];
+        auto fetch = [&](float4* dst, uint32_t b) {
+#pragma unroll
+          for (int u = 0; u < 8; u++) dst[u] = src[8 * b + u];
+        };
+        auto add = [&](const float4* v) {
+#pragma unroll
+          for (int u = 0; u < 8; u++) {
+            acc = acc + v[u].x;
+            acc = acc + v[u].y;
+            acc = acc + v[u].z;
+            acc = acc + v[u].w;
+          }
+        };
+        fetch(ba, 0);
+        for (uint32_t b = 0; b < nb; b += 2) {
+          fetch(bb, b + 1);
+          add(ba);
+          fetch(ba, min(b + 2, nb - 1));  // the last round re-reads a batch it does not add
+          add(bb);
+        }
+      }
+    } else if (s + 1 < nsec) {
+      produce(s + 1);
+    }
+    __syncthreads();
+  }
+  if (wave != 0) return;
+  if (lane < ne) r.logits[(size_t)t * ne + lane] = acc;
+  uint32_t id;
+  float w;
+  gate_wave(r.gating, ne, r.k, lane < ne ? acc : 0.0f, lane, &id, &w, scratch);
+  if (lane < r.k) {
+    r.ids[(size_t)t * r.k + lane] = id;
+    r.w[(size_t)t * r.k + lane] = w;
+  }
+  route_comb(r, t, id, w, lane);
+  if (routed) {
+    __threadfence();
+    if (lane == 0) atomicAdd(routed, 1u);
+  }
 }
 
 }  // namespace gmoe

@@ -276,6 +276,110 @@ k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __r
   }
 }
 
+// Terms a packed unit adds to a row's dot: one per sub-block (Q4_K, Q5_K: 8 of 32 values;
+// Q6_K, Q3_K, Q2_K: 16 of 16), or one per block of the eight-block Q8_0 units.
+template <int QT>
+__host__ __device__ constexpr uint32_t unit_terms() {
+  return (QT == Q4_K || QT == Q5_K || QT == Q8_0) ? 8u : 16u;
+}
+
+// Gate/up for single-token calls (decode batch 1): a workgroup of 8 waves takes one
+// 64-row tile, waves 0-3 the gate matrix and waves 4-7 the up matrix, each wave a quarter
+// of the K range. A wave holds a quarter of the units a one-wave stream would, so every
+// SIMD keeps several streams in flight and their arithmetic overlaps the loads (two
+// workgroups a CU). Bit-exact with k_gu_units: each wave writes its units' terms (pk_unit
+// with PkTerms, every term evaluated as the reference writes it) to LDS, and waves 0 and
+// 4 then add a row's terms in K order from 0.0, the reference's row dot
+// (quant/mod.rs:266-279); h = silu(g) * u is quantised per 32 rows by wave 0.
+// Measured on the C2 layer at one token: gate/up 33.9 -> 31.5 us a call. With two tokens
+// (both tokens' terms in LDS: one workgroup a CU) the same split took 67 us against 55.
+// With ra.n > 0 (speculative decode) the last row of the grid is the exact routing:
+// workgroup x < n routes token x (route_token), hidden under the expert tiles.
+// grid.x = row tiles of d_ff, grid.y = active-expert slot (+ the routing row).
+struct SplitArgs {
+  const ExpertWork* work;
+  const uint32_t* slot_tok;
+  const int8_t* xq;
+  const float* xs;
+  const uint32_t* xsum;
+  int8_t* hq;
+  float* hsc;
+  uint32_t* hsum;
+  uint32_t ne, d, f, rsec;
+  int hkind;
+  int32_t hoff;
+};
+constexpr uint32_t kSplitWaves = 8, kSplitParts = 4;
+
+template <int QT>
+__global__ void __launch_bounds__(64 * kSplitWaves, 4) k_gu_split(SplitArgs A, RouteArgs ra) {
+  constexpr int U = UT_<QT>::U, EU = UT_<QT>::EU;
+  constexpr uint32_t NT = unit_terms<QT>();
+  using Act = ActLds<QT, true>;
+  extern __shared__ uint4 dsm[];
+  float* lds = reinterpret_cast<float*>(dsm);
+  if (ra.n && blockIdx.y == gridDim.y - 1) {
+    if (blockIdx.x < ra.n) route_token(ra, blockIdx.x, lds, A.rsec, nullptr);
+    return;
+  }
+  const uint32_t r0 = blockIdx.x * kTileRows;
+  if (r0 >= A.f) return;  // (the routing row may widen the grid)
+  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const uint32_t mat = wave / kSplitParts, part = wave % kSplitParts;
+  const uint32_t nunit = unit_count<QT>(A.d), nterm = nunit * NT;
+  const uint32_t u0 = nunit * part / kSplitParts, u1 = nunit * (part + 1) / kSplitParts;
+  // LDS: terms [2 matrices][nterm][64], u's row sums [64], the token's row, and its staged
+  // activations
+  float* terms = lds;
+  float* usum = terms + (size_t)2 * nterm * 64;
+  uint32_t* rows = reinterpret_cast<uint32_t*>(usum + 64);
+  uint8_t* acts = reinterpret_cast<uint8_t*>(rows + 4);
+  // active experts y, y + ny, ... (the grid is sized for the usual count; rare extra
+  // candidates are taken by the same workgroups)
+  const uint32_t ny = gridDim.y - (ra.n ? 1 : 0);
+  for (uint32_t a = blockIdx.y; a < A.ne; a += ny) {
+  const ExpertWork* W = A.work + a;
+  const uint32_t m = W->m, s0 = W->s0;
+  if (m != 1) break;  // m = 0: past the last active expert (one token a call: m <= 1)
+  UnitStream<QT, 1> st(W->w[mat] + (size_t)blockIdx.x * nunit * kTileRows * U, u0, u1, lane);
+  st.prime();  // the weights' first loads overlap the staging of the activations
+  if (tid == 0) rows[0] = A.slot_tok[s0];
+  __syncthreads();
+  stage_acts<QT, true>(acts, A.d, 1u, rows, A.d, 0, A.xq, A.xs, A.xsum, nullptr);
+  __syncthreads();
+  st.run([&](uint32_t u, const uint32_t* w) {
+    const uint32_t off = u * EU;
+    const PkTerms a{reinterpret_cast<const int8_t*>(acts) + off, reinterpret_cast<const float*>(acts + Act::qb(A.d) + off / 8),
+                    reinterpret_cast<const uint32_t*>(acts + Act::qb(A.d) + Act::sb(A.d) + (Act::SW ? off / Act::SW * 4 : 0u)),
+                    terms + ((size_t)mat * nterm + u * NT) * 64 + lane};
+    pk_unit<QT>(w, 1u, 1u, [&](uint32_t) { return a; });
+  });
+  __syncthreads();
+  // waves 0 (gate) and 4 (up): the row dot, its terms added in K order
+  if (part == 0) {
+    const float* tv = terms + (size_t)mat * nterm * 64 + lane;
+    float acc = 0.0f;
+    for (uint32_t j0 = 0; j0 < nterm; j0 += 16) {  // 16 loads in flight, then their adds
+      float v[16];
+#pragma unroll
+      for (int i = 0; i < 16; i++) v[i] = tv[(j0 + i) * 64];
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc = acc + v[i];
+    }
+    if (mat == 1) usum[lane] = acc;
+    else terms[lane] = acc;  // g, over its own first term (read back below by this wave)
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const bool valid = r0 + (lane & 32) + 32 <= A.f;  // this lane's 32-row block lies inside d_ff
+    const float h = swiglu(terms[lane], usum[lane]);
+    quant_wave(h, lane, valid, A.hq + (size_t)s0 * A.f + r0, A.hsc + (size_t)s0 * (A.f / 32) + r0 / 32,
+               A.hkind ? A.hsum + (size_t)s0 * (A.f / sum_width(A.hkind)) : nullptr, r0, A.hkind, A.hoff);
+  }
+  __syncthreads();  // the LDS is the next expert's
+  }
+}
+
 // Down: the row's units are split over gridDim.y workgroups of KS waves each. A
 // workgroup adds its waves' partial sums in wave order and writes them to its own
 // partial slice y[blockIdx.y]; the combine adds the slices in order.
@@ -331,97 +435,117 @@ k_dn_units(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32_
   }
 }
 
+// The part of a chunk of a down tile with the combine folded in that follows its set-up
+// (stream primed, rows[] holding the chunk's slots, the lane's running sums zeroed, a
+// barrier): stages the chunk's h, streams the wave's units, adds the waves' row sums in
+// wave order and adds y * w into the zeroed output with an atomic add. A token's output
+// element then receives exactly k <= 2 terms; float addition is commutative, so 0 + p1 +
+// p2 is the same in either arrival order and the result is the combine's
+// (llama/mod.rs:974-997, moe/mod.rs:104-109) bit for bit, run to run. Weights: slot_w[slot],
+// or with spec set the exact routing's (slot, weight) per (token, position), a candidate
+// slot no routed pair names adding nothing and a routed pair the candidates missed giving
+// NaN, as the combine does.
+struct DnAtomicArgs {
+  uint32_t f, d, k, spec;
+  const uint32_t* slot_tok;
+  const uint32_t* slot_of;
+  const float* slot_w;
+  const int8_t* hq;
+  const float* hsc;
+  const uint32_t* hsum;
+  const float* hf;
+  float* out;
+};
+
+template <int QT, bool PACKED, int KS, class Stream>
+__device__ __forceinline__ void dn_atomic_chunk(Stream& st, const DnAtomicArgs& A, const float* accs, float* my,
+                                                const uint32_t* rows, uint8_t* acts, uint32_t mt, uint32_t m,
+                                                uint32_t slot0, uint32_t r0) {
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t nblk = unit_blocks<QT>(A.f), per = ActLds<QT, PACKED>::per_token(A.f);
+  stage_acts<QT, PACKED>(acts, A.f, m, rows, A.f, 0, A.hq, A.hsc, A.hsum, A.hf);
+  __syncthreads();
+  // wave 0, lane t < m: chunk member t's token and combine weight, loaded here so that
+  // their latency hides behind the stream (m <= kFuseMaxTokens <= 64, k <= 2). fl: 1 the
+  // slot is a routed pair's, 2 a routed pair of the token has no candidate slot (NaN).
+  uint32_t rtok = 0, rfl = 0;
+  float rwt = 0.0f;
+  if (wave == 0 && lane < m) {
+    const uint32_t slot = slot0 + lane;
+    rtok = A.slot_tok[slot];
+    if (A.spec) {
+      uint32_t sl[2];
+      float wv[2];
+#pragma unroll
+      for (uint32_t i = 0; i < 2; i++)
+        if (i < A.k) {
+          sl[i] = A.slot_of[(size_t)rtok * A.k + i];
+          wv[i] = A.slot_w[(size_t)rtok * A.k + i];
+        }
+#pragma unroll
+      for (uint32_t i = 0; i < 2; i++)
+        if (i < A.k) {
+          if (sl[i] == slot) {
+            rfl |= 1u;
+            rwt = wv[i];
+          }
+          if (sl[i] == ~0u) rfl |= 2u;
+        }
+    } else {
+      rfl = 1u;
+      rwt = A.slot_w[slot];
+    }
+  }
+  st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED>(w, acts, per, A.f, u, 0, nblk, my, m); });
+  __syncthreads();
+  if (wave == 0) {
+    const uint32_t row = r0 + lane;
+    for (uint32_t t = 0; t < m; t++) {
+      float y = accs[t * 64 + lane];
+#pragma unroll
+      for (int w2 = 1; w2 < KS; w2++) y += accs[(w2 * mt + t) * 64 + lane];
+      const uint32_t tok = lane_u(rtok, t), fl = lane_u(rfl, t);
+      const float wt = __uint_as_float(lane_u(__float_as_uint(rwt), t));
+      if (row < A.d) {
+        if (fl & 1u) atomicAdd(A.out + (size_t)tok * A.d + row, y * wt);
+        if (fl & 2u) atomicAdd(A.out + (size_t)tok * A.d + row, __int_as_float(0x7fc00000));
+      }
+    }
+  }
+  __syncthreads();
+}
+
 // Down with the combine folded in, for layers of top-k <= 2: a workgroup of KS waves takes
 // one 64-row tile of one expert over the whole K range (wave w its w-th share of the
-// units), adds the waves' row sums in wave order, and adds y * w into the zeroed output
-// with an atomic add. A token's output element then receives exactly k <= 2 terms; float
-// addition is commutative, so 0 + p1 + p2 is the same in either arrival order and the
-// result is the combine's (llama/mod.rs:974-997, moe/mod.rs:104-109) bit for bit, run
-// to run. Weights: slot_w[slot], or with spec set the exact routing's (slot, weight)
-// per (token, position), a candidate slot no routed pair names adding nothing and a
-// routed pair the candidates missed giving NaN, as the combine does.
+// units) and runs dn_atomic_chunk over its tokens.
 // grid.x = row tiles of d, grid.z = active-expert slot.
 template <int QT, bool PACKED, int KS, int RD = 2>
 __global__ void __launch_bounds__(64 * KS, 2)
-k_dn_atomic(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32_t d, uint32_t mt,
-            const uint32_t* __restrict__ slot_tok, const uint32_t* __restrict__ slot_of,
-            const float* __restrict__ slot_w, uint32_t k, uint32_t spec, const int8_t* __restrict__ hq,
-            const float* __restrict__ hsc, const uint32_t* __restrict__ hsum, const float* __restrict__ hf,
-            float* __restrict__ out) {
+k_dn_atomic(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t mt, DnAtomicArgs A) {
   constexpr int U = UT_<QT>::U;
   extern __shared__ uint4 dsm[];
   float* accs = reinterpret_cast<float*>(dsm);  // [KS][mt][64]
   uint32_t* rows = reinterpret_cast<uint32_t*>(accs + KS * mt * 64);  // [mt] slot of each chunk member
   uint8_t* acts = reinterpret_cast<uint8_t*>(rows + ((mt + 3) & ~3u));
   for (uint32_t a = blockIdx.z; a < ne; a += gridDim.z) {
-  const ExpertWork* W = work + a;
-  const uint32_t m_all = W->m;
-  if (m_all == 0) break;
-  const uint32_t s0 = W->s0;
-  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const uint32_t r0 = blockIdx.x * kTileRows;
-  const uint32_t nblk = unit_blocks<QT>(f), nunit = unit_count<QT>(f);
-  const uint32_t u0 = (nunit * wave) / KS, u1 = (nunit * (wave + 1)) / KS;
-  const uint32_t per = ActLds<QT, PACKED>::per_token(f);
-  float* my = accs + wave * mt * 64 + lane;
-  UnitStream<QT, RD> st(W->w[2] + (size_t)blockIdx.x * nunit * kTileRows * U, u0, u1, lane);
-  for (uint32_t c0 = 0; c0 < m_all; c0 += mt) {
-    const uint32_t m = min(mt, m_all - c0);
-    st.prime();
-    for (uint32_t t = threadIdx.x; t < m; t += blockDim.x) rows[t] = s0 + c0 + t;
-    for (uint32_t t = 0; t < m; t++) my[t * 64] = 0.0f;
-    __syncthreads();
-    stage_acts<QT, PACKED>(acts, f, m, rows, f, 0, hq, hsc, hsum, hf);
-    __syncthreads();
-    // wave 0, lane t < m: chunk member t's token and combine weight, loaded here so that
-    // their latency hides behind the stream (m <= kFuseMaxTokens <= 64, k <= 2). fl: 1 the
-    // slot is a routed pair's, 2 a routed pair of the token has no candidate slot (NaN).
-    uint32_t rtok = 0, rfl = 0;
-    float rwt = 0.0f;
-    if (wave == 0 && lane < m) {
-      const uint32_t slot = s0 + c0 + lane;
-      rtok = slot_tok[slot];
-      if (spec) {
-        uint32_t sl[2];
-        float wv[2];
-#pragma unroll
-        for (uint32_t i = 0; i < 2; i++)
-          if (i < k) {
-            sl[i] = slot_of[(size_t)rtok * k + i];
-            wv[i] = slot_w[(size_t)rtok * k + i];
-          }
-#pragma unroll
-        for (uint32_t i = 0; i < 2; i++)
-          if (i < k) {
-            if (sl[i] == slot) {
-              rfl |= 1u;
-              rwt = wv[i];
-            }
-            if (sl[i] == ~0u) rfl |= 2u;
-          }
-      } else {
-        rfl = 1u;
-        rwt = slot_w[slot];
-      }
+    const ExpertWork* W = work + a;
+    const uint32_t m_all = W->m;
+    if (m_all == 0) break;
+    const uint32_t s0 = W->s0;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t r0 = blockIdx.x * kTileRows;
+    const uint32_t nunit = unit_count<QT>(A.f);
+    const uint32_t u0 = (nunit * wave) / KS, u1 = (nunit * (wave + 1)) / KS;
+    float* my = accs + wave * mt * 64 + lane;
+    UnitStream<QT, RD> st(W->w[2] + (size_t)blockIdx.x * nunit * kTileRows * U, u0, u1, lane);
+    for (uint32_t c0 = 0; c0 < m_all; c0 += mt) {
+      const uint32_t m = min(mt, m_all - c0);
+      st.prime();
+      for (uint32_t t = threadIdx.x; t < m; t += blockDim.x) rows[t] = s0 + c0 + t;
+      for (uint32_t t = 0; t < m; t++) my[t * 64] = 0.0f;
+      __syncthreads();
+      dn_atomic_chunk<QT, PACKED, KS>(st, A, accs, my, rows, acts, mt, m, s0 + c0, r0);
     }
-    st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED>(w, acts, per, f, u, 0, nblk, my, m); });
-    __syncthreads();
-    if (wave == 0) {
-      const uint32_t row = r0 + lane;
-      for (uint32_t t = 0; t < m; t++) {
-        float y = accs[t * 64 + lane];
-#pragma unroll
-        for (int w2 = 1; w2 < KS; w2++) y += accs[(w2 * mt + t) * 64 + lane];
-        const uint32_t tok = lane_u(rtok, t), fl = lane_u(rfl, t);
-        const float wt = __uint_as_float(lane_u(__float_as_uint(rwt), t));
-        if (row < d) {
-          if (fl & 1u) atomicAdd(out + (size_t)tok * d + row, y * wt);
-          if (fl & 2u) atomicAdd(out + (size_t)tok * d + row, __int_as_float(0x7fc00000));
-        }
-      }
-    }
-    __syncthreads();
-  }
   }
 }
 
@@ -506,6 +630,48 @@ static uint32_t chunk_tokens(const LayerDev& L, uint32_t n, uint32_t per_token_b
   return min(min(n, usual), fit ? fit : kLdsBudget / per_token_bytes);
 }
 
+// The split gate/up (k_gu_split) serves packed math at one token a call for the K-quant
+// types, whose units are one block, when its LDS (every term of a row tile of both
+// matrices) fits.
+template <int QT>
+static uint32_t split_lds(const LayerDev& L, const RouteArgs& ra, uint32_t* rsec) {
+  const uint32_t nterm = unit_count<QT>(L.d) * unit_terms<QT>();
+  size_t lds = (size_t)2 * nterm * 64 * 4 + 64 * 4 + 16 + ActLds<QT, true>::per_token(L.d);
+  *rsec = 0;
+  if (ra.n) {  // route_token's sections: the longest multiple of 64 values whose halves take <= 64 KB
+    *rsec = min(L.d, ((64u * 1024u / (8u * L.ne)) - 4u) & ~63u);
+    lds = max(lds, (size_t)route_token_lds(L.ne, L.k, *rsec) * 4);
+  }
+  return lds <= kLdsBudget ? (uint32_t)lds : 0u;
+}
+
+template <int QT>
+static bool split_ok(const LayerDev& L, uint32_t n, const RouteArgs& ra) {
+  if constexpr (UT_<QT>::G != 1 || !has_int8_kernel(QT)) {
+    return false;
+  } else {
+    uint32_t rsec;
+    const uint32_t nterm = unit_count<QT>(L.d) * unit_terms<QT>();
+    return L.math == 0 && n == 1 && nterm % 16 == 0 && unit_count<QT>(L.d) >= kSplitParts &&
+           (!ra.n || (ra.n == n && L.ne <= 64 && L.d % 64 == 0)) && split_lds<QT>(L, ra, &rsec) != 0;
+  }
+}
+
+template <int QT>
+static hipError_t go_gu_split(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
+  uint32_t rsec = 0;
+  const uint32_t lds = split_lds<QT>(L, ra, &rsec);
+  if (lds == 0 || n != 1) return hipErrorInvalidValue;
+  static const bool once = allow_lds(k_gu_split<QT>);
+  (void)once;
+  const uint32_t tiles = (L.f + kTileRows - 1) / kTileRows;
+  const dim3 g(max(tiles, ra.n), min(L.ne, n * L.k) + (ra.n ? 1 : 0));
+  const SplitArgs A{B.work, B.slot_tok, B.xq, B.xs, B.xsum, B.hq, B.hsc, B.hsum, L.ne, L.d, L.f, rsec,
+                    sum_kind_of(L.qt_down), sum_offset_of(L.qt_down)};
+  hipLaunchKernelGGL((k_gu_split<QT>), g, dim3(64 * kSplitWaves), lds, st, A, ra);
+  return hipGetLastError();
+}
+
 template <int QT, bool PACKED, int D>
 static hipError_t go_gu(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
   const uint32_t per = 2 * 64 * 4 + ActLds<QT, PACKED>::per_token(L.d) + 4;
@@ -568,9 +734,9 @@ static hipError_t go_dn_atomic_rd(const LayerDev& L, const FwdBufs& B, uint32_t 
   static const bool once = allow_lds(k_dn_atomic<QT, PACKED, kDnAtomicKS, RD>);
   (void)once;
   const dim3 g((L.d + kTileRows - 1) / kTileRows, 1, min(L.ne, n * L.k));
+  const DnAtomicArgs A{L.f, L.d, L.k, B.spec, B.slot_tok, B.slot_of, B.slot_w, B.hq, B.hsc, B.hsum, B.hf, B.out};
   hipLaunchKernelGGL((k_dn_atomic<QT, PACKED, kDnAtomicKS, RD>), g, dim3(64 * kDnAtomicKS), mt * per + 16, st, B.work,
-                     L.ne, L.f, L.d, mt, B.slot_tok, B.slot_of, B.slot_w, L.k, B.spec, B.hq, B.hsc, B.hsum, B.hf,
-                     B.out);
+                     L.ne, mt, A);
   return hipGetLastError();
 }
 
@@ -591,6 +757,7 @@ template <int QT>
 hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
   if constexpr (has_int8_kernel(QT)) {
     if (L.math == 0) {
+      if (B.hq && split_ok<QT>(L, n, ra)) return go_gu_split<QT>(L, B, n, ra, st);
       if (n <= kDeepRingTokens) return go_gu<QT, true, 4>(L, B, n, ra, st);
       if (n * L.k <= L.ne) return go_gu<QT, true, 1>(L, B, n, ra, st);
       return go_gu<QT, true, 2>(L, B, n, ra, st);

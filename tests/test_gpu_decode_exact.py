@@ -62,3 +62,38 @@ def test_decode_gateup_is_bit_exact(dev, qt):
                                    f"{got.reshape(-1)[bad[0]]!r} vs {want.reshape(-1)[bad[0]]!r}")
     finally:
         layer.release()
+
+
+@pytest.mark.parametrize("qt", [G.Q4_K, G.Q5_K, G.Q6_K, G.Q3_K, G.Q2_K])
+@pytest.mark.parametrize("d", [2048, 1280])
+def test_split_gateup_is_bit_exact(dev, qt, d):
+    """Single-token calls with four or more units a row run the gate/up tile's K range
+    split over four waves a matrix (k_gu_split: terms kept, then added in K order); the
+    outputs stay bit-exact, also with parts of unequal length (d 1280: 5 units), and the
+    two-token calls between them (k_gu_units) too."""
+    f, ne, k = 512, 8, 2
+    rng = np.random.default_rng(190 + qt + d)
+    gate = M.quantize(qt, rng.normal(0, 0.05, ne * f * d).astype(np.float32))
+    up = M.quantize(qt, rng.normal(0, 0.05, ne * f * d).astype(np.float32))
+    down = onehot_down(rng, ne, d, f)
+    u = M.skew_direction(191 + qt, d)
+    router = M.skew_router(rng.normal(0, 0.02, ne * d).astype(np.float32), ne, d, u)
+    qts = (qt, qt, G.Q8_0)
+    layer = G.MoeLayer(dev, d, f, ne, k, router, gate, up, down, qts, math=G.MATH_PACKED)
+    L = dict(d=d, f=f, ne=ne, k=k, gating=0, combine=0, packed=1, router=router, qtypes=qts,
+             gate=gate, up=up, down=down)
+    try:
+        for n in (1, 2, 1, 2):
+            say(f"split gate/up bit-exact, type {qt}, d={d}, n={n}")
+            hs = M.skew_tokens(rng.normal(0, 1, (n, d)).astype(np.float32), u)
+            out, ids, w = layer.feed_forward_batch(hs)
+            wout, wids, ww = O.feed_forward_batch(L, hs, threads=min(16, len(os.sched_getaffinity(0))))
+            assert np.array_equal(ids, wids), "routing differs"
+            assert np.array_equal(bits(w), bits(ww)), "routing weights differ"
+            got = out.astype(np.float32)
+            want = np.asarray(wout, dtype=np.float32)
+            bad = np.flatnonzero(bits(got) != bits(want))
+            assert bad.size == 0, (f"n={n}: {bad.size} outputs differ, first at {bad[0]}: "
+                                   f"{got.reshape(-1)[bad[0]]!r} vs {want.reshape(-1)[bad[0]]!r}")
+    finally:
+        layer.release()
