@@ -689,7 +689,10 @@ gmoe_status run_layer(gmoe_ctx* c, Layer& L, FwdBufs B, uint32_t n, hipStream_t 
     ra.comb_slot = B.slot_of;  // unused by the speculative dispatch: the combine's slots
     ra.comb_w = B.slot_w;      // (n*k <= the n*ne candidate slots)
     ra.combine = D.combine;
-    HIP_TRY(launch_spec_front(D, B, n, quant ? 1 : 0, st));
+    // a single-token call whose gate/up can route for itself folds the front end into
+    // that launch; otherwise the front end runs first and dispatches
+    ra.self = n == 1 && !B.nx && B.hq && gateup_self_ok(D, n) ? 1u : 0u;
+    if (!ra.self) HIP_TRY(launch_spec_front(D, B, n, quant ? 1 : 0, st));
   } else if (front_small_ok(D, n)) {
     const bool split = n >= kFrontSplitTokens;
     HIP_TRY(launch_front_small(D, B, n, quant ? 1 : 0, !split, st));

@@ -1004,7 +1004,10 @@ __device__ __forceinline__ void route_logit(const RouteArgs& r, uint32_t x, floa
 // halves of [ne][sec + 4]); lane e reads its products 32 at a time from two register
 // buffers, each fetched one batch ahead. Then wave 0 gates the token (gate_wave), writes
 // its logits, ids and weights and the combine's (slot, weight) pairs, and bumps `routed`
-// (when given) after a release fence. sec: a multiple of 64 (d too), lds: route_token_lds floats.
+// (when given) after a release fence. With cand, the token's candidate experts in
+// ascending id (LDS, nc of them, one token a call), a routed pair's slot is its
+// expert's rank among them; otherwise the search of route_comb finds it. sec: a
+// multiple of 64 (d too), lds: route_token_lds floats.
 // Every thread of the workgroup calls this; ne <= 64.
 // ---------------------------------------------------------------------------------
 __host__ __device__ inline uint32_t route_token_lds(uint32_t ne, uint32_t k, uint32_t sec) {
@@ -1012,7 +1015,7 @@ __host__ __device__ inline uint32_t route_token_lds(uint32_t ne, uint32_t k, uin
 }
 
 __device__ __forceinline__ void route_token(const RouteArgs& r, uint32_t t, float* lds, uint32_t sec,
-                                            uint32_t* routed) {
+                                            uint32_t* routed, const uint32_t* cand = nullptr, uint32_t nc = 0) {
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, np = blockDim.x - 64;
   const uint32_t ne = r.ne, d = r.d, row = sec + 4, nsec = (d + sec - 1) / sec;
   float* prod = lds;  // [2][ne][row]
@@ -1086,11 +1089,149 @@ __device__ __forceinline__ void route_token(const RouteArgs& r, uint32_t t, floa
     r.ids[(size_t)t * r.k + lane] = id;
     r.w[(size_t)t * r.k + lane] = w;
   }
-  route_comb(r, t, id, w, lane);
+  if (cand) {  // one token, its candidates cand[0..nc) (LDS): a routed pair's slot is its rank
+    uint32_t p = lane;
+    if (r.combine == 0) {
+      p = 0;
+      for (uint32_t j = 0; j < r.k; j++) p += lane_u(id, j) < id ? 1u : 0u;
+    }
+    if (lane < r.k) {
+      uint32_t slot = ~0u;
+      for (uint32_t j = 0; j < nc; j++)
+        if (cand[j] == id) slot = j;
+      r.comb_slot[(size_t)t * r.k + p] = slot;
+      r.comb_w[(size_t)t * r.k + p] = w;
+    }
+  } else {
+    route_comb(r, t, id, w, lane);
+  }
   if (routed) {
     __threadfence();
     if (lane == 0) atomicAdd(routed, 1u);
   }
+}
+
+// ---------------------------------------------------------------------------------
+// Speculative routing (decode). The exact router logit is d dependent f32 adds
+// (simd/mod.rs:13-16); the expert products only need to know which experts to stream.
+//  * logit L~_e: the same rounded products w*h summed as d/64-long lane sums and a
+//    64-lane tree. With S the exact sum of the rounded products and A = sum |products|,
+//    recursive summation gives |L_seq - S| <= g(d-1) A and the tree |L~ - S| <= g(m) A,
+//    m = d/64 + 4 KB + 7 (every lane addition, zero padding included, and the 6 tree
+//    levels; KB float4 pairs a lane loads at a time), g(m) = m u / (1 - m u), u = 2^-24;
+//    so |L~ - L_seq| <= delta_e.
+//  * candidates: expert e is left out only when at least k others certainly rank before
+//    it, L~_j - delta_j > L~_e + delta_e + eps_e; eps_e keeps their probabilities apart
+//    after expf and the normalisation, so the exact order puts them first whatever the
+//    tie rule. Non-finite logits, or fewer than k experts safely above expf's underflow,
+//    make every expert a candidate. The exact top k is therefore a subset.
+// ---------------------------------------------------------------------------------
+constexpr uint32_t kSpecMaxExperts = 64;
+
+__device__ __forceinline__ double sum_gamma(double m) {
+  const double u = 0x1p-24;
+  return m * u / (1.0 - m * u);
+}
+
+// Wave w of the workgroup takes experts w, w + waves, ...: lt[e] = the products' tree sum,
+// la[e] = the sum of their magnitudes (LDS, written by lane 0). hs: the token's row. KB:
+// float4 pairs a lane has in flight.
+template <int KB>
+__device__ __forceinline__ void spec_dots(const float* __restrict__ router, const float* hs, uint32_t ne, uint32_t d,
+                                          float* lt, float* la) {
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+  const float4* xr = reinterpret_cast<const float4*>(hs);
+  const uint32_t n4 = d / 4;
+  for (uint32_t e = wave; e < ne; e += nw) {
+    const float4* wr = reinterpret_cast<const float4*>(router + (size_t)e * d);
+    float sm = 0.0f, ab = 0.0f;
+    for (uint32_t j0 = 0; j0 < n4; j0 += 64 * KB) {  // lane j: float4 columns j, j + 64, ...
+      float4 wv[KB], xv[KB];
+#pragma unroll
+      for (int i = 0; i < KB; i++) {
+        const uint32_t j = j0 + lane + 64 * i;
+        if (j < n4) {
+          wv[i] = wr[j];
+          xv[i] = xr[j];
+        } else {
+          wv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          xv[i] = wv[i];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < KB; i++) {
+        const float p0 = wv[i].x * xv[i].x, p1 = wv[i].y * xv[i].y, p2 = wv[i].z * xv[i].z, p3 = wv[i].w * xv[i].w;
+        sm = sm + p0; sm = sm + p1; sm = sm + p2; sm = sm + p3;
+        ab = ab + fabsf(p0); ab = ab + fabsf(p1); ab = ab + fabsf(p2); ab = ab + fabsf(p3);
+      }
+    }
+    sm = wave64_sum(sm);  // a tree of 6 levels, as the bound counts
+    ab = wave64_sum(ab);
+    if (lane == 0) {
+      lt[e] = sm;
+      la[e] = ab;
+    }
+  }
+}
+
+// One wave (lane e < ne: expert e), after lt/la are complete: the candidate test in
+// double. Returns the number of candidates nc; cl[0..nc) (LDS) holds them in ascending id,
+// *cand says whether this lane's expert is one and *pos its rank among them. sb: LDS of
+// 2 * kSpecMaxExperts doubles. KB: that of the spec_dots that made lt and la.
+template <int KB>
+__device__ __forceinline__ uint32_t spec_candidates(uint32_t ne, uint32_t k, uint32_t d, uint32_t gating, const float* lt,
+                                                    const float* la, double* sb, uint32_t* cl, uint32_t lane, bool* cand,
+                                                    uint32_t* pos) {
+  const double m_tree = (double)(d / 64 + 4 * KB + 7), m_seq = (double)d;
+  const bool valid = lane < ne;
+  const double Lt = valid ? (double)lt[lane] : 0.0;
+  const double A = valid ? (double)la[lane] / (1.0 - sum_gamma(m_tree)) : 0.0;
+  const double delta = (sum_gamma(m_seq) + sum_gamma(m_tree)) * A * (1.0 + 0x1p-20);
+  const bool fin = !valid || (isfinite(Lt) && isfinite(delta));
+  const double lo = Lt - delta, hi = Lt + delta;
+  // every lane reads every expert's bounds from LDS, eight at a time with their loads
+  // issued together (a shuffle per expert would wait out one LDS round trip each)
+  if (valid) {
+    sb[lane] = lo;
+    sb[kSpecMaxExperts + lane] = hi;
+  }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");  // one wave: its DS writes land before these reads
+  // f(j, lo_j, hi_j) for j = 0 .. ne-1 in order
+  auto each = [&](auto f) {
+    for (uint32_t j0 = 0; j0 < ne; j0 += 8) {
+      double l8[8], h8[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const uint32_t j = min(j0 + i, ne - 1);
+        l8[i] = sb[j];
+        h8[i] = sb[kSpecMaxExperts + j];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        if (j0 + i < ne) f(j0 + i, l8[i], h8[i]);
+    }
+  };
+  double maxhi = -INFINITY;
+  each([&](uint32_t, double, double hj) { maxhi = fmax(maxhi, hj); });
+  const bool all_fin = __ballot(!fin) == 0ull;
+  // experts certainly clear of expf's underflow relative to the largest logit
+  const uint32_t safe = (uint32_t)__popcll(__ballot(valid && lo - maxhi > -80.0));
+  const bool all = !all_fin || (gating != 1 && safe < k);
+  const double eps = 4e-6 * (1.0 + fabs(Lt) + fabs(maxhi));
+  uint32_t above = 0;
+  each([&](uint32_t j, double loj, double) {
+    if (j != lane && loj > hi + eps) above++;
+  });
+  const bool c = valid && (all || above < k);
+  const uint64_t cm = __ballot(c);
+  const uint32_t p = (uint32_t)__popcll(cm & ((1ull << lane) - 1ull)), nc = (uint32_t)__popcll(cm);
+  if (c) cl[p] = lane;
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");  // one wave: its DS writes land before these reads
+  *cand = c;
+  *pos = p;
+  return nc;
 }
 
 }  // namespace gmoe

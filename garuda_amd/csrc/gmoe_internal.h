@@ -206,6 +206,7 @@ struct RouteArgs {
   uint32_t* comb_slot;      // [n][k]
   float* comb_w;            // [n][k]
   uint32_t n, ne, k, d, gating, sec, combine;
+  uint32_t self;  // 1: the gate/up launch also does the front end's work (one token)
 };
 // Values of d per LDS half in route_logit. It shares its launch's LDS size with the expert
 // workgroups, so it is kept small (8 KB in all).
@@ -239,6 +240,9 @@ constexpr int kDnKS = 2;
 template <int QT> hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra,
                                           hipStream_t st);
 template <int QT> hipError_t units_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
+// Whether a gate/up launch of this type can fold the speculative front end in (one token,
+// RouteArgs::self; packed math with int8 h, the split gate/up's shapes).
+template <int QT> bool units_self_ok(const LayerDev& L, uint32_t n);
 // Down with the combine folded in (top-k <= 2, out zeroed by the front end beforehand).
 template <int QT> hipError_t units_down_atomic(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st);
 
@@ -301,6 +305,7 @@ constexpr uint32_t kSpecMaxSlots = 512;
 bool spec_ok(const LayerDev& L, uint32_t n);
 hipError_t launch_spec_front(const LayerDev& L, const FwdBufs& B, uint32_t n, int quant, hipStream_t st);
 hipError_t launch_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st);
+bool gateup_self_ok(const LayerDev& L, uint32_t n);
 // ksg = 0: down_ksg(L, n * L.k)
 hipError_t launch_down(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st, uint32_t ksg = 0);
 uint32_t dense_ksg(const LayerDev& L);

@@ -954,11 +954,8 @@ hipError_t launch_front_small(const LayerDev& L, const FwdBufs& B, uint32_t n, i
 // ---------------------------------------------------------------------------------
 
 constexpr int kSpecThreads = 512;
-
-__device__ __forceinline__ double sum_gamma(double m) {
-  const double u = 0x1p-24;
-  return m * u / (1.0 - m * u);
-}
+constexpr int kSpecFrontLoads = 16;  // float4 pairs a lane has in flight in a router dot
+static_assert(kFrontExperts == (int)kSpecMaxExperts, "one expert a lane in the candidate test");
 
 // NORM: the token's row of hs is made first, by the residual add and RMSNorm of
 // add_norm_row (FwdBufs::nx ...), written to nh and kept in LDS, from where the logits
@@ -977,7 +974,6 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
     __syncthreads();
   }
   const float* hs = NORM ? reinterpret_cast<const float*>(hrow) : B.hs + (size_t)t * d;
-  const float4* xr = reinterpret_cast<const float4*>(hs);
   // wave 0's slab pointers for the dispatch (lane e: expert e's gate, up, down), loaded
   // first; the output rows' zeroing and the quantiser's loads (threads of waves 1 on, the
   // activations of their 32-value block) follow the router dots' loads, whose results
@@ -987,39 +983,7 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
   const uint8_t* ep[3] = {nullptr, nullptr, nullptr};
   if (wave == 0 && lane < ne)
     for (int p = 0; p < 3; p++) ep[p] = L.eptr[p * ne + lane];
-  // wave w: experts w, w + 8, ...; lane j: float4 columns j, j + 64, ..., 16 loads in flight
-  constexpr int kB = 16;
-  const uint32_t n4 = d / 4;
-  for (uint32_t e = wave; e < ne; e += kSpecThreads / 64) {
-    const float4* wr = reinterpret_cast<const float4*>(L.router + (size_t)e * d);
-    float sm = 0.0f, ab = 0.0f;
-    for (uint32_t j0 = 0; j0 < n4; j0 += 64 * kB) {
-      float4 wv[kB], xv[kB];
-#pragma unroll
-      for (int i = 0; i < kB; i++) {
-        const uint32_t j = j0 + lane + 64 * i;
-        if (j < n4) {
-          wv[i] = wr[j];
-          xv[i] = xr[j];
-        } else {
-          wv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-          xv[i] = wv[i];
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < kB; i++) {
-        const float p0 = wv[i].x * xv[i].x, p1 = wv[i].y * xv[i].y, p2 = wv[i].z * xv[i].z, p3 = wv[i].w * xv[i].w;
-        sm = sm + p0; sm = sm + p1; sm = sm + p2; sm = sm + p3;
-        ab = ab + fabsf(p0); ab = ab + fabsf(p1); ab = ab + fabsf(p2); ab = ab + fabsf(p3);
-      }
-    }
-    sm = wave64_sum(sm);  // a tree of 6 levels, as the bound below counts
-    ab = wave64_sum(ab);
-    if (lane == 0) {
-      lt[e] = sm;
-      la[e] = ab;
-    }
-  }
+  spec_dots<kSpecFrontLoads>(L.router, hs, ne, d, lt, la);
   if (B.fuse_out)  // the down product adds into the token's output row
     for (uint32_t c = tid; c < d; c += kSpecThreads) B.out[(size_t)t * d + c] = 0.0f;
   const uint32_t nblk = d / 32, qb = tid - 64;  // block of thread tid >= 64
@@ -1054,56 +1018,10 @@ __global__ void __launch_bounds__(kSpecThreads) k_spec_front(LayerDev L, FwdBufs
     }
     return;
   }
-  // candidate test, lane e < ne, in double
-  // each product passes through at most d/64 + 4*kB lane additions (zero padding included)
-  // and 6 tree levels
-  const double m_tree = (double)(d / 64 + 4 * kB + 7), m_seq = (double)d;
+  bool cand;
+  uint32_t pos;
+  const uint32_t nc = spec_candidates<kSpecFrontLoads>(ne, k, d, L.gating, lt, la, sb, cl, lane, &cand, &pos);
   const bool valid = lane < ne;
-  const double Lt = valid ? (double)lt[lane] : 0.0;
-  const double A = valid ? (double)la[lane] / (1.0 - sum_gamma(m_tree)) : 0.0;
-  const double delta = (sum_gamma(m_seq) + sum_gamma(m_tree)) * A * (1.0 + 0x1p-20);
-  const bool fin = !valid || (isfinite(Lt) && isfinite(delta));
-  const double lo = Lt - delta, hi = Lt + delta;
-  // every lane reads every expert's bounds from LDS, eight at a time with their loads
-  // issued together (a shuffle per expert would wait out one LDS round trip each)
-  if (valid) {
-    sb[lane] = lo;
-    sb[kFrontExperts + lane] = hi;
-  }
-  __builtin_amdgcn_wave_barrier();
-  asm volatile("" ::: "memory");  // one wave: its DS writes land before these reads
-  // f(j, lo_j, hi_j) for j = 0 .. ne-1 in order
-  auto each = [&](auto f) {
-    for (uint32_t j0 = 0; j0 < ne; j0 += 8) {
-      double l8[8], h8[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const uint32_t j = min(j0 + i, ne - 1);
-        l8[i] = sb[j];
-        h8[i] = sb[kFrontExperts + j];
-      }
-#pragma unroll
-      for (int i = 0; i < 8; i++)
-        if (j0 + i < ne) f(j0 + i, l8[i], h8[i]);
-    }
-  };
-  double maxhi = -INFINITY;
-  each([&](uint32_t, double, double hj) { maxhi = fmax(maxhi, hj); });
-  const bool all_fin = __ballot(!fin) == 0ull;
-  // experts certainly clear of expf's underflow relative to the largest logit
-  const uint32_t safe = (uint32_t)__popcll(__ballot(valid && lo - maxhi > -80.0));
-  const bool all = !all_fin || (L.gating != 1 && safe < k);
-  const double eps = 4e-6 * (1.0 + fabs(Lt) + fabs(maxhi));
-  uint32_t above = 0;
-  each([&](uint32_t j, double loj, double) {
-    if (j != lane && loj > hi + eps) above++;
-  });
-  const bool cand = valid && (all || above < k);
-  const uint64_t cm = __ballot(cand);
-  const uint32_t pos = (uint32_t)__popcll(cm & ((1ull << lane) - 1ull)), nc = (uint32_t)__popcll(cm);
-  if (cand) cl[pos] = lane;
-  __builtin_amdgcn_wave_barrier();
-  asm volatile("" ::: "memory");  // one wave: its DS writes land before these reads
   const uint32_t my = lane < nc ? cl[lane] : ~0u;
   if (lane < ne) B.cand[(size_t)t * ne + lane] = my;
   if (n == 1) {
@@ -1398,6 +1316,15 @@ uint32_t down_ksg(const LayerDev& L, uint32_t pairs) {
   ksg = max(ksg, (1024 + wgs - 1) / wgs);
   const uint32_t cap = max(1u, row_units(un, L.f) / (kDnKS * 4));
   return max(1u, min(min(ksg, cap), kMaxKsg));
+}
+
+bool gateup_self_ok(const LayerDev& L, uint32_t n) {
+  switch (L.qt_gate) {
+#define SO(T) case T: return units_self_ok<T>(L, n);
+    SO(Q4_K) SO(Q5_K) SO(Q6_K) SO(Q3_K) SO(Q2_K) SO(Q8_0) SO(Q4_0) SO(F16) SO(F32)
+#undef SO
+  }
+  return false;
 }
 
 hipError_t launch_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {

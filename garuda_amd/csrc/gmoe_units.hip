@@ -295,7 +295,24 @@ __host__ __device__ constexpr uint32_t unit_terms() {
 // (both tokens' terms in LDS: one workgroup a CU) the same split took 67 us against 55.
 // With ra.n > 0 (speculative decode) the last row of the grid is the exact routing:
 // workgroup x < n routes token x (route_token), hidden under the expert tiles.
+// With SELF the call's front end is folded in: every workgroup computes the router's
+// parallel dots and the candidate test itself (spec_dots, spec_candidates, as the
+// speculative front end does), so it knows which candidate its slot streams without a
+// dispatch through memory, and quantises the token into LDS itself (stage_acts from the
+// f32 row: quant32's arithmetic, the front end's codes bit for bit). Workgroup x = 0 of
+// each slot writes that slot's work record and pair for the down product; the routing
+// workgroup zeroes the output the down product adds into and writes the dispatch
+// summary (active experts, offsets, empty work records past the candidates).
 // grid.x = row tiles of d_ff, grid.y = active-expert slot (+ the routing row).
+struct SelfArgs {
+  const uint8_t* const* eptr;  // [3][ne] tiled gate, up, down of each expert
+  ExpertWork* work;
+  uint32_t* slot_tok;
+  uint32_t* active;
+  uint32_t* offsets;
+  float* out;  // zeroed for the down product that adds into it, or null
+};
+
 struct SplitArgs {
   const ExpertWork* work;
   const uint32_t* slot_tok;
@@ -310,22 +327,67 @@ struct SplitArgs {
   int32_t hoff;
 };
 constexpr uint32_t kSplitWaves = 8, kSplitParts = 4;
+constexpr int kSplitLoads = 8;  // float4 pairs a lane has in flight in its router dots (SELF)
 
-template <int QT>
-__global__ void __launch_bounds__(64 * kSplitWaves, 4) k_gu_split(SplitArgs A, RouteArgs ra) {
+template <int QT, bool SELF>
+__global__ void __launch_bounds__(64 * kSplitWaves, 4) k_gu_split(SplitArgs A, RouteArgs ra, SelfArgs S) {
   constexpr int U = UT_<QT>::U, EU = UT_<QT>::EU;
   constexpr uint32_t NT = unit_terms<QT>();
   using Act = ActLds<QT, true>;
   extern __shared__ uint4 dsm[];
+  __shared__ float s_lt[kSpecMaxExperts], s_la[kSpecMaxExperts];
+  __shared__ uint32_t s_cl[kSpecMaxExperts], s_nc;
+  __shared__ double s_sb[2 * kSpecMaxExperts];
   float* lds = reinterpret_cast<float*>(dsm);
-  if (ra.n && blockIdx.y == gridDim.y - 1) {
-    if (blockIdx.x < ra.n) route_token(ra, blockIdx.x, lds, A.rsec, nullptr);
+  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const uint32_t mat = wave / kSplitParts, part = wave % kSplitParts;
+  const bool route_row = ra.n && blockIdx.y == gridDim.y - 1;
+  uint32_t nc = 0;
+  const uint8_t* ep = nullptr;  // SELF: lane e's expert matrix of this wave (wave 0: gate, up, down below)
+  const uint8_t* ep3[3] = {nullptr, nullptr, nullptr};
+  if constexpr (SELF) {
+    if (route_row ? blockIdx.x != 0 : blockIdx.x * kTileRows >= A.f) return;
+    if (lane < ra.ne) {
+      ep = S.eptr[mat * ra.ne + lane];
+      if (wave == 0)
+        for (int p = 0; p < 3; p++) ep3[p] = S.eptr[p * ra.ne + lane];
+    }
+    spec_dots<kSplitLoads>(ra.router, ra.hs, ra.ne, ra.d, s_lt, s_la);
+    __syncthreads();
+    if (wave == 0) {
+      bool c;
+      uint32_t p;
+      const uint32_t q = spec_candidates<kSplitLoads>(ra.ne, ra.k, ra.d, ra.gating, s_lt, s_la, s_sb, s_cl, lane, &c, &p);
+      if (lane == 0) s_nc = q;
+    }
+    __syncthreads();
+    nc = s_nc;
+  }
+  if (route_row) {
+    if constexpr (SELF) {
+      // the dispatch summary of the candidates, as the front end writes it for one token,
+      // and the output rows the down product adds into
+      if (wave == 0 && lane < ra.ne) {
+        uint32_t below = 0;
+        for (uint32_t j = 0; j < nc; j++) below += s_cl[j] < lane ? 1u : 0u;
+        S.offsets[lane] = below;
+        if (lane < nc) S.active[1 + lane] = s_cl[lane];
+        if (lane >= nc) S.work[lane].m = 0;
+        if (lane == 0) {
+          S.offsets[ra.ne] = nc;
+          S.active[0] = nc;
+        }
+      }
+      if (S.out)
+        for (uint32_t c = tid; c < ra.d; c += blockDim.x) S.out[c] = 0.0f;
+      route_token(ra, 0, lds, A.rsec, nullptr, s_cl, nc);
+    } else {
+      if (blockIdx.x < ra.n) route_token(ra, blockIdx.x, lds, A.rsec, nullptr);
+    }
     return;
   }
   const uint32_t r0 = blockIdx.x * kTileRows;
   if (r0 >= A.f) return;  // (the routing row may widen the grid)
-  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const uint32_t mat = wave / kSplitParts, part = wave % kSplitParts;
   const uint32_t nunit = unit_count<QT>(A.d), nterm = nunit * NT;
   const uint32_t u0 = nunit * part / kSplitParts, u1 = nunit * (part + 1) / kSplitParts;
   // LDS: terms [2 matrices][nterm][64], u's row sums [64], the token's row, and its staged
@@ -337,15 +399,37 @@ __global__ void __launch_bounds__(64 * kSplitWaves, 4) k_gu_split(SplitArgs A, R
   // active experts y, y + ny, ... (the grid is sized for the usual count; rare extra
   // candidates are taken by the same workgroups)
   const uint32_t ny = gridDim.y - (ra.n ? 1 : 0);
-  for (uint32_t a = blockIdx.y; a < A.ne; a += ny) {
-  const ExpertWork* W = A.work + a;
-  const uint32_t m = W->m, s0 = W->s0;
-  if (m != 1) break;  // m = 0: past the last active expert (one token a call: m <= 1)
-  UnitStream<QT, 1> st(W->w[mat] + (size_t)blockIdx.x * nunit * kTileRows * U, u0, u1, lane);
+  for (uint32_t a = blockIdx.y; a < (SELF ? nc : A.ne); a += ny) {
+  const uint8_t* wmat;
+  uint32_t s0;
+  if constexpr (SELF) {  // slot a streams the a-th candidate; its one pair is slot a, token 0's
+    const uint32_t e = s_cl[a];
+    wmat = reinterpret_cast<const uint8_t*>(__shfl(reinterpret_cast<uintptr_t>(ep), (int)e));
+    s0 = a;
+    if (blockIdx.x == 0 && wave == 0) {
+      const uint8_t* w3[3];
+      for (int p = 0; p < 3; p++) w3[p] = reinterpret_cast<const uint8_t*>(__shfl(reinterpret_cast<uintptr_t>(ep3[p]), (int)e));
+      if (lane == 0) {
+        ExpertWork& W = S.work[a];
+        for (int p = 0; p < 3; p++) W.w[p] = w3[p];
+        W.e = e;
+        W.s0 = a;
+        W.m = 1;
+        S.slot_tok[a] = 0;
+      }
+    }
+  } else {
+    const ExpertWork* W = A.work + a;
+    if (W->m != 1) break;  // m = 0: past the last active expert (one token a call: m <= 1)
+    wmat = W->w[mat];
+    s0 = W->s0;
+  }
+  UnitStream<QT, 1> st(wmat + (size_t)blockIdx.x * nunit * kTileRows * U, u0, u1, lane);
   st.prime();  // the weights' first loads overlap the staging of the activations
-  if (tid == 0) rows[0] = A.slot_tok[s0];
+  if (tid == 0) rows[0] = SELF ? 0u : A.slot_tok[s0];
   __syncthreads();
-  stage_acts<QT, true>(acts, A.d, 1u, rows, A.d, 0, A.xq, A.xs, A.xsum, nullptr);
+  if constexpr (SELF) stage_acts<QT, true>(acts, A.d, 1u, rows, A.d, 0, nullptr, nullptr, nullptr, ra.hs);
+  else stage_acts<QT, true>(acts, A.d, 1u, rows, A.d, 0, A.xq, A.xs, A.xsum, nullptr);
   __syncthreads();
   st.run([&](uint32_t u, const uint32_t* w) {
     const uint32_t off = u * EU;
@@ -661,14 +745,16 @@ template <int QT>
 static hipError_t go_gu_split(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
   uint32_t rsec = 0;
   const uint32_t lds = split_lds<QT>(L, ra, &rsec);
-  if (lds == 0 || n != 1) return hipErrorInvalidValue;
-  static const bool once = allow_lds(k_gu_split<QT>);
+  if (lds == 0 || n != 1 || (ra.self && (!ra.n || L.ne > kSpecMaxExperts))) return hipErrorInvalidValue;
+  static const bool once = allow_lds(k_gu_split<QT, false>) && allow_lds(k_gu_split<QT, true>);
   (void)once;
   const uint32_t tiles = (L.f + kTileRows - 1) / kTileRows;
   const dim3 g(max(tiles, ra.n), min(L.ne, n * L.k) + (ra.n ? 1 : 0));
   const SplitArgs A{B.work, B.slot_tok, B.xq, B.xs, B.xsum, B.hq, B.hsc, B.hsum, L.ne, L.d, L.f, rsec,
                     sum_kind_of(L.qt_down), sum_offset_of(L.qt_down)};
-  hipLaunchKernelGGL((k_gu_split<QT>), g, dim3(64 * kSplitWaves), lds, st, A, ra);
+  const SelfArgs S{L.eptr, B.work, B.slot_tok, B.active, B.offsets, B.fuse_out ? B.out : nullptr};
+  if (ra.self) hipLaunchKernelGGL((k_gu_split<QT, true>), g, dim3(64 * kSplitWaves), lds, st, A, ra, S);
+  else hipLaunchKernelGGL((k_gu_split<QT, false>), g, dim3(64 * kSplitWaves), lds, st, A, ra, S);
   return hipGetLastError();
 }
 
@@ -758,12 +844,20 @@ hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const R
   if constexpr (has_int8_kernel(QT)) {
     if (L.math == 0) {
       if (B.hq && split_ok<QT>(L, n, ra)) return go_gu_split<QT>(L, B, n, ra, st);
+      if (ra.self) return hipErrorInvalidValue;  // (the caller asked only where units_self_ok)
       if (n <= kDeepRingTokens) return go_gu<QT, true, 4>(L, B, n, ra, st);
       if (n * L.k <= L.ne) return go_gu<QT, true, 1>(L, B, n, ra, st);
       return go_gu<QT, true, 2>(L, B, n, ra, st);
     }
   }
   return go_gu<QT, false, 2>(L, B, n, ra, st);
+}
+
+template <int QT>
+bool units_self_ok(const LayerDev& L, uint32_t n) {
+  RouteArgs ra{};
+  ra.n = n;
+  return L.qt_gate == QT && L.qt_up == QT && L.ne <= kSpecMaxExperts && split_ok<QT>(L, n, ra);
 }
 
 template <int QT>
@@ -776,6 +870,7 @@ hipError_t units_down(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t 
 
 template hipError_t units_gateup<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, const RouteArgs&, hipStream_t);
 template hipError_t units_down<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, uint32_t, hipStream_t);
+template bool units_self_ok<GMOE_QT>(const LayerDev&, uint32_t);
 template hipError_t units_down_atomic<GMOE_QT>(const LayerDev&, const FwdBufs&, uint32_t, hipStream_t);
 template hipError_t units_embed<GMOE_QT>(const uint8_t*, uint32_t, const GlueTokens*, const uint32_t*, uint32_t, float*,
                                          hipStream_t);
