@@ -342,7 +342,11 @@ __global__ void __launch_bounds__(64 * kSplitWaves, 4) k_gu_split(SplitArgs A, R
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const uint32_t mat = wave / kSplitParts, part = wave % kSplitParts;
   const bool route_row = ra.n && blockIdx.y == gridDim.y - 1;
-  uint32_t nc = 0;
+  const uint32_t nunit = unit_count<QT>(A.d), nterm = nunit * NT;
+  const uint32_t u0 = nunit * part / kSplitParts, u1 = nunit * (part + 1) / kSplitParts;
+  const size_t toff = (size_t)blockIdx.x * nunit * kTileRows * U;  // the tile's offset in a matrix
+  UnitStream<QT, 1> st(reinterpret_cast<const uint8_t*>(A.work), u0, u0, lane);  // empty until set
+  uint32_t nc = 0, pred = ~0u;  // SELF: the candidate count, slot blockIdx.y's predicted expert
   const uint8_t* ep = nullptr;  // SELF: lane e's expert matrix of this wave (wave 0: gate, up, down below)
   const uint8_t* ep3[3] = {nullptr, nullptr, nullptr};
   if constexpr (SELF) {
@@ -354,6 +358,28 @@ __global__ void __launch_bounds__(64 * kSplitWaves, 4) k_gu_split(SplitArgs A, R
     }
     spec_dots<kSplitLoads>(ra.router, ra.hs, ra.ne, ra.d, s_lt, s_la);
     __syncthreads();
+    // the candidate test's usual outcome is the top k of the parallel logits: slot y's
+    // predicted expert is the y-th lowest id among them, whose stream is primed before the
+    // test (and primed again in the rare call where the test names another)
+    if (!route_row) {
+      const float le = lane < ra.ne ? s_lt[lane] : 0.0f;
+      uint32_t r = 0;
+      for (uint32_t j = 0; j < ra.ne; j++) {
+        const float lj = s_lt[j];
+        r += (lj > le || (lj == le && j < lane)) ? 1u : 0u;
+      }
+      const uint64_t top = __ballot(lane < ra.ne && r < ra.k);
+      if ((uint32_t)__popcll(top) > blockIdx.y) {
+        uint64_t m = top;
+        for (uint32_t i = 0; i < blockIdx.y; i++) m &= m - 1;
+        pred = (uint32_t)__ffsll((unsigned long long)m) - 1;
+        if (blockIdx.x * kTileRows < A.f) {
+          st = UnitStream<QT, 1>(reinterpret_cast<const uint8_t*>(__shfl(reinterpret_cast<uintptr_t>(ep), (int)pred)) + toff,
+                                 u0, u1, lane);
+          st.prime();
+        }
+      }
+    }
     if (wave == 0) {
       bool c;
       uint32_t p;
@@ -388,8 +414,6 @@ __global__ void __launch_bounds__(64 * kSplitWaves, 4) k_gu_split(SplitArgs A, R
   }
   const uint32_t r0 = blockIdx.x * kTileRows;
   if (r0 >= A.f) return;  // (the routing row may widen the grid)
-  const uint32_t nunit = unit_count<QT>(A.d), nterm = nunit * NT;
-  const uint32_t u0 = nunit * part / kSplitParts, u1 = nunit * (part + 1) / kSplitParts;
   // LDS: terms [2 matrices][nterm][64], u's row sums [64], the token's row, and its staged
   // activations
   float* terms = lds;
@@ -402,8 +426,10 @@ __global__ void __launch_bounds__(64 * kSplitWaves, 4) k_gu_split(SplitArgs A, R
   for (uint32_t a = blockIdx.y; a < (SELF ? nc : A.ne); a += ny) {
   const uint8_t* wmat;
   uint32_t s0;
+  bool primed = false;  // the stream already holds this slot's expert (the prediction held)
   if constexpr (SELF) {  // slot a streams the a-th candidate; its one pair is slot a, token 0's
     const uint32_t e = s_cl[a];
+    primed = a == blockIdx.y && e == pred;
     wmat = reinterpret_cast<const uint8_t*>(__shfl(reinterpret_cast<uintptr_t>(ep), (int)e));
     s0 = a;
     if (blockIdx.x == 0 && wave == 0) {
@@ -424,8 +450,10 @@ __global__ void __launch_bounds__(64 * kSplitWaves, 4) k_gu_split(SplitArgs A, R
     wmat = W->w[mat];
     s0 = W->s0;
   }
-  UnitStream<QT, 1> st(wmat + (size_t)blockIdx.x * nunit * kTileRows * U, u0, u1, lane);
-  st.prime();  // the weights' first loads overlap the staging of the activations
+  if (!primed) {
+    st = UnitStream<QT, 1>(wmat + toff, u0, u1, lane);
+    st.prime();  // the weights' first loads overlap the staging of the activations
+  }
   if (tid == 0) rows[0] = SELF ? 0u : A.slot_tok[s0];
   __syncthreads();
   if constexpr (SELF) stage_acts<QT, true>(acts, A.d, 1u, rows, A.d, 0, nullptr, nullptr, nullptr, ra.hs);
