@@ -13,7 +13,8 @@ with HIP events recorded on the stream around every gate/up and down launch, for
 kernel times (the events themselves add about 3 us per launch to a step).
 
 Prints one JSON line with `roofline` (the gate/up kernel: algorithmic bytes per launch /
-its average duration from HIP events on its stream) and `cpu_baseline` (the oracle's
+its average duration from HIP events on its stream; `layer_frac`: the whole layer step's
+algorithmic bytes over its bare time, against the same peak) and `cpu_baseline` (the oracle's
 restatement of the reference's packed CPU path, threaded over rows, on a bounded sample).
 `roofline.traffic` is the HBM bytes per gate/up launch that rocprofv3's FETCH_SIZE and
 WRITE_SIZE counters measured on this same workload, scaled by what they read for a copy of
@@ -845,7 +846,10 @@ def main():
                      "achieved": r["gateup_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": r["gateup_GBs"] / HBM_PEAK_GBS,
                      "traffic": measured_traffic(a.batch, a.math, a.layers),
-                     "bytes_per_launch": r["gateup_bytes"], "avg_launch_us": r["gateup_us"]},
+                     "bytes_per_launch": r["gateup_bytes"], "avg_launch_us": r["gateup_us"],
+                     # the whole layer step (front end, gate/up, down) against the same peak:
+                     # its algorithmic bytes over the bare step time
+                     "layer_achieved": r["layer_GBs"], "layer_frac": r["layer_GBs"] / HBM_PEAK_GBS},
         "cpu_baseline": cpu,
         "prefill": prefill,
         "prefill_packed": prefill_packed,
