@@ -293,15 +293,27 @@ def dense_leg(a, dev, threads, stream, timed):
             for i, (nm, (r, c, qt)) in enumerate(shapes.items())}
     attn = [[G.DenseWeight(dev, shapes[nm][2], shapes[nm][0], shapes[nm][1], raws[nm]) for nm in "qkvo"]
             for _ in range(copies["attn"])]
+    # as the model step runs them: q, k and v stacked into one 6144-row weight (the packed
+    # rows laid end to end, what the model's stacking of the three makes), then o
+    qkv_raw = np.concatenate([raws["q"], raws["k"], raws["v"]])
+    stacked = [(G.DenseWeight(dev, G.Q4_K, 6144, 4096, qkv_raw),
+                G.DenseWeight(dev, G.Q4_K, 4096, 4096, raws["o"])) for _ in range(copies["attn"])]
+    del qkv_raw
     head = [G.DenseWeight(dev, G.Q6_K, 32000, 4096, raws["head"]) for _ in range(copies["head"])]
     del raws
     x = torch.from_numpy(M.fill_gaussian(seed + 0x10, n * 4096, 0.0, 1.0, threads).reshape(n, 4096)).cuda()
     outs = {nm: torch.empty((n, shapes[nm][0]), dtype=torch.float32, device="cuda") for nm in shapes}
+    outs["qkv"] = torch.empty((n, 6144), dtype=torch.float32, device="cuda")
     sh = stream.cuda_stream
 
     def attn_step(i):
         for W, nm in zip(attn[i % len(attn)], "qkvo"):
             W.forward_async(x.data_ptr(), n, outs[nm].data_ptr(), sh)
+
+    def stacked_step(i):
+        Wqkv, Wo = stacked[i % len(stacked)]
+        Wqkv.forward_async(x.data_ptr(), n, outs["qkv"].data_ptr(), sh)
+        Wo.forward_async(x.data_ptr(), n, outs["o"].data_ptr(), sh)
 
     def head_step(i):
         head[i % len(head)].forward_async(x.data_ptr(), n, outs["head"].data_ptr(), sh)
@@ -311,6 +323,8 @@ def dense_leg(a, dev, threads, stream, timed):
     for name, step, nbytes in (
             ("attention q,k,v,o", attn_step, sum(M.byte_size(qt, r * c) for nm, (r, c, qt) in shapes.items()
                                                  if nm != "head")),
+            ("attention qkv stacked + o", stacked_step,
+             sum(M.byte_size(qt, r * c) for nm, (r, c, qt) in shapes.items() if nm != "head")),
             ("output head", head_step, M.byte_size(G.Q6_K, 32000 * 4096))):
         for i in range(8):
             step(i)
@@ -325,9 +339,14 @@ def dense_leg(a, dev, threads, stream, timed):
             W.release()
     for W in head:
         W.release()
+    for ws in stacked:
+        for W in ws:
+            W.release()
     return {"workload": "C5 dense projections at decode batch 8, packed math: one layer's q,k,v,o "
-                        "(Q4_K; 4096x4096, 1024x4096 x2, 4096x4096) and the 32000x4096 Q6_K output head; "
-                        f"{copies['attn']} and {copies['head']} copies rotated", "batch": n, "legs": res}
+                        "(Q4_K; 4096x4096, 1024x4096 x2, 4096x4096) as four calls and as the model step "
+                        "runs them (q,k,v stacked into one 6144-row call, then o), and the 32000x4096 Q6_K "
+                        f"output head; {copies['attn']} and {copies['head']} copies rotated",
+            "batch": n, "legs": res}
 
 
 def prefetch_leg(a, mats, threads):

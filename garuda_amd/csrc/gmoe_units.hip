@@ -216,8 +216,8 @@ __device__ __forceinline__ void unit_tokens(const uint32_t* w, const uint8_t* ac
 // With ra.n > 0 (speculative decode) the last row of the grid is the exact routing
 // instead: workgroup x < n*ne runs route_logit for token x / ne, expert x % ne. The
 // dispatcher starts it with the last wave of expert workgroups, whose tail hides it.
-template <int QT, bool PACKED, int D>
-__global__ void __launch_bounds__(128, D > 2 ? 1 : 2)
+template <int QT, bool PACKED, int D, int TPW = 1>
+__global__ void __launch_bounds__(128 * TPW, D > 2 ? 1 : (TPW > 1 ? 3 : 2))
 k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __restrict__ slot_tok, uint32_t f,
            uint32_t d, uint32_t mt, const int8_t* __restrict__ xq,
            const float* __restrict__ xs, const uint32_t* __restrict__ xsum, const float* __restrict__ hs,
@@ -231,10 +231,10 @@ k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __r
       return;
     }
   }
-  float* accs = reinterpret_cast<float*>(dsm);                 // [2][mt][64] running row sums
-  uint32_t* rows = reinterpret_cast<uint32_t*>(accs + 2 * mt * 64);  // [mt] token of each chunk member
+  float* accs = reinterpret_cast<float*>(dsm);                 // [2 TPW][mt][64] running row sums
+  uint32_t* rows = reinterpret_cast<uint32_t*>(accs + 2 * TPW * mt * 64);  // [mt] token of each chunk member
   uint8_t* acts = reinterpret_cast<uint8_t*>(rows + ((mt + 3) & ~3u));
-  if (blockIdx.x * kTileRows >= f) return;  // (the routing row may widen the grid)
+  if (blockIdx.x * TPW * kTileRows >= f) return;  // (the routing row may widen the grid)
   // active experts y0, y0 + ny, ... (the grid is sized for the usual count; rare extra
   // candidates are taken by the same workgroups)
   const uint32_t y0 = blockIdx.y, ny = gridDim.y - (ra.n ? 1 : 0);
@@ -244,12 +244,14 @@ k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __r
   if (m_all == 0) break;
   const uint32_t s0 = W->s0;
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const uint32_t r0 = blockIdx.x * kTileRows;
+  // wave 2i streams gate, wave 2i+1 up, of tile TPW * blockIdx.x + i
+  const uint32_t tile = blockIdx.x * TPW + wave / 2, r0 = tile * kTileRows;
+  const bool tv = r0 < f;  // (a last workgroup of TPW > 1 may hold a tile past d_ff)
   const uint32_t nblk = unit_blocks<QT>(d), nunit = unit_count<QT>(d);
   const uint32_t per = ActLds<QT, PACKED>::per_token(d);
   float* my = accs + wave * mt * 64 + lane;  // token t's sum of this lane's row: my[t * 64]
-  const uint8_t* mat = wave == 0 ? W->w[0] : W->w[1];
-  UnitStream<QT, D> st(mat + (size_t)blockIdx.x * nunit * kTileRows * U, 0, nunit, lane);
+  const uint8_t* mat = W->w[wave & 1];
+  UnitStream<QT, D> st(mat + (size_t)(tv ? tile : 0) * nunit * kTileRows * U, 0, tv ? nunit : 0, lane);
   for (uint32_t c0 = 0; c0 < m_all; c0 += mt) {
     const uint32_t m = min(mt, m_all - c0);
     st.prime();  // the weights' first loads overlap the staging of the activations
@@ -260,10 +262,10 @@ k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __r
     __syncthreads();
     st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED>(w, acts, per, d, u, 0, nblk, my, m); });
     __syncthreads();
-    if (wave == 0) {
+    if ((wave & 1) == 0 && tv) {
       const bool valid = r0 + (lane & 32) + 32 <= f;  // this lane's 32-row block lies inside d_ff
       for (uint32_t t = 0; t < m; t++) {
-        const float h = swiglu(accs[t * 64 + lane], accs[(mt + t) * 64 + lane]);
+        const float h = swiglu(my[t * 64], my[(mt + t) * 64]);  // the up wave's sums follow
         const size_t slot = s0 + c0 + t;
         if (hf && r0 + lane < f) hf[slot * f + r0 + lane] = h;
         if (hq)
@@ -719,6 +721,14 @@ constexpr uint32_t kLdsBudget = 160 * 1024 - 2048;
 // 88.6 -> 82.5 us. With more tokens an expert the ring of two stays (batch 8: 106.8 us
 // against 111.7-125 with a ring of one and chunks of 3-5 tokens).
 constexpr uint32_t kDeepRingTokens = 1;
+// Q3_K gate/up with more than one token an expert on average runs workgroups of two row
+// tiles with a ring of one unit set: 164 VGPRs, three waves a SIMD, and the two tiles'
+// four waves share one staging of the tokens, so three workgroups a CU still hold 8
+// tokens (kChunkLds3). The C5 slice (Q3_K gate/up, batch 8) went from 172.4 to 164.7 us a
+// call; the same for Q4_K (C2 batch 8: 168.0 -> 172.9 us a step) and Q6_K (C4: 189.3 ->
+// 194.5 us) measured slower, so they keep one tile and two unit sets.
+template <int QT>
+constexpr bool gu_pairs() { return QT == Q3_K; }
 
 template <class K>
 static bool allow_lds(K kernel) {
@@ -736,10 +746,15 @@ static bool allow_lds(K kernel) {
 // Sizing for the whole batch instead would give every workgroup the LDS of n tokens and
 // one workgroup per CU when experts are many and tokens per expert few.
 constexpr uint32_t kChunkLds = 40 * 1024 - 64;
-static uint32_t chunk_tokens(const LayerDev& L, uint32_t n, uint32_t per_token_bytes) {
+// gate/up workgroups of two row tiles: three a CU (twelve waves, three a SIMD)
+constexpr uint32_t kChunkLds3 = 160 * 1024 / 3 - 512;
+static uint32_t chunk_tokens_lds(const LayerDev& L, uint32_t n, uint32_t per_token_bytes, uint32_t budget) {
   const uint32_t usual = max(8u, 2 * ((n * L.k + L.ne - 1) / L.ne));
-  const uint32_t fit = kChunkLds / per_token_bytes;  // 0 when one token needs more (then one, if it fits at all)
+  const uint32_t fit = budget / per_token_bytes;  // 0 when one token needs more (then one, if it fits at all)
   return min(min(n, usual), fit ? fit : kLdsBudget / per_token_bytes);
+}
+static uint32_t chunk_tokens(const LayerDev& L, uint32_t n, uint32_t per_token_bytes) {
+  return chunk_tokens_lds(L, n, per_token_bytes, kChunkLds);
 }
 
 // The split gate/up (k_gu_split) serves packed math at one token a call for the K-quant
@@ -786,19 +801,20 @@ static hipError_t go_gu_split(const LayerDev& L, const FwdBufs& B, uint32_t n, c
   return hipGetLastError();
 }
 
-template <int QT, bool PACKED, int D>
+template <int QT, bool PACKED, int D, int TPW = 1>
 static hipError_t go_gu(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
-  const uint32_t per = 2 * 64 * 4 + ActLds<QT, PACKED>::per_token(L.d) + 4;
-  const uint32_t mt = chunk_tokens(L, n, per + 16);
+  const uint32_t per = 2 * TPW * 64 * 4 + ActLds<QT, PACKED>::per_token(L.d) + 4;
+  const uint32_t mt = TPW > 1 ? chunk_tokens_lds(L, n, per + 16, kChunkLds3) : chunk_tokens(L, n, per + 16);
   if (mt == 0) return hipErrorInvalidValue;
-  static const bool once = allow_lds(k_gu_units<QT, PACKED, D>);
+  static const bool once = allow_lds(k_gu_units<QT, PACKED, D, TPW>);
   (void)once;
-  const uint32_t tiles = (L.f + kTileRows - 1) / kTileRows;
+  const uint32_t tiles = (L.f + kTileRows * TPW - 1) / (kTileRows * TPW);
   uint32_t lds = mt * per + 16;
   if (ra.n) lds = max(lds, route_logit_lds(ra.k, ra.sec));
   const dim3 g(max(tiles, ra.n * ra.ne), min(L.ne, n * L.k) + (ra.n ? 1 : 0));
-  hipLaunchKernelGGL((k_gu_units<QT, PACKED, D>), g, dim3(128), lds, st, B.work, L.ne, B.slot_tok, L.f, L.d, mt, B.xq,
-                     B.xs, B.xsum, B.hs, B.hq, B.hsc, B.hsum, B.hf, sum_kind_of(L.qt_down), sum_offset_of(L.qt_down), ra);
+  hipLaunchKernelGGL((k_gu_units<QT, PACKED, D, TPW>), g, dim3(128 * TPW), lds, st, B.work, L.ne, B.slot_tok, L.f,
+                     L.d, mt, B.xq, B.xs, B.xsum, B.hs, B.hq, B.hsc, B.hsum, B.hf, sum_kind_of(L.qt_down),
+                     sum_offset_of(L.qt_down), ra);
   return hipGetLastError();
 }
 
@@ -875,6 +891,7 @@ hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const R
       if (ra.self) return hipErrorInvalidValue;  // (the caller asked only where units_self_ok)
       if (n <= kDeepRingTokens) return go_gu<QT, true, 4>(L, B, n, ra, st);
       if (n * L.k <= L.ne) return go_gu<QT, true, 1>(L, B, n, ra, st);
+      if constexpr (gu_pairs<QT>()) return go_gu<QT, true, 1, 2>(L, B, n, ra, st);
       return go_gu<QT, true, 2>(L, B, n, ra, st);
     }
   }
