@@ -1635,10 +1635,14 @@ gmoe_status gmoe_prefetch_step(gmoe_ctx* c, gmoe_predictor* p, uint32_t lid, uin
   Layer* L;
   if (gmoe_status s = get_layer(c, lid, &L)) return s;
   HIP_TRY(hipSetDevice(c->device));
-  // the experts this step used and the ones predicted stay; others may be evicted
+  // the experts this step and the step before used, and the ones predicted, stay; only
+  // experts idle for two steps may be evicted to make room for a prediction (a wrong
+  // guess that evicted last step's expert cost a miss whenever routing came back to it)
   Keep keep;
   for (uint32_t i = 0; i < nused; i++)
     if (used[i] >= base && used[i] - base < L->ne) keep.emplace_back(lid, used[i] - base);
+  for (uint32_t i = 0; i < nprev; i++)
+    if (prev[i] >= base && prev[i] - base < L->ne) keep.emplace_back(lid, prev[i] - base);
   for (uint32_t i = 0; i < *npred; i++)
     if (pred[i] >= base && pred[i] - base < L->ne) keep.emplace_back(lid, pred[i] - base);
   c->prefetch_keep = keep;

@@ -440,8 +440,9 @@ gmoe_status gmoe_predictor_set_counts(gmoe_predictor* p, const uint32_t* counts,
  * context's staging thread, and returns without waiting for them (gmoe_expert_state,
  * gmoe_prefetch_wait). *launched and *skipped (may be NULL) count the queued and the
  * skipped ones. The staging thread makes room by evicting least recently used experts
- * other than this step's used and predicted ones, after the evicted layer's last queued
- * call has finished. */
+ * other than this step's and the previous step's used ones and the predicted ones, after
+ * the evicted layer's last queued call has finished; a prediction that finds no such room
+ * is dropped (the forward stages it if it is routed). */
 gmoe_status gmoe_prefetch_step(gmoe_ctx* ctx, gmoe_predictor* p, uint32_t layer_id, uint32_t id_base,
                                const uint32_t* previous, uint32_t n_previous, const uint32_t* used,
                                uint32_t n_used, const uint32_t* predicted_last, uint32_t n_predicted_last,

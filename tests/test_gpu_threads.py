@@ -73,7 +73,7 @@ def test_forwards_beside_prefetch_steps_on_a_small_slab():
     expert_bytes = 3 * G.byte_size(G.Q4_K, D * F)
     with G.Device(0, slab_bytes=4 * (expert_bytes + 4096)) as dev:  # four of the eight experts
         layer = G.MoeLayer(dev, D, F, NE, K, router, mats["gate"], mats["up"], mats["down"], (G.Q4_K,) * 3)
-        eng = PrefetchEngine(dev, ExpertPredictor(NE), depth=3)
+        eng = PrefetchEngine(dev, ExpertPredictor(NE), enabled=True, depth=3)
         inputs = [rng.normal(0, 1, (1, D)).astype(np.float32) for _ in range(30)]
         wants = [O.feed_forward_batch(L, h) for h in inputs]
         try:
