@@ -494,12 +494,14 @@ __global__ void __launch_bounds__(64 * kSplitWaves, 4) k_gu_split(SplitArgs A, R
   }
 }
 
-// Down: the row's units are split over gridDim.y workgroups of KS waves each. A
-// workgroup adds its waves' partial sums in wave order and writes them to its own
-// partial slice y[blockIdx.y]; the combine adds the slices in order.
+// Down: the row's units are split over gridDim.y workgroups of KS unit ranges each. A
+// workgroup adds its ranges' partial sums in range order and writes them to its own
+// partial slice y[blockIdx.y]; the combine adds the slices in order. TS > 1: each range
+// is streamed by TS waves, each for its share of the chunk's tokens (the same sums, each
+// by fewer dependent steps a wave).
 // grid.x = row tiles of d_model, grid.y = K groups, grid.z = active-expert slot.
-template <int QT, bool PACKED, int KS, int RD = 2>
-__global__ void __launch_bounds__(64 * KS, 2)
+template <int QT, bool PACKED, int KS, int RD = 2, int TS = 1>
+__global__ void __launch_bounds__(64 * KS * TS, 2)
 k_dn_units(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32_t d, uint32_t mt, uint32_t part_stride,
            const int8_t* __restrict__ hq, const float* __restrict__ hsc, const uint32_t* __restrict__ hsum,
            const float* __restrict__ hf, float* __restrict__ ypart) {
@@ -514,26 +516,30 @@ k_dn_units(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t f, uint32_
   if (m_all == 0) break;
   const uint32_t s0 = W->s0;
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t rg = TS > 1 ? wave % KS : wave, tg = TS > 1 ? wave / KS : 0u;  // unit range, token share
   const uint32_t r0 = blockIdx.x * kTileRows;
   const uint32_t nblk = unit_blocks<QT>(f), nunit = unit_count<QT>(f);
-  const uint32_t nsl = gridDim.y * KS, sl = blockIdx.y * KS + wave;
+  const uint32_t nsl = gridDim.y * KS, sl = blockIdx.y * KS + rg;
   const uint32_t u0 = (nunit * sl) / nsl, u1 = (nunit * (sl + 1)) / nsl;
   // the workgroup's unit range: its first wave's start to its last wave's end
   const uint32_t uw0 = (nunit * (blockIdx.y * KS)) / nsl, uw1 = (nunit * (blockIdx.y * KS + KS)) / nsl;
   const uint32_t nelem = min(uw1 * EU, f) - min(uw0 * EU, f);
   const uint32_t per = ActLds<QT, PACKED>::per_token(nelem);
   float* y = ypart + (size_t)blockIdx.y * part_stride;
-  float* my = accs + wave * mt * 64 + lane;
+  float* my = accs + rg * mt * 64 + lane;
   UnitStream<QT, RD> st(W->w[2] + (size_t)blockIdx.x * nunit * kTileRows * U, u0, u1, lane);
   for (uint32_t c0 = 0; c0 < m_all; c0 += mt) {
     const uint32_t m = min(mt, m_all - c0);
+    const uint32_t t0 = (m * tg) / TS, t1 = (m * (tg + 1)) / TS;  // the wave's tokens of the chunk
     st.prime();  // the weights' first loads overlap the staging of the activations
     for (uint32_t t = threadIdx.x; t < m; t += blockDim.x) rows[t] = s0 + c0 + t;
-    for (uint32_t t = 0; t < m; t++) my[t * 64] = 0.0f;
+    for (uint32_t t = t0; t < t1; t++) my[t * 64] = 0.0f;
     __syncthreads();
     if (nelem) stage_acts<QT, PACKED>(acts, nelem, m, rows, f, uw0 * EU, hq, hsc, hsum, hf);
     __syncthreads();
-    st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED>(w, acts, per, nelem, u, uw0, nblk, my, m); });
+    st.run([&](uint32_t u, const uint32_t* w) {
+      unit_tokens<QT, PACKED>(w, acts + t0 * per, per, nelem, u, uw0, nblk, my + t0 * 64, t1 - t0);
+    });
     __syncthreads();
     if (wave == 0) {
       const uint32_t row = r0 + lane;
@@ -818,8 +824,17 @@ static hipError_t go_gu(const LayerDev& L, const FwdBufs& B, uint32_t n, const R
   return hipGetLastError();
 }
 
-template <int QT, bool PACKED, int RD>
+template <int QT, bool PACKED, int RD, int TS = 1>
 static hipError_t go_dn_rd(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st);
+
+// Dense projections (one "expert" of weight 1) of a few hundred row tiles at most, from 4
+// tokens on, stream each unit range with two waves, each for half the tokens: there the
+// launch is a short chain per workgroup (one or two units a wave), and the tokens' dots
+// run one after another in a wave. The 32000-row output head (500 row tiles, more
+// workgroups than the chip holds) measured slower that way (55 -> 80 us), so it keeps one.
+static bool dn_token_split(const LayerDev& L, uint32_t n) {
+  return L.ne == 1 && n >= 4 && (L.d + kTileRows - 1) / kTileRows <= 128;
+}
 
 // The K-sliced down product (and the dense projections it runs) streams through a ring of
 // one unit set, as the fused down does: C4 (Q8_0 down) 201 -> 189.6 us a call, the
@@ -827,20 +842,23 @@ static hipError_t go_dn_rd(const LayerDev& L, const FwdBufs& B, uint32_t n, uint
 // 52.9 us, against a ring of two on the same box.
 template <int QT, bool PACKED>
 static hipError_t go_dn(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st) {
+  if constexpr (PACKED) {
+    if (dn_token_split(L, n)) return go_dn_rd<QT, PACKED, 1, 2>(L, B, n, ksg, st);
+  }
   return go_dn_rd<QT, PACKED, 1>(L, B, n, ksg, st);
 }
 
-template <int QT, bool PACKED, int RD>
+template <int QT, bool PACKED, int RD, int TS>
 static hipError_t go_dn_rd(const LayerDev& L, const FwdBufs& B, uint32_t n, uint32_t ksg, hipStream_t st) {
   // a workgroup stages at most ceil(units / ksg) + 1 units
   const uint32_t span = min(((unit_count<QT>(L.f) + ksg - 1) / ksg + 1) * UT_<QT>::EU, L.f);
   const uint32_t per = kDnKS * 64 * 4 + ActLds<QT, PACKED>::per_token(span) + 4;
   const uint32_t mt = chunk_tokens(L, n, per + 16);
   if (mt == 0) return hipErrorInvalidValue;
-  static const bool once = allow_lds(k_dn_units<QT, PACKED, kDnKS, RD>);
+  static const bool once = allow_lds(k_dn_units<QT, PACKED, kDnKS, RD, TS>);
   (void)once;
   const dim3 g((L.d + kTileRows - 1) / kTileRows, ksg, min(L.ne, n * L.k));
-  hipLaunchKernelGGL((k_dn_units<QT, PACKED, kDnKS, RD>), g, dim3(64 * kDnKS), mt * per + 16, st, B.work, L.ne, L.f, L.d, mt,
+  hipLaunchKernelGGL((k_dn_units<QT, PACKED, kDnKS, RD, TS>), g, dim3(64 * kDnKS * TS), mt * per + 16, st, B.work, L.ne, L.f, L.d, mt,
                      B.nslot * L.d, B.hq, B.hsc, B.hsum, B.hf, B.y);
   return hipGetLastError();
 }
