@@ -304,6 +304,10 @@ def dense_leg(a, dev, threads, stream, timed):
     x = torch.from_numpy(M.fill_gaussian(seed + 0x10, n * 4096, 0.0, 1.0, threads).reshape(n, 4096)).cuda()
     outs = {nm: torch.empty((n, shapes[nm][0]), dtype=torch.float32, device="cuda") for nm in shapes}
     outs["qkv"] = torch.empty((n, 6144), dtype=torch.float32, device="cuda")
+    # the model step's form: the K slices left for the next launch to add (rope/append, the
+    # feed-forward's residual add), so no launch of their own
+    parts = {nm: torch.empty((G.DenseWeight.MAX_SLICES, n, r), dtype=torch.float32, device="cuda")
+             for nm, r in (("qkv", 6144), ("o", 4096))}
     sh = stream.cuda_stream
 
     def attn_step(i):
@@ -315,6 +319,11 @@ def dense_leg(a, dev, threads, stream, timed):
         Wqkv.forward_async(x.data_ptr(), n, outs["qkv"].data_ptr(), sh)
         Wo.forward_async(x.data_ptr(), n, outs["o"].data_ptr(), sh)
 
+    def slices_step(i):
+        Wqkv, Wo = stacked[i % len(stacked)]
+        Wqkv.forward_slices_async(x.data_ptr(), n, parts["qkv"].data_ptr(), sh)
+        Wo.forward_slices_async(x.data_ptr(), n, parts["o"].data_ptr(), sh)
+
     def head_step(i):
         head[i % len(head)].forward_async(x.data_ptr(), n, outs["head"].data_ptr(), sh)
 
@@ -324,6 +333,8 @@ def dense_leg(a, dev, threads, stream, timed):
             ("attention q,k,v,o", attn_step, sum(M.byte_size(qt, r * c) for nm, (r, c, qt) in shapes.items()
                                                  if nm != "head")),
             ("attention qkv stacked + o", stacked_step,
+             sum(M.byte_size(qt, r * c) for nm, (r, c, qt) in shapes.items() if nm != "head")),
+            ("attention qkv stacked + o, slices to the next launch", slices_step,
              sum(M.byte_size(qt, r * c) for nm, (r, c, qt) in shapes.items() if nm != "head")),
             ("output head", head_step, M.byte_size(G.Q6_K, 32000 * 4096))):
         for i in range(8):
@@ -343,9 +354,11 @@ def dense_leg(a, dev, threads, stream, timed):
         for W in ws:
             W.release()
     return {"workload": "C5 dense projections at decode batch 8, packed math: one layer's q,k,v,o "
-                        "(Q4_K; 4096x4096, 1024x4096 x2, 4096x4096) as four calls and as the model step "
-                        "runs them (q,k,v stacked into one 6144-row call, then o), and the 32000x4096 Q6_K "
-                        f"output head; {copies['attn']} and {copies['head']} copies rotated",
+                        "(Q4_K; 4096x4096, 1024x4096 x2, 4096x4096) as four calls, stacked (q,k,v in one "
+                        "6144-row call, then o) with the K slices added by a launch of their own, and "
+                        "stacked as the model step runs them (the slices left to the next launch, which "
+                        "adds them: rope/append, the feed-forward's residual add), and the 32000x4096 "
+                        f"Q6_K output head; {copies['attn']} and {copies['head']} copies rotated",
             "batch": n, "legs": res}
 
 

@@ -100,6 +100,7 @@ SIGNATURES = {
     "gmoe_dense_release": (i32, [vp, u32]),
     "gmoe_dense_forward": (i32, [vp, u32, f32p, u32, f32p]),
     "gmoe_dense_forward_async": (i32, [vp, u32, vp, u32, vp, vp]),
+    "gmoe_dense_forward_slices_async": (i32, [vp, u32, vp, u32, vp, u32p, vp]),
     "gmoe_predictor_create": (i32, [u32, C.POINTER(vp)]),
     "gmoe_predictor_destroy": (None, [vp]),
     "gmoe_predictor_observe": (i32, [vp, u32p, u32, u32p, u32]),

@@ -1617,6 +1617,15 @@ gmoe_status gmoe_dense_forward_async(gmoe_ctx* c, uint32_t id, const float* d_xs
   return mark_scratch(c, st);
 }
 
+static_assert(GMOE_DENSE_MAX_SLICES == kMaxKsg, "the dense call's K slices");
+
+gmoe_status gmoe_dense_forward_slices_async(gmoe_ctx* c, uint32_t id, const float* d_xs, uint32_t n, float* d_parts,
+                                            uint32_t* nsl, void* stream) {
+  if (!d_parts) return fail(GMOE_ERR_INFERENCE, "null slice buffer");
+  const float* parts = nullptr;
+  return dense_slices(c, id, d_xs, n, stream ? (hipStream_t)stream : (c ? c->stream : nullptr), &parts, nsl, d_parts);
+}
+
 gmoe_status gmoe_prefetch_step(gmoe_ctx* c, gmoe_predictor* p, uint32_t lid, uint32_t base, const uint32_t* prev,
                                uint32_t nprev, const uint32_t* used, uint32_t nused, const uint32_t* pl,
                                uint32_t npl, uint32_t depth, uint32_t* pred, uint32_t* npred, uint32_t* launched,

@@ -369,6 +369,8 @@ class DenseWeight:
     (llama/mod.rs:148-195) for the attention projections and the output head. `raw` is
     `rows` packed rows of `cols` values of `qtype`; it is copied to the device."""
 
+    MAX_SLICES = 8  # GMOE_DENSE_MAX_SLICES: K slices of forward_slices_async at most
+
     def __init__(self, dev: Device, qtype: int, rows: int, cols: int, raw, math: int = MATH_PACKED):
         self.dev, self.qtype, self.rows, self.cols, self.math = dev, qtype, rows, cols, math
         a = np.ascontiguousarray(raw, dtype=np.uint8) if not isinstance(raw, (bytes, bytearray, memoryview)) \
@@ -404,6 +406,15 @@ class DenseWeight:
     def forward_async(self, d_xs: int, n: int, d_out: int, stream: int = 0) -> None:
         _check(lib().gmoe_dense_forward_async(self.dev.handle, self.id, d_xs or None, n, d_out or None,
                                               stream or None))
+
+    def forward_slices_async(self, d_xs: int, n: int, d_parts: int, stream: int = 0) -> int:
+        """gmoe_dense_forward_slices_async: the K slices of the output into d_parts
+        (MAX_SLICES * n * rows floats), their in-order sum left to the caller; returns the
+        slice count."""
+        nsl = C.c_uint32(0)
+        _check(lib().gmoe_dense_forward_slices_async(self.dev.handle, self.id, d_xs or None, n, d_parts or None,
+                                                     C.byref(nsl), stream or None))
+        return nsl.value
 
     def release(self) -> None:
         _check(lib().gmoe_dense_release(self.dev.handle, self.id))

@@ -216,6 +216,16 @@ gmoe_status gmoe_dense_forward(gmoe_ctx* ctx, uint32_t dense_id, const float* xs
  * Shares the context's scratch with the layer calls: order them on one stream. */
 gmoe_status gmoe_dense_forward_async(gmoe_ctx* ctx, uint32_t dense_id, const float* d_xs, uint32_t n,
                                      float* d_out, void* stream);
+/* gmoe_dense_forward_async without its last step, the in-order sum of the K slices, for a
+ * caller whose next launch adds them itself (the model step folds them into rope/append
+ * and into the feed-forward's residual add). Writes *nsl <= GMOE_DENSE_MAX_SLICES slices
+ * of [n x rows] to d_parts (slice s of row t at d_parts + (s * n + t) * rows; the caller
+ * provides GMOE_DENSE_MAX_SLICES * n * rows floats); parts[0] + parts[1] + ... in that
+ * order is gmoe_dense_forward_async's output bit for bit. No counterpart in the reference,
+ * whose matmul_rows returns the finished rows; this is the split the model step uses. */
+#define GMOE_DENSE_MAX_SLICES 8
+gmoe_status gmoe_dense_forward_slices_async(gmoe_ctx* ctx, uint32_t dense_id, const float* d_xs, uint32_t n,
+                                            float* d_parts, uint32_t* nsl, void* stream);
 
 /* ---- GGUF checkpoints: the slab's source (garuda/src/gguf/mod.rs; llama/mod.rs:551-637) ----
  *

@@ -140,6 +140,46 @@ def test_async_matches_sync(dev):
         hip.hipFree(dout)
 
 
+def test_slices_add_up_to_the_forward(dev):
+    # gmoe_dense_forward_slices_async: its K slices, added in slice order, are the async
+    # forward's output bit for bit (packed decode with the token split, packed with
+    # fewer tokens, and f32 math at a prefill size on MFMA)
+    import ctypes as C
+    hip = _hip()
+    rows, cols = 1024, 4096
+    raw = fast_random_blocks(G.Q4_K, rows * cols // 256, 78)
+    nmax = 96
+    dx, dout, dp = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    assert hip.hipMalloc(C.byref(dx), nmax * cols * 4) == 0 and hip.hipMalloc(C.byref(dout), nmax * rows * 4) == 0
+    assert hip.hipMalloc(C.byref(dp), G.DenseWeight.MAX_SLICES * nmax * rows * 4) == 0
+    try:
+        for math, n in ((G.MATH_PACKED, 8), (G.MATH_PACKED, 3), (G.MATH_F32, 96)):
+            say(f"dense slices math={math} n={n}")
+            xs = np.random.default_rng(9 + n).normal(0, 1, (n, cols)).astype(np.float32)
+            assert hip.hipMemcpy(dx, xs.ctypes.data, xs.nbytes, 1) == 0
+            W = G.DenseWeight(dev, G.Q4_K, rows, cols, raw, math)
+            try:
+                W.forward_async(dx.value, n, dout.value)
+                want = np.empty((n, rows), np.float32)
+                assert hip.hipDeviceSynchronize() == 0
+                assert hip.hipMemcpy(want.ctypes.data, dout, want.nbytes, 2) == 0
+                nsl = W.forward_slices_async(dx.value, n, dp.value)
+                assert 1 <= nsl <= G.DenseWeight.MAX_SLICES
+                parts = np.empty((nsl, n, rows), np.float32)
+                assert hip.hipDeviceSynchronize() == 0
+                assert hip.hipMemcpy(parts.ctypes.data, dp, parts.nbytes, 2) == 0
+                got = parts[0].copy()
+                for s in range(1, nsl):
+                    got = got + parts[s]
+                assert np.array_equal(bits(got), bits(want)), f"math={math} n={n} nsl={nsl}"
+            finally:
+                W.release()
+    finally:
+        hip.hipFree(dx)
+        hip.hipFree(dout)
+        hip.hipFree(dp)
+
+
 def test_from_gguf(dev, tmp_path):
     rows, cols = 256, 512
     raw = G.quantize(G.Q6_K, np.random.default_rng(1).normal(0, 0.02, rows * cols).astype(np.float32))
