@@ -60,8 +60,10 @@ __host__ __device__ constexpr uint32_t unit_count(uint32_t cols) {
 // load is unconditional (the unit index is clamped to the last unit, a re-read the L2
 // serves) and the loop always runs whole rounds of D, only the bodies past u1 being
 // skipped: the loads pending at each use are then the same on every path and the
-// compiler waits for exactly the set it uses.
-template <int QT, int D = 2>
+// compiler waits for exactly the set it uses. STRIDE > 1: the lane's units are u0,
+// u0 + STRIDE, ... below u1 (u1 - u0 a multiple of STRIDE), and the lane's row is its
+// own (src is the lane's first piece).
+template <int QT, int D = 2, int STRIDE = 1>
 struct UnitStream {
   static constexpr int NP = UT_<QT>::U / 16, NW = UT_<QT>::U / 4;
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -70,7 +72,10 @@ struct UnitStream {
   u32x4 g[D][NP];
 
   __device__ __forceinline__ UnitStream(const uint8_t* __restrict__ tile, uint32_t u0_, uint32_t u1_, uint32_t lane)
-      : src(tile + lane * 16), u0(u0_), u1(u1_), ulast(u1_ > u0_ ? u1_ - 1 : u0_) {}
+      : src(tile + lane * 16), u0(u0_), u1(u1_), ulast(u1_ > u0_ ? u1_ - STRIDE : u0_) {}
+  // (STRIDE > 1: the lane's first piece given directly)
+  __device__ __forceinline__ UnitStream(const uint8_t* __restrict__ first, uint32_t u0_, uint32_t u1_)
+      : src(first), u0(u0_), u1(u1_), ulast(u1_ > u0_ ? u1_ - STRIDE : u0_) {}
 
   __device__ __forceinline__ void fetch(int s, uint32_t u) {
     const uint8_t* p = src + (size_t)min(u, ulast) * (NP * 1024);
@@ -81,7 +86,7 @@ struct UnitStream {
   __device__ __forceinline__ void prime() {
     if (u0 >= u1) return;
 #pragma unroll
-    for (int s = 0; s < D; s++) fetch(s, u0 + s);
+    for (int s = 0; s < D; s++) fetch(s, u0 + s * STRIDE);
   }
 
   template <class Body>
@@ -92,18 +97,18 @@ struct UnitStream {
   template <class Body>
   __device__ __forceinline__ void run_range(uint32_t a, uint32_t b, Body body) {
     if (u0 >= u1) return;
-    for (uint32_t u = a; u < b; u += D) {
+    for (uint32_t u = a; u < b; u += D * STRIDE) {
 #pragma unroll
       for (int s = 0; s < D; s++) {
-        if (u + s < u1) {
+        if (u + s * STRIDE < u1) {
           uint32_t w[NW];
 #pragma unroll
           for (int q = 0; q < NP; q++) {
             w[4 * q] = g[s][q].x; w[4 * q + 1] = g[s][q].y; w[4 * q + 2] = g[s][q].z; w[4 * q + 3] = g[s][q].w;
           }
-          body(u + s, w);
+          body(u + s * STRIDE, w);
         }
-        fetch(s, u + s + D);
+        fetch(s, u + (s + D) * STRIDE);
       }
     }
   }

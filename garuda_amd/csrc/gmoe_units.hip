@@ -577,7 +577,9 @@ struct DnAtomicArgs {
   float* out;
 };
 
-template <int QT, bool PACKED, int KS, class Stream>
+// PAIR: the workgroup's 32 rows, lanes l and l + 32 row r0 + l's sums over the even and
+// the odd units.
+template <int QT, bool PACKED, int KS, bool PAIR = false, class Stream>
 __device__ __forceinline__ void dn_atomic_chunk(Stream& st, const DnAtomicArgs& A, const float* accs, float* my,
                                                 const uint32_t* rows, uint8_t* acts, uint32_t mt, uint32_t m,
                                                 uint32_t slot0, uint32_t r0) {
@@ -619,14 +621,21 @@ __device__ __forceinline__ void dn_atomic_chunk(Stream& st, const DnAtomicArgs& 
   st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED>(w, acts, per, A.f, u, 0, nblk, my, m); });
   __syncthreads();
   if (wave == 0) {
-    const uint32_t row = r0 + lane;
+    const uint32_t l = PAIR ? (lane & 31u) : lane, row = r0 + l;
     for (uint32_t t = 0; t < m; t++) {
-      float y = accs[t * 64 + lane];
+      float y;
+      if constexpr (PAIR) {  // waves in order, each its even units' sum then its odd units'
+        y = accs[t * 64 + l] + accs[t * 64 + l + 32];
 #pragma unroll
-      for (int w2 = 1; w2 < KS; w2++) y += accs[(w2 * mt + t) * 64 + lane];
+        for (int w2 = 1; w2 < KS; w2++) y += accs[(w2 * mt + t) * 64 + l] + accs[(w2 * mt + t) * 64 + l + 32];
+      } else {
+        y = accs[t * 64 + lane];
+#pragma unroll
+        for (int w2 = 1; w2 < KS; w2++) y += accs[(w2 * mt + t) * 64 + lane];
+      }
       const uint32_t tok = lane_u(rtok, t), fl = lane_u(rfl, t);
       const float wt = __uint_as_float(lane_u(__float_as_uint(rwt), t));
-      if (row < A.d) {
+      if (row < A.d && (!PAIR || lane < 32)) {
         if (fl & 1u) atomicAdd(A.out + (size_t)tok * A.d + row, y * wt);
         if (fl & 2u) atomicAdd(A.out + (size_t)tok * A.d + row, __int_as_float(0x7fc00000));
       }
@@ -639,7 +648,12 @@ __device__ __forceinline__ void dn_atomic_chunk(Stream& st, const DnAtomicArgs& 
 // one 64-row tile of one expert over the whole K range (wave w its w-th share of the
 // units) and runs dn_atomic_chunk over its tokens.
 // grid.x = row tiles of d, grid.z = active-expert slot.
-template <int QT, bool PACKED, int KS, int RD = 2>
+// PAIR (grids of at most half as many workgroups as the chip has CUs, such as one token's
+// two experts): a workgroup takes half a tile, 32 rows, and each wave's two half-waves
+// stream alternate units of its share (lane l: row l % 32, units of parity l / 32), so
+// every load is still a whole 1 KiB (two 512-byte runs) and twice as many CUs issue them.
+// grid.x = 2 x row tiles.
+template <int QT, bool PACKED, int KS, int RD = 2, bool PAIR = false>
 __global__ void __launch_bounds__(64 * KS, 2)
 k_dn_atomic(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t mt, DnAtomicArgs A) {
   constexpr int U = UT_<QT>::U;
@@ -653,18 +667,30 @@ k_dn_atomic(const ExpertWork* __restrict__ work, uint32_t ne, uint32_t mt, DnAto
     if (m_all == 0) break;
     const uint32_t s0 = W->s0;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint32_t r0 = blockIdx.x * kTileRows;
     const uint32_t nunit = unit_count<QT>(A.f);
-    const uint32_t u0 = (nunit * wave) / KS, u1 = (nunit * (wave + 1)) / KS;
     float* my = accs + wave * mt * 64 + lane;
-    UnitStream<QT, RD> st(W->w[2] + (size_t)blockIdx.x * nunit * kTileRows * U, u0, u1, lane);
-    for (uint32_t c0 = 0; c0 < m_all; c0 += mt) {
-      const uint32_t m = min(mt, m_all - c0);
-      st.prime();
-      for (uint32_t t = threadIdx.x; t < m; t += blockDim.x) rows[t] = s0 + c0 + t;
-      for (uint32_t t = 0; t < m; t++) my[t * 64] = 0.0f;
-      __syncthreads();
-      dn_atomic_chunk<QT, PACKED, KS>(st, A, accs, my, rows, acts, mt, m, s0 + c0, r0);
+    auto chunks = [&](auto& st, uint32_t r0) {
+      for (uint32_t c0 = 0; c0 < m_all; c0 += mt) {
+        const uint32_t m = min(mt, m_all - c0);
+        st.prime();
+        for (uint32_t t = threadIdx.x; t < m; t += blockDim.x) rows[t] = s0 + c0 + t;
+        for (uint32_t t = 0; t < m; t++) my[t * 64] = 0.0f;
+        __syncthreads();
+        dn_atomic_chunk<QT, PACKED, KS, PAIR>(st, A, accs, my, rows, acts, mt, m, s0 + c0, r0);
+      }
+    };
+    if constexpr (PAIR) {
+      const uint32_t tx = blockIdx.x >> 1, hx = blockIdx.x & 1u, ph = lane >> 5, np = (nunit + 1) / 2;
+      const uint32_t p0 = (np * wave) / KS, p1 = (np * (wave + 1)) / KS;
+      const uint32_t u0 = 2 * p0 + ph;
+      uint32_t u1 = 2 * p1 + ph;
+      if (u1 > u0 && u1 - 2 >= nunit) u1 -= 2;  // an odd unit count: the last pair's odd half
+      UnitStream<QT, RD, 2> st(W->w[2] + (size_t)tx * nunit * kTileRows * U + 512 * hx + 16 * (lane & 31u), u0, u1);
+      chunks(st, tx * kTileRows + 32 * hx);
+    } else {
+      const uint32_t u0 = (nunit * wave) / KS, u1 = (nunit * (wave + 1)) / KS;
+      UnitStream<QT, RD> st(W->w[2] + (size_t)blockIdx.x * nunit * kTileRows * U, u0, u1, lane);
+      chunks(st, blockIdx.x * kTileRows);
     }
   }
 }
@@ -864,6 +890,9 @@ static hipError_t go_dn_rd(const LayerDev& L, const FwdBufs& B, uint32_t n, uint
 }
 
 constexpr int kDnAtomicKS = 8;
+// Grids of the fused down product up to this many workgroups (half of MI355X's 256 CUs)
+// run in half tiles (k_dn_atomic's PAIR form), twice as many.
+constexpr uint32_t kDnPairGrid = 128;
 
 static_assert(kFuseMaxTokens <= 64, "k_dn_atomic keeps a chunk's tokens one a lane");
 
@@ -879,12 +908,17 @@ static hipError_t go_dn_atomic_rd(const LayerDev& L, const FwdBufs& B, uint32_t 
   const uint32_t per = kDnAtomicKS * 64 * 4 + ActLds<QT, PACKED>::per_token(L.f) + 4;
   const uint32_t mt = min(n, (kLdsBudget - 16) / per);
   if (mt == 0) return hipErrorInvalidValue;
-  static const bool once = allow_lds(k_dn_atomic<QT, PACKED, kDnAtomicKS, RD>);
+  static const bool once = allow_lds(k_dn_atomic<QT, PACKED, kDnAtomicKS, RD>) &&
+                           allow_lds(k_dn_atomic<QT, PACKED, kDnAtomicKS, RD, true>);
   (void)once;
-  const dim3 g((L.d + kTileRows - 1) / kTileRows, 1, min(L.ne, n * L.k));
+  const uint32_t tiles = (L.d + kTileRows - 1) / kTileRows, slots = min(L.ne, n * L.k);
   const DnAtomicArgs A{L.f, L.d, L.k, B.spec, B.slot_tok, B.slot_of, B.slot_w, B.hq, B.hsc, B.hsum, B.hf, B.out};
-  hipLaunchKernelGGL((k_dn_atomic<QT, PACKED, kDnAtomicKS, RD>), g, dim3(64 * kDnAtomicKS), mt * per + 16, st, B.work,
-                     L.ne, mt, A);
+  if (tiles * slots <= kDnPairGrid)
+    hipLaunchKernelGGL((k_dn_atomic<QT, PACKED, kDnAtomicKS, RD, true>), dim3(2 * tiles, 1, slots),
+                       dim3(64 * kDnAtomicKS), mt * per + 16, st, B.work, L.ne, mt, A);
+  else
+    hipLaunchKernelGGL((k_dn_atomic<QT, PACKED, kDnAtomicKS, RD>), dim3(tiles, 1, slots), dim3(64 * kDnAtomicKS),
+                       mt * per + 16, st, B.work, L.ne, mt, A);
   return hipGetLastError();
 }
 
