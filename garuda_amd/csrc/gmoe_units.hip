@@ -761,6 +761,13 @@ constexpr uint32_t kDeepRingTokens = 1;
 // 194.5 us) measured slower, so they keep one tile and two unit sets.
 template <int QT>
 constexpr bool gu_pairs() { return QT == Q3_K; }
+// Unit sets in the gate/up ring from two tokens an expert on (one tile a workgroup): Q6_K's
+// 224-byte units make a set of 56 registers a lane, and with one set (171 VGPRs against
+// 247, two waves a SIMD either way) C4 (Q6_K gate/up, 4 tokens an expert) went from 189.7
+// to 185.0 us a call on one box; Q4_K keeps two (C2 batch 8: 170.1 -> 172.4 us with one).
+// Capped at three waves a SIMD (167 VGPRs, 2 spilled) Q6_K's took C4 to 191.2 us.
+template <int QT>
+constexpr int gu_ring() { return QT == Q6_K ? 1 : 2; }
 
 template <class K>
 static bool allow_lds(K kernel) {
@@ -944,7 +951,7 @@ hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const R
       if (n <= kDeepRingTokens) return go_gu<QT, true, 4>(L, B, n, ra, st);
       if (n * L.k <= L.ne) return go_gu<QT, true, 1>(L, B, n, ra, st);
       if constexpr (gu_pairs<QT>()) return go_gu<QT, true, 1, 2>(L, B, n, ra, st);
-      return go_gu<QT, true, 2>(L, B, n, ra, st);
+      return go_gu<QT, true, gu_ring<QT>()>(L, B, n, ra, st);
     }
   }
   return go_gu<QT, false, 2>(L, B, n, ra, st);
