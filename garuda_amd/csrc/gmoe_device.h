@@ -379,6 +379,25 @@ __device__ __forceinline__ float wave64_max(float v) {
   p = xor32_pair(v);
   return fmaxf(p.a, p.b);
 }
+// The same butterfly for an unsigned 64-bit maximum, each level moving the two halves
+// (the permlane swaps leave both halves of a lane's pair in the same order).
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  return ((uint64_t)(uint32_t)dpp_i<CTRL>((int)(v >> 32)) << 32) | (uint32_t)dpp_i<CTRL>((int)(uint32_t)v);
+}
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t wave64_max_u64(uint64_t v) {
+  v = max_u64(v, dpp_u64<kDppXor1>(v));
+  v = max_u64(v, dpp_u64<kDppXor2>(v));
+  v = max_u64(v, dpp_u64<kDppHalfMirror>(v));
+  v = max_u64(v, dpp_u64<kDppMirror>(v));
+  auto pl = __builtin_amdgcn_permlane16_swap((int)(uint32_t)v, (int)(uint32_t)v, false, false);
+  auto ph = __builtin_amdgcn_permlane16_swap((int)(v >> 32), (int)(v >> 32), false, false);
+  v = max_u64(((uint64_t)(uint32_t)ph[0] << 32) | (uint32_t)pl[0], ((uint64_t)(uint32_t)ph[1] << 32) | (uint32_t)pl[1]);
+  pl = __builtin_amdgcn_permlane32_swap((int)(uint32_t)v, (int)(uint32_t)v, false, false);
+  ph = __builtin_amdgcn_permlane32_swap((int)(v >> 32), (int)(v >> 32), false, false);
+  return max_u64(((uint64_t)(uint32_t)ph[0] << 32) | (uint32_t)pl[0], ((uint64_t)(uint32_t)ph[1] << 32) | (uint32_t)pl[1]);
+}
 
 // One row's residual add and RMSNorm by the block's first 256 threads; every thread of
 // the block calls it (it holds one barrier). With y, x += y first (written back); with SL,
@@ -836,11 +855,7 @@ __device__ void gate_wave_wide(uint32_t gating, uint32_t ne, uint32_t k, const f
       uint64_t best = 0ull;
 #pragma unroll
       for (int j = 0; j < EPL; j++) best = key[j] > best ? key[j] : best;
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) {
-        const uint64_t b = (uint64_t)__shfl_xor((long long)best, o, 64);
-        best = b > best ? b : best;
-      }
+      best = wave64_max_u64(best);  // DPP and permlane levels: no LDS round trip a level
       const uint32_t e = 0xffffffffu - (uint32_t)best;
 #pragma unroll
       for (int j = 0; j < EPL; j++)

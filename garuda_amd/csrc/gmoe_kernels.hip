@@ -541,6 +541,19 @@ __global__ void __launch_bounds__(64) k_front_wide(LayerDev L, FwdBufs B, uint32
   __shared__ uint32_t gsc[64];  // gating scratch: 2k words (k <= 32)
   const uint32_t ne = L.ne, k = L.k, d = L.d, lane = threadIdx.x, t = blockIdx.x;
   const float* hs = B.hs + (size_t)t * d;
+  // the quantiser's first block a lane (block `lane` of the row), loaded first so that its
+  // latency hides behind the gating
+  const uint32_t nblk = d / 32;
+  const bool pre = quant && lane < nblk;
+  float v0[32];
+  if (pre) {
+    const float4* src = reinterpret_cast<const float4*>(hs + (size_t)lane * 32);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float4 t4 = src[i];
+      v0[4 * i] = t4.x; v0[4 * i + 1] = t4.y; v0[4 * i + 2] = t4.z; v0[4 * i + 3] = t4.w;
+    }
+  }
   float x[kWideEPL];
 #pragma unroll
   for (int j = 0; j < kWideEPL; j++) {
@@ -573,9 +586,12 @@ __global__ void __launch_bounds__(64) k_front_wide(LayerDev L, FwdBufs B, uint32
     B.ids[(size_t)t * k + lane] = id;
     B.w[(size_t)t * k + lane] = w;
   }
+  if (pre) {
+    const size_t gb = (size_t)t * nblk + lane;
+    quant32(v0, B.xq + gb * 32, B.xs + gb, B.xsum, gb, sum_kind_of(L.qt_gate), sum_offset_of(L.qt_gate));
+  }
   if (quant) {
-    const uint32_t nblk = d / 32;
-    for (uint32_t b = lane; b < nblk; b += 64) {
+    for (uint32_t b = lane + 64; b < nblk; b += 64) {
       float v[32];
       const float4* src = reinterpret_cast<const float4*>(hs + (size_t)b * 32);
 #pragma unroll
