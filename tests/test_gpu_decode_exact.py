@@ -97,3 +97,36 @@ def test_split_gateup_is_bit_exact(dev, qt, d):
                                    f"{got.reshape(-1)[bad[0]]!r} vs {want.reshape(-1)[bad[0]]!r}")
     finally:
         layer.release()
+
+
+@pytest.mark.parametrize("f", [768, 1280])
+def test_single_token_down_in_half_tiles(dev, f):
+    """One token's down product runs in half tiles whose half-waves stream alternate units
+    (k_dn_atomic's PAIR form); with 3 or 5 units a row (f 768, 1280) the last pair has one
+    unit. The one-hot down keeps the output bit-exact whatever the summation order, so
+    every row of every half tile must be the reference's."""
+    d, ne, k, qt = 512, 8, 2, G.Q4_K
+    rng = np.random.default_rng(290 + f)
+    gate = M.quantize(qt, rng.normal(0, 0.05, ne * f * d).astype(np.float32))
+    up = M.quantize(qt, rng.normal(0, 0.05, ne * f * d).astype(np.float32))
+    down = onehot_down(rng, ne, d, f)
+    u = M.skew_direction(291 + f, d)
+    router = M.skew_router(rng.normal(0, 0.02, ne * d).astype(np.float32), ne, d, u)
+    qts = (qt, qt, G.Q8_0)
+    layer = G.MoeLayer(dev, d, f, ne, k, router, gate, up, down, qts, math=G.MATH_PACKED)
+    L = dict(d=d, f=f, ne=ne, k=k, gating=0, combine=0, packed=1, router=router, qtypes=qts,
+             gate=gate, up=up, down=down)
+    try:
+        for n in (1, 2, 1):
+            say(f"half-tile down, f={f}, n={n}")
+            hs = M.skew_tokens(rng.normal(0, 1, (n, d)).astype(np.float32), u)
+            out, ids, w = layer.feed_forward_batch(hs)
+            wout, wids, ww = O.feed_forward_batch(L, hs, threads=min(16, len(os.sched_getaffinity(0))))
+            assert np.array_equal(ids, wids), "routing differs"
+            got = out.astype(np.float32)
+            want = np.asarray(wout, dtype=np.float32)
+            bad = np.flatnonzero(bits(got) != bits(want))
+            assert bad.size == 0, (f"n={n}: {bad.size} outputs differ, first at {bad[0]}: "
+                                   f"{got.reshape(-1)[bad[0]]!r} vs {want.reshape(-1)[bad[0]]!r}")
+    finally:
+        layer.release()
