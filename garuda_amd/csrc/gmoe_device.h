@@ -1021,7 +1021,8 @@ __device__ __forceinline__ void route_logit(const RouteArgs& r, uint32_t x, floa
 // its logits, ids and weights and the combine's (slot, weight) pairs, and bumps `routed`
 // (when given) after a release fence. With cand, the token's candidate experts in
 // ascending id (LDS, nc of them, one token a call), a routed pair's slot is its
-// expert's rank among them; otherwise the search of route_comb finds it. sec: a
+// expert's rank among them; otherwise the search of route_comb finds it (nothing with
+// comb_slot null: the routing alone). sec: a
 // multiple of 64 (d too), lds: route_token_lds floats.
 // Every thread of the workgroup calls this; ne <= 64.
 // ---------------------------------------------------------------------------------
@@ -1104,7 +1105,8 @@ __device__ __forceinline__ void route_token(const RouteArgs& r, uint32_t t, floa
     r.ids[(size_t)t * r.k + lane] = id;
     r.w[(size_t)t * r.k + lane] = w;
   }
-  if (cand) {  // one token, its candidates cand[0..nc) (LDS): a routed pair's slot is its rank
+  if (!r.comb_slot) {  // the routing alone (k_route_tok)
+  } else if (cand) {  // one token, its candidates cand[0..nc) (LDS): a routed pair's slot is its rank
     uint32_t p = lane;
     if (r.combine == 0) {
       p = 0;

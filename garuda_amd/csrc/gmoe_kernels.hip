@@ -1097,7 +1097,42 @@ hipError_t launch_spec_front(const LayerDev& L, const FwdBufs& B, uint32_t n, in
   return hipGetLastError();
 }
 
+// Exact routing of one token a workgroup (route_token): lanes of wave 0 run the ne
+// sequential chains (simd/mod.rs:13-16) over the products the other seven waves put in LDS
+// a section ahead, then gate the token (gate_wave). For ne <= 64 and d a multiple of 64 it
+// replaces k_route's one thread a chain, which waits for its loads a batch at a time (68
+// us a single-token call at d 4096, 8 experts).
+constexpr int kRouteTokThreads = 512;
+__global__ void __launch_bounds__(kRouteTokThreads) k_route_tok(RouteArgs r) {
+  extern __shared__ float rt_lds[];
+  route_token(r, blockIdx.x, rt_lds, r.sec, nullptr);
+}
+
 hipError_t launch_route(const LayerDev& L, const FwdBufs& B, uint32_t n, hipStream_t st) {
+  if (!B.logits_in && L.ne <= 64 && L.d % 64 == 0) {
+    RouteArgs r{};
+    r.router = L.router;
+    r.hs = B.hs;
+    r.logits = B.logits;
+    r.ids = B.ids;
+    r.w = B.w;
+    r.n = n;
+    r.ne = L.ne;
+    r.k = L.k;
+    r.d = L.d;
+    r.gating = L.gating;
+    r.combine = L.combine;
+    // sections: the longest multiple of 64 values (at most 1024, at least 64) whose two
+    // halves of products fit 64 KB
+    const uint32_t fit = (65536u / (8u * L.ne) - 4u) & ~63u;
+    r.sec = std::min(L.d, std::max(64u, std::min(fit, 1024u)));
+    const size_t lds = (size_t)route_token_lds(L.ne, L.k, r.sec) * 4;
+    static const bool once = hipFuncSetAttribute((const void*)k_route_tok,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) == hipSuccess;
+    (void)once;
+    hipLaunchKernelGGL(k_route_tok, dim3(n), dim3(kRouteTokThreads), lds, st, r);
+    return hipGetLastError();
+  }
   uint32_t tpb = L.ne >= kRouteThreads ? 1u : kRouteThreads / L.ne;
   size_t shm = (size_t)tpb * L.ne * 4 + tpb * 4 + (size_t)tpb * L.k * 8;
   hipLaunchKernelGGL(k_route, dim3((n + tpb - 1) / tpb), dim3(kRouteThreads), shm, st, L, B, n);
