@@ -648,8 +648,31 @@ __device__ __forceinline__ void pk_q6k(const uint32_t* w, uint32_t m, Tok tok) {
   }
 }
 
+// The words O(s, 2h), O(s, 2h + 1) of sub-block s = s0 + k of a Q3_K slab unit (values
+// v = q2 + 4 * hbit, one a byte) from lane half h's three words t0, t1, t2 of its
+// sub-group (q3s_word); k is a constant once the callers' loops unroll.
+__device__ __forceinline__ void q3s_pair(uint32_t t0, uint32_t t1, uint32_t t2, int k, uint32_t& o0, uint32_t& o1) {
+  if (k == 3) {
+    o0 = ((t0 >> 6) & 0x03030303u) | ((t2 >> 4) & 0x04040404u);
+    o1 = ((t1 >> 6) & 0x03030303u) | ((t2 >> 5) & 0x04040404u);
+  } else {
+    const uint32_t t = k == 0 ? t0 : k == 1 ? t1 : t2;
+    o0 = t & 0x07070707u;
+    o1 = (t >> 3) & 0x07070707u;
+  }
+}
+
+// The four words of sub-block s of a Q3_K slab unit w.
+__device__ __forceinline__ void q3s_words(const uint32_t* w, int s, uint32_t* q) {
+  const uint32_t c = s / 8, x0 = 3 * ((s % 8) / 4);
+#pragma unroll
+  for (uint32_t h = 0; h < 2; h++)
+    q3s_pair(w[q3s_word(c, h, x0)], w[q3s_word(c, h, x0 + 1)], w[q3s_word(c, h, x0 + 2)], s % 4, q[2 * h],
+             q[2 * h + 1]);
+}
+
 // quant/mod.rs:503-540. q = ((qs >> shift) & 3) - (hmask bit ? 0 : 4), dotted as
-// (low2 | hbit << 2) then -4*sum.
+// v = low2 | hbit << 2 (the slab unit's regrouped values, q3s_words) then -4*sum.
 template <class Tok>
 __device__ __forceinline__ void pk_q3k(const uint32_t* w, uint32_t m, Tok tok) {
   float d_all = f16f(w[27]);
@@ -657,14 +680,8 @@ __device__ __forceinline__ void pk_q3k(const uint32_t* w, uint32_t m, Tok tok) {
   q3k_scales(w[24], w[25], w[26], sc4);
 #pragma unroll
   for (int s = 0; s < 16; s++) {
-    const int half = s / 8, j = (s % 8) / 2, o = 16 * (s % 2);
     uint32_t q[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      uint32_t qs = w[(32 + 32 * half + o) / 4 + i];
-      uint32_t hm = w[o / 4 + i];
-      q[i] = ((qs >> (2 * j)) & 0x03030303u) | (((hm >> (4 * half + j)) & 0x01010101u) << 2);
-    }
+    q3s_words(w, s, q);
     float dl = d_all * (float)((int)(int8_t)byte_of(sc4, s) - 32);
     for (uint32_t t = 0; t < m; t++) {
       const auto a = tok(t);

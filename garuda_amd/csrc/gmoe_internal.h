@@ -122,6 +122,42 @@ __host__ __device__ inline int64_t unit_src_byte(uint32_t t, const Unit& u, uint
   return (int64_t)((b0 + g) * u.B + b % u.B);
 }
 
+// Q3_K units in the slab. A packed Q3_K block (quant/mod.rs:503-540, :840-875) keeps each
+// value v = q2 + 4 * hbit (0..7; the quant is v - 4) in two bit planes, qs and hmask, and
+// putting a word of four values together again from them takes four operations. Bytes
+// 0..95 of a slab unit hold the same values regrouped (bytes 96..109, the scales and d,
+// are the block's). With O(s, i) the word of values 4i..4i+3 of sub-block s (one a byte),
+// chunk c (sub-blocks 8c..8c+7) fills bytes 48c..48c+47, and in it sub-group r
+// (sub-blocks s0 = 8c + 4r .. s0 + 3) and lane half h (words i = 2h, 2h + 1) own three
+// words T0, T1, T2, word Tk at byte 48c + 16 (x / 2) + 8h + 4 (x % 2), x = 3r + k:
+//   T0 = O(s0, 2h)     | O(s0, 2h + 1) << 3     | (O(s0 + 3, 2h) & 3) << 6
+//   T1 = O(s0 + 1, 2h) | O(s0 + 1, 2h + 1) << 3 | (O(s0 + 3, 2h + 1) & 3) << 6
+//   T2 = O(s0 + 2, 2h) | O(s0 + 2, 2h + 1) << 3 | (O(s0 + 3, 2h) >> 2) << 6 | (O(s0 + 3, 2h + 1) >> 2) << 7
+// (each shift within its byte). A word of sub-blocks s0..s0 + 2 then takes two operations
+// and one of s0 + 3 four (q3s_pair), and the two halves of a 16-value MFMA step find
+// their words 8 bytes apart in one 16-byte piece.
+__host__ __device__ constexpr uint32_t q3s_word(uint32_t c, uint32_t h, uint32_t x) {
+  return 12 * c + 4 * (x / 2) + 2 * h + x % 2;
+}
+// Value l of sub-block s of packed Q3_K block blk, as v = q2 + 4 * hbit (the is-th
+// sub-block of quant/mod.rs:520-533: shift 2j of qs byte 32 half + 16 (s % 2) + l, mask
+// bit 4 half + j of hmask byte 16 (s % 2) + l).
+__host__ __device__ inline uint32_t q3k_value(const uint8_t* blk, uint32_t s, uint32_t l) {
+  const uint32_t half = s / 8, j = (s % 8) / 2, off = 16 * (s % 2);
+  return ((blk[32 + 32 * half + off + l] >> (2 * j)) & 3u) | (((blk[off + l] >> (4 * half + j)) & 1u) << 2);
+}
+// Byte b < 96 of the slab unit of packed Q3_K block blk.
+__host__ __device__ inline uint8_t q3s_byte(const uint8_t* blk, uint32_t b) {
+  const uint32_t c = b / 48, rem = b % 48, x = 2 * (rem / 16) + (rem % 8) / 4, h = (rem % 16) / 8, e = b % 4;
+  const uint32_t k = x % 3, s0 = 8 * c + 4 * (x / 3);
+  auto o = [&](uint32_t s, uint32_t i) { return q3k_value(blk, s, 4 * i + e); };
+  uint32_t v = o(s0 + k, 2 * h) | o(s0 + k, 2 * h + 1) << 3;
+  if (k == 0) v |= (o(s0 + 3, 2 * h) & 3u) << 6;
+  else if (k == 1) v |= (o(s0 + 3, 2 * h + 1) & 3u) << 6;
+  else v |= (o(s0 + 3, 2 * h) >> 2) << 6 | (o(s0 + 3, 2 * h + 1) >> 2) << 7;
+  return (uint8_t)v;
+}
+
 // One active expert of a call as the expert kernels read it, in a single load: the
 // dispatch writes entry a for the a-th active expert (ascending id) and m = 0 for the
 // entries after the last one.

@@ -1174,9 +1174,13 @@ k_tile_rows(uint32_t qt, const uint8_t* __restrict__ raw, uint32_t r0, uint32_t 
   uint32_t v[4] = {0, 0, 0, 0};
   if (rl < nrows && row < rows) {
     const uint8_t* src = raw + (uint64_t)rl * rb;
-    for (uint32_t b = 0; b < 16; b++) {
-      int64_t s = unit_src_byte(qt, un, nblk, u, p * 16 + b);
-      if (s >= 0) v[b / 4] |= (uint32_t)src[s] << (8 * (b % 4));
+    if (qt == Q3_K && p < 6) {  // the regrouped values (q3s_byte); the unit is one block
+      for (uint32_t b = 0; b < 16; b++) v[b / 4] |= (uint32_t)q3s_byte(src + (uint64_t)u * un.B, p * 16 + b) << (8 * (b % 4));
+    } else {
+      for (uint32_t b = 0; b < 16; b++) {
+        int64_t s = unit_src_byte(qt, un, nblk, u, p * 16 + b);
+        if (s >= 0) v[b / 4] |= (uint32_t)src[s] << (8 * (b % 4));
+      }
     }
   }
   const uint64_t tile = r0 / kTileRows + lt;

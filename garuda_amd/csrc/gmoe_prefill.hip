@@ -83,9 +83,9 @@ template <> struct PF<Q6_K> {  // ql[128] | qh[64] | scales[16] | d
   static constexpr int EU = 256, KC = 128, NPC = 8, SU16 = 1, SW = 0, NW = 4;
   static constexpr int piece(int c, int i) { return i < 4 ? 4 * c + i : i < 6 ? 8 + 2 * c + (i - 4) : 12 + (i - 6); }
 };
-template <> struct PF<Q3_K> {  // hmask[32] | qs[64] | scales[12] d
-  static constexpr int EU = 256, KC = 128, NPC = 5, SU16 = 16, SW = 0, NW = 8;
-  static constexpr int piece(int c, int i) { return i < 2 ? i : i < 4 ? 2 + 2 * c + (i - 2) : 6; }
+template <> struct PF<Q3_K> {  // values regrouped (q3s_word): sub-blocks 8c.. in pieces 3c..3c+2 | scales[12] d
+  static constexpr int EU = 256, KC = 128, NPC = 4, SU16 = 16, SW = 0, NW = 8;
+  static constexpr int piece(int c, int i) { return i < 3 ? 3 * c + i : 6; }
 };
 template <> struct PF<Q2_K> {  // scales[16] | qs[64] | d dmin
   static constexpr int EU = 256, KC = 128, NPC = 4, SU16 = 16, SW = 16, NW = 8;
@@ -264,21 +264,37 @@ template <> struct Dec<Q6_K> {
   static __device__ __forceinline__ void mins(const uint8_t*, uint32_t, half8&, half8&) {}
 };
 
+// Q3_K step S (sub-block S) of chunk C: lane half h's words O(S, 2h), O(S, 2h + 1) of the
+// regrouped values v = q2 + 4 * hbit (q3s_word: the half's three words of the sub-group
+// sit at bytes 48C + 16 (x / 2) + 4 (x % 2) + 8h of the unit).
+template <int C, int S>
+__device__ __forceinline__ u32x2 q3s_step(const uint8_t* row, uint32_t h) {
+  constexpr int x0 = 3 * ((S % 8) / 4), k = S % 4;
+  auto word = [&](auto xc) {
+    constexpr int x = decltype(xc)::value;
+    return *reinterpret_cast<const uint32_t*>(pf_at<Q3_K, C, 48 * C + 16 * (x / 2) + 4 * (x % 2)>(row) + 8 * h);
+  };
+  uint32_t b0, b1;
+  if constexpr (k == 3) {
+    q3s_pair(word(std::integral_constant<int, x0>{}), word(std::integral_constant<int, x0 + 1>{}),
+             word(std::integral_constant<int, x0 + 2>{}), k, b0, b1);
+  } else {
+    const uint32_t t = word(std::integral_constant<int, x0 + k>{});
+    q3s_pair(t, t, t, k, b0, b1);
+  }
+  return u32x2{b0, b1};
+}
+
 template <> struct Dec<Q3_K> {
   static constexpr int QT = Q3_K;
   template <int C, int S>
   static __device__ __forceinline__ half8 frag(const uint8_t* row, uint32_t h) {
-    constexpr int n = S / 8, j4 = (S % 8) / 2, is = 8 * n + 2 * j4 + S % 2;
-    const u32x2 hm = ld8(pf_at<QT, C, 16 * (S % 2)>(row) + 8 * h);
-    const u32x2 qs = ld8(pf_at<QT, C, 32 + 32 * n + 16 * (S % 2)>(row) + 8 * h);
+    constexpr int is = S;
     const u32x4 tl = ld16(pf_at<QT, C, 96>(row));  // scales[12] | d
     uint32_t sc4[4];
     q3k_scales(tl.x, tl.y, tl.z, sc4);
     const int scs = (int)((sc4[is / 4] >> (8 * (is % 4))) & 0xffu) - 32;
-    u32x2 b;  // q2 + 4 * hbit in [0, 7]; the value is b - 4
-#pragma unroll
-    for (int d = 0; d < 2; d++)
-      b[d] = ((qs[d] >> (2 * j4)) & 0x03030303u) | (((hm[d] >> (4 * n + j4)) & 0x01010101u) << 2);
+    const u32x2 b = q3s_step<C, S>(row, h);  // q2 + 4 * hbit in [0, 7]; the value is b - 4
     half8 o;
     const half2_t s2 = h2s((_Float16)(float)scs);
 #pragma unroll
@@ -756,13 +772,7 @@ template <> struct PQ<Q3_K> {
   static constexpr int QT = Q3_K, SBW = 16, SWS = 0;
   template <int C, int S>
   static __device__ __forceinline__ half8 qfrag(const uint8_t* row, uint32_t h) {
-    constexpr int n = S / 8, j4 = (S % 8) / 2;
-    const u32x2 hm = ld8(pf_at<QT, C, 16 * (S % 2)>(row) + 8 * h);
-    const u32x2 qs = ld8(pf_at<QT, C, 32 + 32 * n + 16 * (S % 2)>(row) + 8 * h);
-    u32x2 b;  // q2 + 4 * hbit in [0, 7]; the quant is b - 4
-#pragma unroll
-    for (int d = 0; d < 2; d++)
-      b[d] = ((qs[d] >> (2 * j4)) & 0x03030303u) | (((hm[d] >> (4 * n + j4)) & 0x01010101u) << 2);
+    const u32x2 b = q3s_step<C, S>(row, h);  // q2 + 4 * hbit in [0, 7]; the quant is b - 4
     return bytes_fma(b, h2s((_Float16)1.0f), h2s((_Float16)-1028.0f));
   }
   template <int C, int SB>

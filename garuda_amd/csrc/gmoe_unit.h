@@ -40,6 +40,19 @@ __device__ __forceinline__ void unit_deq32(const uint32_t* w, int q, float* out)
     }
   } else if constexpr (QT == F16) {
     deq32<F16>(w + 16 * q, 0, out);
+  } else if constexpr (QT == Q3_K) {  // deq32<Q3_K>'s arithmetic over the regrouped values
+    const float d_all = f16f(w[27]);
+    uint32_t sc4[4];
+    q3k_scales(w[24], w[25], w[26], sc4);
+#pragma unroll
+    for (int sb = 0; sb < 2; sb++) {
+      const int s = 2 * q + sb;
+      uint32_t v[4];
+      q3s_words(w, s, v);
+      const float dl = d_all * (float)((int)(int8_t)byte_of(sc4, s) - 32);
+#pragma unroll
+      for (int l = 0; l < 16; l++) out[16 * sb + l] = dl * (float)((int)byte_of(v, l) - 4);
+    }
   } else {
     deq32<QT>(w, q, out);
   }
