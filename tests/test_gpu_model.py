@@ -423,7 +423,7 @@ def gpu_model_packed_table(dev, w, embd_qt, math, max_positions=64, tied=True):
     return (model, kv, moe, dense, head), table, ohead
 
 
-@pytest.mark.parametrize("embd_qt", [G.Q6_K, G.Q8_0, G.Q4_K])
+@pytest.mark.parametrize("embd_qt", [G.Q6_K, G.Q8_0, G.Q4_K, G.Q3_K])
 def test_packed_token_table_with_tied_head(dev, weights, embd_qt):
     """token_embd kept packed in HBM (Weight::Packed): each token's row is dequantised on the
     device, bit for bit the reference's dequantize (the first layer's residual input is
