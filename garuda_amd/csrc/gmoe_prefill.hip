@@ -26,9 +26,10 @@
 // workgroups take NW * 32 rows of f (both matrices: 256 for NW = 8), down workgroups NW *
 // 64 rows of d. Each wave owns two 32-row MFMA row tiles (gate and up of its 32 rows, or
 // two 32-row halves of its 64 down rows) and both 32-token tiles: 4 accumulators of 32x32,
-// plus 4 of partial block sums. Per chunk of K (128 values, 64 for F16) the workgroup copies the
-// chunk's raw 16-byte pieces of its rows (the slab's tiled layout makes each piece of 64
-// rows one 1 KiB run) and the tokens' hi/lo activations into LDS; a lane then decodes
+// plus 4 of partial block sums. Per chunk of K (PF<QT>::KC values: 128; 64 for Q5_K and
+// Q8_0, 32 for F16) the workgroup copies the chunk's raw 16-byte pieces of its rows (the
+// slab's tiled layout makes each piece of 64 rows one 1 KiB run) and the tokens' hi/lo
+// activations into LDS; a lane then decodes
 // its row's 8 values of each 16-value K step straight into the MFMA B operand.
 //
 // v_mfma_f32_32x32x16_f16 (operand layout checked on the device): lane l supplies row
