@@ -152,6 +152,19 @@ __device__ __forceinline__ half8 bytes_fma(u32x2 b, half2_t mul, half2_t add) {
   return o;
 }
 
+// 8 bytes (two dwords) -> 8 fp16 values byte * 2^-24: each byte beside a zero byte, the
+// fp16 subnormal of that mantissa (exact for bytes < 1024).
+__device__ __forceinline__ half8 bytes_sub(u32x2 b) {
+  half8 o;
+#pragma unroll
+  for (int d = 0; d < 2; d++) {
+    const half2_t p0 = h2(__builtin_amdgcn_perm(0u, b[d], 0x0c010c00u));
+    const half2_t p1 = h2(__builtin_amdgcn_perm(0u, b[d], 0x0c030c02u));
+    o[4 * d] = p0.x; o[4 * d + 1] = p0.y; o[4 * d + 2] = p1.x; o[4 * d + 3] = p1.y;
+  }
+  return o;
+}
+
 __device__ __forceinline__ _Float16 fh(uint32_t v) { return (_Float16)(float)v; }
 // The low half of v as f32 (a scale or min; non-finite ones give non-finite outputs).
 __device__ __forceinline__ float f16v(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)v); }
@@ -717,13 +730,15 @@ template <> struct PQ<Q4_K> {
     const uint32_t mask = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
     q.x &= mask;
     q.y &= mask;
-    // low nibble: (1024 + q) - 1024; high nibble in place (16q): (1024 + 16q) / 16 - 64
-    return high ? bytes_fma(q, h2s((_Float16)0.0625f), h2s((_Float16)-64.0f))
-                : bytes_fma(q, h2s((_Float16)1.0f), h2s((_Float16)-1024.0f));
+    // the quants as fp16 subnormals, q * 2^-24 (a high nibble in place, 16q * 2^-24): the
+    // sub-block's dot comes out as dot * 2^-24 (2^-20), exact, and rowf scales d * sc by
+    // the inverse power of two, so (d * sc) * dot is the same single rounding
+    return bytes_sub(q);
   }
   template <int C, int SB>
   static __device__ __forceinline__ void rowf(const uint8_t* row, float* rf) {
     kq_rowf<SB>(ld16(pf_at<QT, C, 0>(row)), rf);
+    rf[0] *= (SB & 1) ? 0x1p20f : 0x1p24f;
   }
   static __device__ __forceinline__ float term(float dot, const float* rf, float xs, float s) {
     return xs * (rf[0] * dot - rf[1] * s);
@@ -741,11 +756,12 @@ template <> struct PQ<Q5_K> {
 #pragma unroll
     for (int d = 0; d < 2; d++)
       b[d] = ((sb & 1 ? ql[d] >> 4 : ql[d]) & 0x0f0f0f0fu) | (((qh[d] >> sb) & 0x01010101u) << 4);
-    return bytes_fma(b, h2s((_Float16)1.0f), h2s((_Float16)-1024.0f));
+    return bytes_sub(b);  // q * 2^-24, as for Q4_K
   }
   template <int C, int SB>
   static __device__ __forceinline__ void rowf(const uint8_t* row, float* rf) {
     kq_rowf<SB>(ld16(pf_at<QT, C, 0>(row)), rf);
+    rf[0] *= 0x1p24f;
   }
   static __device__ __forceinline__ float term(float dot, const float* rf, float xs, float s) {
     return xs * (rf[0] * dot - rf[1] * s);
@@ -798,14 +814,14 @@ template <> struct PQ<Q2_K> {
     u32x2 b;
 #pragma unroll
     for (int d = 0; d < 2; d++) b[d] = (qs[d] >> (2 * j4)) & 0x03030303u;
-    return bytes_fma(b, h2s((_Float16)1.0f), h2s((_Float16)-1024.0f));
+    return bytes_sub(b);  // q * 2^-24, as for Q4_K
   }
   template <int C, int SB>
   static __device__ __forceinline__ void rowf(const uint8_t* row, float* rf) {
     const u32x4 scb = ld16(pf_at<QT, C, 0>(row));
     const uint32_t dd = ld16(pf_at<QT, C, 80>(row)).x;
     const uint32_t sc = (scb[SB / 4] >> (8 * (SB % 4))) & 0xffu;
-    rf[0] = f16v(dd) * (float)(sc & 15u);
+    rf[0] = f16v(dd) * (float)(sc & 15u) * 0x1p24f;
     rf[1] = f16v(dd >> 16) * (float)(sc >> 4);
   }
   static __device__ __forceinline__ float term(float dot, const float* rf, float xs, float s) {
