@@ -153,7 +153,9 @@ __device__ __forceinline__ half8 bytes_fma(u32x2 b, half2_t mul, half2_t add) {
 }
 
 // 8 bytes (two dwords) -> 8 fp16 values byte * 2^-24: each byte beside a zero byte, the
-// fp16 subnormal of that mantissa (exact for bytes < 1024).
+// fp16 subnormal of that mantissa (exact for bytes < 1024). The MFMAs keep fp16
+// subnormals under the kernels' default float mode (no flush-to-zero flag is set here);
+// the packed-prefill tests compare every output bit for bit.
 __device__ __forceinline__ half8 bytes_sub(u32x2 b) {
   half8 o;
 #pragma unroll
