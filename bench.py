@@ -261,7 +261,8 @@ def prefill_leg(a, dev, mats, threads, stream, timed, cpu, packed=False):
             "packed arithmetic adds one float term per 32-value sub-block per (row, token) of gate/up, five VALU "
             "operations evaluated in K order, which bound k_pq near 20% of peak" if packed else
             "algorithmic flops (sum of expert tokens x 6 d f) over the two MFMA launches' "
-            "time; the exact-product scheme issues two fp16 MFMA passes per product")
+            "time; the exact-product scheme issues two fp16 MFMA passes per product (with the min-term "
+            "passes and padded token tiles 2.46x the algorithmic work), which bound k_pf near 36% of peak")
     return {
         "cpu_baseline": cpu_rec,
         "workload": f"C3 prefill: the C2 layer at {n} tokens, Zipf(1.1)-skewed routing, {mname} math, "
