@@ -648,20 +648,6 @@ __device__ __forceinline__ void pk_q6k(const uint32_t* w, uint32_t m, Tok tok) {
   }
 }
 
-// The words O(s, 2h), O(s, 2h + 1) of sub-block s = s0 + k of a Q3_K slab unit (values
-// v = q2 + 4 * hbit, one a byte) from lane half h's three words t0, t1, t2 of its
-// sub-group (q3s_word); k is a constant once the callers' loops unroll.
-__device__ __forceinline__ void q3s_pair(uint32_t t0, uint32_t t1, uint32_t t2, int k, uint32_t& o0, uint32_t& o1) {
-  if (k == 3) {
-    o0 = ((t0 >> 6) & 0x03030303u) | ((t2 >> 4) & 0x04040404u);
-    o1 = ((t1 >> 6) & 0x03030303u) | ((t2 >> 5) & 0x04040404u);
-  } else {
-    const uint32_t t = k == 0 ? t0 : k == 1 ? t1 : t2;
-    o0 = t & 0x07070707u;
-    o1 = (t >> 3) & 0x07070707u;
-  }
-}
-
 // The four words of sub-block s of a Q3_K slab unit w.
 __device__ __forceinline__ void q3s_words(const uint32_t* w, int s, uint32_t* q) {
   const uint32_t c = s / 8, x0 = 3 * ((s % 8) / 4);

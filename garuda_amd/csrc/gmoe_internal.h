@@ -139,6 +139,20 @@ __host__ __device__ inline int64_t unit_src_byte(uint32_t t, const Unit& u, uint
 __host__ __device__ constexpr uint32_t q3s_word(uint32_t c, uint32_t h, uint32_t x) {
   return 12 * c + 4 * (x / 2) + 2 * h + x % 2;
 }
+// The words O(s, 2h), O(s, 2h + 1) of sub-block s = s0 + k of a Q3_K slab unit (values
+// v = q2 + 4 * hbit, one a byte) from lane half h's three words t0, t1, t2 of its
+// sub-group (q3s_word); k is a constant once the callers' loops unroll.
+__host__ __device__ __forceinline__ void q3s_pair(uint32_t t0, uint32_t t1, uint32_t t2, int k, uint32_t& o0,
+                                                  uint32_t& o1) {
+  if (k == 3) {
+    o0 = ((t0 >> 6) & 0x03030303u) | ((t2 >> 4) & 0x04040404u);
+    o1 = ((t1 >> 6) & 0x03030303u) | ((t2 >> 5) & 0x04040404u);
+  } else {
+    const uint32_t t = k == 0 ? t0 : k == 1 ? t1 : t2;
+    o0 = t & 0x07070707u;
+    o1 = (t >> 3) & 0x07070707u;
+  }
+}
 // Value l of sub-block s of packed Q3_K block blk, as v = q2 + 4 * hbit (the is-th
 // sub-block of quant/mod.rs:520-533: shift 2j of qs byte 32 half + 16 (s % 2) + l, mask
 // bit 4 half + j of hmask byte 16 (s % 2) + l).
