@@ -554,9 +554,48 @@ template <int QT>
 __host__ __device__ constexpr int32_t sum_offset() { return sum_offset_of(QT); }
 
 // quant/mod.rs:586-621
-template <class Tok>
+// PIPE: tokens outermost, each token's codes read one group (64 values) ahead of its dots;
+// the same operations in the same order (the down product with the combine takes it: C2
+// batch 8 down 56.3 -> 54.5 us; gate/up, whose grids need its registers for occupancy,
+// keeps the group-outer form).
+template <bool PIPE = false, class Tok>
 __device__ __forceinline__ void pk_q4k(const uint32_t* w, uint32_t m, Tok tok) {
   float d = f16f(w[0]), dmin = f16f(w[0] >> 16);
+  if constexpr (PIPE) {
+    for (uint32_t t = 0; t < m; t++) {
+      const auto a = tok(t);
+      const uint4* xv = reinterpret_cast<const uint4*>(a.x);
+      uint4 xn[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) xn[k] = xv[k];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        uint32_t xa[16];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          xa[4 * k] = xn[k].x; xa[4 * k + 1] = xn[k].y; xa[4 * k + 2] = xn[k].z; xa[4 * k + 3] = xn[k].w;
+        }
+        if (c < 3) {
+#pragma unroll
+          for (int k = 0; k < 4; k++) xn[k] = xv[4 * (c + 1) + k];
+        }
+        uint32_t sc1, m1, sc2, m2;
+        scale_min_k4(w + 1, 2 * c, sc1, m1);
+        scale_min_k4(w + 1, 2 * c + 1, sc2, m2);
+        int dl = 0, dh = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const uint32_t v = w[4 + 8 * c + i];
+          dl = sdot4(v & 0x0f0f0f0fu, xa[i], dl);
+          dh = sdot4((v >> 4) & 0x0f0f0f0fu, xa[8 + i], dh);
+        }
+        const float s1 = __uint_as_float(a.sm[2 * c]), s2 = __uint_as_float(a.sm[2 * c + 1]);
+        a.put(2 * c, a.xs[2 * c] * (d * (float)sc1 * (float)dl - dmin * (float)m1 * s1));
+        a.put(2 * c + 1, a.xs[2 * c + 1] * (d * (float)sc2 * (float)dh - dmin * (float)m2 * s2));
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     uint32_t sc1, m1, sc2, m2;
@@ -664,18 +703,27 @@ __device__ __forceinline__ void pk_q3k(const uint32_t* w, uint32_t m, Tok tok) {
   float d_all = f16f(w[27]);
   uint32_t sc4[4];
   q3k_scales(w[24], w[25], w[26], sc4);
+  uint32_t q[16][4];
+  float dl[16];
 #pragma unroll
   for (int s = 0; s < 16; s++) {
-    uint32_t q[4];
-    q3s_words(w, s, q);
-    float dl = d_all * (float)((int)(int8_t)byte_of(sc4, s) - 32);
-    for (uint32_t t = 0; t < m; t++) {
-      const auto a = tok(t);
-      const uint32_t* xa = reinterpret_cast<const uint32_t*>(a.x + 16 * s);
-      int dt = (int)a.sm[s];  // -4 * the sub-block's sum
+    q3s_words(w, s, q[s]);
+    dl[s] = d_all * (float)((int)(int8_t)byte_of(sc4, s) - 32);
+  }
+  for (uint32_t t = 0; t < m; t++) {  // each token's 16 sub-blocks, its codes read a sub-block ahead
+    const auto a = tok(t);
+    const uint4* xv = reinterpret_cast<const uint4*>(a.x);
+    uint4 xn = xv[0];
 #pragma unroll
-      for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
-      a.put(s, a.xs[s / 2] * dl * (float)dt);
+    for (int s = 0; s < 16; s++) {
+      const uint4 xc = xn;
+      if (s < 15) xn = xv[s + 1];
+      int dt = (int)a.sm[s];  // -4 * the sub-block's sum
+      dt = sdot4(q[s][0], xc.x, dt);
+      dt = sdot4(q[s][1], xc.y, dt);
+      dt = sdot4(q[s][2], xc.z, dt);
+      dt = sdot4(q[s][3], xc.w, dt);
+      a.put(s, a.xs[s / 2] * dl[s] * (float)dt);
     }
   }
 }
@@ -727,9 +775,9 @@ __device__ __forceinline__ void pk_q80_unit(const uint32_t* w, uint32_t nvalid, 
 
 // One slab unit of a packed type against m tokens (nvalid: blocks of the unit inside the
 // row, for the eight-block Q8_0 units).
-template <int QT, class Tok>
+template <int QT, bool PIPE = false, class Tok>
 __device__ __forceinline__ void pk_unit(const uint32_t* w, uint32_t nvalid, uint32_t m, Tok tok) {
-  if constexpr (QT == Q4_K) pk_q4k(w, m, tok);
+  if constexpr (QT == Q4_K) pk_q4k<PIPE>(w, m, tok);
   else if constexpr (QT == Q5_K) pk_q5k(w, m, tok);
   else if constexpr (QT == Q6_K) pk_q6k(w, m, tok);
   else if constexpr (QT == Q3_K) pk_q3k(w, m, tok);

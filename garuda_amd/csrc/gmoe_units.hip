@@ -161,7 +161,7 @@ __device__ __forceinline__ void stage_acts(uint8_t* lds, uint32_t nelem, uint32_
 // running the sub-block groups outermost instead, the sums read and written in LDS per
 // group, measured slower: C4 225 -> 305 us). f32: the dequantised values of one 32-value
 // group at a time, each group applied to every token, in group order.
-template <int QT, bool PACKED>
+template <int QT, bool PACKED, bool PIPE = false>
 __device__ __forceinline__ void unit_tokens(const uint32_t* w, const uint8_t* acts, uint32_t per, uint32_t nelem,
                                             uint32_t u, uint32_t ubase, uint32_t nblk, float* my, uint32_t m) {
   if constexpr (PACKED) {
@@ -175,7 +175,7 @@ __device__ __forceinline__ void unit_tokens(const uint32_t* w, const uint8_t* ac
       float acc = my[t * 64];
       const PkTok a{reinterpret_cast<const int8_t*>(tok) + off, reinterpret_cast<const float*>(tok + o_s),
                     reinterpret_cast<const uint32_t*>(tok + o_h), &acc};
-      pk_unit<QT>(w, nvalid, 1u, [&](uint32_t) { return a; });
+      pk_unit<QT, PIPE>(w, nvalid, 1u, [&](uint32_t) { return a; });
       my[t * 64] = acc;
     }
   } else {
@@ -618,7 +618,7 @@ __device__ __forceinline__ void dn_atomic_chunk(Stream& st, const DnAtomicArgs& 
       rwt = A.slot_w[slot];
     }
   }
-  st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED>(w, acts, per, A.f, u, 0, nblk, my, m); });
+  st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED, true>(w, acts, per, A.f, u, 0, nblk, my, m); });
   __syncthreads();
   if (wave == 0) {
     const uint32_t l = PAIR ? (lane & 31u) : lane, row = r0 + l;
