@@ -662,26 +662,31 @@ __device__ __forceinline__ void pk_q5k(const uint32_t* w, uint32_t m, Tok tok) {
 template <class Tok>
 __device__ __forceinline__ void pk_q6k(const uint32_t* w, uint32_t m, Tok tok) {
   float d = f16f(w[52]);
+  for (uint32_t t = 0; t < m; t++) {  // each token's 16 sub-blocks, its codes read a sub-block ahead
+    const auto a = tok(t);
+    const uint4* xv = reinterpret_cast<const uint4*>(a.x);
+    uint4 xn = xv[0];
 #pragma unroll
-  for (int s = 0; s < 16; s++) {
-    const int half = s / 8, quarter = (s % 8) / 2, l0 = 16 * (s % 2);
-    uint32_t q[4];
+    for (int s = 0; s < 16; s++) {
+      const uint4 xc = xn;
+      if (s < 15) xn = xv[s + 1];
+      const int half = s / 8, quarter = (s % 8) / 2, l0 = 16 * (s % 2);
+      uint32_t q[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      int l = l0 + 4 * i;
-      uint32_t ql = w[(64 * half + l + (quarter & 1) * 32) / 4];
-      uint32_t qh = w[(128 + 32 * half + l) / 4];
-      uint32_t lo4 = (quarter < 2) ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
-      uint32_t hi2 = ((qh >> (2 * quarter)) & 0x03030303u) << 4;
-      q[i] = lo4 | hi2;
-    }
-    float sc = (float)(int8_t)byte_of(w, 192 + s);
-    for (uint32_t t = 0; t < m; t++) {
-      const auto a = tok(t);
-      const uint32_t* xa = reinterpret_cast<const uint32_t*>(a.x + 16 * s);
+      for (int i = 0; i < 4; i++) {
+        int l = l0 + 4 * i;
+        uint32_t ql = w[(64 * half + l + (quarter & 1) * 32) / 4];
+        uint32_t qh = w[(128 + 32 * half + l) / 4];
+        uint32_t lo4 = (quarter < 2) ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
+        uint32_t hi2 = ((qh >> (2 * quarter)) & 0x03030303u) << 4;
+        q[i] = lo4 | hi2;
+      }
+      const float sc = (float)(int8_t)byte_of(w, 192 + s);
       int dt = (int)a.sm[s];  // -32 * the sub-block's sum
-#pragma unroll
-      for (int i = 0; i < 4; i++) dt = sdot4(q[i], xa[i], dt);
+      dt = sdot4(q[0], xc.x, dt);
+      dt = sdot4(q[1], xc.y, dt);
+      dt = sdot4(q[2], xc.z, dt);
+      dt = sdot4(q[3], xc.w, dt);
       a.put(s, a.xs[s / 2] * d * sc * (float)dt);
     }
   }
