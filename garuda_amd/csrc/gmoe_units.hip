@@ -216,7 +216,7 @@ __device__ __forceinline__ void unit_tokens(const uint32_t* w, const uint8_t* ac
 // With ra.n > 0 (speculative decode) the last row of the grid is the exact routing
 // instead: workgroup x < n*ne runs route_logit for token x / ne, expert x % ne. The
 // dispatcher starts it with the last wave of expert workgroups, whose tail hides it.
-template <int QT, bool PACKED, int D, int TPW = 1>
+template <int QT, bool PACKED, int D, int TPW = 1, bool PIPE = false>
 __global__ void __launch_bounds__(128 * TPW, D > 2 ? 1 : (TPW > 1 ? 3 : 2))
 k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __restrict__ slot_tok, uint32_t f,
            uint32_t d, uint32_t mt, const int8_t* __restrict__ xq,
@@ -260,7 +260,7 @@ k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __r
     __syncthreads();
     stage_acts<QT, PACKED>(acts, d, m, rows, d, 0, xq, xs, xsum, hs);
     __syncthreads();
-    st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED>(w, acts, per, d, u, 0, nblk, my, m); });
+    st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED, PIPE>(w, acts, per, d, u, 0, nblk, my, m); });
     __syncthreads();
     if ((wave & 1) == 0 && tv) {
       const bool valid = r0 + (lane & 32) + 32 <= f;  // this lane's 32-row block lies inside d_ff
@@ -840,18 +840,18 @@ static hipError_t go_gu_split(const LayerDev& L, const FwdBufs& B, uint32_t n, c
   return hipGetLastError();
 }
 
-template <int QT, bool PACKED, int D, int TPW = 1>
+template <int QT, bool PACKED, int D, int TPW = 1, bool PIPE = false>
 static hipError_t go_gu(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
   const uint32_t per = 2 * TPW * 64 * 4 + ActLds<QT, PACKED>::per_token(L.d) + 4;
   const uint32_t mt = TPW > 1 ? chunk_tokens_lds(L, n, per + 16, kChunkLds3) : chunk_tokens(L, n, per + 16);
   if (mt == 0) return hipErrorInvalidValue;
-  static const bool once = allow_lds(k_gu_units<QT, PACKED, D, TPW>);
+  static const bool once = allow_lds(k_gu_units<QT, PACKED, D, TPW, PIPE>);
   (void)once;
   const uint32_t tiles = (L.f + kTileRows * TPW - 1) / (kTileRows * TPW);
   uint32_t lds = mt * per + 16;
   if (ra.n) lds = max(lds, route_logit_lds(ra.k, ra.sec));
   const dim3 g(max(tiles, ra.n * ra.ne), min(L.ne, n * L.k) + (ra.n ? 1 : 0));
-  hipLaunchKernelGGL((k_gu_units<QT, PACKED, D, TPW>), g, dim3(128 * TPW), lds, st, B.work, L.ne, B.slot_tok, L.f,
+  hipLaunchKernelGGL((k_gu_units<QT, PACKED, D, TPW, PIPE>), g, dim3(128 * TPW), lds, st, B.work, L.ne, B.slot_tok, L.f,
                      L.d, mt, B.xq, B.xs, B.xsum, B.hs, B.hq, B.hsc, B.hsum, B.hf, sum_kind_of(L.qt_down),
                      sum_offset_of(L.qt_down), ra);
   return hipGetLastError();
@@ -949,6 +949,11 @@ hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const R
       if (B.hq && split_ok<QT>(L, n, ra)) return go_gu_split<QT>(L, B, n, ra, st);
       if (ra.self) return hipErrorInvalidValue;  // (the caller asked only where units_self_ok)
       if (n <= kDeepRingTokens) return go_gu<QT, true, 4>(L, B, n, ra, st);
+      // Q4_K at half a token an expert or fewer: the dots read the codes a group ahead
+      // (182 VGPRs, two waves a SIMD, which still hold such a grid in one round)
+      if constexpr (QT == Q4_K) {
+        if (2 * n * L.k <= L.ne) return go_gu<QT, true, 1, 1, true>(L, B, n, ra, st);
+      }
       if (n * L.k <= L.ne) return go_gu<QT, true, 1>(L, B, n, ra, st);
       if constexpr (gu_pairs<QT>()) return go_gu<QT, true, 1, 2>(L, B, n, ra, st);
       return go_gu<QT, true, gu_ring<QT>()>(L, B, n, ra, st);
