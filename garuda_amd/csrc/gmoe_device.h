@@ -554,14 +554,52 @@ template <int QT>
 __host__ __device__ constexpr int32_t sum_offset() { return sum_offset_of(QT); }
 
 // quant/mod.rs:586-621
-// PIPE: tokens outermost, each token's codes read one group (64 values) ahead of its dots;
-// the same operations in the same order (the down product with the combine takes it: C2
-// batch 8 down 56.3 -> 54.5 us; gate/up, whose grids need its registers for occupancy,
-// keeps the group-outer form).
-template <bool PIPE = false, class Tok>
+// PIPE 1: tokens outermost, each token's codes read one group (64 values) ahead of its
+// dots; PIPE 2: half a group ahead, each group's low-nibble chain then its high-nibble
+// chain (fewer registers: 167 VGPRs in gate/up, three waves a SIMD). The same operations
+// in the same order either way (the two chains are separate sums). Measured: the down
+// product with the combine and gate/up at half a token an expert take 1 (C2 batch 8
+// down 56.3 -> 54.5 us, batch 2 92.6 -> 90.5 us), gate/up at up to one token an expert
+// takes 2 (batch 4 134.1 -> 133.2 us); gate/up above that keeps the group-outer form.
+template <int PIPE = 0, class Tok>
 __device__ __forceinline__ void pk_q4k(const uint32_t* w, uint32_t m, Tok tok) {
   float d = f16f(w[0]), dmin = f16f(w[0] >> 16);
-  if constexpr (PIPE) {
+  if constexpr (PIPE == 2) {
+    for (uint32_t t = 0; t < m; t++) {
+      const auto a = tok(t);
+      const uint4* xv = reinterpret_cast<const uint4*>(a.x);
+      // half a group (32 codes, two uint4) in flight ahead of the chain that needs it
+      uint4 xn0 = xv[0], xn1 = xv[1];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        uint32_t sc1, m1, sc2, m2;
+        scale_min_k4(w + 1, 2 * c, sc1, m1);
+        scale_min_k4(w + 1, 2 * c + 1, sc2, m2);
+        uint4 x0 = xn0, x1 = xn1;
+        xn0 = xv[4 * c + 2];
+        xn1 = xv[4 * c + 3];
+        const uint32_t lo_x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        int dl = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) dl = sdot4(w[4 + 8 * c + i] & 0x0f0f0f0fu, lo_x[i], dl);
+        x0 = xn0;
+        x1 = xn1;
+        if (c < 3) {
+          xn0 = xv[4 * c + 4];
+          xn1 = xv[4 * c + 5];
+        }
+        const uint32_t hi_x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        int dh = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) dh = sdot4((w[4 + 8 * c + i] >> 4) & 0x0f0f0f0fu, hi_x[i], dh);
+        const float s1 = __uint_as_float(a.sm[2 * c]), s2 = __uint_as_float(a.sm[2 * c + 1]);
+        a.put(2 * c, a.xs[2 * c] * (d * (float)sc1 * (float)dl - dmin * (float)m1 * s1));
+        a.put(2 * c + 1, a.xs[2 * c + 1] * (d * (float)sc2 * (float)dh - dmin * (float)m2 * s2));
+      }
+    }
+    return;
+  }
+  if constexpr (PIPE == 1) {
     for (uint32_t t = 0; t < m; t++) {
       const auto a = tok(t);
       const uint4* xv = reinterpret_cast<const uint4*>(a.x);
@@ -780,7 +818,7 @@ __device__ __forceinline__ void pk_q80_unit(const uint32_t* w, uint32_t nvalid, 
 
 // One slab unit of a packed type against m tokens (nvalid: blocks of the unit inside the
 // row, for the eight-block Q8_0 units).
-template <int QT, bool PIPE = false, class Tok>
+template <int QT, int PIPE = 0, class Tok>
 __device__ __forceinline__ void pk_unit(const uint32_t* w, uint32_t nvalid, uint32_t m, Tok tok) {
   if constexpr (QT == Q4_K) pk_q4k<PIPE>(w, m, tok);
   else if constexpr (QT == Q5_K) pk_q5k(w, m, tok);

@@ -161,7 +161,7 @@ __device__ __forceinline__ void stage_acts(uint8_t* lds, uint32_t nelem, uint32_
 // running the sub-block groups outermost instead, the sums read and written in LDS per
 // group, measured slower: C4 225 -> 305 us). f32: the dequantised values of one 32-value
 // group at a time, each group applied to every token, in group order.
-template <int QT, bool PACKED, bool PIPE = false>
+template <int QT, bool PACKED, int PIPE = 0>
 __device__ __forceinline__ void unit_tokens(const uint32_t* w, const uint8_t* acts, uint32_t per, uint32_t nelem,
                                             uint32_t u, uint32_t ubase, uint32_t nblk, float* my, uint32_t m) {
   if constexpr (PACKED) {
@@ -216,7 +216,7 @@ __device__ __forceinline__ void unit_tokens(const uint32_t* w, const uint8_t* ac
 // With ra.n > 0 (speculative decode) the last row of the grid is the exact routing
 // instead: workgroup x < n*ne runs route_logit for token x / ne, expert x % ne. The
 // dispatcher starts it with the last wave of expert workgroups, whose tail hides it.
-template <int QT, bool PACKED, int D, int TPW = 1, bool PIPE = false>
+template <int QT, bool PACKED, int D, int TPW = 1, int PIPE = 0>
 __global__ void __launch_bounds__(128 * TPW, D > 2 ? 1 : (TPW > 1 ? 3 : 2))
 k_gu_units(const ExpertWork* __restrict__ work, uint32_t ne, const uint32_t* __restrict__ slot_tok, uint32_t f,
            uint32_t d, uint32_t mt, const int8_t* __restrict__ xq,
@@ -618,7 +618,7 @@ __device__ __forceinline__ void dn_atomic_chunk(Stream& st, const DnAtomicArgs& 
       rwt = A.slot_w[slot];
     }
   }
-  st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED, true>(w, acts, per, A.f, u, 0, nblk, my, m); });
+  st.run([&](uint32_t u, const uint32_t* w) { unit_tokens<QT, PACKED, 1>(w, acts, per, A.f, u, 0, nblk, my, m); });
   __syncthreads();
   if (wave == 0) {
     const uint32_t l = PAIR ? (lane & 31u) : lane, row = r0 + l;
@@ -840,7 +840,7 @@ static hipError_t go_gu_split(const LayerDev& L, const FwdBufs& B, uint32_t n, c
   return hipGetLastError();
 }
 
-template <int QT, bool PACKED, int D, int TPW = 1, bool PIPE = false>
+template <int QT, bool PACKED, int D, int TPW = 1, int PIPE = 0>
 static hipError_t go_gu(const LayerDev& L, const FwdBufs& B, uint32_t n, const RouteArgs& ra, hipStream_t st) {
   const uint32_t per = 2 * TPW * 64 * 4 + ActLds<QT, PACKED>::per_token(L.d) + 4;
   const uint32_t mt = TPW > 1 ? chunk_tokens_lds(L, n, per + 16, kChunkLds3) : chunk_tokens(L, n, per + 16);
@@ -950,9 +950,11 @@ hipError_t units_gateup(const LayerDev& L, const FwdBufs& B, uint32_t n, const R
       if (ra.self) return hipErrorInvalidValue;  // (the caller asked only where units_self_ok)
       if (n <= kDeepRingTokens) return go_gu<QT, true, 4>(L, B, n, ra, st);
       // Q4_K at half a token an expert or fewer: the dots read the codes a group ahead
-      // (182 VGPRs, two waves a SIMD, which still hold such a grid in one round)
+      // (182 VGPRs, two waves a SIMD, which still hold such a grid in one round); up to
+      // one token an expert, half a group ahead (167 VGPRs, three waves a SIMD)
       if constexpr (QT == Q4_K) {
-        if (2 * n * L.k <= L.ne) return go_gu<QT, true, 1, 1, true>(L, B, n, ra, st);
+        if (2 * n * L.k <= L.ne) return go_gu<QT, true, 1, 1, 1>(L, B, n, ra, st);
+        if (n * L.k <= L.ne) return go_gu<QT, true, 1, 1, 2>(L, B, n, ra, st);
       }
       if (n * L.k <= L.ne) return go_gu<QT, true, 1>(L, B, n, ra, st);
       if constexpr (gu_pairs<QT>()) return go_gu<QT, true, 1, 2>(L, B, n, ra, st);
